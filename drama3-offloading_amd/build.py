@@ -1,0 +1,86 @@
+"""Build libmoeoffload.so (all HIP kernels + the C ABI) for gfx950, in-tree.
+
+    python drama3-offloading_amd/build.py [--jobs N] [--asm]
+
+Each csrc/*.hip is compiled to an object with hipcc, then linked into one
+shared library next to this file.  The library links the HIP runtime by its
+soname, so a process that has already imported torch resolves it to torch's
+own runtime (one HIP runtime per process).  `--asm` also writes the gfx950
+assembly of each source into _build/ for inspection.
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+CSRC = HERE / "csrc"
+BUILD = HERE / "_build"
+LIB = HERE / "libmoeoffload.so"
+ARCH = "gfx950"
+
+HIPCC = os.environ.get("HIPCC") or shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+
+# -packed-fp32-ops: keep hipcc from emitting v_pk_{add,mul,fma}_f32, which
+# have given silently wrong results on this hardware.  The host pass warns
+# that it does not know the feature; that warning is harmless.
+DEVICE_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function",
+]
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC.glob("*.hip"))
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in proc.stdout.splitlines()
+                    if "packed-fp32-ops' is not a recognized feature" not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
+    if out.strip():
+        print(out, file=sys.stderr)
+
+
+def compile_one(src: Path, asm: bool) -> Path:
+    obj = BUILD / (src.stem + ".o")
+    _run([HIPCC, *DEVICE_FLAGS, "-c", str(src), "-o", str(obj)])
+    if asm:
+        _run([HIPCC, *DEVICE_FLAGS, "--cuda-device-only", "-S", str(src),
+              "-o", str(BUILD / (src.stem + ".s"))])
+    return obj
+
+
+def build(jobs: int = 8, asm: bool = False) -> Path:
+    if not Path(HIPCC).exists() and shutil.which(HIPCC) is None:
+        raise RuntimeError(f"hipcc not found ({HIPCC})")
+    BUILD.mkdir(exist_ok=True)
+    srcs = sources()
+    with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        objs = list(ex.map(lambda s: compile_one(s, asm), srcs))
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+          *map(str, objs), "-ldl"])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 1))
+    ap.add_argument("--asm", action="store_true")
+    args = ap.parse_args()
+    lib = build(args.jobs, args.asm)
+    print(lib)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,91 @@
+// Error reporting, version and host-pool entry points of the C ABI.
+#include "common.hpp"
+
+#include <dlfcn.h>
+#include <string.h>
+
+namespace moe {
+
+static thread_local char g_err[1024] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+void clear_error() { g_err[0] = '\0'; }
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return static_cast<int>(e);
+  }
+  return MOE_OK;
+}
+
+}  // namespace moe
+
+extern "C" {
+
+const char* moe_last_error(void) { return moe::g_err; }
+
+const char* moe_version(void) { return "moeoffload 0.1 gfx950"; }
+
+const char* moe_hip_runtime_path(void) {
+  static char path[1024] = "";
+  Dl_info info;
+  void* sym = reinterpret_cast<void*>(&hipGetLastError);
+  if (dladdr(sym, &info) && info.dli_fname) {
+    strncpy(path, info.dli_fname, sizeof(path) - 1);
+  }
+  return path;
+}
+
+int moe_host_alloc(void** host_ptr, size_t bytes, int flags) {
+  MOE_REQUIRE(host_ptr != nullptr, "moe_host_alloc: host_ptr is NULL");
+  MOE_REQUIRE(bytes > 0, "moe_host_alloc: zero bytes");
+  MOE_REQUIRE(flags == 0 || flags == 1, "moe_host_alloc: flags must be 0 or 1");
+  unsigned f = hipHostMallocMapped | (flags ? hipHostMallocNonCoherent : hipHostMallocCoherent);
+  hipError_t e = hipHostMalloc(host_ptr, bytes, f);
+  if (e != hipSuccess) {
+    moe::set_error("moe_host_alloc(%zu B): %s", bytes, hipGetErrorString(e));
+    *host_ptr = nullptr;
+    return static_cast<int>(e);
+  }
+  return MOE_OK;
+}
+
+int moe_host_free(void* host_ptr) {
+  if (host_ptr == nullptr) return MOE_OK;
+  hipError_t e = hipHostFree(host_ptr);
+  if (e != hipSuccess) {
+    moe::set_error("moe_host_free: %s", hipGetErrorString(e));
+    return static_cast<int>(e);
+  }
+  return MOE_OK;
+}
+
+int moe_device_ptr_of(const void* host_ptr, void** dev_ptr) {
+  MOE_REQUIRE(host_ptr != nullptr && dev_ptr != nullptr, "moe_device_ptr_of: NULL argument");
+  hipPointerAttribute_t attr;
+  hipError_t e = hipPointerGetAttributes(&attr, host_ptr);
+  if (e != hipSuccess || attr.type != hipMemoryTypeHost) {
+    (void)hipGetLastError();  // clear the sticky error of a failed query
+    moe::set_error("moe_device_ptr_of: %p is not page-locked host memory "
+                   "(expected a contiguous page-locked CPU buffer)", host_ptr);
+    return MOE_EINVAL;
+  }
+  void* d = nullptr;
+  e = hipHostGetDevicePointer(&d, const_cast<void*>(host_ptr), 0);
+  if (e != hipSuccess) {
+    moe::set_error("moe_device_ptr_of: hipHostGetDevicePointer: %s", hipGetErrorString(e));
+    return static_cast<int>(e);
+  }
+  *dev_ptr = d;
+  return MOE_OK;
+}
+
+}  // extern "C"

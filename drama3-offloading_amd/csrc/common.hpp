@@ -1,0 +1,124 @@
+// Shared helpers for libmoeoffload: error reporting, launch checks, bf16 and
+// e4m3fn arithmetic used identically by every kernel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/moe_offload.h"
+
+namespace moe {
+
+// Thread-local text of the last failure; set by fail()/check_launch().
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define MOE_REQUIRE(cond, ...)        \
+  do {                                \
+    if (!(cond)) {                    \
+      ::moe::set_error(__VA_ARGS__);  \
+      return MOE_EINVAL;              \
+    }                                 \
+  } while (0)
+
+// Sync-free launch check: reads the sticky launch error without waiting.
+int check_launch(const char* what);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ----------------------------------------------------------------- bf16
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even float -> bf16 bits (NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// -------------------------------------------------------------- e4m3fn
+
+// float -> OCP e4m3fn code, round-to-nearest-even, saturating at +-448.
+// Every step is exact except the one rint(), so this is the correctly
+// rounded conversion; it matches the oracle's encoder bit for bit.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float v) {
+  uint32_t sign = (__float_as_uint(v) >> 24) & 0x80u;
+  float a = fabsf(v);
+  if (!(a == a)) return sign | 0x7fu;          // NaN
+  if (a >= 448.0f) return sign | 0x7eu;        // saturate
+  if (a < 0.015625f) {                         // below 2^-6: subnormal grid 2^-9
+    uint32_t m = static_cast<uint32_t>(rintf(a * 512.0f));   // 0..8; 8 == code 8
+    return sign | m;
+  }
+  int e;
+  float fr = frexpf(a, &e);                    // a = fr * 2^e, fr in [0.5, 1)
+  // a = (1 + m/8) * 2^(e-1): mantissa grid is fr*16 - 8 in [0, 8)
+  uint32_t m = static_cast<uint32_t>(rintf(fr * 16.0f - 8.0f));
+  int eb = e - 1 + 7;
+  if (m == 8u) { m = 0u; eb += 1; }
+  return sign | (static_cast<uint32_t>(eb) << 3) | m;
+}
+
+// Per-128-group activation scale: amax / 448 in float32, division correctly
+// rounded (HIP's default float division).
+__device__ __forceinline__ float act_scale(float amax) { return amax / 448.0f; }
+
+// Quantise v with scale s (s == 0 => 0).
+__device__ __forceinline__ uint32_t quant_e4m3(float v, float s) {
+  return s == 0.0f ? 0u : f32_to_e4m3(v / s);
+}
+
+// ------------------------------------------------------------ wave utils
+
+template <typename T>
+__device__ __forceinline__ T wave_bcast(T v, int lane) { return __shfl(v, lane, 64); }
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// ---------------------------------------------------------------- MFMA
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// 32 bytes (two 16-byte loads) as an MFMA operand; `p` 16-byte aligned.
+// The _nt form streams from HBM without keeping the lines in the caches.
+__device__ __forceinline__ v8i load_op32_nt(const uint8_t* p) {
+  const u32x4* s = reinterpret_cast<const u32x4*>(p);
+  u32x4 lo = __builtin_nontemporal_load(s);
+  u32x4 hi = __builtin_nontemporal_load(s + 1);
+  return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+}
+__device__ __forceinline__ v8i load_op32(const uint8_t* p) {
+  const u32x4* s = reinterpret_cast<const u32x4*>(p);
+  u32x4 lo = s[0];
+  u32x4 hi = s[1];
+  return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+}
+
+// 16x16x128 e4m3 x e4m3 -> f32 on gfx950, block scales neutral (E8M0 127 = 1.0).
+// Lane l supplies row (l % 16) of A and column (l % 16) of B, 32 bytes each,
+// covering the same 32 reduction indices for both operands; the four lane
+// groups (l / 16) cover disjoint 32-index sets, so the product is the full
+// 128-term dot product.  Result: lane l holds C[4*(l/16) + i][l % 16].
+__device__ __forceinline__ v4f mfma_e4m3_16x16x128(v8i a, v8i b, v4f c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+
+}  // namespace moe

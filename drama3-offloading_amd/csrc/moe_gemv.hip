@@ -1,0 +1,322 @@
+// W8A8 block-FP8 expert FFN, per (token, expert) pair: the decode GEMV path.
+//
+// For pair p = t*K + k with expert e = ids[p]:
+//   xq, xs = e4m3 quantisation of x[t], per 128 columns, scale amax/448
+//   h[p][r] = sum_g s13[e][r/128][g] * xs[g] * <w13[e][r][g*128:+128], xq[g*128:+128]>
+//   a = SiLU(h[:I]) * h[I:], quantised per 128 (aq, as)
+//   y[c]    = sum_g s2[e][c/128][g] * as[g] * <w2[e][c][g*128:+128], aq[g*128:+128]>
+//   out[t]  = sum_k w[t][k] * y_k  (k in order, float32) -> bf16
+//
+// Each 128-term block product runs on one v_mfma_scale_f32_16x16x128_f8f6f4
+// with the weight rows as the A operand (16 rows per wave) and the quantised
+// activation as every column of B; column 0 of the result is used.  Weights
+// are read straight from HBM into the A registers: each lane reads 32
+// contiguous bytes of its row per block, so a wave reads 16 rows x 128 B,
+// whole cache lines.  The block scales multiply the fp32 block result, so the
+// scale of every 128x128 weight block is applied exactly once per block.
+//
+// Kernel 1 (gate/up): grid (2I/64, pairs), 4 waves x 16 rows, x quantised
+// into LDS by the workgroup.  Kernel 2 (down + combine): grid (H/16, tokens),
+// one wave per k; each wave turns its h row into aq in LDS, does its 16 output
+// rows of w2, and the workgroup sums the k partials in order.
+#include "common.hpp"
+
+namespace moe {
+
+constexpr int kMaxHidden = 8192;
+constexpr int kMaxInter = 2048;
+constexpr int kMaxK = 16;
+
+__device__ __forceinline__ int64_t load_id(const void* ids, int ids64, int64_t p) {
+  return ids64 ? reinterpret_cast<const int64_t*>(ids)[p]
+               : static_cast<int64_t>(reinterpret_cast<const int32_t*>(ids)[p]);
+}
+
+__device__ __forceinline__ float load_w(const void* w, int wbf16, int64_t p) {
+  return wbf16 ? bf16_to_f32(reinterpret_cast<const uint16_t*>(w)[p])
+               : reinterpret_cast<const float*>(w)[p];
+}
+
+// Quantise `n` bf16 values (n % 2048 handled in passes) into LDS codes and
+// per-128 scales with 256 threads: 16 threads x 8 values per group.
+__device__ __forceinline__ void quantize_row_bf16_to_lds(const uint16_t* __restrict__ xr, int n,
+                                                         uint8_t* __restrict__ q,
+                                                         float* __restrict__ sc) {
+  const int tid = threadIdx.x;
+  for (int base = 0; base < n; base += 2048) {
+    const int i = base + tid * 8;
+    float v[8];
+    float amax = 0.0f;
+    if (i < n) {
+      uint4 raw = *reinterpret_cast<const uint4*>(xr + i);
+      const uint32_t r[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[2 * j] = __uint_as_float(r[j] << 16);
+        v[2 * j + 1] = __uint_as_float(r[j] & 0xffff0000u);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    }
+    // the 16 threads of a 128-group are 16 consecutive lanes of one wave
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    if (i < n) {
+      const float s = act_scale(amax);
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) lo |= quant_e4m3(v[j], s) << (8 * j);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) hi |= quant_e4m3(v[4 + j], s) << (8 * j);
+      *reinterpret_cast<uint2*>(q + i) = make_uint2(lo, hi);
+      if ((tid & 15) == 0) sc[i >> 7] = s;
+    }
+  }
+}
+
+// ------------------------------------------------------------ kernel 1
+
+__global__ __launch_bounds__(256) void gateup_gemv_kernel(
+    const uint16_t* __restrict__ x, const void* __restrict__ ids, int ids64, int32_t top_k,
+    const uint8_t* __restrict__ w13, const float* __restrict__ s13, int64_t w13_es,
+    int64_t s13_es, int32_t n_experts, int32_t hidden, int32_t inter, float* __restrict__ h) {
+  __shared__ __align__(16) uint8_t xq[kMaxHidden];
+  __shared__ float xs[kMaxHidden / 128];
+  const int64_t p = blockIdx.y;
+  const int64_t t = p / top_k;
+  const int64_t e = load_id(ids, ids64, p);
+  const int rows2 = 2 * inter;
+  const int G = hidden >> 7;
+  quantize_row_bf16_to_lds(x + t * hidden, hidden, xq, xs);
+  __syncthreads();
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int r0 = blockIdx.x * 64 + wave * 16;
+  const int q = lane >> 4;
+  float* hp = h + p * rows2;
+  if (e < 0 || e >= n_experts) {   // no such expert: poison, never read out of bounds
+    if (lane < 16) hp[r0 + lane] = __builtin_nanf("");
+    return;
+  }
+  const uint8_t* wrow =
+      w13 + e * w13_es + static_cast<int64_t>(r0 + (lane & 15)) * hidden + q * 32;
+  const float* srow = s13 + e * s13_es + static_cast<int64_t>(r0 >> 7) * G;
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+  constexpr int CH = 8;   // K blocks of loads kept in flight per lane
+  for (int g0 = 0; g0 < G; g0 += CH) {
+    v8i a[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      if (g0 + c < G) {
+        a[c] = load_op32_nt(wrow + (g0 + c) * 128);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int g = g0 + c;
+      if (g < G) {
+        const v8i b = load_op32(xq + g * 128 + q * 32);
+        v4f z = {0.f, 0.f, 0.f, 0.f};
+        v4f d = mfma_e4m3_16x16x128(a[c], b, z);
+        const float sc = srow[g] * xs[g];
+        acc[0] += d[0] * sc;
+        acc[1] += d[1] * sc;
+        acc[2] += d[2] * sc;
+        acc[3] += d[3] * sc;
+      }
+    }
+  }
+  if ((lane & 15) == 0) {
+    const int r = r0 + 4 * q;
+    *reinterpret_cast<float4*>(hp + r) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  }
+}
+
+// ------------------------------------------------------------ kernel 2
+
+__global__ __launch_bounds__(1024) void down_gemv_kernel(
+    const float* __restrict__ h, const void* __restrict__ ids, int ids64,
+    const void* __restrict__ weights, int wbf16, int32_t top_k, const uint8_t* __restrict__ w2,
+    const float* __restrict__ s2, int64_t w2_es, int64_t s2_es, int32_t n_experts,
+    int32_t hidden, int32_t inter, uint16_t* __restrict__ out) {
+  __shared__ __align__(16) uint8_t aq[kMaxK][kMaxInter];
+  __shared__ float as_[kMaxK][kMaxInter / 128];
+  __shared__ float part[kMaxK][16];
+  const int wave = threadIdx.x >> 6;   // == k
+  const int lane = threadIdx.x & 63;
+  const int64_t t = blockIdx.y;
+  const int64_t p = t * top_k + wave;
+  const int64_t e = load_id(ids, ids64, p);
+  const bool valid = e >= 0 && e < n_experts;
+  const int Gi = inter >> 7;
+  const float* hp = h + p * (2 * inter);
+  // SiLU(gate) * up for this pair, quantised per 128 into LDS: 16 lanes x 8
+  for (int base = 0; base < inter; base += 512) {
+    const int j = base + lane * 8;
+    float a[8];
+    float amax = 0.0f;
+    if (j < inter) {
+      float4 g0 = *reinterpret_cast<const float4*>(hp + j);
+      float4 g1 = *reinterpret_cast<const float4*>(hp + j + 4);
+      float4 u0 = *reinterpret_cast<const float4*>(hp + inter + j);
+      float4 u1 = *reinterpret_cast<const float4*>(hp + inter + j + 4);
+      const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+      const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        a[i] = gv[i] / (1.0f + expf(-gv[i])) * uv[i];
+        amax = fmaxf(amax, fabsf(a[i]));
+      }
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    if (j < inter) {
+      const float s = act_scale(amax);
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) lo |= quant_e4m3(a[i], s) << (8 * i);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) hi |= quant_e4m3(a[4 + i], s) << (8 * i);
+      *reinterpret_cast<uint2*>(&aq[wave][j]) = make_uint2(lo, hi);
+      if ((lane & 15) == 0) as_[wave][j >> 7] = s;
+    }
+  }
+  __syncthreads();
+
+  const int c0 = blockIdx.x * 16;
+  const int q = lane >> 4;
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+  if (valid) {
+    const uint8_t* wrow =
+        w2 + e * w2_es + static_cast<int64_t>(c0 + (lane & 15)) * inter + q * 32;
+    const float* srow = s2 + e * s2_es + static_cast<int64_t>(c0 >> 7) * Gi;
+    constexpr int CH = 4;
+    for (int g0 = 0; g0 < Gi; g0 += CH) {
+      v8i a[CH];
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        if (g0 + c < Gi) {
+          a[c] = load_op32_nt(wrow + (g0 + c) * 128);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int g = g0 + c;
+        if (g < Gi) {
+          const v8i b = load_op32(&aq[wave][g * 128 + q * 32]);
+          v4f z = {0.f, 0.f, 0.f, 0.f};
+          v4f d = mfma_e4m3_16x16x128(a[c], b, z);
+          const float sc = srow[g] * as_[wave][g];
+          acc[0] += d[0] * sc;
+          acc[1] += d[1] * sc;
+          acc[2] += d[2] * sc;
+          acc[3] += d[3] * sc;
+        }
+      }
+    }
+  }
+  if ((lane & 15) == 0) {
+    const float wk = load_w(weights, wbf16, p);
+    const float nan = __builtin_nanf("");
+#pragma unroll
+    for (int i = 0; i < 4; ++i) part[wave][4 * q + i] = valid ? wk * acc[i] : nan;
+  }
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    float sum = 0.0f;
+    for (int k = 0; k < top_k; ++k) sum += part[k][threadIdx.x];
+    out[t * hidden + c0 + threadIdx.x] = f32_to_bf16(sum);
+  }
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" size_t moe_fp8_moe_workspace(int32_t tokens, int32_t top_k, int32_t n_experts,
+                                        int32_t hidden, int32_t inter) {
+  (void)n_experts;
+  (void)hidden;
+  if (tokens <= 0 || top_k <= 0 || inter <= 0) return 256;
+  // h: one float32 row of 2*inter per (token, expert) pair, 256-byte aligned
+  const size_t h = static_cast<size_t>(tokens) * top_k * 2 * inter * sizeof(float);
+  return (h + 255) & ~static_cast<size_t>(255);
+}
+
+extern "C" int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t ids_dtype,
+                                      const void* weights, int32_t w_dtype, int32_t tokens,
+                                      int32_t top_k, const void* w13, const float* s13,
+                                      const void* w2, const float* s2, int32_t n_experts,
+                                      int32_t hidden, int32_t inter,
+                                      const moe_expert_strides* strides, void* out,
+                                      void* workspace, size_t workspace_bytes, int32_t mode,
+                                      void* stream) {
+  MOE_REQUIRE(x && ids && weights && w13 && s13 && w2 && s2 && out,
+              "moe_fp8_moe_forward: NULL pointer");
+  MOE_REQUIRE(tokens >= 0, "moe_fp8_moe_forward: tokens < 0");
+  MOE_REQUIRE(top_k >= 1 && top_k <= kMaxK, "moe_fp8_moe_forward: need 1 <= top_k <= %d", kMaxK);
+  MOE_REQUIRE(hidden >= 128 && hidden % 128 == 0 && hidden <= kMaxHidden,
+              "moe_fp8_moe_forward: hidden must be a multiple of 128 in [128, %d] (got %d)",
+              kMaxHidden, hidden);
+  MOE_REQUIRE(inter >= 128 && inter % 128 == 0 && inter <= kMaxInter,
+              "moe_fp8_moe_forward: inter must be a multiple of 128 in [128, %d] (got %d)",
+              kMaxInter, inter);
+  MOE_REQUIRE(n_experts >= 1, "moe_fp8_moe_forward: n_experts < 1");
+  MOE_REQUIRE(ids_dtype == MOE_I32 || ids_dtype == MOE_I64, "moe_fp8_moe_forward: bad ids_dtype");
+  MOE_REQUIRE(w_dtype == MOE_F32 || w_dtype == MOE_BF16, "moe_fp8_moe_forward: bad w_dtype");
+  MOE_REQUIRE(mode >= 0 && mode <= 2, "moe_fp8_moe_forward: mode must be 0, 1 or 2");
+  MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w13) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(w2) % 16 == 0,
+              "moe_fp8_moe_forward: x, w13 and w2 must be 16-byte aligned");
+  moe_expert_strides es;
+  if (strides) {
+    es = *strides;
+  } else {
+    es.w13 = 2LL * inter * hidden;
+    es.s13 = (2LL * inter / 128) * (hidden / 128);
+    es.w2 = static_cast<int64_t>(hidden) * inter;
+    es.s2 = (static_cast<int64_t>(hidden) / 128) * (inter / 128);
+  }
+  MOE_REQUIRE(es.w13 >= 2LL * inter * hidden && es.w2 >= static_cast<int64_t>(hidden) * inter &&
+                  es.s13 >= (2LL * inter / 128) * (hidden / 128) &&
+                  es.s2 >= (static_cast<int64_t>(hidden) / 128) * (inter / 128),
+              "moe_fp8_moe_forward: expert strides smaller than one expert");
+  MOE_REQUIRE(es.w13 % 16 == 0 && es.w2 % 16 == 0,
+              "moe_fp8_moe_forward: w13/w2 expert strides must be multiples of 16 bytes");
+  if (tokens == 0) return MOE_OK;
+  const size_t need = moe_fp8_moe_workspace(tokens, top_k, n_experts, hidden, inter);
+  MOE_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+              "moe_fp8_moe_forward: workspace of %zu bytes needed, %zu given", need,
+              workspace_bytes);
+  MOE_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
+              "moe_fp8_moe_forward: workspace must be 16-byte aligned");
+  hipStream_t s = as_stream(stream);
+  float* h = static_cast<float*>(workspace);
+  const int ids64 = ids_dtype == MOE_I64;
+  const int wbf16 = w_dtype == MOE_BF16;
+  const int64_t pairs = static_cast<int64_t>(tokens) * top_k;
+  MOE_REQUIRE(pairs <= 65535LL, "moe_fp8_moe_forward: too many (token, expert) pairs (%lld)",
+              (long long)pairs);
+  hipLaunchKernelGGL(gateup_gemv_kernel, dim3((2 * inter) / 64, pairs), dim3(256), 0, s,
+                     static_cast<const uint16_t*>(x), ids, ids64, top_k,
+                     static_cast<const uint8_t*>(w13), s13, es.w13, es.s13, n_experts, hidden,
+                     inter, h);
+  int rc = check_launch("moe_fp8_moe_forward(gate/up)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(down_gemv_kernel, dim3(hidden / 16, tokens), dim3(64 * top_k), 0, s, h, ids,
+                     ids64, weights, wbf16, top_k, static_cast<const uint8_t*>(w2), s2, es.w2,
+                     es.s2, n_experts, hidden, inter, static_cast<uint16_t*>(out));
+  return check_launch("moe_fp8_moe_forward(down)");
+}
+
+extern "C" int moe_fp8_moe_forward(const void* x, const void* ids, int32_t ids_dtype,
+                                   const void* weights, int32_t w_dtype, int32_t tokens,
+                                   int32_t top_k, const void* w13, const float* s13,
+                                   const void* w2, const float* s2, int32_t n_experts,
+                                   int32_t hidden, int32_t inter, void* out, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  return moe_fp8_moe_forward_ex(x, ids, ids_dtype, weights, w_dtype, tokens, top_k, w13, s13, w2,
+                                s2, n_experts, hidden, inter, nullptr, out, workspace,
+                                workspace_bytes, 0, stream);
+}

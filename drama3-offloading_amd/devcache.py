@@ -1,0 +1,201 @@
+"""Device-resident expert cache: no host sync, hipGraph capturable.
+
+Drop-in for bin/devcache.py.  Same per-layer state on the experts module,
+same function names and the same dispatch, with the two Triton kernels and
+the CUDA extension replaced by libmoeoffload's HIP kernels:
+
+  _dc_slot_of[E]      int32  expert -> slot, -1 absent
+  _dc_slot_expert[C]  int32  slot -> expert, -1 empty
+  _dc_stamp[C]        int64  step at which the slot was last used
+  _dc_step[1]         int64  bumped on the device by every resolve
+  _dc_w13/_dc_w2/_dc_s13/_dc_s2   the cache buffers, one slot per row
+  _dc_out/_dc_fslot/_dc_fexp/_dc_nmiss  per-call scratch, preallocated
+  _dc_stats[2]        int64  hits, misses counted on the device (new: the
+                             reference has no hit counter, bin/devcache.py:274)
+
+Per decode step (rows == 1): `moe_resolve_slots` (one wavefront; decisions
+identical to bin/devcache.py:65-98) then one `moe_fetch` launch that copies
+every queued miss, all four buffers, from page-locked host memory into its
+slot, reading the miss list and count on the device at run time -- so the
+captured graph serves different experts on every replay -- then
+`fp8_moe_forward` on the whole cache buffer with slot ids.  Prefill
+(rows != 1) goes to offload.offloaded_forward, as in the reference
+(bin/devcache.py:270-271).
+"""
+from __future__ import annotations
+
+import sys as _sys
+
+import torch
+
+import hipfetch
+from fp8_moe import fp8_moe_forward
+
+EXPERT_BYTES = 3_146_496
+
+# Accepted for drop-in compatibility with --fetch-backend (bin/devcache.py:191):
+# every value selects the one HIP fetch kernel.  The reference's two backends
+# existed because one was Triton; there is only one implementation here.
+FETCH_BACKEND = "hip"
+_BACKENDS = ("hip", "cpp", "triton")
+_BACKEND_NOTED = False
+# Grid x-dimension of the fetch kernel per job (bin/devcache.py:193).
+CPP_BLOCKS_PER_JOB = 64
+_dev_ptr_cache: dict[int, int] = {}
+
+
+def init_dev_cache(experts, device: torch.device, capacity: int) -> None:
+    """Allocate one layer's cache buffers and slot table (bin/devcache.py:138-167)."""
+    lib = hipfetch.require()
+    n_experts = experts.num_experts
+    if not 1 <= capacity <= 4096:
+        raise ValueError(f"capacity must be in [1, 4096], got {capacity}")
+    experts._dc_cap = capacity
+    experts._dc_slot_of = torch.empty((n_experts,), dtype=torch.int32, device=device)
+    experts._dc_slot_expert = torch.empty((capacity,), dtype=torch.int32, device=device)
+    # stamps -C..-1 so the first `capacity` misses take slots 0, 1, 2, ...
+    experts._dc_stamp = torch.empty((capacity,), dtype=torch.int64, device=device)
+    experts._dc_step = torch.empty((1,), dtype=torch.int64, device=device)
+    with torch.cuda.device(device):
+        lib.slots_init(experts._dc_slot_of, experts._dc_slot_expert, experts._dc_stamp,
+                       experts._dc_step)
+
+    def buf(src):
+        return torch.zeros((capacity, *src.shape[1:]), dtype=src.dtype, device=device)
+
+    experts._dc_w13 = buf(experts.w13_weight)
+    experts._dc_w2 = buf(experts.w2_weight)
+    experts._dc_s13 = torch.ones((capacity, *experts.w13_scale_inv.shape[1:]),
+                                 dtype=torch.float32, device=device)
+    experts._dc_s2 = torch.ones((capacity, *experts.w2_scale_inv.shape[1:]),
+                                dtype=torch.float32, device=device)
+    # scratch, allocated once so nothing allocates inside a captured region
+    kmax = max(8, getattr(experts, "_dc_kmax", 8))
+    experts._dc_out = torch.zeros(kmax, dtype=torch.int32, device=device)
+    experts._dc_fslot = torch.zeros(kmax, dtype=torch.int32, device=device)
+    experts._dc_fexp = torch.zeros(kmax, dtype=torch.int32, device=device)
+    experts._dc_nmiss = torch.zeros(1, dtype=torch.int32, device=device)
+    experts._dc_stats = torch.zeros(2, dtype=torch.int64, device=device)
+    experts._dc_pairs = None
+
+
+def reset_dev_cache(experts) -> None:
+    """Empty an initialised cache in place: same tensors (so a captured graph
+    that references them stays valid), table back to its initial state,
+    device hit/miss counters cleared.  Slot contents are left as they are;
+    an empty slot is never handed out before it is filled."""
+    lib = hipfetch.require()
+    with torch.cuda.device(experts._dc_slot_of.device):
+        lib.slots_init(experts._dc_slot_of, experts._dc_slot_expert, experts._dc_stamp,
+                       experts._dc_step)
+        experts._dc_stats.zero_()
+
+
+def _copy_pairs(experts):
+    """(host, cache) byte views moved on a miss (bin/devcache.py:170-181)."""
+    return (
+        (experts.w13_weight.view(torch.uint8).reshape(-1),
+         experts._dc_w13.view(torch.uint8).reshape(-1)),
+        (experts.w2_weight.view(torch.uint8).reshape(-1),
+         experts._dc_w2.view(torch.uint8).reshape(-1)),
+        (experts.w13_scale_inv.view(torch.uint8).reshape(-1),
+         experts._dc_s13.view(torch.uint8).reshape(-1)),
+        (experts.w2_scale_inv.view(torch.uint8).reshape(-1),
+         experts._dc_s2.view(torch.uint8).reshape(-1)),
+    )
+
+
+def _device_ptr(lib, host: torch.Tensor) -> int:
+    """Device address of a page-locked host tensor, cached by host address
+    (bin/devcache.py:194,213-217)."""
+    key = host.data_ptr()
+    base = _dev_ptr_cache.get(key)
+    if base is None:
+        if not host.is_pinned():
+            raise RuntimeError("expected a contiguous page-locked CPU tensor; run pin_experts "
+                               "first (offload.pin_experts)")
+        base = lib.device_ptr_of(key)
+        _dev_ptr_cache[key] = base
+    return base
+
+
+def _fetch_pairs(experts, lib):
+    """[(src device address, dst address, bytes per record)] for the 4 buffers."""
+    pairs = experts._dc_pairs
+    if pairs is None:
+        pairs = []
+        for host, cache in _copy_pairs(experts):
+            per = host.numel() // experts.num_experts
+            pairs.append((_device_ptr(lib, host), cache.data_ptr(), per))
+        experts._dc_pairs = pairs
+    return pairs
+
+
+def _note_backend() -> None:
+    global _BACKEND_NOTED
+    if FETCH_BACKEND not in _BACKENDS:
+        raise ValueError(f"FETCH_BACKEND must be one of {_BACKENDS}, got {FETCH_BACKEND!r}")
+    if FETCH_BACKEND != "hip" and not _BACKEND_NOTED:
+        _BACKEND_NOTED = True
+        print(f"fetch backend {FETCH_BACKEND!r} maps to the HIP fetch kernel",
+              file=_sys.stderr, flush=True)
+
+
+def dev_resolve_and_fetch(experts, topk_ids: torch.Tensor) -> torch.Tensor:
+    """Resolve ids to slots, fetching misses.  Returns slot indices (int32),
+    no sync (bin/devcache.py:230-255)."""
+    _note_backend()
+    lib = hipfetch.require()
+    k = topk_ids.numel()
+    if k > experts._dc_cap:
+        # more ids than slots would make the table hand out a slot twice in
+        # one call; the reference's gather path handles such calls
+        raise ValueError(f"{k} ids exceed the cache capacity {experts._dc_cap}; "
+                         "use offload.offloaded_forward for this call")
+    if k > experts._dc_out.numel():
+        raise ValueError(f"{k} ids exceed the preallocated scratch ({experts._dc_out.numel()})")
+    ids = topk_ids.reshape(-1)
+    if ids.dtype not in (torch.int32, torch.int64):
+        ids = ids.to(torch.int32)
+    lib.resolve_slots(ids, experts._dc_slot_of, experts._dc_slot_expert, experts._dc_stamp,
+                      experts._dc_step, experts._dc_out, experts._dc_fslot, experts._dc_fexp,
+                      experts._dc_nmiss, experts._dc_stats)
+    lib.fetch(_fetch_pairs(experts, lib), experts._dc_fexp, experts._dc_fslot,
+              experts._dc_nmiss, max_jobs=k, blocks_per_job=CPP_BLOCKS_PER_JOB)
+    return experts._dc_out[:k]
+
+
+def dev_cached_forward(self, x, topk_ids, topk_weights):
+    """MoEExperts.forward using the device-resident cache (bin/devcache.py:258-277).
+    Decode only; other calls go to the gather path."""
+    import offload
+    if topk_ids.shape[0] != 1 or not getattr(self, "_dc_cap", 0):
+        return offload.offloaded_forward(self, x, topk_ids, topk_weights)
+    slots = dev_resolve_and_fetch(self, topk_ids)
+    return fp8_moe_forward(x, slots.reshape(topk_ids.shape), topk_weights, self._dc_w13,
+                           self._dc_s13, self._dc_w2, self._dc_s2)
+
+
+def install_dev_cache(model, device, capacity: int) -> int:
+    """Allocate the device cache on every offloaded layer and swap in the
+    forward.  Returns the number of layers (bin/devcache.py:280-301).
+    Requires the host expert tensors to be page-locked (pin_experts)."""
+    from moe import MoEExperts
+    n = 0
+    for layer in model.backbone.model.layers:
+        experts = getattr(layer.mlp, "experts", None)
+        if experts is None or experts.w13_weight.device.type != "cpu":
+            continue
+        if not experts.w13_weight.is_pinned():
+            raise RuntimeError(
+                "device cache needs pinned expert tensors; run pin_experts first")
+        init_dev_cache(experts, device, capacity)
+        n += 1
+    MoEExperts.forward = dev_cached_forward
+    return n
+
+
+def cache_stats(experts) -> tuple[int, int]:
+    """(hits, misses) counted on the device since init (one host sync)."""
+    s = experts._dc_stats.tolist()
+    return int(s[0]), int(s[1])

@@ -1,0 +1,275 @@
+"""Load libmoeoffload.so, the HIP (gfx950) kernels of the expert-offload path.
+
+Counterpart of bin/cppfetch.py: `load()` returns the bound library or None,
+and never raises; `last_error()` says why it is None.  Unlike the reference,
+nothing falls back to another backend when the library is missing: the
+callers in devcache/offload/fp8_moe raise through `require()`, so a GPU run
+without the native code fails loudly instead of silently running something
+else.
+
+The library is built in-tree by `python drama3-offloading_amd/build.py` (no
+JIT, no per-user cache).  torch is imported before the library is opened so
+that the library's libamdhip64.so.7 dependency resolves to the runtime torch
+already loaded; `load()` verifies that, because a second HIP runtime in the
+process would not understand torch's streams or allocations.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = Path(os.environ.get("MOE_OFFLOAD_LIB", HERE / "libmoeoffload.so"))
+
+MOE_I32, MOE_I64, MOE_F32, MOE_BF16 = 0, 1, 2, 3
+
+_lib = None
+_err: str | None = None
+
+
+class ExpertStrides(C.Structure):
+    """moe_expert_strides (include/moe_offload.h)."""
+    _fields_ = [("w13", C.c_int64), ("s13", C.c_int64), ("w2", C.c_int64), ("s2", C.c_int64)]
+
+
+class FetchPair(C.Structure):
+    """moe_fetch_pair (include/moe_offload.h)."""
+    _fields_ = [("src", C.c_void_p), ("dst", C.c_void_p), ("bytes", C.c_int64)]
+
+
+_vp, _i32, _i64, _sz = C.c_void_p, C.c_int32, C.c_int64, C.c_size_t
+
+# name -> (restype, argtypes); every entry point of include/moe_offload.h
+SIGNATURES = {
+    "moe_last_error": (C.c_char_p, []),
+    "moe_version": (C.c_char_p, []),
+    "moe_hip_runtime_path": (C.c_char_p, []),
+    "moe_host_alloc": (C.c_int, [C.POINTER(_vp), _sz, C.c_int]),
+    "moe_host_free": (C.c_int, [_vp]),
+    "moe_device_ptr_of": (C.c_int, [_vp, C.POINTER(_vp)]),
+    "moe_slots_init": (C.c_int, [_vp, _i32, _vp, _vp, _i32, _vp, _vp]),
+    "moe_resolve_slots": (C.c_int, [_vp, _i32, _i32, _vp, _i32, _vp, _vp, _i32, _vp, _vp, _vp,
+                                    _vp, _vp, _vp, _vp]),
+    "moe_fetch": (C.c_int, [C.POINTER(FetchPair), _i32, _vp, _vp, _vp, _i32, _i32, _vp]),
+    "moe_router_topk": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _i32, _vp,
+                                  _i32, _vp]),
+    "moe_fp8_moe_workspace": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "moe_fp8_moe_forward": (C.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
+                                      _i32, _i32, _i32, _vp, _vp, _sz, _vp]),
+    "moe_fp8_moe_forward_ex": (C.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp,
+                                         _vp, _i32, _i32, _i32, C.POINTER(ExpertStrides), _vp,
+                                         _vp, _sz, _i32, _vp]),
+    "moe_permute": (C.c_int, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "moe_unpermute": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp]),
+    "moe_unique_inverse": (C.c_int, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
+}
+
+
+def declared_symbols() -> list[str]:
+    """Every function declared in include/moe_offload.h (parsed from the text)."""
+    import re
+    hdr = (HERE.parent / "include" / "moe_offload.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\**\s+\**(moe_[a-z_0-9]+)\(", hdr,
+                                 flags=re.M)))
+
+
+class NativeError(RuntimeError):
+    pass
+
+
+class Native:
+    """Thin typed wrapper over the C ABI.  Tensor arguments are passed by
+    data_ptr(); every call is enqueued on torch's current stream."""
+
+    def __init__(self, cdll: C.CDLL):
+        self.cdll = cdll
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(cdll, name)
+            fn.restype = res
+            fn.argtypes = args
+
+    # ------------------------------------------------------------ helpers
+    def _check(self, rc: int, what: str) -> None:
+        if rc != 0:
+            msg = self.cdll.moe_last_error().decode(errors="replace")
+            raise NativeError(f"{what} failed ({rc}): {msg}")
+
+    @staticmethod
+    def stream() -> int:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+
+    @staticmethod
+    def _ptr(t) -> int | None:
+        return None if t is None else t.data_ptr()
+
+    @staticmethod
+    def _dtype_code(t) -> int:
+        import torch
+        return {torch.int32: MOE_I32, torch.int64: MOE_I64, torch.float32: MOE_F32,
+                torch.bfloat16: MOE_BF16}[t.dtype]
+
+    def version(self) -> str:
+        return self.cdll.moe_version().decode()
+
+    def hip_runtime_path(self) -> str:
+        return self.cdll.moe_hip_runtime_path().decode()
+
+    # ------------------------------------------------------------ host pool
+    def host_alloc(self, nbytes: int, noncoherent: bool = False) -> int:
+        p = C.c_void_p()
+        self._check(self.cdll.moe_host_alloc(C.byref(p), nbytes, 1 if noncoherent else 0),
+                    "moe_host_alloc")
+        return p.value
+
+    def host_free(self, ptr: int) -> None:
+        self._check(self.cdll.moe_host_free(ptr), "moe_host_free")
+
+    def device_ptr_of(self, host_ptr: int) -> int:
+        d = C.c_void_p()
+        self._check(self.cdll.moe_device_ptr_of(host_ptr, C.byref(d)), "moe_device_ptr_of")
+        return d.value
+
+    # ------------------------------------------------------------ slots
+    def slots_init(self, slot_of, slot_expert, stamp, step) -> None:
+        self._check(self.cdll.moe_slots_init(slot_of.data_ptr(), slot_of.numel(),
+                                             slot_expert.data_ptr(), stamp.data_ptr(),
+                                             slot_expert.numel(), step.data_ptr(), self.stream()),
+                    "moe_slots_init")
+
+    def resolve_slots(self, ids, slot_of, slot_expert, stamp, step, out_slot, fetch_slot,
+                      fetch_expert, nmiss, stats=None) -> None:
+        self._check(self.cdll.moe_resolve_slots(
+            ids.data_ptr(), self._dtype_code(ids), ids.numel(), slot_of.data_ptr(),
+            slot_of.numel(), slot_expert.data_ptr(), stamp.data_ptr(), slot_expert.numel(),
+            step.data_ptr(), out_slot.data_ptr(), fetch_slot.data_ptr(), fetch_expert.data_ptr(),
+            nmiss.data_ptr(), self._ptr(stats), self.stream()), "moe_resolve_slots")
+
+    # ------------------------------------------------------------ fetch
+    def fetch(self, pairs, fetch_expert, fetch_slot, nmiss, max_jobs: int,
+              blocks_per_job: int) -> None:
+        """pairs: [(src_device_addr, dst_device_addr, bytes_per_record), ...]"""
+        arr = (FetchPair * len(pairs))(*[FetchPair(s, d, b) for s, d, b in pairs])
+        self._check(self.cdll.moe_fetch(arr, len(pairs), fetch_expert.data_ptr(),
+                                        fetch_slot.data_ptr(), nmiss.data_ptr(), max_jobs,
+                                        blocks_per_job, self.stream()), "moe_fetch")
+
+    # ------------------------------------------------------------ router
+    def router_topk(self, x, w, bias, top_k: int, logits, ids, weights) -> None:
+        T, H = x.shape
+        E = w.shape[0]
+        self._check(self.cdll.moe_router_topk(
+            x.data_ptr(), w.data_ptr(), self._ptr(bias), T, H, E, top_k, logits.data_ptr(),
+            ids.data_ptr(), self._dtype_code(ids), weights.data_ptr(), self._dtype_code(weights),
+            self.stream()), "moe_router_topk")
+
+    # ------------------------------------------------------------ experts
+    def fp8_moe_workspace(self, tokens, top_k, n_experts, hidden, inter) -> int:
+        return int(self.cdll.moe_fp8_moe_workspace(tokens, top_k, n_experts, hidden, inter))
+
+    def fp8_moe_forward(self, x, ids, weights, w13, s13, w2, s2, out, workspace,
+                        mode: int = 0) -> None:
+        """w13/s13/w2/s2 may be strided along the expert axis (views into a
+        packed record pool); every other dimension must be contiguous."""
+        T, H = x.shape
+        K = ids.shape[-1]
+        n = w13.shape[0]
+        inter = w2.shape[-1]
+        for t in (w13, s13, w2, s2):
+            if not t[0].is_contiguous():
+                raise ValueError("expert weights must be contiguous within an expert")
+        es = ExpertStrides(w13.stride(0), s13.stride(0), w2.stride(0), s2.stride(0))
+        self._check(self.cdll.moe_fp8_moe_forward_ex(
+            x.data_ptr(), ids.data_ptr(), self._dtype_code(ids), weights.data_ptr(),
+            self._dtype_code(weights), T, K, w13.data_ptr(), s13.data_ptr(), w2.data_ptr(),
+            s2.data_ptr(), n, H, inter, C.byref(es), out.data_ptr(), workspace.data_ptr(),
+            workspace.numel() * workspace.element_size(), mode, self.stream()),
+            "moe_fp8_moe_forward")
+
+    # ------------------------------------------------------------ permute
+    def permute(self, ids, n_experts: int, counts, offsets, sorted_pairs, pair_pos) -> None:
+        T, K = ids.shape
+        self._check(self.cdll.moe_permute(ids.data_ptr(), self._dtype_code(ids), T, K, n_experts,
+                                          counts.data_ptr(), offsets.data_ptr(),
+                                          sorted_pairs.data_ptr(), pair_pos.data_ptr(),
+                                          self.stream()), "moe_permute")
+
+    def unique_inverse(self, ids, n_experts: int, counts, n_unique, uniq, rank_of,
+                       inverse) -> None:
+        T, K = ids.shape
+        self._check(self.cdll.moe_unique_inverse(
+            ids.data_ptr(), self._dtype_code(ids), T, K, n_experts, counts.data_ptr(),
+            n_unique.data_ptr(), uniq.data_ptr(), rank_of.data_ptr(), inverse.data_ptr(),
+            self.stream()), "moe_unique_inverse")
+
+    def unpermute(self, y, pair_pos, weights, out) -> None:
+        T, K = weights.shape
+        H = y.shape[-1]
+        self._check(self.cdll.moe_unpermute(y.data_ptr(), pair_pos.data_ptr(),
+                                            weights.data_ptr(), self._dtype_code(weights), T, K,
+                                            H, out.data_ptr(), self.stream()), "moe_unpermute")
+
+
+def _torch_hip_runtime() -> str | None:
+    """Path of the libamdhip64 torch loaded, from /proc/self/maps."""
+    try:
+        with open("/proc/self/maps") as fh:
+            for line in fh:
+                if "libamdhip64.so" in line:
+                    return line.split()[-1]
+    except OSError:
+        pass
+    return None
+
+
+def load(verbose: bool = False):
+    """Return the bound library, or None with the reason in last_error().
+    Never raises (bin/cppfetch.py:141-179 contract)."""
+    global _lib, _err
+    if _lib is not None or _err is not None:
+        return _lib
+    try:
+        import torch  # noqa: F401  -- load torch's HIP runtime first
+    except Exception as exc:                                   # noqa: BLE001
+        _err = f"torch import failed: {type(exc).__name__}: {exc}"
+        return None
+    if not LIB_PATH.is_file():
+        _err = (f"missing {LIB_PATH}; build it with "
+                f"`python drama3-offloading_amd/build.py` (needs hipcc)")
+        return None
+    try:
+        cdll = C.CDLL(str(LIB_PATH), mode=C.RTLD_GLOBAL)
+        lib = Native(cdll)
+    except (OSError, AttributeError) as exc:
+        _err = f"{type(exc).__name__}: {exc}"
+        return None
+    ours = lib.hip_runtime_path()
+    theirs = _torch_hip_runtime()
+    if theirs and ours and os.path.realpath(ours) != os.path.realpath(theirs):
+        _err = (f"libmoeoffload bound HIP runtime {ours} but torch uses {theirs}; "
+                f"two HIP runtimes in one process cannot share streams")
+        return None
+    if verbose:
+        print(f"libmoeoffload: {LIB_PATH} ({lib.version()}), HIP runtime {ours}")
+    _lib = lib
+    return _lib
+
+
+def last_error() -> str | None:
+    return _err
+
+
+def require() -> Native:
+    """The library, or RuntimeError naming why it cannot be used."""
+    lib = load()
+    if lib is None:
+        raise RuntimeError(f"libmoeoffload (HIP kernels) unavailable: {_err}")
+    return lib
+
+
+def reset() -> None:
+    """Forget a previous load result (tests)."""
+    global _lib, _err
+    _lib = None
+    _err = None

@@ -1,0 +1,215 @@
+/*
+ * moe_offload.h -- C ABI of libmoeoffload.so, the MI355X (gfx950) expert-offload
+ * MoE path.
+ *
+ * Conventions for every entry point:
+ *   - arguments are plain pointers and sizes; device pointers are HBM
+ *     addresses, "host" pointers are page-locked host memory;
+ *   - kernels are enqueued on `stream` (a hipStream_t; NULL = the null
+ *     stream) and never synchronise, never allocate and never record a
+ *     memset, so every call can sit inside a captured hipGraph;
+ *   - every quantity that changes from call to call at replay time (expert
+ *     ids, miss counts, the LRU step) is read from device memory by the
+ *     kernel, never baked into a launch argument;
+ *   - the return value is 0 on success, MOE_EINVAL (-1) when a precondition
+ *     fails (nothing is enqueued), or the positive hipError_t of a failed
+ *     launch; moe_last_error() then describes the failure (thread-local).
+ */
+#ifndef MOE_OFFLOAD_H
+#define MOE_OFFLOAD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOE_OK 0
+#define MOE_EINVAL (-1)
+
+/* dtype codes for arguments that accept more than one element type */
+#define MOE_I32 0
+#define MOE_I64 1
+#define MOE_F32 2
+#define MOE_BF16 3
+
+/* ------------------------------------------------------------------ misc */
+
+/* Text of the last failure on this thread ("" if none). */
+const char* moe_last_error(void);
+
+/* Library version string, and the path of the HIP runtime library this
+ * library resolved its HIP symbols from (to check it shares the caller's
+ * runtime). */
+const char* moe_version(void);
+const char* moe_hip_runtime_path(void);
+
+/* ------------------------------------------------------------- host pool */
+
+/* Page-locked, device-mapped host allocation for an expert pool.
+ * flags: 0 = coherent (hipHostMallocMapped), 1 = non-coherent
+ * (hipHostMallocMapped | hipHostMallocNonCoherent).
+ * Replaces the per-layer Tensor.pin_memory() of pin_experts
+ * (bin/offload.py:664-699) with one region per pool. */
+int moe_host_alloc(void** host_ptr, size_t bytes, int flags);
+int moe_host_free(void* host_ptr);
+
+/* Device-side address of page-locked host memory (hipHostGetDevicePointer).
+ * Replaces device_ptr_of (csrc/fetch_experts.cu:40-47). Fails with
+ * MOE_EINVAL for memory the runtime does not know as page-locked (the
+ * reference's "expected a contiguous page-locked CPU tensor"). */
+int moe_device_ptr_of(const void* host_ptr, void** dev_ptr);
+
+/* ------------------------------------------------------------ slot table */
+
+/* Initialise one layer's slot table: slot_of[0..n_experts) = -1,
+ * slot_expert[0..cap) = -1, slot_stamp[c] = -(cap - c), step = 0.
+ * Replaces the table set-up of init_dev_cache (bin/devcache.py:146-152). */
+int moe_slots_init(int32_t* slot_of, int32_t n_experts, int32_t* slot_expert,
+                   int64_t* slot_stamp, int32_t cap, int64_t* step, void* stream);
+
+/* Resolve k expert ids to cache slots on the device, queueing misses.
+ * Replaces _resolve_slots (bin/devcache.py:45-98) with identical decisions:
+ * step += 1; a hit stamps its slot; a miss takes the slot with the smallest
+ * stamp (lowest index on a tie), evicting its expert.  Outputs
+ * out_slot[k], fetch_slot[<=k], fetch_expert[<=k], nmiss[1].
+ * ids_dtype: MOE_I32 or MOE_I64.  stats (nullable) is int64[2]
+ * {hits, misses} accumulated on the device -- the reference keeps no such
+ * counter (bin/devcache.py:274).  Constraints: 1 <= cap <= 4096,
+ * n_experts >= 1; ids must lie in [0, n_experts) (an out-of-range id is
+ * ignored and reported as slot -1). */
+int moe_resolve_slots(const void* ids, int32_t ids_dtype, int32_t k,
+                      int32_t* slot_of, int32_t n_experts,
+                      int32_t* slot_expert, int64_t* slot_stamp, int32_t cap,
+                      int64_t* step, int32_t* out_slot, int32_t* fetch_slot,
+                      int32_t* fetch_expert, int32_t* nmiss, int64_t* stats,
+                      void* stream);
+
+/* ----------------------------------------------------------------- fetch */
+
+/* One (host buffer, cache buffer) pair moved on a miss: record j of the
+ * host buffer (src + j * bytes) is copied to slot s of the cache buffer
+ * (dst + s * bytes).  Mirrors _copy_pairs (bin/devcache.py:170-181). */
+typedef struct moe_fetch_pair {
+  const void* src;   /* device-side address of the page-locked host buffer */
+  void* dst;         /* HBM cache buffer */
+  int64_t bytes;     /* bytes per expert record in this buffer */
+} moe_fetch_pair;
+
+/* Copy the queued misses host -> HBM with a zero-copy gather kernel.
+ * Job j < *nmiss copies expert fetch_expert[j] into slot fetch_slot[j] for
+ * every pair; jobs j >= *nmiss (read on the device at run time) retire
+ * without writing.  The grid is (blocks_per_job, max_jobs) x 256 threads.
+ * Replaces fetch_experts/fetch_kernel (csrc/fetch_experts.cu:49-94) and the
+ * four per-buffer launches of _cpp_fetch (bin/devcache.py:197-220) with one
+ * launch.  Preconditions: 1 <= npairs <= 4; each pair's src, dst and bytes
+ * are 4-byte aligned (16-byte aligned pairs take the 16-byte path);
+ * 1 <= max_jobs <= 65535; 1 <= blocks_per_job <= 65535. */
+int moe_fetch(const moe_fetch_pair* pairs, int32_t npairs,
+              const int32_t* fetch_expert, const int32_t* fetch_slot,
+              const int32_t* nmiss, int32_t max_jobs, int32_t blocks_per_job,
+              void* stream);
+
+/* ---------------------------------------------------------------- router */
+
+/* Router: logits = x . W^T (+ bias), softmax, top_k, renormalise.
+ * x [tokens, hidden] bf16, w [n_experts, hidden] bf16, bias [n_experts]
+ * f32 or NULL.  Writes ids [tokens, top_k] (ids_dtype MOE_I32/MOE_I64),
+ * weights [tokens, top_k] (w_dtype MOE_F32/MOE_BF16), and the f32 logits
+ * [tokens, n_experts] to `logits` (caller-provided, also the workspace).
+ * Logits are float32 roundings of float64-accumulated exact products;
+ * selection is by descending logit, ties to the lower index.
+ * Replaces upstream's gate + softmax + topk + norm_topk_prob
+ * (moe.py:217-220 per notes/01-static-findings.md:133-138).
+ * Constraints: hidden % 8 == 0, 1 <= top_k <= 32, top_k <= n_experts <= 4096. */
+int moe_router_topk(const void* x, const void* w, const float* bias,
+                    int32_t tokens, int32_t hidden, int32_t n_experts,
+                    int32_t top_k, float* logits, void* ids, int32_t ids_dtype,
+                    void* weights, int32_t w_dtype, void* stream);
+
+/* ------------------------------------------------------- expert compute */
+
+/* Workspace bytes moe_fp8_moe_forward needs for this shape. */
+size_t moe_fp8_moe_workspace(int32_t tokens, int32_t top_k, int32_t n_experts,
+                             int32_t hidden, int32_t inter);
+
+/* W8A8 block-FP8 MoE forward, the counterpart of upstream
+ * fp8_moe_forward(x, topk_ids, topk_weights, w13, s13, w2, s2) as called at
+ * bin/devcache.py:275-277 and bin/offload.py:239.
+ *   x        [tokens, hidden] bf16
+ *   ids      [tokens, top_k]  MOE_I32/MOE_I64, index into the expert axis
+ *   weights  [tokens, top_k]  MOE_F32/MOE_BF16
+ *   w13      [n_experts, 2*inter, hidden] e4m3fn (gate rows, then up rows)
+ *   s13      [n_experts, 2*inter/128, hidden/128] f32 scale_inv
+ *   w2       [n_experts, hidden, inter] e4m3fn
+ *   s2       [n_experts, hidden/128, inter/128] f32 scale_inv
+ *   out      [tokens, hidden] bf16
+ * Activations are quantised per token per 128 columns (scale amax/448).
+ * Dispatch: decode-sized calls use the per-pair GEMV kernels, larger ones the
+ * permuted grouped GEMM; both give bit-identical rows.
+ * Constraints: hidden % 128 == 0, inter % 128 == 0, 1 <= top_k <= 16. */
+int moe_fp8_moe_forward(const void* x, const void* ids, int32_t ids_dtype,
+                        const void* weights, int32_t w_dtype, int32_t tokens,
+                        int32_t top_k, const void* w13, const float* s13,
+                        const void* w2, const float* s2, int32_t n_experts,
+                        int32_t hidden, int32_t inter, void* out,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* Distance between consecutive experts of each weight buffer, in elements
+ * of that buffer (e4m3 bytes for w13/w2, floats for s13/s2).  Dense
+ * [n, ...] buffers use the product of the trailing dimensions; a packed
+ * record pool (w13|w2|s13|s2 per record) uses the record size. */
+typedef struct moe_expert_strides {
+  int64_t w13;
+  int64_t s13;
+  int64_t w2;
+  int64_t s2;
+} moe_expert_strides;
+
+/* moe_fp8_moe_forward with explicit expert strides (NULL = dense) and a
+ * kernel choice: mode 0 automatic, 1 per-pair GEMV, 2 grouped. */
+int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t ids_dtype,
+                           const void* weights, int32_t w_dtype,
+                           int32_t tokens, int32_t top_k, const void* w13,
+                           const float* s13, const void* w2, const float* s2,
+                           int32_t n_experts, int32_t hidden, int32_t inter,
+                           const moe_expert_strides* strides, void* out,
+                           void* workspace, size_t workspace_bytes,
+                           int32_t mode, void* stream);
+
+/* ------------------------------------------------------ permute/unpermute */
+
+/* Stable token->expert grouping of ids [tokens, top_k]:
+ * counts[n_experts], offsets[n_experts + 1] (exclusive scan),
+ * sorted_pairs[tokens*top_k] (pair p = t*top_k + k, sorted by expert, stable)
+ * and pair_pos[tokens*top_k] (the inverse).  The counterpart of the
+ * reference's torch.unique(return_inverse) remap (bin/offload.py:157-158,
+ * 447-448) and of the sort inside upstream fp8_moe_forward.
+ * Constraints: n_experts <= 4096, tokens*top_k <= 1<<24. */
+int moe_permute(const void* ids, int32_t ids_dtype, int32_t tokens,
+                int32_t top_k, int32_t n_experts, int32_t* counts,
+                int32_t* offsets, int32_t* sorted_pairs, int32_t* pair_pos,
+                void* stream);
+
+/* out[t] = sum_k weights[t,k] * y[pair_pos[t*top_k+k]] in k order, as bf16.
+ * y [tokens*top_k, hidden] f32. */
+int moe_unpermute(const float* y, const int32_t* pair_pos, const void* weights,
+                  int32_t w_dtype, int32_t tokens, int32_t top_k,
+                  int32_t hidden, void* out, void* stream);
+
+/* Distinct experts of ids in ascending order and the renumbering of every
+ * pair into that list (torch.unique(sorted, return_inverse), the remap of
+ * bin/offload.py:157-158): n_unique[1], uniq[<=n_experts],
+ * inverse[tokens*top_k] int32.  Needs counts/offsets from moe_permute.
+ * Also writes rank_of[n_experts] (position in uniq, -1 when absent). */
+int moe_unique_inverse(const void* ids, int32_t ids_dtype, int32_t tokens,
+                       int32_t top_k, int32_t n_experts, const int32_t* counts,
+                       int32_t* n_unique, int32_t* uniq, int32_t* rank_of,
+                       int32_t* inverse, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_OFFLOAD_H */

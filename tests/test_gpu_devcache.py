@@ -1,0 +1,145 @@
+"""The device cache end to end (bin/test_devcache.py, restated): outputs
+through the cache equal the all-resident outputs EXACTLY over 40 steps at
+capacities 16/32/64 of 64 experts with real shapes, eviction exercised, and a
+captured step replays DYNAMIC with the right bytes."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import say
+
+pytestmark = pytest.mark.gpu
+E, H, I, K = 64, 2048, 512, 8
+
+
+@pytest.fixture(scope="module")
+def pair(dev):
+    import moe
+    import synth
+    ref = moe.MoEExperts(E, H, I, device=dev)
+    synth.fill_experts(ref, seed=0, recipe="devtest")
+    host = moe.MoEExperts(E, H, I, device="cpu")
+    for n in ("w13_weight", "w2_weight", "w13_scale_inv", "w2_scale_inv"):
+        setattr(host, n, getattr(ref, n).cpu().pin_memory())
+    return ref, host
+
+
+@pytest.mark.parametrize("cap", [16, 32, E])
+def test_cache_is_bit_exact_against_resident(lib, dev, pair, cap):
+    import devcache
+    from fp8_moe import fp8_moe_forward
+    ref, host = pair
+    devcache.init_dev_cache(host, dev, cap)
+    torch.manual_seed(cap)
+    say(f"devcache: capacity {cap}")
+    for step in range(40):
+        x = torch.randn(1, H, device=dev).to(torch.bfloat16)
+        ids = torch.randperm(E, device=dev)[:K].unsqueeze(0)
+        w = torch.rand(1, K, device=dev).to(torch.bfloat16)
+        w = w / w.sum(-1, keepdim=True)
+        want = fp8_moe_forward(x, ids, w, ref.w13_weight, ref.w13_scale_inv, ref.w2_weight,
+                               ref.w2_scale_inv)
+        slots = devcache.dev_resolve_and_fetch(host, ids)
+        got = fp8_moe_forward(x, slots.reshape(ids.shape), w, host._dc_w13, host._dc_s13,
+                              host._dc_w2, host._dc_s2)
+        assert torch.equal(want, got), f"step {step}"
+    occupied = int((host._dc_slot_expert >= 0).sum())
+    assert occupied == cap
+    hits, misses = devcache.cache_stats(host)
+    assert hits + misses == 40 * K and (cap >= E or misses > cap)
+
+
+def test_capture_dynamic_and_bytes(lib, dev, pair):
+    import devcache
+    from fp8_moe import fp8_moe_forward
+    ref, host = pair
+    devcache.init_dev_cache(host, dev, 32)
+    ids_warm = torch.randperm(E, device=dev)[:K].unsqueeze(0)
+    ids_cap = torch.randperm(E, device=dev)[:K].unsqueeze(0)
+    ids_rep = torch.randperm(E, device=dev)[:K].unsqueeze(0)
+    ids_live = ids_warm.clone()
+
+    def run():
+        return devcache.dev_resolve_and_fetch(host, ids_live)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            run()
+    torch.cuda.current_stream().wait_stream(s)
+    ids_live.copy_(ids_cap)
+    g = torch.cuda.CUDAGraph()
+    say("devcache: capture")
+    with torch.cuda.graph(g):
+        out = run()
+    ids_live.copy_(ids_rep)
+    g.replay()
+    torch.cuda.synchronize()
+    slots = out.clone()
+    occupant = host._dc_slot_expert[slots.long()]
+    assert torch.equal(occupant, ids_rep.reshape(-1).int()), "replay served the wrong experts"
+    x = torch.randn(1, H, device=dev).to(torch.bfloat16)
+    w = torch.rand(1, K, device=dev)
+    w = w / w.sum(-1, keepdim=True)
+    want = fp8_moe_forward(x, ids_rep, w, ref.w13_weight, ref.w13_scale_inv, ref.w2_weight,
+                           ref.w2_scale_inv)
+    got = fp8_moe_forward(x, slots.reshape(1, K), w, host._dc_w13, host._dc_s13, host._dc_w2,
+                          host._dc_s2)
+    assert torch.equal(want, got)
+
+
+def test_whole_decode_layer_graph_replays_match_eager(lib, dev, pair):
+    """route -> resolve -> fetch -> experts captured once; several replays,
+    eager work and syncs in between, each checked against the same step
+    run eagerly on a twin cache."""
+    import devcache
+    import moe
+    import synth
+    from fp8_moe import fp8_moe_forward
+    ref, host = pair
+    host2 = moe.MoEExperts(E, H, I, device="cpu")
+    for n in ("w13_weight", "w2_weight", "w13_scale_inv", "w2_scale_inv"):
+        setattr(host2, n, getattr(host, n))
+    devcache.init_dev_cache(host, dev, 24)
+    devcache.init_dev_cache(host2, dev, 24)
+    gate = synth.router_weight(5, n_experts=E).to(dev)
+    x_live = torch.zeros((1, H), dtype=torch.bfloat16, device=dev)
+    bias = torch.zeros(E, device=dev)
+    rids = torch.empty((1, K), dtype=torch.int64, device=dev)
+    rw = torch.empty((1, K), dtype=torch.float32, device=dev)
+    rl = torch.empty((1, E), dtype=torch.float32, device=dev)
+    out = torch.empty((1, H), dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device=dev)
+
+    def step(hmod, o):
+        moe.route(x_live, gate, K, bias=bias, out=(rids, rw, rl))
+        sl = devcache.dev_resolve_and_fetch(hmod, rids)
+        fp8_moe_forward(x_live, sl.reshape(1, K), rw, hmod._dc_w13, hmod._dc_s13, hmod._dc_w2,
+                        hmod._dc_s2, out=o, workspace=ws)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step(host, out)
+    torch.cuda.current_stream().wait_stream(s)
+    devcache.reset_dev_cache(host)                    # fresh table after warm-up
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step(host, out)
+    devcache.reset_dev_cache(host)
+    rng = np.random.default_rng(0)
+    twin = torch.empty_like(out)
+    for r in range(6):
+        x_live.copy_(synth.hidden_states(100 + r, 1).to(dev))
+        bias.copy_(torch.from_numpy(rng.gumbel(size=E).astype(np.float32) * 3))
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        _ = torch.randn(1000, device=dev).sum().item()   # eager work between replays
+        step(host2, twin)
+        torch.cuda.synchronize()
+        say(f"graph replay {r}")
+        assert torch.equal(got, twin), f"replay {r}"
+        assert torch.equal(host._dc_slot_of, host2._dc_slot_of)
+        assert torch.equal(host._dc_stamp, host2._dc_stamp)

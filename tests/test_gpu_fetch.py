@@ -1,0 +1,169 @@
+"""Expert fetch on the GPU: byte-exact against the self-identifying pattern
+(bin/bench_hostread.py:257-327), surplus jobs retire, DYNAMIC under graph
+replay (bin/bench_hostread.py:852-934)."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import say
+
+pytestmark = pytest.mark.gpu
+RB = 3_146_496
+W64 = RB // 8
+
+
+@pytest.fixture(scope="module")
+def pool():
+    """256 pinned records carrying (e << 32) | k."""
+    n = 256
+    say("fetch: building 256-record pinned pattern pool")
+    host = torch.empty(n * RB, dtype=torch.uint8, pin_memory=True)
+    h64 = host.view(torch.int64).view(n, W64)
+    k = torch.arange(W64, dtype=torch.int64)
+    for e in range(n):
+        torch.add(k, e << 32, out=h64[e])
+    return host
+
+
+def _check(cache, ids, slot0=0):
+    d64 = cache.view(torch.int64).view(cache.shape[0] // RB, W64)
+    k = torch.arange(W64, dtype=torch.int64, device=cache.device)
+    bad = 0
+    for j, e in enumerate(ids):
+        bad += int((d64[slot0 + j] != k + (int(e) << 32)).sum())
+    return bad
+
+
+def _untouched(cache, lo, hi):
+    d64 = cache.view(torch.int64).view(cache.shape[0] // RB, W64)
+    return bool((d64[lo:hi] == -1).all())
+
+
+@pytest.mark.parametrize("length", [8, 32, 64, 128])
+def test_fetch_zipf_lists_byte_exact(lib, dev, pool, length):
+    rng = np.random.default_rng(20261017 + length)
+    import synth
+    ids = synth.zipf_miss_list(rng, length)
+    cache = torch.full((128 * RB,), 255, dtype=torch.uint8, device=dev)
+    fexp = torch.tensor(ids, dtype=torch.int32, device=dev)
+    fslot = torch.arange(length, dtype=torch.int32, device=dev)
+    nmiss = torch.tensor([length], dtype=torch.int32, device=dev)
+    src = lib.device_ptr_of(pool.data_ptr())
+    say(f"fetch: zipf list of {length}")
+    lib.fetch([(src, cache.data_ptr(), RB)], fexp, fslot, nmiss, max_jobs=length,
+              blocks_per_job=64)
+    torch.cuda.synchronize()
+    assert _check(cache, ids) == 0
+    assert _untouched(cache, length, 128)
+
+
+def test_fetch_honours_device_side_job_count(lib, dev, pool):
+    cache = torch.full((8 * RB,), 255, dtype=torch.uint8, device=dev)
+    ids = [200, 3, 77, 150, 9, 1, 255, 64]
+    fexp = torch.tensor(ids, dtype=torch.int32, device=dev)
+    fslot = torch.tensor([7, 6, 5, 4, 3, 2, 1, 0], dtype=torch.int32, device=dev)
+    nmiss = torch.tensor([3], dtype=torch.int32, device=dev)
+    src = lib.device_ptr_of(pool.data_ptr())
+    say("fetch: nmiss 3 of a grid of 8")
+    lib.fetch([(src, cache.data_ptr(), RB)], fexp, fslot, nmiss, max_jobs=8, blocks_per_job=16)
+    torch.cuda.synchronize()
+    d64 = cache.view(torch.int64).view(8, W64)
+    assert int(d64[7, 1] >> 32) == 200 and int(d64[6, 1] >> 32) == 3 and int(d64[5, 1] >> 32) == 77
+    assert _untouched(cache, 0, 5)
+
+
+def test_fetch_four_pairs_including_unaligned(lib, dev):
+    """The four reference buffers in one launch, plus an 8-byte-per-record
+    pair (the toy-shape case the reference routed to Triton,
+    bin/devcache.py:205-212)."""
+    n, C = 16, 6
+    sizes = [4096, 2048, 48, 8]
+    hosts, caches, pairs = [], [], []
+    for i, b in enumerate(sizes):
+        h = torch.empty(n * b, dtype=torch.uint8, pin_memory=True)
+        h.copy_(torch.randint(0, 256, (n * b,), dtype=torch.uint8))
+        c = torch.zeros(C * b, dtype=torch.uint8, device=dev)
+        hosts.append(h)
+        caches.append(c)
+        pairs.append((lib.device_ptr_of(h.data_ptr()), c.data_ptr(), b))
+    fexp = torch.tensor([5, 0, 15, 9], dtype=torch.int32, device=dev)
+    fslot = torch.tensor([2, 5, 0, 3], dtype=torch.int32, device=dev)
+    nmiss = torch.tensor([4], dtype=torch.int32, device=dev)
+    say("fetch: four pairs incl. 8-byte records")
+    lib.fetch(pairs, fexp, fslot, nmiss, max_jobs=4, blocks_per_job=3)
+    torch.cuda.synchronize()
+    for h, c, b in zip(hosts, caches, sizes):
+        hv, cv = h.view(n, b), c.cpu().view(C, b)
+        for e, s in zip([5, 0, 15, 9], [2, 5, 0, 3]):
+            assert torch.equal(cv[s], hv[e])
+        assert torch.all(cv[1] == 0) and torch.all(cv[4] == 0)
+
+
+@pytest.mark.parametrize("noncoherent", [False, True])
+def test_fetch_from_library_host_pool(lib, dev, noncoherent):
+    n = 8
+    ptr = lib.host_alloc(n * RB, noncoherent=noncoherent)
+    try:
+        import ctypes
+        arr = np.ctypeslib.as_array((ctypes.c_int64 * (n * W64)).from_address(ptr)).reshape(n, W64)
+        arr[:] = (np.arange(n, dtype=np.int64)[:, None] << 32) | np.arange(W64, dtype=np.int64)
+        cache = torch.full((4 * RB,), 255, dtype=torch.uint8, device=dev)
+        fexp = torch.tensor([6, 1, 3, 7], dtype=torch.int32, device=dev)
+        fslot = torch.arange(4, dtype=torch.int32, device=dev)
+        nmiss = torch.tensor([4], dtype=torch.int32, device=dev)
+        say(f"fetch: library host pool noncoherent={noncoherent}")
+        lib.fetch([(lib.device_ptr_of(ptr), cache.data_ptr(), RB)], fexp, fslot, nmiss,
+                  max_jobs=4, blocks_per_job=32)
+        torch.cuda.synchronize()
+        assert _check(cache, [6, 1, 3, 7]) == 0
+    finally:
+        torch.cuda.synchronize()
+        lib.host_free(ptr)
+
+
+def test_pageable_source_is_rejected(lib):
+    import hipfetch
+    t = torch.empty(1 << 20, dtype=torch.uint8)
+    with pytest.raises(hipfetch.NativeError, match="page-locked"):
+        lib.device_ptr_of(t.data_ptr())
+
+
+def test_capture_replays_dynamic_and_honours_job_count(lib, dev, pool):
+    """Sets A (warm-up), C (set before capture), B (set before replay): the
+    replay must serve B (DYNAMIC); a second replay with nmiss halved must
+    leave the surplus slots untouched."""
+    jobs = 8
+    rng = np.random.default_rng(5)
+    perm = rng.permutation(256)
+    A, Cs, B = perm[:8].tolist(), perm[8:16].tolist(), perm[16:24].tolist()
+    cache = torch.full((jobs * RB,), 255, dtype=torch.uint8, device=dev)
+    fexp = torch.tensor(A, dtype=torch.int32, device=dev)
+    fslot = torch.arange(jobs, dtype=torch.int32, device=dev)
+    nmiss = torch.tensor([jobs], dtype=torch.int32, device=dev)
+    src = lib.device_ptr_of(pool.data_ptr())
+    pairs = [(src, cache.data_ptr(), RB)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            lib.fetch(pairs, fexp, fslot, nmiss, jobs, 64)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    fexp.copy_(torch.tensor(Cs, dtype=torch.int32))
+    g = torch.cuda.CUDAGraph()
+    say("fetch: capture")
+    with torch.cuda.graph(g):
+        lib.fetch(pairs, fexp, fslot, nmiss, jobs, 64)
+    cache.fill_(255)
+    fexp.copy_(torch.tensor(B, dtype=torch.int32))
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    assert _check(cache, B) == 0, "replay did not serve the replay-time experts"
+    cache.fill_(255)
+    nmiss.fill_(jobs // 2)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    assert _check(cache, B[:jobs // 2]) == 0
+    assert _untouched(cache, jobs // 2, jobs)

@@ -1,0 +1,111 @@
+"""Router and permute/unpermute on the GPU: expert ids and orderings
+bit-exact against the oracle, weights within float32 rounding."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import say
+from oracle import permute as operm
+from oracle import router as orouter
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("T", [1, 7, 64, 512])
+def test_router_ids_bit_exact(lib, dev, T):
+    import moe
+    import synth
+    x = synth.hidden_states(T, T).to(dev)
+    w = synth.router_weight(T).to(dev)
+    say(f"router: T={T}")
+    ids, wts, logits = moe.route(x, w, 8)
+    torch.cuda.synchronize()
+    o_ids, o_w, o_lg = orouter.route(x.float().cpu().numpy(), w.float().cpu().numpy(), 8)
+    assert np.array_equal(logits.cpu().numpy(), o_lg)
+    assert np.array_equal(ids.cpu().numpy(), o_ids)
+    np.testing.assert_allclose(wts.cpu().numpy(), o_w, rtol=2e-6, atol=1e-7)
+
+
+def test_router_with_bias_int32_bf16_outputs(lib, dev):
+    import moe
+    import synth
+    T = 16
+    x = synth.hidden_states(1, T).to(dev)
+    w = synth.router_weight(1).to(dev)
+    rng = np.random.default_rng(0)
+    bias = torch.from_numpy(synth.decode_route_bias(rng, 1, 1)[0, 0]).to(dev)
+    ids, wts, logits = moe.route(x, w, 8, bias=bias, ids_dtype=torch.int32,
+                                 weights_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    o_ids, o_w, o_lg = orouter.route(x.float().cpu().numpy(), w.float().cpu().numpy(), 8,
+                                     bias.cpu().numpy())
+    assert np.array_equal(ids.cpu().numpy(), o_ids)
+    np.testing.assert_allclose(wts.float().cpu().numpy(), o_w, rtol=8e-3)
+
+
+def test_router_tie_break_lower_index(lib, dev):
+    import moe
+    H, E = 128, 64
+    x = torch.zeros((1, H), dtype=torch.bfloat16, device=dev)
+    w = torch.zeros((E, H), dtype=torch.bfloat16, device=dev)
+    bias = torch.zeros(E, device=dev)
+    bias[[3, 9, 40, 41, 50]] = 1.0
+    bias[[60, 2]] = 0.5
+    ids, wts, _ = moe.route(x, w, 8, bias=bias)
+    torch.cuda.synchronize()
+    assert ids[0].tolist() == [3, 9, 40, 41, 50, 2, 60, 0]
+
+
+def _ids_cases(traces):
+    rows, ids = traces["trace_prefill_rows"], traces["trace_prefill_ids"]
+    cases = [ids[:rows[0]].astype(np.int64), ids[rows[0]:rows[0] + rows[1]].astype(np.int64)]
+    rng = np.random.default_rng(3)
+    cases.append(np.stack([rng.choice(256, 8, replace=False) for _ in range(512)]))
+    cases.append(np.array([[17, 3, 200, 5, 6, 7, 8, 9]]))
+    cases.append(rng.integers(0, 4096, size=(2000, 8)))
+    return cases
+
+
+def test_permute_and_unique_bit_exact(lib, dev, traces):
+    for c, ids_np in enumerate(_ids_cases(traces)):
+        E = 4096 if ids_np.max() >= 256 else 256
+        T, K = ids_np.shape
+        ids = torch.from_numpy(ids_np).to(dev)
+        if c % 2:
+            ids = ids.int()
+        counts = torch.empty(E, dtype=torch.int32, device=dev)
+        offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+        sp = torch.empty(T * K, dtype=torch.int32, device=dev)
+        pos = torch.empty(T * K, dtype=torch.int32, device=dev)
+        nu = torch.empty(1, dtype=torch.int32, device=dev)
+        uniq = torch.full((E,), -7, dtype=torch.int32, device=dev)
+        rank = torch.empty(E, dtype=torch.int32, device=dev)
+        inv = torch.empty(T * K, dtype=torch.int32, device=dev)
+        say(f"permute: case {c} T={T} E={E}")
+        lib.permute(ids, E, counts, offsets, sp, pos)
+        lib.unique_inverse(ids, E, counts, nu, uniq, rank, inv)
+        torch.cuda.synchronize()
+        oc, oo, osp, opos = operm.permute(ids_np, E)
+        assert np.array_equal(counts.cpu().numpy(), oc)
+        assert np.array_equal(offsets.cpu().numpy(), oo)
+        assert np.array_equal(sp.cpu().numpy(), osp)
+        assert np.array_equal(pos.cpu().numpy(), opos)
+        u, iv = operm.unique_inverse(ids_np)
+        n = int(nu.item())
+        assert n == len(u) and np.array_equal(uniq[:n].cpu().numpy(), u)
+        assert np.array_equal(inv.cpu().numpy(), iv.reshape(-1))
+
+
+def test_unpermute_matches_oracle(lib, dev):
+    rng = np.random.default_rng(9)
+    T, K, H = 33, 8, 2048
+    ids_np = np.stack([rng.choice(256, K, replace=False) for _ in range(T)])
+    _, _, _, opos = operm.permute(ids_np, 256)
+    y = torch.randn((T * K, H), generator=torch.Generator().manual_seed(1))
+    w = torch.rand((T, K), generator=torch.Generator().manual_seed(2))
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+    lib.unpermute(y.to(dev), torch.from_numpy(opos).to(dev), w.to(dev), out)
+    torch.cuda.synchronize()
+    want = operm.unpermute(y.numpy(), opos, w.numpy(), K)
+    got = out.float().cpu().numpy()
+    assert np.abs(got - want).max() <= np.abs(want).max() * 2 ** -8

@@ -1,0 +1,149 @@
+"""CPU-only checks: the C-ABI library loads and exports every declared entry
+point, preconditions are rejected before anything is launched, and the host
+logic of the hook surface behaves as the reference's does."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+
+def test_library_exports_every_declared_symbol(lib):
+    import hipfetch
+    declared = hipfetch.declared_symbols()
+    assert len(declared) >= 15
+    for name in declared:
+        assert hasattr(lib.cdll, name), name
+    assert set(declared) == set(hipfetch.SIGNATURES)
+
+
+def test_library_shares_torchs_hip_runtime(lib):
+    import hipfetch
+    ours = lib.hip_runtime_path()
+    assert ours.endswith(".so") or ".so." in ours
+    theirs = hipfetch._torch_hip_runtime()
+    if theirs:
+        import os
+        assert os.path.realpath(ours) == os.path.realpath(theirs)
+
+
+def test_preconditions_are_rejected_without_launching(lib):
+    c = lib.cdll
+    pairs = (ctypes.c_byte * 64)()
+    assert c.moe_fetch(ctypes.cast(pairs, ctypes.POINTER(__import__("hipfetch").FetchPair)), 5,
+                       1, 1, 1, 8, 64, None) == -1
+    assert b"npairs" in c.moe_last_error()
+    p = ctypes.c_void_p()
+    assert c.moe_host_alloc(ctypes.byref(p), 16, 7) == -1
+    assert c.moe_slots_init(1, 256, 1, 1, 5000, 1, None) == -1
+    assert b"cap" in c.moe_last_error()
+    assert c.moe_fp8_moe_forward(1, 1, 0, 1, 2, 1, 8, 16, 1, 16, 1, 4, 2000, 512, 1, 16, 1 << 30,
+                                 None) == -1
+    assert b"hidden" in c.moe_last_error()
+    assert c.moe_router_topk(16, 16, None, 1, 2048, 256, 40, 1, 1, 0, 1, 2, None) == -1
+
+
+def test_workspace_size_formula(lib):
+    assert lib.fp8_moe_workspace(1, 8, 256, 2048, 512) == 8 * 1024 * 4
+    assert lib.fp8_moe_workspace(512, 8, 256, 2048, 512) == 512 * 8 * 1024 * 4
+
+
+def test_loader_contract_missing_library(tmp_path, monkeypatch):
+    import hipfetch
+    monkeypatch.setattr(hipfetch, "LIB_PATH", tmp_path / "nope.so")
+    hipfetch.reset()
+    try:
+        assert hipfetch.load() is None
+        assert "missing" in hipfetch.last_error()
+        with pytest.raises(RuntimeError, match="unavailable"):
+            hipfetch.require()
+    finally:
+        monkeypatch.undo()
+        hipfetch.reset()
+        assert hipfetch.load() is not None
+
+
+def test_fetch_backend_knob(lib):
+    import devcache
+
+    class Fake:
+        _dc_cap = 4
+        _dc_out = torch.zeros(8, dtype=torch.int32)
+
+    devcache.FETCH_BACKEND = "bogus"
+    try:
+        with pytest.raises(ValueError, match="FETCH_BACKEND"):
+            devcache.dev_resolve_and_fetch(Fake(), torch.zeros((1, 8), dtype=torch.long))
+    finally:
+        devcache.FETCH_BACKEND = "hip"
+    # more ids than slots is refused before anything is enqueued
+    with pytest.raises(ValueError, match="capacity"):
+        devcache.dev_resolve_and_fetch(Fake(), torch.zeros((1, 8), dtype=torch.long))
+
+
+def test_capacity_sizing_arithmetic():
+    import offload
+    GiB = 2 ** 30
+    # (free - (2 + 1.5) GiB) // (40 * 3,146,496)  (bin/offload.py:641-646)
+    assert offload.capacity_for_free_vram(None, 40, 256, free_bytes=20 * GiB) == \
+        int((20 - 3.5) * GiB // (40 * 3_146_496))
+    assert offload.capacity_for_free_vram(None, 40, 256, free_bytes=3 * GiB) == 0
+    assert offload.capacity_for_free_vram(None, 40, 256, free_bytes=280 * GiB) == 256
+    assert offload.capacity_for_free_vram(None, 40, 256, free_bytes=280 * GiB,
+                                          cap_per_layer=96) == 96
+
+
+def test_router_trace_and_census_host_logic():
+    import offload
+    offload.enable_census(2, 8)
+    offload.TRACE.enabled = True
+    offload.TRACE.records.clear()
+    try:
+        offload._count(1, torch.tensor([[1, 2, 3]]))
+        offload._count(1, torch.tensor([[1, 2, 3], [3, 4, 5]]))
+        offload.TRACE.add(1, torch.tensor([[1, 2, 3]]))
+        offload.TRACE.add(0, torch.tensor([[1, 2], [3, 4]]))
+        assert offload.CENSUS[1].tolist() == [0, 2, 2, 3, 1, 1, 0, 0]
+        assert offload.CENSUS_DECODE[1].tolist() == [0, 1, 1, 1, 0, 0, 0, 0]
+        assert [r["phase"] for r in offload.TRACE.records] == ["decode", "prefill"]
+    finally:
+        offload.CENSUS = None
+        offload.CENSUS_DECODE = None
+        offload.TRACE.enabled = False
+        offload.TRACE.records.clear()
+
+
+def test_fp8_moe_forward_has_no_cpu_path(lib):
+    from fp8_moe import fp8_moe_forward
+    x = torch.zeros((1, 256), dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        fp8_moe_forward(x, torch.zeros((1, 1), dtype=torch.long), torch.ones((1, 1)),
+                        torch.zeros((1, 256, 256), dtype=torch.float8_e4m3fn),
+                        torch.ones((1, 2, 2)),
+                        torch.zeros((1, 256, 128), dtype=torch.float8_e4m3fn),
+                        torch.ones((1, 2, 1)))
+
+
+def test_moe_experts_surface():
+    import moe
+    m = moe.MoEExperts(4, 256, 128)
+    assert [n for n, _ in m.named_parameters()] == []          # buffers, not Parameters
+    assert sorted(n for n, _ in m.named_buffers()) == ["w13_scale_inv", "w13_weight",
+                                                       "w2_scale_inv", "w2_weight"]
+    assert m.w13_weight.shape == (4, 256, 256) and m.w2_scale_inv.shape == (4, 2, 1)
+    w = torch.arange(4 * 256 * 256, dtype=torch.int64).remainder(251).to(torch.uint8)
+    m.w13_weight.view(torch.uint8).copy_(w.view(4, 256, 256))
+    sel = moe.select_fp8(m.w13_weight, torch.tensor([2, 0]))
+    assert torch.equal(sel.view(torch.uint8), m.w13_weight.view(torch.uint8)[[2, 0]])
+    with pytest.raises(RuntimeError, match="host memory"):
+        m(torch.zeros((1, 256), dtype=torch.bfloat16), torch.zeros((1, 1), dtype=torch.long),
+          torch.ones((1, 1)))
+
+
+def test_zipf_generators_are_seeded_and_distinct():
+    import synth
+    a = synth.zipf_miss_list(np.random.default_rng(1), 64)
+    b = synth.zipf_miss_list(np.random.default_rng(1), 64)
+    assert np.array_equal(a, b) and len(set(a.tolist())) == 64
+    bias = synth.decode_route_bias(np.random.default_rng(0), 60, 2, 256, 1.1, 50)
+    assert bias.shape == (60, 2, 256) and bias.dtype == np.float32
