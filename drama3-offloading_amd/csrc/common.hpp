@@ -69,6 +69,9 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float v) {
 // rounded (HIP's default float division).
 __device__ __forceinline__ float act_scale(float amax) { return amax / 448.0f; }
 
+// SiLU(g) * u in float32, the one formula every expert kernel uses.
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
 // Quantise v with scale s (s == 0 => 0).
 __device__ __forceinline__ uint32_t quant_e4m3(float v, float s) {
   return s == 0.0f ? 0u : f32_to_e4m3(v / s);

@@ -76,7 +76,13 @@ __device__ __forceinline__ void quantize_row_bf16_to_lds(const uint16_t* __restr
 
 // ------------------------------------------------------------ kernel 1
 
-__global__ __launch_bounds__(256) void gateup_gemv_kernel(
+// One wave per workgroup, 16 weight rows of one (token, expert) pair.  The
+// wave first issues the loads of its whole 16 x H weight tile (up to 16
+// K-blocks, 32 bytes per lane each, all in flight at once), then quantises
+// x[t] into LDS while they travel, then runs the MFMAs.
+constexpr int kGateUpChunk = 16;
+
+__global__ __launch_bounds__(64) void gateup_gemv_kernel(
     const uint16_t* __restrict__ x, const void* __restrict__ ids, int ids64, int32_t top_k,
     const uint8_t* __restrict__ w13, const float* __restrict__ s13, int64_t w13_es,
     int64_t s13_es, int32_t n_experts, int32_t hidden, int32_t inter, float* __restrict__ h) {
@@ -85,40 +91,79 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
   const int64_t p = blockIdx.y;
   const int64_t t = p / top_k;
   const int64_t e = load_id(ids, ids64, p);
+  const bool valid = e >= 0 && e < n_experts;
   const int rows2 = 2 * inter;
   const int G = hidden >> 7;
-  quantize_row_bf16_to_lds(x + t * hidden, hidden, xq, xs);
-  __syncthreads();
-
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int r0 = blockIdx.x * 64 + wave * 16;
+  const int lane = threadIdx.x;
+  const int r0 = blockIdx.x * 16;
   const int q = lane >> 4;
+  const uint8_t* wrow =
+      w13 + (valid ? e : 0) * w13_es + static_cast<int64_t>(r0 + (lane & 15)) * hidden + q * 32;
+  v8i a[kGateUpChunk];
+  if (valid) {
+#pragma unroll
+    for (int c = 0; c < kGateUpChunk; ++c)
+      if (c < G) a[c] = load_op32_nt(wrow + c * 128);
+  }
+  // x[t] -> e4m3 codes + per-128 scales in LDS: 32 values per lane, 4 lanes per group
+  const uint16_t* xr = x + t * hidden;
+  for (int base = 0; base < hidden; base += 2048) {
+    const int i = base + lane * 32;
+    float v[32];
+    float amax = 0.0f;
+    if (i < hidden) {
+      const uint4* src = reinterpret_cast<const uint4*>(xr + i);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint4 raw = src[u];
+        const uint32_t rr[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[u * 8 + 2 * j] = __uint_as_float(rr[j] << 16);
+          v[u * 8 + 2 * j + 1] = __uint_as_float(rr[j] & 0xffff0000u);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    if (i < hidden) {
+      const float sc = act_scale(amax);
+      uint32_t wds[8];
+#pragma unroll
+      for (int w = 0; w < 8; ++w) {
+        uint32_t wd = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wd |= quant_e4m3(v[w * 4 + j], sc) << (8 * j);
+        wds[w] = wd;
+      }
+      *reinterpret_cast<uint4*>(xq + i) = make_uint4(wds[0], wds[1], wds[2], wds[3]);
+      *reinterpret_cast<uint4*>(xq + i + 16) = make_uint4(wds[4], wds[5], wds[6], wds[7]);
+      if ((lane & 3) == 0) xs[i >> 7] = sc;
+    }
+  }
+  __syncthreads();
   float* hp = h + p * rows2;
-  if (e < 0 || e >= n_experts) {   // no such expert: poison, never read out of bounds
+  if (!valid) {   // no such expert: poison the rows, never read out of bounds
     if (lane < 16) hp[r0 + lane] = __builtin_nanf("");
     return;
   }
-  const uint8_t* wrow =
-      w13 + e * w13_es + static_cast<int64_t>(r0 + (lane & 15)) * hidden + q * 32;
   const float* srow = s13 + e * s13_es + static_cast<int64_t>(r0 >> 7) * G;
   v4f acc = {0.f, 0.f, 0.f, 0.f};
-  constexpr int CH = 8;   // K blocks of loads kept in flight per lane
-  for (int g0 = 0; g0 < G; g0 += CH) {
-    v8i a[CH];
+  for (int g0 = 0; g0 < G; g0 += kGateUpChunk) {
+    if (g0 > 0) {
 #pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      if (g0 + c < G) {
-        a[c] = load_op32_nt(wrow + (g0 + c) * 128);
-      }
+      for (int c = 0; c < kGateUpChunk; ++c)
+        if (g0 + c < G) a[c] = load_op32_nt(wrow + (g0 + c) * 128);
     }
 #pragma unroll
-    for (int c = 0; c < CH; ++c) {
+    for (int c = 0; c < kGateUpChunk; ++c) {
       const int g = g0 + c;
       if (g < G) {
         const v8i b = load_op32(xq + g * 128 + q * 32);
-        v4f z = {0.f, 0.f, 0.f, 0.f};
-        v4f d = mfma_e4m3_16x16x128(a[c], b, z);
+        const v4f z = {0.f, 0.f, 0.f, 0.f};
+        const v4f d = mfma_e4m3_16x16x128(a[c], b, z);
         const float sc = srow[g] * xs[g];
         acc[0] += d[0] * sc;
         acc[1] += d[1] * sc;
@@ -135,6 +180,11 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
 
 // ------------------------------------------------------------ kernel 2
 
+// Workgroup = one wave per k, 16 output rows of w2 per wave.  The weight
+// loads go out first; SiLU(gate)*up of the pair is quantised into LDS while
+// they travel; the k partial results are summed in k order.
+constexpr int kDownChunk = 4;   // K-blocks of w2 in flight per lane (inter 512 = one chunk)
+
 __global__ __launch_bounds__(1024) void down_gemv_kernel(
     const float* __restrict__ h, const void* __restrict__ ids, int ids64,
     const void* __restrict__ weights, int wbf16, int32_t top_k, const uint8_t* __restrict__ w2,
@@ -150,63 +200,66 @@ __global__ __launch_bounds__(1024) void down_gemv_kernel(
   const int64_t e = load_id(ids, ids64, p);
   const bool valid = e >= 0 && e < n_experts;
   const int Gi = inter >> 7;
+  const int c0 = blockIdx.x * 16;
+  const int q = lane >> 4;
+  const uint8_t* wrow =
+      w2 + (valid ? e : 0) * w2_es + static_cast<int64_t>(c0 + (lane & 15)) * inter + q * 32;
+  v8i a[kDownChunk];
+  if (valid) {
+#pragma unroll
+    for (int c = 0; c < kDownChunk; ++c)
+      if (c < Gi) a[c] = load_op32_nt(wrow + c * 128);
+  }
   const float* hp = h + p * (2 * inter);
   // SiLU(gate) * up for this pair, quantised per 128 into LDS: 16 lanes x 8
   for (int base = 0; base < inter; base += 512) {
     const int j = base + lane * 8;
-    float a[8];
+    float av[8];
     float amax = 0.0f;
     if (j < inter) {
-      float4 g0 = *reinterpret_cast<const float4*>(hp + j);
-      float4 g1 = *reinterpret_cast<const float4*>(hp + j + 4);
-      float4 u0 = *reinterpret_cast<const float4*>(hp + inter + j);
-      float4 u1 = *reinterpret_cast<const float4*>(hp + inter + j + 4);
+      const float4 g0 = *reinterpret_cast<const float4*>(hp + j);
+      const float4 g1 = *reinterpret_cast<const float4*>(hp + j + 4);
+      const float4 u0 = *reinterpret_cast<const float4*>(hp + inter + j);
+      const float4 u1 = *reinterpret_cast<const float4*>(hp + inter + j + 4);
       const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
       const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        a[i] = gv[i] / (1.0f + expf(-gv[i])) * uv[i];
-        amax = fmaxf(amax, fabsf(a[i]));
+        av[i] = silu_mul(gv[i], uv[i]);
+        amax = fmaxf(amax, fabsf(av[i]));
       }
     }
 #pragma unroll
     for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
     if (j < inter) {
-      const float s = act_scale(amax);
+      const float sc = act_scale(amax);
       uint32_t lo = 0, hi = 0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) lo |= quant_e4m3(a[i], s) << (8 * i);
+      for (int i = 0; i < 4; ++i) lo |= quant_e4m3(av[i], sc) << (8 * i);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) hi |= quant_e4m3(a[4 + i], s) << (8 * i);
+      for (int i = 0; i < 4; ++i) hi |= quant_e4m3(av[4 + i], sc) << (8 * i);
       *reinterpret_cast<uint2*>(&aq[wave][j]) = make_uint2(lo, hi);
-      if ((lane & 15) == 0) as_[wave][j >> 7] = s;
+      if ((lane & 15) == 0) as_[wave][j >> 7] = sc;
     }
   }
   __syncthreads();
 
-  const int c0 = blockIdx.x * 16;
-  const int q = lane >> 4;
   v4f acc = {0.f, 0.f, 0.f, 0.f};
   if (valid) {
-    const uint8_t* wrow =
-        w2 + e * w2_es + static_cast<int64_t>(c0 + (lane & 15)) * inter + q * 32;
     const float* srow = s2 + e * s2_es + static_cast<int64_t>(c0 >> 7) * Gi;
-    constexpr int CH = 4;
-    for (int g0 = 0; g0 < Gi; g0 += CH) {
-      v8i a[CH];
+    for (int g0 = 0; g0 < Gi; g0 += kDownChunk) {
+      if (g0 > 0) {
 #pragma unroll
-      for (int c = 0; c < CH; ++c) {
-        if (g0 + c < Gi) {
-          a[c] = load_op32_nt(wrow + (g0 + c) * 128);
-        }
+        for (int c = 0; c < kDownChunk; ++c)
+          if (g0 + c < Gi) a[c] = load_op32_nt(wrow + (g0 + c) * 128);
       }
 #pragma unroll
-      for (int c = 0; c < CH; ++c) {
+      for (int c = 0; c < kDownChunk; ++c) {
         const int g = g0 + c;
         if (g < Gi) {
           const v8i b = load_op32(&aq[wave][g * 128 + q * 32]);
-          v4f z = {0.f, 0.f, 0.f, 0.f};
-          v4f d = mfma_e4m3_16x16x128(a[c], b, z);
+          const v4f z = {0.f, 0.f, 0.f, 0.f};
+          const v4f d = mfma_e4m3_16x16x128(a[c], b, z);
           const float sc = srow[g] * as_[wave][g];
           acc[0] += d[0] * sc;
           acc[1] += d[1] * sc;
@@ -220,12 +273,12 @@ __global__ __launch_bounds__(1024) void down_gemv_kernel(
     const float wk = load_w(weights, wbf16, p);
     const float nan = __builtin_nanf("");
 #pragma unroll
-    for (int i = 0; i < 4; ++i) part[wave][4 * q + i] = valid ? wk * acc[i] : nan;
+    for (int i = 0; i < 4; ++i) part[wave][4 * q + i] = valid ? __fmul_rn(wk, acc[i]) : nan;
   }
   __syncthreads();
   if (threadIdx.x < 16) {
     float sum = 0.0f;
-    for (int k = 0; k < top_k; ++k) sum += part[k][threadIdx.x];
+    for (int k = 0; k < top_k; ++k) sum = __fadd_rn(sum, part[k][threadIdx.x]);
     out[t * hidden + c0 + threadIdx.x] = f32_to_bf16(sum);
   }
 }
@@ -298,7 +351,7 @@ extern "C" int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t id
   const int64_t pairs = static_cast<int64_t>(tokens) * top_k;
   MOE_REQUIRE(pairs <= 65535LL, "moe_fp8_moe_forward: too many (token, expert) pairs (%lld)",
               (long long)pairs);
-  hipLaunchKernelGGL(gateup_gemv_kernel, dim3((2 * inter) / 64, pairs), dim3(256), 0, s,
+  hipLaunchKernelGGL(gateup_gemv_kernel, dim3((2 * inter) / 16, pairs), dim3(64), 0, s,
                      static_cast<const uint16_t*>(x), ids, ids64, top_k,
                      static_cast<const uint8_t*>(w13), s13, es.w13, es.s13, n_experts, hidden,
                      inter, h);

@@ -1,19 +1,22 @@
 // Token -> expert grouping (permute), its inverse (unpermute), and the
 // torch.unique-style renumbering the reference uses for its gathered subsets.
 //
-// permute: one workgroup of 1024 threads.  Expert ids are staged through LDS
-// as uint16 in chunks; thread i owns experts i, i+1024, ... and scans every
-// chunk (all threads read the same LDS word, a broadcast), first counting its
-// experts, then -- after a block-wide exclusive scan of the counts -- writing
-// the positions of its experts' pairs in pair order.  The order is therefore
-// stable by construction and identical on every run, and no atomics or
-// cleared counters are needed (graph-safe: nothing to memset).
+// permute: one workgroup of 1024 threads, O(pairs) work:
+//   1. histogram of expert ids in LDS (atomic adds; counts do not depend on
+//      the order they land in);
+//   2. block-wide exclusive scan -> offsets, and a cursor per expert;
+//   3. every pair claims a position inside its expert's segment with an LDS
+//      atomic (arbitrary order within the segment at this point);
+//   4. each thread insertion-sorts the segments of its experts by pair index
+//      (segments are short and already nearly sorted), which restores the
+//      stable order, then writes the inverse map.
+// The result equals a stable sort by expert, identically on every run, and
+// no memory has to be cleared beforehand (nothing to memset in a graph).
 #include "common.hpp"
 
 namespace moe {
 
 constexpr int kPermThreads = 1024;
-constexpr int kPermChunk = 8192;   // ids staged per LDS pass
 constexpr int kPermMaxExperts = 4096;
 constexpr int kPermPer = kPermMaxExperts / kPermThreads;
 
@@ -55,73 +58,65 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(
     const void* __restrict__ ids, int ids64, int64_t P, int32_t n_experts,
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ sorted_pairs,
     int32_t* __restrict__ pair_pos) {
-  __shared__ uint16_t sid[kPermChunk];
+  __shared__ int32_t cnt[kPermMaxExperts];
   __shared__ int32_t scratch[40];
   const int tid = threadIdx.x;
-  int32_t cnt[kPermPer];
-#pragma unroll
-  for (int i = 0; i < kPermPer; ++i) cnt[i] = 0;
-
-  // pass 1: count
-  for (int64_t c0 = 0; c0 < P; c0 += kPermChunk) {
-    const int n = static_cast<int>(min<int64_t>(kPermChunk, P - c0));
-    for (int i = tid; i < n; i += kPermThreads) {
-      int32_t e = read_id(ids, ids64, c0 + i);
-      sid[i] = (e >= 0 && e < n_experts) ? static_cast<uint16_t>(e) : 0xffff;
-    }
-    __syncthreads();
-    for (int i = 0; i < n; ++i) {
-      const int e = sid[i];
-#pragma unroll
-      for (int j = 0; j < kPermPer; ++j) cnt[j] += (e == tid + j * kPermThreads);
-    }
-    __syncthreads();
+  for (int e = tid; e < n_experts; e += kPermThreads) cnt[e] = 0;
+  __syncthreads();
+  for (int64_t p = tid; p < P; p += kPermThreads) {
+    const int32_t e = read_id(ids, ids64, p);
+    if (e >= 0 && e < n_experts) atomicAdd(&cnt[e], 1);
   }
-  // exclusive scan over experts in index order: expert x = tid + j*1024
-  int32_t base = 0;
-  int32_t run[kPermPer];
+  __syncthreads();
+  // thread t owns the contiguous experts [t*PER, t*PER + PER)
+  int32_t mine[kPermPer];
+  int32_t sum = 0;
 #pragma unroll
   for (int j = 0; j < kPermPer; ++j) {
-    int32_t pre;
-    int32_t tot = block_exclusive_scan(cnt[j], scratch, &pre);
-    run[j] = base + pre;
-    const int x = tid + j * kPermThreads;
-    if (x < n_experts) {
-      counts[x] = cnt[j];
-      offsets[x] = run[j];
-    }
-    base += tot;
+    const int x = tid * kPermPer + j;
+    mine[j] = x < n_experts ? cnt[x] : 0;
+    sum += mine[j];
   }
-  if (tid == 0) offsets[n_experts] = base;
-
-  // pass 2: place, in pair order
-  for (int64_t c0 = 0; c0 < P; c0 += kPermChunk) {
-    const int n = static_cast<int>(min<int64_t>(kPermChunk, P - c0));
-    for (int i = tid; i < n; i += kPermThreads) {
-      int32_t e = read_id(ids, ids64, c0 + i);
-      sid[i] = (e >= 0 && e < n_experts) ? static_cast<uint16_t>(e) : 0xffff;
-    }
-    __syncthreads();
-    for (int i = 0; i < n; ++i) {
-      const int e = sid[i];
+  int32_t base;
+  const int32_t total = block_exclusive_scan(sum, scratch, &base);
+  int32_t seg[kPermPer];
 #pragma unroll
-      for (int j = 0; j < kPermPer; ++j) {
-        if (e == tid + j * kPermThreads) {
-          const int32_t pos = run[j]++;
-          sorted_pairs[pos] = static_cast<int32_t>(c0 + i);
-          pair_pos[c0 + i] = pos;
-        }
-      }
+  for (int j = 0; j < kPermPer; ++j) {
+    const int x = tid * kPermPer + j;
+    seg[j] = base;
+    if (x < n_experts) {
+      counts[x] = mine[j];
+      offsets[x] = base;
+      cnt[x] = base;              // becomes the placement cursor
     }
-    __syncthreads();
+    base += mine[j];
   }
-  // pairs with an out-of-range id have no position
-  for (int64_t c0 = 0; c0 < P; c0 += kPermThreads) {
-    const int64_t p = c0 + tid;
-    if (p < P) {
-      int32_t e = read_id(ids, ids64, p);
-      if (e < 0 || e >= n_experts) pair_pos[p] = -1;
+  if (tid == 0) offsets[n_experts] = total;
+  __syncthreads();
+  for (int64_t p = tid; p < P; p += kPermThreads) {
+    const int32_t e = read_id(ids, ids64, p);
+    if (e >= 0 && e < n_experts) {
+      const int32_t pos = atomicAdd(&cnt[e], 1);
+      sorted_pairs[pos] = static_cast<int32_t>(p);
+    } else {
+      pair_pos[p] = -1;           // no such expert: no position
     }
+  }
+  __threadfence_block();
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kPermPer; ++j) {
+    const int32_t lo = seg[j], hi = seg[j] + mine[j];
+    for (int32_t i = lo + 1; i < hi; ++i) {      // insertion sort, nearly sorted input
+      const int32_t v = sorted_pairs[i];
+      int32_t k = i - 1;
+      while (k >= lo && sorted_pairs[k] > v) {
+        sorted_pairs[k + 1] = sorted_pairs[k];
+        --k;
+      }
+      sorted_pairs[k + 1] = v;
+    }
+    for (int32_t i = lo; i < hi; ++i) pair_pos[sorted_pairs[i]] = i;
   }
 }
 
@@ -155,7 +150,10 @@ __global__ __launch_bounds__(kPermThreads) void unique_inverse_kernel(
   }
 }
 
-// out[t][c] = sum_k w[t][k] * y[pair_pos[t*K+k]][c], k in order, float32 -> bf16
+// out[t][c] = sum_k w[t][k] * y[pair_pos[t*K+k]][c], k in order -> bf16.
+// Each product is rounded before it is added (no fused multiply-add), which
+// is exactly the combine of the per-pair GEMV path, so both paths give
+// bit-identical outputs.
 __global__ __launch_bounds__(256) void unpermute_kernel(const float* __restrict__ y,
                                                         const int32_t* __restrict__ pair_pos,
                                                         const void* __restrict__ weights,
@@ -175,16 +173,30 @@ __global__ __launch_bounds__(256) void unpermute_kernel(const float* __restrict_
       continue;
     }
     const float4 v = *reinterpret_cast<const float4*>(y + static_cast<int64_t>(pos) * hidden + c);
-    acc.x += w * v.x;
-    acc.y += w * v.y;
-    acc.z += w * v.z;
-    acc.w += w * v.w;
+    acc.x = __fadd_rn(acc.x, __fmul_rn(w, v.x));
+    acc.y = __fadd_rn(acc.y, __fmul_rn(w, v.y));
+    acc.z = __fadd_rn(acc.z, __fmul_rn(w, v.z));
+    acc.w = __fadd_rn(acc.w, __fmul_rn(w, v.w));
   }
   uint16_t* o = out + t * hidden + c;
   o[0] = f32_to_bf16(acc.x);
   o[1] = f32_to_bf16(acc.y);
   o[2] = f32_to_bf16(acc.z);
   o[3] = f32_to_bf16(acc.w);
+}
+
+int launch_permute(const void* ids, int ids64, int64_t P, int32_t n_experts, int32_t* counts,
+                   int32_t* offsets, int32_t* sorted_pairs, int32_t* pair_pos, hipStream_t s) {
+  hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(kPermThreads), 0, s, ids, ids64, P, n_experts,
+                     counts, offsets, sorted_pairs, pair_pos);
+  return check_launch("moe_permute");
+}
+
+int launch_unpermute(const float* y, const int32_t* pair_pos, const void* weights, int wbf16,
+                     int32_t tokens, int32_t top_k, int32_t hidden, uint16_t* out, hipStream_t s) {
+  hipLaunchKernelGGL(unpermute_kernel, dim3((hidden / 4 + 255) / 256, tokens), dim3(256), 0, s,
+                     y, pair_pos, weights, wbf16, top_k, hidden, out);
+  return check_launch("moe_unpermute");
 }
 
 }  // namespace moe
@@ -201,10 +213,8 @@ extern "C" int moe_permute(const void* ids, int32_t ids_dtype, int32_t tokens, i
               "moe_permute: need 1 <= n_experts <= %d", kPermMaxExperts);
   const int64_t P = static_cast<int64_t>(tokens) * top_k;
   MOE_REQUIRE(P <= (1LL << 24), "moe_permute: too many pairs (%lld)", (long long)P);
-  hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(kPermThreads), 0, as_stream(stream), ids,
-                     ids_dtype == MOE_I64 ? 1 : 0, P, n_experts, counts, offsets, sorted_pairs,
-                     pair_pos);
-  return check_launch("moe_permute");
+  return launch_permute(ids, ids_dtype == MOE_I64 ? 1 : 0, P, n_experts, counts, offsets,
+                        sorted_pairs, pair_pos, as_stream(stream));
 }
 
 extern "C" int moe_unique_inverse(const void* ids, int32_t ids_dtype, int32_t tokens,
@@ -233,8 +243,6 @@ extern "C" int moe_unpermute(const float* y, const int32_t* pair_pos, const void
   MOE_REQUIRE(hidden > 0 && hidden % 4 == 0, "moe_unpermute: hidden %% 4 != 0");
   MOE_REQUIRE(reinterpret_cast<uintptr_t>(y) % 16 == 0, "moe_unpermute: y must be 16-byte aligned");
   if (tokens == 0) return MOE_OK;
-  hipLaunchKernelGGL(unpermute_kernel, dim3((hidden / 4 + 255) / 256, tokens), dim3(256), 0,
-                     as_stream(stream), y, pair_pos, weights, w_dtype == MOE_BF16 ? 1 : 0, top_k,
-                     hidden, static_cast<uint16_t*>(out));
-  return check_launch("moe_unpermute");
+  return launch_unpermute(y, pair_pos, weights, w_dtype == MOE_BF16 ? 1 : 0, tokens, top_k,
+                          hidden, static_cast<uint16_t*>(out), as_stream(stream));
 }

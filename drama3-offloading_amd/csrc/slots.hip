@@ -13,10 +13,13 @@
 // later id of the same call.
 //
 // One wavefront does the whole resolve.  The ids are processed in order (two
-// simultaneous misses must not get the same slot), but each victim search is
-// a wave-wide arg-min over stamps kept in registers (C/64 per lane) instead
-// of a sequential C-element scan, and all table writes are issued by lane 0
-// so its own program order makes them visible to its later reads.
+// simultaneous misses must not get the same slot), but nothing in the loop
+// waits on memory: stamps and slot owners live in registers (C/64 slots per
+// lane), lane r holds id r and its slot as loaded at the start, and every
+// eviction or assignment is applied to the later lanes' copies at once, so
+// each lane sees exactly the table the sequential reference loop would.  The
+// victim search is a wave-wide arg-min instead of a C-element scan.  Lane 0
+// issues the table writes in program order.
 #include "common.hpp"
 
 namespace moe {
@@ -44,68 +47,92 @@ __global__ __launch_bounds__(64) void resolve_kernel(
     int32_t* __restrict__ fetch_slot, int32_t* __restrict__ fetch_expert,
     int32_t* __restrict__ nmiss_ptr, int64_t* __restrict__ stats) {
   const int lane = threadIdx.x;
-  // Stamps of slots lane + 64*i live in this lane's registers.
+  // Slot c = lane + 64*j lives in lane's registers: its stamp and its expert.
   int64_t st[PER];
+  int32_t se[PER];
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    int c = lane + 64 * i;
-    st[i] = c < cap ? stamp[c] : INT64_MAX;
+  for (int j = 0; j < PER; ++j) {
+    const int c = lane + 64 * j;
+    st[j] = c < cap ? stamp[c] : INT64_MAX;
+    se[j] = c < cap ? slot_expert[c] : -1;
   }
   // Read at run time, never a launch argument: a captured step would
   // otherwise stamp the same value on every replay.
   const int64_t step = *step_ptr + 1;
   int32_t nm = 0;
   int64_t hits = 0;
-  for (int32_t i = 0; i < k; ++i) {
-    int32_t e = ids64 ? static_cast<int32_t>(reinterpret_cast<const int64_t*>(ids)[i])
-                      : reinterpret_cast<const int32_t*>(ids)[i];
-    if (e < 0 || e >= n_experts) {           // cannot index slot_of: report, skip
-      if (lane == 0) out_slot[i] = -1;
-      continue;
+  for (int32_t base = 0; base < k; base += 64) {
+    // lane r holds id base+r and its current slot (coherent load: lane 0's
+    // table writes of the previous chunk are visible after the fence below)
+    int32_t my_e = -1, my_s = -1;
+    if (base + lane < k) {
+      my_e = ids64 ? static_cast<int32_t>(reinterpret_cast<const int64_t*>(ids)[base + lane])
+                   : reinterpret_cast<const int32_t*>(ids)[base + lane];
+      if (my_e >= 0 && my_e < n_experts)
+        my_s = __hip_atomic_load(slot_of + my_e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else
+        my_e = -1;
     }
-    int32_t s = 0;
-    if (lane == 0) s = slot_of[e];
-    s = wave_bcast(s, 0);
-    if (s < 0) {
-      // arg-min over (stamp, slot) across the wave
-      int64_t bst = INT64_MAX;
-      int32_t bix = INT32_MAX;
+    const int n = min(64, k - base);
+    for (int r = 0; r < n; ++r) {
+      const int32_t e = __shfl(my_e, r, 64);
+      int32_t s = __shfl(my_s, r, 64);
+      if (e < 0) {                                  // cannot index slot_of: report, skip
+        if (lane == 0) out_slot[base + r] = -1;
+        continue;
+      }
+      if (s < 0) {
+        // arg-min over (stamp, slot) across the wave: lowest slot wins a tie
+        int64_t bst = INT64_MAX;
+        int32_t bix = INT32_MAX;
 #pragma unroll
-      for (int j = 0; j < PER; ++j) {
-        int c = lane + 64 * j;
-        if (c < cap && (st[j] < bst)) { bst = st[j]; bix = c; }
-      }
+        for (int j = 0; j < PER; ++j) {
+          const int c = lane + 64 * j;
+          if (c < cap && st[j] < bst) { bst = st[j]; bix = c; }
+        }
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        int64_t ost = __shfl_xor(bst, o, 64);
-        int32_t oix = __shfl_xor(bix, o, 64);
-        if (ost < bst || (ost == bst && oix < bix)) { bst = ost; bix = oix; }
+        for (int o = 32; o > 0; o >>= 1) {
+          const int64_t ost = __shfl_xor(bst, o, 64);
+          const int32_t oix = __shfl_xor(bix, o, 64);
+          if (ost < bst || (ost == bst && oix < bix)) { bst = ost; bix = oix; }
+        }
+        s = bix;
+        int32_t vloc = -1;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+          if (j == (s >> 6)) {
+            vloc = se[j];
+            if ((s & 63) == lane) se[j] = e;
+          }
+        }
+        const int32_t victim = __shfl(vloc, s & 63, 64);
+        // later ids of this call see the table as it is now
+        if (lane > r) {
+          if (my_e == victim) my_s = -1;
+          if (my_e == e) my_s = s;
+        }
+        if (lane == 0) {
+          if (victim >= 0) slot_of[victim] = -1;
+          slot_of[e] = s;
+          slot_expert[s] = e;
+          fetch_slot[nm] = s;
+          fetch_expert[nm] = e;
+        }
+        ++nm;
+      } else {
+        ++hits;
       }
-      s = bix;
-      if (lane == 0) {
-        int32_t victim = slot_expert[s];
-        if (victim >= 0) slot_of[victim] = -1;
-        slot_of[e] = s;
-        slot_expert[s] = e;
-        fetch_slot[nm] = s;
-        fetch_expert[nm] = e;
-      }
-      ++nm;
-    } else {
-      ++hits;
-    }
-    // the owning lane stamps the slot
-    if ((s & 63) == lane) {
 #pragma unroll
       for (int j = 0; j < PER; ++j)
-        if (j == (s >> 6)) st[j] = step;
+        if (j == (s >> 6) && (s & 63) == lane) st[j] = step;
+      if (lane == 0) out_slot[base + r] = s;
     }
-    if (lane == 0) out_slot[i] = s;
+    __threadfence();
   }
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    int c = lane + 64 * i;
-    if (c < cap) stamp[c] = st[i];
+  for (int j = 0; j < PER; ++j) {
+    const int c = lane + 64 * j;
+    if (c < cap) stamp[c] = st[j];
   }
   if (lane == 0) {
     *step_ptr = step;

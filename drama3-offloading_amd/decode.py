@@ -1,0 +1,204 @@
+"""The 40-layer batch-1 decode step with experts offloaded, captured in one
+hipGraph.
+
+Per layer, all on one stream, nothing synchronising and nothing allocating:
+
+    h     = x @ W_stub[l]                     non-expert compute (bf16 matmul stub)
+    ids,w = router(h, gate[l], bias[l])       top-8 of 256 (HIP)
+    slots = resolve(ids, table[l])            device LRU, misses queued (HIP)
+    fetch(pool[l] -> cache[l], misses)        zero-copy host -> HBM (HIP)
+    y     = fp8_moe_forward(h, slots, w)      W8A8 expert FFN on the cache (HIP)
+    x     = h + y
+
+This is the path Drama3DecodeGraphs captures around dev_cached_forward in the
+reference (bin/prefix_kv.py:383-457 driving bin/devcache.py:258-277), with
+the rest of the transformer replaced by one [2048, 2048] matmul per layer.
+Expert popularity follows a per-layer Zipf law that is redrawn every
+`drift_every` steps, injected as a router bias (log-popularity + Gumbel
+noise); the bias for the next step is staged into a fixed buffer before each
+replay.
+
+mode "cached": per-layer cache of `capacity` packed records, LRU on device.
+mode "nocache": every routed expert is fetched on every step (0 % hit; the
+reference's uncached per-expert transfer), into 8 fixed slots.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+import hipfetch
+import synth
+from hostpool import DRAMA3, HostPool, RecordLayout
+
+
+@dataclass
+class DecodeConfig:
+    layers: int = 40
+    n_experts: int = 256
+    top_k: int = 8
+    hidden: int = 2048
+    inter: int = 512
+    capacity: int = 96
+    mode: str = "cached"            # "cached" | "nocache"
+    seed: int = 0
+    schedule_steps: int = 200
+    drift_every: int = 50
+    zipf_s: float = 1.1
+    gate_std: float = 0.002
+    blocks_per_job: int = 64
+    noncoherent_pool: bool = False
+
+
+def fill_pool_on_gpu(pool: HostPool, seed: int, layer: int, device, chunk: int = 64,
+                     std: float = 0.02) -> None:
+    """Seeded N(0, std) weights, 128x128-block quantised, generated on the GPU
+    and written into the page-locked pool as packed records."""
+    lay = pool.layout
+    H, I = lay.hidden, lay.inter
+    g = torch.Generator(device=device).manual_seed(seed * 7919 + layer)
+    for e0 in range(0, pool.n, chunk):
+        n = min(chunk, pool.n - e0)
+        w13, s13 = synth.quantize_blocks(torch.randn((n, 2 * I, H), generator=g, device=device) * std)
+        w2, s2 = synth.quantize_blocks(torch.randn((n, H, I), generator=g, device=device) * std)
+        pool.write(e0, lay.pack(w13, s13, w2, s2))
+    torch.cuda.synchronize(device)
+
+
+class DecodeHarness:
+    def __init__(self, cfg: DecodeConfig, device=None, pools: list[HostPool] | None = None):
+        self.cfg = cfg
+        self.lib = hipfetch.require()
+        self.dev = torch.device(device or "cuda:0")
+        self.layout = RecordLayout(cfg.hidden, cfg.inter)
+        L, E, K, H = cfg.layers, cfg.n_experts, cfg.top_k, cfg.hidden
+        dev = self.dev
+        if pools is None:
+            pools = []
+            for l in range(L):
+                p = HostPool(E, self.layout, noncoherent=cfg.noncoherent_pool)
+                fill_pool_on_gpu(p, cfg.seed, l, dev)
+                pools.append(p)
+        self.pools = pools
+        C = cfg.capacity if cfg.mode == "cached" else K
+        if C < K:
+            raise ValueError(f"capacity {C} < top_k {K}")
+        self.C = C
+        RB = self.layout.record_bytes
+        self.cache = [torch.zeros((C, RB), dtype=torch.uint8, device=dev) for _ in range(L)]
+        self.views = [self.layout.views(c) for c in self.cache]
+        # slot tables and per-layer scratch
+        i32 = dict(dtype=torch.int32, device=dev)
+        self.slot_of = [torch.empty(E, **i32) for _ in range(L)]
+        self.slot_expert = [torch.empty(C, **i32) for _ in range(L)]
+        self.stamp = [torch.empty(C, dtype=torch.int64, device=dev) for _ in range(L)]
+        self.step = [torch.empty(1, dtype=torch.int64, device=dev) for _ in range(L)]
+        self.stats = torch.zeros((L, 2), dtype=torch.int64, device=dev)
+        self.ids = torch.zeros((L, 1, K), **i32)
+        self.wts = torch.zeros((L, 1, K), dtype=torch.float32, device=dev)
+        self.logits = torch.zeros((L, 1, E), dtype=torch.float32, device=dev)
+        self.arrivals = torch.zeros((L, self.lib.router_arrivals(1)), **i32)
+        self.out_slot = torch.zeros((L, 1, K), **i32)
+        self.fslot = torch.zeros((L, K), **i32)
+        self.fexp = torch.zeros((L, K), **i32)
+        self.nmiss = torch.zeros((L, 1), **i32)
+        self.fixed_slots = torch.arange(K, **i32).view(1, K)
+        self.all_miss = torch.full((1,), K, **i32)
+        self.reset_tables()
+        # non-expert stub, router gates, routing schedule
+        g = torch.Generator(device=dev).manual_seed(cfg.seed + 1)
+        # std 1/sqrt(H) keeps the residual stream's scale from layer to layer
+        self.w_stub = (torch.randn((L, H, H), generator=g, device=dev) * (1.0 / H ** 0.5)).to(torch.bfloat16)
+        self.gate = (torch.randn((L, E, H), generator=g, device=dev) * cfg.gate_std).to(torch.bfloat16)
+        rng = np.random.default_rng(cfg.seed)
+        bias = synth.decode_route_bias(rng, cfg.schedule_steps, L, E, cfg.zipf_s, cfg.drift_every)
+        self.bias_all = torch.from_numpy(bias).to(dev)
+        self.bias_live = torch.empty((L, E), dtype=torch.float32, device=dev)
+        self.x0 = synth.hidden_states(cfg.seed, 1, H, device="cpu").to(dev)
+        self.x = self.x0.clone()
+        self.h = torch.empty((1, H), dtype=torch.bfloat16, device=dev)
+        self.y = torch.empty((1, H), dtype=torch.bfloat16, device=dev)
+        ws = self.lib.fp8_moe_workspace(1, K, C, H, cfg.inter)
+        self.ws = torch.empty(ws, dtype=torch.uint8, device=dev)
+        self.pairs = [p.fetch_pair(c) for p, c in zip(self.pools, self.cache)]
+        self.graph = None
+        self.cursor = 0
+
+    # -------------------------------------------------------------- state
+    def reset_tables(self) -> None:
+        for l in range(self.cfg.layers):
+            self.lib.slots_init(self.slot_of[l], self.slot_expert[l], self.stamp[l], self.step[l])
+        self.stats.zero_()
+
+    def stage(self, s: int) -> None:
+        """Bias of schedule step s into the fixed buffer the graph reads."""
+        self.bias_live.copy_(self.bias_all[s % self.cfg.schedule_steps])
+
+    # -------------------------------------------------------------- step
+    def layer(self, l: int) -> None:
+        cfg, lib = self.cfg, self.lib
+        torch.mm(self.x, self.w_stub[l], out=self.h)
+        lib.router_topk(self.h, self.gate[l], self.bias_live[l], cfg.top_k, self.logits[l],
+                        self.arrivals[l], self.ids[l], self.wts[l])
+        w13, s13, w2, s2 = self.views[l]
+        if cfg.mode == "cached":
+            lib.resolve_slots(self.ids[l], self.slot_of[l], self.slot_expert[l], self.stamp[l],
+                              self.step[l], self.out_slot[l], self.fslot[l], self.fexp[l],
+                              self.nmiss[l], self.stats[l])
+            lib.fetch([self.pairs[l]], self.fexp[l], self.fslot[l], self.nmiss[l],
+                      max_jobs=cfg.top_k, blocks_per_job=cfg.blocks_per_job)
+            slots = self.out_slot[l]
+        else:
+            lib.fetch([self.pairs[l]], self.ids[l].view(-1), self.fixed_slots.view(-1),
+                      self.all_miss, max_jobs=cfg.top_k, blocks_per_job=cfg.blocks_per_job)
+            slots = self.fixed_slots
+        lib.fp8_moe_forward(self.h, slots, self.wts[l], w13, s13, w2, s2, self.y, self.ws)
+        torch.add(self.h, self.y, out=self.x)
+
+    def step_eager(self) -> None:
+        # every step starts from the same input token state (the stub has no
+        # embedding); feeding the last layer's output back would compound
+        # the residual stream's growth over thousands of layer applications
+        self.x.copy_(self.x0)
+        for l in range(self.cfg.layers):
+            self.layer(l)
+
+    def capture(self) -> torch.cuda.CUDAGraph:
+        s = torch.cuda.Stream(device=self.dev)
+        s.wait_stream(torch.cuda.current_stream(self.dev))
+        with torch.cuda.stream(s):
+            self.stage(0)
+            self.step_eager()                       # warm-up outside capture
+        torch.cuda.current_stream(self.dev).wait_stream(s)
+        torch.cuda.synchronize(self.dev)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.step_eager()
+        self.graph = g
+        self.restart()
+        return g
+
+    def restart(self) -> None:
+        """Empty caches, first input, schedule from step 0."""
+        self.reset_tables()
+        self.x.copy_(self.x0)
+        self.cursor = 0
+        torch.cuda.synchronize(self.dev)
+
+    def replay(self, n: int = 1) -> None:
+        for _ in range(n):
+            self.stage(self.cursor)
+            self.graph.replay()
+            self.cursor += 1
+
+    def hit_rate(self) -> tuple[int, int]:
+        s = self.stats.sum(0).tolist()
+        return int(s[0]), int(s[1])
+
+    def close(self) -> None:
+        self.graph = None
+        for p in self.pools:
+            p.close()
+        self.pools = []

@@ -52,8 +52,8 @@ SIGNATURES = {
     "moe_resolve_slots": (C.c_int, [_vp, _i32, _i32, _vp, _i32, _vp, _vp, _i32, _vp, _vp, _vp,
                                     _vp, _vp, _vp, _vp]),
     "moe_fetch": (C.c_int, [C.POINTER(FetchPair), _i32, _vp, _vp, _vp, _i32, _i32, _vp]),
-    "moe_router_topk": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _i32, _vp,
-                                  _i32, _vp]),
+    "moe_router_topk": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _i32,
+                                  _vp, _i32, _vp]),
     "moe_fp8_moe_workspace": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "moe_fp8_moe_forward": (C.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
                                       _i32, _i32, _i32, _vp, _vp, _sz, _vp]),
@@ -156,13 +156,20 @@ class Native:
                                         blocks_per_job, self.stream()), "moe_fetch")
 
     # ------------------------------------------------------------ router
-    def router_topk(self, x, w, bias, top_k: int, logits, ids, weights) -> None:
+    @staticmethod
+    def router_arrivals(tokens: int) -> int:
+        """int32 counters moe_router_topk needs (zeroed once at allocation)."""
+        return (tokens + 3) // 4
+
+    def router_topk(self, x, w, bias, top_k: int, logits, arrivals, ids, weights) -> None:
         T, H = x.shape
         E = w.shape[0]
+        if arrivals.numel() < self.router_arrivals(T) or arrivals.dtype.itemsize != 4:
+            raise ValueError(f"arrivals must be int32[{self.router_arrivals(T)}] (zeroed)")
         self._check(self.cdll.moe_router_topk(
             x.data_ptr(), w.data_ptr(), self._ptr(bias), T, H, E, top_k, logits.data_ptr(),
-            ids.data_ptr(), self._dtype_code(ids), weights.data_ptr(), self._dtype_code(weights),
-            self.stream()), "moe_router_topk")
+            arrivals.data_ptr(), ids.data_ptr(), self._dtype_code(ids), weights.data_ptr(),
+            self._dtype_code(weights), self.stream()), "moe_router_topk")
 
     # ------------------------------------------------------------ experts
     def fp8_moe_workspace(self, tokens, top_k, n_experts, hidden, inter) -> int:

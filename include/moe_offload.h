@@ -120,13 +120,17 @@ int moe_fetch(const moe_fetch_pair* pairs, int32_t npairs,
  * [tokens, n_experts] to `logits` (caller-provided, also the workspace).
  * Logits are float32 roundings of float64-accumulated exact products;
  * selection is by descending logit, ties to the lower index.
+ * `arrivals` is int32[ceil(tokens/4)], zeroed once when allocated; each call
+ * leaves it zeroed again (the workgroups of one launch count in on it and the
+ * last one selects).  One launch; calls must not overlap on one `arrivals`.
  * Replaces upstream's gate + softmax + topk + norm_topk_prob
  * (moe.py:217-220 per notes/01-static-findings.md:133-138).
  * Constraints: hidden % 8 == 0, 1 <= top_k <= 32, top_k <= n_experts <= 4096. */
 int moe_router_topk(const void* x, const void* w, const float* bias,
                     int32_t tokens, int32_t hidden, int32_t n_experts,
-                    int32_t top_k, float* logits, void* ids, int32_t ids_dtype,
-                    void* weights, int32_t w_dtype, void* stream);
+                    int32_t top_k, float* logits, int32_t* arrivals, void* ids,
+                    int32_t ids_dtype, void* weights, int32_t w_dtype,
+                    void* stream);
 
 /* ------------------------------------------------------- expert compute */
 

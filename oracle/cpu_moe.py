@@ -1,0 +1,82 @@
+"""The reference's CPU MoE path, timed as the bench's CPU baseline.
+
+Oracle (test infrastructure; only bench.py's cpu_baseline leg runs it).
+
+Upstream's non-FP8-compute path gathers the routed experts, dequantises them
+per 128x128 block and multiplies with ordinary matmuls (`expert_weights` ->
+`dequantize_fp8_blocks(select_fp8(w, index), scale_inv[index], dtype)`, then
+`forward_gathered` bmm; notes/13-non-ada-gpus.md:37-53).  Restated here with
+torch on the host cores in float32, reading the packed records straight out
+of the page-locked pool the GPU fetches from.  One decode step mirrors the
+GPU harness: per layer a [2048, 2048] stub matmul, the router, then the
+8 routed experts.
+"""
+from __future__ import annotations
+
+import time
+
+import torch
+
+
+def dequantize_fp8_blocks(q_u8: torch.Tensor, scale_inv: torch.Tensor,
+                          dtype=torch.float32) -> torch.Tensor:
+    """q [n, R, C] uint8 e4m3 codes, scale_inv [n, R/128, C/128] -> [n, R, C]."""
+    w = q_u8.view(torch.float8_e4m3fn).to(dtype)
+    s = scale_inv.to(dtype).repeat_interleave(128, dim=-2).repeat_interleave(128, dim=-1)
+    return w * s
+
+
+def moe_forward_cpu(x: torch.Tensor, ids: torch.Tensor, wts: torch.Tensor,
+                    records: torch.Tensor, layout) -> torch.Tensor:
+    """x [T, H] float32, ids/wts [T, K], records uint8 [E, record_bytes]."""
+    T, K = ids.shape
+    H, I = layout.hidden, layout.inter
+    uniq, inv = torch.unique(ids, return_inverse=True)
+    rec = records[uniq]                                          # CPU gather (select_fp8)
+    n = rec.shape[0]
+    w13 = dequantize_fp8_blocks(rec[:, :layout.off_w2].view(n, 2 * I, H),
+                                rec[:, layout.off_s13:layout.off_s2].contiguous()
+                                .view(torch.float32).view(n, 2 * I // 128, H // 128))
+    w2 = dequantize_fp8_blocks(rec[:, layout.off_w2:layout.off_s13].view(n, H, I),
+                               rec[:, layout.off_s2:].contiguous()
+                               .view(torch.float32).view(n, H // 128, I // 128))
+    flat = inv.reshape(-1)
+    xs = x.repeat_interleave(K, dim=0).unsqueeze(-1)             # [T*K, H, 1]
+    h = torch.bmm(w13[flat], xs).squeeze(-1)                     # [T*K, 2I]
+    a = torch.nn.functional.silu(h[:, :I]) * h[:, I:]
+    y = torch.bmm(w2[flat], a.unsqueeze(-1)).squeeze(-1)         # [T*K, H]
+    return (y.view(T, K, H) * wts.unsqueeze(-1)).sum(1)
+
+
+def decode_step_cpu(x, w_stub, gate, bias, records, layout, top_k=8, layers=None):
+    """One batch-1 decode step over `layers` layers (all by default)."""
+    L = w_stub.shape[0] if layers is None else layers
+    for l in range(L):
+        h = x @ w_stub[l]
+        logits = h @ gate[l].T + bias[l]
+        val, ids = torch.topk(logits, top_k, dim=-1)
+        wts = torch.softmax(val, dim=-1)
+        x = h + moe_forward_cpu(h, ids, wts, records[l], layout)
+    return x
+
+
+def time_decode(w_stub, gate, bias, records, layout, x0, budget_s: float = 12.0,
+                top_k: int = 8):
+    """Run whole layers until ~budget_s of CPU work; returns
+    (seconds per token, layers run, threads)."""
+    L = w_stub.shape[0]
+    x = x0
+    # warm-up one layer
+    decode_step_cpu(x, w_stub[:1], gate[:1], bias[:1], records[:1], layout, top_k)
+    t0 = time.perf_counter()
+    done = 0
+    while True:
+        l = done % L
+        x = decode_step_cpu(x, w_stub[l:l + 1], gate[l:l + 1], bias[l:l + 1],
+                            records[l:l + 1], layout, top_k)
+        done += 1
+        el = time.perf_counter() - t0
+        if (el >= budget_s and done >= 4) or done >= 4 * L:
+            break
+    per_layer = el / done
+    return per_layer * L, done, torch.get_num_threads()
