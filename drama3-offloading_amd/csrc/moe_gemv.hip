@@ -189,7 +189,8 @@ __global__ __launch_bounds__(1024) void down_gemv_kernel(
     const float* __restrict__ h, const void* __restrict__ ids, int ids64,
     const void* __restrict__ weights, int wbf16, int32_t top_k, const uint8_t* __restrict__ w2,
     const float* __restrict__ s2, int64_t w2_es, int64_t s2_es, int32_t n_experts,
-    int32_t hidden, int32_t inter, uint16_t* __restrict__ out) {
+    int32_t hidden, int32_t inter, const uint16_t* __restrict__ residual,
+    uint16_t* __restrict__ out) {
   __shared__ __align__(16) uint8_t aq[kMaxK][kMaxInter];
   __shared__ float as_[kMaxK][kMaxInter / 128];
   __shared__ float part[kMaxK][16];
@@ -279,7 +280,10 @@ __global__ __launch_bounds__(1024) void down_gemv_kernel(
   if (threadIdx.x < 16) {
     float sum = 0.0f;
     for (int k = 0; k < top_k; ++k) sum = __fadd_rn(sum, part[k][threadIdx.x]);
-    out[t * hidden + c0 + threadIdx.x] = f32_to_bf16(sum);
+    const int64_t o = t * hidden + c0 + threadIdx.x;
+    uint16_t y = f32_to_bf16(sum);
+    if (residual) y = f32_to_bf16(bf16_to_f32(residual[o]) + bf16_to_f32(y));
+    out[o] = y;
   }
 }
 
@@ -302,7 +306,8 @@ extern "C" int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t id
                                       int32_t top_k, const void* w13, const float* s13,
                                       const void* w2, const float* s2, int32_t n_experts,
                                       int32_t hidden, int32_t inter,
-                                      const moe_expert_strides* strides, void* out,
+                                      const moe_expert_strides* strides,
+                                      const void* residual, void* out,
                                       void* workspace, size_t workspace_bytes, int32_t mode,
                                       void* stream) {
   MOE_REQUIRE(x && ids && weights && w13 && s13 && w2 && s2 && out,
@@ -359,7 +364,8 @@ extern "C" int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t id
   if (rc) return rc;
   hipLaunchKernelGGL(down_gemv_kernel, dim3(hidden / 16, tokens), dim3(64 * top_k), 0, s, h, ids,
                      ids64, weights, wbf16, top_k, static_cast<const uint8_t*>(w2), s2, es.w2,
-                     es.s2, n_experts, hidden, inter, static_cast<uint16_t*>(out));
+                     es.s2, n_experts, hidden, inter, static_cast<const uint16_t*>(residual),
+                     static_cast<uint16_t*>(out));
   return check_launch("moe_fp8_moe_forward(down)");
 }
 
@@ -370,6 +376,6 @@ extern "C" int moe_fp8_moe_forward(const void* x, const void* ids, int32_t ids_d
                                    int32_t hidden, int32_t inter, void* out, void* workspace,
                                    size_t workspace_bytes, void* stream) {
   return moe_fp8_moe_forward_ex(x, ids, ids_dtype, weights, w_dtype, tokens, top_k, w13, s13, w2,
-                                s2, n_experts, hidden, inter, nullptr, out, workspace,
+                                s2, n_experts, hidden, inter, nullptr, nullptr, out, workspace,
                                 workspace_bytes, 0, stream);
 }

@@ -1,0 +1,143 @@
+// The slot-table resolve of one call, by one wavefront (shared by the
+// standalone resolve kernel and the fused top-k + resolve decode kernel).
+//
+// Decisions are exactly those of bin/devcache.py:65-98: step += 1; each id
+// in order: a hit stamps its slot; a miss takes the slot with the smallest
+// stamp (the lowest index on a tie), evicts that slot's expert and queues
+// (slot, expert) for the fetch.  Slots used in the current step carry the
+// largest stamp, so no later id of the same call can take them.
+//
+// Nothing in the loop waits on memory: slot stamps and owners live in
+// registers (C/64 slots per lane), lane r holds id r of the current chunk of
+// 64 and its slot as loaded at the start of the chunk, and every eviction or
+// assignment is applied to the later lanes' copies immediately, so each id
+// sees exactly the table the sequential loop would.  The victim search is a
+// wave-wide arg-min.  Lane 0 issues the table writes, in program order.
+#pragma once
+
+#include "common.hpp"
+
+namespace moe {
+
+constexpr int kMaxCap = 4096;
+
+// id_at(i) -> expert id at position i of the call (evaluated by lane i%64 of
+// chunk i/64); out-of-range ids (< 0 or >= n_experts) are reported as slot -1.
+template <int PER, typename IdAt>
+__device__ __forceinline__ void resolve_wave_impl(IdAt id_at, int32_t k, int32_t n_experts,
+                                                  int32_t* __restrict__ slot_of,
+                                                  int32_t* __restrict__ slot_expert,
+                                                  int64_t* __restrict__ stamp, int32_t cap,
+                                                  int64_t* __restrict__ step_ptr,
+                                                  int32_t* __restrict__ out_slot,
+                                                  int32_t* __restrict__ fetch_slot,
+                                                  int32_t* __restrict__ fetch_expert,
+                                                  int32_t* __restrict__ nmiss_ptr,
+                                                  int64_t* __restrict__ stats) {
+  const int lane = threadIdx.x & 63;
+  int64_t st[PER];
+  int32_t se[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int c = lane + 64 * j;
+    st[j] = c < cap ? stamp[c] : INT64_MAX;
+    se[j] = c < cap ? slot_expert[c] : -1;
+  }
+  // read at run time, never a launch argument: a captured step would
+  // otherwise stamp the same value on every replay
+  const int64_t step = *step_ptr + 1;
+  int32_t nm = 0;
+  int64_t hits = 0;
+  for (int32_t base = 0; base < k; base += 64) {
+    int32_t my_e = -1, my_s = -1;
+    if (base + lane < k) {
+      my_e = id_at(base + lane);
+      if (my_e >= 0 && my_e < n_experts)
+        // coherent load: lane 0's writes of the previous chunk were fenced
+        my_s = __hip_atomic_load(slot_of + my_e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else
+        my_e = -1;
+    }
+    const int n = min(64, k - base);
+    for (int r = 0; r < n; ++r) {
+      const int32_t e = __shfl(my_e, r, 64);
+      int32_t s = __shfl(my_s, r, 64);
+      if (e < 0) {
+        if (lane == 0) out_slot[base + r] = -1;
+        continue;
+      }
+      if (s < 0) {
+        int64_t bst = INT64_MAX;
+        int32_t bix = INT32_MAX;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+          const int c = lane + 64 * j;
+          if (c < cap && st[j] < bst) { bst = st[j]; bix = c; }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+          const int64_t ost = __shfl_xor(bst, o, 64);
+          const int32_t oix = __shfl_xor(bix, o, 64);
+          if (ost < bst || (ost == bst && oix < bix)) { bst = ost; bix = oix; }
+        }
+        s = bix;
+        int32_t vloc = -1;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+          if (j == (s >> 6)) {
+            vloc = se[j];
+            if ((s & 63) == lane) se[j] = e;
+          }
+        }
+        const int32_t victim = __shfl(vloc, s & 63, 64);
+        if (lane > r) {                      // later ids see the table as it is now
+          if (my_e == victim) my_s = -1;
+          if (my_e == e) my_s = s;
+        }
+        if (lane == 0) {
+          if (victim >= 0) slot_of[victim] = -1;
+          slot_of[e] = s;
+          slot_expert[s] = e;
+          fetch_slot[nm] = s;
+          fetch_expert[nm] = e;
+        }
+        ++nm;
+      } else {
+        ++hits;
+      }
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        if (j == (s >> 6) && (s & 63) == lane) st[j] = step;
+      if (lane == 0) out_slot[base + r] = s;
+    }
+    if (base + 64 < k) __threadfence();
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int c = lane + 64 * j;
+    if (c < cap) stamp[c] = st[j];
+  }
+  if (lane == 0) {
+    *step_ptr = step;
+    *nmiss_ptr = nm;
+    if (stats) {
+      stats[0] += hits;
+      stats[1] += nm;
+    }
+  }
+}
+
+// Ids already held one per lane (k <= 64): lane r passes the r-th id.
+template <int PER>
+__device__ __forceinline__ void resolve_wave(int32_t my_id, int32_t k, int32_t n_experts,
+                                             int32_t* slot_of, int32_t* slot_expert,
+                                             int64_t* stamp, int32_t cap, int64_t* step_ptr,
+                                             int32_t* out_slot, int32_t* fetch_slot,
+                                             int32_t* fetch_expert, int32_t* nmiss_ptr,
+                                             int64_t* stats) {
+  resolve_wave_impl<PER>([my_id](int) { return my_id; }, k, n_experts, slot_of, slot_expert,
+                         stamp, cap, step_ptr, out_slot, fetch_slot, fetch_expert, nmiss_ptr,
+                         stats);
+}
+
+}  // namespace moe

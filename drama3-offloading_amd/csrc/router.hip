@@ -7,37 +7,81 @@
 // exact for ordinary data, the rounded logit does not depend on the order of
 // summation, which is what lets expert ids match the oracle bit for bit.
 //
-// One launch: grid (E/4, ceil(T/4)), 4 waves per workgroup.  Wave w of
-// workgroup (bx, by) computes the logit of expert 4*bx + w for the 4 tokens
-// of token block `by`, reading its 4 KiB gate row once.  Each workgroup then
-// bumps the token block's arrival counter; the last one to arrive selects the
-// top-k of those tokens (one wave per token, logits in registers) and puts
-// the counter back to zero, so the counters never need clearing between
-// calls (nothing to memset inside a graph).
+// Kernels:
+//   logits: grid (E/4, ceil(T/4)), 4 waves; wave w of workgroup (bx, by)
+//           computes expert 4*bx + w for the 4 tokens of block by, reading its
+//           4 KiB gate row once.
+//   topk:   one wave per token, logits in registers, k rounds of wave arg-max.
+//   topk_resolve (decode): one wave does the top-k of one token AND the slot
+//           table update for those ids (slots.hip's resolve, same decisions),
+//           saving a launch per layer on the decode step.
+// Cross-workgroup hand-offs happen only at kernel boundaries: on MI355X each
+// XCD has its own L2, and a device-scope fence inside a kernel costs more
+// than a launch.
 #include "common.hpp"
+#include "resolve.hpp"
 
 namespace moe {
 
 constexpr int kMaxTopK = 32;
 constexpr int kTokBlock = 4;
 
+__global__ __launch_bounds__(256) void router_logits_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ bias,
+    int32_t tokens, int32_t hidden, int32_t n_experts, float* __restrict__ logits) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int e = blockIdx.x * 4 + wave;
+  const int t0 = blockIdx.y * kTokBlock;
+  const int nt = min(kTokBlock, tokens - t0);
+  if (e >= n_experts) return;
+  const int nv = hidden >> 3;                 // 16-byte vectors per row
+  const uint4* wr = reinterpret_cast<const uint4*>(w + static_cast<int64_t>(e) * hidden);
+  double acc[kTokBlock] = {0.0, 0.0, 0.0, 0.0};
+  for (int i = lane; i < nv; i += 64) {
+    const uint4 b = wr[i];
+    const uint32_t bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int tt = 0; tt < kTokBlock; ++tt) {
+      if (tt < nt) {
+        const uint4 a = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(t0 + tt) * hidden)[i];
+        const uint32_t av[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float a0 = __uint_as_float(av[j] << 16), a1 = __uint_as_float(av[j] & 0xffff0000u);
+          const float b0 = __uint_as_float(bv[j] << 16), b1 = __uint_as_float(bv[j] & 0xffff0000u);
+          acc[tt] += static_cast<double>(a0 * b0);     // exact products
+          acc[tt] += static_cast<double>(a1 * b1);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int tt = 0; tt < kTokBlock; ++tt) {
+    const double s = wave_sum_f64(acc[tt]);
+    if (lane == 0 && tt < nt) {
+      float l = static_cast<float>(s);
+      if (bias) l += bias[e];
+      logits[static_cast<int64_t>(t0 + tt) * n_experts + e] = l;
+    }
+  }
+}
+
+// Top-k of one token's logits by one wave.  Lane r < k ends up holding the
+// r-th pick (*id, *wt = its renormalised softmax weight).
 template <int PER>
-__device__ void topk_one_token(const float* __restrict__ row, int32_t n_experts, int32_t top_k,
-                               int64_t t, void* __restrict__ ids, int ids64,
-                               void* __restrict__ weights, int wbf16) {
+__device__ __forceinline__ void wave_topk(const float* __restrict__ row, int32_t n_experts,
+                                          int32_t top_k, int32_t* id, float* wt) {
   const int lane = threadIdx.x & 63;
   float v[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int e = lane + 64 * j;
-    // coherent loads: other workgroups wrote these logits
-    v[j] = e < n_experts ? __hip_atomic_load(row + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                         : -INFINITY;
+    v[j] = e < n_experts ? row[e] : -INFINITY;
   }
   uint64_t taken = 0;   // bit j: expert lane + 64*j already selected
-  float m = 0.0f, sum = 0.0f;
-  float myv = 0.0f;
-  int myi = 0;
+  float m = 0.0f, sum = 0.0f, myv = 0.0f;
+  int myi = -1;
   for (int r = 0; r < top_k; ++r) {
     float bv = 0.0f;
     int bi = INT32_MAX;
@@ -62,112 +106,126 @@ __device__ void topk_one_token(const float* __restrict__ row, int32_t n_experts,
     if (r == 0) m = bv;
     const float ex = expf(bv - m);
     sum += ex;
-    if (lane == r) {       // lane r keeps round r's pick
+    if (lane == r) {
       myv = ex;
       myi = bi;
     }
   }
-  if (lane < top_k) {
-    const int64_t o = t * top_k + lane;
-    if (ids64) reinterpret_cast<int64_t*>(ids)[o] = myi;
-    else reinterpret_cast<int32_t*>(ids)[o] = myi;
-    const float wv = myv / sum;
-    if (wbf16) reinterpret_cast<uint16_t*>(weights)[o] = f32_to_bf16(wv);
-    else reinterpret_cast<float*>(weights)[o] = wv;
-  }
+  *id = myi;
+  *wt = myv / sum;
 }
 
 template <int PER>
-__global__ __launch_bounds__(256) void router_kernel(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ bias,
-    int32_t tokens, int32_t hidden, int32_t n_experts, int32_t top_k, float* __restrict__ logits,
-    int32_t* __restrict__ arrivals, void* __restrict__ ids, int ids64, void* __restrict__ weights,
-    int wbf16) {
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int e = blockIdx.x * 4 + wave;
-  const int t0 = blockIdx.y * kTokBlock;
-  const int nt = min(kTokBlock, tokens - t0);
-  if (e < n_experts) {
-    const int nv = hidden >> 3;                 // 16-byte vectors per row
-    const uint4* wr = reinterpret_cast<const uint4*>(w + static_cast<int64_t>(e) * hidden);
-    double acc[kTokBlock] = {0.0, 0.0, 0.0, 0.0};
-    for (int i = lane; i < nv; i += 64) {
-      const uint4 b = wr[i];
-      const uint32_t bv[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-      for (int tt = 0; tt < kTokBlock; ++tt) {
-        if (tt < nt) {
-          const uint4 a = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(t0 + tt) * hidden)[i];
-          const uint32_t av[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float a0 = __uint_as_float(av[j] << 16), a1 = __uint_as_float(av[j] & 0xffff0000u);
-            const float b0 = __uint_as_float(bv[j] << 16), b1 = __uint_as_float(bv[j] & 0xffff0000u);
-            acc[tt] += static_cast<double>(a0 * b0);     // exact products
-            acc[tt] += static_cast<double>(a1 * b1);
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int tt = 0; tt < kTokBlock; ++tt) {
-      const double s = wave_sum_f64(acc[tt]);
-      if (lane == 0 && tt < nt) {
-        float l = static_cast<float>(s);
-        if (bias) l += bias[e];
-        logits[static_cast<int64_t>(t0 + tt) * n_experts + e] = l;
-      }
-    }
+__global__ __launch_bounds__(64) void router_topk_kernel(const float* __restrict__ logits,
+                                                         int32_t n_experts, int32_t top_k,
+                                                         void* __restrict__ ids, int ids64,
+                                                         void* __restrict__ weights, int wbf16) {
+  const int64_t t = blockIdx.x;
+  const int lane = threadIdx.x;
+  int32_t id;
+  float wt;
+  wave_topk<PER>(logits + t * n_experts, n_experts, top_k, &id, &wt);
+  if (lane < top_k) {
+    const int64_t o = t * top_k + lane;
+    if (ids64) reinterpret_cast<int64_t*>(ids)[o] = id;
+    else reinterpret_cast<int32_t*>(ids)[o] = id;
+    if (wbf16) reinterpret_cast<uint16_t*>(weights)[o] = f32_to_bf16(wt);
+    else reinterpret_cast<float*>(weights)[o] = wt;
   }
-  // the last workgroup of this token block selects
-  __shared__ int last;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = atomicAdd(&arrivals[blockIdx.y], 1);
-    last = prev == static_cast<int>(gridDim.x) - 1;
+}
+
+template <int PER, int PERC>
+__global__ __launch_bounds__(64) void topk_resolve_kernel(
+    const float* __restrict__ logits, int32_t n_experts, int32_t top_k, int32_t* __restrict__ ids,
+    float* __restrict__ weights, int32_t* __restrict__ slot_of, int32_t* __restrict__ slot_expert,
+    int64_t* __restrict__ stamp, int32_t cap, int64_t* __restrict__ step_ptr,
+    int32_t* __restrict__ out_slot, int32_t* __restrict__ fetch_slot,
+    int32_t* __restrict__ fetch_expert, int32_t* __restrict__ nmiss_ptr,
+    int64_t* __restrict__ stats) {
+  const int lane = threadIdx.x;
+  int32_t id;
+  float wt;
+  wave_topk<PER>(logits, n_experts, top_k, &id, &wt);
+  if (lane < top_k) {
+    ids[lane] = id;
+    weights[lane] = wt;
   }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  if (wave < nt) {
-    const int64_t t = t0 + wave;
-    topk_one_token<PER>(logits + t * n_experts, n_experts, top_k, t, ids, ids64, weights, wbf16);
-  }
-  if (threadIdx.x == 0) arrivals[blockIdx.y] = 0;
+  // the picks are already one per lane: resolve them in pick order
+  resolve_wave<PERC>(lane < top_k ? id : -1, top_k, n_experts, slot_of, slot_expert, stamp, cap,
+                     step_ptr, out_slot, fetch_slot, fetch_expert, nmiss_ptr, stats);
 }
 
 }  // namespace moe
 
+using namespace moe;
+
 extern "C" int moe_router_topk(const void* x, const void* w, const float* bias, int32_t tokens,
                                int32_t hidden, int32_t n_experts, int32_t top_k, float* logits,
-                               int32_t* arrivals, void* ids, int32_t ids_dtype, void* weights,
-                               int32_t w_dtype, void* stream) {
-  MOE_REQUIRE(x && w && logits && arrivals && ids && weights, "moe_router_topk: NULL pointer");
+                               void* ids, int32_t ids_dtype, void* weights, int32_t w_dtype,
+                               void* stream) {
+  MOE_REQUIRE(x && w && logits && ids && weights, "moe_router_topk: NULL pointer");
   MOE_REQUIRE(tokens >= 0, "moe_router_topk: tokens < 0");
   MOE_REQUIRE(hidden > 0 && hidden % 8 == 0, "moe_router_topk: hidden %% 8 != 0 (%d)", hidden);
-  MOE_REQUIRE(top_k >= 1 && top_k <= moe::kMaxTopK && top_k <= n_experts && n_experts <= 4096,
+  MOE_REQUIRE(top_k >= 1 && top_k <= kMaxTopK && top_k <= n_experts && n_experts <= 4096,
               "moe_router_topk: need 1 <= top_k <= min(32, n_experts), n_experts <= 4096");
   MOE_REQUIRE(ids_dtype == MOE_I32 || ids_dtype == MOE_I64, "moe_router_topk: bad ids_dtype");
   MOE_REQUIRE(w_dtype == MOE_F32 || w_dtype == MOE_BF16, "moe_router_topk: bad w_dtype");
   MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0,
               "moe_router_topk: x and w must be 16-byte aligned");
   if (tokens == 0) return MOE_OK;
-  const dim3 grid((n_experts + 3) / 4, (tokens + moe::kTokBlock - 1) / moe::kTokBlock);
+  const dim3 grid((n_experts + 3) / 4, (tokens + kTokBlock - 1) / kTokBlock);
   MOE_REQUIRE(grid.y <= 65535, "moe_router_topk: too many tokens (%d)", tokens);
-  hipStream_t s = moe::as_stream(stream);
+  hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(router_logits_kernel, grid, dim3(256), 0, s,
+                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias,
+                     tokens, hidden, n_experts, logits);
+  int rc = check_launch("moe_router_topk(logits)");
+  if (rc) return rc;
   const int i64 = ids_dtype == MOE_I64 ? 1 : 0, bf = w_dtype == MOE_BF16 ? 1 : 0;
-  const uint16_t* xp = static_cast<const uint16_t*>(x);
-  const uint16_t* wp = static_cast<const uint16_t*>(w);
   if (n_experts <= 256)
-    hipLaunchKernelGGL(moe::router_kernel<4>, grid, dim3(256), 0, s, xp, wp, bias, tokens, hidden,
-                       n_experts, top_k, logits, arrivals, ids, i64, weights, bf);
+    hipLaunchKernelGGL(router_topk_kernel<4>, dim3(tokens), dim3(64), 0, s, logits, n_experts,
+                       top_k, ids, i64, weights, bf);
   else if (n_experts <= 1024)
-    hipLaunchKernelGGL(moe::router_kernel<16>, grid, dim3(256), 0, s, xp, wp, bias, tokens,
-                       hidden, n_experts, top_k, logits, arrivals, ids, i64, weights, bf);
+    hipLaunchKernelGGL(router_topk_kernel<16>, dim3(tokens), dim3(64), 0, s, logits, n_experts,
+                       top_k, ids, i64, weights, bf);
   else
-    hipLaunchKernelGGL(moe::router_kernel<64>, grid, dim3(256), 0, s, xp, wp, bias, tokens,
-                       hidden, n_experts, top_k, logits, arrivals, ids, i64, weights, bf);
-  return moe::check_launch("moe_router_topk");
+    hipLaunchKernelGGL(router_topk_kernel<64>, dim3(tokens), dim3(64), 0, s, logits, n_experts,
+                       top_k, ids, i64, weights, bf);
+  return check_launch("moe_router_topk(topk)");
+}
+
+extern "C" int moe_route_resolve(const void* x, const void* w, const float* bias, int32_t hidden,
+                                 int32_t n_experts, int32_t top_k, float* logits, int32_t* ids,
+                                 float* weights, int32_t* slot_of, int32_t* slot_expert,
+                                 int64_t* slot_stamp, int32_t cap, int64_t* step,
+                                 int32_t* out_slot, int32_t* fetch_slot, int32_t* fetch_expert,
+                                 int32_t* nmiss, int64_t* stats, void* stream) {
+  MOE_REQUIRE(x && w && logits && ids && weights && slot_of && slot_expert && slot_stamp && step &&
+                  out_slot && fetch_slot && fetch_expert && nmiss,
+              "moe_route_resolve: NULL pointer");
+  MOE_REQUIRE(hidden > 0 && hidden % 8 == 0, "moe_route_resolve: hidden %% 8 != 0 (%d)", hidden);
+  MOE_REQUIRE(top_k >= 1 && top_k <= kMaxTopK && top_k <= n_experts && n_experts <= 4096,
+              "moe_route_resolve: need 1 <= top_k <= min(32, n_experts), n_experts <= 4096");
+  MOE_REQUIRE(cap >= 1 && cap <= kMaxCap, "moe_route_resolve: need 1 <= cap <= %d", kMaxCap);
+  MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0,
+              "moe_route_resolve: x and w must be 16-byte aligned");
+  hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(router_logits_kernel, dim3((n_experts + 3) / 4, 1), dim3(256), 0, s,
+                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias, 1,
+                     hidden, n_experts, logits);
+  int rc = check_launch("moe_route_resolve(logits)");
+  if (rc) return rc;
+#define MOE_TR(PE, PC)                                                                          \
+  hipLaunchKernelGGL((topk_resolve_kernel<PE, PC>), dim3(1), dim3(64), 0, s, logits, n_experts, \
+                     top_k, ids, weights, slot_of, slot_expert, slot_stamp, cap, step, out_slot, \
+                     fetch_slot, fetch_expert, nmiss, stats)
+  if (n_experts <= 256) {
+    if (cap <= 256) MOE_TR(4, 4); else if (cap <= 1024) MOE_TR(4, 16); else MOE_TR(4, 64);
+  } else if (n_experts <= 1024) {
+    if (cap <= 256) MOE_TR(16, 4); else if (cap <= 1024) MOE_TR(16, 16); else MOE_TR(16, 64);
+  } else {
+    if (cap <= 256) MOE_TR(64, 4); else if (cap <= 1024) MOE_TR(64, 16); else MOE_TR(64, 64);
+  }
+#undef MOE_TR
+  return check_launch("moe_route_resolve(topk+resolve)");
 }

@@ -99,7 +99,6 @@ class DecodeHarness:
         self.ids = torch.zeros((L, 1, K), **i32)
         self.wts = torch.zeros((L, 1, K), dtype=torch.float32, device=dev)
         self.logits = torch.zeros((L, 1, E), dtype=torch.float32, device=dev)
-        self.arrivals = torch.zeros((L, self.lib.router_arrivals(1)), **i32)
         self.out_slot = torch.zeros((L, 1, K), **i32)
         self.fslot = torch.zeros((L, K), **i32)
         self.fexp = torch.zeros((L, K), **i32)
@@ -140,22 +139,25 @@ class DecodeHarness:
     def layer(self, l: int) -> None:
         cfg, lib = self.cfg, self.lib
         torch.mm(self.x, self.w_stub[l], out=self.h)
-        lib.router_topk(self.h, self.gate[l], self.bias_live[l], cfg.top_k, self.logits[l],
-                        self.arrivals[l], self.ids[l], self.wts[l])
         w13, s13, w2, s2 = self.views[l]
         if cfg.mode == "cached":
-            lib.resolve_slots(self.ids[l], self.slot_of[l], self.slot_expert[l], self.stamp[l],
-                              self.step[l], self.out_slot[l], self.fslot[l], self.fexp[l],
-                              self.nmiss[l], self.stats[l])
+            # router + slot resolve (two launches), then the miss fetch
+            lib.route_resolve(self.h, self.gate[l], self.bias_live[l], cfg.top_k, self.logits[l],
+                              self.ids[l], self.wts[l], self.slot_of[l], self.slot_expert[l],
+                              self.stamp[l], self.step[l], self.out_slot[l], self.fslot[l],
+                              self.fexp[l], self.nmiss[l], self.stats[l])
             lib.fetch([self.pairs[l]], self.fexp[l], self.fslot[l], self.nmiss[l],
                       max_jobs=cfg.top_k, blocks_per_job=cfg.blocks_per_job)
             slots = self.out_slot[l]
         else:
+            lib.router_topk(self.h, self.gate[l], self.bias_live[l], cfg.top_k, self.logits[l],
+                            self.ids[l], self.wts[l])
             lib.fetch([self.pairs[l]], self.ids[l].view(-1), self.fixed_slots.view(-1),
                       self.all_miss, max_jobs=cfg.top_k, blocks_per_job=cfg.blocks_per_job)
             slots = self.fixed_slots
-        lib.fp8_moe_forward(self.h, slots, self.wts[l], w13, s13, w2, s2, self.y, self.ws)
-        torch.add(self.h, self.y, out=self.x)
+        # x = h + MoE(h), the residual add fused into the down kernel
+        lib.fp8_moe_forward(self.h, slots, self.wts[l], w13, s13, w2, s2, self.x, self.ws,
+                            residual=self.h)
 
     def step_eager(self) -> None:
         # every step starts from the same input token state (the stub has no

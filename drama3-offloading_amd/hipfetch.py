@@ -52,14 +52,16 @@ SIGNATURES = {
     "moe_resolve_slots": (C.c_int, [_vp, _i32, _i32, _vp, _i32, _vp, _vp, _i32, _vp, _vp, _vp,
                                     _vp, _vp, _vp, _vp]),
     "moe_fetch": (C.c_int, [C.POINTER(FetchPair), _i32, _vp, _vp, _vp, _i32, _i32, _vp]),
-    "moe_router_topk": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _i32,
-                                  _vp, _i32, _vp]),
+    "moe_router_topk": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _i32, _vp,
+                                  _i32, _vp]),
+    "moe_route_resolve": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp,
+                                    _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "moe_fp8_moe_workspace": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "moe_fp8_moe_forward": (C.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
                                       _i32, _i32, _i32, _vp, _vp, _sz, _vp]),
     "moe_fp8_moe_forward_ex": (C.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp,
                                          _vp, _i32, _i32, _i32, C.POINTER(ExpertStrides), _vp,
-                                         _vp, _sz, _i32, _vp]),
+                                         _vp, _vp, _sz, _i32, _vp]),
     "moe_permute": (C.c_int, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
     "moe_unpermute": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp]),
     "moe_unique_inverse": (C.c_int, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
@@ -156,27 +158,34 @@ class Native:
                                         blocks_per_job, self.stream()), "moe_fetch")
 
     # ------------------------------------------------------------ router
-    @staticmethod
-    def router_arrivals(tokens: int) -> int:
-        """int32 counters moe_router_topk needs (zeroed once at allocation)."""
-        return (tokens + 3) // 4
-
-    def router_topk(self, x, w, bias, top_k: int, logits, arrivals, ids, weights) -> None:
+    def router_topk(self, x, w, bias, top_k: int, logits, ids, weights) -> None:
         T, H = x.shape
         E = w.shape[0]
-        if arrivals.numel() < self.router_arrivals(T) or arrivals.dtype.itemsize != 4:
-            raise ValueError(f"arrivals must be int32[{self.router_arrivals(T)}] (zeroed)")
         self._check(self.cdll.moe_router_topk(
             x.data_ptr(), w.data_ptr(), self._ptr(bias), T, H, E, top_k, logits.data_ptr(),
-            arrivals.data_ptr(), ids.data_ptr(), self._dtype_code(ids), weights.data_ptr(),
-            self._dtype_code(weights), self.stream()), "moe_router_topk")
+            ids.data_ptr(), self._dtype_code(ids), weights.data_ptr(), self._dtype_code(weights),
+            self.stream()), "moe_router_topk")
+
+    def route_resolve(self, x, w, bias, top_k: int, logits, ids, weights, slot_of, slot_expert,
+                      stamp, step, out_slot, fetch_slot, fetch_expert, nmiss, stats=None) -> None:
+        """Router + slot resolve of one token (ids int32, weights float32)."""
+        if x.shape[0] != 1:
+            raise ValueError("route_resolve takes exactly one token")
+        H = x.shape[1]
+        E = w.shape[0]
+        self._check(self.cdll.moe_route_resolve(
+            x.data_ptr(), w.data_ptr(), self._ptr(bias), H, E, top_k, logits.data_ptr(),
+            ids.data_ptr(), weights.data_ptr(), slot_of.data_ptr(), slot_expert.data_ptr(),
+            stamp.data_ptr(), slot_expert.numel(), step.data_ptr(), out_slot.data_ptr(),
+            fetch_slot.data_ptr(), fetch_expert.data_ptr(), nmiss.data_ptr(), self._ptr(stats),
+            self.stream()), "moe_route_resolve")
 
     # ------------------------------------------------------------ experts
     def fp8_moe_workspace(self, tokens, top_k, n_experts, hidden, inter) -> int:
         return int(self.cdll.moe_fp8_moe_workspace(tokens, top_k, n_experts, hidden, inter))
 
     def fp8_moe_forward(self, x, ids, weights, w13, s13, w2, s2, out, workspace,
-                        mode: int = 0) -> None:
+                        mode: int = 0, residual=None) -> None:
         """w13/s13/w2/s2 may be strided along the expert axis (views into a
         packed record pool); every other dimension must be contiguous."""
         T, H = x.shape
@@ -190,7 +199,8 @@ class Native:
         self._check(self.cdll.moe_fp8_moe_forward_ex(
             x.data_ptr(), ids.data_ptr(), self._dtype_code(ids), weights.data_ptr(),
             self._dtype_code(weights), T, K, w13.data_ptr(), s13.data_ptr(), w2.data_ptr(),
-            s2.data_ptr(), n, H, inter, C.byref(es), out.data_ptr(), workspace.data_ptr(),
+            s2.data_ptr(), n, H, inter, C.byref(es), self._ptr(residual), out.data_ptr(),
+            workspace.data_ptr(),
             workspace.numel() * workspace.element_size(), mode, self.stream()),
             "moe_fp8_moe_forward")
 

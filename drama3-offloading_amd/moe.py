@@ -78,8 +78,7 @@ def route(x: torch.Tensor, gate_weight: torch.Tensor, top_k: int = 8,
 
     x [T, H] bf16, gate_weight [E, H] bf16.  Returns (topk_ids [T, k],
     topk_weights [T, k], logits [T, E] float32).  `out` may be a preallocated
-    (ids, weights, logits, arrivals) tuple (graph capture); arrivals is the
-    router's int32 counter array, zeroed once."""
+    (ids, weights, logits) triple (graph capture)."""
     lib = hipfetch.require()
     T = x.shape[0]
     E = gate_weight.shape[0]
@@ -87,11 +86,9 @@ def route(x: torch.Tensor, gate_weight: torch.Tensor, top_k: int = 8,
         ids = torch.empty((T, top_k), dtype=ids_dtype, device=x.device)
         wts = torch.empty((T, top_k), dtype=weights_dtype, device=x.device)
         logits = torch.empty((T, E), dtype=torch.float32, device=x.device)
-        arrivals = torch.zeros(lib.router_arrivals(T), dtype=torch.int32, device=x.device)
     else:
-        ids, wts, logits, arrivals = out
-    lib.router_topk(x.contiguous(), gate_weight.contiguous(), bias, top_k, logits, arrivals, ids,
-                    wts)
+        ids, wts, logits = out
+    lib.router_topk(x.contiguous(), gate_weight.contiguous(), bias, top_k, logits, ids, wts)
     return ids, wts, logits
 
 

@@ -120,17 +120,30 @@ int moe_fetch(const moe_fetch_pair* pairs, int32_t npairs,
  * [tokens, n_experts] to `logits` (caller-provided, also the workspace).
  * Logits are float32 roundings of float64-accumulated exact products;
  * selection is by descending logit, ties to the lower index.
- * `arrivals` is int32[ceil(tokens/4)], zeroed once when allocated; each call
- * leaves it zeroed again (the workgroups of one launch count in on it and the
- * last one selects).  One launch; calls must not overlap on one `arrivals`.
  * Replaces upstream's gate + softmax + topk + norm_topk_prob
  * (moe.py:217-220 per notes/01-static-findings.md:133-138).
  * Constraints: hidden % 8 == 0, 1 <= top_k <= 32, top_k <= n_experts <= 4096. */
 int moe_router_topk(const void* x, const void* w, const float* bias,
                     int32_t tokens, int32_t hidden, int32_t n_experts,
-                    int32_t top_k, float* logits, int32_t* arrivals, void* ids,
-                    int32_t ids_dtype, void* weights, int32_t w_dtype,
-                    void* stream);
+                    int32_t top_k, float* logits, void* ids, int32_t ids_dtype,
+                    void* weights, int32_t w_dtype, void* stream);
+
+/* Decode-step fusion of the router and the slot-table resolve for ONE token:
+ * moe_router_topk (ids int32 [top_k], weights f32 [top_k], logits f32
+ * [n_experts]) followed by moe_resolve_slots on those ids, in two launches
+ * instead of three.  Outputs and table updates are exactly those of the two
+ * entry points called in sequence.  It has no single counterpart in the
+ * reference: it fuses the router (moe.py:217-220) with _resolve_slots
+ * (bin/devcache.py:45-98) as they occur back to back in the decode step
+ * (bin/devcache.py:230-239). */
+int moe_route_resolve(const void* x, const void* w, const float* bias,
+                      int32_t hidden, int32_t n_experts, int32_t top_k,
+                      float* logits, int32_t* ids, float* weights,
+                      int32_t* slot_of, int32_t* slot_expert,
+                      int64_t* slot_stamp, int32_t cap, int64_t* step,
+                      int32_t* out_slot, int32_t* fetch_slot,
+                      int32_t* fetch_expert, int32_t* nmiss, int64_t* stats,
+                      void* stream);
 
 /* ------------------------------------------------------- expert compute */
 
@@ -171,14 +184,18 @@ typedef struct moe_expert_strides {
   int64_t s2;
 } moe_expert_strides;
 
-/* moe_fp8_moe_forward with explicit expert strides (NULL = dense) and a
- * kernel choice: mode 0 automatic, 1 per-pair GEMV, 2 grouped. */
+/* moe_fp8_moe_forward with explicit expert strides (NULL = dense), an
+ * optional bf16 residual [tokens, hidden] added to the bf16 result the way a
+ * bf16 tensor add would (out = bf16(residual + bf16(sum_k w*y)); NULL =
+ * none; it may be x itself, not out), and a kernel choice: mode 0 automatic,
+ * 1 per-pair GEMV, 2 grouped. */
 int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t ids_dtype,
                            const void* weights, int32_t w_dtype,
                            int32_t tokens, int32_t top_k, const void* w13,
                            const float* s13, const void* w2, const float* s2,
                            int32_t n_experts, int32_t hidden, int32_t inter,
-                           const moe_expert_strides* strides, void* out,
+                           const moe_expert_strides* strides,
+                           const void* residual, void* out,
                            void* workspace, size_t workspace_bytes,
                            int32_t mode, void* stream);
 

@@ -109,12 +109,11 @@ def test_whole_decode_layer_graph_replays_match_eager(lib, dev, pair):
     rids = torch.empty((1, K), dtype=torch.int64, device=dev)
     rw = torch.empty((1, K), dtype=torch.float32, device=dev)
     rl = torch.empty((1, E), dtype=torch.float32, device=dev)
-    arr = torch.zeros(1, dtype=torch.int32, device=dev)
     out = torch.empty((1, H), dtype=torch.bfloat16, device=dev)
     ws = torch.empty(1 << 20, dtype=torch.uint8, device=dev)
 
     def step(hmod, o):
-        moe.route(x_live, gate, K, bias=bias, out=(rids, rw, rl, arr))
+        moe.route(x_live, gate, K, bias=bias, out=(rids, rw, rl))
         sl = devcache.dev_resolve_and_fetch(hmod, rids)
         fp8_moe_forward(x_live, sl.reshape(1, K), rw, hmod._dc_w13, hmod._dc_s13, hmod._dc_w2,
                         hmod._dc_s2, out=o, workspace=ws)

@@ -145,3 +145,28 @@ def test_rejects_cpu_inputs():
                         torch.zeros((1, 256, 256), dtype=torch.float8_e4m3fn),
                         torch.ones((1, 2, 2)), torch.zeros((1, 256, 128), dtype=torch.float8_e4m3fn),
                         torch.ones((1, 2, 1)))
+
+
+def test_residual_fusion_equals_bf16_add(lib, dev):
+    """out = bf16(residual + bf16(moe)) inside the down kernel equals the MoE
+    output followed by a separate bf16 tensor add."""
+    import synth
+    E, H, I, T, K = 12, 2048, 512, 3, 8
+    host, devt = _experts(13, E, H, I, "blockq", dev)
+    x = synth.hidden_states(13, T).to(dev)
+    res = synth.hidden_states(14, T).to(dev)
+    rng = np.random.default_rng(15)
+    ids = torch.tensor(np.stack([rng.choice(E, K, replace=False) for _ in range(T)]), device=dev)
+    w = torch.full((T, K), 1.0 / K, device=dev)
+    plain = _run(x, ids, w, devt)
+    fused = torch.empty_like(plain)
+    ws = torch.empty(lib.fp8_moe_workspace(T, K, E, H, I), dtype=torch.uint8, device=dev)
+    w13, s13, w2, s2 = devt
+    lib.fp8_moe_forward(x, ids, w, w13.view(torch.float8_e4m3fn), s13,
+                        w2.view(torch.float8_e4m3fn), s2, fused, ws, residual=res)
+    fused_x = torch.empty_like(plain)
+    lib.fp8_moe_forward(x, ids, w, w13.view(torch.float8_e4m3fn), s13,
+                        w2.view(torch.float8_e4m3fn), s2, fused_x, ws, residual=x)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, res + plain)
+    assert torch.equal(fused_x, x + plain)

@@ -109,3 +109,45 @@ def test_unpermute_matches_oracle(lib, dev):
     want = operm.unpermute(y.numpy(), opos, w.numpy(), K)
     got = out.float().cpu().numpy()
     assert np.abs(got - want).max() <= np.abs(want).max() * 2 ** -8
+
+
+def test_route_resolve_equals_router_then_resolve(lib, dev):
+    """The fused decode entry gives the oracle's router ids/weights and the
+    oracle's slot decisions, step after step, tables included."""
+    import synth
+    from oracle import slots as oslots
+    E, H, K, C = 256, 2048, 8, 20
+    w = synth.router_weight(7).to(dev)
+    rng = np.random.default_rng(3)
+    i32 = dict(dtype=torch.int32, device=dev)
+    slot_of = torch.empty(E, **i32)
+    slot_expert = torch.empty(C, **i32)
+    stamp = torch.empty(C, dtype=torch.int64, device=dev)
+    step = torch.empty(1, dtype=torch.int64, device=dev)
+    stats = torch.zeros(2, dtype=torch.int64, device=dev)
+    lib.slots_init(slot_of, slot_expert, stamp, step)
+    logits = torch.empty((1, E), device=dev)
+    ids = torch.empty((1, K), **i32)
+    wts = torch.empty((1, K), device=dev)
+    out_slot = torch.empty(K, **i32)
+    fs = torch.empty(K, **i32)
+    fe = torch.empty(K, **i32)
+    nm = torch.empty(1, **i32)
+    tab = oslots.SlotTable.fresh(E, C)
+    for s in range(30):
+        x = synth.hidden_states(500 + s, 1).to(dev)
+        bias = torch.from_numpy((rng.gumbel(size=E) * 2).astype(np.float32)).to(dev)
+        lib.route_resolve(x, w, bias, K, logits, ids, wts, slot_of, slot_expert, stamp, step,
+                          out_slot, fs, fe, nm, stats)
+        torch.cuda.synchronize()
+        o_ids, o_w, o_lg = orouter.route(x.float().cpu().numpy(), w.float().cpu().numpy(), K,
+                                         bias.cpu().numpy())
+        assert np.array_equal(ids.cpu().numpy(), o_ids), f"step {s}"
+        np.testing.assert_allclose(wts.cpu().numpy(), o_w, rtol=2e-6, atol=1e-7)
+        want = oslots.resolve(tab, o_ids[0].tolist())
+        n = int(nm.item())
+        assert out_slot.tolist() == want[0] and fs[:n].tolist() == want[1]
+        assert fe[:n].tolist() == want[2]
+    so, se, st, stp = tab.arrays()
+    assert np.array_equal(slot_of.cpu().numpy(), so) and np.array_equal(stamp.cpu().numpy(), st)
+    assert int(step.item()) == int(stp)

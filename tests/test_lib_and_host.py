@@ -40,7 +40,10 @@ def test_preconditions_are_rejected_without_launching(lib):
     assert c.moe_fp8_moe_forward(1, 1, 0, 1, 2, 1, 8, 16, 1, 16, 1, 4, 2000, 512, 1, 16, 1 << 30,
                                  None) == -1
     assert b"hidden" in c.moe_last_error()
-    assert c.moe_router_topk(16, 16, None, 1, 2048, 256, 40, 1, 1, 1, 0, 1, 2, None) == -1
+    assert c.moe_router_topk(16, 16, None, 1, 2048, 256, 40, 1, 1, 0, 1, 2, None) == -1
+    assert c.moe_route_resolve(16, 16, None, 2048, 256, 8, 1, 1, 1, 1, 1, 1, 9999, 1, 1, 1, 1, 1,
+                               None, None) == -1
+    assert b"cap" in c.moe_last_error()
 
 
 def test_workspace_size_formula(lib):
