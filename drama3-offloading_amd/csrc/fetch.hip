@@ -6,43 +6,57 @@
 // :182).  This kernel reads which expert goes to which slot, and how many
 // jobs there are, from device memory when it runs.
 //
-// Shape: grid (blocks_per_job, max_jobs), 256 threads.  Job j = blockIdx.y
-// copies expert fetch_expert[j] into slot fetch_slot[j] for every buffer
-// pair; jobs with j >= *nmiss retire at once, so the grid can be sized for
-// the worst case (every id a miss) and stay static under capture.
+// Work distribution: the nmiss queued records (read at run time) are cut
+// into pieces of kFetchThreads * kFetchUnroll 16-byte vectors (8 KiB) per
+// buffer pair, and the pieces are dealt round-robin to every workgroup of the
+// grid, whatever the miss count.  The grid is deliberately small:
+// blocks_per_job * min(max_jobs, 8) workgroups of 128 threads keep about
+// 128 KiB of host reads in flight at the default of 2, which is the host
+// link's bandwidth-delay product (~57 GB/s x ~2 us).  Measured on MI355X, more
+// outstanding reads lower the throughput (51 GB/s with 64 x 256-thread
+// workgroups per job against 56.5 GB/s here at 8 misses, 53.9 at 1 miss; the
+// copy engine's H2D rate on the same pool is 57.2 GB/s).
 //
-// Transfer: 16-byte loads per lane, wave-contiguous (a wave instruction
-// covers 1 KiB of one record), UNROLL loads in flight per lane before the
-// matching stores, so each wave keeps UNROLL KiB of host reads outstanding.
+// Each lane issues kFetchUnroll 16-byte loads, wave-contiguous (one wave
+// instruction covers 1 KiB of one record), before the matching stores.
 // Pairs whose sizes or addresses are not 16-byte aligned (tiny scale blocks
-// of toy shapes) take a 4-byte path in the same launch.
+// of toy shapes) are copied in 4-byte words by whole workgroups.
 #include "common.hpp"
 
 namespace moe {
 
-constexpr int kFetchThreads = 256;
+constexpr int kFetchThreads = 128;
 constexpr int kFetchUnroll = 4;
-
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kFetchMaxJobsInGrid = 8;
 
 struct FetchArgs {
   const char* src[4];
   char* dst[4];
   int64_t bytes[4];
-  int32_t vec16[4];   // 1 if the pair takes the 16-byte path
+  int64_t pieces[4];      // pieces of this pair per record
+  int32_t vec16[4];       // 1 if the pair takes the 16-byte path
   int32_t npairs;
+  int64_t pieces_per_job; // sum of pieces over pairs
 };
 
 __global__ __launch_bounds__(kFetchThreads) void fetch_kernel(FetchArgs a,
                                                               const int32_t* __restrict__ fexp,
                                                               const int32_t* __restrict__ fslot,
-                                                              const int32_t* __restrict__ nmiss) {
-  const int j = blockIdx.y;
-  if (j >= *nmiss) return;
-  const int64_t e = fexp[j];
-  const int64_t s = fslot[j];
-  // block b of a job owns the rows b, b + gridDim.x, ... of blockDim.x*UNROLL vectors
-  for (int p = 0; p < a.npairs; ++p) {
+                                                              const int32_t* __restrict__ nmiss,
+                                                              int32_t max_jobs) {
+  const int32_t nm = min(*nmiss, max_jobs);
+  const int64_t total = static_cast<int64_t>(nm) * a.pieces_per_job;
+  const int64_t row = static_cast<int64_t>(kFetchThreads) * kFetchUnroll;   // vectors per piece
+  for (int64_t item = blockIdx.x; item < total; item += gridDim.x) {
+    const int64_t j = item / a.pieces_per_job;
+    int64_t k = item - j * a.pieces_per_job;
+    int p = 0;
+    while (p + 1 < a.npairs && k >= a.pieces[p]) {
+      k -= a.pieces[p];
+      ++p;
+    }
+    const int64_t e = fexp[j];
+    const int64_t s = fslot[j];
     const int64_t bytes = a.bytes[p];
     const char* src = a.src[p] + e * bytes;
     char* dst = a.dst[p] + s * bytes;
@@ -50,28 +64,23 @@ __global__ __launch_bounds__(kFetchThreads) void fetch_kernel(FetchArgs a,
       const int64_t n = bytes >> 4;
       const u32x4* sv = reinterpret_cast<const u32x4*>(src);
       u32x4* dv = reinterpret_cast<u32x4*>(dst);
-      const int64_t row = static_cast<int64_t>(blockDim.x) * kFetchUnroll;
-      // rows of blockDim*UNROLL vectors are interleaved across the job's blocks
-      for (int64_t r0 = blockIdx.x * row; r0 < n; r0 += gridDim.x * row) {
-        const int64_t base = r0 + threadIdx.x;
-        if (r0 + row <= n) {
-          u32x4 v[kFetchUnroll];
+      const int64_t r0 = k * row;
+      const int64_t base = r0 + threadIdx.x;
+      if (r0 + row <= n) {
+        u32x4 v[kFetchUnroll];
 #pragma unroll
-          for (int u = 0; u < kFetchUnroll; ++u)
-            v[u] = __builtin_nontemporal_load(sv + base + u * blockDim.x);
+        for (int u = 0; u < kFetchUnroll; ++u)
+          v[u] = __builtin_nontemporal_load(sv + base + u * kFetchThreads);
 #pragma unroll
-          for (int u = 0; u < kFetchUnroll; ++u) dv[base + u * blockDim.x] = v[u];
-        } else {
-          for (int64_t i = base; i < n && i < r0 + row; i += blockDim.x) dv[i] = sv[i];
-        }
+        for (int u = 0; u < kFetchUnroll; ++u) dv[base + u * kFetchThreads] = v[u];
+      } else {
+        for (int64_t i = base; i < n; i += kFetchThreads) dv[i] = sv[i];
       }
     } else {
       const int64_t n = bytes >> 2;
       const uint32_t* sw = reinterpret_cast<const uint32_t*>(src);
       uint32_t* dw = reinterpret_cast<uint32_t*>(dst);
-      for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
-           i += static_cast<int64_t>(gridDim.x) * blockDim.x)
-        dw[i] = sw[i];
+      for (int64_t i = threadIdx.x; i < n; i += kFetchThreads) dw[i] = sw[i];
     }
   }
 }
@@ -86,10 +95,11 @@ extern "C" int moe_fetch(const moe_fetch_pair* pairs, int32_t npairs,
   MOE_REQUIRE(npairs >= 1 && npairs <= 4, "moe_fetch: need 1 <= npairs <= 4 (got %d)", npairs);
   MOE_REQUIRE(fetch_expert && fetch_slot && nmiss, "moe_fetch: NULL job list");
   MOE_REQUIRE(max_jobs >= 1 && max_jobs <= 65535, "moe_fetch: need 1 <= max_jobs <= 65535");
-  MOE_REQUIRE(blocks_per_job >= 1 && blocks_per_job <= 65535,
-              "moe_fetch: need 1 <= blocks_per_job <= 65535");
+  MOE_REQUIRE(blocks_per_job >= 1 && blocks_per_job <= 4096,
+              "moe_fetch: need 1 <= blocks_per_job <= 4096");
   moe::FetchArgs a = {};
   a.npairs = npairs;
+  const int64_t row = static_cast<int64_t>(moe::kFetchThreads) * moe::kFetchUnroll;
   for (int p = 0; p < npairs; ++p) {
     const uintptr_t sa = reinterpret_cast<uintptr_t>(pairs[p].src);
     const uintptr_t da = reinterpret_cast<uintptr_t>(pairs[p].dst);
@@ -103,8 +113,12 @@ extern "C" int moe_fetch(const moe_fetch_pair* pairs, int32_t npairs,
     a.dst[p] = static_cast<char*>(pairs[p].dst);
     a.bytes[p] = b;
     a.vec16[p] = (b % 16 == 0 && sa % 16 == 0 && da % 16 == 0) ? 1 : 0;
+    a.pieces[p] = a.vec16[p] ? ((b >> 4) + row - 1) / row : 1;
+    a.pieces_per_job += a.pieces[p];
   }
-  hipLaunchKernelGGL(moe::fetch_kernel, dim3(blocks_per_job, max_jobs), dim3(moe::kFetchThreads),
-                     0, moe::as_stream(stream), a, fetch_expert, fetch_slot, nmiss);
+  const int grid = blocks_per_job * (max_jobs < moe::kFetchMaxJobsInGrid ? max_jobs
+                                                                          : moe::kFetchMaxJobsInGrid);
+  hipLaunchKernelGGL(moe::fetch_kernel, dim3(grid), dim3(moe::kFetchThreads), 0,
+                     moe::as_stream(stream), a, fetch_expert, fetch_slot, nmiss, max_jobs);
   return moe::check_launch("moe_fetch");
 }

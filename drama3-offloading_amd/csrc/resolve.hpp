@@ -9,7 +9,7 @@
 //
 // Nothing in the loop waits on memory: slot stamps and owners live in
 // registers (C/64 slots per lane), lane r holds id r of the current chunk of
-// 64 and its slot as loaded at the start of the chunk, and every eviction or
+// 64 and its slot as it was at the start of the chunk, and every eviction or
 // assignment is applied to the later lanes' copies immediately, so each id
 // sees exactly the table the sequential loop would.  The victim search is a
 // wave-wide arg-min.  Lane 0 issues the table writes, in program order.
@@ -21,8 +21,140 @@ namespace moe {
 
 constexpr int kMaxCap = 4096;
 
-// id_at(i) -> expert id at position i of the call (evaluated by lane i%64 of
-// chunk i/64); out-of-range ids (< 0 or >= n_experts) are reported as slot -1.
+// Slot stamps and owners of a table, slot c = lane + 64*j in lane's register j.
+template <int PER>
+struct SlotRegs {
+  int64_t st[PER];
+  int32_t se[PER];
+
+  __device__ __forceinline__ void load(const int64_t* stamp, const int32_t* slot_expert,
+                                       int32_t cap) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int c = lane + 64 * j;
+      st[j] = c < cap ? stamp[c] : INT64_MAX;
+      se[j] = c < cap ? slot_expert[c] : -1;
+    }
+  }
+};
+
+// slot_of of an expert table of at most 64*PER entries, entry x in lane x%64's
+// register x/64; lookup(x) for a per-lane x via PER shuffles.
+template <int PER>
+struct ExpertRegs {
+  int32_t so[PER];
+
+  __device__ __forceinline__ void load(const int32_t* slot_of, int32_t n_experts) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int x = lane + 64 * j;
+      so[j] = x < n_experts ? slot_of[x] : -1;
+    }
+  }
+  __device__ __forceinline__ int32_t lookup(int32_t x) const {
+    int32_t r = -1;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int32_t v = __shfl(so[j], x & 63, 64);
+      if ((x >> 6) == j) r = v;
+    }
+    return r;
+  }
+};
+
+// Resolve one chunk of <= 64 ids (lane r: my_e = id r, my_s = its slot now).
+// Returns nothing; updates the registers, the table in memory (lane 0), the
+// outputs, and nm / hits.
+template <int PER>
+__device__ __forceinline__ void resolve_chunk(SlotRegs<PER>& t, int32_t my_e, int32_t my_s,
+                                              int n, int32_t base, int64_t step, int32_t cap,
+                                              int32_t* __restrict__ slot_of,
+                                              int32_t* __restrict__ slot_expert,
+                                              int32_t* __restrict__ out_slot,
+                                              int32_t* __restrict__ fetch_slot,
+                                              int32_t* __restrict__ fetch_expert, int32_t& nm,
+                                              int64_t& hits) {
+  const int lane = threadIdx.x & 63;
+  for (int r = 0; r < n; ++r) {
+    const int32_t e = __shfl(my_e, r, 64);
+    int32_t s = __shfl(my_s, r, 64);
+    if (e < 0) {
+      if (lane == 0) out_slot[base + r] = -1;
+      continue;
+    }
+    if (s < 0) {
+      int64_t bst = INT64_MAX;
+      int32_t bix = INT32_MAX;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        const int c = lane + 64 * j;
+        if (c < cap && t.st[j] < bst) { bst = t.st[j]; bix = c; }
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const int64_t ost = __shfl_xor(bst, o, 64);
+        const int32_t oix = __shfl_xor(bix, o, 64);
+        if (ost < bst || (ost == bst && oix < bix)) { bst = ost; bix = oix; }
+      }
+      s = bix;
+      int32_t vloc = -1;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        if (j == (s >> 6)) {
+          vloc = t.se[j];
+          if ((s & 63) == lane) t.se[j] = e;
+        }
+      }
+      const int32_t victim = __shfl(vloc, s & 63, 64);
+      if (lane > r) {                      // later ids see the table as it is now
+        if (my_e == victim) my_s = -1;
+        if (my_e == e) my_s = s;
+      }
+      if (lane == 0) {
+        if (victim >= 0) slot_of[victim] = -1;
+        slot_of[e] = s;
+        slot_expert[s] = e;
+        fetch_slot[nm] = s;
+        fetch_expert[nm] = e;
+      }
+      ++nm;
+    } else {
+      ++hits;
+    }
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      if (j == (s >> 6) && (s & 63) == lane) t.st[j] = step;
+    if (lane == 0) out_slot[base + r] = s;
+  }
+}
+
+template <int PER>
+__device__ __forceinline__ void resolve_finish(const SlotRegs<PER>& t, int64_t step, int32_t nm,
+                                               int64_t hits, int32_t cap,
+                                               int64_t* __restrict__ stamp,
+                                               int64_t* __restrict__ step_ptr,
+                                               int32_t* __restrict__ nmiss_ptr,
+                                               int64_t* __restrict__ stats) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int c = lane + 64 * j;
+    if (c < cap) stamp[c] = t.st[j];
+  }
+  if (lane == 0) {
+    *step_ptr = step;
+    *nmiss_ptr = nm;
+    if (stats) {
+      stats[0] += hits;
+      stats[1] += nm;
+    }
+  }
+}
+
+// General resolve of k ids from memory: id_at(i) -> id i (called by lane
+// i%64 of chunk i/64); out-of-range ids are reported as slot -1.
 template <int PER, typename IdAt>
 __device__ __forceinline__ void resolve_wave_impl(IdAt id_at, int32_t k, int32_t n_experts,
                                                   int32_t* __restrict__ slot_of,
@@ -35,14 +167,8 @@ __device__ __forceinline__ void resolve_wave_impl(IdAt id_at, int32_t k, int32_t
                                                   int32_t* __restrict__ nmiss_ptr,
                                                   int64_t* __restrict__ stats) {
   const int lane = threadIdx.x & 63;
-  int64_t st[PER];
-  int32_t se[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int c = lane + 64 * j;
-    st[j] = c < cap ? stamp[c] : INT64_MAX;
-    se[j] = c < cap ? slot_expert[c] : -1;
-  }
+  SlotRegs<PER> t;
+  t.load(stamp, slot_expert, cap);
   // read at run time, never a launch argument: a captured step would
   // otherwise stamp the same value on every replay
   const int64_t step = *step_ptr + 1;
@@ -58,86 +184,11 @@ __device__ __forceinline__ void resolve_wave_impl(IdAt id_at, int32_t k, int32_t
       else
         my_e = -1;
     }
-    const int n = min(64, k - base);
-    for (int r = 0; r < n; ++r) {
-      const int32_t e = __shfl(my_e, r, 64);
-      int32_t s = __shfl(my_s, r, 64);
-      if (e < 0) {
-        if (lane == 0) out_slot[base + r] = -1;
-        continue;
-      }
-      if (s < 0) {
-        int64_t bst = INT64_MAX;
-        int32_t bix = INT32_MAX;
-#pragma unroll
-        for (int j = 0; j < PER; ++j) {
-          const int c = lane + 64 * j;
-          if (c < cap && st[j] < bst) { bst = st[j]; bix = c; }
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-          const int64_t ost = __shfl_xor(bst, o, 64);
-          const int32_t oix = __shfl_xor(bix, o, 64);
-          if (ost < bst || (ost == bst && oix < bix)) { bst = ost; bix = oix; }
-        }
-        s = bix;
-        int32_t vloc = -1;
-#pragma unroll
-        for (int j = 0; j < PER; ++j) {
-          if (j == (s >> 6)) {
-            vloc = se[j];
-            if ((s & 63) == lane) se[j] = e;
-          }
-        }
-        const int32_t victim = __shfl(vloc, s & 63, 64);
-        if (lane > r) {                      // later ids see the table as it is now
-          if (my_e == victim) my_s = -1;
-          if (my_e == e) my_s = s;
-        }
-        if (lane == 0) {
-          if (victim >= 0) slot_of[victim] = -1;
-          slot_of[e] = s;
-          slot_expert[s] = e;
-          fetch_slot[nm] = s;
-          fetch_expert[nm] = e;
-        }
-        ++nm;
-      } else {
-        ++hits;
-      }
-#pragma unroll
-      for (int j = 0; j < PER; ++j)
-        if (j == (s >> 6) && (s & 63) == lane) st[j] = step;
-      if (lane == 0) out_slot[base + r] = s;
-    }
+    resolve_chunk<PER>(t, my_e, my_s, min(64, k - base), base, step, cap, slot_of, slot_expert,
+                       out_slot, fetch_slot, fetch_expert, nm, hits);
     if (base + 64 < k) __threadfence();
   }
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int c = lane + 64 * j;
-    if (c < cap) stamp[c] = st[j];
-  }
-  if (lane == 0) {
-    *step_ptr = step;
-    *nmiss_ptr = nm;
-    if (stats) {
-      stats[0] += hits;
-      stats[1] += nm;
-    }
-  }
-}
-
-// Ids already held one per lane (k <= 64): lane r passes the r-th id.
-template <int PER>
-__device__ __forceinline__ void resolve_wave(int32_t my_id, int32_t k, int32_t n_experts,
-                                             int32_t* slot_of, int32_t* slot_expert,
-                                             int64_t* stamp, int32_t cap, int64_t* step_ptr,
-                                             int32_t* out_slot, int32_t* fetch_slot,
-                                             int32_t* fetch_expert, int32_t* nmiss_ptr,
-                                             int64_t* stats) {
-  resolve_wave_impl<PER>([my_id](int) { return my_id; }, k, n_experts, slot_of, slot_expert,
-                         stamp, cap, step_ptr, out_slot, fetch_slot, fetch_expert, nmiss_ptr,
-                         stats);
+  resolve_finish<PER>(t, step, nm, hits, cap, stamp, step_ptr, nmiss_ptr, stats);
 }
 
 }  // namespace moe

@@ -143,6 +143,12 @@ __global__ __launch_bounds__(64) void topk_resolve_kernel(
     int32_t* __restrict__ fetch_expert, int32_t* __restrict__ nmiss_ptr,
     int64_t* __restrict__ stats) {
   const int lane = threadIdx.x;
+  // every load of the table goes out before the top-k: one memory round trip
+  SlotRegs<PERC> t;
+  t.load(stamp, slot_expert, cap);
+  ExpertRegs<PER> table;
+  table.load(slot_of, n_experts);
+  const int64_t step = *step_ptr + 1;
   int32_t id;
   float wt;
   wave_topk<PER>(logits, n_experts, top_k, &id, &wt);
@@ -151,8 +157,14 @@ __global__ __launch_bounds__(64) void topk_resolve_kernel(
     weights[lane] = wt;
   }
   // the picks are already one per lane: resolve them in pick order
-  resolve_wave<PERC>(lane < top_k ? id : -1, top_k, n_experts, slot_of, slot_expert, stamp, cap,
-                     step_ptr, out_slot, fetch_slot, fetch_expert, nmiss_ptr, stats);
+  const int32_t my_e = lane < top_k ? id : -1;
+  const int32_t found = table.lookup(my_e < 0 ? 0 : my_e);
+  const int32_t my_s = my_e < 0 ? -1 : found;
+  int32_t nm = 0;
+  int64_t hits = 0;
+  resolve_chunk<PERC>(t, my_e, my_s, top_k, 0, step, cap, slot_of, slot_expert, out_slot,
+                      fetch_slot, fetch_expert, nm, hits);
+  resolve_finish<PERC>(t, step, nm, hits, cap, stamp, step_ptr, nmiss_ptr, stats);
 }
 
 }  // namespace moe

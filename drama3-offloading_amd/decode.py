@@ -48,7 +48,7 @@ class DecodeConfig:
     drift_every: int = 50
     zipf_s: float = 1.1
     gate_std: float = 0.002
-    blocks_per_job: int = 64
+    blocks_per_job: int = 2
     noncoherent_pool: bool = False
 
 

@@ -39,8 +39,9 @@ EXPERT_BYTES = 3_146_496
 FETCH_BACKEND = "hip"
 _BACKENDS = ("hip", "cpp", "triton")
 _BACKEND_NOTED = False
-# Grid x-dimension of the fetch kernel per job (bin/devcache.py:193).
-CPP_BLOCKS_PER_JOB = 64
+# Fetch workgroups per job, up to 8 jobs (bin/devcache.py:193).  2 keeps
+# ~128 KiB of host reads in flight, the link's bandwidth-delay product.
+CPP_BLOCKS_PER_JOB = 2
 _dev_ptr_cache: dict[int, int] = {}
 
 

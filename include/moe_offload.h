@@ -98,9 +98,12 @@ typedef struct moe_fetch_pair {
 } moe_fetch_pair;
 
 /* Copy the queued misses host -> HBM with a zero-copy gather kernel.
- * Job j < *nmiss copies expert fetch_expert[j] into slot fetch_slot[j] for
- * every pair; jobs j >= *nmiss (read on the device at run time) retire
- * without writing.  The grid is (blocks_per_job, max_jobs) x 256 threads.
+ * Job j < min(*nmiss, max_jobs) copies expert fetch_expert[j] into slot
+ * fetch_slot[j] for every pair; *nmiss is read on the device at run time,
+ * so later jobs cost nothing.  The grid is blocks_per_job * min(max_jobs, 8)
+ * workgroups of 128 threads over which the queued records are dealt in
+ * 8 KiB pieces (default 2 per job: ~128 KiB of host reads in flight, the
+ * link's bandwidth-delay product; more outstanding reads measured slower).
  * Replaces fetch_experts/fetch_kernel (csrc/fetch_experts.cu:49-94) and the
  * four per-buffer launches of _cpp_fetch (bin/devcache.py:197-220) with one
  * launch.  Preconditions: 1 <= npairs <= 4; each pair's src, dst and bytes
