@@ -20,6 +20,7 @@
 // one wave per k; each wave turns its h row into aq in LDS, does its 16 output
 // rows of w2, and the workgroup sums the k partials in order.
 #include "common.hpp"
+#include "grouped.hpp"
 
 namespace moe {
 
@@ -291,14 +292,25 @@ __global__ __launch_bounds__(1024) void down_gemv_kernel(
 
 using namespace moe;
 
+// Calls of at most this many tokens take the per-pair GEMV kernels by default;
+// larger ones the grouped kernels, which read each expert's weights once.
+constexpr int32_t kGemvMaxTokens = 2;
+
+static bool use_grouped(int32_t tokens, int32_t hidden, int32_t mode) {
+  if (mode == 1) return false;
+  if (mode == 2) return true;
+  return tokens > kGemvMaxTokens && hidden % 256 == 0;
+}
+
 extern "C" size_t moe_fp8_moe_workspace(int32_t tokens, int32_t top_k, int32_t n_experts,
                                         int32_t hidden, int32_t inter) {
-  (void)n_experts;
-  (void)hidden;
-  if (tokens <= 0 || top_k <= 0 || inter <= 0) return 256;
-  // h: one float32 row of 2*inter per (token, expert) pair, 256-byte aligned
+  if (tokens <= 0 || top_k <= 0 || inter <= 0 || hidden <= 0 || n_experts <= 0) return 256;
+  // per-pair GEMV: one float32 row of 2*inter per (token, expert) pair
   const size_t h = static_cast<size_t>(tokens) * top_k * 2 * inter * sizeof(float);
-  return (h + 255) & ~static_cast<size_t>(255);
+  size_t need = (h + 255) & ~static_cast<size_t>(255);
+  // grouped: permutation, quantised activations and permuted outputs
+  const size_t g = grouped_layout(tokens, top_k, n_experts, hidden, inter).total;
+  return need > g ? need : g;
 }
 
 extern "C" int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t ids_dtype,
@@ -354,6 +366,16 @@ extern "C" int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t id
   const int ids64 = ids_dtype == MOE_I64;
   const int wbf16 = w_dtype == MOE_BF16;
   const int64_t pairs = static_cast<int64_t>(tokens) * top_k;
+  if (use_grouped(tokens, hidden, mode)) {
+    MOE_REQUIRE(hidden % 256 == 0, "moe_fp8_moe_forward: the grouped kernels need hidden %% 256 == 0");
+    MOE_REQUIRE(n_experts <= 4096 && pairs <= (1LL << 24) && tokens <= 65535,
+                "moe_fp8_moe_forward: grouped path limits: n_experts <= 4096, tokens <= 65535");
+    return launch_grouped(static_cast<const uint16_t*>(x), ids, ids64, weights, wbf16, tokens,
+                          top_k, static_cast<const uint8_t*>(w13), s13,
+                          static_cast<const uint8_t*>(w2), s2, es, n_experts, hidden, inter,
+                          static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out),
+                          static_cast<char*>(workspace), s);
+  }
   MOE_REQUIRE(pairs <= 65535LL, "moe_fp8_moe_forward: too many (token, expert) pairs (%lld)",
               (long long)pairs);
   hipLaunchKernelGGL(gateup_gemv_kernel, dim3((2 * inter) / 16, pairs), dim3(64), 0, s,

@@ -13,6 +13,7 @@
 // The result equals a stable sort by expert, identically on every run, and
 // no memory has to be cleared beforehand (nothing to memset in a graph).
 #include "common.hpp"
+#include "grouped.hpp"
 
 namespace moe {
 
@@ -158,6 +159,7 @@ __global__ __launch_bounds__(256) void unpermute_kernel(const float* __restrict_
                                                         const int32_t* __restrict__ pair_pos,
                                                         const void* __restrict__ weights,
                                                         int wbf16, int32_t top_k, int32_t hidden,
+                                                        const uint16_t* __restrict__ residual,
                                                         uint16_t* __restrict__ out) {
   const int64_t t = blockIdx.y;
   const int c = (blockIdx.x * 256 + threadIdx.x) * 4;
@@ -178,11 +180,16 @@ __global__ __launch_bounds__(256) void unpermute_kernel(const float* __restrict_
     acc.z = __fadd_rn(acc.z, __fmul_rn(w, v.z));
     acc.w = __fadd_rn(acc.w, __fmul_rn(w, v.w));
   }
+  uint16_t v[4] = {f32_to_bf16(acc.x), f32_to_bf16(acc.y), f32_to_bf16(acc.z),
+                   f32_to_bf16(acc.w)};
+  if (residual) {   // a bf16 tensor add: bf16(res + bf16(moe))
+    const uint16_t* r = residual + t * hidden + c;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = f32_to_bf16(bf16_to_f32(r[i]) + bf16_to_f32(v[i]));
+  }
   uint16_t* o = out + t * hidden + c;
-  o[0] = f32_to_bf16(acc.x);
-  o[1] = f32_to_bf16(acc.y);
-  o[2] = f32_to_bf16(acc.z);
-  o[3] = f32_to_bf16(acc.w);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = v[i];
 }
 
 int launch_permute(const void* ids, int ids64, int64_t P, int32_t n_experts, int32_t* counts,
@@ -193,9 +200,10 @@ int launch_permute(const void* ids, int ids64, int64_t P, int32_t n_experts, int
 }
 
 int launch_unpermute(const float* y, const int32_t* pair_pos, const void* weights, int wbf16,
-                     int32_t tokens, int32_t top_k, int32_t hidden, uint16_t* out, hipStream_t s) {
+                     int32_t tokens, int32_t top_k, int32_t hidden, const uint16_t* residual,
+                     uint16_t* out, hipStream_t s) {
   hipLaunchKernelGGL(unpermute_kernel, dim3((hidden / 4 + 255) / 256, tokens), dim3(256), 0, s,
-                     y, pair_pos, weights, wbf16, top_k, hidden, out);
+                     y, pair_pos, weights, wbf16, top_k, hidden, residual, out);
   return check_launch("moe_unpermute");
 }
 
@@ -244,5 +252,5 @@ extern "C" int moe_unpermute(const float* y, const int32_t* pair_pos, const void
   MOE_REQUIRE(reinterpret_cast<uintptr_t>(y) % 16 == 0, "moe_unpermute: y must be 16-byte aligned");
   if (tokens == 0) return MOE_OK;
   return launch_unpermute(y, pair_pos, weights, w_dtype == MOE_BF16 ? 1 : 0, tokens, top_k,
-                          hidden, static_cast<uint16_t*>(out), as_stream(stream));
+                          hidden, nullptr, static_cast<uint16_t*>(out), as_stream(stream));
 }
