@@ -13,16 +13,16 @@
 //                128 columns across the four waves, and writes aq/as rows in
 //                permuted order.
 //   down:        grid (E, H/256), 4 waves x 4 tiles of 16 output features;
-//                the A operand is the expert's contiguous aq rows.  y rows in
-//                permuted order, float32.
+//                the activations are the expert's contiguous aq rows.  y rows
+//                in permuted order, float32.
 //   unpermute:   out[t] = sum_k w[t,k] * y[pos[t,k]] (permute.hip).
 //
-// MFMA 16x16x128 e4m3: tokens are the rows (A operand), weight rows the
-// columns (B operand); every lane supplies the same 32-byte reduction slice
-// of its row/column as the decode GEMV does, block scales multiply each
-// 128-deep block result as weight_scale * activation_scale, and the blocks
-// are summed in the same order, so a row computed here equals the decode
-// GEMV's row for the same (token, expert).
+// MFMA 16x16x128 e4m3 with the same operand roles as the decode GEMV:
+// weight rows are the A operand, activations the B operand (here one token
+// per B column), every lane supplies the same 32-byte reduction slice, block
+// scales multiply each 128-deep block result as weight_scale *
+// activation_scale, and the blocks are summed in the same order -- so every
+// (token, expert) row computed here is bit-identical to the decode GEMV's.
 #include "common.hpp"
 #include "grouped.hpp"
 
@@ -70,6 +70,9 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restr
 
 // --------------------------------------------------------------- gate/up
 
+// Weight rows are the A operand (16 rows per tile, as in the decode GEMV) and
+// the tokens the B operand (16 token columns per tile): lane l's result
+// element i is weight row 4*(l/16) + i of the tile for token column l % 16.
 __global__ __launch_bounds__(256) void grouped_gateup_kernel(
     const uint8_t* __restrict__ xq, const float* __restrict__ xs,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
@@ -77,7 +80,7 @@ __global__ __launch_bounds__(256) void grouped_gateup_kernel(
     const float* __restrict__ s13, int64_t w13_es, int64_t s13_es, int32_t hidden, int32_t inter,
     uint8_t* __restrict__ aq, float* __restrict__ as_) {
   __shared__ int32_t tok[kMTiles * 16];
-  __shared__ float rowmax[4][kMTiles * 16];
+  __shared__ float colmax[4][kMTiles * 16];
   const int e = blockIdx.x;
   const int jb = blockIdx.y;
   const int32_t m_e = counts[e];
@@ -86,9 +89,10 @@ __global__ __launch_bounds__(256) void grouped_gateup_kernel(
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int q = lane >> 4;
+  const int col = lane & 15;
   const int G = hidden >> 7;
   const int Gi = inter >> 7;
-  // the four column tiles of this wave: gate j0, gate j0+16, up j0, up j0+16
+  // the four row tiles of this wave: gate j0, gate j0+16, up j0, up j0+16
   const int j0 = jb * 128 + wave * 32;
   int rows[4];
   rows[0] = j0;
@@ -98,11 +102,11 @@ __global__ __launch_bounds__(256) void grouped_gateup_kernel(
   const uint8_t* wb = w13 + static_cast<int64_t>(e) * w13_es;
   const float* sb = s13 + static_cast<int64_t>(e) * s13_es;
   for (int m0 = 0; m0 < m_e; m0 += kMTiles * 16) {
-    const int mrows = min(kMTiles * 16, m_e - m0);
-    const int ntiles = (mrows + 15) >> 4;
+    const int mcols = min(kMTiles * 16, m_e - m0);
+    const int ntiles = (mcols + 15) >> 4;
     __syncthreads();
     if (threadIdx.x < kMTiles * 16)
-      tok[threadIdx.x] = threadIdx.x < mrows ? sorted_pairs[off + m0 + threadIdx.x] / top_k : -1;
+      tok[threadIdx.x] = threadIdx.x < mcols ? sorted_pairs[off + m0 + threadIdx.x] / top_k : -1;
     __syncthreads();
     v4f acc[kMTiles][4];
 #pragma unroll
@@ -110,72 +114,70 @@ __global__ __launch_bounds__(256) void grouped_gateup_kernel(
 #pragma unroll
       for (int t = 0; t < 4; ++t) acc[mt][t] = v4f{0.f, 0.f, 0.f, 0.f};
     for (int g = 0; g < G; ++g) {
-      v8i b[4];
+      v8i wa[4];
       float ws[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        b[t] = load_op32_nt(wb + static_cast<int64_t>(rows[t] + (lane & 15)) * hidden + g * 128 + q * 32);
+        wa[t] = load_op32_nt(wb + static_cast<int64_t>(rows[t] + col) * hidden + g * 128 + q * 32);
         ws[t] = sb[(rows[t] >> 7) * G + g];
       }
 #pragma unroll
       for (int mt = 0; mt < kMTiles; ++mt) {
         if (mt < ntiles) {
-          const int tr = tok[mt * 16 + (lane & 15)];
-          v8i a = v8i{0, 0, 0, 0, 0, 0, 0, 0};
-          if (tr >= 0) a = load_op32(xq + static_cast<int64_t>(tr) * hidden + g * 128 + q * 32);
-          float xsr[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int tt = tok[mt * 16 + 4 * q + i];
-            xsr[i] = tt >= 0 ? xs[static_cast<int64_t>(tt) * G + g] : 0.0f;
+          const int tc = tok[mt * 16 + col];
+          v8i xb = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+          float xsc = 0.0f;
+          if (tc >= 0) {
+            xb = load_op32(xq + static_cast<int64_t>(tc) * hidden + g * 128 + q * 32);
+            xsc = xs[static_cast<int64_t>(tc) * G + g];
           }
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             const v4f z = {0.f, 0.f, 0.f, 0.f};
-            const v4f d = mfma_e4m3_16x16x128(a, b[t], z);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[mt][t][i] += d[i] * (ws[t] * xsr[i]);
+            const v4f d = mfma_e4m3_16x16x128(wa[t], xb, z);
+            const float sc = ws[t] * xsc;
+            acc[mt][t][0] += d[0] * sc;
+            acc[mt][t][1] += d[1] * sc;
+            acc[mt][t][2] += d[2] * sc;
+            acc[mt][t][3] += d[3] * sc;
           }
         }
       }
     }
-    // a = SiLU(gate) * up; per-token amax over the 128 columns of group jb
+    // a = SiLU(gate) * up for j = j0 + 16t + 4q + i; per-token amax over the
+    // 128 columns of group jb (8 per lane, 4 row groups, 4 waves)
     float av[kMTiles][2][4];
 #pragma unroll
     for (int mt = 0; mt < kMTiles; ++mt) {
+      float mx = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float mx = 0.0f;
+      for (int t = 0; t < 2; ++t) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int i = 0; i < 4; ++i) {
           av[mt][t][i] = silu_mul(acc[mt][t][i], acc[mt][t + 2][i]);
           mx = fmaxf(mx, fabsf(av[mt][t][i]));
         }
-        // the 16 lanes of a row group hold the 16 columns of each tile
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-        if ((lane & 15) == 0) rowmax[wave][mt * 16 + 4 * q + i] = mx;
       }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      if (q == 0) colmax[wave][mt * 16 + col] = mx;
     }
     __syncthreads();
 #pragma unroll
     for (int mt = 0; mt < kMTiles; ++mt) {
-      if (mt < ntiles) {
+      const int c = mt * 16 + col;
+      if (mt < ntiles && c < mcols) {
+        const float amax = fmaxf(fmaxf(colmax[0][c], colmax[1][c]), fmaxf(colmax[2][c], colmax[3][c]));
+        const float sc = act_scale(amax);
+        const int64_t pos = off + m0 + c;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = mt * 16 + 4 * q + i;
-          if (r < mrows) {
-            const float amax = fmaxf(fmaxf(rowmax[0][r], rowmax[1][r]),
-                                     fmaxf(rowmax[2][r], rowmax[3][r]));
-            const float sc = act_scale(amax);
-            const int64_t pos = off + m0 + r;
+        for (int t = 0; t < 2; ++t) {
+          uint32_t wd = 0;
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
-              aq[pos * inter + j0 + t * 16 + (lane & 15)] =
-                  static_cast<uint8_t>(quant_e4m3(av[mt][t][i], sc));
-            if (wave == 0 && (lane & 15) == 0) as_[pos * Gi + jb] = sc;
-          }
+          for (int i = 0; i < 4; ++i) wd |= quant_e4m3(av[mt][t][i], sc) << (8 * i);
+          *reinterpret_cast<uint32_t*>(aq + pos * inter + j0 + t * 16 + 4 * q) = wd;
         }
+        if (wave == 0 && q == 0) as_[pos * Gi + jb] = sc;
       }
     }
   }
@@ -183,6 +185,9 @@ __global__ __launch_bounds__(256) void grouped_gateup_kernel(
 
 // --------------------------------------------------------------- down
 
+// w2 rows (output features) are the A operand, the expert's contiguous aq
+// rows (tokens) the B operand; lane l's element i is feature 4*(l/16) + i of
+// the tile for token column l % 16.
 __global__ __launch_bounds__(256) void grouped_down_kernel(
     const uint8_t* __restrict__ aq, const float* __restrict__ as_,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
@@ -195,62 +200,61 @@ __global__ __launch_bounds__(256) void grouped_down_kernel(
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int q = lane >> 4;
+  const int col = lane & 15;
   const int Gi = inter >> 7;
   const int c0 = blockIdx.y * 256 + wave * 64;
   const uint8_t* wb = w2 + static_cast<int64_t>(e) * w2_es;
   const float* sb = s2 + static_cast<int64_t>(e) * s2_es;
   for (int m0 = 0; m0 < m_e; m0 += kMTiles * 16) {
-    const int mrows = min(kMTiles * 16, m_e - m0);
-    const int ntiles = (mrows + 15) >> 4;
+    const int mcols = min(kMTiles * 16, m_e - m0);
+    const int ntiles = (mcols + 15) >> 4;
     v4f acc[kMTiles][4];
 #pragma unroll
     for (int mt = 0; mt < kMTiles; ++mt)
 #pragma unroll
       for (int t = 0; t < 4; ++t) acc[mt][t] = v4f{0.f, 0.f, 0.f, 0.f};
     for (int g = 0; g < Gi; ++g) {
-      v8i b[4];
+      v8i wa[4];
       float ws[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int c = c0 + t * 16;
-        b[t] = load_op32_nt(wb + static_cast<int64_t>(c + (lane & 15)) * inter + g * 128 + q * 32);
+        wa[t] = load_op32_nt(wb + static_cast<int64_t>(c + col) * inter + g * 128 + q * 32);
         ws[t] = sb[(c >> 7) * Gi + g];
       }
 #pragma unroll
       for (int mt = 0; mt < kMTiles; ++mt) {
         if (mt < ntiles) {
-          const int rr = mt * 16 + (lane & 15);
-          v8i a = v8i{0, 0, 0, 0, 0, 0, 0, 0};
-          if (rr < mrows)
-            a = load_op32(aq + static_cast<int64_t>(off + m0 + rr) * inter + g * 128 + q * 32);
-          float sar[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int r = mt * 16 + 4 * q + i;
-            sar[i] = r < mrows ? as_[static_cast<int64_t>(off + m0 + r) * Gi + g] : 0.0f;
+          const int cc = mt * 16 + col;
+          v8i ab = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+          float asc = 0.0f;
+          if (cc < mcols) {
+            const int64_t pos = off + m0 + cc;
+            ab = load_op32(aq + pos * inter + g * 128 + q * 32);
+            asc = as_[pos * Gi + g];
           }
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             const v4f z = {0.f, 0.f, 0.f, 0.f};
-            const v4f d = mfma_e4m3_16x16x128(a, b[t], z);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[mt][t][i] += d[i] * (ws[t] * sar[i]);
+            const v4f d = mfma_e4m3_16x16x128(wa[t], ab, z);
+            const float sc = ws[t] * asc;
+            acc[mt][t][0] += d[0] * sc;
+            acc[mt][t][1] += d[1] * sc;
+            acc[mt][t][2] += d[2] * sc;
+            acc[mt][t][3] += d[3] * sc;
           }
         }
       }
     }
 #pragma unroll
     for (int mt = 0; mt < kMTiles; ++mt) {
-      if (mt < ntiles) {
+      const int cc = mt * 16 + col;
+      if (mt < ntiles && cc < mcols) {
+        float* yr = y + static_cast<int64_t>(off + m0 + cc) * hidden + c0 + 4 * q;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = mt * 16 + 4 * q + i;
-          if (r < mrows) {
-            float* yr = y + static_cast<int64_t>(off + m0 + r) * hidden + c0 + (lane & 15);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) yr[t * 16] = acc[mt][t][i];
-          }
-        }
+        for (int t = 0; t < 4; ++t)
+          *reinterpret_cast<float4*>(yr + t * 16) =
+              make_float4(acc[mt][t][0], acc[mt][t][1], acc[mt][t][2], acc[mt][t][3]);
       }
     }
   }

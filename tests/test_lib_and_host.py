@@ -47,8 +47,17 @@ def test_preconditions_are_rejected_without_launching(lib):
 
 
 def test_workspace_size_formula(lib):
-    assert lib.fp8_moe_workspace(1, 8, 256, 2048, 512) == 8 * 1024 * 4
-    assert lib.fp8_moe_workspace(512, 8, 256, 2048, 512) == 512 * 8 * 1024 * 4
+    def al(v):
+        return (v + 255) // 256 * 256
+
+    def grouped(T, K, E, H, I):
+        P = T * K
+        return (al(4 * E) + al(4 * (E + 1)) + 2 * al(4 * P) + al(T * H) + al(4 * T * H // 128)
+                + al(P * I) + al(4 * P * I // 128) + al(4 * P * H))
+
+    for T in (1, 2, 5, 512):
+        gemv = al(T * 8 * 1024 * 4)
+        assert lib.fp8_moe_workspace(T, 8, 256, 2048, 512) == max(gemv, grouped(T, 8, 256, 2048, 512))
 
 
 def test_loader_contract_missing_library(tmp_path, monkeypatch):
