@@ -115,6 +115,15 @@ __device__ __forceinline__ v8i load_op32(const uint8_t* p) {
   return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
 }
 
+// acc += d * sc with one fused multiply-add (one rounding) per element,
+// written out so that every kernel rounds its block sums identically.
+__device__ __forceinline__ void block_fma(v4f& acc, const v4f& d, float sc) {
+  acc[0] = fmaf(d[0], sc, acc[0]);
+  acc[1] = fmaf(d[1], sc, acc[1]);
+  acc[2] = fmaf(d[2], sc, acc[2]);
+  acc[3] = fmaf(d[3], sc, acc[3]);
+}
+
 // 16x16x128 e4m3 x e4m3 -> f32 on gfx950, block scales neutral (E8M0 127 = 1.0).
 // Lane l supplies row (l % 16) of A and column (l % 16) of B, 32 bytes each,
 // covering the same 32 reduction indices for both operands; the four lane

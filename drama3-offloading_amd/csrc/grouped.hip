@@ -136,10 +136,7 @@ __global__ __launch_bounds__(256) void grouped_gateup_kernel(
             const v4f z = {0.f, 0.f, 0.f, 0.f};
             const v4f d = mfma_e4m3_16x16x128(wa[t], xb, z);
             const float sc = ws[t] * xsc;
-            acc[mt][t][0] += d[0] * sc;
-            acc[mt][t][1] += d[1] * sc;
-            acc[mt][t][2] += d[2] * sc;
-            acc[mt][t][3] += d[3] * sc;
+            block_fma(acc[mt][t], d, sc);
           }
         }
       }
@@ -238,10 +235,7 @@ __global__ __launch_bounds__(256) void grouped_down_kernel(
             const v4f z = {0.f, 0.f, 0.f, 0.f};
             const v4f d = mfma_e4m3_16x16x128(wa[t], ab, z);
             const float sc = ws[t] * asc;
-            acc[mt][t][0] += d[0] * sc;
-            acc[mt][t][1] += d[1] * sc;
-            acc[mt][t][2] += d[2] * sc;
-            acc[mt][t][3] += d[3] * sc;
+            block_fma(acc[mt][t], d, sc);
           }
         }
       }

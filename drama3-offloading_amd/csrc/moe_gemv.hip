@@ -166,10 +166,7 @@ __global__ __launch_bounds__(64) void gateup_gemv_kernel(
         const v4f z = {0.f, 0.f, 0.f, 0.f};
         const v4f d = mfma_e4m3_16x16x128(a[c], b, z);
         const float sc = srow[g] * xs[g];
-        acc[0] += d[0] * sc;
-        acc[1] += d[1] * sc;
-        acc[2] += d[2] * sc;
-        acc[3] += d[3] * sc;
+        block_fma(acc, d, sc);
       }
     }
   }
@@ -263,10 +260,7 @@ __global__ __launch_bounds__(1024) void down_gemv_kernel(
           const v4f z = {0.f, 0.f, 0.f, 0.f};
           const v4f d = mfma_e4m3_16x16x128(a[c], b, z);
           const float sc = srow[g] * as_[wave][g];
-          acc[0] += d[0] * sc;
-          acc[1] += d[1] * sc;
-          acc[2] += d[2] * sc;
-          acc[3] += d[3] * sc;
+          block_fma(acc, d, sc);
         }
       }
     }
