@@ -5,7 +5,7 @@
 //   h[p][r] = sum_g s13[e][r/128][g] * xs[g] * <w13[e][r][g*128:+128], xq[g*128:+128]>
 //   a = SiLU(h[:I]) * h[I:], quantised per 128 (aq, as)
 //   y[c]    = sum_g s2[e][c/128][g] * as[g] * <w2[e][c][g*128:+128], aq[g*128:+128]>
-//   out[t]  = sum_k w[t][k] * y_k  (k in order, float32) -> bf16
+//   out[t]  = fma(w[t][k], y_k, out[t]) for k in order, float32 -> bf16
 //
 // Each 128-term block product runs on one v_mfma_scale_f32_16x16x128_f8f6f4
 // with the weight rows as the A operand (16 rows per wave) and the quantised
@@ -15,8 +15,8 @@
 // whole cache lines.  The block scales multiply the fp32 block result, so the
 // scale of every 128x128 weight block is applied exactly once per block.
 //
-// Kernel 1 (gate/up): grid (2I/64, pairs), 4 waves x 16 rows, x quantised
-// into LDS by the workgroup.  Kernel 2 (down + combine): grid (H/16, tokens),
+// Kernel 1 (gate/up): grid (2I/16, pairs), one wave of 16 rows per workgroup,
+// x quantised into LDS by that wave.  Kernel 2 (down + combine): grid (H/16, tokens),
 // one wave per k; each wave turns its h row into aq in LDS, does its 16 output
 // rows of w2, and the workgroup sums the k partials in order.
 #include "common.hpp"
@@ -36,43 +36,6 @@ __device__ __forceinline__ int64_t load_id(const void* ids, int ids64, int64_t p
 __device__ __forceinline__ float load_w(const void* w, int wbf16, int64_t p) {
   return wbf16 ? bf16_to_f32(reinterpret_cast<const uint16_t*>(w)[p])
                : reinterpret_cast<const float*>(w)[p];
-}
-
-// Quantise `n` bf16 values (n % 2048 handled in passes) into LDS codes and
-// per-128 scales with 256 threads: 16 threads x 8 values per group.
-__device__ __forceinline__ void quantize_row_bf16_to_lds(const uint16_t* __restrict__ xr, int n,
-                                                         uint8_t* __restrict__ q,
-                                                         float* __restrict__ sc) {
-  const int tid = threadIdx.x;
-  for (int base = 0; base < n; base += 2048) {
-    const int i = base + tid * 8;
-    float v[8];
-    float amax = 0.0f;
-    if (i < n) {
-      uint4 raw = *reinterpret_cast<const uint4*>(xr + i);
-      const uint32_t r[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[2 * j] = __uint_as_float(r[j] << 16);
-        v[2 * j + 1] = __uint_as_float(r[j] & 0xffff0000u);
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
-    }
-    // the 16 threads of a 128-group are 16 consecutive lanes of one wave
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-    if (i < n) {
-      const float s = act_scale(amax);
-      uint32_t lo = 0, hi = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) lo |= quant_e4m3(v[j], s) << (8 * j);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) hi |= quant_e4m3(v[4 + j], s) << (8 * j);
-      *reinterpret_cast<uint2*>(q + i) = make_uint2(lo, hi);
-      if ((tid & 15) == 0) sc[i >> 7] = s;
-    }
-  }
 }
 
 // ------------------------------------------------------------ kernel 1
@@ -192,6 +155,7 @@ __global__ __launch_bounds__(1024) void down_gemv_kernel(
   __shared__ __align__(16) uint8_t aq[kMaxK][kMaxInter];
   __shared__ float as_[kMaxK][kMaxInter / 128];
   __shared__ float part[kMaxK][16];
+  __shared__ float wpart[kMaxK];
   const int wave = threadIdx.x >> 6;   // == k
   const int lane = threadIdx.x & 63;
   const int64_t t = blockIdx.y;
@@ -266,15 +230,16 @@ __global__ __launch_bounds__(1024) void down_gemv_kernel(
     }
   }
   if ((lane & 15) == 0) {
-    const float wk = load_w(weights, wbf16, p);
     const float nan = __builtin_nanf("");
 #pragma unroll
-    for (int i = 0; i < 4; ++i) part[wave][4 * q + i] = valid ? __fmul_rn(wk, acc[i]) : nan;
+    for (int i = 0; i < 4; ++i) part[wave][4 * q + i] = valid ? acc[i] : nan;
   }
+  if (lane == 0) wpart[wave] = load_w(weights, wbf16, p);
   __syncthreads();
   if (threadIdx.x < 16) {
+    // sum = fma(w_k, y_k, sum), k in order: the combine of the grouped path too
     float sum = 0.0f;
-    for (int k = 0; k < top_k; ++k) sum = __fadd_rn(sum, part[k][threadIdx.x]);
+    for (int k = 0; k < top_k; ++k) sum = fmaf(wpart[k], part[k][threadIdx.x], sum);
     const int64_t o = t * hidden + c0 + threadIdx.x;
     uint16_t y = f32_to_bf16(sum);
     if (residual) y = f32_to_bf16(bf16_to_f32(residual[o]) + bf16_to_f32(y));

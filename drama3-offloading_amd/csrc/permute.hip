@@ -152,7 +152,7 @@ __global__ __launch_bounds__(kPermThreads) void unique_inverse_kernel(
 }
 
 // out[t][c] = sum_k w[t][k] * y[pair_pos[t*K+k]][c], k in order -> bf16.
-// Each product is rounded before it is added (no fused multiply-add), which
+// Each term is one explicit fused multiply-add, acc = fma(w, y, acc), which
 // is exactly the combine of the per-pair GEMV path, so both paths give
 // bit-identical outputs.
 __global__ __launch_bounds__(256) void unpermute_kernel(const float* __restrict__ y,
@@ -175,10 +175,10 @@ __global__ __launch_bounds__(256) void unpermute_kernel(const float* __restrict_
       continue;
     }
     const float4 v = *reinterpret_cast<const float4*>(y + static_cast<int64_t>(pos) * hidden + c);
-    acc.x = __fadd_rn(acc.x, __fmul_rn(w, v.x));
-    acc.y = __fadd_rn(acc.y, __fmul_rn(w, v.y));
-    acc.z = __fadd_rn(acc.z, __fmul_rn(w, v.z));
-    acc.w = __fadd_rn(acc.w, __fmul_rn(w, v.w));
+    acc.x = fmaf(w, v.x, acc.x);
+    acc.y = fmaf(w, v.y, acc.y);
+    acc.z = fmaf(w, v.z, acc.z);
+    acc.w = fmaf(w, v.w, acc.w);
   }
   uint16_t v[4] = {f32_to_bf16(acc.x), f32_to_bf16(acc.y), f32_to_bf16(acc.z),
                    f32_to_bf16(acc.w)};
