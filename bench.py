@@ -157,6 +157,117 @@ def gemv_standalone(lib, harness, reps: int = 400):
     return dt, K * per_expert + 2 * 2 * harness.cfg.hidden
 
 
+# ------------------------------------------------------------ kernel probes
+# One kernel (or one expert-FFN call) at a time on resident data, for the
+# roofline figures and for rocprofv3 (kernel trace and counter passes).
+
+def resident_records(dev, n: int, layout, seed: int = 3, distinct: int = 16):
+    """n packed expert records in HBM: `distinct` seeded N(0, 0.02) experts,
+    128x128-block quantised, repeated (the bytes differ only in address, which
+    is what the timing needs)."""
+    import torch
+    import synth
+    g = torch.Generator(device=dev).manual_seed(seed)
+    H, I = layout.hidden, layout.inter
+    w13, s13 = synth.quantize_blocks(torch.randn((distinct, 2 * I, H), generator=g, device=dev) * 0.02)
+    w2, s2 = synth.quantize_blocks(torch.randn((distinct, H, I), generator=g, device=dev) * 0.02)
+    base = layout.pack(w13, s13, w2, s2)
+    rec = torch.empty((n, layout.record_bytes), dtype=torch.uint8, device=dev)
+    for i in range(0, n, distinct):
+        m = min(distinct, n - i)
+        rec[i:i + m] = base[:m]
+    return rec
+
+
+def graph_time(dev, body, calls: int) -> float:
+    """Seconds per call of `body(r)` for r < calls, captured in one hipGraph
+    and timed with events on the stream the graph runs on."""
+    import torch
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        for r in range(min(3, calls)):
+            body(r)
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize(dev)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for r in range(calls):
+            body(r)
+    g.replay()
+    torch.cuda.synchronize(dev)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    g.replay()
+    b.record()
+    torch.cuda.synchronize(dev)
+    del g
+    return a.elapsed_time(b) / 1000.0 / calls
+
+
+def gemv_resident(lib, dev, layout, n_records: int = 2048, calls: int = 200, top_k: int = 8):
+    """Decode expert FFN (gate/up GEMV + down GEMV, 8 experts, 1 token) over
+    random experts of n_records resident records (6.4 GB at 2048, so the
+    256 MB Infinity Cache serves few of them).  Returns (s/call, bytes/call)."""
+    import numpy as np
+    import torch
+    rec = resident_records(dev, n_records, layout)
+    views = layout.views(rec)
+    rng = np.random.default_rng(11)
+    ids = torch.tensor(np.stack([rng.choice(n_records, top_k, replace=False)
+                                 for _ in range(calls)])[:, None, :], dtype=torch.int32, device=dev)
+    x = torch.randn((1, layout.hidden), device=dev).to(torch.bfloat16)
+    w = torch.full((1, top_k), 1.0 / top_k, device=dev)
+    out = torch.empty_like(x)
+    ws = torch.empty(lib.fp8_moe_workspace(1, top_k, n_records, layout.hidden, layout.inter),
+                     dtype=torch.uint8, device=dev)
+    dt = graph_time(dev, lambda r: lib.fp8_moe_forward(x, ids[r], w, *views, out, ws, mode=1), calls)
+    if not bool(torch.isfinite(out.float()).all()):
+        raise RuntimeError("GEMV probe produced non-finite output")
+    del rec
+    return dt, top_k * layout.record_bytes + 2 * 2 * layout.hidden
+
+
+def fill_pool_bytes(pool, dev, seed: int, chunk: int = 64) -> None:
+    """Seeded random bytes in every record of a page-locked pool (fetch
+    timing and byte-exact checks need distinct records, not weights)."""
+    import torch
+    g = torch.Generator(device=dev).manual_seed(seed)
+    RB = pool.layout.record_bytes
+    for e0 in range(0, pool.n, chunk):
+        n = min(chunk, pool.n - e0)
+        pool.write(e0, torch.randint(0, 256, (n, RB), generator=g, dtype=torch.uint8, device=dev))
+    torch.cuda.synchronize(dev)
+
+
+def run_probe(args) -> int:
+    """--probe gemv|fetch: the named kernel alone, many launches, one JSON line."""
+    import torch
+    import hipfetch
+    from hostpool import DRAMA3, HostPool
+    lib = hipfetch.require()
+    dev = torch.device("cuda:0")
+    if args.probe == "gemv":
+        dt, nbytes = gemv_resident(lib, dev, DRAMA3, calls=args.steps)
+        res = {"probe": "gemv", "what": "decode expert FFN, 8 experts x 1 token, resident records, "
+               "graph of back-to-back calls", "us_per_call": round(1e6 * dt, 3),
+               "bytes_per_call": nbytes, "GBps": round(nbytes / dt / 1e9, 2)}
+    elif args.probe == "fetch":
+        pools = [HostPool(256, DRAMA3) for _ in range(4)]
+        for i, p in enumerate(pools):
+            fill_pool_bytes(p, dev, i)
+        dt, nbytes = fetch_standalone(lib, pools, dev, reps=args.steps)
+        res = {"probe": "fetch", "what": "8 records of 3,146,496 B per launch from 4 page-locked "
+               "pools of 256 records", "us_per_launch": round(1e6 * dt, 2),
+               "bytes_per_launch": nbytes, "GBps": round(nbytes / dt / 1e9, 3)}
+        for p in pools:
+            p.close()
+    else:
+        raise SystemExit(f"unknown probe {args.probe!r}")
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 def cpu_baseline(harness, budget_s: float):
     import torch
     from oracle import cpu_moe
@@ -196,11 +307,15 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--noncoherent-pool", action="store_true")
+    ap.add_argument("--probe", choices=["gemv", "fetch"],
+                    help="time one kernel alone (--steps launches) instead of the decode step")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(expert parallelism is a design note only); run with --gpus 1", file=sys.stderr)
         return 2
+    if args.probe:
+        return run_probe(args)
 
     import torch
     import decode

@@ -8,6 +8,7 @@
 #include <stdio.h>
 
 #include "../../include/moe_offload.h"
+#include "e4m3.hpp"
 
 namespace moe {
 
@@ -42,40 +43,8 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
-// -------------------------------------------------------------- e4m3fn
-
-// float -> OCP e4m3fn code, round-to-nearest-even, saturating at +-448.
-// Every step is exact except the one rint(), so this is the correctly
-// rounded conversion; it matches the oracle's encoder bit for bit.
-__device__ __forceinline__ uint32_t f32_to_e4m3(float v) {
-  uint32_t sign = (__float_as_uint(v) >> 24) & 0x80u;
-  float a = fabsf(v);
-  if (!(a == a)) return sign | 0x7fu;          // NaN
-  if (a >= 448.0f) return sign | 0x7eu;        // saturate
-  if (a < 0.015625f) {                         // below 2^-6: subnormal grid 2^-9
-    uint32_t m = static_cast<uint32_t>(rintf(a * 512.0f));   // 0..8; 8 == code 8
-    return sign | m;
-  }
-  int e;
-  float fr = frexpf(a, &e);                    // a = fr * 2^e, fr in [0.5, 1)
-  // a = (1 + m/8) * 2^(e-1): mantissa grid is fr*16 - 8 in [0, 8)
-  uint32_t m = static_cast<uint32_t>(rintf(fr * 16.0f - 8.0f));
-  int eb = e - 1 + 7;
-  if (m == 8u) { m = 0u; eb += 1; }
-  return sign | (static_cast<uint32_t>(eb) << 3) | m;
-}
-
-// Per-128-group activation scale: amax / 448 in float32, division correctly
-// rounded (HIP's default float division).
-__device__ __forceinline__ float act_scale(float amax) { return amax / 448.0f; }
-
 // SiLU(g) * u in float32, the one formula every expert kernel uses.
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
-
-// Quantise v with scale s (s == 0 => 0).
-__device__ __forceinline__ uint32_t quant_e4m3(float v, float s) {
-  return s == 0.0f ? 0u : f32_to_e4m3(v / s);
-}
 
 // ------------------------------------------------------------ wave utils
 

@@ -40,6 +40,43 @@ __device__ __forceinline__ float load_w(const void* w, int wbf16, int64_t p) {
 
 // ------------------------------------------------------------ kernel 1
 
+// 32 bf16 values of x held by one lane (4 x 16 bytes, elements i..i+31) ->
+// e4m3 codes and the group scale in LDS.  Four consecutive lanes form one
+// 128-column group; every lane of the wave calls this (the group maximum is
+// a cross-lane exchange), lanes past the end with live == false.
+__device__ __forceinline__ void quantize_x32(const uint4 (&raw)[4], bool live, int i,
+                                             uint8_t* __restrict__ xq, float* __restrict__ xs) {
+  float v[32];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const uint32_t rr[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[u * 8 + 2 * j] = __uint_as_float(rr[j] << 16);
+      v[u * 8 + 2 * j + 1] = __uint_as_float(rr[j] & 0xffff0000u);
+    }
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  if (live) {
+    const float sc = act_scale(amax);
+    uint32_t wds[8];
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      uint32_t wd = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wd |= quant_e4m3(v[w * 4 + j], sc) << (8 * j);
+      wds[w] = wd;
+    }
+    *reinterpret_cast<uint4*>(xq + i) = make_uint4(wds[0], wds[1], wds[2], wds[3]);
+    *reinterpret_cast<uint4*>(xq + i + 16) = make_uint4(wds[4], wds[5], wds[6], wds[7]);
+    if ((threadIdx.x & 3) == 0) xs[i >> 7] = sc;
+  }
+}
+
 // One wave per workgroup, 16 weight rows of one (token, expert) pair.  The
 // wave first issues the loads of its whole 16 x H weight tile (up to 16
 // K-blocks, 32 bytes per lane each, all in flight at once), then quantises
@@ -63,49 +100,30 @@ __global__ __launch_bounds__(64) void gateup_gemv_kernel(
   const int q = lane >> 4;
   const uint8_t* wrow =
       w13 + (valid ? e : 0) * w13_es + static_cast<int64_t>(r0 + (lane & 15)) * hidden + q * 32;
-  v8i a[kGateUpChunk];
-  if (valid) {
-#pragma unroll
-    for (int c = 0; c < kGateUpChunk; ++c)
-      if (c < G) a[c] = load_op32_nt(wrow + c * 128);
-  }
-  // x[t] -> e4m3 codes + per-128 scales in LDS: 32 values per lane, 4 lanes per group
+  // The first 2048 values of x[t] are loaded before the weights: loads
+  // retire in issue order (vmcnt), so x issued first can be quantised while
+  // the weight tile is still in flight.  No load sits under a branch (lanes
+  // and blocks past the end re-read an in-bounds address and ignore it):
+  // a conditional load makes the compiler's wait at the join cover every
+  // load issued before it, weights included.
   const uint16_t* xr = x + t * hidden;
-  for (int base = 0; base < hidden; base += 2048) {
+  const uint4* xsrc = reinterpret_cast<const uint4*>(xr + (lane * 32 < hidden ? lane * 32 : 0));
+  uint4 xraw[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) xraw[u] = xsrc[u];
+  v8i a[kGateUpChunk];
+#pragma unroll
+  for (int c = 0; c < kGateUpChunk; ++c) a[c] = load_op32_nt(wrow + (c < G ? c : G - 1) * 128);
+  __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the math below
+  // x[t] -> e4m3 codes + per-128 scales in LDS: 32 values per lane, 4 lanes per group
+  quantize_x32(xraw, lane * 32 < hidden, lane * 32, xq, xs);
+  for (int base = 2048; base < hidden; base += 2048) {
     const int i = base + lane * 32;
-    float v[32];
-    float amax = 0.0f;
-    if (i < hidden) {
-      const uint4* src = reinterpret_cast<const uint4*>(xr + i);
+    const uint4* src = reinterpret_cast<const uint4*>(xr + (i < hidden ? i : 0));
+    uint4 raw[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const uint4 raw = src[u];
-        const uint32_t rr[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          v[u * 8 + 2 * j] = __uint_as_float(rr[j] << 16);
-          v[u * 8 + 2 * j + 1] = __uint_as_float(rr[j] & 0xffff0000u);
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
-    }
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    if (i < hidden) {
-      const float sc = act_scale(amax);
-      uint32_t wds[8];
-#pragma unroll
-      for (int w = 0; w < 8; ++w) {
-        uint32_t wd = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) wd |= quant_e4m3(v[w * 4 + j], sc) << (8 * j);
-        wds[w] = wd;
-      }
-      *reinterpret_cast<uint4*>(xq + i) = make_uint4(wds[0], wds[1], wds[2], wds[3]);
-      *reinterpret_cast<uint4*>(xq + i + 16) = make_uint4(wds[4], wds[5], wds[6], wds[7]);
-      if ((lane & 3) == 0) xs[i >> 7] = sc;
-    }
+    for (int u = 0; u < 4; ++u) raw[u] = src[u];
+    quantize_x32(raw, i < hidden, i, xq, xs);
   }
   __syncthreads();
   float* hp = h + p * rows2;
@@ -141,6 +159,35 @@ __global__ __launch_bounds__(64) void gateup_gemv_kernel(
 
 // ------------------------------------------------------------ kernel 2
 
+// SiLU(gate) * up of 8 intermediate columns j..j+7 held by one lane
+// (hr = gate[j..j+3], gate[j+4..j+7], up[j..j+3], up[j+4..j+7]) -> e4m3
+// codes and the group scale in LDS; 16 consecutive lanes form one 128-group.
+// Every lane of the wave calls this, lanes past the end with live == false.
+__device__ __forceinline__ void silu_quantize8(const float4 (&hr)[4], bool live, int j,
+                                               uint8_t* __restrict__ aq, float* __restrict__ as) {
+  const float gv[8] = {hr[0].x, hr[0].y, hr[0].z, hr[0].w, hr[1].x, hr[1].y, hr[1].z, hr[1].w};
+  const float uv[8] = {hr[2].x, hr[2].y, hr[2].z, hr[2].w, hr[3].x, hr[3].y, hr[3].z, hr[3].w};
+  float av[8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    av[i] = silu_mul(gv[i], uv[i]);
+    amax = fmaxf(amax, fabsf(av[i]));
+  }
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  if (live) {
+    const float sc = act_scale(amax);
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lo |= quant_e4m3(av[i], sc) << (8 * i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hi |= quant_e4m3(av[4 + i], sc) << (8 * i);
+    *reinterpret_cast<uint2*>(aq + j) = make_uint2(lo, hi);
+    if ((threadIdx.x & 15) == 0) as[j >> 7] = sc;
+  }
+}
+
 // Workgroup = one wave per k, 16 output rows of w2 per wave.  The weight
 // loads go out first; SiLU(gate)*up of the pair is quantised into LDS while
 // they travel; the k partial results are summed in k order.
@@ -167,43 +214,32 @@ __global__ __launch_bounds__(1024) void down_gemv_kernel(
   const int q = lane >> 4;
   const uint8_t* wrow =
       w2 + (valid ? e : 0) * w2_es + static_cast<int64_t>(c0 + (lane & 15)) * inter + q * 32;
-  v8i a[kDownChunk];
-  if (valid) {
-#pragma unroll
-    for (int c = 0; c < kDownChunk; ++c)
-      if (c < Gi) a[c] = load_op32_nt(wrow + c * 128);
-  }
+  // The pair's first 512 gate and up values are loaded before the weights
+  // (loads retire in issue order), so SiLU and the quantisation run while
+  // the weight tile is in flight.
+  // No load under a branch, for the reason given in the gate/up kernel.
   const float* hp = h + p * (2 * inter);
+  const int j0 = lane * 8 < inter ? lane * 8 : 0;
+  float4 hraw[4];
+  hraw[0] = *reinterpret_cast<const float4*>(hp + j0);
+  hraw[1] = *reinterpret_cast<const float4*>(hp + j0 + 4);
+  hraw[2] = *reinterpret_cast<const float4*>(hp + inter + j0);
+  hraw[3] = *reinterpret_cast<const float4*>(hp + inter + j0 + 4);
+  v8i a[kDownChunk];
+#pragma unroll
+  for (int c = 0; c < kDownChunk; ++c) a[c] = load_op32_nt(wrow + (c < Gi ? c : Gi - 1) * 128);
+  __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the math below
   // SiLU(gate) * up for this pair, quantised per 128 into LDS: 16 lanes x 8
-  for (int base = 0; base < inter; base += 512) {
+  silu_quantize8(hraw, lane * 8 < inter, lane * 8, aq[wave], as_[wave]);
+  for (int base = 512; base < inter; base += 512) {
     const int j = base + lane * 8;
-    float av[8];
-    float amax = 0.0f;
-    if (j < inter) {
-      const float4 g0 = *reinterpret_cast<const float4*>(hp + j);
-      const float4 g1 = *reinterpret_cast<const float4*>(hp + j + 4);
-      const float4 u0 = *reinterpret_cast<const float4*>(hp + inter + j);
-      const float4 u1 = *reinterpret_cast<const float4*>(hp + inter + j + 4);
-      const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-      const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        av[i] = silu_mul(gv[i], uv[i]);
-        amax = fmaxf(amax, fabsf(av[i]));
-      }
-    }
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-    if (j < inter) {
-      const float sc = act_scale(amax);
-      uint32_t lo = 0, hi = 0;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) lo |= quant_e4m3(av[i], sc) << (8 * i);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) hi |= quant_e4m3(av[4 + i], sc) << (8 * i);
-      *reinterpret_cast<uint2*>(&aq[wave][j]) = make_uint2(lo, hi);
-      if ((lane & 15) == 0) as_[wave][j >> 7] = sc;
-    }
+    const int jj = j < inter ? j : 0;
+    float4 hr[4];
+    hr[0] = *reinterpret_cast<const float4*>(hp + jj);
+    hr[1] = *reinterpret_cast<const float4*>(hp + jj + 4);
+    hr[2] = *reinterpret_cast<const float4*>(hp + inter + jj);
+    hr[3] = *reinterpret_cast<const float4*>(hp + inter + jj + 4);
+    silu_quantize8(hr, j < inter, j, aq[wave], as_[wave]);
   }
   __syncthreads();
 
