@@ -183,6 +183,7 @@ def install_dev_cache(model, device, capacity: int) -> int:
     Requires the host expert tensors to be page-locked (pin_experts)."""
     from moe import MoEExperts
     n = 0
+    classes = set()
     for layer in model.backbone.model.layers:
         experts = getattr(layer.mlp, "experts", None)
         if experts is None or experts.w13_weight.device.type != "cpu":
@@ -191,8 +192,14 @@ def install_dev_cache(model, device, capacity: int) -> int:
             raise RuntimeError(
                 "device cache needs pinned expert tensors; run pin_experts first")
         init_dev_cache(experts, device, capacity)
+        classes.add(type(experts))
         n += 1
-    MoEExperts.forward = dev_cached_forward
+    # the class the model's experts are built from (upstream's MoEExperts in
+    # the reference's model); this package's stand-in when there are none
+    for cls in classes or {MoEExperts}:
+        if not hasattr(cls, "_stock_forward"):
+            cls._stock_forward = cls.forward
+        cls.forward = dev_cached_forward
     return n
 
 

@@ -57,6 +57,24 @@ def test_fetch_zipf_lists_byte_exact(lib, dev, pool, length):
     assert _untouched(cache, length, 128)
 
 
+def test_fetch_list_of_256_as_two_replays_of_128(lib, dev, pool):
+    """A 256-long miss list exceeds the 128-slot cache: it runs as two
+    128-job launches over the two halves of the list, each checked."""
+    import synth
+    ids = synth.zipf_miss_list(np.random.default_rng(20261273), 256)
+    cache = torch.full((128 * RB,), 255, dtype=torch.uint8, device=dev)
+    fslot = torch.arange(128, dtype=torch.int32, device=dev)
+    nmiss = torch.tensor([128], dtype=torch.int32, device=dev)
+    src = lib.device_ptr_of(pool.data_ptr())
+    say("fetch: zipf list of 256 as 2 x 128")
+    for half in (ids[:128], ids[128:]):
+        fexp = torch.tensor(half, dtype=torch.int32, device=dev)
+        lib.fetch([(src, cache.data_ptr(), RB)], fexp, fslot, nmiss, max_jobs=128,
+                  blocks_per_job=2)
+        torch.cuda.synchronize()
+        assert _check(cache, half) == 0
+
+
 def test_fetch_honours_device_side_job_count(lib, dev, pool):
     cache = torch.full((8 * RB,), 255, dtype=torch.uint8, device=dev)
     ids = [200, 3, 77, 150, 9, 1, 255, 64]

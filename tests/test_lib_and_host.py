@@ -159,3 +159,22 @@ def test_zipf_generators_are_seeded_and_distinct():
     assert np.array_equal(a, b) and len(set(a.tolist())) == 64
     bias = synth.decode_route_bias(np.random.default_rng(0), 60, 2, 256, 1.1, 50)
     assert bias.shape == (60, 2, 256) and bias.dtype == np.float32
+
+
+def test_install_offload_hooks_the_given_expert_class():
+    """install_offload patches the class the model's experts are built from
+    (upstream's MoEExperts in the reference's model) and keeps its resident
+    forward as _stock_forward, idempotently (bin/offload.py:702-704)."""
+    import moe
+    import offload
+
+    class Upstream(moe.MoEExperts):     # stands in for fish-speech's class
+        def forward(self, x, topk_ids, topk_weights):
+            return x
+
+    orig = Upstream.forward
+    offload.install_offload(Upstream)
+    offload.install_offload(Upstream)
+    assert Upstream.forward is offload.offloaded_forward
+    assert Upstream._stock_forward is orig
+    assert moe.MoEExperts.forward is not offload.offloaded_forward
