@@ -30,6 +30,7 @@ sys.path.insert(0, str(ROOT / "drama3-offloading_amd"))
 
 METRIC = "decode tokens/s (40-layer MoE, bs=1) at 0%/~60% hit; fetch GB/s; %HBM peak"
 HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0      # dense e4m3 MFMA, MI355X
 PCIE5_X16_GBS = 64.0
 
 
@@ -126,37 +127,6 @@ def fetch_standalone(lib, pools, dev, jobs: int = 8, reps: int = 160, bpj: int =
     return dt, jobs * RB
 
 
-def gemv_standalone(lib, harness, reps: int = 400):
-    """Average duration of one decode expert FFN (gate/up + down kernels) on
-    8 resident records, rotating over all layers' caches (> 256 MiB of
-    distinct records between reuses, so the Infinity Cache does not serve them)."""
-    import numpy as np
-    import torch
-    dev = harness.dev
-    L, C, K = harness.cfg.layers, harness.C, harness.cfg.top_k
-    rng = np.random.default_rng(11)
-    slots = torch.tensor(np.stack([rng.choice(C, K, replace=False) for _ in range(reps)])[:, None, :],
-                         dtype=torch.int32, device=dev)
-    x = torch.randn((1, harness.cfg.hidden), device=dev).to(torch.bfloat16)
-    w = torch.full((1, K), 1.0 / K, device=dev)
-    out = torch.empty_like(x)
-    for r in range(4):
-        v = harness.views[r % L]
-        lib.fp8_moe_forward(x, slots[r], w, *v, out, harness.ws)
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for r in range(reps):
-        v = harness.views[r % L]
-        lib.fp8_moe_forward(x, slots[r], w, *v, out, harness.ws)
-    b.record()
-    torch.cuda.synchronize()
-    dt = a.elapsed_time(b) / 1000.0 / reps
-    lay = harness.layout
-    per_expert = lay.w13_bytes + lay.w2_bytes + lay.s13_bytes + lay.s2_bytes
-    return dt, K * per_expert + 2 * 2 * harness.cfg.hidden
-
-
 # ------------------------------------------------------------ kernel probes
 # One kernel (or one expert-FFN call) at a time on resident data, for the
 # roofline figures and for rocprofv3 (kernel trace and counter passes).
@@ -226,6 +196,146 @@ def gemv_resident(lib, dev, layout, n_records: int = 2048, calls: int = 200, top
         raise RuntimeError("GEMV probe produced non-finite output")
     del rec
     return dt, top_k * layout.record_bytes + 2 * 2 * layout.hidden
+
+
+def prefill_bench(lib, harness, tokens: int = 512, passes: int = 2):
+    """512-token prefill through all layers: router, distinct experts, one
+    fetch of their records from the page-locked pool (no host sync), grouped
+    FFN with the residual fused; then the grouped FFN alone on resident
+    gathered experts (HBM and MFMA figures)."""
+    import torch
+    import synth
+    from prefill import DevicePrefill
+    dev, cfg = harness.dev, harness.cfg
+    L, E, K, H = cfg.layers, cfg.n_experts, cfg.top_k, cfg.hidden
+    pf = DevicePrefill.for_records(E, K, tokens, dev, harness.layout)
+    # the prefill workload's own router: N(0, 0.02) gates, no popularity bias
+    g = torch.Generator(device=dev).manual_seed(cfg.seed + 5)
+    gate = (torch.randn((L, E, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    x0 = synth.hidden_states(cfg.seed + 7, tokens, H).to(dev)
+    x = x0.clone()
+    y = torch.empty_like(x)
+    ids = torch.zeros((tokens, K), dtype=torch.int32, device=dev)
+    wts = torch.zeros((tokens, K), dtype=torch.float32, device=dev)
+    logits = torch.zeros((tokens, E), dtype=torch.float32, device=dev)
+    n_unique = torch.zeros(L, dtype=torch.int32, device=dev)
+
+    def one_pass():
+        x.copy_(x0)
+        for l in range(L):
+            lib.router_topk(x, gate[l], None, K, logits, ids, wts)
+            pf.forward(x, ids, wts, [harness.pools[l].dev_ptr], out=y, residual=x)
+            n_unique[l:l + 1].copy_(pf.n_unique)
+            x.copy_(y)
+
+    one_pass()                                   # warm-up
+    torch.cuda.synchronize(dev)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(passes):
+        one_pass()
+    b.record()
+    torch.cuda.synchronize(dev)
+    dt = a.elapsed_time(b) / 1000.0 / passes
+    uniq = n_unique.float()
+    fetched = float(uniq.sum()) * harness.layout.record_bytes
+    finite = bool(torch.isfinite(x.float()).all())
+    # grouped FFN alone, on the experts the last layer gathered (resident)
+    w13, s13, w2, s2 = pf.views
+    local = pf.inverse[:tokens * K].view(tokens, K).clone()
+    out = torch.empty_like(x)
+    g_dt = graph_time(dev, lambda r: lib.fp8_moe_forward(x0, local, wts, w13, s13, w2, s2, out,
+                                                         pf.ws, mode=2), 20)
+    n_last = int(n_unique[L - 1])
+    g_bytes = n_last * harness.layout.record_bytes + tokens * H * 2 * 2
+    g_flops = tokens * K * 2 * (2 * cfg.inter * H + H * cfg.inter)
+    del pf
+    return {
+        "workload": f"{tokens}-token prefill through {L} layers: router, distinct experts of "
+                    "the layer fetched once from the page-locked pool (device-side, no host "
+                    "sync), permute, grouped W8A8 FFN, unpermute with routing weights",
+        "tokens": tokens, "layers": L, "ms_per_pass": round(1e3 * dt, 3),
+        "tokens_per_s": round(tokens / dt, 1),
+        "distinct_experts_per_layer": round(float(uniq.mean()), 1),
+        "fetch_GBps_in_pass": round(fetched / dt / 1e9, 2),
+        "grouped_ffn": {"us": round(1e6 * g_dt, 2), "distinct_experts": n_last,
+                        "GBps": round(g_bytes / g_dt / 1e9, 1),
+                        "hbm_frac": round(g_bytes / g_dt / 1e9 / HBM_PEAK_GBS, 4),
+                        "TFLOPs": round(g_flops / g_dt / 1e12, 2),
+                        "fp8_dense_peak_TFLOPs": FP8_PEAK_TFLOPS},
+        "finite_output": finite,
+    }
+
+
+def resident_bench(lib, harness, batches=(1, 8, 32, 128), steps: int = 20, warmup: int = 3):
+    """All 40 x 256 expert records resident in HBM (30 GiB, no offload):
+    batched decode at B tokens per step, top-8 of a uniform router, the
+    non-expert stub per layer, the whole step in one hipGraph."""
+    import numpy as np
+    import torch
+    dev, cfg = harness.dev, harness.cfg
+    L, E, K, H, I = cfg.layers, cfg.n_experts, cfg.top_k, cfg.hidden, cfg.inter
+    lay = harness.layout
+    recs = [torch.empty((E, lay.record_bytes), dtype=torch.uint8, device=dev) for _ in range(L)]
+    for l in range(L):
+        recs[l].copy_(harness.pools[l].tensor, non_blocking=True)
+    torch.cuda.synchronize(dev)
+    views = [lay.views(r) for r in recs]
+    g = torch.Generator(device=dev).manual_seed(cfg.seed + 11)
+    gate = (torch.randn((L, E, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    out = {}
+    for B in batches:
+        x0 = torch.randn((B, H), generator=g, device=dev).to(torch.bfloat16)
+        x = x0.clone()
+        h = torch.empty_like(x)
+        ids = torch.zeros((L, B, K), dtype=torch.int32, device=dev)
+        wts = torch.zeros((L, B, K), dtype=torch.float32, device=dev)
+        logits = torch.zeros((B, E), dtype=torch.float32, device=dev)
+        ws = torch.empty(lib.fp8_moe_workspace(B, K, E, H, I), dtype=torch.uint8, device=dev)
+
+        def step(_r=0):
+            x.copy_(x0)
+            for l in range(L):
+                torch.mm(x, harness.w_stub[l], out=h)
+                lib.router_topk(h, gate[l], None, K, logits, ids[l], wts[l])
+                lib.fp8_moe_forward(h, ids[l], wts[l], *views[l], x, ws, residual=h)
+
+        s = torch.cuda.Stream(device=dev)
+        s.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(s):
+            step()
+        torch.cuda.current_stream(dev).wait_stream(s)
+        torch.cuda.synchronize(dev)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        for _ in range(warmup):
+            graph.replay()
+        torch.cuda.synchronize(dev)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            graph.replay()
+        b.record()
+        torch.cuda.synchronize(dev)
+        dt = a.elapsed_time(b) / 1000.0 / steps
+        distinct = np.array([np.unique(ids[l].cpu().numpy()).size for l in range(L)])
+        wbytes = float(distinct.sum()) * lay.record_bytes
+        flops = L * B * K * 2 * (2 * I * H + H * I)
+        out[str(B)] = {"tokens_per_s": round(B / dt, 1), "ms_per_step": round(1e3 * dt, 4),
+                       "distinct_experts_per_layer": round(float(distinct.mean()), 1),
+                       "expert_GBps": round(wbytes / dt / 1e9, 1),
+                       "expert_TFLOPs": round(flops / dt / 1e12, 3),
+                       "kernels": "GEMV" if B <= 2 else "grouped",
+                       "finite_output": bool(torch.isfinite(x.float()).all())}
+        del graph
+    del recs, views
+    torch.cuda.empty_cache()
+    return {"workload": f"all {L}x{E} expert records resident in HBM ({L * E * lay.record_bytes / 2**30:.1f} GiB), "
+                        "batched decode, uniform top-8 router, bf16 2048x2048 stub per layer, "
+                        "whole step in one hipGraph; expert_GBps counts each distinct expert's "
+                        "record once per layer",
+            "batches": out}
 
 
 def fill_pool_bytes(pool, dev, seed: int, chunk: int = 64) -> None:
@@ -307,6 +417,8 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--noncoherent-pool", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the prefill and all-resident measurements")
     ap.add_argument("--probe", choices=["gemv", "fetch"],
                     help="time one kernel alone (--steps launches) instead of the decode step")
     args = ap.parse_args()
@@ -352,7 +464,7 @@ def main() -> int:
     log("standalone kernel timing")
     link = link_peak(pools, dev)
     f_dt, f_bytes = fetch_standalone(lib, pools, dev)
-    g_dt, g_bytes = gemv_standalone(lib, hc)
+    g_dt, g_bytes = gemv_resident(lib, dev, hc.layout)
     fetch_gbs = f_bytes / f_dt / 1e9
     gemv_gbs = g_bytes / g_dt / 1e9
     log(f"link (copy engine) {link:.2f} GB/s; fetch {fetch_gbs:.2f} GB/s "
@@ -375,6 +487,18 @@ def main() -> int:
     dt0 = timed_replays(h0c, args.steps)
     tps_nocache = args.steps / dt0
     log(f"0% hit: {tps_nocache:.2f} tok/s, {1e3 * dt0 / args.steps:.3f} ms/step")
+
+    prefill = resident = None
+    if not args.no_extra:
+        log("prefill (512 tokens, 40 layers)")
+        prefill = prefill_bench(lib, h0c)
+        log(f"prefill: {prefill['tokens_per_s']} tok/s, {prefill['ms_per_pass']} ms/pass, "
+            f"{prefill['distinct_experts_per_layer']} experts/layer, grouped FFN "
+            f"{prefill['grouped_ffn']['us']} us")
+        log("all-resident batched decode")
+        resident = resident_bench(lib, h0c)
+        log("resident: " + ", ".join(f"B={b}: {v['tokens_per_s']} tok/s"
+                                     for b, v in resident["batches"].items()))
 
     miss_bytes_per_step = misses / args.steps * pools[0].layout.record_bytes
     result = {
@@ -418,7 +542,9 @@ def main() -> int:
             "launch_us": round(1e6 * f_dt, 2),
         },
         "roofline_gemv": {
-            "kernel": "moe gateup_gemv_kernel + down_gemv_kernel (8 experts, 1 token)",
+            "kernel": "moe gateup_gemv_kernel + down_gemv_kernel (8 experts, 1 token; "
+                      "25,180,160 B per call; 200 back-to-back calls in a hipGraph over "
+                      "2048 resident records)",
             "bound": "hbm",
             "achieved": round(gemv_gbs, 2),
             "peak": HBM_PEAK_GBS,
@@ -428,6 +554,8 @@ def main() -> int:
             "call_us": round(1e6 * g_dt, 3),
         },
         "cpu_baseline": cpu,
+        "prefill": prefill,
+        "all_resident": resident,
         "finite_output": x_ok,
         "wall_s": round(time.perf_counter() - t_start, 1),
     }

@@ -1,32 +1,37 @@
 // Token -> expert grouping (permute), its inverse (unpermute), and the
 // torch.unique-style renumbering the reference uses for its gathered subsets.
 //
-// permute: one workgroup of 1024 threads, O(pairs) work:
+// permute: one workgroup, O(pairs) work, stable and deterministic:
 //   1. histogram of expert ids in LDS (atomic adds; counts do not depend on
 //      the order they land in);
 //   2. block-wide exclusive scan -> offsets, and a cursor per expert;
-//   3. every pair claims a position inside its expert's segment with an LDS
-//      atomic (arbitrary order within the segment at this point);
-//   4. each thread insertion-sorts the segments of its experts by pair index
-//      (segments are short and already nearly sorted), which restores the
-//      stable order, then writes the inverse map.
-// The result equals a stable sort by expert, identically on every run, and
-// no memory has to be cleared beforehand (nothing to memset in a graph).
+//   3. pairs are placed in rounds of 512 in pair order.  In a round, each
+//      wave ranks its lanes among the lanes with the same expert (ballot
+//      matching, one pass per distinct expert in the wave), the per-wave
+//      counts of an expert are packed as 7-bit fields of one 64-bit LDS word
+//      (8 waves x at most 64), so a lane's position is
+//        cursor[e] + (counts of e in earlier waves) + (rank in its wave)
+//      -- exactly its rank in a stable sort -- and the expert's cursor then
+//      advances by the round's total.
+// No memory has to be cleared beforehand (nothing to memset in a graph).
 #include "common.hpp"
 #include "grouped.hpp"
 
 namespace moe {
 
-constexpr int kPermThreads = 1024;
+constexpr int kPermThreads = 1024;     // unique_inverse
 constexpr int kPermMaxExperts = 4096;
 constexpr int kPermPer = kPermMaxExperts / kPermThreads;
+constexpr int kPlaceThreads = 512;     // permute: 8 waves, 7-bit count fields in a uint64
+constexpr int kPlacePer = kPermMaxExperts / kPlaceThreads;
 
 __device__ __forceinline__ int32_t read_id(const void* ids, int ids64, int64_t p) {
   return ids64 ? static_cast<int32_t>(reinterpret_cast<const int64_t*>(ids)[p])
                : reinterpret_cast<const int32_t*>(ids)[p];
 }
 
-// Exclusive scan over kPermThreads values, returns the total.
+// Exclusive scan over the NW * 64 threads' values, returns the total.
+template <int NW>
 __device__ int32_t block_exclusive_scan(int32_t v, int32_t* scratch, int32_t* out_prefix) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int32_t incl = v;
@@ -37,16 +42,16 @@ __device__ int32_t block_exclusive_scan(int32_t v, int32_t* scratch, int32_t* ou
   }
   if (lane == 63) scratch[wave] = incl;
   __syncthreads();
-  if (tid < 16) {
+  if (tid < NW) {
     int32_t w = scratch[tid];
     int32_t wi = w;
 #pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
+    for (int o = 1; o < NW; o <<= 1) {
       int32_t n = __shfl_up(wi, o, 64);
       if (tid >= o) wi += n;
     }
     scratch[16 + tid] = wi - w;    // exclusive wave offsets
-    if (tid == 15) scratch[32] = wi;
+    if (tid == NW - 1) scratch[32] = wi;
   }
   __syncthreads();
   *out_prefix = scratch[16 + wave] + incl - v;
@@ -55,69 +60,95 @@ __device__ int32_t block_exclusive_scan(int32_t v, int32_t* scratch, int32_t* ou
   return total;
 }
 
-__global__ __launch_bounds__(kPermThreads) void permute_kernel(
+__global__ __launch_bounds__(kPlaceThreads) void permute_kernel(
     const void* __restrict__ ids, int ids64, int64_t P, int32_t n_experts,
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ sorted_pairs,
     int32_t* __restrict__ pair_pos) {
-  __shared__ int32_t cnt[kPermMaxExperts];
+  __shared__ int32_t cursor[kPermMaxExperts];
+  __shared__ uint64_t fields[kPermMaxExperts];
   __shared__ int32_t scratch[40];
   const int tid = threadIdx.x;
-  for (int e = tid; e < n_experts; e += kPermThreads) cnt[e] = 0;
-  __syncthreads();
-  for (int64_t p = tid; p < P; p += kPermThreads) {
-    const int32_t e = read_id(ids, ids64, p);
-    if (e >= 0 && e < n_experts) atomicAdd(&cnt[e], 1);
+  const int lane = tid & 63, wave = tid >> 6;
+  for (int e = tid; e < n_experts; e += kPlaceThreads) {
+    cursor[e] = 0;
+    fields[e] = 0;
   }
   __syncthreads();
-  // thread t owns the contiguous experts [t*PER, t*PER + PER)
-  int32_t mine[kPermPer];
+  for (int64_t p = tid; p < P; p += kPlaceThreads) {
+    const int32_t e = read_id(ids, ids64, p);
+    if (e >= 0 && e < n_experts) atomicAdd(&cursor[e], 1);
+  }
+  __syncthreads();
+  // thread t owns the contiguous experts [t*PER, t*PER + PER) for the scan
+  int32_t mine[kPlacePer];
   int32_t sum = 0;
 #pragma unroll
-  for (int j = 0; j < kPermPer; ++j) {
-    const int x = tid * kPermPer + j;
-    mine[j] = x < n_experts ? cnt[x] : 0;
+  for (int j = 0; j < kPlacePer; ++j) {
+    const int x = tid * kPlacePer + j;
+    mine[j] = x < n_experts ? cursor[x] : 0;
     sum += mine[j];
   }
   int32_t base;
-  const int32_t total = block_exclusive_scan(sum, scratch, &base);
-  int32_t seg[kPermPer];
+  const int32_t total = block_exclusive_scan<kPlaceThreads / 64>(sum, scratch, &base);
 #pragma unroll
-  for (int j = 0; j < kPermPer; ++j) {
-    const int x = tid * kPermPer + j;
-    seg[j] = base;
+  for (int j = 0; j < kPlacePer; ++j) {
+    const int x = tid * kPlacePer + j;
     if (x < n_experts) {
       counts[x] = mine[j];
       offsets[x] = base;
-      cnt[x] = base;              // becomes the placement cursor
+      cursor[x] = base;            // becomes the placement cursor
     }
     base += mine[j];
   }
   if (tid == 0) offsets[n_experts] = total;
   __syncthreads();
-  for (int64_t p = tid; p < P; p += kPermThreads) {
-    const int32_t e = read_id(ids, ids64, p);
-    if (e >= 0 && e < n_experts) {
-      const int32_t pos = atomicAdd(&cnt[e], 1);
-      sorted_pairs[pos] = static_cast<int32_t>(p);
-    } else {
-      pair_pos[p] = -1;           // no such expert: no position
-    }
-  }
-  __threadfence_block();
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < kPermPer; ++j) {
-    const int32_t lo = seg[j], hi = seg[j] + mine[j];
-    for (int32_t i = lo + 1; i < hi; ++i) {      // insertion sort, nearly sorted input
-      const int32_t v = sorted_pairs[i];
-      int32_t k = i - 1;
-      while (k >= lo && sorted_pairs[k] > v) {
-        sorted_pairs[k + 1] = sorted_pairs[k];
-        --k;
+  const uint64_t below_lane = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int64_t r0 = 0; r0 < P; r0 += kPlaceThreads) {
+    const int64_t p = r0 + tid;
+    int32_t e = -1;
+    if (p < P) {
+      e = read_id(ids, ids64, p);
+      if (e < 0 || e >= n_experts) {
+        pair_pos[p] = -1;          // no such expert: no position
+        e = -1;
       }
-      sorted_pairs[k + 1] = v;
     }
-    for (int32_t i = lo; i < hi; ++i) pair_pos[sorted_pairs[i]] = i;
+    // rank among the lanes of this wave with the same expert
+    int rank = 0, wcount = 0;
+    uint64_t todo = __ballot(e >= 0);
+    while (todo) {
+      const int leader = __builtin_ctzll(todo);
+      const int32_t el = __shfl(e, leader, 64);
+      const uint64_t m = __ballot(e == el);
+      if (e == el) {
+        rank = __popcll(m & below_lane);
+        wcount = __popcll(m);
+      }
+      todo &= ~m;
+    }
+    const bool first = e >= 0 && rank == 0;     // one lane per (wave, expert)
+    if (first) atomicAdd(reinterpret_cast<unsigned long long*>(&fields[e]),
+                         static_cast<unsigned long long>(wcount) << (7 * wave));
+    __syncthreads();
+    uint64_t f = 0;
+    if (e >= 0) {
+      f = fields[e];
+      int32_t before = 0;
+      for (int w = 0; w < wave; ++w) before += static_cast<int32_t>((f >> (7 * w)) & 0x7f);
+      const int32_t pos = cursor[e] + before + rank;
+      sorted_pairs[pos] = static_cast<int32_t>(p);
+      pair_pos[p] = pos;
+    }
+    __syncthreads();
+    // the lowest wave holding expert e advances its cursor and clears its word
+    if (first && (f & ((1ull << (7 * wave)) - 1ull)) == 0ull) {
+      int32_t tot = 0;
+#pragma unroll
+      for (int w = 0; w < kPlaceThreads / 64; ++w) tot += static_cast<int32_t>((f >> (7 * w)) & 0x7f);
+      cursor[e] += tot;
+      fields[e] = 0;
+    }
+    __syncthreads();
   }
 }
 
@@ -134,7 +165,7 @@ __global__ __launch_bounds__(kPermThreads) void unique_inverse_kernel(
     const int x = tid + j * kPermThreads;
     const int32_t present = (x < n_experts && counts[x] > 0) ? 1 : 0;
     int32_t pre;
-    int32_t tot = block_exclusive_scan(present, scratch, &pre);
+    int32_t tot = block_exclusive_scan<kPermThreads / 64>(present, scratch, &pre);
     if (x < n_experts) {
       const int32_t r = present ? base + pre : -1;
       srank[x] = r;
@@ -192,9 +223,57 @@ __global__ __launch_bounds__(256) void unpermute_kernel(const float* __restrict_
   for (int i = 0; i < 4; ++i) o[i] = v[i];
 }
 
+// Hybrid prefill gather plan: the distinct experts uniq[0..n) of a call are
+// split between those resident in the device cache (copied device to device
+// from their slot) and the rest (fetched from the host pool), both lists in
+// uniq order.  The table is only read: no stamp, no insert.  One wave; the
+// lists are compacted with ballots, so the result is deterministic.
+__global__ __launch_bounds__(64) void gather_plan_kernel(
+    const int32_t* __restrict__ uniq, const int32_t* __restrict__ n_unique,
+    const int32_t* slot_of, int32_t n_experts, int32_t cap,
+    int32_t* __restrict__ host_expert, int32_t* __restrict__ host_dst, int32_t* __restrict__ n_host,
+    int32_t* __restrict__ cache_src, int32_t* __restrict__ cache_dst,
+    int32_t* __restrict__ n_cache, int64_t* __restrict__ stats) {
+  const int lane = threadIdx.x;
+  const int n = min(max(*n_unique, 0), n_experts);
+  int nh = 0, nc = 0;
+  for (int base = 0; base < n; base += 64) {
+    const int i = base + lane;
+    const int32_t e = i < n ? uniq[i] : -1;
+    const bool valid = e >= 0 && e < n_experts;
+    const int32_t s = valid && slot_of ? slot_of[e] : -1;   // no cache: all from host
+    const bool cached = valid && s >= 0 && s < cap;
+    const bool host = valid && !cached;
+    const uint64_t mc = __ballot(cached);
+    const uint64_t mh = __ballot(host);
+    const int rc = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mc >> 32),
+                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mc), 0));
+    const int rh = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mh >> 32),
+                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mh), 0));
+    if (cached) {
+      cache_src[nc + rc] = s;
+      cache_dst[nc + rc] = i;
+    }
+    if (host) {
+      host_expert[nh + rh] = e;
+      host_dst[nh + rh] = i;
+    }
+    nc += __popcll(mc);
+    nh += __popcll(mh);
+  }
+  if (lane == 0) {
+    *n_host = nh;
+    *n_cache = nc;
+    if (stats) {
+      stats[0] += nc;
+      stats[1] += nh;
+    }
+  }
+}
+
 int launch_permute(const void* ids, int ids64, int64_t P, int32_t n_experts, int32_t* counts,
                    int32_t* offsets, int32_t* sorted_pairs, int32_t* pair_pos, hipStream_t s) {
-  hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(kPermThreads), 0, s, ids, ids64, P, n_experts,
+  hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(kPlaceThreads), 0, s, ids, ids64, P, n_experts,
                      counts, offsets, sorted_pairs, pair_pos);
   return check_launch("moe_permute");
 }
@@ -253,4 +332,21 @@ extern "C" int moe_unpermute(const float* y, const int32_t* pair_pos, const void
   if (tokens == 0) return MOE_OK;
   return launch_unpermute(y, pair_pos, weights, w_dtype == MOE_BF16 ? 1 : 0, tokens, top_k,
                           hidden, nullptr, static_cast<uint16_t*>(out), as_stream(stream));
+}
+
+extern "C" int moe_gather_plan(const int32_t* uniq, const int32_t* n_unique,
+                               const int32_t* slot_of, int32_t n_experts, int32_t cap,
+                               int32_t* host_expert, int32_t* host_dst, int32_t* n_host,
+                               int32_t* cache_src, int32_t* cache_dst, int32_t* n_cache,
+                               int64_t* stats, void* stream) {
+  MOE_REQUIRE(uniq && n_unique && host_expert && host_dst && n_host && cache_src && cache_dst &&
+                  n_cache, "moe_gather_plan: NULL pointer");
+  MOE_REQUIRE(n_experts >= 1 && n_experts <= kPermMaxExperts,
+              "moe_gather_plan: need 1 <= n_experts <= %d", kPermMaxExperts);
+  MOE_REQUIRE(cap >= 0 && (cap == 0 || slot_of), "moe_gather_plan: cap > 0 needs slot_of");
+  if (cap == 0) slot_of = nullptr;   // no device cache: every expert from the host
+  hipLaunchKernelGGL(gather_plan_kernel, dim3(1), dim3(64), 0, as_stream(stream), uniq, n_unique,
+                     slot_of, n_experts, cap, host_expert, host_dst, n_host, cache_src, cache_dst,
+                     n_cache, stats);
+  return check_launch("moe_gather_plan");
 }

@@ -43,6 +43,13 @@ _BACKEND_NOTED = False
 # ~128 KiB of host reads in flight, the link's bandwidth-delay product.
 CPP_BLOCKS_PER_JOB = 2
 _dev_ptr_cache: dict[int, int] = {}
+# Multi-token calls on a layer with a device cache: False keeps the
+# reference's dispatch to offload.offloaded_forward (host unique, per-expert
+# copies); True runs prefill.DevicePrefill instead -- distinct experts, the
+# hybrid cache/host gather (when offload.HYBRID_GATHER) and the grouped
+# kernels all on the device, no host sync.  Outputs are identical.
+DEVICE_PREFILL = False
+_prefill = None
 
 
 def init_dev_cache(experts, device: torch.device, capacity: int) -> None:
@@ -166,11 +173,43 @@ def dev_resolve_and_fetch(experts, topk_ids: torch.Tensor) -> torch.Tensor:
     return experts._dc_out[:k]
 
 
+def _device_prefill(self, x, topk_ids, topk_weights):
+    """A multi-token call on the device: prefill.DevicePrefill over this
+    layer's host buffers, reading the layer's cache for the hybrid gather.
+    One set of gather buffers is shared by every layer (calls are ordered on
+    one stream) and regrown when a call needs more tokens."""
+    global _prefill
+    import offload
+    from prefill import DevicePrefill
+    offload._count(getattr(self, "_layer_index", -1), topk_ids)
+    offload.TRACE.add(getattr(self, "_layer_index", -1), topk_ids)
+    lib = hipfetch.require()
+    T, K = topk_ids.shape
+    p = _prefill
+    if (p is None or p.max_tokens < T or p.K != K or p.dev != x.device
+            or [g.shape[1:] for g in p.gather] != [h.shape[1:] for h in
+                                                    (self.w13_weight, self.w2_weight,
+                                                     self.w13_scale_inv, self.w2_scale_inv)]
+            or p.E != self.num_experts):
+        _prefill = p = None
+        p = DevicePrefill.for_experts(self, K, max(T, 512), x.device)
+        _prefill = p
+    pairs = _copy_pairs(self)
+    host_src = [_device_ptr(lib, host) for host, _ in pairs]
+    cache = None
+    if offload.HYBRID_GATHER and getattr(self, "_dc_cap", 0):
+        cache = (self._dc_slot_of, self._dc_cap, [c.data_ptr() for _, c in pairs])
+    return p.forward(x, topk_ids, topk_weights, host_src, cache)
+
+
 def dev_cached_forward(self, x, topk_ids, topk_weights):
     """MoEExperts.forward using the device-resident cache (bin/devcache.py:258-277).
-    Decode only; other calls go to the gather path."""
+    Decode only; other calls go to the gather path (on the device when
+    DEVICE_PREFILL)."""
     import offload
     if topk_ids.shape[0] != 1 or not getattr(self, "_dc_cap", 0):
+        if DEVICE_PREFILL and getattr(self, "_dc_cap", 0) and x.is_cuda:
+            return _device_prefill(self, x, topk_ids, topk_weights)
         return offload.offloaded_forward(self, x, topk_ids, topk_weights)
     slots = dev_resolve_and_fetch(self, topk_ids)
     return fp8_moe_forward(x, slots.reshape(topk_ids.shape), topk_weights, self._dc_w13,

@@ -65,6 +65,8 @@ SIGNATURES = {
     "moe_permute": (C.c_int, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
     "moe_unpermute": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp]),
     "moe_unique_inverse": (C.c_int, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "moe_gather_plan": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                  _vp]),
 }
 
 
@@ -219,6 +221,14 @@ class Native:
             ids.data_ptr(), self._dtype_code(ids), T, K, n_experts, counts.data_ptr(),
             n_unique.data_ptr(), uniq.data_ptr(), rank_of.data_ptr(), inverse.data_ptr(),
             self.stream()), "moe_unique_inverse")
+
+    def gather_plan(self, uniq, n_unique, slot_of, cap: int, host_expert, host_dst, n_host,
+                    cache_src, cache_dst, n_cache, stats=None) -> None:
+        self._check(self.cdll.moe_gather_plan(
+            uniq.data_ptr(), n_unique.data_ptr(), self._ptr(slot_of), uniq.numel(), cap,
+            host_expert.data_ptr(), host_dst.data_ptr(), n_host.data_ptr(), cache_src.data_ptr(),
+            cache_dst.data_ptr(), n_cache.data_ptr(), self._ptr(stats), self.stream()),
+            "moe_gather_plan")
 
     def unpermute(self, y, pair_pos, weights, out) -> None:
         T, K = weights.shape

@@ -232,6 +232,25 @@ int moe_unique_inverse(const void* ids, int32_t ids_dtype, int32_t tokens,
                        int32_t* n_unique, int32_t* uniq, int32_t* rank_of,
                        int32_t* inverse, void* stream);
 
+/* Hybrid prefill gather plan.  The distinct experts uniq[0..*n_unique) of a
+ * multi-token call (from moe_unique_inverse) are split between the device
+ * cache and the host pool: expert e = uniq[i] with 0 <= slot_of[e] < cap is
+ * queued as (cache_src = slot_of[e], cache_dst = i), every other expert as
+ * (host_expert = e, host_dst = i), both lists in uniq order; counts go to
+ * n_host[1] and n_cache[1].  Two moe_fetch launches then fill gather slot i
+ * from the cache slot (device to device) or from the host record.  The table
+ * is only read -- no insert, no stamp -- so prefill never evicts the decode
+ * working set.  cap == 0 (slot_of may be NULL) sends every expert to the
+ * host list.  stats (nullable) int64[2] accumulates {cache copies, host
+ * copies}.  Replaces the host loop of the reference's hybrid gather
+ * (bin/offload.py:195-224), which needs slot_of.cpu() and a per-expert copy.
+ * Lists need n_experts entries each; 1 <= n_experts <= 4096. */
+int moe_gather_plan(const int32_t* uniq, const int32_t* n_unique,
+                    const int32_t* slot_of, int32_t n_experts, int32_t cap,
+                    int32_t* host_expert, int32_t* host_dst, int32_t* n_host,
+                    int32_t* cache_src, int32_t* cache_dst, int32_t* n_cache,
+                    int64_t* stats, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

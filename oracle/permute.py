@@ -68,3 +68,22 @@ def unpermute(y_perm, pair_pos, weights, top_k: int):
     for k in range(top_k):
         out += w[:, k:k + 1] * y[pos[:, k]]
     return out
+
+
+def gather_plan(uniq, slot_of, cap: int):
+    """Hybrid prefill gather (bin/offload.py:195-224): for i, e in
+    enumerate(uniq), a resident expert (slot_of[e] >= 0, i.e. in [0, cap))
+    is copied from its cache slot into gather row i, any other expert from
+    its host record.  Returns (host_expert, host_dst, cache_src, cache_dst),
+    each in uniq order; the table is not modified."""
+    host_e, host_d, cache_s, cache_d = [], [], [], []
+    for i, e in enumerate(int(v) for v in np.asarray(uniq).reshape(-1)):
+        s = int(slot_of[e]) if slot_of is not None else -1
+        if 0 <= s < cap:
+            cache_s.append(s)
+            cache_d.append(i)
+        else:
+            host_e.append(e)
+            host_d.append(i)
+    as32 = lambda v: np.array(v, np.int32)      # noqa: E731
+    return as32(host_e), as32(host_d), as32(cache_s), as32(cache_d)

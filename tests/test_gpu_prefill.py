@@ -1,0 +1,141 @@
+"""Device-side prefill gather on the GPU: the gather plan against the
+oracle, gathered bytes against the host records, hybrid (cache + host) equal
+to host-only byte for byte, and the MoE output through the device path equal
+to the reference-form gather path (bin/offload.py:137-239) bit for bit."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import say
+from oracle import permute as op
+
+pytestmark = pytest.mark.gpu
+E, H, I, K = 64, 2048, 512, 8
+
+
+def test_gather_plan_matches_oracle(lib, dev):
+    rng = np.random.default_rng(3)
+    for n_uniq, cap in ((37, 20), (64, 64), (5, 0), (64, 1)):
+        uniq = np.sort(rng.choice(E, n_uniq, replace=False)).astype(np.int32)
+        slot_of = np.full(E, -1, np.int32)
+        if cap:
+            res = rng.choice(E, min(cap, E), replace=False)
+            slot_of[res] = rng.permutation(cap)[:res.size]
+        say(f"gather plan: {n_uniq} experts, cap {cap}")
+        t = lambda a: torch.from_numpy(a).to(dev)      # noqa: E731
+        u = torch.full((E,), -7, dtype=torch.int32, device=dev)
+        u[:n_uniq] = t(uniq)
+        n = torch.tensor([n_uniq], dtype=torch.int32, device=dev)
+        bufs = [torch.full((E,), -9, dtype=torch.int32, device=dev) for _ in range(4)]
+        nh = torch.zeros(1, dtype=torch.int32, device=dev)
+        nc = torch.zeros(1, dtype=torch.int32, device=dev)
+        stats = torch.zeros(2, dtype=torch.int64, device=dev)
+        so = t(slot_of) if cap else None
+        lib.gather_plan(u, n, so, cap, bufs[0], bufs[1], nh, bufs[2], bufs[3], nc, stats)
+        torch.cuda.synchronize()
+        he, hd, cs, cd = op.gather_plan(uniq, slot_of if cap else None, cap)
+        assert int(nh) == he.size and int(nc) == cs.size
+        for got, want in zip(bufs, (he, hd, cs, cd)):
+            assert np.array_equal(got[:want.size].cpu().numpy(), want)
+        assert stats.tolist() == [cs.size, he.size]
+        if cap:
+            assert np.array_equal(so.cpu().numpy(), slot_of)     # read only
+
+
+@pytest.fixture(scope="module")
+def layer(dev):
+    """E experts in page-locked host buffers (reference layout) and the same
+    experts resident on the GPU."""
+    import moe
+    import synth
+    ref = moe.MoEExperts(E, H, I, device=dev)
+    synth.fill_experts(ref, seed=5, recipe="devtest")
+    host = moe.MoEExperts(E, H, I, device="cpu")
+    for n in ("w13_weight", "w2_weight", "w13_scale_inv", "w2_scale_inv"):
+        setattr(host, n, getattr(ref, n).cpu().pin_memory())
+    return ref, host
+
+
+def _routing(T, seed, dev):
+    rng = np.random.default_rng(seed)
+    ids = torch.tensor(np.stack([rng.choice(E, K, replace=False) for _ in range(T)]), device=dev)
+    w = torch.rand((T, K), generator=torch.Generator().manual_seed(seed)).to(dev)
+    return ids, w / w.sum(-1, keepdim=True)
+
+
+def test_device_prefill_equals_resident_and_gathers_exact_bytes(lib, dev, layer):
+    import devcache
+    from fp8_moe import fp8_moe_forward
+    from prefill import DevicePrefill
+    ref, host = layer
+    T = 55
+    x = torch.randn((T, H), device=dev).to(torch.bfloat16)
+    ids, w = _routing(T, 1, dev)
+    pf = DevicePrefill.for_experts(host, K, 64, dev)
+    src = [devcache._device_ptr(lib, getattr(host, n)) for n in
+           ("w13_weight", "w2_weight", "w13_scale_inv", "w2_scale_inv")]
+    say("prefill: host-only gather")
+    got = pf.forward(x, ids, w, src)
+    want = fp8_moe_forward(x, ids, w, ref.w13_weight, ref.w13_scale_inv, ref.w2_weight,
+                           ref.w2_scale_inv)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    uniq = torch.unique(ids).cpu()
+    n = int(pf.n_unique)
+    assert n == uniq.numel() and torch.equal(pf.uniq[:n].cpu(), uniq.to(torch.int32))
+    assert torch.equal(pf.gather[0][:n].view(torch.uint8).cpu(),
+                       host.w13_weight.view(torch.uint8)[uniq])
+    assert torch.equal(pf.gather[3][:n].cpu(), host.w2_scale_inv[uniq])
+
+
+def test_hybrid_gather_equals_host_gather(lib, dev, layer):
+    import devcache
+    from prefill import DevicePrefill
+    ref, host = layer
+    devcache.init_dev_cache(host, dev, 24)
+    for s in range(6):                       # populate the cache through decode calls
+        devcache.dev_resolve_and_fetch(host, _routing(1, 100 + s, dev)[0])
+    torch.cuda.synchronize()
+    table_before = (host._dc_slot_of.clone(), host._dc_stamp.clone(), host._dc_step.clone())
+    T = 40
+    x = torch.randn((T, H), device=dev).to(torch.bfloat16)
+    ids, w = _routing(T, 2, dev)
+    pairs = devcache._copy_pairs(host)
+    src = [devcache._device_ptr(lib, h) for h, _ in pairs]
+    a = DevicePrefill.for_experts(host, K, 64, dev)
+    b = DevicePrefill.for_experts(host, K, 64, dev)
+    say("prefill: hybrid vs host-only gather")
+    out_a = a.forward(x, ids, w, src)
+    out_b = b.forward(x, ids, w, src, cache=(host._dc_slot_of, host._dc_cap,
+                                             [c.data_ptr() for _, c in pairs]))
+    torch.cuda.synchronize()
+    n = int(a.n_unique)
+    for ga, gb in zip(a.gather, b.gather):
+        assert torch.equal(ga[:n].view(torch.uint8), gb[:n].view(torch.uint8))
+    assert torch.equal(out_a, out_b)
+    resident = int((host._dc_slot_of[a.uniq[:n].long()] >= 0).sum())
+    assert b.copy_stats() == (resident, n - resident) and resident > 0
+    for t0, t1 in zip(table_before, (host._dc_slot_of, host._dc_stamp, host._dc_step)):
+        assert torch.equal(t0, t1)               # the table is only read
+
+
+def test_dev_cached_forward_device_prefill_equals_reference_form(lib, dev, layer):
+    import devcache
+    import offload
+    ref, host = layer
+    devcache.init_dev_cache(host, dev, 16)
+    devcache.dev_resolve_and_fetch(host, _routing(1, 7, dev)[0])
+    T = 33
+    x = torch.randn((T, H), device=dev).to(torch.bfloat16)
+    ids, w = _routing(T, 3, dev)
+    assert devcache.DEVICE_PREFILL is False
+    say("prefill: dev_cached_forward, reference-form then device path")
+    want = devcache.dev_cached_forward(host, x, ids, w)
+    devcache.DEVICE_PREFILL = True
+    try:
+        got = devcache.dev_cached_forward(host, x, ids, w)
+    finally:
+        devcache.DEVICE_PREFILL = False
+    torch.cuda.synchronize()
+    assert offload.HYBRID_GATHER
+    assert torch.equal(got, want)

@@ -52,3 +52,24 @@ def test_fetch_pattern_and_expected_cache():
     assert fetch.which_expert(after[2]) == 9 and fetch.which_expert(after[0]) == 3
     assert np.all(after[1] == -1) and np.all(after[3] == -1)     # surplus job retired
     assert fetch.EXPERT_BYTES == 2 * 512 * 2048 + 2048 * 512 + 8 * 16 * 4 + 16 * 4 * 4
+
+
+def test_gather_plan_reads_the_table_only_and_covers_every_expert():
+    """Every distinct expert lands in exactly one list at its own gather row;
+    resident ones name their slot; the table is unchanged."""
+    from oracle import permute as op
+    rng = np.random.default_rng(4)
+    E, C = 256, 40
+    slot_of = np.full(E, -1, np.int32)
+    resident = rng.choice(E, C, replace=False)
+    slot_of[resident] = rng.permutation(C)
+    before = slot_of.copy()
+    uniq = np.unique(rng.integers(0, E, 300))
+    he, hd, cs, cd = op.gather_plan(uniq, slot_of, C)
+    assert np.array_equal(slot_of, before)
+    assert sorted(np.concatenate([hd, cd]).tolist()) == list(range(uniq.size))
+    assert all(slot_of[uniq[d]] == s for s, d in zip(cs, cd))
+    assert all(slot_of[e] < 0 and uniq[d] == e for e, d in zip(he, hd))
+    assert cs.size == np.isin(uniq, resident).sum()
+    he0, hd0, cs0, _ = op.gather_plan(uniq, None, 0)
+    assert np.array_equal(he0, uniq) and cs0.size == 0
