@@ -31,6 +31,12 @@ sys.path.insert(0, str(ROOT / "drama3-offloading_amd"))
 METRIC = "decode tokens/s (40-layer MoE, bs=1) at 0%/~60% hit; fetch GB/s; %HBM peak"
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0      # dense e4m3 MFMA, MI355X
+# HBM traffic per launch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes
+# over `--probe fetch|gemv`, scaled by the same counters on a plain copy of
+# known size (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); the passes and the
+# calibration are recorded in profiles/hbm_traffic.md.
+TRAFFIC_FETCH_BYTES = (24630 + 24582) * 1024          # host reads + HBM writes, 8 records
+TRAFFIC_GEMV_BYTES = (16686 + 8578 + 32 + 4) * 1024   # gate/up + down, 8 experts x 1 token
 PCIE5_X16_GBS = 64.0
 
 
@@ -372,6 +378,23 @@ def run_probe(args) -> int:
                "bytes_per_launch": nbytes, "GBps": round(nbytes / dt / 1e9, 3)}
         for p in pools:
             p.close()
+    elif args.probe == "copy":
+        # a plain elementwise copy of known size: reads and writes 256 MiB,
+        # the calibration for the HBM traffic counters
+        n = 64 << 20
+        src = torch.rand(n, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(args.steps):
+            torch.mul(src, 1.0, out=dst)
+        b.record()
+        torch.cuda.synchronize()
+        dt = a.elapsed_time(b) / 1000.0 / args.steps
+        res = {"probe": "copy", "what": "torch.mul(src, 1.0, out=dst) over 64 Mi float32",
+               "bytes_read": 4 * n, "bytes_written": 4 * n, "us_per_launch": round(1e6 * dt, 2),
+               "GBps": round(8 * n / dt / 1e9, 1)}
     else:
         raise SystemExit(f"unknown probe {args.probe!r}")
     print(json.dumps(res), flush=True)
@@ -419,7 +442,7 @@ def main() -> int:
     ap.add_argument("--noncoherent-pool", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the prefill and all-resident measurements")
-    ap.add_argument("--probe", choices=["gemv", "fetch"],
+    ap.add_argument("--probe", choices=["gemv", "fetch", "copy"],
                     help="time one kernel alone (--steps launches) instead of the decode step")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -538,7 +561,9 @@ def main() -> int:
             "published_link_peak": PCIE5_X16_GBS,
             "unit": "GB/s",
             "frac": round(fetch_gbs / link, 4),
-            "traffic": None,
+            "traffic": TRAFFIC_FETCH_BYTES,
+            "traffic_note": "bytes per launch (host reads + HBM writes), PMC, algorithmic "
+                            "50,343,936",
             "launch_us": round(1e6 * f_dt, 2),
         },
         "roofline_gemv": {
@@ -550,7 +575,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": TRAFFIC_GEMV_BYTES,
+            "traffic_note": "HBM bytes per call, PMC, algorithmic 25,180,160",
             "call_us": round(1e6 * g_dt, 3),
         },
         "cpu_baseline": cpu,
