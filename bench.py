@@ -410,9 +410,14 @@ def cpu_baseline(harness, budget_s: float):
     bias = harness.bias_all[0].cpu()
     records = [p.tensor for p in harness.pools]
     x0 = harness.x0.float().cpu()
-    threads = torch.get_num_threads()
+    torch.set_num_threads(os.cpu_count() or 1)
     sec_per_tok, layers_run, threads = cpu_moe.time_decode(w_stub, gate, bias, records,
                                                            harness.layout, x0, budget_s, cfg.top_k)
+    layer_all = cpu_moe.time_single_layer(x0, w_stub, gate, bias, records, harness.layout,
+                                          cfg.top_k, iters=20)
+    layer_one = cpu_moe.time_single_layer(x0, w_stub, gate, bias, records, harness.layout,
+                                          cfg.top_k, iters=20, threads=1)
+    gather = cpu_moe.time_gather(records[0], list(range(0, 256, 32)), iters=20)
     model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -426,7 +431,11 @@ def cpu_baseline(harness, budget_s: float):
             "sample": (f"{layers_run} layer evaluations ({layers_run / cfg.layers:.2f} tokens) of "
                        f"the same 40-layer decode step on the host cores: stub matmul, router, "
                        f"dequantise-then-matmul MoE reading the page-locked pool; float32 torch, "
-                       f"{threads} threads, os.cpu_count()={os.cpu_count()}, CPU '{model}'")}
+                       f"{threads} threads, os.cpu_count()={os.cpu_count()}, CPU '{model}'"),
+            "single_layer_ms_median": {"threads_all": round(1e3 * layer_all, 2),
+                                       "threads_1": round(1e3 * layer_one, 2),
+                                       "iters": 20},
+            "gather_8_records_ms_median": round(1e3 * gather, 3)}
 
 
 def main() -> int:

@@ -80,3 +80,37 @@ def time_decode(w_stub, gate, bias, records, layout, x0, budget_s: float = 12.0,
             break
     per_layer = el / done
     return per_layer * L, done, torch.get_num_threads()
+
+
+def median_seconds(fn, iters: int = 20, warmup: int = 2) -> float:
+    """Median wall time of fn() over `iters` runs after `warmup` runs."""
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def time_single_layer(x, w_stub, gate, bias, records, layout, top_k: int = 8,
+                      iters: int = 20, threads: int | None = None) -> float:
+    """Median seconds of one decode layer (stub, router, 8-expert
+    dequantise-then-matmul MoE) on `threads` host threads."""
+    old = torch.get_num_threads()
+    if threads:
+        torch.set_num_threads(threads)
+    try:
+        return median_seconds(lambda: decode_step_cpu(x, w_stub[:1], gate[:1], bias[:1],
+                                                      records[:1], layout, top_k), iters)
+    finally:
+        torch.set_num_threads(old)
+
+
+def time_gather(records, ids, iters: int = 20) -> float:
+    """Median seconds of gathering the routed records on the host (the CPU
+    side of the reference's "gather" copy mode, bin/offload.py:181-185)."""
+    idx = torch.as_tensor(ids, dtype=torch.long)
+    return median_seconds(lambda: records.index_select(0, idx), iters)
