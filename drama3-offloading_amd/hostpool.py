@@ -58,8 +58,15 @@ class RecordLayout:
         return self.off_s13 + self.s13_bytes
 
     @property
-    def record_bytes(self) -> int:
+    def payload_bytes(self) -> int:
         return self.off_s2 + self.s2_bytes
+
+    @property
+    def record_bytes(self) -> int:
+        """Payload rounded up to 256 bytes, so every record of a pool starts
+        256-byte aligned (the kernels' 16-byte loads need it); Drama-3's
+        3,146,496-byte record needs no padding."""
+        return (self.payload_bytes + 255) // 256 * 256
 
     def views(self, rec: torch.Tensor):
         """uint8 [n, record_bytes] -> (w13 e4m3 [n,2I,H], s13 f32, w2 e4m3 [n,H,I], s2 f32),
@@ -69,18 +76,18 @@ class RecordLayout:
         w13 = rec[:, :self.off_w2].view(torch.float8_e4m3fn).view(n, 2 * I, H)
         w2 = rec[:, self.off_w2:self.off_s13].view(torch.float8_e4m3fn).view(n, H, I)
         s13 = rec[:, self.off_s13:self.off_s2].view(torch.float32).view(n, 2 * I // 128, H // 128)
-        s2 = rec[:, self.off_s2:].view(torch.float32).view(n, H // 128, I // 128)
+        s2 = rec[:, self.off_s2:self.payload_bytes].view(torch.float32).view(n, H // 128, I // 128)
         return w13, s13, w2, s2
 
     def pack(self, w13: torch.Tensor, s13: torch.Tensor, w2: torch.Tensor,
              s2: torch.Tensor) -> torch.Tensor:
         """Dense per-buffer tensors [n, ...] -> packed uint8 records [n, record_bytes]."""
         n = w13.shape[0]
-        rec = torch.empty((n, self.record_bytes), dtype=torch.uint8, device=w13.device)
+        rec = torch.zeros((n, self.record_bytes), dtype=torch.uint8, device=w13.device)
         rec[:, :self.off_w2] = w13.reshape(n, -1).view(torch.uint8)
         rec[:, self.off_w2:self.off_s13] = w2.reshape(n, -1).view(torch.uint8)
         rec[:, self.off_s13:self.off_s2] = s13.reshape(n, -1).contiguous().view(torch.uint8)
-        rec[:, self.off_s2:] = s2.reshape(n, -1).contiguous().view(torch.uint8)
+        rec[:, self.off_s2:self.payload_bytes] = s2.reshape(n, -1).contiguous().view(torch.uint8)
         return rec
 
 

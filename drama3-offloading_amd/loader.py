@@ -122,7 +122,7 @@ def record_plan(index: ShardIndex, layer: int, expert: int, layout: RecordLayout
         t = index.get(name)
         _expect(t, name, dtype, shape)
         plan.append((t, off))
-    if sum(t.nbytes for t, _ in plan) != layout.record_bytes:
+    if sum(t.nbytes for t, _ in plan) != layout.payload_bytes:
         raise ValueError("expert tensors do not fill one record")
     return plan
 
@@ -152,7 +152,7 @@ class _Maps:
 def fill_records(index: ShardIndex, layer: int, dst: np.ndarray, layout: RecordLayout,
                  threads: int = 8) -> int:
     """Copy layer `layer`'s experts into dst, a uint8 array [n_experts,
-    record_bytes] (a HostPool's .array).  Returns the bytes copied."""
+    record_bytes] (a HostPool's .array).  Returns the payload bytes copied."""
     if index.root is None:
         raise ValueError("index has no shard directory to read from")
     plan = layer_plan(index, layer, layout, dst.shape[0])
@@ -162,7 +162,8 @@ def fill_records(index: ShardIndex, layer: int, dst: np.ndarray, layout: RecordL
         row = dst[e]
         for t, off in plan[e]:
             row[off:off + t.nbytes] = maps(t.shard)[t.start:t.start + t.nbytes]
-        return layout.record_bytes
+        row[layout.payload_bytes:] = 0          # alignment padding, if any
+        return layout.payload_bytes
 
     with ThreadPoolExecutor(max_workers=max(1, threads)) as ex:
         return sum(ex.map(one, range(dst.shape[0])))

@@ -38,7 +38,7 @@ def moe_forward_cpu(x: torch.Tensor, ids: torch.Tensor, wts: torch.Tensor,
                                 rec[:, layout.off_s13:layout.off_s2].contiguous()
                                 .view(torch.float32).view(n, 2 * I // 128, H // 128))
     w2 = dequantize_fp8_blocks(rec[:, layout.off_w2:layout.off_s13].view(n, H, I),
-                               rec[:, layout.off_s2:].contiguous()
+                               rec[:, layout.off_s2:layout.payload_bytes].contiguous()
                                .view(torch.float32).view(n, H // 128, I // 128))
     flat = inv.reshape(-1)
     xs = x.repeat_interleave(K, dim=0).unsqueeze(-1)             # [T*K, H, 1]

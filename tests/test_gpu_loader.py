@@ -22,7 +22,7 @@ def test_pools_from_shards_feed_the_fetch_and_ffn(lib, dev, tmp_path):
     say("loader: pools from shards")
     pools, nbytes = loader.load_host_pools(tmp_path, [0, 1], lay, threads=4)
     try:
-        assert nbytes == 2 * E * lay.record_bytes
+        assert nbytes == 2 * E * lay.payload_bytes
         index = loader.ShardIndex.from_dir(tmp_path)
         ref = moe.MoEExperts(E, H, I)
         loader.fill_expert_buffers(index, 1, ref)

@@ -37,6 +37,7 @@ def test_plan_matches_reference_checkpoint_layout():
         assert len(plan) == 256
         for rec in plan:
             assert sum(t.nbytes for t, _ in rec) == DRAMA3.record_bytes == 3_146_496
+            assert DRAMA3.payload_bytes == DRAMA3.record_bytes
             offs = sorted((off, t.nbytes) for t, off in rec)
             for (o0, n0), (o1, _) in zip(offs, offs[1:]):
                 assert o0 + n0 == o1                     # contiguous, no gaps or overlap
@@ -50,7 +51,10 @@ def _write_shards(tmp_path, layers=2, E=6, H=256, I=128, seed=0):
     from safetensors.torch import save_file
     from loader import EXPERT
     g = torch.Generator().manual_seed(seed)
-    f8 = lambda *s: torch.randint(0, 256, s, generator=g, dtype=torch.uint8).view(torch.float8_e4m3fn)  # noqa
+    # finite codes of magnitude < 2 with random signs (no NaN codes 0x7f / 0xff)
+    f8 = lambda *s: (torch.randint(0, 0x40, s, generator=g, dtype=torch.uint8)          # noqa
+                     | (torch.randint(0, 2, s, generator=g, dtype=torch.uint8) << 7)
+                     ).view(torch.float8_e4m3fn)
     sc = lambda *s: torch.rand(s, generator=g) + 0.5                                                       # noqa
     tensors = {}
     for l in range(layers):
@@ -83,7 +87,7 @@ def test_records_from_shards_equal_packed_tensors(tmp_path):
     assert index.n_experts(0) == 6 and index.n_experts(1) == 6
     for l in range(2):
         dst = np.zeros((6, lay.record_bytes), np.uint8)
-        assert loader.fill_records(index, l, dst, lay, threads=3) == 6 * lay.record_bytes
+        assert loader.fill_records(index, l, dst, lay, threads=3) == 6 * lay.payload_bytes
         for e in range(6):
             g, u, d = _expert(tensors, l, e, "weight")
             gs, us, ds = _expert(tensors, l, e, "weight_scale_inv")
