@@ -57,6 +57,45 @@ __device__ __forceinline__ float wave_max_f32(float v) {
   return v;
 }
 
+// Wave-wide max / min of a 64-bit key, returned uniform (in every lane):
+// DPP exchanges inside each row of 16 lanes (quad xor 1, quad xor 2, half-row
+// mirror, row mirror), then the four row results are read as scalars.  A
+// handful of VALU cycles per step instead of an LDS-crossbar shuffle.
+template <bool kMax>
+__device__ __forceinline__ uint64_t wave_reduce_u64(uint64_t v) {
+  uint32_t lo = static_cast<uint32_t>(v), hi = static_cast<uint32_t>(v >> 32);
+#define MOE_DPP_STEP(CTRL)                                                             \
+  {                                                                                    \
+    const uint32_t olo = __builtin_amdgcn_update_dpp(lo, lo, CTRL, 0xf, 0xf, false);   \
+    const uint32_t ohi = __builtin_amdgcn_update_dpp(hi, hi, CTRL, 0xf, 0xf, false);   \
+    const uint64_t o = (static_cast<uint64_t>(ohi) << 32) | olo;                       \
+    const uint64_t c = (static_cast<uint64_t>(hi) << 32) | lo;                         \
+    if (kMax ? (o > c) : (o < c)) {                                                    \
+      lo = olo;                                                                        \
+      hi = ohi;                                                                        \
+    }                                                                                  \
+  }
+  MOE_DPP_STEP(0x0B1)   // quad_perm [1,0,3,2]
+  MOE_DPP_STEP(0x04E)   // quad_perm [2,3,0,1]
+  MOE_DPP_STEP(0x141)   // row_half_mirror
+  MOE_DPP_STEP(0x140)   // row_mirror
+#undef MOE_DPP_STEP
+  uint64_t best = 0;
+#pragma unroll
+  for (int row = 0; row < 4; ++row) {
+    const uint64_t x =
+        (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(hi), row * 16))) << 32) |
+        static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lo), row * 16));
+    best = row == 0 ? x : (kMax ? (x > best ? x : best) : (x < best ? x : best));
+  }
+  return best;
+}
+
+// Value of lane `src` (uniform) as a scalar.
+__device__ __forceinline__ int32_t lane_value(int32_t v, int src) {
+  return __builtin_amdgcn_readlane(v, src);
+}
+
 __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

@@ -78,27 +78,25 @@ __device__ __forceinline__ void resolve_chunk(SlotRegs<PER>& t, int32_t my_e, in
                                               int64_t& hits) {
   const int lane = threadIdx.x & 63;
   for (int r = 0; r < n; ++r) {
-    const int32_t e = __shfl(my_e, r, 64);
-    int32_t s = __shfl(my_s, r, 64);
+    const int32_t e = lane_value(my_e, r);
+    int32_t s = lane_value(my_s, r);
     if (e < 0) {
       if (lane == 0) out_slot[base + r] = -1;
       continue;
     }
     if (s < 0) {
-      int64_t bst = INT64_MAX;
-      int32_t bix = INT32_MAX;
+      // victim = smallest stamp, lowest slot on a tie: one wave-wide min of
+      // (stamp + 4096) << 12 | slot.  Stamps start at -cap >= -4096 and grow
+      // by one per call, so they stay far below 2^51.
+      uint64_t mine = ~0ull;
 #pragma unroll
       for (int j = 0; j < PER; ++j) {
         const int c = lane + 64 * j;
-        if (c < cap && t.st[j] < bst) { bst = t.st[j]; bix = c; }
+        const uint64_t k =
+            c < cap ? (static_cast<uint64_t>(t.st[j] + kMaxCap) << 12) | static_cast<uint64_t>(c) : ~0ull;
+        mine = k < mine ? k : mine;
       }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const int64_t ost = __shfl_xor(bst, o, 64);
-        const int32_t oix = __shfl_xor(bix, o, 64);
-        if (ost < bst || (ost == bst && oix < bix)) { bst = ost; bix = oix; }
-      }
-      s = bix;
+      s = static_cast<int32_t>(wave_reduce_u64<false>(mine) & 0xfffull);
       int32_t vloc = -1;
 #pragma unroll
       for (int j = 0; j < PER; ++j) {
@@ -107,7 +105,7 @@ __device__ __forceinline__ void resolve_chunk(SlotRegs<PER>& t, int32_t my_e, in
           if ((s & 63) == lane) t.se[j] = e;
         }
       }
-      const int32_t victim = __shfl(vloc, s & 63, 64);
+      const int32_t victim = lane_value(vloc, s & 63);
       if (lane > r) {                      // later ids see the table as it is now
         if (my_e == victim) my_s = -1;
         if (my_e == e) my_s = s;

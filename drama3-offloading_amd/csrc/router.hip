@@ -11,7 +11,8 @@
 //   logits: grid (E/4, ceil(T/4)), 4 waves; wave w of workgroup (bx, by)
 //           computes expert 4*bx + w for the 4 tokens of block by, reading its
 //           4 KiB gate row once.
-//   topk:   one wave per token, logits in registers, k rounds of wave arg-max.
+//   topk:   one wave per token, logits in registers, k rounds of a wave-wide
+//           max of (logit, ~index) keys (DPP, no LDS shuffles).
 //   topk_resolve (decode): one wave does the top-k of one token AND the slot
 //           table update for those ids (slots.hip's resolve, same decisions),
 //           saving a launch per layer on the decode step.
@@ -67,42 +68,48 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   }
 }
 
+// Order-preserving 32-bit key of a float logit: larger logit, larger key;
+// NaN ranks below every number (it is picked only when nothing else is left).
+__device__ __forceinline__ uint32_t logit_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if (!(f == f)) return 1u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_logit(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
 // Top-k of one token's logits by one wave.  Lane r < k ends up holding the
-// r-th pick (*id, *wt = its renormalised softmax weight).
+// r-th pick (*id, *wt = its renormalised softmax weight).  Each candidate is
+// one 64-bit key, logit key above (~index) below, so a single wave-wide max
+// gives the largest logit with ties to the lower index; the pick's key is
+// then cleared.  Experts past n_experts get key 0 and are never picked
+// (top_k <= n_experts).
 template <int PER>
 __device__ __forceinline__ void wave_topk(const float* __restrict__ row, int32_t n_experts,
                                           int32_t top_k, int32_t* id, float* wt) {
   const int lane = threadIdx.x & 63;
-  float v[PER];
+  uint64_t key[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int e = lane + 64 * j;
-    v[j] = e < n_experts ? row[e] : -INFINITY;
+    key[j] = e < n_experts
+                 ? (static_cast<uint64_t>(logit_key(row[e])) << 32) | (0xffffffffu - static_cast<uint32_t>(e))
+                 : 0ull;
   }
-  uint64_t taken = 0;   // bit j: expert lane + 64*j already selected
   float m = 0.0f, sum = 0.0f, myv = 0.0f;
   int myi = -1;
   for (int r = 0; r < top_k; ++r) {
-    float bv = 0.0f;
-    int bi = INT32_MAX;
+    uint64_t b = key[0];
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int e = lane + 64 * j;
-      if (e < n_experts && !((taken >> j) & 1ull) && (bi == INT32_MAX || v[j] > bv)) {
-        bv = v[j];
-        bi = e;
-      }
-    }
+    for (int j = 1; j < PER; ++j) b = key[j] > b ? key[j] : b;
+    const uint64_t best = wave_reduce_u64<true>(b);
+    const int bi = static_cast<int>(0xffffffffu - static_cast<uint32_t>(best));
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      if (oi != INT32_MAX && (bi == INT32_MAX || ov > bv || (ov == bv && oi < bi))) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if ((bi & 63) == lane) taken |= 1ull << (bi >> 6);
+    for (int j = 0; j < PER; ++j)
+      if (key[j] == best) key[j] = 0ull;
+    const float bv = key_logit(static_cast<uint32_t>(best >> 32));
     if (r == 0) m = bv;
     const float ex = expf(bv - m);
     sum += ex;
