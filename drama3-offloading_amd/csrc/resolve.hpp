@@ -128,13 +128,27 @@ __device__ __forceinline__ void resolve_chunk(SlotRegs<PER>& t, int32_t my_e, in
   }
 }
 
+// The device hit/miss counters, read when the kernel starts (with the other
+// table loads) so that adding this call's counts at the end costs no
+// memory round trip.
+struct StatsPrefetch {
+  int64_t hits = 0, misses = 0;
+  __device__ __forceinline__ void load(const int64_t* stats) {
+    if (stats) {
+      hits = stats[0];
+      misses = stats[1];
+    }
+  }
+};
+
 template <int PER>
 __device__ __forceinline__ void resolve_finish(const SlotRegs<PER>& t, int64_t step, int32_t nm,
                                                int64_t hits, int32_t cap,
                                                int64_t* __restrict__ stamp,
                                                int64_t* __restrict__ step_ptr,
                                                int32_t* __restrict__ nmiss_ptr,
-                                               int64_t* __restrict__ stats) {
+                                               int64_t* __restrict__ stats,
+                                               const StatsPrefetch& prev) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
@@ -145,8 +159,8 @@ __device__ __forceinline__ void resolve_finish(const SlotRegs<PER>& t, int64_t s
     *step_ptr = step;
     *nmiss_ptr = nm;
     if (stats) {
-      stats[0] += hits;
-      stats[1] += nm;
+      stats[0] = prev.hits + hits;
+      stats[1] = prev.misses + nm;
     }
   }
 }
@@ -167,6 +181,8 @@ __device__ __forceinline__ void resolve_wave_impl(IdAt id_at, int32_t k, int32_t
   const int lane = threadIdx.x & 63;
   SlotRegs<PER> t;
   t.load(stamp, slot_expert, cap);
+  StatsPrefetch prev;
+  prev.load(stats);
   // read at run time, never a launch argument: a captured step would
   // otherwise stamp the same value on every replay
   const int64_t step = *step_ptr + 1;
@@ -186,7 +202,7 @@ __device__ __forceinline__ void resolve_wave_impl(IdAt id_at, int32_t k, int32_t
                        out_slot, fetch_slot, fetch_expert, nm, hits);
     if (base + 64 < k) __threadfence();
   }
-  resolve_finish<PER>(t, step, nm, hits, cap, stamp, step_ptr, nmiss_ptr, stats);
+  resolve_finish<PER>(t, step, nm, hits, cap, stamp, step_ptr, nmiss_ptr, stats, prev);
 }
 
 }  // namespace moe

@@ -25,28 +25,80 @@
 namespace moe {
 
 constexpr int kMaxTopK = 32;
-constexpr int kTokBlock = 4;
+constexpr int kTokBlock = 4;     // tokens per logits workgroup when tokens > 1
 
+// Wave-wide float64 sum, uniform in every lane: DPP butterfly inside each
+// row of 16 lanes, then the four row sums read as scalars and added in row
+// order.  The products summed here are exact and their float64 partial sums
+// are exact for ordinary data, so the order does not change the result.
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t u = __double_as_longlong(v);
+  const uint32_t lo = __builtin_amdgcn_update_dpp(static_cast<uint32_t>(u), static_cast<uint32_t>(u),
+                                                  CTRL, 0xf, 0xf, false);
+  const uint32_t hi = __builtin_amdgcn_update_dpp(static_cast<uint32_t>(u >> 32),
+                                                  static_cast<uint32_t>(u >> 32), CTRL, 0xf, 0xf,
+                                                  false);
+  return __longlong_as_double(static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo));
+}
+
+__device__ __forceinline__ double wave_sum_f64_dpp(double v) {
+  v += dpp_f64<0x0B1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f64<0x04E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f64<0x141>(v);   // row_half_mirror
+  v += dpp_f64<0x140>(v);   // row_mirror
+  const uint64_t u = __double_as_longlong(v);
+  double s = 0.0;
+#pragma unroll
+  for (int row = 0; row < 4; ++row) {
+    const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(u)), row * 16);
+    const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(u >> 32)), row * 16);
+    s += __longlong_as_double(static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo));
+  }
+  return s;
+}
+
+// One wave per (expert, block of TB tokens): the expert's gate row and the
+// tokens' rows are read in chunks of 4 x 16 bytes per lane, every load of a
+// chunk issued before any of it is used (no load under a branch: lanes and
+// tokens past the end re-read an in-bounds address and add nothing).
+template <int TB>
 __global__ __launch_bounds__(256) void router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ bias,
     int32_t tokens, int32_t hidden, int32_t n_experts, float* __restrict__ logits) {
+  constexpr int U = 4;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int e = blockIdx.x * 4 + wave;
-  const int t0 = blockIdx.y * kTokBlock;
-  const int nt = min(kTokBlock, tokens - t0);
+  const int t0 = blockIdx.y * TB;
+  const int nt = min(TB, tokens - t0);
   if (e >= n_experts) return;
   const int nv = hidden >> 3;                 // 16-byte vectors per row
   const uint4* wr = reinterpret_cast<const uint4*>(w + static_cast<int64_t>(e) * hidden);
-  double acc[kTokBlock] = {0.0, 0.0, 0.0, 0.0};
-  for (int i = lane; i < nv; i += 64) {
-    const uint4 b = wr[i];
-    const uint32_t bv[4] = {b.x, b.y, b.z, b.w};
+  const uint4* xr[TB];
 #pragma unroll
-    for (int tt = 0; tt < kTokBlock; ++tt) {
-      if (tt < nt) {
-        const uint4 a = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(t0 + tt) * hidden)[i];
-        const uint32_t av[4] = {a.x, a.y, a.z, a.w};
+  for (int tt = 0; tt < TB; ++tt)
+    xr[tt] = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(t0 + min(tt, nt - 1)) * hidden);
+  double acc[TB];
+#pragma unroll
+  for (int tt = 0; tt < TB; ++tt) acc[tt] = 0.0;
+  for (int i0 = 0; i0 < nv; i0 += 64 * U) {
+    uint4 b[U], a[TB][U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + 64 * u + lane;
+      const int ic = i < nv ? i : nv - 1;
+      b[u] = wr[ic];
+#pragma unroll
+      for (int tt = 0; tt < TB; ++tt) a[tt][u] = xr[tt][ic];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (i0 + 64 * u + lane >= nv) continue;
+      const uint32_t bv[4] = {b[u].x, b[u].y, b[u].z, b[u].w};
+#pragma unroll
+      for (int tt = 0; tt < TB; ++tt) {
+        const uint32_t av[4] = {a[tt][u].x, a[tt][u].y, a[tt][u].z, a[tt][u].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const float a0 = __uint_as_float(av[j] << 16), a1 = __uint_as_float(av[j] & 0xffff0000u);
@@ -58,8 +110,8 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
     }
   }
 #pragma unroll
-  for (int tt = 0; tt < kTokBlock; ++tt) {
-    const double s = wave_sum_f64(acc[tt]);
+  for (int tt = 0; tt < TB; ++tt) {
+    const double s = wave_sum_f64_dpp(acc[tt]);
     if (lane == 0 && tt < nt) {
       float l = static_cast<float>(s);
       if (bias) l += bias[e];
@@ -155,6 +207,8 @@ __global__ __launch_bounds__(64) void topk_resolve_kernel(
   t.load(stamp, slot_expert, cap);
   ExpertRegs<PER> table;
   table.load(slot_of, n_experts);
+  StatsPrefetch prev;
+  prev.load(stats);
   const int64_t step = *step_ptr + 1;
   int32_t id;
   float wt;
@@ -171,7 +225,7 @@ __global__ __launch_bounds__(64) void topk_resolve_kernel(
   int64_t hits = 0;
   resolve_chunk<PERC>(t, my_e, my_s, top_k, 0, step, cap, slot_of, slot_expert, out_slot,
                       fetch_slot, fetch_expert, nm, hits);
-  resolve_finish<PERC>(t, step, nm, hits, cap, stamp, step_ptr, nmiss_ptr, stats);
+  resolve_finish<PERC>(t, step, nm, hits, cap, stamp, step_ptr, nmiss_ptr, stats, prev);
 }
 
 }  // namespace moe
@@ -195,9 +249,14 @@ extern "C" int moe_router_topk(const void* x, const void* w, const float* bias, 
   const dim3 grid((n_experts + 3) / 4, (tokens + kTokBlock - 1) / kTokBlock);
   MOE_REQUIRE(grid.y <= 65535, "moe_router_topk: too many tokens (%d)", tokens);
   hipStream_t s = as_stream(stream);
-  hipLaunchKernelGGL(router_logits_kernel, grid, dim3(256), 0, s,
-                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias,
-                     tokens, hidden, n_experts, logits);
+  if (tokens == 1)
+    hipLaunchKernelGGL(router_logits_kernel<1>, grid, dim3(256), 0, s,
+                       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias,
+                       tokens, hidden, n_experts, logits);
+  else
+    hipLaunchKernelGGL(router_logits_kernel<kTokBlock>, grid, dim3(256), 0, s,
+                       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias,
+                       tokens, hidden, n_experts, logits);
   int rc = check_launch("moe_router_topk(logits)");
   if (rc) return rc;
   const int i64 = ids_dtype == MOE_I64 ? 1 : 0, bf = w_dtype == MOE_BF16 ? 1 : 0;
@@ -229,7 +288,7 @@ extern "C" int moe_route_resolve(const void* x, const void* w, const float* bias
   MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0,
               "moe_route_resolve: x and w must be 16-byte aligned");
   hipStream_t s = as_stream(stream);
-  hipLaunchKernelGGL(router_logits_kernel, dim3((n_experts + 3) / 4, 1), dim3(256), 0, s,
+  hipLaunchKernelGGL(router_logits_kernel<1>, dim3((n_experts + 3) / 4, 1), dim3(256), 0, s,
                      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias, 1,
                      hidden, n_experts, logits);
   int rc = check_launch("moe_route_resolve(logits)");
