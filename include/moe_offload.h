@@ -216,7 +216,9 @@ int moe_permute(const void* ids, int32_t ids_dtype, int32_t tokens,
                 int32_t* offsets, int32_t* sorted_pairs, int32_t* pair_pos,
                 void* stream);
 
-/* out[t] = sum_k weights[t,k] * y[pair_pos[t*top_k+k]] in k order, as bf16.
+/* out[t] = sum over k of weights[t,k] * y[pair_pos[t*top_k+k]], accumulated
+ * in k order as acc = fma(w, y, acc) in float32, rounded to bf16 (the
+ * combine of the decode path, so both give identical rows).
  * y [tokens*top_k, hidden] f32. */
 int moe_unpermute(const float* y, const int32_t* pair_pos, const void* weights,
                   int32_t w_dtype, int32_t tokens, int32_t top_k,
