@@ -48,6 +48,36 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f +
 
 // ------------------------------------------------------------ wave utils
 
+// SiLU(gate) * up of 8 intermediate columns j..j+7 held by one lane
+// (hr = gate[j..j+3], gate[j+4..j+7], up[j..j+3], up[j+4..j+7]) -> e4m3
+// codes and the group scale in LDS; 16 consecutive lanes form one 128-group.
+// Every lane of the wave calls this, lanes past the end with live == false.
+__device__ __forceinline__ void silu_quantize8(const float4 (&hr)[4], bool live, int j,
+                                               uint8_t* __restrict__ aq, float* __restrict__ as) {
+  const float gv[8] = {hr[0].x, hr[0].y, hr[0].z, hr[0].w, hr[1].x, hr[1].y, hr[1].z, hr[1].w};
+  const float uv[8] = {hr[2].x, hr[2].y, hr[2].z, hr[2].w, hr[3].x, hr[3].y, hr[3].z, hr[3].w};
+  float av[8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    av[i] = silu_mul(gv[i], uv[i]);
+    amax = fmaxf(amax, fabsf(av[i]));
+  }
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  if (live) {
+    const float sc = act_scale(amax);
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lo |= quant_e4m3(av[i], sc) << (8 * i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hi |= quant_e4m3(av[4 + i], sc) << (8 * i);
+    *reinterpret_cast<uint2*>(aq + j) = make_uint2(lo, hi);
+    if ((threadIdx.x & 15) == 0) as[j >> 7] = sc;
+  }
+}
+
+
 template <typename T>
 __device__ __forceinline__ T wave_bcast(T v, int lane) { return __shfl(v, lane, 64); }
 

@@ -159,35 +159,6 @@ __global__ __launch_bounds__(64) void gateup_gemv_kernel(
 
 // ------------------------------------------------------------ kernel 2
 
-// SiLU(gate) * up of 8 intermediate columns j..j+7 held by one lane
-// (hr = gate[j..j+3], gate[j+4..j+7], up[j..j+3], up[j+4..j+7]) -> e4m3
-// codes and the group scale in LDS; 16 consecutive lanes form one 128-group.
-// Every lane of the wave calls this, lanes past the end with live == false.
-__device__ __forceinline__ void silu_quantize8(const float4 (&hr)[4], bool live, int j,
-                                               uint8_t* __restrict__ aq, float* __restrict__ as) {
-  const float gv[8] = {hr[0].x, hr[0].y, hr[0].z, hr[0].w, hr[1].x, hr[1].y, hr[1].z, hr[1].w};
-  const float uv[8] = {hr[2].x, hr[2].y, hr[2].z, hr[2].w, hr[3].x, hr[3].y, hr[3].z, hr[3].w};
-  float av[8];
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    av[i] = silu_mul(gv[i], uv[i]);
-    amax = fmaxf(amax, fabsf(av[i]));
-  }
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-  if (live) {
-    const float sc = act_scale(amax);
-    uint32_t lo = 0, hi = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) lo |= quant_e4m3(av[i], sc) << (8 * i);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) hi |= quant_e4m3(av[4 + i], sc) << (8 * i);
-    *reinterpret_cast<uint2*>(aq + j) = make_uint2(lo, hi);
-    if ((threadIdx.x & 15) == 0) as[j >> 7] = sc;
-  }
-}
-
 // Workgroup = one wave per k, 16 output rows of w2 per wave.  The weight
 // loads go out first; SiLU(gate)*up of the pair is quantised into LDS while
 // they travel; the k partial results are summed in k order.
@@ -294,7 +265,7 @@ constexpr int32_t kGemvMaxTokens = 2;
 static bool use_grouped(int32_t tokens, int32_t hidden, int32_t mode) {
   if (mode == 1) return false;
   if (mode == 2) return true;
-  return tokens > kGemvMaxTokens && hidden % 256 == 0;
+  return tokens > kGemvMaxTokens;
 }
 
 extern "C" size_t moe_fp8_moe_workspace(int32_t tokens, int32_t top_k, int32_t n_experts,
@@ -362,7 +333,6 @@ extern "C" int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t id
   const int wbf16 = w_dtype == MOE_BF16;
   const int64_t pairs = static_cast<int64_t>(tokens) * top_k;
   if (use_grouped(tokens, hidden, mode)) {
-    MOE_REQUIRE(hidden % 256 == 0, "moe_fp8_moe_forward: the grouped kernels need hidden %% 256 == 0");
     MOE_REQUIRE(n_experts <= 4096 && pairs <= (1LL << 24) && tokens <= 65535,
                 "moe_fp8_moe_forward: grouped path limits: n_experts <= 4096, tokens <= 65535");
     return launch_grouped(static_cast<const uint16_t*>(x), ids, ids64, weights, wbf16, tokens,

@@ -63,7 +63,8 @@ __device__ int32_t block_exclusive_scan(int32_t v, int32_t* scratch, int32_t* ou
 __global__ __launch_bounds__(kPlaceThreads) void permute_kernel(
     const void* __restrict__ ids, int ids64, int64_t P, int32_t n_experts,
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ sorted_pairs,
-    int32_t* __restrict__ pair_pos) {
+    int32_t* __restrict__ pair_pos, int32_t* __restrict__ tiles, int32_t* __restrict__ n_tiles,
+    int32_t tile_tokens) {
   __shared__ int32_t cursor[kPermMaxExperts];
   __shared__ uint64_t fields[kPermMaxExperts];
   __shared__ int32_t scratch[40];
@@ -101,6 +102,29 @@ __global__ __launch_bounds__(kPlaceThreads) void permute_kernel(
     base += mine[j];
   }
   if (tid == 0) offsets[n_experts] = total;
+  if (tiles) {
+    // work tiles of the grouped kernels: (expert, first row of the segment)
+    // for every tile_tokens rows of every expert's segment, in expert order
+    int32_t nt[kPlacePer];
+    int32_t tsum = 0;
+#pragma unroll
+    for (int j = 0; j < kPlacePer; ++j) {
+      nt[j] = (mine[j] + tile_tokens - 1) / tile_tokens;
+      tsum += nt[j];
+    }
+    int32_t tbase;
+    const int32_t ttotal = block_exclusive_scan<kPlaceThreads / 64>(tsum, scratch, &tbase);
+#pragma unroll
+    for (int j = 0; j < kPlacePer; ++j) {
+      const int x = tid * kPlacePer + j;
+      for (int32_t i = 0; i < nt[j]; ++i) {
+        tiles[2 * (tbase + i)] = x;
+        tiles[2 * (tbase + i) + 1] = i * tile_tokens;
+      }
+      tbase += nt[j];
+    }
+    if (tid == 0) *n_tiles = ttotal;
+  }
   __syncthreads();
   const uint64_t below_lane = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   for (int64_t r0 = 0; r0 < P; r0 += kPlaceThreads) {
@@ -272,9 +296,10 @@ __global__ __launch_bounds__(64) void gather_plan_kernel(
 }
 
 int launch_permute(const void* ids, int ids64, int64_t P, int32_t n_experts, int32_t* counts,
-                   int32_t* offsets, int32_t* sorted_pairs, int32_t* pair_pos, hipStream_t s) {
+                   int32_t* offsets, int32_t* sorted_pairs, int32_t* pair_pos, hipStream_t s,
+                   int32_t* tiles, int32_t* n_tiles, int32_t tile_tokens) {
   hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(kPlaceThreads), 0, s, ids, ids64, P, n_experts,
-                     counts, offsets, sorted_pairs, pair_pos);
+                     counts, offsets, sorted_pairs, pair_pos, tiles, n_tiles, tile_tokens);
   return check_launch("moe_permute");
 }
 

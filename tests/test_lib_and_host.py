@@ -52,7 +52,9 @@ def test_workspace_size_formula(lib):
 
     def grouped(T, K, E, H, I):
         P = T * K
-        return (al(4 * E) + al(4 * (E + 1)) + 2 * al(4 * P) + al(T * H) + al(4 * T * H // 128)
+        max_tiles = (P + 31) // 32 + E              # 32-token work tiles, one list entry each
+        return (al(4 * E) + al(4 * (E + 1)) + 2 * al(4 * P) + al(8 * max_tiles) + al(4)
+                + al(T * H) + al(4 * T * H // 128) + al(4 * P * 2 * I)
                 + al(P * I) + al(4 * P * I // 128) + al(4 * P * H))
 
     for T in (1, 2, 5, 512):
