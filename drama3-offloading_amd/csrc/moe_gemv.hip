@@ -288,8 +288,6 @@ extern "C" int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t id
                                       const void* residual, void* out,
                                       void* workspace, size_t workspace_bytes, int32_t mode,
                                       void* stream) {
-  MOE_REQUIRE(x && ids && weights && w13 && s13 && w2 && s2 && out,
-              "moe_fp8_moe_forward: NULL pointer");
   MOE_REQUIRE(tokens >= 0, "moe_fp8_moe_forward: tokens < 0");
   MOE_REQUIRE(top_k >= 1 && top_k <= kMaxK, "moe_fp8_moe_forward: need 1 <= top_k <= %d", kMaxK);
   MOE_REQUIRE(hidden >= 128 && hidden % 128 == 0 && hidden <= kMaxHidden,
@@ -302,6 +300,9 @@ extern "C" int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t id
   MOE_REQUIRE(ids_dtype == MOE_I32 || ids_dtype == MOE_I64, "moe_fp8_moe_forward: bad ids_dtype");
   MOE_REQUIRE(w_dtype == MOE_F32 || w_dtype == MOE_BF16, "moe_fp8_moe_forward: bad w_dtype");
   MOE_REQUIRE(mode >= 0 && mode <= 2, "moe_fp8_moe_forward: mode must be 0, 1 or 2");
+  if (tokens == 0) return MOE_OK;   // an empty call touches nothing (its tensors may be NULL)
+  MOE_REQUIRE(x && ids && weights && w13 && s13 && w2 && s2 && out,
+              "moe_fp8_moe_forward: NULL pointer");
   MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w13) % 16 == 0 &&
                   reinterpret_cast<uintptr_t>(w2) % 16 == 0,
               "moe_fp8_moe_forward: x, w13 and w2 must be 16-byte aligned");
@@ -320,7 +321,6 @@ extern "C" int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t id
               "moe_fp8_moe_forward: expert strides smaller than one expert");
   MOE_REQUIRE(es.w13 % 16 == 0 && es.w2 % 16 == 0,
               "moe_fp8_moe_forward: w13/w2 expert strides must be multiples of 16 bytes");
-  if (tokens == 0) return MOE_OK;
   const size_t need = moe_fp8_moe_workspace(tokens, top_k, n_experts, hidden, inter);
   MOE_REQUIRE(workspace != nullptr && workspace_bytes >= need,
               "moe_fp8_moe_forward: workspace of %zu bytes needed, %zu given", need,

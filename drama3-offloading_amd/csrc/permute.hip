@@ -318,12 +318,15 @@ using namespace moe;
 extern "C" int moe_permute(const void* ids, int32_t ids_dtype, int32_t tokens, int32_t top_k,
                            int32_t n_experts, int32_t* counts, int32_t* offsets,
                            int32_t* sorted_pairs, int32_t* pair_pos, void* stream) {
-  MOE_REQUIRE(ids && counts && offsets && sorted_pairs && pair_pos, "moe_permute: NULL pointer");
   MOE_REQUIRE(ids_dtype == MOE_I32 || ids_dtype == MOE_I64, "moe_permute: bad ids_dtype");
   MOE_REQUIRE(tokens >= 0 && top_k >= 1, "moe_permute: need tokens >= 0, top_k >= 1");
   MOE_REQUIRE(n_experts >= 1 && n_experts <= kPermMaxExperts,
               "moe_permute: need 1 <= n_experts <= %d", kPermMaxExperts);
   const int64_t P = static_cast<int64_t>(tokens) * top_k;
+  // no pairs: counts and offsets are still written (all zero); the per-pair
+  // arrays may be NULL
+  MOE_REQUIRE(counts && offsets && (P == 0 || (ids && sorted_pairs && pair_pos)),
+              "moe_permute: NULL pointer");
   MOE_REQUIRE(P <= (1LL << 24), "moe_permute: too many pairs (%lld)", (long long)P);
   return launch_permute(ids, ids_dtype == MOE_I64 ? 1 : 0, P, n_experts, counts, offsets,
                         sorted_pairs, pair_pos, as_stream(stream));
@@ -333,13 +336,13 @@ extern "C" int moe_unique_inverse(const void* ids, int32_t ids_dtype, int32_t to
                                   int32_t top_k, int32_t n_experts, const int32_t* counts,
                                   int32_t* n_unique, int32_t* uniq, int32_t* rank_of,
                                   int32_t* inverse, void* stream) {
-  MOE_REQUIRE(ids && counts && n_unique && uniq && rank_of && inverse,
-              "moe_unique_inverse: NULL pointer");
   MOE_REQUIRE(ids_dtype == MOE_I32 || ids_dtype == MOE_I64, "moe_unique_inverse: bad ids_dtype");
   MOE_REQUIRE(tokens >= 0 && top_k >= 1, "moe_unique_inverse: need tokens >= 0, top_k >= 1");
   MOE_REQUIRE(n_experts >= 1 && n_experts <= kPermMaxExperts,
               "moe_unique_inverse: need 1 <= n_experts <= %d", kPermMaxExperts);
   const int64_t P = static_cast<int64_t>(tokens) * top_k;
+  MOE_REQUIRE(counts && n_unique && uniq && rank_of && (P == 0 || (ids && inverse)),
+              "moe_unique_inverse: NULL pointer");
   hipLaunchKernelGGL(unique_inverse_kernel, dim3(1), dim3(kPermThreads), 0, as_stream(stream), ids,
                      ids_dtype == MOE_I64 ? 1 : 0, P, n_experts, counts, n_unique, uniq, rank_of,
                      inverse);
@@ -349,12 +352,12 @@ extern "C" int moe_unique_inverse(const void* ids, int32_t ids_dtype, int32_t to
 extern "C" int moe_unpermute(const float* y, const int32_t* pair_pos, const void* weights,
                              int32_t w_dtype, int32_t tokens, int32_t top_k, int32_t hidden,
                              void* out, void* stream) {
-  MOE_REQUIRE(y && pair_pos && weights && out, "moe_unpermute: NULL pointer");
   MOE_REQUIRE(w_dtype == MOE_F32 || w_dtype == MOE_BF16, "moe_unpermute: bad w_dtype");
   MOE_REQUIRE(tokens >= 0 && top_k >= 1, "moe_unpermute: need tokens >= 0, top_k >= 1");
   MOE_REQUIRE(hidden > 0 && hidden % 4 == 0, "moe_unpermute: hidden %% 4 != 0");
-  MOE_REQUIRE(reinterpret_cast<uintptr_t>(y) % 16 == 0, "moe_unpermute: y must be 16-byte aligned");
   if (tokens == 0) return MOE_OK;
+  MOE_REQUIRE(y && pair_pos && weights && out, "moe_unpermute: NULL pointer");
+  MOE_REQUIRE(reinterpret_cast<uintptr_t>(y) % 16 == 0, "moe_unpermute: y must be 16-byte aligned");
   return launch_unpermute(y, pair_pos, weights, w_dtype == MOE_BF16 ? 1 : 0, tokens, top_k,
                           hidden, nullptr, static_cast<uint16_t*>(out), as_stream(stream));
 }

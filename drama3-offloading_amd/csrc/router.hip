@@ -236,16 +236,16 @@ extern "C" int moe_router_topk(const void* x, const void* w, const float* bias, 
                                int32_t hidden, int32_t n_experts, int32_t top_k, float* logits,
                                void* ids, int32_t ids_dtype, void* weights, int32_t w_dtype,
                                void* stream) {
-  MOE_REQUIRE(x && w && logits && ids && weights, "moe_router_topk: NULL pointer");
   MOE_REQUIRE(tokens >= 0, "moe_router_topk: tokens < 0");
   MOE_REQUIRE(hidden > 0 && hidden % 8 == 0, "moe_router_topk: hidden %% 8 != 0 (%d)", hidden);
   MOE_REQUIRE(top_k >= 1 && top_k <= kMaxTopK && top_k <= n_experts && n_experts <= 4096,
               "moe_router_topk: need 1 <= top_k <= min(32, n_experts), n_experts <= 4096");
   MOE_REQUIRE(ids_dtype == MOE_I32 || ids_dtype == MOE_I64, "moe_router_topk: bad ids_dtype");
   MOE_REQUIRE(w_dtype == MOE_F32 || w_dtype == MOE_BF16, "moe_router_topk: bad w_dtype");
+  if (tokens == 0) return MOE_OK;   // an empty call touches nothing (its tensors may be NULL)
+  MOE_REQUIRE(x && w && logits && ids && weights, "moe_router_topk: NULL pointer");
   MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0,
               "moe_router_topk: x and w must be 16-byte aligned");
-  if (tokens == 0) return MOE_OK;
   const dim3 grid((n_experts + 3) / 4, (tokens + kTokBlock - 1) / kTokBlock);
   MOE_REQUIRE(grid.y <= 65535, "moe_router_topk: too many tokens (%d)", tokens);
   hipStream_t s = as_stream(stream);

@@ -13,7 +13,10 @@
  *     kernel, never baked into a launch argument;
  *   - the return value is 0 on success, MOE_EINVAL (-1) when a precondition
  *     fails (nothing is enqueued), or the positive hipError_t of a failed
- *     launch; moe_last_error() then describes the failure (thread-local).
+ *     launch; moe_last_error() then describes the failure (thread-local);
+ *   - a call with zero tokens does nothing and may pass NULL for its
+ *     per-token arrays (moe_permute / moe_unique_inverse still write their
+ *     per-expert outputs: all experts empty).
  */
 #ifndef MOE_OFFLOAD_H
 #define MOE_OFFLOAD_H
