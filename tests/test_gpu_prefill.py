@@ -139,3 +139,50 @@ def test_dev_cached_forward_device_prefill_equals_reference_form(lib, dev, layer
     torch.cuda.synchronize()
     assert offload.HYBRID_GATHER
     assert torch.equal(got, want)
+
+
+def test_device_prefill_is_capturable_and_dynamic(lib, dev, layer):
+    """The device prefill has no host synchronisation, so a whole call is
+    captured once and replayed with different routing each time; every
+    replay equals the eager call on the same ids (hybrid gather included)."""
+    import devcache
+    from prefill import DevicePrefill
+    ref, host = layer
+    devcache.init_dev_cache(host, dev, 20)
+    for s in range(4):
+        devcache.dev_resolve_and_fetch(host, _routing(1, 200 + s, dev)[0])
+    T = 24
+    x = torch.randn((T, H), device=dev).to(torch.bfloat16)
+    ids_live = torch.zeros((T, K), dtype=torch.int64, device=dev)
+    w_live = torch.zeros((T, K), device=dev)
+    pairs = devcache._copy_pairs(host)
+    src = [devcache._device_ptr(lib, h) for h, _ in pairs]
+    cache = (host._dc_slot_of, host._dc_cap, [c.data_ptr() for _, c in pairs])
+    pf = DevicePrefill.for_experts(host, K, T, dev)
+    out = torch.empty_like(x)
+
+    def body():
+        pf.forward(x, ids_live, w_live, src, cache, out=out)
+
+    ids0, w0 = _routing(T, 50, dev)
+    ids_live.copy_(ids0)
+    w_live.copy_(w0)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        body()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    say("prefill: capture")
+    with torch.cuda.graph(g):
+        body()
+    eager = DevicePrefill.for_experts(host, K, T, dev)
+    for r in range(4):
+        ids_r, w_r = _routing(T, 60 + r, dev)
+        ids_live.copy_(ids_r)
+        w_live.copy_(w_r)
+        g.replay()
+        torch.cuda.synchronize()
+        want = eager.forward(x, ids_r, w_r, src, cache)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {r}"
