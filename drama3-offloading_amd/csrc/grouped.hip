@@ -1,25 +1,24 @@
 // Grouped W8A8 expert FFN for many tokens (prefill, batched decode): token
-// rows are permuted into per-expert segments (permute.hip), every expert's
-// weights are read from HBM once for all of its tokens, and the results are
-// un-permuted with the routing weights.
+// rows are permuted into per-expert segments (permute.hip), the segments are
+// cut into tiles of up to 32 rows, every expert's weights are read from HBM
+// once per tile, and the results are un-permuted with the routing weights.
 //
 //   quant_rows:  x [T, H] bf16 -> xq [T, H] e4m3, xs [T, H/128]   (per token)
-//   gateup:      grid (E, I/128), 4 waves.  Workgroup = expert e, quant
-//                group jb of the intermediate: wave w owns gate columns
-//                j in [jb*128 + 32w, +32) and the up columns j + I, i.e. four
-//                16-column MFMA tiles, for up to 64 tokens of the segment at a
-//                time.  After the 2048-deep reduction it forms
-//                a = SiLU(gate) * up, takes the per-token amax over the group's
-//                128 columns across the four waves, and writes aq/as rows in
+//   gateup:      work items (tile, 64 rows of w13), 4 waves x 16 rows each
+//                with every K-block of the wave's rows in flight at once; the
+//                tile's xq rows are staged in LDS for the 4 waves.  A fixed
+//                grid of workgroups strides over the items, whose count the
+//                permute kernel leaves on the device.  h [pos, 2I] float32 in
 //                permuted order.
-//   down:        grid (E, H/256), 4 waves x 4 tiles of 16 output features;
-//                the activations are the expert's contiguous aq rows.  y rows
-//                in permuted order, float32.
+//   silu:        one wave per permuted row: a = SiLU(gate) * up, quantised
+//                per 128 (aq, as) -- the decode GEMV's own function.
+//   down:        work items (tile, 64 rows of w2) the same way, the tile's aq
+//                rows staged in LDS.  y [pos, H] float32.
 //   unpermute:   out[t] = sum_k w[t,k] * y[pos[t,k]] (permute.hip).
 //
 // MFMA 16x16x128 e4m3 with the same operand roles as the decode GEMV:
-// weight rows are the A operand, activations the B operand (here one token
-// per B column), every lane supplies the same 32-byte reduction slice, block
+// weight rows are the A operand, activations the B operand (one token per B
+// column), every lane supplies the same 32-byte reduction slice, block
 // scales multiply each 128-deep block result as weight_scale *
 // activation_scale, and the blocks are summed in the same order -- so every
 // (token, expert) row computed here is bit-identical to the decode GEMV's.
