@@ -8,9 +8,9 @@
 // summation, which is what lets expert ids match the oracle bit for bit.
 //
 // Kernels:
-//   logits: grid (E/4, ceil(T/4)), 4 waves; wave w of workgroup (bx, by)
-//           computes expert 4*bx + w for the 4 tokens of block by, reading its
-//           4 KiB gate row once.
+//   logits: grid (E/4, ceil(T/TB)), 4 waves, TB = 1 for one token else 4;
+//           wave w of workgroup (bx, by) computes expert 4*bx + w for the TB
+//           tokens of block by, reading its 4 KiB gate row once.
 //   topk:   one wave per token, logits in registers, k rounds of a wave-wide
 //           max of (logit, ~index) keys (DPP, no LDS shuffles).
 //   topk_resolve (decode): one wave does the top-k of one token AND the slot
