@@ -499,7 +499,10 @@ def cpu_baseline(harness, budget_s: float):
                        f"{threads} threads, os.cpu_count()={os.cpu_count()}, CPU '{model}'"),
             "single_layer_ms_median": {"threads_all": round(1e3 * layer_all, 2),
                                        "threads_1": round(1e3 * layer_one, 2),
-                                       "iters": 20},
+                                       "iters": 20, "warmup": 3},
+            "single_layer_expert_GBps": {
+                "threads_all": round(cfg.top_k * harness.layout.record_bytes / layer_all / 1e9, 3),
+                "threads_1": round(cfg.top_k * harness.layout.record_bytes / layer_one / 1e9, 3)},
             "gather_8_records_ms_median": round(1e3 * gather, 3)}
 
 

@@ -82,7 +82,7 @@ def time_decode(w_stub, gate, bias, records, layout, x0, budget_s: float = 12.0,
     return per_layer * L, done, torch.get_num_threads()
 
 
-def median_seconds(fn, iters: int = 20, warmup: int = 2) -> float:
+def median_seconds(fn, iters: int = 20, warmup: int = 3) -> float:
     """Median wall time of fn() over `iters` runs after `warmup` runs."""
     for _ in range(warmup):
         fn()
