@@ -4,16 +4,13 @@
 // once per tile, and the results are un-permuted with the routing weights.
 //
 //   quant_rows:  x [T, H] bf16 -> xq [T, H] e4m3, xs [T, H/128]   (per token)
-//   gateup:      work items (tile, 64 rows of w13), 4 waves x 16 rows each
-//                with every K-block of the wave's rows in flight at once; the
-//                tile's xq rows are staged in LDS for the 4 waves.  A fixed
-//                grid of workgroups strides over the items, whose count the
-//                permute kernel leaves on the device.  h [pos, 2I] float32 in
+//   gate/up:     grouped_stream_kernel over (tile, rows of w13) work items,
+//                the tile's xq rows gathered by token: h [pos, 2I] float32 in
 //                permuted order.
 //   silu:        one wave per permuted row: a = SiLU(gate) * up, quantised
 //                per 128 (aq, as) -- the decode GEMV's own function.
-//   down:        work items (tile, 64 rows of w2) the same way, the tile's aq
-//                rows staged in LDS.  y [pos, H] float32.
+//   down:        grouped_stream_kernel over (tile, rows of w2) work items on
+//                the tile's aq rows: y [pos, H] float32.
 //   unpermute:   out[t] = sum_k w[t,k] * y[pos[t,k]] (permute.hip).
 //
 // MFMA 16x16x128 e4m3 with the same operand roles as the decode GEMV:
@@ -22,11 +19,14 @@
 // scales multiply each 128-deep block result as weight_scale *
 // activation_scale, and the blocks are summed in the same order -- so every
 // (token, expert) row computed here is bit-identical to the decode GEMV's.
+#include <math.h>
+
+#include <type_traits>
+
 #include "common.hpp"
 #include "grouped.hpp"
 
 namespace moe {
-
 
 // --------------------------------------------------------------- quant x
 
@@ -66,169 +66,288 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restr
   }
 }
 
-// ------------------------------------------------------- work items
+
+// ---------------------------------------------------- streamed expert GEMM
 //
-// A tile is up to kTileTok consecutive rows (tokens) of one expert's segment
-// (listed by the permute kernel).  A work item is (tile, group of 64 weight
-// rows): 4 waves x 16 rows, every K-block of a wave's rows loaded at once
-// (all of the item's weight bytes in flight), the tile's activations staged
-// once in LDS for the 4 waves.  Two such workgroups fit on a CU, so one
-// streams weights while the other stages and computes.  Grids are a fixed number of workgroups that
-// stride over the items, whose count is read on the device.
+// One kernel computes both projections.  For the weight rows r of one expert
+// and the permuted rows pos of one of its tiles (up to 32 consecutive rows
+// of the expert's segment, listed by the permute kernel):
+//
+//   out[pos][r] = sum over K-blocks kb, in order, of
+//                 MFMA(w[e][r][kb], act[pos][kb]) * (w_scale[r/128][kb] * act_scale[pos][kb])
+//
+//   gate/up:  w = w13 (2I rows, K = H), act = xq gathered by token, out = h
+//   down:     w = w2  (H rows,  K = I), act = aq in permuted order,  out = y
+//
+// A work item is (tile, 64*GPW consecutive weight rows).  One workgroup of 4
+// waves takes one item; wave w owns GPW groups of 16 rows.  The wave's
+// (K-block, group) units, K-block-major, stream through a ring of 16
+// operand registers per lane: unit u+16 is loaded as soon as the MFMA of
+// unit u has read its slot, so 16 K-blocks (32 KiB per wave) stay in flight
+// from the item's first load to its last.  The tile's activation rows are
+// copied once into LDS by direct global->LDS loads, 16-byte units
+// XOR-swizzled by row against bank conflicts, together with their scales and
+// the item's weight scales; K beyond 16 blocks is staged 16 blocks at a time.
+// Items are dealt to the 8 XCDs in contiguous ranges, so the items of one
+// tile mostly share an L2.
 
-constexpr int kTileTok = 32;         // tokens per tile (two MFMA column tiles)
+constexpr int kTileTok = 32;          // permuted rows per tile (two MFMA column tiles)
 constexpr int kColTiles = kTileTok / 16;
-constexpr int kItemWaves = 4;        // 64 weight rows per work item
-constexpr int kKChunk = 16;          // K-blocks of 128 in flight per lane (2048 columns)
-constexpr int kKHalf = kKChunk / 2;  // K-blocks of activations staged at a time
-constexpr int kItemWGs = 1024;       // workgroups striding over the items (2 resident per CU)
-constexpr int kStagePad = 16;        // LDS row padding (bytes) against bank conflicts
-constexpr int kDownKChunk = 4;       // K-blocks per chunk in the down kernel (inter 512 = 1 chunk)
+constexpr int kWaves = 4;             // waves per workgroup
+constexpr int kRing = 16;             // K-block operands in flight per lane
+constexpr int kStageBlocks = 16;      // K-blocks of activations staged at a time
+constexpr int kStageRowBytes = kStageBlocks * 128;
+constexpr int kMaxGPW = 8;            // groups of 16 rows per wave
+constexpr int kMaxScaleRows = kMaxGPW / 2;   // 128-row weight-scale rows per item
+constexpr int kMinItems = 400;        // fewest work items worth a bigger GPW
 
-// (expert, first segment row, segment offset, rows in the tile) of a tile.
-struct TileInfo {
-  int32_t e = 0, m0 = 0, off = 0, ncols = 0;
-  __device__ __forceinline__ void load(const int32_t* tiles, const int32_t* offsets,
-                                       const int32_t* counts, int64_t tile) {
-    e = tiles[2 * tile];
-    m0 = tiles[2 * tile + 1];
-    off = offsets[e];
-    ncols = min(kTileTok, counts[e] - m0);
-  }
+// LDS of one workgroup: the activation tile first (the direct loads address
+// it from offset 0), then the scales and the tile's token rows.
+constexpr int kLdsAct = kTileTok * kStageRowBytes;
+constexpr int kLdsActScale = kLdsAct;
+constexpr int kLdsWScale = kLdsActScale + 4 * kTileTok * kStageBlocks;
+constexpr int kLdsTok = kLdsWScale + 4 * kMaxScaleRows * kStageBlocks;
+constexpr int kLdsBytes = kLdsTok + 4 * kTileTok;
+
+struct StreamArgs {
+  const uint8_t* act;      // activation rows, e4m3, G*128 bytes each
+  const float* act_s;      // their per-128 scales, G per row
+  const int32_t* sorted;   // gather only: permuted row -> token * top_k + k
+  const int32_t* counts;   // rows per expert
+  const int32_t* offsets;  // first permuted row per expert
+  const int32_t* tiles;    // (expert, first segment row) per tile
+  const int32_t* n_tiles;  // tile count, written by the permute kernel
+  const uint8_t* w;        // [E][rows][G*128] e4m3, expert stride w_es bytes
+  const float* ws;         // [E][rows/128][G] f32, expert stride s_es floats
+  float* out;              // [pairs][rows] f32, permuted order
+  int64_t w_es, s_es;
+  int32_t top_k, rows, G;
 };
 
-// Staging of an activation tile, rows [0, kTileTok) x 16-byte units
-// [0, UNITS), in two steps so that the loads can be issued early:
-// stage_load reads row r from src_row(r), stage_store writes it to LDS (or
-// zeros when row_live(r) is false).
-template <int UNITS>
-struct Stage {
-  static constexpr int kPer = kTileTok * UNITS / (64 * kItemWaves);
-  u32x4 v[kPer];
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-  template <typename SrcRow>
-  __device__ __forceinline__ void load(SrcRow src_row) {
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      const int i = threadIdx.x + u * 64 * kItemWaves;
-      v[u] = *reinterpret_cast<const u32x4*>(src_row(i / UNITS) + (i % UNITS) * 16);
-    }
-  }
-  template <int PITCH, typename Live>
-  __device__ __forceinline__ void store(uint8_t (*dst)[PITCH], Live row_live) const {
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      const int i = threadIdx.x + u * 64 * kItemWaves;
-      *reinterpret_cast<u32x4*>(&dst[i / UNITS][(i % UNITS) * 16]) =
-          row_live(i / UNITS) ? v[u] : u32x4{0u, 0u, 0u, 0u};
-    }
-  }
-};
+// 32-byte MFMA operand from two 16-byte units of LDS.
+__device__ __forceinline__ v8i lds_op32(const uint8_t* p0, const uint8_t* p1) {
+  const u32x4 lo = *reinterpret_cast<const u32x4*>(p0);
+  const u32x4 hi = *reinterpret_cast<const u32x4*>(p1);
+  return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+}
 
-// --------------------------------------------------------------- gate/up
+template <int RING, int GPW, bool GATHER>
+__global__ __launch_bounds__(64 * kWaves) void grouped_stream_kernel(StreamArgs A) {
+  static_assert(RING % GPW == 0 && RING <= kRing && GPW <= kMaxGPW, "ring slots per group");
+  constexpr int KPP = RING / GPW;                   // K-blocks per pass of the ring
+  __shared__ __align__(16) uint8_t smem[kLdsBytes];
+  uint8_t* xt = smem;
+  float* xst = reinterpret_cast<float*>(smem + kLdsActScale);
+  float* wsc = reinterpret_cast<float*>(smem + kLdsWScale);
+  int32_t* tok = reinterpret_cast<int32_t*>(smem + kLdsTok);
 
-// h[pos][r] for the 2I weight rows r and the tile's rows pos: exactly the
-// decode GEMV's per-row arithmetic (block results scaled weight-scale first,
-// summed with one fma per block in K order).
-__global__ __launch_bounds__(64 * kItemWaves) void grouped_gateup_kernel(
-    const uint8_t* __restrict__ xq, const float* __restrict__ xs,
-    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
-    const int32_t* __restrict__ sorted_pairs, const int32_t* __restrict__ tiles,
-    const int32_t* __restrict__ n_tiles, int32_t top_k, const uint8_t* __restrict__ w13,
-    const float* __restrict__ s13, int64_t w13_es, int64_t s13_es, int32_t hidden, int32_t inter,
-    float* __restrict__ h) {
-  __shared__ __align__(16) uint8_t xt[kTileTok][kKHalf * 128 + kStagePad];
-  __shared__ float xst[kTileTok][kKHalf];
-  __shared__ int32_t tok[kTileTok];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int q = lane >> 4;
   const int col = lane & 15;
-  const int G = hidden >> 7;
-  const int rows2 = 2 * inter;
-  const int groups = rows2 / (16 * kItemWaves);
-  const int64_t n_items = static_cast<int64_t>(*n_tiles) * groups;
-  // the tile entry of the next item is fetched while this one runs
-  TileInfo nxt;
-  if (blockIdx.x < n_items) nxt.load(tiles, offsets, counts, blockIdx.x / groups);
-  for (int64_t item = blockIdx.x; item < n_items; item += gridDim.x) {
-    const TileInfo cur = nxt;
-    if (item + gridDim.x < n_items) nxt.load(tiles, offsets, counts, (item + gridDim.x) / groups);
-    const int r0 = static_cast<int>(item % groups) * (16 * kItemWaves) + wave * 16;
-    const int32_t e = cur.e;
-    const int32_t m0 = cur.m0;
-    const int32_t off = cur.off;
-    const int32_t ncols = cur.ncols;
-    const int nct = (ncols + 15) >> 4;                 // column tiles in use
-    const uint8_t* wrow = w13 + static_cast<int64_t>(e) * w13_es +
-                          static_cast<int64_t>(r0 + col) * hidden + q * 32;
-    const float* srow = s13 + static_cast<int64_t>(e) * s13_es + static_cast<int64_t>(r0 >> 7) * G;
-    __syncthreads();                 // the previous item is done with tok / xt
-    if (threadIdx.x < kTileTok)
-      tok[threadIdx.x] =
-          threadIdx.x < ncols ? sorted_pairs[off + m0 + threadIdx.x] / top_k : -1;
-    v4f acc[kColTiles];
+  const int G = A.G;
+  const int64_t K = static_cast<int64_t>(G) * 128;
+
+  // item of this workgroup: XCD x = blockIdx % 8 takes items [x*n8, (x+1)*n8)
+  const int ipt = A.rows / (64 * GPW);
+  const int64_t n_items = static_cast<int64_t>(*A.n_tiles) * ipt;
+  const int64_t n8 = (n_items + 7) >> 3;
+  const int64_t slot8 = blockIdx.x >> 3;
+  const int64_t item = static_cast<int64_t>(blockIdx.x & 7) * n8 + slot8;
+  if (slot8 >= n8 || item >= n_items) return;      // whole workgroup
+  const int64_t tile = item / ipt;
+  const int32_t e = A.tiles[2 * tile];
+  const int32_t m0 = A.tiles[2 * tile + 1];
+  const int32_t seg = A.offsets[e] + m0;            // first permuted row of the tile
+  const int32_t ncols = min(kTileTok, A.counts[e] - m0);
+  const int nct = (ncols + 15) >> 4;                // column tiles in use
+  const int row0 = static_cast<int>(item % ipt) * (64 * GPW);
+  const int rw = row0 + wave * (16 * GPW);          // the wave's first row
+  const int sb0 = row0 >> 7;                        // the item's first scale row
+  const int nsb = ((row0 + 64 * GPW - 1) >> 7) - sb0 + 1;
+  const int Gs = min(G, kStageBlocks);              // K-blocks per staged row
+  const int upr = Gs * 8;                           // 16-byte units per staged row
+  const int swz = (Gs & 1) ? 7 : 15;                // unit XOR mask (within the row)
+
+  // token rows of the tile (gather form), issued before the weights
+  int32_t tokv = 0;
+  if (GATHER && threadIdx.x < kTileTok)
+    tokv = A.sorted[seg + min(static_cast<int>(threadIdx.x), ncols - 1)] / A.top_k;
+  __builtin_amdgcn_sched_barrier(0);
+
+  // fill the ring: unit s = (K-block s / GPW, group s % GPW)
+  const uint8_t* wl = A.w + static_cast<int64_t>(e) * A.w_es +
+                      static_cast<int64_t>(rw + col) * K + q * 32;
+  v8i a[RING];
 #pragma unroll
-    for (int m = 0; m < kColTiles; ++m) acc[m] = v4f{0.f, 0.f, 0.f, 0.f};
-    __syncthreads();                 // tok visible
-    for (int k0 = 0; k0 < G; k0 += kKChunk) {
-      // activations of the first half go out before the weights: loads
-      // retire in issue order, so they can be staged while the weights travel
-      Stage<kKHalf * 128 / 16> st;
-      auto src_row = [&](int kh) {
-        return [&, kh](int r) {
-          const int32_t tc = tok[r];
-          const int kb = kh * 128;
-          return xq + static_cast<int64_t>(tc >= 0 ? tc : 0) * hidden + (kb < hidden ? kb : 0);
-        };
-      };
-      st.load(src_row(k0));
-      v8i a[kKChunk];
+  for (int s = 0; s < RING; ++s) {
+    const int kb = min(s / GPW, G - 1);
+    a[s] = load_op32_nt(wl + static_cast<int64_t>(s % GPW) * 16 * K + kb * 128);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  if (GATHER && threadIdx.x < kTileTok) tok[threadIdx.x] = tokv;
+  __syncthreads();
+
+  auto act_row = [&](int r) -> int64_t {
+    const int rr = min(r, ncols - 1);
+    return GATHER ? static_cast<int64_t>(tok[rr]) : static_cast<int64_t>(seg + rr);
+  };
+  // K-blocks [16*ph, 16*ph + Gs) of the tile's rows [0, 16*nct) into LDS.
+  // Rows past ncols repeat the last row; their columns are never stored.
+  auto stage = [&](int ph) {
+    const int kb0 = ph * kStageBlocks;
+    const int nwin = 2 * nct * Gs;                  // 1 KiB windows, 16 bytes per lane
+    for (int win = wave; win < nwin; win += kWaves) {
+      const int U = win * 64 + lane;
+      const int r = U / upr;
+      const int c = (U - r * upr) ^ (r & swz);      // source unit of LDS unit U
+      const int kb = kb0 + (c >> 3);
+      const uint8_t* src = A.act + act_row(r) * K + (kb < G ? kb * 128 + (c & 7) * 16 : 0);
+      __builtin_amdgcn_global_load_lds(src, (lds_ptr_t)(xt + win * 1024), 16, 0, 0);
+    }
+    for (int i = threadIdx.x; i < 16 * nct * Gs; i += 64 * kWaves) {
+      const int kb = kb0 + i % Gs;
+      xst[i] = kb < G ? A.act_s[act_row(i / Gs) * G + kb] : 0.0f;
+    }
+    for (int i = threadIdx.x; i < nsb * Gs; i += 64 * kWaves) {
+      const int kb = kb0 + i % Gs;
+      wsc[i] = kb < G ? A.ws[static_cast<int64_t>(e) * A.s_es +
+                             static_cast<int64_t>(sb0 + i / Gs) * G + kb]
+                      : 0.0f;
+    }
+    __builtin_amdgcn_s_waitcnt(0);                  // this wave's direct loads landed
+    __syncthreads();
+  };
+  stage(0);
+
+  v4f acc[GPW][kColTiles];
 #pragma unroll
-      for (int c = 0; c < kKChunk; ++c) {
-        const int g = k0 + c < G ? k0 + c : G - 1;
-        a[c] = load_op32_nt(wrow + g * 128);
-      }
+  for (int j = 0; j < GPW; ++j)
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int kh = k0 + half * kKHalf;            // first K-block of this half
-        if (half > 0) {
-          __syncthreads();           // the first half's xt reads are done
-          st.load(src_row(kh));
-        } else if (k0 > 0) {
-          __syncthreads();           // the previous chunk's xt reads are done
+    for (int m = 0; m < kColTiles; ++m) acc[j][m] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // one pass: K-blocks [p*KPP, p*KPP + KPP) of every group; REFILL issues the
+  // loads of the next pass into the slots just read
+  auto pass = [&](int p, auto refill) {
+    const int kb0 = p * KPP;
+    if (kb0 > 0 && (kb0 & (kStageBlocks - 1)) == 0) {   // next 16 K-blocks (K > 2048)
+      __syncthreads();
+      stage(kb0 / kStageBlocks);
+    }
+#pragma unroll
+    for (int i = 0; i < KPP; ++i) {
+      const int kb = kb0 + i;
+      if (kb < G) {
+        const int kl = kb & (kStageBlocks - 1);
+        v8i b[kColTiles];
+        float as[kColTiles];
+#pragma unroll
+        for (int m = 0; m < kColTiles; ++m) {
+          if (m < nct) {
+            const int R = m * 16 + col;
+            const uint8_t* rowp = xt + R * (upr * 16);
+            const int c0 = kl * 8 + q * 2;
+            const int sw = R & swz;
+            b[m] = lds_op32(rowp + ((c0 ^ sw) << 4), rowp + (((c0 + 1) ^ sw) << 4));
+            as[m] = xst[R * Gs + kl];
+          }
         }
-        st.store(xt, [&](int r) { return tok[r] >= 0 && kh < G; });
-        for (int i = threadIdx.x; i < kTileTok * kKHalf; i += 64 * kItemWaves) {
-          const int cc = i / kKHalf, g = i % kKHalf;
-          const int32_t t2 = tok[cc];
-          xst[cc][g] = (t2 >= 0 && kh + g < G) ? xs[static_cast<int64_t>(t2) * G + kh + g] : 0.0f;
-        }
-        __syncthreads();
 #pragma unroll
-        for (int c = 0; c < kKHalf; ++c) {
-          if (kh + c < G) {
+        for (int j = 0; j < GPW; ++j) {
+          const float wsj = wsc[(((rw + 16 * j) >> 7) - sb0) * Gs + kl];
 #pragma unroll
-            for (int m = 0; m < kColTiles; ++m) {
-              if (m < nct) {
-                const v8i b = load_op32(&xt[m * 16 + col][c * 128 + q * 32]);
-                const v4f z = {0.f, 0.f, 0.f, 0.f};
-                const v4f d = mfma_e4m3_16x16x128(a[half * kKHalf + c], b, z);
-                const float sc = srow[kh + c] * xst[m * 16 + col][c];
-                block_fma(acc[m], d, sc);
-              }
+          for (int m = 0; m < kColTiles; ++m) {
+            if (m < nct) {
+              const v4f z = {0.f, 0.f, 0.f, 0.f};
+              const v4f d = mfma_e4m3_16x16x128(a[i * GPW + j], b[m], z);
+              block_fma(acc[j][m], d, wsj * as[m]);
             }
           }
         }
       }
+      if constexpr (decltype(refill)::value) {
+        const int kn = min(kb + KPP, G - 1);
+#pragma unroll
+        for (int j = 0; j < GPW; ++j)
+          a[i * GPW + j] = load_op32_nt(wl + static_cast<int64_t>(j) * 16 * K + kn * 128);
+      }
     }
+  };
+  const int npass = (G + KPP - 1) / KPP;
+  for (int p = 0; p + 1 < npass; ++p) pass(p, std::true_type{});
+  pass(npass - 1, std::false_type{});
+
+#pragma unroll
+  for (int j = 0; j < GPW; ++j)
 #pragma unroll
     for (int m = 0; m < kColTiles; ++m) {
       const int cc = m * 16 + col;
-      if (cc < ncols)
-        *reinterpret_cast<float4*>(h + static_cast<int64_t>(off + m0 + cc) * rows2 + r0 + 4 * q) =
-            make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
+      if (m < nct && cc < ncols)
+        *reinterpret_cast<float4*>(A.out + static_cast<int64_t>(seg + cc) * A.rows + rw + 16 * j +
+                                   4 * q) = make_float4(acc[j][m][0], acc[j][m][1], acc[j][m][2],
+                                                        acc[j][m][3]);
     }
+}
+
+// Work-item shapes, in increasing rows per item: (ring slots, groups of 16
+// rows per wave).  The last trades ring depth for rows so that the
+// accumulators of 8 groups fit beside the ring at 2 waves per SIMD.
+struct StreamShape {
+  int ring, gpw;
+};
+constexpr StreamShape kShapes[] = {{16, 1}, {16, 2}, {16, 4}, {8, 8}};
+constexpr int kNumShapes = sizeof(kShapes) / sizeof(kShapes[0]);
+
+// Resident workgroups of the streamed kernel (2 per CU).
+static int resident_slots() {
+  static int slots = 0;
+  if (slots == 0) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    slots = 2 * cus;
+  }
+  return slots;
+}
+
+// Shape for a projection of `rows` weight rows.  Bigger items amortise each
+// workgroup's start (tile look-up, staging, first loads), but items run in
+// rounds of the resident slots, and an item count just past a whole round
+// leaves most CUs idle in the last one.  So: the biggest shape whose item
+// count, at the expected tile count (distinct experts of P uniform picks,
+// plus partial tiles), is at least kMinItems and fills at least 80 % of its
+// last round.
+static int pick_shape(int64_t P, int32_t n_experts, int32_t rows) {
+  const double E = n_experts;
+  const double tiles = E * (1.0 - exp(-static_cast<double>(P) / E)) +
+                       static_cast<double>(P) / kTileTok;
+  const double slots = resident_slots();
+  int best = 0;
+  for (int i = 1; i < kNumShapes; ++i) {
+    const int g = kShapes[i].gpw;
+    if (rows % (64 * g) != 0) continue;
+    const double items = tiles * rows / (64.0 * g);
+    const double fill = items / (ceil(items / slots) * slots);
+    if (items >= kMinItems && fill >= 0.8) best = i;
+  }
+  return best;
+}
+
+template <bool GATHER>
+static void launch_stream(const StreamArgs& A, int shape, int64_t max_tiles, hipStream_t s) {
+  const int64_t items = max_tiles * (A.rows / (64 * kShapes[shape].gpw));
+  const dim3 grid(static_cast<unsigned>((items + 7) & ~int64_t{7}));
+  const dim3 block(64 * kWaves);
+  switch (shape) {
+    case 0: hipLaunchKernelGGL((grouped_stream_kernel<16, 1, GATHER>), grid, block, 0, s, A); break;
+    case 1: hipLaunchKernelGGL((grouped_stream_kernel<16, 2, GATHER>), grid, block, 0, s, A); break;
+    case 2: hipLaunchKernelGGL((grouped_stream_kernel<16, 4, GATHER>), grid, block, 0, s, A); break;
+    default: hipLaunchKernelGGL((grouped_stream_kernel<8, 8, GATHER>), grid, block, 0, s, A); break;
   }
 }
 
@@ -257,90 +376,6 @@ __global__ __launch_bounds__(512) void grouped_silu_kernel(const float* __restri
   }
 }
 
-// --------------------------------------------------------------- down
-
-// y[pos][c] for the H output rows c: w2 rows are the A operand, the tile's
-// aq rows (staged in LDS) the B operand.
-__global__ __launch_bounds__(64 * kItemWaves) void grouped_down_kernel(
-    const uint8_t* __restrict__ aq, const float* __restrict__ as_,
-    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
-    const int32_t* __restrict__ tiles, const int32_t* __restrict__ n_tiles,
-    const uint8_t* __restrict__ w2, const float* __restrict__ s2, int64_t w2_es, int64_t s2_es,
-    int32_t hidden, int32_t inter, float* __restrict__ y) {
-  __shared__ __align__(16) uint8_t at[kTileTok][kDownKChunk * 128 + kStagePad];
-  __shared__ float ast[kTileTok][kDownKChunk];
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int q = lane >> 4;
-  const int col = lane & 15;
-  const int Gi = inter >> 7;
-  const int groups = hidden / (16 * kItemWaves);
-  const int64_t n_items = static_cast<int64_t>(*n_tiles) * groups;
-  TileInfo nxt;
-  if (blockIdx.x < n_items) nxt.load(tiles, offsets, counts, blockIdx.x / groups);
-  for (int64_t item = blockIdx.x; item < n_items; item += gridDim.x) {
-    const TileInfo cur = nxt;
-    if (item + gridDim.x < n_items) nxt.load(tiles, offsets, counts, (item + gridDim.x) / groups);
-    const int c0 = static_cast<int>(item % groups) * (16 * kItemWaves) + wave * 16;
-    const int32_t e = cur.e;
-    const int32_t m0 = cur.m0;
-    const int32_t off = cur.off;
-    const int32_t ncols = cur.ncols;
-    const int nct = (ncols + 15) >> 4;
-    const uint8_t* wrow = w2 + static_cast<int64_t>(e) * w2_es +
-                          static_cast<int64_t>(c0 + col) * inter + q * 32;
-    const float* srow = s2 + static_cast<int64_t>(e) * s2_es + static_cast<int64_t>(c0 >> 7) * Gi;
-    v4f acc[kColTiles];
-#pragma unroll
-    for (int m = 0; m < kColTiles; ++m) acc[m] = v4f{0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < Gi; k0 += kDownKChunk) {
-      v8i a[kDownKChunk];
-#pragma unroll
-      for (int c = 0; c < kDownKChunk; ++c) {
-        const int g = k0 + c < Gi ? k0 + c : Gi - 1;
-        a[c] = load_op32_nt(wrow + g * 128);
-      }
-      __syncthreads();               // the previous item / chunk is done with at
-      {
-        Stage<kDownKChunk * 128 / 16> st;
-        st.load([&](int r) {
-          const int kb = k0 * 128;
-          return aq + static_cast<int64_t>(off + m0 + (r < ncols ? r : 0)) * inter +
-                 (kb < inter ? kb : 0);
-        });
-        st.store(at, [&](int r) { return r < ncols; });
-      }
-      for (int i = threadIdx.x; i < kTileTok * kDownKChunk; i += 64 * kItemWaves) {
-        const int cc = i / kDownKChunk, g = i % kDownKChunk;
-        ast[cc][g] = (cc < ncols && k0 + g < Gi)
-                         ? as_[static_cast<int64_t>(off + m0 + cc) * Gi + k0 + g] : 0.0f;
-      }
-      __syncthreads();
-#pragma unroll
-      for (int c = 0; c < kDownKChunk; ++c) {
-        if (k0 + c < Gi) {
-#pragma unroll
-          for (int m = 0; m < kColTiles; ++m) {
-            if (m < nct) {
-              const v8i b = load_op32(&at[m * 16 + col][c * 128 + q * 32]);
-              const v4f z = {0.f, 0.f, 0.f, 0.f};
-              const v4f d = mfma_e4m3_16x16x128(a[c], b, z);
-              const float sc = srow[k0 + c] * ast[m * 16 + col][c];
-              block_fma(acc[m], d, sc);
-            }
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int m = 0; m < kColTiles; ++m) {
-      const int cc = m * 16 + col;
-      if (cc < ncols)
-        *reinterpret_cast<float4*>(y + static_cast<int64_t>(off + m0 + cc) * hidden + c0 + 4 * q) =
-            make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
-    }
-  }
-}
 
 // --------------------------------------------------------------- driver
 
@@ -393,22 +428,24 @@ int launch_grouped(const uint16_t* x, const void* ids, int ids64, const void* we
   hipLaunchKernelGGL(quant_rows_kernel, dim3(tokens), dim3(256), 0, s, x, hidden, xq, xs);
   rc = check_launch("moe_fp8_moe_forward(quant)");
   if (rc) return rc;
-  const int64_t gu_items = max_tiles * ((2 * inter) / (16 * kItemWaves));
-  hipLaunchKernelGGL(grouped_gateup_kernel,
-                     dim3(static_cast<unsigned>(gu_items < kItemWGs ? gu_items : kItemWGs)),
-                     dim3(64 * kItemWaves), 0, s, xq, xs, counts, offsets, sorted, tiles, n_tiles,
-                     top_k, w13, s13, es.w13, es.s13, hidden, inter, h);
+  StreamArgs gu{};
+  gu.act = xq;  gu.act_s = xs;  gu.sorted = sorted;
+  gu.counts = counts;  gu.offsets = offsets;  gu.tiles = tiles;  gu.n_tiles = n_tiles;
+  gu.w = w13;  gu.ws = s13;  gu.out = h;  gu.w_es = es.w13;  gu.s_es = es.s13;
+  gu.top_k = top_k;  gu.rows = 2 * inter;  gu.G = hidden / 128;
+  launch_stream<true>(gu, pick_shape(P, n_experts, gu.rows), max_tiles, s);
   rc = check_launch("moe_fp8_moe_forward(grouped gate/up)");
   if (rc) return rc;
   hipLaunchKernelGGL(grouped_silu_kernel, dim3(static_cast<unsigned>((P + 7) / 8)), dim3(512), 0, s,
                      h, offsets, n_experts, inter, aq, as_);
   rc = check_launch("moe_fp8_moe_forward(grouped silu)");
   if (rc) return rc;
-  const int64_t dn_items = max_tiles * (hidden / (16 * kItemWaves));
-  hipLaunchKernelGGL(grouped_down_kernel,
-                     dim3(static_cast<unsigned>(dn_items < kItemWGs ? dn_items : kItemWGs)),
-                     dim3(64 * kItemWaves), 0, s, aq, as_, counts, offsets, tiles, n_tiles, w2, s2,
-                     es.w2, es.s2, hidden, inter, y);
+  StreamArgs dn{};
+  dn.act = aq;  dn.act_s = as_;  dn.sorted = nullptr;
+  dn.counts = counts;  dn.offsets = offsets;  dn.tiles = tiles;  dn.n_tiles = n_tiles;
+  dn.w = w2;  dn.ws = s2;  dn.out = y;  dn.w_es = es.w2;  dn.s_es = es.s2;
+  dn.top_k = top_k;  dn.rows = hidden;  dn.G = inter / 128;
+  launch_stream<false>(dn, pick_shape(P, n_experts, dn.rows), max_tiles, s);
   rc = check_launch("moe_fp8_moe_forward(grouped down)");
   if (rc) return rc;
   return launch_unpermute(y, pos, weights, wbf16, tokens, top_k, hidden, residual, out, s);

@@ -6,8 +6,8 @@
 //      the order they land in);
 //   2. block-wide exclusive scan -> offsets, and a cursor per expert;
 //   3. pairs are placed in rounds of 512 in pair order.  In a round, each
-//      wave ranks its lanes among the lanes with the same expert (ballot
-//      matching, one pass per distinct expert in the wave), the per-wave
+//      wave ranks its lanes among the lanes with the same expert (bit-sliced
+//      ballot matching, one ballot per bit of the id), the per-wave
 //      counts of an expert are packed as 7-bit fields of one 64-bit LDS word
 //      (8 waves x at most 64), so a lane's position is
 //        cursor[e] + (counts of e in earlier waves) + (rank in its wave)
@@ -24,6 +24,7 @@ constexpr int kPermMaxExperts = 4096;
 constexpr int kPermPer = kPermMaxExperts / kPermThreads;
 constexpr int kPlaceThreads = 512;     // permute: 8 waves, 7-bit count fields in a uint64
 constexpr int kPlacePer = kPermMaxExperts / kPlaceThreads;
+constexpr int kHoldRounds = 8;         // placement rounds whose ids stay in registers
 
 __device__ __forceinline__ int32_t read_id(const void* ids, int ids64, int64_t p) {
   return ids64 ? static_cast<int32_t>(reinterpret_cast<const int64_t*>(ids)[p])
@@ -60,6 +61,22 @@ __device__ int32_t block_exclusive_scan(int32_t v, int32_t* scratch, int32_t* ou
   return total;
 }
 
+// Stable rank of a lane among the lanes of its wave holding the same expert
+// e (e < 0: none), and the number of such lanes.  The match mask is the AND,
+// over the bits of the id, of the ballot of that bit or of its complement:
+// one ballot per id bit rather than one pass per distinct expert.
+__device__ __forceinline__ void wave_match_rank(int32_t e, int nbits, uint64_t below_lane,
+                                                int& rank, int& count) {
+  uint64_t m = __ballot(e >= 0);
+  for (int b = 0; b < nbits; ++b) {
+    const bool bit = (e >> b) & 1;
+    const uint64_t bb = __ballot(bit);
+    m &= bit ? bb : ~bb;
+  }
+  rank = __popcll(m & below_lane);
+  count = __popcll(m);
+}
+
 __global__ __launch_bounds__(kPlaceThreads) void permute_kernel(
     const void* __restrict__ ids, int ids64, int64_t P, int32_t n_experts,
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ sorted_pairs,
@@ -70,12 +87,29 @@ __global__ __launch_bounds__(kPlaceThreads) void permute_kernel(
   __shared__ int32_t scratch[40];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
+  // ids of the first kHoldRounds rounds, read once with all loads in flight
+  // (-1: id out of range, -2: past the last pair)
+  int32_t held[kHoldRounds];
+#pragma unroll
+  for (int r = 0; r < kHoldRounds; ++r) held[r] = -2;
+  if (P > 0) {
+#pragma unroll
+    for (int r = 0; r < kHoldRounds; ++r) {
+      const int64_t p = static_cast<int64_t>(r) * kPlaceThreads + tid;
+      const int32_t e = read_id(ids, ids64, p < P ? p : P - 1);
+      held[r] = p < P ? ((e >= 0 && e < n_experts) ? e : -1) : -2;
+    }
+  }
   for (int e = tid; e < n_experts; e += kPlaceThreads) {
     cursor[e] = 0;
     fields[e] = 0;
   }
   __syncthreads();
-  for (int64_t p = tid; p < P; p += kPlaceThreads) {
+#pragma unroll
+  for (int r = 0; r < kHoldRounds; ++r)
+    if (held[r] >= 0) atomicAdd(&cursor[held[r]], 1);
+  for (int64_t p = static_cast<int64_t>(kHoldRounds) * kPlaceThreads + tid; p < P;
+       p += kPlaceThreads) {
     const int32_t e = read_id(ids, ids64, p);
     if (e >= 0 && e < n_experts) atomicAdd(&cursor[e], 1);
   }
@@ -127,30 +161,14 @@ __global__ __launch_bounds__(kPlaceThreads) void permute_kernel(
   }
   __syncthreads();
   const uint64_t below_lane = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int64_t r0 = 0; r0 < P; r0 += kPlaceThreads) {
+  const int nbits = n_experts > 1 ? 32 - __clz(n_experts - 1) : 0;
+  // one round: pairs r0 + [0, 512), e the (held) expert code of pair r0 + tid
+  auto place = [&](int64_t r0, int32_t e) {
     const int64_t p = r0 + tid;
-    int32_t e = -1;
-    if (p < P) {
-      e = read_id(ids, ids64, p);
-      if (e < 0 || e >= n_experts) {
-        pair_pos[p] = -1;          // no such expert: no position
-        e = -1;
-      }
-    }
-    // rank among the lanes of this wave with the same expert
-    int rank = 0, wcount = 0;
-    uint64_t todo = __ballot(e >= 0);
-    while (todo) {
-      const int leader = __builtin_ctzll(todo);
-      const int32_t el = __shfl(e, leader, 64);
-      const uint64_t m = __ballot(e == el);
-      if (e == el) {
-        rank = __popcll(m & below_lane);
-        wcount = __popcll(m);
-      }
-      todo &= ~m;
-    }
-    const bool first = e >= 0 && rank == 0;     // one lane per (wave, expert)
+    if (e == -1) pair_pos[p] = -1;             // no such expert: no position
+    int rank, wcount;
+    wave_match_rank(e, nbits, below_lane, rank, wcount);
+    const bool first = e >= 0 && rank == 0;    // one lane per (wave, expert)
     if (first) atomicAdd(reinterpret_cast<unsigned long long*>(&fields[e]),
                          static_cast<unsigned long long>(wcount) << (7 * wave));
     __syncthreads();
@@ -173,6 +191,19 @@ __global__ __launch_bounds__(kPlaceThreads) void permute_kernel(
       fields[e] = 0;
     }
     __syncthreads();
+  };
+  const int64_t n_rounds = (P + kPlaceThreads - 1) / kPlaceThreads;
+#pragma unroll
+  for (int r = 0; r < kHoldRounds; ++r)
+    if (r < n_rounds) place(static_cast<int64_t>(r) * kPlaceThreads, held[r]);
+  for (int64_t r = kHoldRounds; r < n_rounds; ++r) {
+    const int64_t p = r * kPlaceThreads + tid;
+    int32_t e = -2;
+    if (p < P) {
+      e = read_id(ids, ids64, p);
+      if (e < 0 || e >= n_experts) e = -1;
+    }
+    place(r * kPlaceThreads, e);
   }
 }
 
