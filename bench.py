@@ -422,7 +422,7 @@ def fill_pool_bytes(pool, dev, seed: int, chunk: int = 64) -> None:
 
 
 def run_probe(args) -> int:
-    """--probe gemv|fetch: the named kernel alone, many launches, one JSON line."""
+    """--probe gemv|fetch|copy|grouped: the named kernel(s) alone, many launches, one JSON line."""
     import torch
     import hipfetch
     from hostpool import DRAMA3, HostPool
@@ -443,6 +443,28 @@ def run_probe(args) -> int:
                "bytes_per_launch": nbytes, "GBps": round(nbytes / dt / 1e9, 3)}
         for p in pools:
             p.close()
+    elif args.probe == "grouped":
+        # the grouped W8A8 FFN alone (permute .. unpermute) on 256 resident
+        # records, uniform top-8 routing of --tokens tokens
+        E, K, T = 256, 8, args.tokens
+        rec = resident_records(dev, E, DRAMA3)
+        w13, s13, w2, s2 = DRAMA3.views(rec)
+        g = torch.Generator(device="cpu").manual_seed(11)
+        ids = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)])
+        ids = ids.to(torch.int32).to(dev)
+        wts = torch.softmax(torch.randn((T, K), generator=g), dim=-1).to(dev)
+        x = torch.randn((T, DRAMA3.hidden), generator=g).to(torch.bfloat16).to(dev)
+        out = torch.empty_like(x)
+        ws = torch.empty(lib.fp8_moe_workspace(T, K, E, DRAMA3.hidden, DRAMA3.inter),
+                         dtype=torch.uint8, device=dev)
+        dt = graph_time(dev, lambda r: lib.fp8_moe_forward(x, ids, wts, w13, s13, w2, s2, out, ws,
+                                                          mode=2), args.steps)
+        distinct = int(torch.unique(ids).numel())
+        nbytes = distinct * DRAMA3.record_bytes
+        res = {"probe": "grouped", "what": f"grouped FFN, {T} tokens x top-{K} uniform over {E} "
+               "resident records, graph of back-to-back calls", "tokens": T,
+               "distinct_experts": distinct, "us_per_call": round(1e6 * dt, 2),
+               "expert_bytes_per_call": nbytes, "GBps": round(nbytes / dt / 1e9, 1)}
     elif args.probe == "copy":
         # a plain elementwise copy of known size: reads and writes 256 MiB,
         # the calibration for the HBM traffic counters
@@ -519,7 +541,8 @@ def main() -> int:
     ap.add_argument("--noncoherent-pool", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the prefill and all-resident measurements")
-    ap.add_argument("--probe", choices=["gemv", "fetch", "copy"],
+    ap.add_argument("--tokens", type=int, default=512, help="tokens per call of --probe grouped")
+    ap.add_argument("--probe", choices=["gemv", "fetch", "copy", "grouped"],
                     help="time one kernel alone (--steps launches) instead of the decode step")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
