@@ -132,3 +132,40 @@ def test_grouped_packed_record_views(lib, dev):
     b = _fwd(x, ids, w, devt, mode=2)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("H,I,T,E,K", [(4096, 384, 40, 8, 4), (2560, 256, 70, 6, 3),
+                                       (4096, 512, 512, 64, 8)])
+def test_grouped_long_rows_equal_gemv(lib, dev, H, I, T, E, K):
+    """Hidden sizes above 2048 (gate/up activations staged 16 K-blocks at a
+    time: 2 stages at 4096, 16 + 4 blocks at 2560) and odd K-block counts of
+    the down projection (inter 384 = 3 blocks).  The last case is large
+    enough for the host to pick the 512-row down items and 128-row gate/up
+    items."""
+    import synth
+    _, devt = _experts(H + I, E, H, I, dev)
+    x = synth.hidden_states(H + T, T, H).to(dev)
+    ids, w = _routing(T, E, K, H + E, dev)
+    say(f"grouped long rows: H={H} I={I} T={T} E={E} K={K}")
+    a = _fwd(x, ids, w, devt, mode=1)
+    b = _fwd(x, ids, w, devt, mode=2)
+    torch.cuda.synchronize()
+    assert torch.isfinite(b.float()).all()
+    if not torch.equal(a, b):
+        d = (a.float() - b.float()).abs()
+        pytest.fail(f"grouped != GEMV: {int((d > 0).sum())} elements differ, max {float(d.max())}")
+
+
+def test_grouped_long_rows_match_oracle(lib, dev):
+    import synth
+    T, E, H, I, K = 6, 5, 4096, 384, 4
+    host, devt = _experts(77, E, H, I, dev)
+    x = synth.hidden_states(77, T, H).to(dev)
+    ids, w = _routing(T, E, K, 77, dev)
+    got = _fwd(x, ids, w, devt, mode=2)
+    torch.cuda.synchronize()
+    want = omoe.forward_w8a8(x.float().cpu().numpy(), ids.cpu().numpy(),
+                             w.cpu().numpy().astype(np.float64), *(t.numpy() for t in host))
+    err = omoe.max_rel_err(got.float().cpu().numpy(), want)
+    print(f"grouped (H={H}, I={I}) max rel err vs W8A8 oracle {err:.2e}")
+    assert err <= TOL
