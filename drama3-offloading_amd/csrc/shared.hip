@@ -1,0 +1,234 @@
+// Shared expert of the MoE block (bf16, dense, every token) and the decode
+// step's finiteness guard.
+//
+// The MoE block's output with a gated shared expert, in the bf16 op order of
+// the model's own modules (every Linear rounds its f32 sum to bf16, every
+// elementwise op rounds its f32 result to bf16):
+//
+//   g, u  = x W_gate^T, x W_up^T                  [T, Is]
+//   a     = bf16(silu(g)) * u                      [T, Is]
+//   d     = a W_down^T                             [T, H]
+//   s     = bf16(sigmoid(x w_sg^T))                [T, 1]
+//   out   = residual + (routed + s * d)            [T, H]
+//
+// moe_shared_gate_up computes a and s (one wave per intermediate row j,
+// holding the gate and up rows of j; one extra wave for the sigmoid gate
+// row), moe_shared_down the rest (4 output rows per wave) with the routed
+// output and the residual added in its epilogue.  Both are GEMVs over
+// weights read once per 4 tokens: HBM-bound at decode (6 MiB per layer at
+// H = 2048, Is = 512).  Sums are f32 fused multiply-adds over each lane's
+// 16-byte slices in row order, then a butterfly over the 64 lanes.
+#include "common.hpp"
+
+namespace moe {
+
+constexpr int kSharedTB = 4;   // tokens per pass over the weights
+
+__device__ __forceinline__ u32x4 load16(const uint16_t* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+// acc + sum of the 8 bf16 products of two 16-byte slices, one fma each in order.
+__device__ __forceinline__ float dot8_bf16(u32x4 w, u32x4 x, float acc) {
+  const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+  const uint32_t xv[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc = fmaf(__uint_as_float(wv[i] << 16), __uint_as_float(xv[i] << 16), acc);
+    acc = fmaf(__uint_as_float(wv[i] & 0xffff0000u), __uint_as_float(xv[i] & 0xffff0000u), acc);
+  }
+  return acc;
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// bf16 rounding of an f32 value, returned as f32.
+__device__ __forceinline__ float rbf16(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+__global__ __launch_bounds__(256) void shared_gate_up_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg, const uint16_t* __restrict__ wu,
+    const uint16_t* __restrict__ wsg, int32_t tokens, int32_t hidden, int32_t inter,
+    uint16_t* __restrict__ act, float* __restrict__ sig) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int j = blockIdx.x * 4 + wave;           // j == inter: the sigmoid gate row
+  if (j > inter) return;                         // no barriers below
+  const bool gate_row = j == inter;
+  const uint16_t* ra = gate_row ? wsg : wg + static_cast<int64_t>(j) * hidden;
+  const uint16_t* rb = gate_row ? wsg : wu + static_cast<int64_t>(j) * hidden;
+  const int nch = hidden >> 3;                    // 16-byte slices per row
+  for (int t0 = 0; t0 < tokens; t0 += kSharedTB) {
+    float aa[kSharedTB], ab[kSharedTB];
+#pragma unroll
+    for (int t = 0; t < kSharedTB; ++t) aa[t] = ab[t] = 0.0f;
+    for (int c = lane; c < nch; c += 64) {
+      const u32x4 va = load16(ra + c * 8);
+      const u32x4 vb = load16(rb + c * 8);
+#pragma unroll
+      for (int t = 0; t < kSharedTB; ++t) {
+        const int tt = min(t0 + t, tokens - 1);
+        const u32x4 xv = load16(x + static_cast<int64_t>(tt) * hidden + c * 8);
+        aa[t] = dot8_bf16(va, xv, aa[t]);
+        ab[t] = dot8_bf16(vb, xv, ab[t]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < kSharedTB; ++t) {
+      aa[t] = wave_sum_f32(aa[t]);
+      ab[t] = wave_sum_f32(ab[t]);
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int t = 0; t < kSharedTB; ++t) {
+        if (t0 + t >= tokens) break;
+        if (gate_row) {
+          const float z = rbf16(aa[t]);
+          sig[t0 + t] = rbf16(1.0f / (1.0f + expf(-z)));
+        } else {
+          const float g = rbf16(aa[t]);
+          const float u = rbf16(ab[t]);
+          const float s = rbf16(g / (1.0f + expf(-g)));
+          act[static_cast<int64_t>(t0 + t) * inter + j] = f32_to_bf16(s * u);
+        }
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void shared_down_kernel(
+    const uint16_t* __restrict__ act, const float* __restrict__ sig,
+    const uint16_t* __restrict__ wd, int32_t tokens, int32_t hidden, int32_t inter,
+    const uint16_t* __restrict__ routed, const uint16_t* __restrict__ residual,
+    uint16_t* __restrict__ out) {
+  constexpr int kRows = 4;                        // output rows per wave
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r0 = (blockIdx.x * 4 + wave) * kRows;
+  if (r0 >= hidden) return;                       // hidden % 16 == 0: all kRows rows exist
+  const int nch = inter >> 3;
+  for (int t0 = 0; t0 < tokens; t0 += kSharedTB) {
+    float acc[kRows][kSharedTB];
+#pragma unroll
+    for (int i = 0; i < kRows; ++i)
+#pragma unroll
+      for (int t = 0; t < kSharedTB; ++t) acc[i][t] = 0.0f;
+    for (int c = lane; c < nch; c += 64) {
+      u32x4 w[kRows];
+#pragma unroll
+      for (int i = 0; i < kRows; ++i) w[i] = load16(wd + static_cast<int64_t>(r0 + i) * inter + c * 8);
+#pragma unroll
+      for (int t = 0; t < kSharedTB; ++t) {
+        const int tt = min(t0 + t, tokens - 1);
+        const u32x4 av = load16(act + static_cast<int64_t>(tt) * inter + c * 8);
+#pragma unroll
+        for (int i = 0; i < kRows; ++i) acc[i][t] = dot8_bf16(w[i], av, acc[i][t]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kRows; ++i)
+#pragma unroll
+      for (int t = 0; t < kSharedTB; ++t) acc[i][t] = wave_sum_f32(acc[i][t]);
+    // lane i * kSharedTB + t finishes (row r0 + i, token t0 + t)
+#pragma unroll
+    for (int i = 0; i < kRows; ++i)
+#pragma unroll
+      for (int t = 0; t < kSharedTB; ++t) {
+        if (lane != i * kSharedTB + t || t0 + t >= tokens) continue;
+        const int64_t o = static_cast<int64_t>(t0 + t) * hidden + r0 + i;
+        const float d = rbf16(acc[i][t]);
+        float v = rbf16(sig[t0 + t] * d);
+        if (routed) v = rbf16(bf16_to_f32(routed[o]) + v);
+        if (residual) v = rbf16(bf16_to_f32(residual[o]) + v);
+        out[o] = f32_to_bf16(v);
+      }
+  }
+}
+
+// flag = 1 when every element of x is finite, else 0.  One workgroup, so the
+// flag is written exactly once and needs no clearing before (a graph replays
+// it as is).
+__global__ __launch_bounds__(1024) void all_finite_kernel(const void* __restrict__ x, int f32,
+                                                          int64_t n, int32_t* __restrict__ flag) {
+  bool ok = true;
+  const int64_t nbytes = n * (f32 ? 4 : 2);
+  const int64_t nvec = nbytes >> 4;               // whole 16-byte units
+  const u32x4* v = reinterpret_cast<const u32x4*>(x);
+  for (int64_t i = threadIdx.x; i < nvec; i += blockDim.x) {
+    const u32x4 u = v[i];
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      // all exponent bits set: Inf or NaN (f32: one value per word, bf16: two)
+      ok = ok && (w[k] & 0x7f800000u) != 0x7f800000u && (f32 || (w[k] & 0x7f80u) != 0x7f80u);
+    }
+  }
+  // the tail past the last whole unit, one element per thread
+  const int64_t done = (nvec << 4) / (f32 ? 4 : 2);
+  for (int64_t i = done + threadIdx.x; i < n; i += blockDim.x) {
+    if (f32) {
+      ok = ok && (reinterpret_cast<const uint32_t*>(x)[i] & 0x7f800000u) != 0x7f800000u;
+    } else {
+      ok = ok && (reinterpret_cast<const uint16_t*>(x)[i] & 0x7f80u) != 0x7f80u;
+    }
+  }
+  const int all = __syncthreads_and(ok ? 1 : 0);
+  if (threadIdx.x == 0) *flag = all ? 1 : 0;
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" int moe_shared_gate_up(const void* x, const void* w_gate, const void* w_up,
+                                  const void* w_sgate, int32_t tokens, int32_t hidden,
+                                  int32_t inter, void* act, float* sig, void* stream) {
+  MOE_REQUIRE(tokens >= 0, "moe_shared_gate_up: tokens < 0");
+  MOE_REQUIRE(hidden >= 128 && hidden % 128 == 0 && inter >= 128 && inter % 128 == 0,
+              "moe_shared_gate_up: hidden and inter must be positive multiples of 128");
+  if (tokens == 0) return MOE_OK;
+  MOE_REQUIRE(x && w_gate && w_up && w_sgate && act && sig, "moe_shared_gate_up: NULL pointer");
+  MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(w_gate) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(w_up) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(w_sgate) % 16 == 0,
+              "moe_shared_gate_up: x and weights must be 16-byte aligned");
+  const unsigned grid = static_cast<unsigned>((inter + 1 + 3) / 4);
+  hipLaunchKernelGGL(shared_gate_up_kernel, dim3(grid), dim3(256), 0, as_stream(stream),
+                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w_gate),
+                     static_cast<const uint16_t*>(w_up), static_cast<const uint16_t*>(w_sgate),
+                     tokens, hidden, inter, static_cast<uint16_t*>(act), sig);
+  return check_launch("moe_shared_gate_up");
+}
+
+extern "C" int moe_shared_down(const void* act, const float* sig, const void* w_down,
+                               int32_t tokens, int32_t hidden, int32_t inter, const void* routed,
+                               const void* residual, void* out, void* stream) {
+  MOE_REQUIRE(tokens >= 0, "moe_shared_down: tokens < 0");
+  MOE_REQUIRE(hidden >= 128 && hidden % 128 == 0 && inter >= 128 && inter % 128 == 0,
+              "moe_shared_down: hidden and inter must be positive multiples of 128");
+  if (tokens == 0) return MOE_OK;
+  MOE_REQUIRE(act && sig && w_down && out, "moe_shared_down: NULL pointer");
+  MOE_REQUIRE(reinterpret_cast<uintptr_t>(act) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(w_down) % 16 == 0,
+              "moe_shared_down: act and w_down must be 16-byte aligned");
+  const unsigned grid = static_cast<unsigned>(hidden / 16);
+  hipLaunchKernelGGL(shared_down_kernel, dim3(grid), dim3(256), 0, as_stream(stream),
+                     static_cast<const uint16_t*>(act), sig, static_cast<const uint16_t*>(w_down),
+                     tokens, hidden, inter, static_cast<const uint16_t*>(routed),
+                     static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out));
+  return check_launch("moe_shared_down");
+}
+
+extern "C" int moe_all_finite(const void* x, int32_t dtype, int64_t n, int32_t* flag,
+                              void* stream) {
+  MOE_REQUIRE(dtype == MOE_F32 || dtype == MOE_BF16, "moe_all_finite: dtype must be F32 or BF16");
+  MOE_REQUIRE(n >= 0 && flag, "moe_all_finite: need n >= 0 and a flag");
+  MOE_REQUIRE(n == 0 || x, "moe_all_finite: NULL x");
+  MOE_REQUIRE(n == 0 || reinterpret_cast<uintptr_t>(x) % 16 == 0,
+              "moe_all_finite: x must be 16-byte aligned");
+  hipLaunchKernelGGL(all_finite_kernel, dim3(1), dim3(1024), 0, as_stream(stream), x,
+                     dtype == MOE_F32 ? 1 : 0, n, flag);
+  return check_launch("moe_all_finite");
+}

@@ -67,6 +67,9 @@ SIGNATURES = {
     "moe_unique_inverse": (C.c_int, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "moe_gather_plan": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                   _vp]),
+    "moe_shared_gate_up": (C.c_int, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp]),
+    "moe_shared_down": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
+    "moe_all_finite": (C.c_int, [_vp, _i32, _i64, _vp, _vp]),
 }
 
 
@@ -229,6 +232,38 @@ class Native:
             host_expert.data_ptr(), host_dst.data_ptr(), n_host.data_ptr(), cache_src.data_ptr(),
             cache_dst.data_ptr(), n_cache.data_ptr(), self._ptr(stats), self.stream()),
             "moe_gather_plan")
+
+    def shared_gate_up(self, x, w_gate, w_up, w_sgate, act, sig) -> None:
+        """Shared expert, first half: act [T, Is] bf16 and the sigmoid gate
+        sig [T] f32 from x [T, H] bf16 (weights bf16, row-major)."""
+        T, H = x.shape
+        Is = w_gate.shape[0]
+        if w_gate.shape != (Is, H) or w_up.shape != (Is, H) or w_sgate.numel() != H:
+            raise ValueError("shared expert weights do not match x")
+        if act.shape != (T, Is) or sig.numel() < T:
+            raise ValueError("shared expert scratch too small")
+        self._check(self.cdll.moe_shared_gate_up(
+            x.data_ptr(), w_gate.data_ptr(), w_up.data_ptr(), w_sgate.data_ptr(), T, H, Is,
+            act.data_ptr(), sig.data_ptr(), self.stream()), "moe_shared_gate_up")
+
+    def shared_down(self, act, sig, w_down, out, routed=None, residual=None) -> None:
+        """Shared expert, second half: out = residual + (routed + sig * act W_down^T),
+        each term rounded to bf16 (routed / residual optional)."""
+        T, Is = act.shape
+        H = w_down.shape[0]
+        if w_down.shape != (H, Is) or out.shape != (T, H):
+            raise ValueError("shared expert down weights do not match")
+        for t in (routed, residual):
+            if t is not None and t.shape != (T, H):
+                raise ValueError("routed / residual must be [T, H]")
+        self._check(self.cdll.moe_shared_down(
+            act.data_ptr(), sig.data_ptr(), w_down.data_ptr(), T, H, Is, self._ptr(routed),
+            self._ptr(residual), out.data_ptr(), self.stream()), "moe_shared_down")
+
+    def all_finite(self, x, flag) -> None:
+        """flag[0] (int32, device) = 1 if every element of x (f32 or bf16) is finite."""
+        self._check(self.cdll.moe_all_finite(x.data_ptr(), self._dtype_code(x), x.numel(),
+                                             flag.data_ptr(), self.stream()), "moe_all_finite")
 
     def unpermute(self, y, pair_pos, weights, out) -> None:
         T, K = weights.shape

@@ -256,6 +256,43 @@ int moe_gather_plan(const int32_t* uniq, const int32_t* n_unique,
                     int32_t* cache_src, int32_t* cache_dst, int32_t* n_cache,
                     int64_t* stats, void* stream);
 
+/* Shared expert of the MoE block, first half.  The model gates a dense bf16
+ * expert that every token passes through with a sigmoid and adds it to the
+ * routed experts' output (notes/drama3-config.json:215-216
+ * shared_expert_gate, shared_expert_intermediate_size 512;
+ * notes/01-static-findings.md:80-82; checkpoint tensors
+ * layers.N.mlp.shared_expert.{gate,up,down}_proj.weight and
+ * layers.N.mlp.shared_expert_gate.weight [1, H], bf16).  The module itself
+ * is upstream's and not in the reference; this is its conventional form.
+ *   x [tokens, hidden], w_gate / w_up [inter, hidden], w_sgate [hidden]: bf16
+ *   act [tokens, inter] bf16 = bf16(silu(bf16(x w_gate^T))) * bf16(x w_up^T)
+ *   sig [tokens] f32 = bf16(sigmoid(bf16(x w_sgate^T)))  (bf16 values)
+ * Each product rounds to bf16 as the model's bf16 modules do.  hidden and
+ * inter positive multiples of 128; x and weights 16-byte aligned. */
+int moe_shared_gate_up(const void* x, const void* w_gate, const void* w_up,
+                       const void* w_sgate, int32_t tokens, int32_t hidden,
+                       int32_t inter, void* act, float* sig, void* stream);
+
+/* Shared expert, second half, and the block's sums:
+ *   d   = bf16(act w_down^T)                 w_down [hidden, inter] bf16
+ *   v   = bf16(sig * d)
+ *   v   = bf16(routed + v)      if routed   (the routed experts' bf16 output)
+ *   out = bf16(residual + v)    if residual
+ * out [tokens, hidden] bf16 may alias routed or residual. */
+int moe_shared_down(const void* act, const float* sig, const void* w_down,
+                    int32_t tokens, int32_t hidden, int32_t inter,
+                    const void* routed, const void* residual, void* out,
+                    void* stream);
+
+/* Decode-step finiteness guard: *flag = 1 if every one of the n elements of
+ * x (dtype MOE_F32 or MOE_BF16, 16-byte aligned) is finite, else 0; the
+ * device-side counterpart of the decode graph's
+ * `finite.copy_(torch.isfinite(logits).all())` (generate.py:376-377 as
+ * quoted in notes/botnotes/lm-head-inf-sentinel.md:18-28).  One workgroup
+ * writes the flag, so nothing has to be cleared before a graph replay. */
+int moe_all_finite(const void* x, int32_t dtype, int64_t n, int32_t* flag,
+                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif
