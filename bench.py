@@ -422,7 +422,7 @@ def fill_pool_bytes(pool, dev, seed: int, chunk: int = 64) -> None:
 
 
 def run_probe(args) -> int:
-    """--probe gemv|fetch|copy|grouped: the named kernel(s) alone, many launches, one JSON line."""
+    """--probe gemv|fetch|copy|grouped|shared: the named kernel(s) alone, many launches, one JSON line."""
     import torch
     import hipfetch
     from hostpool import DRAMA3, HostPool
@@ -465,6 +465,12 @@ def run_probe(args) -> int:
                "resident records, graph of back-to-back calls", "tokens": T,
                "distinct_experts": distinct, "us_per_call": round(1e6 * dt, 2),
                "expert_bytes_per_call": nbytes, "GBps": round(nbytes / dt / 1e9, 1)}
+    elif args.probe == "shared":
+        dt, nbytes = shared_resident(lib, dev, shared_weights(dev, 40, DRAMA3.hidden, 512),
+                                     calls=args.steps)
+        res = {"probe": "shared", "what": "shared expert gate/up + down, 1 token, graph of "
+               "back-to-back calls over 40 layers' bf16 weights", "us_per_call": round(1e6 * dt, 3),
+               "bytes_per_call": nbytes, "GBps": round(nbytes / dt / 1e9, 1)}
     elif args.probe == "copy":
         # a plain elementwise copy of known size: reads and writes 256 MiB,
         # the calibration for the HBM traffic counters
@@ -486,6 +492,70 @@ def run_probe(args) -> int:
         raise SystemExit(f"unknown probe {args.probe!r}")
     print(json.dumps(res), flush=True)
     return 0
+
+
+def shared_weights(dev, layers: int, hidden: int, inter: int, seed: int = 5):
+    """Seeded bf16 shared experts for every layer: (gate, up, down, sigmoid gate)."""
+    import torch
+    g = torch.Generator(device=dev).manual_seed(seed)
+    rnd = lambda *s, std: (torch.randn(s, generator=g, device=dev) * std).to(torch.bfloat16)
+    return (rnd(layers, inter, hidden, std=0.02), rnd(layers, inter, hidden, std=0.02),
+            rnd(layers, hidden, inter, std=0.005), rnd(layers, hidden, std=0.02))
+
+
+def shared_resident(lib, dev, weights, calls: int = 200):
+    """Seconds per shared-expert call (gate/up + down, 1 token) rotating over
+    the layers' weights in a graph, and its algorithmic HBM bytes."""
+    import torch
+    wg, wu, wd, wsg = weights
+    L, Is, H = wg.shape
+    x = torch.randn((1, H), device=dev).to(torch.bfloat16)
+    act = torch.empty((1, Is), dtype=torch.bfloat16, device=dev)
+    sig = torch.empty(1, dtype=torch.float32, device=dev)
+    out = torch.empty((1, H), dtype=torch.bfloat16, device=dev)
+
+    def body(r):
+        lib.shared_gate_up(x, wg[r % L], wu[r % L], wsg[r % L], act, sig)
+        lib.shared_down(act, sig, wd[r % L], out, routed=x, residual=x)
+    dt = graph_time(dev, body, calls)
+    return dt, 2 * (3 * Is * H + H)
+
+
+def moe_block_bench(lib, cfg, pools, dev, steps: int, warmup: int):
+    """The decode step with the full MoE block: routed experts through the
+    cache plus the gated shared expert on a second stream, and the
+    finiteness guard, in one hipGraph (same schedule and cache size as the
+    headline step)."""
+    import torch
+    import decode
+    cfgb = decode.DecodeConfig(**{**cfg.__dict__, "shared_expert": True})
+    hb = decode.DecodeHarness(cfgb, dev, pools=pools)
+    hb.capture()
+    hb.replay(warmup)
+    torch.cuda.synchronize()
+    h0, m0 = hb.hit_rate()
+    dt = timed_replays(hb, steps)
+    h1, m1 = hb.hit_rate()
+    finite = int(hb.finite.item())
+    sdt, sbytes = shared_resident(lib, dev, (hb.sh_wg, hb.sh_wu, hb.sh_wd, hb.sh_wsg))
+    hb.graph = None
+    hb.pools = []
+    del hb
+    torch.cuda.empty_cache()
+    return {
+        "workload": "the headline decode step with each layer's full MoE block: routed experts "
+                    "via the device cache plus a gated bf16 shared expert (intermediate "
+                    f"{cfgb.shared_inter}) on a second stream beside router/resolve/fetch, and "
+                    "a device finiteness flag over the step output; one hipGraph",
+        "tokens_per_s": round(steps / dt, 3),
+        "ms_per_step": round(1e3 * dt / steps, 4),
+        "hit_rate": round((h1 - h0) / max(1, (h1 - h0) + (m1 - m0)), 4),
+        "finite_flag": finite,
+        "shared_expert_alone": {"us_per_layer": round(1e6 * sdt, 3), "bytes": sbytes,
+                                "GBps": round(sbytes / sdt / 1e9, 1),
+                                "what": "shared_gate_up + shared_down, 1 token, graph of "
+                                        "back-to-back calls rotating over 40 layers' weights"},
+    }
 
 
 def cpu_baseline(harness, budget_s: float):
@@ -542,7 +612,7 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the prefill and all-resident measurements")
     ap.add_argument("--tokens", type=int, default=512, help="tokens per call of --probe grouped")
-    ap.add_argument("--probe", choices=["gemv", "fetch", "copy", "grouped"],
+    ap.add_argument("--probe", choices=["gemv", "fetch", "copy", "grouped", "shared"],
                     help="time one kernel alone (--steps launches) instead of the decode step")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -607,6 +677,13 @@ def main() -> int:
     del hc.cache, hc.views
     hc.pools = []
     torch.cuda.empty_cache()
+    block = None
+    if not args.no_extra:
+        log("MoE block step (routed + shared expert branch + finiteness guard)")
+        block = moe_block_bench(lib, cfg, pools, dev, args.steps, args.warmup)
+        log(f"MoE block: {block['tokens_per_s']} tok/s, {block['ms_per_step']} ms/step, "
+            f"finite flag {block['finite_flag']}, shared expert alone "
+            f"{block['shared_expert_alone']['us_per_layer']} us/layer")
     cfg0 = decode.DecodeConfig(**{**cfg.__dict__, "mode": "nocache"})
     h0c = decode.DecodeHarness(cfg0, dev, pools=pools)
     h0c.capture()
@@ -691,6 +768,7 @@ def main() -> int:
                                           "as two 128-job launches"},
         "hbm_measured_GBps": streams,
         "cpu_baseline": cpu,
+        "moe_block": block,
         "prefill": prefill,
         "all_resident": resident,
         "finite_output": x_ok,

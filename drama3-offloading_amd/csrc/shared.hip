@@ -15,14 +15,14 @@
 // holding the gate and up rows of j; one extra wave for the sigmoid gate
 // row), moe_shared_down the rest (4 output rows per wave) with the routed
 // output and the residual added in its epilogue.  Both are GEMVs over
-// weights read once per 4 tokens: HBM-bound at decode (6 MiB per layer at
-// H = 2048, Is = 512).  Sums are f32 fused multiply-adds over each lane's
-// 16-byte slices in row order, then a butterfly over the 64 lanes.
+// weights read once per 4 tokens (per token at decode): HBM-bound, 6 MiB per
+// layer at H = 2048, Is = 512.  Sums are f32 fused multiply-adds over each
+// lane's 16-byte slices in row order, then a butterfly over the 64 lanes.
 #include "common.hpp"
 
 namespace moe {
 
-constexpr int kSharedTB = 4;   // tokens per pass over the weights
+constexpr int kSharedTB = 4;   // tokens per pass over the weights (1 when there is one)
 
 __device__ __forceinline__ u32x4 load16(const uint16_t* p) {
   return *reinterpret_cast<const u32x4*>(p);
@@ -49,6 +49,12 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
 // bf16 rounding of an f32 value, returned as f32.
 __device__ __forceinline__ float rbf16(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
+// Each lane takes the 16-byte slices c = lane, lane + 64, ... of a row, in
+// batches of kUnroll slices whose loads are all issued before any is used;
+// slices past the row end load the last slice again and are not summed.
+constexpr int kUnroll = 4;
+
+template <int TB>
 __global__ __launch_bounds__(256) void shared_gate_up_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg, const uint16_t* __restrict__ wu,
     const uint16_t* __restrict__ wsg, int32_t tokens, int32_t hidden, int32_t inter,
@@ -60,29 +66,43 @@ __global__ __launch_bounds__(256) void shared_gate_up_kernel(
   const uint16_t* ra = gate_row ? wsg : wg + static_cast<int64_t>(j) * hidden;
   const uint16_t* rb = gate_row ? wsg : wu + static_cast<int64_t>(j) * hidden;
   const int nch = hidden >> 3;                    // 16-byte slices per row
-  for (int t0 = 0; t0 < tokens; t0 += kSharedTB) {
-    float aa[kSharedTB], ab[kSharedTB];
+  for (int t0 = 0; t0 < tokens; t0 += TB) {
+    float aa[TB], ab[TB];
 #pragma unroll
-    for (int t = 0; t < kSharedTB; ++t) aa[t] = ab[t] = 0.0f;
-    for (int c = lane; c < nch; c += 64) {
-      const u32x4 va = load16(ra + c * 8);
-      const u32x4 vb = load16(rb + c * 8);
+    for (int t = 0; t < TB; ++t) aa[t] = ab[t] = 0.0f;
+    for (int c0 = 0; c0 < nch; c0 += 64 * kUnroll) {
+      u32x4 va[kUnroll], vb[kUnroll], xv[TB][kUnroll];
 #pragma unroll
-      for (int t = 0; t < kSharedTB; ++t) {
-        const int tt = min(t0 + t, tokens - 1);
-        const u32x4 xv = load16(x + static_cast<int64_t>(tt) * hidden + c * 8);
-        aa[t] = dot8_bf16(va, xv, aa[t]);
-        ab[t] = dot8_bf16(vb, xv, ab[t]);
+      for (int u = 0; u < kUnroll; ++u) {
+        const int c = min(c0 + u * 64 + lane, nch - 1);
+        va[u] = load16(ra + c * 8);
+        vb[u] = load16(rb + c * 8);
+      }
+#pragma unroll
+      for (int t = 0; t < TB; ++t)
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+          const int c = min(c0 + u * 64 + lane, nch - 1);
+          xv[t][u] = load16(x + static_cast<int64_t>(min(t0 + t, tokens - 1)) * hidden + c * 8);
+        }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (c0 + u * 64 + lane >= nch) continue;
+#pragma unroll
+        for (int t = 0; t < TB; ++t) {
+          aa[t] = dot8_bf16(va[u], xv[t][u], aa[t]);
+          ab[t] = dot8_bf16(vb[u], xv[t][u], ab[t]);
+        }
       }
     }
 #pragma unroll
-    for (int t = 0; t < kSharedTB; ++t) {
+    for (int t = 0; t < TB; ++t) {
       aa[t] = wave_sum_f32(aa[t]);
       ab[t] = wave_sum_f32(ab[t]);
     }
     if (lane == 0) {
 #pragma unroll
-      for (int t = 0; t < kSharedTB; ++t) {
+      for (int t = 0; t < TB; ++t) {
         if (t0 + t >= tokens) break;
         if (gate_row) {
           const float z = rbf16(aa[t]);
@@ -98,6 +118,7 @@ __global__ __launch_bounds__(256) void shared_gate_up_kernel(
   }
 }
 
+template <int TB>
 __global__ __launch_bounds__(256) void shared_down_kernel(
     const uint16_t* __restrict__ act, const float* __restrict__ sig,
     const uint16_t* __restrict__ wd, int32_t tokens, int32_t hidden, int32_t inter,
@@ -108,34 +129,47 @@ __global__ __launch_bounds__(256) void shared_down_kernel(
   const int r0 = (blockIdx.x * 4 + wave) * kRows;
   if (r0 >= hidden) return;                       // hidden % 16 == 0: all kRows rows exist
   const int nch = inter >> 3;
-  for (int t0 = 0; t0 < tokens; t0 += kSharedTB) {
-    float acc[kRows][kSharedTB];
+  for (int t0 = 0; t0 < tokens; t0 += TB) {
+    float acc[kRows][TB];
 #pragma unroll
     for (int i = 0; i < kRows; ++i)
 #pragma unroll
-      for (int t = 0; t < kSharedTB; ++t) acc[i][t] = 0.0f;
-    for (int c = lane; c < nch; c += 64) {
-      u32x4 w[kRows];
+      for (int t = 0; t < TB; ++t) acc[i][t] = 0.0f;
+    for (int c0 = 0; c0 < nch; c0 += 64 * kUnroll) {
+      u32x4 w[kUnroll][kRows], av[TB][kUnroll];
 #pragma unroll
-      for (int i = 0; i < kRows; ++i) w[i] = load16(wd + static_cast<int64_t>(r0 + i) * inter + c * 8);
+      for (int u = 0; u < kUnroll; ++u) {
+        const int c = min(c0 + u * 64 + lane, nch - 1);
 #pragma unroll
-      for (int t = 0; t < kSharedTB; ++t) {
-        const int tt = min(t0 + t, tokens - 1);
-        const u32x4 av = load16(act + static_cast<int64_t>(tt) * inter + c * 8);
+        for (int i = 0; i < kRows; ++i)
+          w[u][i] = load16(wd + static_cast<int64_t>(r0 + i) * inter + c * 8);
+      }
 #pragma unroll
-        for (int i = 0; i < kRows; ++i) acc[i][t] = dot8_bf16(w[i], av, acc[i][t]);
+      for (int t = 0; t < TB; ++t)
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+          const int c = min(c0 + u * 64 + lane, nch - 1);
+          av[t][u] = load16(act + static_cast<int64_t>(min(t0 + t, tokens - 1)) * inter + c * 8);
+        }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (c0 + u * 64 + lane >= nch) continue;
+#pragma unroll
+        for (int t = 0; t < TB; ++t)
+#pragma unroll
+          for (int i = 0; i < kRows; ++i) acc[i][t] = dot8_bf16(w[u][i], av[t][u], acc[i][t]);
       }
     }
 #pragma unroll
     for (int i = 0; i < kRows; ++i)
 #pragma unroll
-      for (int t = 0; t < kSharedTB; ++t) acc[i][t] = wave_sum_f32(acc[i][t]);
-    // lane i * kSharedTB + t finishes (row r0 + i, token t0 + t)
+      for (int t = 0; t < TB; ++t) acc[i][t] = wave_sum_f32(acc[i][t]);
+    // lane i * TB + t finishes (row r0 + i, token t0 + t)
 #pragma unroll
     for (int i = 0; i < kRows; ++i)
 #pragma unroll
-      for (int t = 0; t < kSharedTB; ++t) {
-        if (lane != i * kSharedTB + t || t0 + t >= tokens) continue;
+      for (int t = 0; t < TB; ++t) {
+        if (lane != i * TB + t || t0 + t >= tokens) continue;
         const int64_t o = static_cast<int64_t>(t0 + t) * hidden + r0 + i;
         const float d = rbf16(acc[i][t]);
         float v = rbf16(sig[t0 + t] * d);
@@ -195,7 +229,8 @@ extern "C" int moe_shared_gate_up(const void* x, const void* w_gate, const void*
                   reinterpret_cast<uintptr_t>(w_sgate) % 16 == 0,
               "moe_shared_gate_up: x and weights must be 16-byte aligned");
   const unsigned grid = static_cast<unsigned>((inter + 1 + 3) / 4);
-  hipLaunchKernelGGL(shared_gate_up_kernel, dim3(grid), dim3(256), 0, as_stream(stream),
+  auto kern = tokens == 1 ? shared_gate_up_kernel<1> : shared_gate_up_kernel<kSharedTB>;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, as_stream(stream),
                      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w_gate),
                      static_cast<const uint16_t*>(w_up), static_cast<const uint16_t*>(w_sgate),
                      tokens, hidden, inter, static_cast<uint16_t*>(act), sig);
@@ -214,7 +249,8 @@ extern "C" int moe_shared_down(const void* act, const float* sig, const void* w_
                   reinterpret_cast<uintptr_t>(w_down) % 16 == 0,
               "moe_shared_down: act and w_down must be 16-byte aligned");
   const unsigned grid = static_cast<unsigned>(hidden / 16);
-  hipLaunchKernelGGL(shared_down_kernel, dim3(grid), dim3(256), 0, as_stream(stream),
+  auto kern = tokens == 1 ? shared_down_kernel<1> : shared_down_kernel<kSharedTB>;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, as_stream(stream),
                      static_cast<const uint16_t*>(act), sig, static_cast<const uint16_t*>(w_down),
                      tokens, hidden, inter, static_cast<const uint16_t*>(routed),
                      static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out));

@@ -10,6 +10,20 @@ Per layer, all on one stream, nothing synchronising and nothing allocating:
     y     = fp8_moe_forward(h, slots, w)      W8A8 expert FFN on the cache (HIP)
     x     = h + y
 
+With `shared_expert`, the step is the full MoE block: the gated bf16 shared
+expert's first half runs right after h, its down kernel after the routed
+experts, adding the routed output and the residual,
+
+    act, s = shared_gate_up(h)
+    x      = h + (y + s * shared_down(act))
+
+(A second captured stream for the first half, beside the router, resolve
+and fetch, measured slower than one stream: the graph's event nodes cost
+more than the overlap gained.)
+
+and after the last layer a device flag records whether x is finite (the
+decode graph's finiteness guard).
+
 This is the path Drama3DecodeGraphs captures around dev_cached_forward in the
 reference (bin/prefix_kv.py:383-457 driving bin/devcache.py:258-277), with
 the rest of the transformer replaced by one [2048, 2048] matmul per layer.
@@ -50,6 +64,8 @@ class DecodeConfig:
     gate_std: float = 0.002
     blocks_per_job: int = 2
     noncoherent_pool: bool = False
+    shared_expert: bool = False     # the MoE block's gated bf16 shared expert
+    shared_inter: int = 512
 
 
 def fill_pool_on_gpu(pool: HostPool, seed: int, layer: int, device, chunk: int = 64,
@@ -122,6 +138,21 @@ class DecodeHarness:
         ws = self.lib.fp8_moe_workspace(1, K, C, H, cfg.inter)
         self.ws = torch.empty(ws, dtype=torch.uint8, device=dev)
         self.pairs = [p.fetch_pair(c) for p, c in zip(self.pools, self.cache)]
+        if cfg.shared_expert:
+            # seeded bf16 shared experts, resident (6 MiB per layer at 2048 x 512)
+            g2 = torch.Generator(device=dev).manual_seed(cfg.seed + 3)
+            Is = cfg.shared_inter
+            rnd = lambda *s, std: (torch.randn(s, generator=g2, device=dev) * std).to(torch.bfloat16)
+            # N(0, 0.02) like the routed experts, down N(0, 0.005): with no norm in
+            # the stub, a second quadratic term per layer at the routed experts'
+            # scale grows the residual stream past bf16 range within 40 layers
+            self.sh_wg = rnd(L, Is, H, std=0.02)
+            self.sh_wu = rnd(L, Is, H, std=0.02)
+            self.sh_wd = rnd(L, H, Is, std=0.005)
+            self.sh_wsg = rnd(L, H, std=0.02)
+            self.sh_act = torch.empty((1, Is), dtype=torch.bfloat16, device=dev)
+            self.sh_sig = torch.empty(1, dtype=torch.float32, device=dev)
+        self.finite = torch.ones(1, dtype=torch.int32, device=dev)
         self.graph = None
         self.cursor = 0
 
@@ -139,6 +170,9 @@ class DecodeHarness:
     def layer(self, l: int) -> None:
         cfg, lib = self.cfg, self.lib
         torch.mm(self.x, self.w_stub[l], out=self.h)
+        if cfg.shared_expert:
+            lib.shared_gate_up(self.h, self.sh_wg[l], self.sh_wu[l], self.sh_wsg[l],
+                               self.sh_act, self.sh_sig)
         w13, s13, w2, s2 = self.views[l]
         if cfg.mode == "cached":
             # router + slot resolve (two launches), then the miss fetch
@@ -155,9 +189,15 @@ class DecodeHarness:
             lib.fetch([self.pairs[l]], self.ids[l].view(-1), self.fixed_slots.view(-1),
                       self.all_miss, max_jobs=cfg.top_k, blocks_per_job=cfg.blocks_per_job)
             slots = self.fixed_slots
-        # x = h + MoE(h), the residual add fused into the down kernel
-        lib.fp8_moe_forward(self.h, slots, self.wts[l], w13, s13, w2, s2, self.x, self.ws,
+        if cfg.shared_expert:
+            # y = routed experts; x = h + (y + shared), both sums in the shared down kernel
+            lib.fp8_moe_forward(self.h, slots, self.wts[l], w13, s13, w2, s2, self.y, self.ws)
+            lib.shared_down(self.sh_act, self.sh_sig, self.sh_wd[l], self.x, routed=self.y,
                             residual=self.h)
+        else:
+            # x = h + MoE(h), the residual add fused into the down kernel
+            lib.fp8_moe_forward(self.h, slots, self.wts[l], w13, s13, w2, s2, self.x, self.ws,
+                                residual=self.h)
 
     def step_eager(self) -> None:
         # every step starts from the same input token state (the stub has no
@@ -166,6 +206,8 @@ class DecodeHarness:
         self.x.copy_(self.x0)
         for l in range(self.cfg.layers):
             self.layer(l)
+        if self.cfg.shared_expert:
+            self.lib.all_finite(self.x, self.finite)
 
     def capture(self) -> torch.cuda.CUDAGraph:
         s = torch.cuda.Stream(device=self.dev)
