@@ -523,9 +523,8 @@ def shared_resident(lib, dev, weights, calls: int = 200):
 
 def moe_block_bench(lib, cfg, pools, dev, steps: int, warmup: int):
     """The decode step with the full MoE block: routed experts through the
-    cache plus the gated shared expert on a second stream, and the
-    finiteness guard, in one hipGraph (same schedule and cache size as the
-    headline step)."""
+    cache plus the gated shared expert, and the finiteness guard, in one
+    hipGraph (same schedule and cache size as the headline step)."""
     import torch
     import decode
     cfgb = decode.DecodeConfig(**{**cfg.__dict__, "shared_expert": True})
@@ -545,8 +544,8 @@ def moe_block_bench(lib, cfg, pools, dev, steps: int, warmup: int):
     return {
         "workload": "the headline decode step with each layer's full MoE block: routed experts "
                     "via the device cache plus a gated bf16 shared expert (intermediate "
-                    f"{cfgb.shared_inter}) on a second stream beside router/resolve/fetch, and "
-                    "a device finiteness flag over the step output; one hipGraph",
+                    f"{cfgb.shared_inter}, N(0,0.02) gate/up, N(0,0.005) down), and a device "
+                    "finiteness flag over the step output; one hipGraph",
         "tokens_per_s": round(steps / dt, 3),
         "ms_per_step": round(1e3 * dt / steps, 4),
         "hit_rate": round((h1 - h0) / max(1, (h1 - h0) + (m1 - m0)), 4),
@@ -679,7 +678,7 @@ def main() -> int:
     torch.cuda.empty_cache()
     block = None
     if not args.no_extra:
-        log("MoE block step (routed + shared expert branch + finiteness guard)")
+        log("MoE block step (routed + shared expert + finiteness guard)")
         block = moe_block_bench(lib, cfg, pools, dev, args.steps, args.warmup)
         log(f"MoE block: {block['tokens_per_s']} tok/s, {block['ms_per_step']} ms/step, "
             f"finite flag {block['finite_flag']}, shared expert alone "

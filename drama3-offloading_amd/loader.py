@@ -34,6 +34,8 @@ from hostpool import RecordLayout
 
 EXPERT = "model.language_model.layers.{layer}.mlp.experts.{expert}.{proj}.{what}"
 ROUTER_GATE = "model.language_model.layers.{layer}.mlp.gate.weight"
+SHARED = "model.language_model.layers.{layer}.mlp.shared_expert.{proj}.weight"
+SHARED_GATE = "model.language_model.layers.{layer}.mlp.shared_expert_gate.weight"
 _DTYPE_BYTES = {"F8_E4M3": 1, "BF16": 2, "F16": 2, "F32": 4}
 
 
@@ -214,3 +216,30 @@ def fill_expert_buffers(index: ShardIndex, layer: int, experts, threads: int = 8
 
     with ThreadPoolExecutor(max_workers=max(1, threads)) as ex:
         list(ex.map(one, range(n)))
+
+
+def load_shared_expert(index: ShardIndex, layer: int, device=None) -> dict:
+    """The layer's gated shared expert as bf16 tensors, shaped as the shared
+    expert kernels take them: {"gate": [Is, H], "up": [Is, H], "down": [H, Is],
+    "sgate": [H]} (checkpoint tensors layers.N.mlp.shared_expert.*_proj.weight
+    and layers.N.mlp.shared_expert_gate.weight [1, H], all BF16)."""
+    import torch
+    if index.root is None:
+        raise ValueError("index has no shard directory to read from")
+    names = {"gate": SHARED.format(layer=layer, proj="gate_proj"),
+             "up": SHARED.format(layer=layer, proj="up_proj"),
+             "down": SHARED.format(layer=layer, proj="down_proj"),
+             "sgate": SHARED_GATE.format(layer=layer)}
+    ent = {k: index.get(n) for k, n in names.items()}
+    Is, H = ent["gate"].shape
+    want = {"gate": (Is, H), "up": (Is, H), "down": (H, Is), "sgate": (1, H)}
+    maps = _Maps(index.root)
+    out = {}
+    for k, t in ent.items():
+        _expect(t, names[k], "BF16", want[k])
+        raw = np.array(maps(t.shard)[t.start:t.start + t.nbytes])      # own copy
+        v = torch.from_numpy(raw).view(torch.bfloat16).view(*t.shape)
+        out[k] = v.reshape(-1) if k == "sgate" else v
+    if device is not None:
+        out = {k: v.to(device) for k, v in out.items()}
+    return out

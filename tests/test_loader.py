@@ -43,8 +43,13 @@ def test_plan_matches_reference_checkpoint_layout():
                 assert o0 + n0 == o1                     # contiguous, no gaps or overlap
         gate = index.get(loader.ROUTER_GATE.format(layer=layer))
         assert gate.dtype == "BF16" and gate.shape == (256, 2048)
-    shared = entries["model.language_model.layers.0.mlp.shared_expert.down_proj.weight"]
-    assert shared["dtype"] == "BF16" and shared["shape"] == [2048, 512]
+    for layer in (0, 39):
+        for proj, shape in (("gate_proj", [512, 2048]), ("up_proj", [512, 2048]),
+                            ("down_proj", [2048, 512])):
+            m = entries[loader.SHARED.format(layer=layer, proj=proj)]
+            assert m["dtype"] == "BF16" and m["shape"] == shape
+        m = entries[loader.SHARED_GATE.format(layer=layer)]
+        assert m["dtype"] == "BF16" and m["shape"] == [1, 2048]
 
 
 def _write_shards(tmp_path, layers=2, E=6, H=256, I=128, seed=0):
@@ -65,6 +70,10 @@ def _write_shards(tmp_path, layers=2, E=6, H=256, I=128, seed=0):
                     sc(shape[0] // 128, shape[1] // 128)
         tensors[f"model.language_model.layers.{l}.mlp.gate.weight"] = torch.zeros((E, H),
                                                                                    dtype=torch.bfloat16)
+        bf = lambda *s: torch.randn(s, generator=g).to(torch.bfloat16)               # noqa
+        for proj, shape in (("gate_proj", (I, H)), ("up_proj", (I, H)), ("down_proj", (H, I))):
+            tensors[f"model.language_model.layers.{l}.mlp.shared_expert.{proj}.weight"] = bf(*shape)
+        tensors[f"model.language_model.layers.{l}.mlp.shared_expert_gate.weight"] = bf(1, H)
     names = sorted(tensors)
     half = len(names) // 2 + 3                   # split one layer's experts across both shards
     save_file({n: tensors[n] for n in names[:half]}, tmp_path / "model-00001-of-00002.safetensors")
@@ -124,3 +133,17 @@ def test_wrong_dtype_and_missing_tensor_are_refused(tmp_path):
         loader.record_plan(index, 0, 0, lay)
     with pytest.raises(KeyError, match="layers.3"):
         loader.record_plan(index, 3, 0, lay)
+
+
+def test_shared_expert_from_shards(tmp_path):
+    import loader
+    tensors = _write_shards(tmp_path, seed=5)
+    index = loader.ShardIndex.from_dir(tmp_path)
+    for l in range(2):
+        got = loader.load_shared_expert(index, l)
+        pre = f"model.language_model.layers.{l}.mlp."
+        assert torch.equal(got["gate"], tensors[pre + "shared_expert.gate_proj.weight"])
+        assert torch.equal(got["up"], tensors[pre + "shared_expert.up_proj.weight"])
+        assert torch.equal(got["down"], tensors[pre + "shared_expert.down_proj.weight"])
+        assert torch.equal(got["sgate"], tensors[pre + "shared_expert_gate.weight"].reshape(-1))
+        assert got["gate"].shape == (128, 256) and got["sgate"].shape == (256,)
