@@ -21,8 +21,24 @@
 // rows of w2, and the workgroup sums the k partials in order.
 #include "common.hpp"
 #include "grouped.hpp"
+#include "shared.hpp"
 
 namespace moe {
+
+// The MoE block's shared expert carried along by the two decode launches
+// (moe_fp8_moe_block_forward): kernel 1 computes its act and sigmoid gate in
+// extra workgroups, kernel 2 its down rows in one extra wave per workgroup,
+// with the arithmetic of the standalone shared-expert kernels (shared.hpp).
+struct SharedRefs {
+  const uint16_t* wg;    // [Is, H] bf16
+  const uint16_t* wu;    // [Is, H]
+  const uint16_t* wd;    // [H, Is]
+  const uint16_t* wsg;   // [H]
+  int32_t inter;         // Is
+  uint16_t* act;         // [T, Is] bf16 scratch
+  float* sig;            // [T] scratch
+};
+constexpr int kSharedJPW = 2;   // shared intermediate rows (gate + up) per kernel-1 wave
 
 constexpr int kMaxHidden = 8192;
 constexpr int kMaxInter = 2048;
@@ -83,12 +99,44 @@ __device__ __forceinline__ void quantize_x32(const uint4 (&raw)[4], bool live, i
 // x[t] into LDS while they travel, then runs the MFMAs.
 constexpr int kGateUpChunk = 16;
 
+template <bool SHARED>
 __global__ __launch_bounds__(64) void gateup_gemv_kernel(
     const uint16_t* __restrict__ x, const void* __restrict__ ids, int ids64, int32_t top_k,
     const uint8_t* __restrict__ w13, const float* __restrict__ s13, int64_t w13_es,
-    int64_t s13_es, int32_t n_experts, int32_t hidden, int32_t inter, float* __restrict__ h) {
+    int64_t s13_es, int32_t n_experts, int32_t hidden, int32_t inter, float* __restrict__ h,
+    int32_t tokens, SharedRefs sh) {
   __shared__ __align__(16) uint8_t xq[kMaxHidden];
   __shared__ float xs[kMaxHidden / 128];
+  if (SHARED && blockIdx.y >= static_cast<unsigned>(tokens * top_k)) {
+    // shared expert rows j0, j0 + 1 (gate and up each; j == Is is the sigmoid gate row)
+    const int lane = threadIdx.x;
+    const int j0 = ((blockIdx.y - tokens * top_k) * gridDim.x + blockIdx.x) * kSharedJPW;
+    if (j0 > sh.inter) return;                   // the whole workgroup
+    const uint16_t* rows[2 * kSharedJPW];
+#pragma unroll
+    for (int i = 0; i < kSharedJPW; ++i) {
+      const int j = min(j0 + i, sh.inter);
+      const bool gate_row = j == sh.inter;
+      rows[2 * i] = gate_row ? sh.wsg : sh.wg + static_cast<int64_t>(j) * hidden;
+      rows[2 * i + 1] = gate_row ? sh.wsg : sh.wu + static_cast<int64_t>(j) * hidden;
+    }
+    for (int t = 0; t < tokens; ++t) {
+      float acc[2 * kSharedJPW][1];
+      rows_dot_bf16<2 * kSharedJPW, 1, 4>(rows, x, hidden, t, tokens, hidden >> 3, lane, acc);
+      if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < kSharedJPW; ++i) {
+          const int j = j0 + i;
+          if (j < sh.inter)
+            sh.act[static_cast<int64_t>(t) * sh.inter + j] = shared_act(acc[2 * i][0],
+                                                                        acc[2 * i + 1][0]);
+          else if (j == sh.inter)
+            sh.sig[t] = shared_sig(acc[2 * i][0]);
+        }
+      }
+    }
+    return;
+  }
   const int64_t p = blockIdx.y;
   const int64_t t = p / top_k;
   const int64_t e = load_id(ids, ids64, p);
@@ -164,19 +212,38 @@ __global__ __launch_bounds__(64) void gateup_gemv_kernel(
 // they travel; the k partial results are summed in k order.
 constexpr int kDownChunk = 4;   // K-blocks of w2 in flight per lane (inter 512 = one chunk)
 
+template <bool SHARED>
 __global__ __launch_bounds__(1024) void down_gemv_kernel(
     const float* __restrict__ h, const void* __restrict__ ids, int ids64,
     const void* __restrict__ weights, int wbf16, int32_t top_k, const uint8_t* __restrict__ w2,
     const float* __restrict__ s2, int64_t w2_es, int64_t s2_es, int32_t n_experts,
     int32_t hidden, int32_t inter, const uint16_t* __restrict__ residual,
-    uint16_t* __restrict__ out) {
+    uint16_t* __restrict__ out, SharedRefs sh) {
   __shared__ __align__(16) uint8_t aq[kMaxK][kMaxInter];
   __shared__ float as_[kMaxK][kMaxInter / 128];
   __shared__ float part[kMaxK][16];
   __shared__ float wpart[kMaxK];
-  const int wave = threadIdx.x >> 6;   // == k
+  __shared__ float spart[SHARED ? 16 : 1];
+  const int wave = threadIdx.x >> 6;   // == k; SHARED: wave top_k is the shared expert's
   const int lane = threadIdx.x & 63;
   const int64_t t = blockIdx.y;
+  if (SHARED && wave == top_k) {
+    // the shared expert's 16 down rows of this workgroup, token t
+    const int r0 = blockIdx.x * 16;
+    const uint16_t* rows[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) rows[i] = sh.wd + static_cast<int64_t>(r0 + i) * sh.inter;
+    float acc[16][1];
+    rows_dot_bf16<16, 1, 1>(rows, sh.act, sh.inter, static_cast<int>(t),
+                            static_cast<int>(t) + 1, sh.inter >> 3, lane, acc);
+    if (lane == 0) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) spart[i] = acc[i][0];
+    }
+    __syncthreads();                  // pairs with the routed waves' two barriers;
+    __syncthreads();                  // threads 0..15 then combine, spart included
+    return;
+  }
   const int64_t p = t * top_k + wave;
   const int64_t e = load_id(ids, ids64, p);
   const bool valid = e >= 0 && e < n_experts;
@@ -249,9 +316,49 @@ __global__ __launch_bounds__(1024) void down_gemv_kernel(
     for (int k = 0; k < top_k; ++k) sum = fmaf(wpart[k], part[k][threadIdx.x], sum);
     const int64_t o = t * hidden + c0 + threadIdx.x;
     uint16_t y = f32_to_bf16(sum);
-    if (residual) y = f32_to_bf16(bf16_to_f32(residual[o]) + bf16_to_f32(y));
+    if (SHARED) {
+      // out = residual + (routed + sig * shared), as moe_shared_down on the routed output
+      y = shared_out(spart[threadIdx.x], sh.sig[t], &y, residual ? residual + o : nullptr);
+    } else if (residual) {
+      y = f32_to_bf16(bf16_to_f32(residual[o]) + bf16_to_f32(y));
+    }
     out[o] = y;
   }
+}
+
+// The two decode launches; `sh` (nullable) carries the shared expert along.
+static int launch_gemv(const uint16_t* x, const void* ids, int ids64, const void* weights,
+                       int wbf16, int32_t tokens, int32_t top_k, const uint8_t* w13,
+                       const float* s13, const uint8_t* w2, const float* s2,
+                       const moe_expert_strides& es, int32_t n_experts, int32_t hidden,
+                       int32_t inter, const uint16_t* residual, uint16_t* out, float* h,
+                       const SharedRefs* sh, hipStream_t s) {
+  const int64_t pairs = static_cast<int64_t>(tokens) * top_k;
+  const unsigned gx = static_cast<unsigned>((2 * inter) / 16);
+  if (sh) {
+    // extra rows of workgroups for the shared expert's Is + 1 rows (the last: sigmoid gate)
+    const unsigned sy =
+        static_cast<unsigned>((sh->inter + 1 + kSharedJPW * gx - 1) / (kSharedJPW * gx));
+    hipLaunchKernelGGL(gateup_gemv_kernel<true>, dim3(gx, pairs + sy), dim3(64), 0, s, x, ids,
+                       ids64, top_k, w13, s13, es.w13, es.s13, n_experts, hidden, inter, h,
+                       tokens, *sh);
+  } else {
+    hipLaunchKernelGGL(gateup_gemv_kernel<false>, dim3(gx, pairs), dim3(64), 0, s, x, ids, ids64,
+                       top_k, w13, s13, es.w13, es.s13, n_experts, hidden, inter, h, tokens,
+                       SharedRefs{});
+  }
+  int rc = check_launch("moe_fp8_moe_forward(gate/up)");
+  if (rc) return rc;
+  if (sh) {
+    hipLaunchKernelGGL(down_gemv_kernel<true>, dim3(hidden / 16, tokens), dim3(64 * (top_k + 1)),
+                       0, s, h, ids, ids64, weights, wbf16, top_k, w2, s2, es.w2, es.s2,
+                       n_experts, hidden, inter, residual, out, *sh);
+  } else {
+    hipLaunchKernelGGL(down_gemv_kernel<false>, dim3(hidden / 16, tokens), dim3(64 * top_k), 0, s,
+                       h, ids, ids64, weights, wbf16, top_k, w2, s2, es.w2, es.s2, n_experts,
+                       hidden, inter, residual, out, SharedRefs{});
+  }
+  return check_launch("moe_fp8_moe_forward(down)");
 }
 
 }  // namespace moe
@@ -279,15 +386,16 @@ extern "C" size_t moe_fp8_moe_workspace(int32_t tokens, int32_t top_k, int32_t n
   return need > g ? need : g;
 }
 
-extern "C" int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t ids_dtype,
-                                      const void* weights, int32_t w_dtype, int32_t tokens,
-                                      int32_t top_k, const void* w13, const float* s13,
-                                      const void* w2, const float* s2, int32_t n_experts,
-                                      int32_t hidden, int32_t inter,
-                                      const moe_expert_strides* strides,
-                                      const void* residual, void* out,
-                                      void* workspace, size_t workspace_bytes, int32_t mode,
-                                      void* stream) {
+// The routed-expert call: preconditions, then the GEMV or grouped path.
+// `sh` (nullable) asks for the shared expert on the GEMV path; *fused tells
+// whether it was carried along (the caller runs it after a grouped call).
+static int forward_impl(const void* x, const void* ids, int32_t ids_dtype, const void* weights,
+                        int32_t w_dtype, int32_t tokens, int32_t top_k, const void* w13,
+                        const float* s13, const void* w2, const float* s2, int32_t n_experts,
+                        int32_t hidden, int32_t inter, const moe_expert_strides* strides,
+                        const void* residual, void* out, void* workspace, size_t workspace_bytes,
+                        int32_t mode, const SharedRefs* sh, bool* fused, void* stream) {
+  *fused = false;
   MOE_REQUIRE(tokens >= 0, "moe_fp8_moe_forward: tokens < 0");
   MOE_REQUIRE(top_k >= 1 && top_k <= kMaxK, "moe_fp8_moe_forward: need 1 <= top_k <= %d", kMaxK);
   MOE_REQUIRE(hidden >= 128 && hidden % 128 == 0 && hidden <= kMaxHidden,
@@ -343,17 +451,100 @@ extern "C" int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t id
   }
   MOE_REQUIRE(pairs <= 65535LL, "moe_fp8_moe_forward: too many (token, expert) pairs (%lld)",
               (long long)pairs);
-  hipLaunchKernelGGL(gateup_gemv_kernel, dim3((2 * inter) / 16, pairs), dim3(64), 0, s,
-                     static_cast<const uint16_t*>(x), ids, ids64, top_k,
-                     static_cast<const uint8_t*>(w13), s13, es.w13, es.s13, n_experts, hidden,
-                     inter, h);
-  int rc = check_launch("moe_fp8_moe_forward(gate/up)");
+  // the shared expert rides along when its extra wave fits the down workgroup
+  if (sh && top_k + 1 > kMaxK) sh = nullptr;
+  *fused = sh != nullptr;
+  return launch_gemv(static_cast<const uint16_t*>(x), ids, ids64, weights, wbf16, tokens, top_k,
+                     static_cast<const uint8_t*>(w13), s13, static_cast<const uint8_t*>(w2), s2,
+                     es, n_experts, hidden, inter, static_cast<const uint16_t*>(residual),
+                     static_cast<uint16_t*>(out), h, sh, s);
+}
+
+extern "C" int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t ids_dtype,
+                                      const void* weights, int32_t w_dtype, int32_t tokens,
+                                      int32_t top_k, const void* w13, const float* s13,
+                                      const void* w2, const float* s2, int32_t n_experts,
+                                      int32_t hidden, int32_t inter,
+                                      const moe_expert_strides* strides,
+                                      const void* residual, void* out,
+                                      void* workspace, size_t workspace_bytes, int32_t mode,
+                                      void* stream) {
+  bool fused;
+  return forward_impl(x, ids, ids_dtype, weights, w_dtype, tokens, top_k, w13, s13, w2, s2,
+                      n_experts, hidden, inter, strides, residual, out, workspace, workspace_bytes,
+                      mode, nullptr, &fused, stream);
+}
+
+static size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+extern "C" size_t moe_fp8_moe_block_workspace(int32_t tokens, int32_t top_k, int32_t n_experts,
+                                              int32_t hidden, int32_t inter,
+                                              int32_t shared_inter) {
+  const size_t base = align256(moe_fp8_moe_workspace(tokens, top_k, n_experts, hidden, inter));
+  if (tokens <= 0 || shared_inter <= 0) return base;
+  return base + align256(static_cast<size_t>(tokens) * shared_inter * sizeof(uint16_t)) +
+         align256(static_cast<size_t>(tokens) * sizeof(float));
+}
+
+extern "C" int moe_fp8_moe_block_forward(const void* x, const void* ids, int32_t ids_dtype,
+                                         const void* weights, int32_t w_dtype, int32_t tokens,
+                                         int32_t top_k, const void* w13, const float* s13,
+                                         const void* w2, const float* s2, int32_t n_experts,
+                                         int32_t hidden, int32_t inter,
+                                         const moe_expert_strides* strides,
+                                         const moe_shared_expert* shared, const void* residual,
+                                         void* out, void* workspace, size_t workspace_bytes,
+                                         int32_t mode, void* stream) {
+  MOE_REQUIRE(tokens >= 0, "moe_fp8_moe_block_forward: tokens < 0");
+  MOE_REQUIRE(shared != nullptr, "moe_fp8_moe_block_forward: NULL shared expert");
+  const int32_t Is = shared->inter;
+  MOE_REQUIRE(Is >= 128 && Is % 128 == 0,
+              "moe_fp8_moe_block_forward: shared inter must be a positive multiple of 128");
+  if (tokens > 0) {
+    MOE_REQUIRE(shared->w_gate && shared->w_up && shared->w_down && shared->w_sgate,
+                "moe_fp8_moe_block_forward: NULL shared expert weight");
+    MOE_REQUIRE(reinterpret_cast<uintptr_t>(shared->w_gate) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(shared->w_up) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(shared->w_down) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(shared->w_sgate) % 16 == 0,
+                "moe_fp8_moe_block_forward: shared expert weights must be 16-byte aligned");
+    const size_t need = moe_fp8_moe_block_workspace(tokens, top_k, n_experts, hidden, inter, Is);
+    MOE_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+                "moe_fp8_moe_block_forward: workspace of %zu bytes needed, %zu given", need,
+                workspace_bytes);
+  }
+  bool fused = false;
+  if (tokens == 0)                   // preconditions only; an empty call touches nothing
+    return forward_impl(x, ids, ids_dtype, weights, w_dtype, tokens, top_k, w13, s13, w2, s2,
+                        n_experts, hidden, inter, strides, residual, out, workspace,
+                        workspace_bytes, mode, nullptr, &fused, stream);
+  // workspace: the routed call's, then act [T, Is] bf16, then sig [T] f32
+  char* ws = static_cast<char*>(workspace);
+  const size_t base = align256(moe_fp8_moe_workspace(tokens, top_k, n_experts, hidden, inter));
+  uint16_t* act = reinterpret_cast<uint16_t*>(ws + base);
+  float* sig = reinterpret_cast<float*>(
+      ws + base + align256(static_cast<size_t>(tokens) * Is * sizeof(uint16_t)));
+  const SharedRefs sh{static_cast<const uint16_t*>(shared->w_gate),
+                      static_cast<const uint16_t*>(shared->w_up),
+                      static_cast<const uint16_t*>(shared->w_down),
+                      static_cast<const uint16_t*>(shared->w_sgate), Is, act, sig};
+  if (!use_grouped(tokens, hidden, mode) && top_k + 1 <= kMaxK) {
+    // decode: the shared expert rides in the two GEMV launches, residual last
+    return forward_impl(x, ids, ids_dtype, weights, w_dtype, tokens, top_k, w13, s13, w2, s2,
+                        n_experts, hidden, inter, strides, residual, out, workspace, base, mode,
+                        &sh, &fused, stream);
+  }
+  // otherwise: routed experts into out, then the shared expert adds to it in place
+  int rc = forward_impl(x, ids, ids_dtype, weights, w_dtype, tokens, top_k, w13, s13, w2, s2,
+                        n_experts, hidden, inter, strides, nullptr, out, workspace, base, mode,
+                        nullptr, &fused, stream);
   if (rc) return rc;
-  hipLaunchKernelGGL(down_gemv_kernel, dim3(hidden / 16, tokens), dim3(64 * top_k), 0, s, h, ids,
-                     ids64, weights, wbf16, top_k, static_cast<const uint8_t*>(w2), s2, es.w2,
-                     es.s2, n_experts, hidden, inter, static_cast<const uint16_t*>(residual),
-                     static_cast<uint16_t*>(out));
-  return check_launch("moe_fp8_moe_forward(down)");
+  hipStream_t s = as_stream(stream);
+  rc = launch_shared_gate_up(static_cast<const uint16_t*>(x), sh.wg, sh.wu, sh.wsg, tokens, hidden,
+                             Is, act, sig, s);
+  if (rc) return rc;
+  return launch_shared_down(act, sig, sh.wd, tokens, hidden, Is, static_cast<const uint16_t*>(out),
+                            static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out), s);
 }
 
 extern "C" int moe_fp8_moe_forward(const void* x, const void* ids, int32_t ids_dtype,

@@ -18,41 +18,12 @@
 // weights read once per 4 tokens (per token at decode): HBM-bound, 6 MiB per
 // layer at H = 2048, Is = 512.  Sums are f32 fused multiply-adds over each
 // lane's 16-byte slices in row order, then a butterfly over the 64 lanes.
-#include "common.hpp"
+#include "shared.hpp"
 
 namespace moe {
 
 constexpr int kSharedTB = 4;   // tokens per pass over the weights (1 when there is one)
-
-__device__ __forceinline__ u32x4 load16(const uint16_t* p) {
-  return *reinterpret_cast<const u32x4*>(p);
-}
-
-// acc + sum of the 8 bf16 products of two 16-byte slices, one fma each in order.
-__device__ __forceinline__ float dot8_bf16(u32x4 w, u32x4 x, float acc) {
-  const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
-  const uint32_t xv[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    acc = fmaf(__uint_as_float(wv[i] << 16), __uint_as_float(xv[i] << 16), acc);
-    acc = fmaf(__uint_as_float(wv[i] & 0xffff0000u), __uint_as_float(xv[i] & 0xffff0000u), acc);
-  }
-  return acc;
-}
-
-__device__ __forceinline__ float wave_sum_f32(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
-// bf16 rounding of an f32 value, returned as f32.
-__device__ __forceinline__ float rbf16(float v) { return bf16_to_f32(f32_to_bf16(v)); }
-
-// Each lane takes the 16-byte slices c = lane, lane + 64, ... of a row, in
-// batches of kUnroll slices whose loads are all issued before any is used;
-// slices past the row end load the last slice again and are not summed.
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 4;     // 16-byte slices per lane in flight per row
 
 template <int TB>
 __global__ __launch_bounds__(256) void shared_gate_up_kernel(
@@ -63,56 +34,19 @@ __global__ __launch_bounds__(256) void shared_gate_up_kernel(
   const int j = blockIdx.x * 4 + wave;           // j == inter: the sigmoid gate row
   if (j > inter) return;                         // no barriers below
   const bool gate_row = j == inter;
-  const uint16_t* ra = gate_row ? wsg : wg + static_cast<int64_t>(j) * hidden;
-  const uint16_t* rb = gate_row ? wsg : wu + static_cast<int64_t>(j) * hidden;
-  const int nch = hidden >> 3;                    // 16-byte slices per row
+  const uint16_t* const rows[2] = {gate_row ? wsg : wg + static_cast<int64_t>(j) * hidden,
+                                   gate_row ? wsg : wu + static_cast<int64_t>(j) * hidden};
   for (int t0 = 0; t0 < tokens; t0 += TB) {
-    float aa[TB], ab[TB];
-#pragma unroll
-    for (int t = 0; t < TB; ++t) aa[t] = ab[t] = 0.0f;
-    for (int c0 = 0; c0 < nch; c0 += 64 * kUnroll) {
-      u32x4 va[kUnroll], vb[kUnroll], xv[TB][kUnroll];
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int c = min(c0 + u * 64 + lane, nch - 1);
-        va[u] = load16(ra + c * 8);
-        vb[u] = load16(rb + c * 8);
-      }
-#pragma unroll
-      for (int t = 0; t < TB; ++t)
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          const int c = min(c0 + u * 64 + lane, nch - 1);
-          xv[t][u] = load16(x + static_cast<int64_t>(min(t0 + t, tokens - 1)) * hidden + c * 8);
-        }
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        if (c0 + u * 64 + lane >= nch) continue;
-#pragma unroll
-        for (int t = 0; t < TB; ++t) {
-          aa[t] = dot8_bf16(va[u], xv[t][u], aa[t]);
-          ab[t] = dot8_bf16(vb[u], xv[t][u], ab[t]);
-        }
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < TB; ++t) {
-      aa[t] = wave_sum_f32(aa[t]);
-      ab[t] = wave_sum_f32(ab[t]);
-    }
+    float acc[2][TB];
+    rows_dot_bf16<2, TB, kUnroll>(rows, x, hidden, t0, tokens, hidden >> 3, lane, acc);
     if (lane == 0) {
 #pragma unroll
       for (int t = 0; t < TB; ++t) {
         if (t0 + t >= tokens) break;
-        if (gate_row) {
-          const float z = rbf16(aa[t]);
-          sig[t0 + t] = rbf16(1.0f / (1.0f + expf(-z)));
-        } else {
-          const float g = rbf16(aa[t]);
-          const float u = rbf16(ab[t]);
-          const float s = rbf16(g / (1.0f + expf(-g)));
-          act[static_cast<int64_t>(t0 + t) * inter + j] = f32_to_bf16(s * u);
-        }
+        if (gate_row)
+          sig[t0 + t] = shared_sig(acc[0][t]);
+        else
+          act[static_cast<int64_t>(t0 + t) * inter + j] = shared_act(acc[0][t], acc[1][t]);
       }
     }
   }
@@ -128,42 +62,12 @@ __global__ __launch_bounds__(256) void shared_down_kernel(
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int r0 = (blockIdx.x * 4 + wave) * kRows;
   if (r0 >= hidden) return;                       // hidden % 16 == 0: all kRows rows exist
-  const int nch = inter >> 3;
+  const uint16_t* rows[kRows];
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) rows[i] = wd + static_cast<int64_t>(r0 + i) * inter;
   for (int t0 = 0; t0 < tokens; t0 += TB) {
     float acc[kRows][TB];
-#pragma unroll
-    for (int i = 0; i < kRows; ++i)
-#pragma unroll
-      for (int t = 0; t < TB; ++t) acc[i][t] = 0.0f;
-    for (int c0 = 0; c0 < nch; c0 += 64 * kUnroll) {
-      u32x4 w[kUnroll][kRows], av[TB][kUnroll];
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int c = min(c0 + u * 64 + lane, nch - 1);
-#pragma unroll
-        for (int i = 0; i < kRows; ++i)
-          w[u][i] = load16(wd + static_cast<int64_t>(r0 + i) * inter + c * 8);
-      }
-#pragma unroll
-      for (int t = 0; t < TB; ++t)
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          const int c = min(c0 + u * 64 + lane, nch - 1);
-          av[t][u] = load16(act + static_cast<int64_t>(min(t0 + t, tokens - 1)) * inter + c * 8);
-        }
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        if (c0 + u * 64 + lane >= nch) continue;
-#pragma unroll
-        for (int t = 0; t < TB; ++t)
-#pragma unroll
-          for (int i = 0; i < kRows; ++i) acc[i][t] = dot8_bf16(w[u][i], av[t][u], acc[i][t]);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < kRows; ++i)
-#pragma unroll
-      for (int t = 0; t < TB; ++t) acc[i][t] = wave_sum_f32(acc[i][t]);
+    rows_dot_bf16<kRows, TB, kUnroll>(rows, act, inter, t0, tokens, inter >> 3, lane, acc);
     // lane i * TB + t finishes (row r0 + i, token t0 + t)
 #pragma unroll
     for (int i = 0; i < kRows; ++i)
@@ -171,11 +75,8 @@ __global__ __launch_bounds__(256) void shared_down_kernel(
       for (int t = 0; t < TB; ++t) {
         if (lane != i * TB + t || t0 + t >= tokens) continue;
         const int64_t o = static_cast<int64_t>(t0 + t) * hidden + r0 + i;
-        const float d = rbf16(acc[i][t]);
-        float v = rbf16(sig[t0 + t] * d);
-        if (routed) v = rbf16(bf16_to_f32(routed[o]) + v);
-        if (residual) v = rbf16(bf16_to_f32(residual[o]) + v);
-        out[o] = f32_to_bf16(v);
+        out[o] = shared_out(acc[i][t], sig[t0 + t], routed ? routed + o : nullptr,
+                            residual ? residual + o : nullptr);
       }
   }
 }
@@ -211,6 +112,25 @@ __global__ __launch_bounds__(1024) void all_finite_kernel(const void* __restrict
   if (threadIdx.x == 0) *flag = all ? 1 : 0;
 }
 
+int launch_shared_gate_up(const uint16_t* x, const uint16_t* wg, const uint16_t* wu,
+                          const uint16_t* wsg, int32_t tokens, int32_t hidden, int32_t inter,
+                          uint16_t* act, float* sig, hipStream_t s) {
+  const unsigned grid = static_cast<unsigned>((inter + 1 + 3) / 4);
+  auto kern = tokens == 1 ? shared_gate_up_kernel<1> : shared_gate_up_kernel<kSharedTB>;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, s, x, wg, wu, wsg, tokens, hidden, inter, act,
+                     sig);
+  return check_launch("moe_shared_gate_up");
+}
+
+int launch_shared_down(const uint16_t* act, const float* sig, const uint16_t* wd, int32_t tokens,
+                       int32_t hidden, int32_t inter, const uint16_t* routed,
+                       const uint16_t* residual, uint16_t* out, hipStream_t s) {
+  auto kern = tokens == 1 ? shared_down_kernel<1> : shared_down_kernel<kSharedTB>;
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(hidden / 16)), dim3(256), 0, s, act, sig,
+                     wd, tokens, hidden, inter, routed, residual, out);
+  return check_launch("moe_shared_down");
+}
+
 }  // namespace moe
 
 using namespace moe;
@@ -228,13 +148,10 @@ extern "C" int moe_shared_gate_up(const void* x, const void* w_gate, const void*
                   reinterpret_cast<uintptr_t>(w_up) % 16 == 0 &&
                   reinterpret_cast<uintptr_t>(w_sgate) % 16 == 0,
               "moe_shared_gate_up: x and weights must be 16-byte aligned");
-  const unsigned grid = static_cast<unsigned>((inter + 1 + 3) / 4);
-  auto kern = tokens == 1 ? shared_gate_up_kernel<1> : shared_gate_up_kernel<kSharedTB>;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, as_stream(stream),
-                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w_gate),
-                     static_cast<const uint16_t*>(w_up), static_cast<const uint16_t*>(w_sgate),
-                     tokens, hidden, inter, static_cast<uint16_t*>(act), sig);
-  return check_launch("moe_shared_gate_up");
+  return launch_shared_gate_up(static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w_gate),
+                               static_cast<const uint16_t*>(w_up),
+                               static_cast<const uint16_t*>(w_sgate), tokens, hidden, inter,
+                               static_cast<uint16_t*>(act), sig, as_stream(stream));
 }
 
 extern "C" int moe_shared_down(const void* act, const float* sig, const void* w_down,
@@ -248,13 +165,11 @@ extern "C" int moe_shared_down(const void* act, const float* sig, const void* w_
   MOE_REQUIRE(reinterpret_cast<uintptr_t>(act) % 16 == 0 &&
                   reinterpret_cast<uintptr_t>(w_down) % 16 == 0,
               "moe_shared_down: act and w_down must be 16-byte aligned");
-  const unsigned grid = static_cast<unsigned>(hidden / 16);
-  auto kern = tokens == 1 ? shared_down_kernel<1> : shared_down_kernel<kSharedTB>;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, as_stream(stream),
-                     static_cast<const uint16_t*>(act), sig, static_cast<const uint16_t*>(w_down),
-                     tokens, hidden, inter, static_cast<const uint16_t*>(routed),
-                     static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out));
-  return check_launch("moe_shared_down");
+  return launch_shared_down(static_cast<const uint16_t*>(act), sig,
+                            static_cast<const uint16_t*>(w_down), tokens, hidden, inter,
+                            static_cast<const uint16_t*>(routed),
+                            static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out),
+                            as_stream(stream));
 }
 
 extern "C" int moe_all_finite(const void* x, int32_t dtype, int64_t n, int32_t* flag,

@@ -10,16 +10,11 @@ Per layer, all on one stream, nothing synchronising and nothing allocating:
     y     = fp8_moe_forward(h, slots, w)      W8A8 expert FFN on the cache (HIP)
     x     = h + y
 
-With `shared_expert`, the step is the full MoE block: the gated bf16 shared
-expert's first half runs right after h, its down kernel after the routed
-experts, adding the routed output and the residual,
+With `shared_expert`, the step is the full MoE block, one call after the
+fetch: the gated bf16 shared expert rides in the two routed GEMV launches
+(moe_fp8_moe_block_forward), which also add the residual,
 
-    act, s = shared_gate_up(h)
-    x      = h + (y + s * shared_down(act))
-
-(A second captured stream for the first half, beside the router, resolve
-and fetch, measured slower than one stream: the graph's event nodes cost
-more than the overlap gained.)
+    x = h + (y + sigmoid(h w_sg) * shared(h))
 
 and after the last layer a device flag records whether x is finite (the
 decode graph's finiteness guard).
@@ -150,11 +145,16 @@ class DecodeHarness:
             self.sh_wu = rnd(L, Is, H, std=0.02)
             self.sh_wd = rnd(L, H, Is, std=0.005)
             self.sh_wsg = rnd(L, H, std=0.02)
-            self.sh_act = torch.empty((1, Is), dtype=torch.bfloat16, device=dev)
-            self.sh_sig = torch.empty(1, dtype=torch.float32, device=dev)
+            self.ws_block = torch.empty(
+                self.lib.fp8_moe_block_workspace(1, K, C, H, cfg.inter, Is), dtype=torch.uint8,
+                device=dev)
         self.finite = torch.ones(1, dtype=torch.int32, device=dev)
         self.graph = None
         self.cursor = 0
+
+    def shared(self, l: int):
+        """Layer l's shared expert (gate, up, down, sigmoid gate)."""
+        return self.sh_wg[l], self.sh_wu[l], self.sh_wd[l], self.sh_wsg[l]
 
     # -------------------------------------------------------------- state
     def reset_tables(self) -> None:
@@ -170,9 +170,6 @@ class DecodeHarness:
     def layer(self, l: int) -> None:
         cfg, lib = self.cfg, self.lib
         torch.mm(self.x, self.w_stub[l], out=self.h)
-        if cfg.shared_expert:
-            lib.shared_gate_up(self.h, self.sh_wg[l], self.sh_wu[l], self.sh_wsg[l],
-                               self.sh_act, self.sh_sig)
         w13, s13, w2, s2 = self.views[l]
         if cfg.mode == "cached":
             # router + slot resolve (two launches), then the miss fetch
@@ -190,10 +187,9 @@ class DecodeHarness:
                       self.all_miss, max_jobs=cfg.top_k, blocks_per_job=cfg.blocks_per_job)
             slots = self.fixed_slots
         if cfg.shared_expert:
-            # y = routed experts; x = h + (y + shared), both sums in the shared down kernel
-            lib.fp8_moe_forward(self.h, slots, self.wts[l], w13, s13, w2, s2, self.y, self.ws)
-            lib.shared_down(self.sh_act, self.sh_sig, self.sh_wd[l], self.x, routed=self.y,
-                            residual=self.h)
+            # x = h + (routed + shared): the whole block in the two decode launches
+            lib.fp8_moe_block_forward(self.h, slots, self.wts[l], w13, s13, w2, s2,
+                                      self.shared(l), self.x, self.ws_block, residual=self.h)
         else:
             # x = h + MoE(h), the residual add fused into the down kernel
             lib.fp8_moe_forward(self.h, slots, self.wts[l], w13, s13, w2, s2, self.x, self.ws,

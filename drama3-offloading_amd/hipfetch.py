@@ -33,6 +33,12 @@ class ExpertStrides(C.Structure):
     _fields_ = [("w13", C.c_int64), ("s13", C.c_int64), ("w2", C.c_int64), ("s2", C.c_int64)]
 
 
+class SharedExpert(C.Structure):
+    """moe_shared_expert (include/moe_offload.h)."""
+    _fields_ = [("w_gate", C.c_void_p), ("w_up", C.c_void_p), ("w_down", C.c_void_p),
+                ("w_sgate", C.c_void_p), ("inter", C.c_int32)]
+
+
 class FetchPair(C.Structure):
     """moe_fetch_pair (include/moe_offload.h)."""
     _fields_ = [("src", C.c_void_p), ("dst", C.c_void_p), ("bytes", C.c_int64)]
@@ -70,6 +76,11 @@ SIGNATURES = {
     "moe_shared_gate_up": (C.c_int, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp]),
     "moe_shared_down": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "moe_all_finite": (C.c_int, [_vp, _i32, _i64, _vp, _vp]),
+    "moe_fp8_moe_block_workspace": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "moe_fp8_moe_block_forward": (C.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp,
+                                            _vp, _i32, _i32, _i32, C.POINTER(ExpertStrides),
+                                            C.POINTER(SharedExpert), _vp, _vp, _vp, _sz, _i32,
+                                            _vp]),
 }
 
 
@@ -208,6 +219,36 @@ class Native:
             workspace.data_ptr(),
             workspace.numel() * workspace.element_size(), mode, self.stream()),
             "moe_fp8_moe_forward")
+
+    def fp8_moe_block_workspace(self, tokens, top_k, n_experts, hidden, inter,
+                                shared_inter) -> int:
+        return int(self.cdll.moe_fp8_moe_block_workspace(tokens, top_k, n_experts, hidden, inter,
+                                                         shared_inter))
+
+    def fp8_moe_block_forward(self, x, ids, weights, w13, s13, w2, s2, shared, out, workspace,
+                              mode: int = 0, residual=None) -> None:
+        """The MoE block: routed experts plus the gated shared expert,
+        shared = (w_gate [Is, H], w_up [Is, H], w_down [H, Is], w_sgate [H]) bf16;
+        out = residual + (routed + sigmoid-gated shared), each sum rounded to bf16."""
+        T, H = x.shape
+        K = ids.shape[-1]
+        n = w13.shape[0]
+        inter = w2.shape[-1]
+        wg, wu, wd, wsg = shared
+        Is = wg.shape[0]
+        if wg.shape != (Is, H) or wu.shape != (Is, H) or wd.shape != (H, Is) or wsg.numel() != H:
+            raise ValueError("shared expert weights do not match x")
+        for t in (w13, s13, w2, s2):
+            if not t[0].is_contiguous():
+                raise ValueError("expert weights must be contiguous within an expert")
+        es = ExpertStrides(w13.stride(0), s13.stride(0), w2.stride(0), s2.stride(0))
+        se = SharedExpert(wg.data_ptr(), wu.data_ptr(), wd.data_ptr(), wsg.data_ptr(), Is)
+        self._check(self.cdll.moe_fp8_moe_block_forward(
+            x.data_ptr(), ids.data_ptr(), self._dtype_code(ids), weights.data_ptr(),
+            self._dtype_code(weights), T, K, w13.data_ptr(), s13.data_ptr(), w2.data_ptr(),
+            s2.data_ptr(), n, H, inter, C.byref(es), C.byref(se), self._ptr(residual),
+            out.data_ptr(), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+            mode, self.stream()), "moe_fp8_moe_block_forward")
 
     # ------------------------------------------------------------ permute
     def permute(self, ids, n_experts: int, counts, offsets, sorted_pairs, pair_pos) -> None:

@@ -293,6 +293,44 @@ int moe_shared_down(const void* act, const float* sig, const void* w_down,
 int moe_all_finite(const void* x, int32_t dtype, int64_t n, int32_t* flag,
                    void* stream);
 
+/* The MoE block's shared expert as one argument: bf16 weights w_gate and
+ * w_up [inter, hidden], w_down [hidden, inter], w_sgate [hidden], all
+ * 16-byte aligned. */
+typedef struct moe_shared_expert {
+  const void* w_gate;
+  const void* w_up;
+  const void* w_down;
+  const void* w_sgate;
+  int32_t inter;
+} moe_shared_expert;
+
+/* Workspace of moe_fp8_moe_block_forward: moe_fp8_moe_workspace's plus the
+ * shared expert's act and gate scratch. */
+size_t moe_fp8_moe_block_workspace(int32_t tokens, int32_t top_k,
+                                   int32_t n_experts, int32_t hidden,
+                                   int32_t inter, int32_t shared_inter);
+
+/* The whole MoE block in one call:
+ *   out = bf16(residual + bf16(routed + bf16(sig * shared_down)))
+ * with routed the bf16 result of moe_fp8_moe_forward_ex on the same
+ * arguments and the shared terms those of moe_shared_gate_up/_down, bit for
+ * bit.  On the per-pair GEMV path (decode) the shared expert is carried by
+ * the two routed launches: extra workgroups of the gate/up launch and one
+ * extra wave per workgroup of the down launch (needs top_k <= 15).  A
+ * grouped call runs the routed experts, then the two shared-expert kernels
+ * on its output.  No counterpart in the reference: upstream's MoE block
+ * calls the expert forward (bin/devcache.py:275-277) and the shared expert
+ * separately. */
+int moe_fp8_moe_block_forward(const void* x, const void* ids, int32_t ids_dtype,
+                              const void* weights, int32_t w_dtype, int32_t tokens,
+                              int32_t top_k, const void* w13, const float* s13,
+                              const void* w2, const float* s2, int32_t n_experts,
+                              int32_t hidden, int32_t inter,
+                              const moe_expert_strides* strides,
+                              const moe_shared_expert* shared, const void* residual,
+                              void* out, void* workspace, size_t workspace_bytes,
+                              int32_t mode, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
