@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void shared_gate_up_kernel(
   }
 }
 
-template <int TB>
+template <int TB, int U>
 __global__ __launch_bounds__(256) void shared_down_kernel(
     const uint16_t* __restrict__ act, const float* __restrict__ sig,
     const uint16_t* __restrict__ wd, int32_t tokens, int32_t hidden, int32_t inter,
@@ -67,7 +67,7 @@ __global__ __launch_bounds__(256) void shared_down_kernel(
   for (int i = 0; i < kRows; ++i) rows[i] = wd + static_cast<int64_t>(r0 + i) * inter;
   for (int t0 = 0; t0 < tokens; t0 += TB) {
     float acc[kRows][TB];
-    rows_dot_bf16<kRows, TB, kUnroll>(rows, act, inter, t0, tokens, inter >> 3, lane, acc);
+    rows_dot_bf16<kRows, TB, U>(rows, act, inter, t0, tokens, inter >> 3, lane, acc);
     // lane i * TB + t finishes (row r0 + i, token t0 + t)
 #pragma unroll
     for (int i = 0; i < kRows; ++i)
@@ -125,7 +125,11 @@ int launch_shared_gate_up(const uint16_t* x, const uint16_t* wg, const uint16_t*
 int launch_shared_down(const uint16_t* act, const float* sig, const uint16_t* wd, int32_t tokens,
                        int32_t hidden, int32_t inter, const uint16_t* routed,
                        const uint16_t* residual, uint16_t* out, hipStream_t s) {
-  auto kern = tokens == 1 ? shared_down_kernel<1> : shared_down_kernel<kSharedTB>;
+  // one 16-byte slice per lane and row covers inter <= 512: no batch to fill
+  const bool one = inter <= 512;
+  auto kern = tokens == 1 ? (one ? shared_down_kernel<1, 1> : shared_down_kernel<1, kUnroll>)
+                          : (one ? shared_down_kernel<kSharedTB, 1>
+                                 : shared_down_kernel<kSharedTB, kUnroll>);
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(hidden / 16)), dim3(256), 0, s, act, sig,
                      wd, tokens, hidden, inter, routed, residual, out);
   return check_launch("moe_shared_down");
