@@ -46,6 +46,45 @@ def test_preconditions_are_rejected_without_launching(lib):
     assert b"cap" in c.moe_last_error()
 
 
+def test_shared_and_block_preconditions_are_rejected_without_launching(lib):
+    import ctypes as C
+    import hipfetch
+    c = lib.cdll
+    one = C.c_void_p(16)                   # never dereferenced: every call fails a check first
+    assert c.moe_shared_gate_up(one, one, one, one, 1, 2048, 500, one, one, None) == -1
+    assert b"multiples of 128" in c.moe_last_error()
+    assert c.moe_shared_gate_up(None, one, one, one, 1, 2048, 512, one, one, None) == -1
+    assert b"NULL" in c.moe_last_error()
+    assert c.moe_shared_gate_up(C.c_void_p(8), one, one, one, 1, 2048, 512, one, one, None) == -1
+    assert b"aligned" in c.moe_last_error()
+    assert c.moe_shared_gate_up(None, None, None, None, 0, 2048, 512, None, None, None) == 0
+    assert c.moe_shared_down(one, one, one, 1, 2000, 512, None, None, one, None) == -1
+    assert b"multiples of 128" in c.moe_last_error()
+    assert c.moe_shared_down(None, None, None, 0, 2048, 512, None, None, None, None) == 0
+    assert c.moe_all_finite(one, 7, 4, one, None) == -1
+    assert b"dtype" in c.moe_last_error()
+    assert c.moe_all_finite(C.c_void_p(4), hipfetch.MOE_F32, 4, one, None) == -1
+    assert b"aligned" in c.moe_last_error()
+    # the block call: shared expert missing, misaligned, workspace too small
+    es = hipfetch.ExpertStrides(2 * 512 * 2048, 8 * 16, 2048 * 512, 16 * 4)
+    args = lambda sh, ws_bytes: (one, one, hipfetch.MOE_I32, one, hipfetch.MOE_F32, 1, 8, one, one,
+                                 one, one, 16, 2048, 512, C.byref(es), sh, None, one, one,
+                                 ws_bytes, 0, None)
+    assert c.moe_fp8_moe_block_forward(*args(None, 1 << 30)) == -1
+    assert b"shared expert" in c.moe_last_error()
+    bad = hipfetch.SharedExpert(one, one, one, C.c_void_p(8), 512)
+    assert c.moe_fp8_moe_block_forward(*args(C.byref(bad), 1 << 30)) == -1
+    assert b"aligned" in c.moe_last_error()
+    ok = hipfetch.SharedExpert(one, one, one, one, 512)
+    need = c.moe_fp8_moe_block_workspace(1, 8, 16, 2048, 512, 512)
+    assert need > c.moe_fp8_moe_workspace(1, 8, 16, 2048, 512)
+    assert c.moe_fp8_moe_block_forward(*args(C.byref(ok), need - 1)) == -1
+    assert b"workspace" in c.moe_last_error()
+    odd = hipfetch.SharedExpert(one, one, one, one, 200)
+    assert c.moe_fp8_moe_block_forward(*args(C.byref(odd), 1 << 30)) == -1
+    assert b"shared inter" in c.moe_last_error()
+
+
 def test_workspace_size_formula(lib):
     def al(v):
         return (v + 255) // 256 * 256
