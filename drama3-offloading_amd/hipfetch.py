@@ -19,6 +19,8 @@ import ctypes as C
 import os
 from pathlib import Path
 
+import numpy as np
+
 HERE = Path(__file__).resolve().parent
 LIB_PATH = Path(os.environ.get("MOE_OFFLOAD_LIB", HERE / "libmoeoffload.so"))
 
@@ -76,6 +78,12 @@ SIGNATURES = {
     "moe_shared_gate_up": (C.c_int, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp]),
     "moe_shared_down": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "moe_all_finite": (C.c_int, [_vp, _i32, _i64, _vp, _vp]),
+    "moe_codec_histogram": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _i32]),
+    "moe_codec_bound": (_i64, [_i64, _i64]),
+    "moe_codec_encode": (_i64, [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i32]),
+    "moe_codec_table": (C.c_int, [_vp, _vp]),
+    "moe_fetch_coded": (C.c_int, [_vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _i64,
+                                  _i32, _vp]),
     "moe_fp8_moe_block_workspace": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "moe_fp8_moe_block_forward": (C.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp,
                                             _vp, _i32, _i32, _i32, C.POINTER(ExpertStrides),
@@ -305,6 +313,52 @@ class Native:
         """flag[0] (int32, device) = 1 if every element of x (f32 or bf16) is finite."""
         self._check(self.cdll.moe_all_finite(x.data_ptr(), self._dtype_code(x), x.numel(),
                                              flag.data_ptr(), self.stream()), "moe_all_finite")
+
+    # ------------------------------------------------------------ coded pools
+    def codec_histogram(self, records: np.ndarray, fp8_bytes: int, threads: int = 8):
+        """Counts of the 16 e4m3 exponent values over the fp8 part of every
+        record of records (uint8 [n, record_bytes], host memory)."""
+        n, rb = records.shape
+        hist = np.zeros(16, dtype=np.uint64)
+        self._check(self.cdll.moe_codec_histogram(records.ctypes.data, n, rb, fp8_bytes,
+                                                  hist.ctypes.data, threads), "moe_codec_histogram")
+        return hist
+
+    def codec_bound(self, record_bytes: int, fp8_bytes: int) -> int:
+        return int(self.cdll.moe_codec_bound(record_bytes, fp8_bytes))
+
+    def codec_encode(self, records: np.ndarray, fp8_bytes: int, lengths, dst: np.ndarray,
+                     threads: int = 8):
+        """Code every record of records into dst (uint8, host); returns
+        (bytes used, record offsets int64 [n+1], block offsets uint32 [n, nblk+1])."""
+        n, rb = records.shape
+        nblk = fp8_bytes // 8192
+        ln = np.ascontiguousarray(lengths, dtype=np.uint8)
+        rec_off = np.zeros(n + 1, dtype=np.int64)
+        blk_off = np.zeros((n, nblk + 1), dtype=np.uint32)
+        used = int(self.cdll.moe_codec_encode(records.ctypes.data, n, rb, fp8_bytes,
+                                              ln.ctypes.data, dst.ctypes.data, dst.nbytes,
+                                              rec_off.ctypes.data, blk_off.ctypes.data, threads))
+        if used < 0:
+            self._check(used, "moe_codec_encode")
+        return used, rec_off, blk_off
+
+    def codec_table(self, lengths) -> np.ndarray:
+        ln = np.ascontiguousarray(lengths, dtype=np.uint8)
+        lut = np.zeros(256, dtype=np.uint8)
+        self._check(self.cdll.moe_codec_table(ln.ctypes.data, lut.ctypes.data), "moe_codec_table")
+        return lut
+
+    def fetch_coded(self, pool_dev_ptr: int, rec_off, blk_off, record_bytes: int, fp8_bytes: int,
+                    lut, fetch_expert, fetch_slot, nmiss, max_jobs: int, cache,
+                    workgroups: int = 32) -> None:
+        """Decode coded records fetch_expert[j] into cache slots fetch_slot[j],
+        j < nmiss[0] (device tensors); cache uint8 [slots, >= record_bytes]."""
+        self._check(self.cdll.moe_fetch_coded(
+            pool_dev_ptr, rec_off.data_ptr(), blk_off.data_ptr(), record_bytes, fp8_bytes,
+            lut.data_ptr(), fetch_expert.data_ptr(), fetch_slot.data_ptr(), nmiss.data_ptr(),
+            max_jobs, cache.data_ptr(), cache.stride(0) * cache.element_size(), workgroups,
+            self.stream()), "moe_fetch_coded")
 
     def unpermute(self, y, pair_pos, weights, out) -> None:
         T, K = weights.shape

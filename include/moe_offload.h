@@ -293,6 +293,58 @@ int moe_shared_down(const void* act, const float* sig, const void* w_down,
 int moe_all_finite(const void* x, int32_t dtype, int64_t n, int32_t* flag,
                    void* stream);
 
+/* ------------------------------------------------------------------------
+ * Entropy-coded records.  The reference stores host records raw
+ * (bin/offload.py:603, 3,146,496 B per expert) and the decode step is bound
+ * by moving them (its fetch, csrc/fetch_experts.cu:49-94).  A coded pool
+ * holds the same records with the fp8 bytes' exponent nibble Huffman-coded
+ * (blocks of 8192 bytes; sign and mantissa raw; the bytes after the fp8
+ * part raw), about 84 % of the size for block-scaled weights, and
+ * moe_fetch_coded decodes it on the GPU into cache slots identical to those
+ * moe_fetch fills from the raw pool.  Format: codec.hip.  No counterpart in
+ * the reference; an opt-in host pool format.
+ * ---------------------------------------------------------------------- */
+
+/* Counts of the 16 exponent values over the first fp8_bytes of each of the
+ * n_records records (host memory) into hist[16]. */
+int moe_codec_histogram(const void* records, int64_t n_records,
+                        int64_t record_bytes, int64_t fp8_bytes,
+                        uint64_t* hist, int32_t threads);
+
+/* Largest coded size of one record (bytes), or -1 if fp8_bytes is not a
+ * positive multiple of 8192. */
+int64_t moe_codec_bound(int64_t record_bytes, int64_t fp8_bytes);
+
+/* Code n_records records into dst (host): code_lengths[16] are the exponent
+ * code lengths (1..8 bits, a prefix code).  Writes rec_offset[n + 1] (each
+ * record's byte offset in dst, 256-aligned; the last is the total) and
+ * blk_offset[n][nblk + 1] (each block's offset within its record; the last
+ * is the raw tail's).  Returns the bytes used, or MOE_EINVAL. */
+int64_t moe_codec_encode(const void* records, int64_t n_records,
+                         int64_t record_bytes, int64_t fp8_bytes,
+                         const uint8_t* code_lengths, void* dst,
+                         int64_t dst_capacity, int64_t* rec_offset,
+                         uint32_t* blk_offset, int32_t threads);
+
+/* The decoder's 256-entry table for code_lengths: entry p = length << 4 |
+ * symbol of the code that the stream bits p (least significant first)
+ * start with. */
+int moe_codec_table(const uint8_t* code_lengths, uint8_t* lut);
+
+/* moe_fetch for a coded pool: job j < min(*nmiss, max_jobs) decodes coded
+ * record fetch_expert[j] into cache slot fetch_slot[j] (slot_bytes apart).
+ * pool: device address of the page-locked coded pool (256-byte aligned);
+ * rec_offset, blk_offset, lut: device copies of moe_codec_encode's and
+ * moe_codec_table's outputs.  Job lists are read on the device, so a
+ * captured call serves new misses on every replay.  workgroups: grid size
+ * (4 waves each, one 8192-byte block per wave at a time). */
+int moe_fetch_coded(const void* pool, const int64_t* rec_offset,
+                    const uint32_t* blk_offset, int64_t record_bytes,
+                    int64_t fp8_bytes, const uint8_t* lut,
+                    const int32_t* fetch_expert, const int32_t* fetch_slot,
+                    const int32_t* nmiss, int32_t max_jobs, void* cache,
+                    int64_t slot_bytes, int32_t workgroups, void* stream);
+
 /* The MoE block's shared expert as one argument: bf16 weights w_gate and
  * w_up [inter, hidden], w_down [hidden, inter], w_sgate [hidden], all
  * 16-byte aligned. */

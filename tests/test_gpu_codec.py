@@ -1,0 +1,93 @@
+"""Fetch of entropy-coded records on the GPU: the cache slots it fills equal
+the raw records byte for byte (the closed form: decoding is the identity on
+the stored bytes), for miss lists read on the device, under graph replay
+with the lists changing, and for a record layout with a padded tail."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import say
+
+pytestmark = pytest.mark.gpu
+
+
+def _raw_records(n, H, I, seed):
+    import synth
+    from hostpool import RecordLayout
+    lay = RecordLayout(H, I)
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    w13, s13 = synth.quantize_blocks(torch.randn((n, 2 * I, H), generator=g) * 0.02)
+    w2, s2 = synth.quantize_blocks(torch.randn((n, H, I), generator=g) * 0.02)
+    rec = lay.pack(w13, s13, w2, s2).numpy()
+    if lay.record_bytes > lay.payload_bytes:
+        rec[:, lay.payload_bytes:] = np.arange(lay.record_bytes - lay.payload_bytes) % 251
+    return lay, rec
+
+
+@pytest.mark.parametrize("H,I,n,workgroups", [(2048, 512, 24, 32), (256, 128, 40, 3)])
+def test_coded_fetch_fills_slots_with_the_raw_records(lib, dev, H, I, n, workgroups):
+    import codec
+    lay, raw = _raw_records(n, H, I, H + n)
+    pool = codec.CodedPool(raw, lay, dev)
+    say(f"coded fetch: H={H} I={I} n={n} ratio {pool.ratio:.4f}")
+    C = 12
+    cache = torch.zeros((C, lay.record_bytes), dtype=torch.uint8, device=dev)
+    rng = np.random.default_rng(7)
+    try:
+        for jobs in (1, 3, 8):
+            experts = rng.choice(n, jobs, replace=False)
+            slots = rng.choice(C, jobs, replace=False)
+            cache.fill_(0xAB)
+            fe = torch.tensor(experts, dtype=torch.int32, device=dev)
+            fs = torch.tensor(slots, dtype=torch.int32, device=dev)
+            nm = torch.tensor([jobs], dtype=torch.int32, device=dev)
+            pool.fetch(cache, fe, fs, nm, max_jobs=8, workgroups=workgroups)
+            torch.cuda.synchronize()
+            got = cache.cpu().numpy()
+            for e, s in zip(experts, slots):
+                assert np.array_equal(got[s], raw[e]), f"slot {s} != record {e} (jobs {jobs})"
+            for s in set(range(C)) - set(slots.tolist()):
+                assert (got[s] == 0xAB).all(), f"slot {s} written without a job"
+    finally:
+        pool.close()
+
+
+def test_coded_fetch_in_a_graph_with_changing_lists(lib, dev):
+    import codec
+    lay, raw = _raw_records(16, 2048, 512, 11)
+    pool = codec.CodedPool(raw, lay, dev)
+    C = 8
+    cache = torch.zeros((C, lay.record_bytes), dtype=torch.uint8, device=dev)
+    fe = torch.zeros(8, dtype=torch.int32, device=dev)
+    fs = torch.zeros(8, dtype=torch.int32, device=dev)
+    nm = torch.zeros(1, dtype=torch.int32, device=dev)
+    try:
+        s = torch.cuda.Stream(device=dev)
+        s.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(s):
+            pool.fetch(cache, fe, fs, nm, max_jobs=8)
+        torch.cuda.current_stream(dev).wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            pool.fetch(cache, fe, fs, nm, max_jobs=8)
+        rng = np.random.default_rng(3)
+        for r in range(5):
+            jobs = int(rng.integers(0, 9))
+            experts = rng.choice(16, jobs, replace=False)
+            slots = rng.choice(C, jobs, replace=False)
+            fe[:jobs] = torch.tensor(experts, dtype=torch.int32)
+            fs[:jobs] = torch.tensor(slots, dtype=torch.int32)
+            nm.fill_(jobs)
+            cache.zero_()
+            torch.cuda.synchronize()
+            say(f"coded fetch graph replay {r}: {jobs} jobs")
+            g.replay()
+            torch.cuda.synchronize()
+            got = cache.cpu().numpy()
+            for e, sl in zip(experts, slots):
+                assert np.array_equal(got[sl], raw[e]), (r, e, sl)
+            for sl in set(range(C)) - set(slots.tolist()):
+                assert not got[sl].any()
+    finally:
+        pool.close()
