@@ -100,27 +100,38 @@ def link_peak(pools, dev, chunk_mib: int = 256, reps: int = 8) -> float:
     return len(srcs) * nb / (a.elapsed_time(b) / 1000.0) / 1e9
 
 
-def fetch_standalone(lib, pools, dev, jobs: int = 8, reps: int = 160, bpj: int = 2):
+def fetch_standalone(lib, pools, dev, jobs: int = 8, reps: int = 160, bpj: int = 2,
+                     coded=None, workgroups: int = 32):
     """Average duration of one fetch launch moving `jobs` distinct records,
-    rotating over every layer's pool (HIP events on the launch stream)."""
+    rotating over every layer's pool (HIP events on the launch stream).
+    With `coded` (one CodedPool per pool), the coded fetch of the same lists;
+    returns (seconds, record bytes, coded bytes read) per launch."""
     import numpy as np
     import torch
     RB = pools[0].layout.record_bytes
     L = len(pools)
     cache = torch.zeros((jobs, RB), dtype=torch.uint8, device=dev)
     rng = np.random.default_rng(7)
-    lists = torch.tensor(np.stack([rng.choice(pools[0].n, jobs, replace=False)
-                                   for _ in range(reps)]), dtype=torch.int32, device=dev)
+    lists_np = np.stack([rng.choice(pools[0].n, jobs, replace=False) for _ in range(reps)])
+    lists = torch.tensor(lists_np, dtype=torch.int32, device=dev)
     fslot = torch.arange(jobs, dtype=torch.int32, device=dev)
     nmiss = torch.tensor([jobs], dtype=torch.int32, device=dev)
-    pairs = [p.fetch_pair(cache) for p in pools]
+    if coded is None:
+        pairs = [p.fetch_pair(cache) for p in pools]
+        launch = lambda r: lib.fetch([pairs[r % L]], lists[r], fslot, nmiss, jobs, bpj)
+        read = jobs * RB
+    else:
+        launch = lambda r: coded[r % L].fetch(cache, lists[r], fslot, nmiss, jobs, workgroups)
+        offs = [c.rec_off.cpu().numpy() for c in coded]
+        read = float(np.mean([sum(int(offs[r % L][e + 1] - offs[r % L][e]) for e in lists_np[r])
+                              for r in range(reps)]))
     for r in range(4):
-        lib.fetch([pairs[r % L]], lists[r], fslot, nmiss, jobs, bpj)
+        launch(r)
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for r in range(reps):
-        lib.fetch([pairs[r % L]], lists[r], fslot, nmiss, jobs, bpj)
+        launch(r)
     b.record()
     torch.cuda.synchronize()
     dt = a.elapsed_time(b) / 1000.0 / reps
@@ -130,7 +141,9 @@ def fetch_standalone(lib, pools, dev, jobs: int = 8, reps: int = 160, bpj: int =
     for j, e in enumerate(last):
         if not torch.equal(cache[j].cpu(), src[e]):
             raise RuntimeError(f"fetch verification failed: slot {j} != expert {e}")
-    return dt, jobs * RB
+    if coded is None:
+        return dt, jobs * RB
+    return dt, jobs * RB, read
 
 
 # ------------------------------------------------------------ kernel probes
@@ -422,7 +435,8 @@ def fill_pool_bytes(pool, dev, seed: int, chunk: int = 64) -> None:
 
 
 def run_probe(args) -> int:
-    """--probe gemv|fetch|copy|grouped|shared: the named kernel(s) alone, many launches, one JSON line."""
+    """--probe gemv|fetch|codec|copy|grouped|shared: the named kernel(s) alone, many launches,
+    one JSON line."""
     import torch
     import hipfetch
     from hostpool import DRAMA3, HostPool
@@ -441,6 +455,23 @@ def run_probe(args) -> int:
         res = {"probe": "fetch", "what": "8 records of 3,146,496 B per launch from 4 page-locked "
                "pools of 256 records", "us_per_launch": round(1e6 * dt, 2),
                "bytes_per_launch": nbytes, "GBps": round(nbytes / dt / 1e9, 3)}
+        for p in pools:
+            p.close()
+    elif args.probe == "codec":
+        # the coded fetch of the same launches as --probe fetch
+        import codec
+        pools = [HostPool(256, DRAMA3) for _ in range(4)]
+        for i, p in enumerate(pools):
+            fill_pool_bytes(p, dev, i)
+        coded = [codec.CodedPool(p.array, DRAMA3, dev, threads=16) for p in pools]
+        dt, nbytes, read = fetch_standalone(lib, pools, dev, reps=args.steps, coded=coded)
+        res = {"probe": "codec", "what": "8 entropy-coded records (3,146,496 B decoded) per "
+               "launch from 4 coded page-locked pools of 256 records, decoded into HBM",
+               "us_per_launch": round(1e6 * dt, 2), "bytes_per_launch": nbytes,
+               "coded_bytes_read": int(read), "ratio": round(read / nbytes, 4),
+               "GBps_decoded": round(nbytes / dt / 1e9, 3), "GBps_link": round(read / dt / 1e9, 3)}
+        for c in coded:
+            c.close()
         for p in pools:
             p.close()
     elif args.probe == "grouped":
@@ -557,6 +588,52 @@ def moe_block_bench(lib, cfg, pools, dev, steps: int, warmup: int):
     }
 
 
+def coded_bench(lib, cfg, hc, dev, steps: int, warmup: int):
+    """The headline decode step with every layer's records also held
+    entropy-coded in page-locked memory and fetched through the coded fetch
+    (same schedule and cache size), plus the coded fetch alone on the
+    standalone launches.  The cache receives the same bytes, so the step's
+    output must equal the raw-pool step's after the same replays."""
+    import torch
+    import decode
+    t0 = time.perf_counter()
+    coded = decode.build_coded_pools(hc.pools, hc.layout, dev)
+    enc_s = time.perf_counter() - t0
+    ratio = sum(c.coded_bytes for c in coded) / sum(c.raw_bytes for c in coded)
+    f_dt, f_bytes, f_read = fetch_standalone(lib, hc.pools, dev, coded=coded)
+    cfgc = decode.DecodeConfig(**{**cfg.__dict__, "coded_pool": True})
+    hcc = decode.DecodeHarness(cfgc, dev, pools=hc.pools, coded=coded)
+    hcc.capture()
+    hcc.replay(warmup)
+    torch.cuda.synchronize()
+    h0, m0 = hcc.hit_rate()
+    dt = timed_replays(hcc, steps)
+    h1, m1 = hcc.hit_rate()
+    same = bool(torch.equal(hcc.x, hc.x))
+    hcc.graph = None
+    hcc.pools = []
+    hcc.close()                                  # frees the coded pools
+    del hcc
+    torch.cuda.empty_cache()
+    return {
+        "workload": "the headline decode step, misses fetched from entropy-coded host records "
+                    "(exponent nibbles Huffman-coded per 8 KiB block, decoded on the GPU into "
+                    "the same cache slots); one hipGraph",
+        "tokens_per_s": round(steps / dt, 3),
+        "ms_per_step": round(1e3 * dt / steps, 4),
+        "hit_rate": round((h1 - h0) / max(1, (h1 - h0) + (m1 - m0)), 4),
+        "ratio": round(ratio, 4),
+        "encode_s": round(enc_s, 1),
+        "x_equal_raw_pool_step": same,
+        "fetch": {"us_per_launch": round(1e6 * f_dt, 2), "bytes_per_launch": f_bytes,
+                  "coded_bytes_read": int(f_read),
+                  "GBps_decoded": round(f_bytes / f_dt / 1e9, 3),
+                  "GBps_link": round(f_read / f_dt / 1e9, 3),
+                  "what": "moe fetch_coded_kernel, same 8-record launches as the raw fetch "
+                          "roofline, 32 workgroups of 4 waves"},
+    }
+
+
 def cpu_baseline(harness, budget_s: float):
     import torch
     from oracle import cpu_moe
@@ -611,7 +688,7 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the prefill and all-resident measurements")
     ap.add_argument("--tokens", type=int, default=512, help="tokens per call of --probe grouped")
-    ap.add_argument("--probe", choices=["gemv", "fetch", "copy", "grouped", "shared"],
+    ap.add_argument("--probe", choices=["gemv", "fetch", "codec", "copy", "grouped", "shared"],
                     help="time one kernel alone (--steps launches) instead of the decode step")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -671,6 +748,15 @@ def main() -> int:
         log("CPU baseline")
         cpu = cpu_baseline(hc, args.cpu_budget)
         log(f"CPU baseline {cpu['value']} tok/s on {cpu['cores']} threads")
+
+    coded = None
+    if not args.no_extra:
+        log("entropy-coded pools: encoding 40 layers")
+        coded = coded_bench(lib, cfg, hc, dev, args.steps, args.warmup)
+        log(f"coded: {coded['tokens_per_s']} tok/s, {coded['ms_per_step']} ms/step, ratio "
+            f"{coded['ratio']}, fetch {coded['fetch']['us_per_launch']} us/launch "
+            f"({coded['fetch']['GBps_decoded']} GB/s decoded, {coded['fetch']['GBps_link']} GB/s "
+            f"link), output equal to the raw-pool step: {coded['x_equal_raw_pool_step']}")
 
     hc.graph = None
     del hc.cache, hc.views
@@ -768,6 +854,7 @@ def main() -> int:
         "hbm_measured_GBps": streams,
         "cpu_baseline": cpu,
         "moe_block": block,
+        "coded_pool": coded,
         "prefill": prefill,
         "all_resident": resident,
         "finite_output": x_ok,

@@ -30,6 +30,10 @@ replay.
 mode "cached": per-layer cache of `capacity` packed records, LRU on device.
 mode "nocache": every routed expert is fetched on every step (0 % hit; the
 reference's uncached per-expert transfer), into 8 fixed slots.
+
+With `coded_pool`, each layer's records are also held entropy-coded in host
+memory (codec.CodedPool) and the fetch decodes them into the same cache
+slots (moe_fetch_coded): the same bytes land in HBM, fewer cross the link.
 """
 from __future__ import annotations
 
@@ -61,6 +65,8 @@ class DecodeConfig:
     noncoherent_pool: bool = False
     shared_expert: bool = False     # the MoE block's gated bf16 shared expert
     shared_inter: int = 512
+    coded_pool: bool = False        # fetch from entropy-coded host records
+    coded_workgroups: int = 32
 
 
 def fill_pool_on_gpu(pool: HostPool, seed: int, layer: int, device, chunk: int = 64,
@@ -79,7 +85,8 @@ def fill_pool_on_gpu(pool: HostPool, seed: int, layer: int, device, chunk: int =
 
 
 class DecodeHarness:
-    def __init__(self, cfg: DecodeConfig, device=None, pools: list[HostPool] | None = None):
+    def __init__(self, cfg: DecodeConfig, device=None, pools: list[HostPool] | None = None,
+                 coded: list | None = None):
         self.cfg = cfg
         self.lib = hipfetch.require()
         self.dev = torch.device(device or "cuda:0")
@@ -133,6 +140,13 @@ class DecodeHarness:
         ws = self.lib.fp8_moe_workspace(1, K, C, H, cfg.inter)
         self.ws = torch.empty(ws, dtype=torch.uint8, device=dev)
         self.pairs = [p.fetch_pair(c) for p, c in zip(self.pools, self.cache)]
+        self.coded = None
+        if cfg.coded_pool:
+            if coded is None:
+                coded = build_coded_pools(self.pools, self.layout, dev)
+            if len(coded) != L:
+                raise ValueError(f"{len(coded)} coded pools for {L} layers")
+            self.coded = coded
         if cfg.shared_expert:
             # seeded bf16 shared experts, resident (6 MiB per layer at 2048 x 512)
             g2 = torch.Generator(device=dev).manual_seed(cfg.seed + 3)
@@ -177,14 +191,12 @@ class DecodeHarness:
                               self.ids[l], self.wts[l], self.slot_of[l], self.slot_expert[l],
                               self.stamp[l], self.step[l], self.out_slot[l], self.fslot[l],
                               self.fexp[l], self.nmiss[l], self.stats[l])
-            lib.fetch([self.pairs[l]], self.fexp[l], self.fslot[l], self.nmiss[l],
-                      max_jobs=cfg.top_k, blocks_per_job=cfg.blocks_per_job)
+            self.fetch(l, self.fexp[l], self.fslot[l], self.nmiss[l])
             slots = self.out_slot[l]
         else:
             lib.router_topk(self.h, self.gate[l], self.bias_live[l], cfg.top_k, self.logits[l],
                             self.ids[l], self.wts[l])
-            lib.fetch([self.pairs[l]], self.ids[l].view(-1), self.fixed_slots.view(-1),
-                      self.all_miss, max_jobs=cfg.top_k, blocks_per_job=cfg.blocks_per_job)
+            self.fetch(l, self.ids[l].view(-1), self.fixed_slots.view(-1), self.all_miss)
             slots = self.fixed_slots
         if cfg.shared_expert:
             # x = h + (routed + shared): the whole block in the two decode launches
@@ -194,6 +206,17 @@ class DecodeHarness:
             # x = h + MoE(h), the residual add fused into the down kernel
             lib.fp8_moe_forward(self.h, slots, self.wts[l], w13, s13, w2, s2, self.x, self.ws,
                                 residual=self.h)
+
+    def fetch(self, l: int, experts, slots, nmiss) -> None:
+        """Layer l's miss fetch: records experts[j] into cache slots slots[j],
+        j < nmiss[0], raw or entropy-coded."""
+        cfg = self.cfg
+        if self.coded is not None:
+            self.coded[l].fetch(self.cache[l], experts, slots, nmiss, max_jobs=cfg.top_k,
+                                workgroups=cfg.coded_workgroups)
+        else:
+            self.lib.fetch([self.pairs[l]], experts, slots, nmiss, max_jobs=cfg.top_k,
+                           blocks_per_job=cfg.blocks_per_job)
 
     def step_eager(self) -> None:
         # every step starts from the same input token state (the stub has no
@@ -242,3 +265,16 @@ class DecodeHarness:
         for p in self.pools:
             p.close()
         self.pools = []
+        for c in self.coded or []:
+            c.close()
+        self.coded = None
+
+
+def build_coded_pools(pools: list[HostPool], layout: RecordLayout, device, threads: int = 16):
+    """One CodedPool per layer from the raw pools (each coded with its own
+    layer's code lengths), sharing one encode scratch buffer."""
+    import codec
+    need = hipfetch.require().codec_bound(layout.record_bytes, layout.off_s13) * max(p.n for p in pools)
+    scratch = np.empty(need, dtype=np.uint8)
+    return [codec.CodedPool(p.array, layout, device, threads=threads, scratch=scratch)
+            for p in pools]

@@ -345,7 +345,7 @@ class Native:
 
     def codec_table(self, lengths) -> np.ndarray:
         ln = np.ascontiguousarray(lengths, dtype=np.uint8)
-        lut = np.zeros(256, dtype=np.uint8)
+        lut = np.zeros(4096, dtype=np.uint16)
         self._check(self.cdll.moe_codec_table(ln.ctypes.data, lut.ctypes.data), "moe_codec_table")
         return lut
 

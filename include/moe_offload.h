@@ -316,7 +316,7 @@ int moe_codec_histogram(const void* records, int64_t n_records,
 int64_t moe_codec_bound(int64_t record_bytes, int64_t fp8_bytes);
 
 /* Code n_records records into dst (host): code_lengths[16] are the exponent
- * code lengths (1..8 bits, a prefix code).  Writes rec_offset[n + 1] (each
+ * code lengths (1..6 bits, a prefix code).  Writes rec_offset[n + 1] (each
  * record's byte offset in dst, 256-aligned; the last is the total) and
  * blk_offset[n][nblk + 1] (each block's offset within its record; the last
  * is the raw tail's).  Returns the bytes used, or MOE_EINVAL. */
@@ -326,10 +326,10 @@ int64_t moe_codec_encode(const void* records, int64_t n_records,
                          int64_t dst_capacity, int64_t* rec_offset,
                          uint32_t* blk_offset, int32_t threads);
 
-/* The decoder's 256-entry table for code_lengths: entry p = length << 4 |
- * symbol of the code that the stream bits p (least significant first)
- * start with. */
-int moe_codec_table(const uint8_t* code_lengths, uint8_t* lut);
+/* The decoder's 4096-entry table for code_lengths (at most 6 bits each):
+ * entry p = first symbol | second symbol << 4 | total length << 8 of the two
+ * codes that the stream bits p (least significant first) start with. */
+int moe_codec_table(const uint8_t* code_lengths, uint16_t* lut);
 
 /* moe_fetch for a coded pool: job j < min(*nmiss, max_jobs) decodes coded
  * record fetch_expert[j] into cache slot fetch_slot[j] (slot_bytes apart).
@@ -337,10 +337,11 @@ int moe_codec_table(const uint8_t* code_lengths, uint8_t* lut);
  * rec_offset, blk_offset, lut: device copies of moe_codec_encode's and
  * moe_codec_table's outputs.  Job lists are read on the device, so a
  * captured call serves new misses on every replay.  workgroups: grid size
- * (4 waves each, one 8192-byte block per wave at a time). */
+ * (4 waves each, one 8192-byte block per wave at a time; 24-32 measured
+ * best on MI355X). */
 int moe_fetch_coded(const void* pool, const int64_t* rec_offset,
                     const uint32_t* blk_offset, int64_t record_bytes,
-                    int64_t fp8_bytes, const uint8_t* lut,
+                    int64_t fp8_bytes, const uint16_t* lut,
                     const int32_t* fetch_expert, const int32_t* fetch_slot,
                     const int32_t* nmiss, int32_t max_jobs, void* cache,
                     int64_t slot_bytes, int32_t workgroups, void* stream);

@@ -8,7 +8,9 @@ matters is that decoding gives back exactly those bytes.  Written from the
 format's definition, not from the library's code:
 
   fp8 block of 8192 bytes x ->
-    nibble plane  4096 B: byte j = nib(x[2j]) | nib(x[2j+1]) << 4,
+    nibble plane  4096 B: nibble byte m of lane l (symbols x[128l + 2m] and
+                  x[128l + 2m + 1]) = nib(first) | nib(second) << 4, stored
+                  at 16 * (64 * (m // 16) + l) + m % 16;
                   nib(v) = (v >> 7) << 3 | (v & 7)
     header        64 B:   byte l = byte length of stream l
     streams:      stream l = exponents (v >> 3) & 15 of x[128l:128l+128],
@@ -28,6 +30,7 @@ import numpy as np
 BLOCK = 8192
 LANES = 64
 PER_LANE = BLOCK // LANES
+ALIGN = 16
 
 
 def canonical(lengths):
@@ -47,7 +50,12 @@ def encode_block(x: np.ndarray, lengths) -> bytes:
     x = np.asarray(x, dtype=np.uint8)
     assert x.size == BLOCK
     nib = ((x >> 7) << 3) | (x & 7)
-    plane = (nib[0::2] | (nib[1::2] << 4)).astype(np.uint8).tobytes()
+    pairs = (nib[0::2] | (nib[1::2] << 4)).astype(np.uint8)      # [lane * 64 + m]
+    plane = bytearray(BLOCK // 2)
+    for lane in range(LANES):
+        for m in range(PER_LANE // 2):
+            plane[16 * (LANES * (m // 16) + lane) + m % 16] = pairs[lane * (PER_LANE // 2) + m]
+    plane = bytes(plane)
     codes = canonical(lengths)
     header = bytearray()
     streams = bytearray()
@@ -62,16 +70,20 @@ def encode_block(x: np.ndarray, lengths) -> bytes:
         header.append(len(stream))
         streams.extend(stream)
     out = plane + bytes(header) + bytes(streams)
-    return out + bytes(-len(out) % 16)
+    return out + bytes(-len(out) % ALIGN)
 
 
 def decode_block(blob: bytes, lengths) -> np.ndarray:
     codes = canonical(lengths)
     by_code = {(c, ln): s for s, (c, ln) in codes.items()}
     plane = np.frombuffer(blob[:BLOCK // 2], dtype=np.uint8)
+    pairs = np.empty(BLOCK // 2, dtype=np.uint8)
+    for lane in range(LANES):
+        for m in range(PER_LANE // 2):
+            pairs[lane * (PER_LANE // 2) + m] = plane[16 * (LANES * (m // 16) + lane) + m % 16]
     nib = np.empty(BLOCK, dtype=np.uint8)
-    nib[0::2] = plane & 15
-    nib[1::2] = plane >> 4
+    nib[0::2] = pairs & 15
+    nib[1::2] = pairs >> 4
     header = blob[BLOCK // 2:BLOCK // 2 + LANES]
     pos = BLOCK // 2 + LANES
     out = np.empty(BLOCK, dtype=np.uint8)

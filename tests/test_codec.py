@@ -73,17 +73,23 @@ def test_every_byte_value_round_trips(lib):
 
 
 def test_decoder_table_matches_canonical_codes(lib):
+    """Entry p: the two codes the stream bits p (least significant first)
+    begin with, per the canonical codes of the oracle."""
     import codec
     lengths = codec.code_lengths([1, 1, 2, 3, 5, 8, 20, 60, 150, 300, 700, 1500, 3000, 4000,
                                   2500, 300])
+    assert lengths.max() <= 6
     lut = lib.codec_table(lengths)
-    codes = ocodec.canonical(lengths)
-    for p in range(256):
-        sym, ln = lut[p] & 15, lut[p] >> 4
-        c, l2 = codes[sym]
-        assert l2 == ln
-        bits = [(p >> k) & 1 for k in range(ln)]           # first ln stream bits of p
-        assert sum(b << (ln - 1 - k) for k, b in enumerate(bits)) == c
+    by_code = {v: s for s, v in ocodec.canonical(lengths).items()}
+    for p in range(4096):
+        bits = [(p >> k) & 1 for k in range(12)]
+        syms, i = [], 0
+        for _ in range(2):
+            c, ln = 0, 0
+            while (c, ln) not in by_code:
+                c, ln, i = (c << 1) | bits[i], ln + 1, i + 1
+            syms.append(by_code[(c, ln)])
+        assert lut[p] == syms[0] | syms[1] << 4 | i << 8, p
 
 
 def test_bad_codes_are_refused(lib):
@@ -95,7 +101,7 @@ def test_bad_codes_are_refused(lib):
     with pytest.raises(hipfetch.NativeError, match="no code"):
         lib.codec_encode(recs, lay.off_s13, [0] * 8 + [3] * 8, scratch)   # exponents 0..7 uncoded
     with pytest.raises(hipfetch.NativeError, match="prefix code"):
-        lib.codec_table([9] + [4] * 15)
+        lib.codec_table([7] + [4] * 15)                                     # longer than 6
 
 
 def test_synthetic_experts_code_to_about_84_percent(lib):
@@ -107,4 +113,4 @@ def test_synthetic_experts_code_to_about_84_percent(lib):
     used, _, _ = lib.codec_encode(recs, fp8, lengths, scratch)
     ratio = used / recs.nbytes
     print(f"coded / raw = {ratio:.4f}")
-    assert 0.80 < ratio < 0.87
+    assert 0.80 < ratio < 0.88

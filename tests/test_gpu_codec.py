@@ -91,3 +91,33 @@ def test_coded_fetch_in_a_graph_with_changing_lists(lib, dev):
                 assert not got[sl].any()
     finally:
         pool.close()
+
+
+@pytest.mark.parametrize("mode", ["cached", "nocache"])
+def test_decode_step_with_coded_pools_equals_raw_pools(lib, dev, mode):
+    """The captured decode step fetching from coded pools fills the same cache
+    slots with the same bytes, so every step's output and the caches equal
+    the raw-pool step's."""
+    import decode
+    cfg = decode.DecodeConfig(layers=3, n_experts=32, top_k=4, hidden=512, inter=256,
+                              capacity=10, schedule_steps=8, drift_every=4, gate_std=0.02,
+                              mode=mode)
+    raw = decode.DecodeHarness(cfg, dev)
+    cfgc = decode.DecodeConfig(**{**cfg.__dict__, "coded_pool": True, "coded_workgroups": 5})
+    cod = decode.DecodeHarness(cfgc, dev, pools=raw.pools)
+    try:
+        say(f"coded decode ({mode}): ratio {np.mean([c.ratio for c in cod.coded]):.4f}")
+        raw.capture()
+        cod.capture()
+        for s in range(6):
+            raw.replay(1)
+            cod.replay(1)
+            torch.cuda.synchronize()
+            assert torch.equal(cod.x, raw.x), f"step {s}"
+        for l in range(cfg.layers):
+            assert torch.equal(cod.cache[l], raw.cache[l]), f"layer {l} cache"
+        assert cod.hit_rate() == raw.hit_rate()
+    finally:
+        cod.pools = []
+        cod.close()
+        raw.close()
