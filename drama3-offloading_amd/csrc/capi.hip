@@ -26,9 +26,39 @@ int check_launch(const char* what) {
   return MOE_OK;
 }
 
+// For each bit pattern u of [first, first + count): the conversion unit's
+// packed e4m3x4 of (u, u with the sign flipped, u ^ 0x00400001, ~u) against
+// four f32_to_e4m3 calls; every mismatching pattern adds one to *mismatches.
+__global__ __launch_bounds__(256) void e4m3_check_kernel(uint32_t first, uint32_t count,
+                                                         unsigned long long* mismatches) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= count) return;
+  const uint32_t u = first + i;
+  const uint32_t us[4] = {u, u ^ 0x80000000u, u ^ 0x00400001u, ~u};
+  float v[4];
+  uint32_t want = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    v[k] = __builtin_bit_cast(float, us[k]);
+    want |= f32_to_e4m3(v[k]) << (8 * k);
+  }
+  if (e4m3x4(v[0], v[1], v[2], v[3]) != want) atomicAdd(mismatches, 1ull);
+}
+
 }  // namespace moe
 
 extern "C" {
+
+int moe_e4m3_check(uint32_t first, uint32_t count, uint64_t* mismatches, void* stream) {
+  MOE_REQUIRE(mismatches != nullptr, "moe_e4m3_check: mismatches is NULL");
+  MOE_REQUIRE(count >= 1 && count <= (1u << 30), "moe_e4m3_check: need 1 <= count <= 2^30");
+  MOE_REQUIRE(static_cast<uint64_t>(first) + count <= (1ull << 32),
+              "moe_e4m3_check: range past 2^32");
+  hipLaunchKernelGGL(moe::e4m3_check_kernel, dim3((count + 255) / 256), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), first, count,
+                     reinterpret_cast<unsigned long long*>(mismatches));
+  return moe::check_launch("moe_e4m3_check");
+}
 
 const char* moe_last_error(void) { return moe::g_err; }
 

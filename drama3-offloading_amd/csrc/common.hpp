@@ -67,12 +67,7 @@ __device__ __forceinline__ void silu_quantize8(const float4 (&hr)[4], bool live,
   for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
   if (live) {
     const float sc = act_scale(amax);
-    uint32_t lo = 0, hi = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) lo |= quant_e4m3(av[i], sc) << (8 * i);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) hi |= quant_e4m3(av[4 + i], sc) << (8 * i);
-    *reinterpret_cast<uint2*>(aq + j) = make_uint2(lo, hi);
+    *reinterpret_cast<uint2*>(aq + j) = make_uint2(quant4_e4m3(av, sc), quant4_e4m3(av + 4, sc));
     if ((threadIdx.x & 15) == 0) as[j >> 7] = sc;
   }
 }

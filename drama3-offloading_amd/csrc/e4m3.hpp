@@ -45,4 +45,35 @@ MOE_HOST_DEVICE uint32_t quant_e4m3(float v, float s) {
   return s == 0.0f ? 0u : c;
 }
 
+#if defined(__HIP__)
+// f32_to_e4m3 of four values, packed little-endian, on the conversion unit:
+// v_cvt_pk_fp8_f32 (OCP e4m3, round to nearest even) of each value clamped
+// to +-448 (beyond 448 the unclamped conversion gives NaN, the encoder
+// saturates), NaN inputs given the encoder's sign | 0x7f.  Equal to four
+// f32_to_e4m3 calls for every float input; moe_e4m3_check compares the two
+// on the device over any range of bit patterns.
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
+  const float v[4] = {a, b, c, d};
+  float k[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) k[i] = __builtin_amdgcn_fmed3f(v[i], -448.0f, 448.0f);
+  uint32_t w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(k[0], k[1], 0, false));
+  w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(k[2], k[3], static_cast<int>(w), true));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (v[i] != v[i]) {
+      const uint32_t nan = ((__builtin_bit_cast(uint32_t, v[i]) >> 24) & 0x80u) | 0x7fu;
+      w = (w & ~(0xffu << (8 * i))) | (nan << (8 * i));
+    }
+  }
+  return w;
+}
+
+// quant_e4m3 of v[0..3] with one scale, packed little-endian.
+__device__ __forceinline__ uint32_t quant4_e4m3(const float* v, float s) {
+  const uint32_t w = e4m3x4(v[0] / s, v[1] / s, v[2] / s, v[3] / s);
+  return s == 0.0f ? 0u : w;
+}
+#endif
+
 }  // namespace moe

@@ -55,12 +55,8 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restr
     for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
     if (i < hidden) {
       const float s = act_scale(amax);
-      uint32_t lo = 0, hi = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) lo |= quant_e4m3(v[j], s) << (8 * j);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) hi |= quant_e4m3(v[4 + j], s) << (8 * j);
-      *reinterpret_cast<uint2*>(xq + t * hidden + i) = make_uint2(lo, hi);
+      *reinterpret_cast<uint2*>(xq + t * hidden + i) =
+          make_uint2(quant4_e4m3(v, s), quant4_e4m3(v + 4, s));
       if ((threadIdx.x & 15) == 0) xs[t * (hidden >> 7) + (i >> 7)] = s;
     }
   }

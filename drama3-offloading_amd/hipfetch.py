@@ -78,6 +78,7 @@ SIGNATURES = {
     "moe_shared_gate_up": (C.c_int, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp]),
     "moe_shared_down": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "moe_all_finite": (C.c_int, [_vp, _i32, _i64, _vp, _vp]),
+    "moe_e4m3_check": (C.c_int, [C.c_uint32, C.c_uint32, _vp, _vp]),
     "moe_codec_histogram": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _i32]),
     "moe_codec_bound": (_i64, [_i64, _i64]),
     "moe_codec_encode": (_i64, [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i32]),
@@ -313,6 +314,13 @@ class Native:
         """flag[0] (int32, device) = 1 if every element of x (f32 or bf16) is finite."""
         self._check(self.cdll.moe_all_finite(x.data_ptr(), self._dtype_code(x), x.numel(),
                                              flag.data_ptr(), self.stream()), "moe_all_finite")
+
+    def e4m3_check(self, first: int, count: int, mismatches) -> None:
+        """Add to mismatches[0] (int64, device) the bit patterns of
+        [first, first + count) whose hardware e4m3 encoding differs from the
+        software encoder's (moe_e4m3_check)."""
+        self._check(self.cdll.moe_e4m3_check(first, count, mismatches.data_ptr(), self.stream()),
+                    "moe_e4m3_check")
 
     # ------------------------------------------------------------ coded pools
     def codec_histogram(self, records: np.ndarray, fp8_bytes: int, threads: int = 8):

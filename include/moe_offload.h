@@ -48,6 +48,17 @@ const char* moe_last_error(void);
 const char* moe_version(void);
 const char* moe_hip_runtime_path(void);
 
+/* Device self-check of the activation quantiser's e4m3 encoding.  The
+ * kernels quantise with the conversion unit (v_cvt_pk_fp8_f32 after a clamp
+ * to +-448, NaN kept as sign | 0x7f); this compares that, for the float bit
+ * patterns first .. first + count - 1 (1 <= count <= 2^30), with the
+ * branch-free software encoder that the CPU tests pin against the oracle's
+ * round-to-nearest-even e4m3fn (oracle/fp8.py), and adds the number of
+ * mismatching patterns to *mismatches (device uint64, not cleared here).
+ * No counterpart in the reference, whose activations are quantised by
+ * torch's float8_e4m3fn cast inside fp8_moe_forward (bin/offload.py:239). */
+int moe_e4m3_check(uint32_t first, uint32_t count, uint64_t* mismatches, void* stream);
+
 /* ------------------------------------------------------------- host pool */
 
 /* Page-locked, device-mapped host allocation for an expert pool.

@@ -61,6 +61,9 @@ def test_shared_and_block_preconditions_are_rejected_without_launching(lib):
     assert c.moe_shared_down(one, one, one, 1, 2000, 512, None, None, one, None) == -1
     assert b"multiples of 128" in c.moe_last_error()
     assert c.moe_shared_down(None, None, None, 0, 2048, 512, None, None, None, None) == 0
+    assert c.moe_e4m3_check(0, 16, None, None) == -1
+    assert c.moe_e4m3_check(0, 0, one, None) == -1
+    assert c.moe_e4m3_check(0xffffff00, 512, one, None) == -1
     assert c.moe_all_finite(one, 7, 4, one, None) == -1
     assert b"dtype" in c.moe_last_error()
     assert c.moe_all_finite(C.c_void_p(4), hipfetch.MOE_F32, 4, one, None) == -1
