@@ -458,15 +458,18 @@ def run_probe(args) -> int:
         for p in pools:
             p.close()
     elif args.probe == "codec":
-        # the coded fetch of the same launches as --probe fetch
+        # the coded fetch of 8-record launches from pools of fp8 expert
+        # weights (the byte pattern of --probe fetch does not compress)
         import codec
+        import decode
         pools = [HostPool(256, DRAMA3) for _ in range(4)]
         for i, p in enumerate(pools):
-            fill_pool_bytes(p, dev, i)
+            decode.fill_pool_on_gpu(p, 0, i, dev)
         coded = [codec.CodedPool(p.array, DRAMA3, dev, threads=16) for p in pools]
         dt, nbytes, read = fetch_standalone(lib, pools, dev, reps=args.steps, coded=coded)
         res = {"probe": "codec", "what": "8 entropy-coded records (3,146,496 B decoded) per "
-               "launch from 4 coded page-locked pools of 256 records, decoded into HBM",
+               "launch from 4 coded page-locked pools of 256 seeded N(0,0.02) fp8 expert "
+               "records, decoded into HBM",
                "us_per_launch": round(1e6 * dt, 2), "bytes_per_launch": nbytes,
                "coded_bytes_read": int(read), "ratio": round(read / nbytes, 4),
                "GBps_decoded": round(nbytes / dt / 1e9, 3), "GBps_link": round(read / dt / 1e9, 3)}
