@@ -217,11 +217,13 @@ def gemv_resident(lib, dev, layout, n_records: int = 2048, calls: int = 200, top
     return dt, top_k * layout.record_bytes + 2 * 2 * layout.hidden
 
 
-def prefill_bench(lib, harness, tokens: int = 512, passes: int = 2):
+def prefill_bench(lib, harness, tokens: int = 512, passes: int = 2, coded=None):
     """512-token prefill through all layers: router, distinct experts, one
     fetch of their records from the page-locked pool (no host sync), grouped
     FFN with the residual fused; then the grouped FFN alone on resident
-    gathered experts (HBM and MFMA figures)."""
+    gathered experts (HBM and MFMA figures).  With `coded` (one CodedPool
+    per layer), the same passes again with the experts decoded from the
+    coded pools; their output must equal the raw passes'."""
     import torch
     import synth
     from prefill import DevicePrefill
@@ -239,23 +241,35 @@ def prefill_bench(lib, harness, tokens: int = 512, passes: int = 2):
     logits = torch.zeros((tokens, E), dtype=torch.float32, device=dev)
     n_unique = torch.zeros(L, dtype=torch.int32, device=dev)
 
-    def one_pass():
+    def one_pass(from_coded=False):
         x.copy_(x0)
         for l in range(L):
             lib.router_topk(x, gate[l], None, K, logits, ids, wts)
-            pf.forward(x, ids, wts, [harness.pools[l].dev_ptr], out=y, residual=x)
+            if from_coded:
+                pf.forward(x, ids, wts, None, out=y, residual=x, coded=coded[l])
+            else:
+                pf.forward(x, ids, wts, [harness.pools[l].dev_ptr], out=y, residual=x)
             n_unique[l:l + 1].copy_(pf.n_unique)
             x.copy_(y)
 
-    one_pass()                                   # warm-up
-    torch.cuda.synchronize(dev)
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for _ in range(passes):
-        one_pass()
-    b.record()
-    torch.cuda.synchronize(dev)
-    dt = a.elapsed_time(b) / 1000.0 / passes
+    def timed(from_coded):
+        one_pass(from_coded)                     # warm-up
+        torch.cuda.synchronize(dev)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(passes):
+            one_pass(from_coded)
+        b.record()
+        torch.cuda.synchronize(dev)
+        return a.elapsed_time(b) / 1000.0 / passes
+
+    dt = timed(False)
+    coded_res = None
+    if coded is not None:
+        x_raw = x.clone()
+        c_dt = timed(True)
+        coded_res = {"ms_per_pass": round(1e3 * c_dt, 3), "tokens_per_s": round(tokens / c_dt, 1),
+                     "output_equal_raw_pool_pass": bool(torch.equal(x, x_raw))}
     uniq = n_unique.float()
     fetched = float(uniq.sum()) * harness.layout.record_bytes
     finite = bool(torch.isfinite(x.float()).all())
@@ -283,6 +297,7 @@ def prefill_bench(lib, harness, tokens: int = 512, passes: int = 2):
                         "TFLOPs": round(g_flops / g_dt / 1e12, 2),
                         "fp8_dense_peak_TFLOPs": FP8_PEAK_TFLOPS},
         "finite_output": finite,
+        "coded_pool": coded_res,
     }
 
 
@@ -596,7 +611,8 @@ def coded_bench(lib, cfg, hc, dev, steps: int, warmup: int):
     entropy-coded in page-locked memory and fetched through the coded fetch
     (same schedule and cache size), plus the coded fetch alone on the
     standalone launches.  The cache receives the same bytes, so the step's
-    output must equal the raw-pool step's after the same replays."""
+    output must equal the raw-pool step's after the same replays.  Returns
+    the result and the coded pools (the caller closes them)."""
     import torch
     import decode
     t0 = time.perf_counter()
@@ -615,7 +631,7 @@ def coded_bench(lib, cfg, hc, dev, steps: int, warmup: int):
     same = bool(torch.equal(hcc.x, hc.x))
     hcc.graph = None
     hcc.pools = []
-    hcc.close()                                  # frees the coded pools
+    hcc.coded = None                             # kept for the prefill measurement
     del hcc
     torch.cuda.empty_cache()
     return {
@@ -634,7 +650,7 @@ def coded_bench(lib, cfg, hc, dev, steps: int, warmup: int):
                   "GBps_link": round(f_read / f_dt / 1e9, 3),
                   "what": "moe fetch_coded_kernel, same 8-record launches as the raw fetch "
                           "roofline, 32 workgroups of 4 waves"},
-    }
+    }, coded
 
 
 def cpu_baseline(harness, budget_s: float):
@@ -752,10 +768,10 @@ def main() -> int:
         cpu = cpu_baseline(hc, args.cpu_budget)
         log(f"CPU baseline {cpu['value']} tok/s on {cpu['cores']} threads")
 
-    coded = None
+    coded = coded_pools = None
     if not args.no_extra:
         log("entropy-coded pools: encoding 40 layers")
-        coded = coded_bench(lib, cfg, hc, dev, args.steps, args.warmup)
+        coded, coded_pools = coded_bench(lib, cfg, hc, dev, args.steps, args.warmup)
         log(f"coded: {coded['tokens_per_s']} tok/s, {coded['ms_per_step']} ms/step, ratio "
             f"{coded['ratio']}, fetch {coded['fetch']['us_per_launch']} us/launch "
             f"({coded['fetch']['GBps_decoded']} GB/s decoded, {coded['fetch']['GBps_link']} GB/s "
@@ -783,10 +799,10 @@ def main() -> int:
     prefill = resident = None
     if not args.no_extra:
         log("prefill (512 tokens, 40 layers)")
-        prefill = prefill_bench(lib, h0c)
+        prefill = prefill_bench(lib, h0c, coded=coded_pools)
         log(f"prefill: {prefill['tokens_per_s']} tok/s, {prefill['ms_per_pass']} ms/pass, "
             f"{prefill['distinct_experts_per_layer']} experts/layer, grouped FFN "
-            f"{prefill['grouped_ffn']['us']} us")
+            f"{prefill['grouped_ffn']['us']} us; from coded pools {prefill['coded_pool']}")
         log("all-resident batched decode")
         resident = resident_bench(lib, h0c)
         log("resident: " + ", ".join(f"B={b}: {v['tokens_per_s']} tok/s"
@@ -865,6 +881,8 @@ def main() -> int:
     }
     print(json.dumps(result), flush=True)
     h0c.graph = None
+    for c in coded_pools or []:
+        c.close()
     for p in pools:
         p.close()
     return 0

@@ -21,7 +21,9 @@ steps are device launches whose sizes are read on the GPU:
 Expert storage is either the packed record pool (hostpool.HostPool, one
 buffer) or the reference's four per-layer buffers w13/w2/s13/s2
 (bin/devcache.py:170-181); `DevicePrefill` works on a list of buffers either
-way.
+way.  A packed pool may also be held entropy-coded (codec.CodedPool); the
+host part of the gather then decodes it into the same rows
+(moe_fetch_coded).
 """
 from __future__ import annotations
 
@@ -93,7 +95,8 @@ class DevicePrefill:
         return cls(bufs, views, top_k, max_tokens, experts.w13_weight.shape[2],
                    experts.w2_weight.shape[2])
 
-    def gather_experts(self, ids: torch.Tensor, host_src: list[int], cache=None) -> torch.Tensor:
+    def gather_experts(self, ids: torch.Tensor, host_src: list[int] | None, cache=None,
+                       coded=None) -> torch.Tensor:
         """Distinct experts of ids [T, K] into the gather rows (row i holds
         expert uniq[i]); returns the renumbered ids [T, K] int32 (a view of
         this object's scratch).
@@ -101,12 +104,17 @@ class DevicePrefill:
         host_src: device addresses of the page-locked host buffers, one per
         gather buffer.  cache: None, or (slot_of, cap, [cache buffer
         addresses, one per gather buffer]) to serve resident experts from the
-        device cache (hybrid gather; the table is only read)."""
+        device cache (hybrid gather; the table is only read).  coded: a
+        codec.CodedPool of the layer's records, read instead of host_src
+        (packed records only)."""
         T, K = ids.shape
         if T > self.max_tokens or K != self.K:
             raise ValueError(f"call of {T}x{K} ids exceeds the prefill scratch "
                              f"({self.max_tokens}x{self.K})")
-        if len(host_src) != len(self.gather):
+        if coded is not None:
+            if len(self.gather) != 1 or self.row_bytes[0] != coded.layout.record_bytes:
+                raise ValueError("a coded pool serves a gather buffer of packed records")
+        elif host_src is None or len(host_src) != len(self.gather):
             raise ValueError("one host buffer per gather buffer")
         P = T * K
         lib = self.lib
@@ -114,10 +122,17 @@ class DevicePrefill:
         lib.unique_inverse(ids, self.E, self.counts, self.n_unique, self.uniq, self.rank_of,
                            self.inverse[:P])
         dst = [g.data_ptr() for g in self.gather]
-        host_pairs = [(s, d, b) for s, d, b in zip(host_src, dst, self.row_bytes)]
+
+        def from_host(experts, rows, n):
+            if coded is not None:
+                coded.fetch(self.gather[0], experts, rows, n, max_jobs=self.E)
+            else:
+                pairs = [(s, d, b) for s, d, b in zip(host_src, dst, self.row_bytes)]
+                lib.fetch(pairs, experts, rows, n, max_jobs=self.E,
+                          blocks_per_job=HOST_BLOCKS_PER_JOB)
+
         if cache is None:
-            lib.fetch(host_pairs, self.uniq, self.rows, self.n_unique, max_jobs=self.E,
-                      blocks_per_job=HOST_BLOCKS_PER_JOB)
+            from_host(self.uniq, self.rows, self.n_unique)
         else:
             slot_of, cap, cache_src = cache
             if len(cache_src) != len(self.gather):
@@ -128,16 +143,15 @@ class DevicePrefill:
             cache_pairs = [(s, d, b) for s, d, b in zip(cache_src, dst, self.row_bytes)]
             lib.fetch(cache_pairs, self.cache_src, self.cache_dst, self.n_cache,
                       max_jobs=self.E, blocks_per_job=CACHE_BLOCKS_PER_JOB)
-            lib.fetch(host_pairs, self.host_expert, self.host_dst, self.n_host,
-                      max_jobs=self.E, blocks_per_job=HOST_BLOCKS_PER_JOB)
+            from_host(self.host_expert, self.host_dst, self.n_host)
         return self.inverse[:P].view(T, K)
 
     def forward(self, x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
-                host_src: list[int], cache=None, out: torch.Tensor | None = None,
-                residual: torch.Tensor | None = None) -> torch.Tensor:
+                host_src: list[int] | None, cache=None, out: torch.Tensor | None = None,
+                residual: torch.Tensor | None = None, coded=None) -> torch.Tensor:
         """MoE output [T, H] bf16 for x [T, H] with the experts read from the
-        host buffers (and, hybrid, the device cache)."""
-        local = self.gather_experts(ids, host_src, cache)
+        host buffers, or the coded pool (and, hybrid, the device cache)."""
+        local = self.gather_experts(ids, host_src, cache, coded)
         if out is None:
             out = torch.empty_like(x)
         w13, s13, w2, s2 = self.views

@@ -186,3 +186,37 @@ def test_device_prefill_is_capturable_and_dynamic(lib, dev, layer):
         want = eager.forward(x, ids_r, w_r, src, cache)
         torch.cuda.synchronize()
         assert torch.equal(out, want), f"replay {r}"
+
+
+def test_prefill_from_coded_pool_equals_raw_pool(lib, dev):
+    """The gather decoded from an entropy-coded pool fills the same rows with
+    the same bytes as the raw pool's, so the outputs are equal; a coded pool
+    refuses a gather of the reference's four buffers."""
+    import codec
+    import decode
+    from hostpool import HostPool, RecordLayout
+    from prefill import DevicePrefill
+    lay = RecordLayout(H, I)
+    pool = HostPool(E, lay)
+    decode.fill_pool_on_gpu(pool, 0, 3, dev)
+    coded = codec.CodedPool(pool.array, lay, dev)
+    try:
+        T = 48
+        x = torch.randn((T, H), device=dev).to(torch.bfloat16)
+        ids, w = _routing(T, 7, dev)
+        a = DevicePrefill.for_records(E, K, 64, dev, lay)
+        b = DevicePrefill.for_records(E, K, 64, dev, lay)
+        say(f"prefill: coded pool (ratio {coded.ratio:.3f}) vs raw pool")
+        out_a = a.forward(x, ids, w, [pool.dev_ptr])
+        out_b = b.forward(x, ids, w, None, coded=coded)
+        torch.cuda.synchronize()
+        n = int(a.n_unique)
+        assert torch.equal(a.gather[0][:n], b.gather[0][:n])
+        assert torch.equal(out_a, out_b)
+        import moe
+        four = DevicePrefill.for_experts(moe.MoEExperts(E, H, I, device="cpu"), K, 64, dev)
+        with pytest.raises(ValueError, match="packed records"):
+            four.gather_experts(ids, None, coded=coded)
+    finally:
+        coded.close()
+        pool.close()
