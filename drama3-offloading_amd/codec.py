@@ -48,19 +48,25 @@ class CodedPool:
     one page-locked, device-mapped region, plus the device-resident index
     (record offsets, block offsets) and decode table the fetch kernel reads.
 
+    layout: a RecordLayout (the packed record: its fp8 part is coded, the
+    block scales after it are kept raw), or an int: the leading bytes of each
+    record to code (e.g. the whole record of one expert's w13 buffer).
     lengths: code lengths to use (default: from this layer's own histogram).
     scratch: optional uint8 host buffer of at least codec_bound * n bytes,
     reused across layers."""
 
-    def __init__(self, records: np.ndarray, layout: RecordLayout, device, lengths=None,
+    def __init__(self, records: np.ndarray, layout: RecordLayout | int, device, lengths=None,
                  threads: int = 8, scratch: np.ndarray | None = None, noncoherent: bool = False):
         self.lib = lib = hipfetch.require()
-        self.layout = layout
+        self.layout = layout if isinstance(layout, RecordLayout) else None
         n, rb = records.shape
-        if rb != layout.record_bytes:
+        if self.layout is not None and rb != layout.record_bytes:
             raise ValueError("records do not match the layout")
         self.n = n
-        self.fp8_bytes = layout.off_s13
+        self.record_bytes = rb
+        self.fp8_bytes = layout.off_s13 if self.layout is not None else int(layout)
+        if not 0 < self.fp8_bytes <= rb:
+            raise ValueError(f"{self.fp8_bytes} coded bytes of a {rb}-byte record")
         if self.fp8_bytes % BLOCK:
             raise ValueError(f"fp8 part of {self.fp8_bytes} bytes is not a multiple of {BLOCK}")
         if lengths is None:
@@ -88,7 +94,7 @@ class CodedPool:
               workgroups: int = DEFAULT_WORKGROUPS) -> None:
         """Decode records fetch_expert[j] into cache slots fetch_slot[j],
         j < nmiss[0] (all read on the device)."""
-        self.lib.fetch_coded(self.dev_ptr, self.rec_off, self.blk_off, self.layout.record_bytes,
+        self.lib.fetch_coded(self.dev_ptr, self.rec_off, self.blk_off, self.record_bytes,
                              self.fp8_bytes, self.lut, fetch_expert, fetch_slot, nmiss, max_jobs,
                              cache, workgroups)
 

@@ -18,7 +18,9 @@ identical to bin/devcache.py:65-98) then one `moe_fetch` launch that copies
 every queued miss, all four buffers, from page-locked host memory into its
 slot, reading the miss list and count on the device at run time -- so the
 captured graph serves different experts on every replay -- then
-`fp8_moe_forward` on the whole cache buffer with slot ids.  Prefill
+`fp8_moe_forward` on the whole cache buffer with slot ids.  With CODED_POOL
+the weights of the misses come from entropy-coded host copies instead
+(two `moe_fetch_coded` launches, then the scales raw).  Prefill
 (rows != 1) goes to offload.offloaded_forward, as in the reference
 (bin/devcache.py:270-271).
 """
@@ -50,6 +52,13 @@ _dev_ptr_cache: dict[int, int] = {}
 # kernels all on the device, no host sync.  Outputs are identical.
 DEVICE_PREFILL = False
 _prefill = None
+# True: init_dev_cache also keeps the layer's w13 and w2 entropy-coded in
+# page-locked memory (codec.CodedPool, about 85 % of their size for
+# block-scaled fp8 weights) and decode misses are fetched from there,
+# decoded on the GPU (moe_fetch_coded; the scales still come raw).  The
+# cache receives the same bytes; the link carries fewer.  Costs about 0.5 s
+# per layer at init and a second page-locked copy of w13/w2.
+CODED_POOL = False
 
 
 def init_dev_cache(experts, device: torch.device, capacity: int) -> None:
@@ -85,6 +94,7 @@ def init_dev_cache(experts, device: torch.device, capacity: int) -> None:
     experts._dc_nmiss = torch.zeros(1, dtype=torch.int32, device=device)
     experts._dc_stats = torch.zeros(2, dtype=torch.int64, device=device)
     experts._dc_pairs = None
+    experts._dc_coded = _code_weights(experts, device) if CODED_POOL else None
 
 
 def reset_dev_cache(experts) -> None:
@@ -97,6 +107,20 @@ def reset_dev_cache(experts) -> None:
         lib.slots_init(experts._dc_slot_of, experts._dc_slot_expert, experts._dc_stamp,
                        experts._dc_step)
         experts._dc_stats.zero_()
+
+
+def _code_weights(experts, device):
+    """(w13, w2) of every expert as two coded pools; the host tensors must be
+    page-locked (pin_experts), which also makes them contiguous."""
+    import codec
+    n = experts.num_experts
+    pools = []
+    for host in (experts.w13_weight, experts.w2_weight):
+        if not host.is_pinned():
+            raise RuntimeError("CODED_POOL needs pinned expert tensors; run pin_experts first")
+        rec = host.view(torch.uint8).reshape(n, -1).numpy()
+        pools.append(codec.CodedPool(rec, rec.shape[1], device))
+    return tuple(pools)
 
 
 def _copy_pairs(experts):
@@ -168,8 +192,18 @@ def dev_resolve_and_fetch(experts, topk_ids: torch.Tensor) -> torch.Tensor:
     lib.resolve_slots(ids, experts._dc_slot_of, experts._dc_slot_expert, experts._dc_stamp,
                       experts._dc_step, experts._dc_out, experts._dc_fslot, experts._dc_fexp,
                       experts._dc_nmiss, experts._dc_stats)
-    lib.fetch(_fetch_pairs(experts, lib), experts._dc_fexp, experts._dc_fslot,
-              experts._dc_nmiss, max_jobs=k, blocks_per_job=CPP_BLOCKS_PER_JOB)
+    coded = getattr(experts, "_dc_coded", None)
+    if coded is None:
+        lib.fetch(_fetch_pairs(experts, lib), experts._dc_fexp, experts._dc_fslot,
+                  experts._dc_nmiss, max_jobs=k, blocks_per_job=CPP_BLOCKS_PER_JOB)
+    else:
+        # weights decoded from the coded pools, scales copied raw
+        cap = experts._dc_cap
+        for pool, cache in zip(coded, (experts._dc_w13, experts._dc_w2)):
+            pool.fetch(cache.view(torch.uint8).reshape(cap, -1), experts._dc_fexp,
+                       experts._dc_fslot, experts._dc_nmiss, max_jobs=k)
+        lib.fetch(_fetch_pairs(experts, lib)[2:], experts._dc_fexp, experts._dc_fslot,
+                  experts._dc_nmiss, max_jobs=k, blocks_per_job=CPP_BLOCKS_PER_JOB)
     return experts._dc_out[:k]
 
 

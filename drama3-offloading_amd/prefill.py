@@ -112,7 +112,7 @@ class DevicePrefill:
             raise ValueError(f"call of {T}x{K} ids exceeds the prefill scratch "
                              f"({self.max_tokens}x{self.K})")
         if coded is not None:
-            if len(self.gather) != 1 or self.row_bytes[0] != coded.layout.record_bytes:
+            if len(self.gather) != 1 or self.row_bytes[0] != coded.record_bytes:
                 raise ValueError("a coded pool serves a gather buffer of packed records")
         elif host_src is None or len(host_src) != len(self.gather):
             raise ValueError("one host buffer per gather buffer")

@@ -143,3 +143,38 @@ def test_whole_decode_layer_graph_replays_match_eager(lib, dev, pair):
         assert torch.equal(got, twin), f"replay {r}"
         assert torch.equal(host._dc_slot_of, host2._dc_slot_of)
         assert torch.equal(host._dc_stamp, host2._dc_stamp)
+
+
+def test_coded_pool_through_the_hooks_equals_raw(lib, dev, pair):
+    """devcache.CODED_POOL: the same decisions, the same cache bytes and the
+    same outputs as the raw fetch, step for step."""
+    import devcache
+    from fp8_moe import fp8_moe_forward
+    import moe
+    ref, host = pair
+    twin = moe.MoEExperts(E, H, I, device="cpu")
+    for n in ("w13_weight", "w2_weight", "w13_scale_inv", "w2_scale_inv"):
+        setattr(twin, n, getattr(host, n))          # the same pinned tensors
+    devcache.init_dev_cache(host, dev, 24)
+    devcache.CODED_POOL = True
+    try:
+        devcache.init_dev_cache(twin, dev, 24)
+    finally:
+        devcache.CODED_POOL = False
+    assert host._dc_coded is None and twin._dc_coded is not None
+    say(f"devcache coded pool: ratios {[round(p.ratio, 3) for p in twin._dc_coded]}")
+    torch.manual_seed(11)
+    for step in range(12):
+        x = torch.randn(1, H, device=dev).to(torch.bfloat16)
+        ids = torch.randperm(E, device=dev)[:K].unsqueeze(0)
+        w = torch.softmax(torch.rand(1, K, device=dev), -1)
+        outs = []
+        for m in (host, twin):
+            slots = devcache.dev_resolve_and_fetch(m, ids)
+            outs.append(fp8_moe_forward(x, slots.reshape(ids.shape), w, m._dc_w13, m._dc_s13,
+                                        m._dc_w2, m._dc_s2))
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0], outs[1]), f"step {step}"
+    for a in ("_dc_w13", "_dc_w2", "_dc_s13", "_dc_s2", "_dc_slot_of", "_dc_stamp"):
+        assert torch.equal(getattr(host, a).view(torch.uint8), getattr(twin, a).view(torch.uint8)), a
+    assert devcache.cache_stats(host) == devcache.cache_stats(twin)
