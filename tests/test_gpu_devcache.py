@@ -89,10 +89,12 @@ def test_capture_dynamic_and_bytes(lib, dev, pair):
     assert torch.equal(want, got)
 
 
-def test_whole_decode_layer_graph_replays_match_eager(lib, dev, pair):
+@pytest.mark.parametrize("coded", [False, True])
+def test_whole_decode_layer_graph_replays_match_eager(lib, dev, pair, coded):
     """route -> resolve -> fetch -> experts captured once; several replays,
     eager work and syncs in between, each checked against the same step
-    run eagerly on a twin cache."""
+    run eagerly on a twin cache (coded: the captured layer fetches from
+    coded pools, devcache.CODED_POOL, the eager twin from the raw buffers)."""
     import devcache
     import moe
     import synth
@@ -101,8 +103,13 @@ def test_whole_decode_layer_graph_replays_match_eager(lib, dev, pair):
     host2 = moe.MoEExperts(E, H, I, device="cpu")
     for n in ("w13_weight", "w2_weight", "w13_scale_inv", "w2_scale_inv"):
         setattr(host2, n, getattr(host, n))
-    devcache.init_dev_cache(host, dev, 24)
+    devcache.CODED_POOL = coded
+    try:
+        devcache.init_dev_cache(host, dev, 24)
+    finally:
+        devcache.CODED_POOL = False
     devcache.init_dev_cache(host2, dev, 24)
+    assert (host._dc_coded is not None) == coded
     gate = synth.router_weight(5, n_experts=E).to(dev)
     x_live = torch.zeros((1, H), dtype=torch.bfloat16, device=dev)
     bias = torch.zeros(E, device=dev)
