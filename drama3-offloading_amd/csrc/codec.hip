@@ -34,6 +34,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <system_error>
 #include <thread>
 #include <vector>
 
@@ -282,30 +283,46 @@ static int64_t encode_block(const uint8_t* x, const CodeTable& t, uint8_t* out) 
 
 using namespace moe;
 
+// fn(i) for i < n, each on its own thread; an index whose thread cannot be
+// started runs on the calling thread, so every started thread is joined.
+template <class F>
+static void run_threads(int n, const F& fn) {
+  std::vector<std::thread> pool;
+  pool.reserve(n);
+  int i = 0;
+  try {
+    for (; i < n; ++i) pool.emplace_back(fn, i);
+  } catch (const std::system_error&) {
+    for (; i < n; ++i) fn(i);
+  }
+  for (auto& th : pool) th.join();
+}
+
+// The host entry points below run worker threads; an allocation failure is
+// reported as MOE_EINVAL, never thrown across the C ABI.
 extern "C" int moe_codec_histogram(const void* records, int64_t n_records, int64_t record_bytes,
-                                   int64_t fp8_bytes, uint64_t* hist, int32_t threads) {
+                                   int64_t fp8_bytes, uint64_t* hist, int32_t threads) try {
   MOE_REQUIRE(records && hist, "moe_codec_histogram: NULL pointer");
   MOE_REQUIRE(n_records >= 0 && fp8_bytes >= 0 && fp8_bytes <= record_bytes,
               "moe_codec_histogram: bad sizes");
   const int nt = std::max(1, std::min<int>(threads, 64));
   std::vector<std::vector<uint64_t>> part(nt, std::vector<uint64_t>(16, 0));
-  std::vector<std::thread> pool;
-  for (int w = 0; w < nt; ++w) {
-    pool.emplace_back([&, w] {
-      for (int64_t r = w; r < n_records; r += nt) {
-        const uint8_t* x = static_cast<const uint8_t*>(records) + r * record_bytes;
-        uint64_t h[16] = {0};
-        for (int64_t i = 0; i < fp8_bytes; ++i) ++h[(x[i] >> 3) & 15];
-        for (int s = 0; s < 16; ++s) part[w][s] += h[s];
-      }
-    });
-  }
-  for (auto& th : pool) th.join();
+  run_threads(nt, [&](int w) {
+    for (int64_t r = w; r < n_records; r += nt) {
+      const uint8_t* x = static_cast<const uint8_t*>(records) + r * record_bytes;
+      uint64_t h[16] = {0};
+      for (int64_t i = 0; i < fp8_bytes; ++i) ++h[(x[i] >> 3) & 15];
+      for (int s = 0; s < 16; ++s) part[w][s] += h[s];
+    }
+  });
   for (int s = 0; s < 16; ++s) {
     hist[s] = 0;
     for (int w = 0; w < nt; ++w) hist[s] += part[w][s];
   }
   return MOE_OK;
+} catch (const std::exception& ex) {
+  set_error("moe_codec_histogram: %s", ex.what());
+  return MOE_EINVAL;
 }
 
 extern "C" int64_t moe_codec_bound(int64_t record_bytes, int64_t fp8_bytes) {
@@ -318,7 +335,7 @@ extern "C" int64_t moe_codec_bound(int64_t record_bytes, int64_t fp8_bytes) {
 extern "C" int64_t moe_codec_encode(const void* records, int64_t n_records, int64_t record_bytes,
                                     int64_t fp8_bytes, const uint8_t* code_lengths, void* dst,
                                     int64_t dst_capacity, int64_t* rec_offset,
-                                    uint32_t* blk_offset, int32_t threads) {
+                                    uint32_t* blk_offset, int32_t threads) try {
   if (!records || !code_lengths || !dst || !rec_offset || !blk_offset || n_records < 0 ||
       fp8_bytes <= 0 || fp8_bytes % kCodecBlock || record_bytes < fp8_bytes) {
     set_error("moe_codec_encode: bad arguments (fp8 bytes must be a positive multiple of %d)",
@@ -343,29 +360,26 @@ extern "C" int64_t moe_codec_encode(const void* records, int64_t n_records, int6
   std::atomic<bool> failed{false};
   for (int64_t r0 = 0; r0 < n_records && !failed; r0 += nt) {
     const int64_t r1 = std::min<int64_t>(n_records, r0 + nt);
-    std::vector<std::thread> pool;
-    for (int64_t r = r0; r < r1; ++r) {
-      pool.emplace_back([&, r] {
-        uint8_t* buf = scratch[r - r0].data();
-        const uint8_t* x = static_cast<const uint8_t*>(records) + r * record_bytes;
-        uint32_t* bo = blk_offset + r * (nblk + 1);
-        int64_t o = 0;
-        for (int64_t b = 0; b < nblk; ++b) {
-          bo[b] = static_cast<uint32_t>(o);
-          const int64_t n = encode_block(x + b * kCodecBlock, t, buf + o);
-          if (n < 0) {
-            failed = true;
-            return;
-          }
-          o += n;
+    run_threads(static_cast<int>(r1 - r0), [&](int k) {
+      const int64_t r = r0 + k;
+      uint8_t* buf = scratch[k].data();
+      const uint8_t* x = static_cast<const uint8_t*>(records) + r * record_bytes;
+      uint32_t* bo = blk_offset + r * (nblk + 1);
+      int64_t o = 0;
+      for (int64_t b = 0; b < nblk; ++b) {
+        bo[b] = static_cast<uint32_t>(o);
+        const int64_t n = encode_block(x + b * kCodecBlock, t, buf + o);
+        if (n < 0) {
+          failed = true;
+          return;
         }
-        bo[nblk] = static_cast<uint32_t>(o);      // the raw tail
-        memcpy(buf + o, x + fp8_bytes, tail);
-        o += tail;
-        size[r] = (o + 255) & ~int64_t{255};
-      });
-    }
-    for (auto& th : pool) th.join();
+        o += n;
+      }
+      bo[nblk] = static_cast<uint32_t>(o);      // the raw tail
+      memcpy(buf + o, x + fp8_bytes, tail);
+      o += tail;
+      size[r] = (o + 255) & ~int64_t{255};
+    });
     if (failed) break;
     for (int64_t r = r0; r < r1; ++r) {
       if (cursor + size[r] > dst_capacity) {
@@ -384,6 +398,9 @@ extern "C" int64_t moe_codec_encode(const void* records, int64_t n_records, int6
   }
   rec_offset[n_records] = cursor;
   return cursor;
+} catch (const std::exception& ex) {
+  set_error("moe_codec_encode: %s", ex.what());
+  return MOE_EINVAL;
 }
 
 extern "C" int moe_codec_table(const uint8_t* code_lengths, uint16_t* lut) {
