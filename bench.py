@@ -37,6 +37,7 @@ FP8_PEAK_TFLOPS = 5000.0      # dense e4m3 MFMA, MI355X
 # calibration are recorded in profiles/hbm_traffic.md.
 TRAFFIC_FETCH_BYTES = (24630 + 24582) * 1024          # host reads + HBM writes, 8 records
 TRAFFIC_GEMV_BYTES = (16686 + 8578 + 32 + 4) * 1024   # gate/up + down, 8 experts x 1 token
+TRAFFIC_CODED_BYTES = (21530 + 24582) * 1024          # coded host reads + HBM writes, 8 records
 PCIE5_X16_GBS = 64.0
 
 
@@ -606,7 +607,7 @@ def moe_block_bench(lib, cfg, pools, dev, steps: int, warmup: int):
     }
 
 
-def coded_bench(lib, cfg, hc, dev, steps: int, warmup: int):
+def coded_bench(lib, cfg, hc, dev, steps: int, warmup: int, link_peak_gbs: float):
     """The headline decode step with every layer's records also held
     entropy-coded in page-locked memory and fetched through the coded fetch
     (same schedule and cache size), plus the coded fetch alone on the
@@ -649,7 +650,14 @@ def coded_bench(lib, cfg, hc, dev, steps: int, warmup: int):
                   "GBps_decoded": round(f_bytes / f_dt / 1e9, 3),
                   "GBps_link": round(f_read / f_dt / 1e9, 3),
                   "what": "moe fetch_coded_kernel, same 8-record launches as the raw fetch "
-                          "roofline, 32 workgroups of 4 waves"},
+                          "roofline, 32 workgroups of 4 waves",
+                  "roofline": {"bound": "host-link", "achieved": round(f_read / f_dt / 1e9, 3),
+                               "peak": round(link_peak_gbs, 3), "unit": "GB/s",
+                               "frac": round(f_read / f_dt / 1e9 / link_peak_gbs, 4),
+                               "traffic": TRAFFIC_CODED_BYTES,
+                               "traffic_note": "bytes per launch (coded host reads + HBM "
+                                               "writes), PMC; achieved counts coded bytes "
+                                               "over the link"}},
     }, coded
 
 
@@ -771,7 +779,7 @@ def main() -> int:
     coded = coded_pools = None
     if not args.no_extra:
         log("entropy-coded pools: encoding 40 layers")
-        coded, coded_pools = coded_bench(lib, cfg, hc, dev, args.steps, args.warmup)
+        coded, coded_pools = coded_bench(lib, cfg, hc, dev, args.steps, args.warmup, link)
         log(f"coded: {coded['tokens_per_s']} tok/s, {coded['ms_per_step']} ms/step, ratio "
             f"{coded['ratio']}, fetch {coded['fetch']['us_per_launch']} us/launch "
             f"({coded['fetch']['GBps_decoded']} GB/s decoded, {coded['fetch']['GBps_link']} GB/s "
