@@ -48,6 +48,22 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f +
 
 // ------------------------------------------------------------ wave utils
 
+// Max over each row of 16 lanes, in every lane of the row, by DPP exchanges
+// (quad xor 1, quad xor 2, half-row mirror, row mirror): no LDS crossbar, so
+// no wait on the counter that LDS and scalar loads share.  fmaxf ignores a
+// NaN operand in any order, so this equals a shuffle butterfly bit for bit.
+__device__ __forceinline__ float row16_max_f32(float v) {
+#define MOE_DPP_MAX(CTRL)                                                                  \
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), \
+                                                          CTRL, 0xf, 0xf, false)));
+  MOE_DPP_MAX(0x0B1)   // quad_perm [1,0,3,2]
+  MOE_DPP_MAX(0x04E)   // quad_perm [2,3,0,1]
+  MOE_DPP_MAX(0x141)   // row_half_mirror
+  MOE_DPP_MAX(0x140)   // row_mirror
+#undef MOE_DPP_MAX
+  return v;
+}
+
 // SiLU(gate) * up of 8 intermediate columns j..j+7 held by one lane
 // (hr = gate[j..j+3], gate[j+4..j+7], up[j..j+3], up[j+4..j+7]) -> e4m3
 // codes and the group scale in LDS; 16 consecutive lanes form one 128-group.
@@ -63,8 +79,7 @@ __device__ __forceinline__ void silu_quantize8(const float4 (&hr)[4], bool live,
     av[i] = silu_mul(gv[i], uv[i]);
     amax = fmaxf(amax, fabsf(av[i]));
   }
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  amax = row16_max_f32(amax);
   if (live) {
     const float sc = act_scale(amax);
     *reinterpret_cast<uint2*>(aq + j) = make_uint2(quant4_e4m3(av, sc), quant4_e4m3(av + 4, sc));

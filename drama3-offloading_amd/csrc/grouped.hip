@@ -51,8 +51,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restr
 #pragma unroll
       for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
     }
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    amax = row16_max_f32(amax);
     if (i < hidden) {
       const float s = act_scale(amax);
       *reinterpret_cast<uint2*>(xq + t * hidden + i) =

@@ -72,8 +72,7 @@ __device__ __forceinline__ void quantize_x8(uint4 raw, bool live, int i,
   float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  amax = row16_max_f32(amax);
   if (live) {
     const float sc = act_scale(amax);
     *reinterpret_cast<uint2*>(xq + i) = make_uint2(quant4_e4m3(v, sc), quant4_e4m3(v + 4, sc));
