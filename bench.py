@@ -635,6 +635,17 @@ def coded_bench(lib, cfg, hc, dev, steps: int, warmup: int, link_peak_gbs: float
     hcc.coded = None                             # kept for the prefill measurement
     del hcc
     torch.cuda.empty_cache()
+    # the same at 0 % hit: every routed expert decoded from the coded pools
+    cfg0 = decode.DecodeConfig(**{**cfgc.__dict__, "mode": "nocache"})
+    h0c = decode.DecodeHarness(cfg0, dev, pools=hc.pools, coded=coded)
+    h0c.capture()
+    h0c.replay(warmup)
+    dt0 = timed_replays(h0c, steps)
+    h0c.graph = None
+    h0c.pools = []
+    h0c.coded = None
+    del h0c
+    torch.cuda.empty_cache()
     return {
         "workload": "the headline decode step, misses fetched from entropy-coded host records "
                     "(exponent nibbles Huffman-coded per 8 KiB block, decoded on the GPU into "
@@ -642,6 +653,8 @@ def coded_bench(lib, cfg, hc, dev, steps: int, warmup: int, link_peak_gbs: float
         "tokens_per_s": round(steps / dt, 3),
         "ms_per_step": round(1e3 * dt / steps, 4),
         "hit_rate": round((h1 - h0) / max(1, (h1 - h0) + (m1 - m0)), 4),
+        "tokens_per_s_0pct_hit": round(steps / dt0, 3),
+        "ms_per_step_0pct_hit": round(1e3 * dt0 / steps, 4),
         "ratio": round(ratio, 4),
         "encode_s": round(enc_s, 1),
         "x_equal_raw_pool_step": same,
@@ -780,7 +793,8 @@ def main() -> int:
     if not args.no_extra:
         log("entropy-coded pools: encoding 40 layers")
         coded, coded_pools = coded_bench(lib, cfg, hc, dev, args.steps, args.warmup, link)
-        log(f"coded: {coded['tokens_per_s']} tok/s, {coded['ms_per_step']} ms/step, ratio "
+        log(f"coded: {coded['tokens_per_s']} tok/s, {coded['ms_per_step']} ms/step "
+            f"({coded['tokens_per_s_0pct_hit']} tok/s at 0 % hit), ratio "
             f"{coded['ratio']}, fetch {coded['fetch']['us_per_launch']} us/launch "
             f"({coded['fetch']['GBps_decoded']} GB/s decoded, {coded['fetch']['GBps_link']} GB/s "
             f"link), output equal to the raw-pool step: {coded['x_equal_raw_pool_step']}")
