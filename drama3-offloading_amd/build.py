@@ -1,12 +1,20 @@
 """Build libmoeoffload.so (all HIP kernels + the C ABI) for gfx950, in-tree.
 
-    python drama3-offloading_amd/build.py [--jobs N] [--asm]
+    python drama3-offloading_amd/build.py [--jobs N] [--asm] [--asan-host]
 
 Each csrc/*.hip is compiled to an object with hipcc, then linked into one
 shared library next to this file.  The library links the HIP runtime by its
 soname, so a process that has already imported torch resolves it to torch's
 own runtime (one HIP runtime per process).  `--asm` also writes the gfx950
 assembly of each source into _build/ for inspection.
+
+`--asan-host` instead builds _build/asan/libmoeoffload.so with the host code
+(the coded-pool encoder, every precondition path) under AddressSanitizer and
+the device code as usual, for the CPU tests:
+
+    MOE_OFFLOAD_LIB=drama3-offloading_amd/_build/asan/libmoeoffload.so \
+    LD_PRELOAD=$(/opt/rocm/llvm/bin/clang -print-file-name=libclang_rt.asan-x86_64.so) \
+    ASAN_OPTIONS=detect_leaks=0 python -m pytest tests -m "not gpu"
 """
 from __future__ import annotations
 
@@ -50,35 +58,48 @@ def _run(cmd: list[str]) -> None:
         print(out, file=sys.stderr)
 
 
-def compile_one(src: Path, asm: bool) -> Path:
-    obj = BUILD / (src.stem + ".o")
-    _run([HIPCC, *DEVICE_FLAGS, "-c", str(src), "-o", str(obj)])
+# host-only AddressSanitizer: each -fsanitize= goes to the host pass alone
+ASAN_HOST_FLAGS = ["-g", "-Xarch_host", "-fsanitize=address",
+                   "-Xarch_host", "-fno-omit-frame-pointer"]
+
+
+def compile_one(src: Path, asm: bool, out_dir: Path = BUILD, extra=()) -> Path:
+    obj = out_dir / (src.stem + ".o")
+    _run([HIPCC, *DEVICE_FLAGS, *extra, "-c", str(src), "-o", str(obj)])
     if asm:
         _run([HIPCC, *DEVICE_FLAGS, "--cuda-device-only", "-S", str(src),
               "-o", str(BUILD / (src.stem + ".s"))])
     return obj
 
 
-def build(jobs: int = 8, asm: bool = False) -> Path:
+def build(jobs: int = 8, asm: bool = False, asan_host: bool = False) -> Path:
     if not Path(HIPCC).exists() and shutil.which(HIPCC) is None:
         raise RuntimeError(f"hipcc not found ({HIPCC})")
-    BUILD.mkdir(exist_ok=True)
+    out_dir = BUILD / "asan" if asan_host else BUILD
+    out_dir.mkdir(parents=True, exist_ok=True)
+    lib = out_dir / LIB.name if asan_host else LIB
+    extra = ASAN_HOST_FLAGS if asan_host else []
     srcs = sources()
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        objs = list(ex.map(lambda s: compile_one(s, asm), srcs))
-    tmp = LIB.with_suffix(".so.tmp")
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+        objs = list(ex.map(lambda s: compile_one(s, asm and not asan_host, out_dir, extra),
+                           srcs))
+    link_extra = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-shared-libasan"] \
+        if asan_host else []
+    tmp = lib.with_suffix(".so.tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *link_extra, "-o", str(tmp),
           *map(str, objs), "-ldl"])
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 1))
     ap.add_argument("--asm", action="store_true")
+    ap.add_argument("--asan-host", action="store_true",
+                    help="host code under AddressSanitizer, into _build/asan/")
     args = ap.parse_args()
-    lib = build(args.jobs, args.asm)
+    lib = build(args.jobs, args.asm, args.asan_host)
     print(lib)
 
 
