@@ -15,9 +15,10 @@
 // whole cache lines.  The block scales multiply the fp32 block result, so the
 // scale of every 128x128 weight block is applied exactly once per block.
 //
-// Kernel 1 (gate/up): grid (2I/32, pairs), two waves of 16 rows each per
-// workgroup, x quantised into LDS by the two together.  Kernel 2 (down + combine): grid (H/16, tokens),
-// one wave per k; each wave turns its h row into aq in LDS, does its 16 output
+// Kernel 1 (gate/up): grid (2I/32, pairs), four waves per workgroup: two
+// 16-row tiles, each split over K between two waves, x quantised into LDS by
+// the four together.  Kernel 2 (down + combine): grid (H/16, tokens), one
+// wave per k; each wave turns its h row into aq in LDS, does its 16 output
 // rows of w2, and the workgroup sums the k partials in order.
 #include "common.hpp"
 #include "grouped.hpp"
@@ -44,14 +45,34 @@ constexpr int kMaxHidden = 8192;
 constexpr int kMaxInter = 2048;
 constexpr int kMaxK = 16;
 
-__device__ __forceinline__ int64_t load_id(const void* ids, int ids64, int64_t p) {
-  return ids64 ? reinterpret_cast<const int64_t*>(ids)[p]
-               : static_cast<int64_t>(reinterpret_cast<const int32_t*>(ids)[p]);
+// The id and the routing weight of pair p are read without a branch on
+// their dtype: a load inside a branch is waited for inside it, and that wait
+// (vmcnt counts in issue order) would also cover every load issued before,
+// putting a memory round trip in front of the weight loads.  Both words are
+// always read (the same one twice for 32-bit ids, both halves of a float
+// weight) and the dtype only selects how they combine.  With p uniform the
+// id reads are scalar loads.
+__device__ __forceinline__ int64_t load_id(const void* ids, int ids64, int p) {
+  const int32_t* w = static_cast<const int32_t*>(ids);
+  const int i = ids64 ? 2 * p : p;
+  const uint32_t lo = static_cast<uint32_t>(w[i]);
+  const int32_t hi = w[ids64 ? i + 1 : i];
+  return ids64 ? static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | lo)
+               : static_cast<int64_t>(static_cast<int32_t>(lo));
 }
 
-__device__ __forceinline__ float load_w(const void* w, int wbf16, int64_t p) {
-  return wbf16 ? bf16_to_f32(reinterpret_cast<const uint16_t*>(w)[p])
-               : reinterpret_cast<const float*>(w)[p];
+// Routing weight of pair p as two 16-bit halves (a bf16 weight: the same
+// half twice); route_weight() combines them where the value is used.
+struct RouteHalves {
+  uint32_t lo, hi;
+};
+__device__ __forceinline__ RouteHalves load_route_halves(const void* w, int wbf16, int p) {
+  const uint16_t* w16 = static_cast<const uint16_t*>(w);
+  const int i = wbf16 ? p : 2 * p;
+  return {w16[i], w16[wbf16 ? i : i + 1]};
+}
+__device__ __forceinline__ float route_weight(RouteHalves r, int wbf16) {
+  return __uint_as_float(wbf16 ? r.lo << 16 : (r.lo | (r.hi << 16)));
 }
 
 // ------------------------------------------------------------ kernel 1
@@ -80,15 +101,30 @@ __device__ __forceinline__ void quantize_x8(uint4 raw, bool live, int i,
   }
 }
 
-// Two waves per workgroup, each 16 weight rows of one (token, expert) pair.
-// Each wave first issues the loads of its whole 16 x H weight tile (up to 16
-// K-blocks, 32 bytes per lane each, all in flight at once), then the two
-// quantise x[t] into the workgroup's LDS together (half each) while the
-// weights travel, then each runs its MFMAs.  Measured on MI355X (8 experts,
-// H 2048, I 512): 7.5 us per launch against 8.6 with four waves and 8.9
-// with one.
-constexpr int kGateUpChunk = 16;
-constexpr int kGateUpWaves = 2;
+// Two 16-row tiles of one (token, expert) pair per workgroup, each split
+// over K between kGateUpSplit waves (contiguous ranges of K-blocks).  Every
+// wave first issues the loads of its part of the tile (up to kGateUpChunk
+// K-blocks of 32 bytes per lane in flight), then the workgroup's waves
+// quantise x[t] into LDS together while the weights travel, then each runs
+// its MFMAs.  The wave with the first range owns the row sums: it
+// accumulates its K-blocks in order and then continues the same chain with
+// the block products the other waves left in LDS, so every row is the one
+// in-order sum over all K-blocks that the grouped kernel forms
+// (bit-identical outputs).
+//
+// A launch of this kernel is one pass: every wave issues its loads once, and
+// its time is the memory time plus each wave's serial instruction stream
+// (issue slots, MFMA and LDS latencies), which the loads do not hide.
+// Splitting K halves that stream and puts a wave on each of the chip's
+// 1024 SIMDs at 8 experts, 2I 1024.  Measured on MI355X (8 experts, H 2048,
+// I 512, rocprofv3 kernel durations): 6.5-6.7 us per launch against
+// 7.4-7.5 with one wave per tile and 8.9-9.1 with K split four ways;
+// reading all of a chunk's B operands before its MFMAs gained nothing
+// (the weights' arrival, not the MFMA chain, paces the loop).
+constexpr int kGateUpTiles = 2;                  // 16-row tiles per workgroup
+constexpr int kGateUpSplit = 2;                  // waves per tile
+constexpr int kGateUpWaves = kGateUpSplit * kGateUpTiles;
+constexpr int kGateUpChunk = 8;                  // K-blocks in flight per lane
 
 template <bool SHARED>
 __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
@@ -98,6 +134,8 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
     int32_t tokens, SharedRefs sh) {
   __shared__ __align__(16) uint8_t xq[kMaxHidden];
   __shared__ float xs[kMaxHidden / 128];
+  __shared__ __align__(16) float dpart[kGateUpTiles][kMaxHidden / 128][16];
+  __shared__ float spart[kGateUpTiles][kMaxHidden / 128];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   if (SHARED && blockIdx.y >= static_cast<unsigned>(tokens * top_k)) {
@@ -131,36 +169,49 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
     }
     return;
   }
-  const int64_t p = blockIdx.y;
-  const int64_t t = p / top_k;
-  const int64_t e = load_id(ids, ids64, p);
-  const bool valid = e >= 0 && e < n_experts;
-  const int rows2 = 2 * inter;
-  const int G = hidden >> 7;
-  const int r0 = (blockIdx.x * kGateUpWaves + wave) * 16;
-  const int q = lane >> 4;
-  const uint8_t* wrow =
-      w13 + (valid ? e : 0) * w13_es + static_cast<int64_t>(r0 + (lane & 15)) * hidden + q * 32;
+  // Every workgroup runs this prologue once, and all of it sits on the
+  // critical path of a launch whose loads all go out at once: 32-bit
+  // arithmetic only (a 64-bit division is ~130 scalar instructions), and
+  // x[t], which does not depend on the expert, goes out before the id.
+  const int p = blockIdx.y;
+  const int t = static_cast<int>(static_cast<uint32_t>(p) / static_cast<uint32_t>(top_k));
   // This wave's first 512 values of x[t] are loaded before the weights:
   // loads retire in issue order (vmcnt), so x issued first can be quantised
   // while the weight tile is still in flight.  No load sits under a branch
   // (lanes and blocks past the end re-read an in-bounds address and ignore
   // it): a conditional load makes the compiler's wait at the join cover
   // every load issued before it, weights included.
-  const uint16_t* xr = x + t * hidden;
+  const uint16_t* xr = x + static_cast<int64_t>(t) * hidden;
   const int i0 = wave * 512 + lane * 8;
   const uint4 xraw = *reinterpret_cast<const uint4*>(xr + (i0 < hidden ? i0 : 0));
+  const int64_t e = load_id(ids, ids64, p);
+  const bool valid = e >= 0 && e < n_experts;
+  const int rows2 = 2 * inter;
+  const int G = hidden >> 7;
+  // wave is uniform: so are the tile, the K range and the scale row, which
+  // is read with scalar loads
+  const int wu = __builtin_amdgcn_readfirstlane(wave);
+  const int tile = wu / kGateUpSplit;
+  const int part = wu % kGateUpSplit;
+  const bool owner = part == 0;          // the wave that forms the row sums
+  const int Gs = (G + kGateUpSplit - 1) / kGateUpSplit;   // K-blocks per part
+  const int gb = min(part * Gs, G);      // this wave's first K-block
+  const int gn = min(gb + Gs, G) - gb;   // and its count (0 for a part past the end)
+  const int r0 = (blockIdx.x * kGateUpTiles + tile) * 16;
+  const int q = lane >> 4;
+  const uint8_t* wrow =
+      w13 + (valid ? e : 0) * w13_es + static_cast<int64_t>(r0 + (lane & 15)) * hidden + q * 32;
   // the tile's block scales go out before the weights (loaded after them,
   // they would add a round trip between the weights' arrival and the MFMAs)
   const float* srow =
       s13 + (valid ? e : 0) * s13_es + static_cast<int64_t>(r0 >> 7) * G;
   float sw[kGateUpChunk];
 #pragma unroll
-  for (int c = 0; c < kGateUpChunk; ++c) sw[c] = srow[c < G ? c : G - 1];
+  for (int c = 0; c < kGateUpChunk; ++c) sw[c] = srow[min(gb + c, G - 1)];
   __builtin_amdgcn_sched_barrier(0);
   v8i a[kGateUpChunk];
 #pragma unroll
-  for (int c = 0; c < kGateUpChunk; ++c) a[c] = load_op32_nt(wrow + (c < G ? c : G - 1) * 128);
+  for (int c = 0; c < kGateUpChunk; ++c) a[c] = load_op32_nt(wrow + min(gb + c, G - 1) * 128);
   __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the math below
   // x[t] -> e4m3 codes + per-128 scales in LDS: 8 values per lane, 16 lanes
   // per group, the workgroup's waves taking 512-value slices in turn
@@ -171,32 +222,62 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
     quantize_x8(raw, i < hidden, i, xq, xs);
   }
   __syncthreads();
-  float* hp = h + p * rows2;
-  if (!valid) {   // no such expert: poison the rows, never read out of bounds
-    if (lane < 16) hp[r0 + lane] = __builtin_nanf("");
+  float* hp = h + static_cast<int64_t>(p) * rows2;
+  if (!valid) {   // no such expert (the whole workgroup): poison the rows, read nothing
+    if (owner && lane < 16) hp[r0 + lane] = __builtin_nanf("");
     return;
   }
+  // The block product d of K-block g (z = 0) times its scale product sc.
+  // The owner folds each into its row sums in order; the other waves
+  // leave them in LDS (lane l holds rows 4(l/16)..+3, as every lane with
+  // the same l/16 does).
   v4f acc = {0.f, 0.f, 0.f, 0.f};
-  for (int g0 = 0; g0 < G; g0 += kGateUpChunk) {
-    if (g0 > 0) {
+  for (int k0 = 0; k0 < gn; k0 += kGateUpChunk) {
+    if (k0 > 0) {
 #pragma unroll
       for (int c = 0; c < kGateUpChunk; ++c)
-        if (g0 + c < G) {
-          a[c] = load_op32_nt(wrow + (g0 + c) * 128);
-          sw[c] = srow[g0 + c];
+        if (k0 + c < gn) {
+          a[c] = load_op32_nt(wrow + (gb + k0 + c) * 128);
+          sw[c] = srow[gb + k0 + c];
         }
     }
+    if (!owner) {
 #pragma unroll
-    for (int c = 0; c < kGateUpChunk; ++c) {
-      const int g = g0 + c;
-      if (g < G) {
-        const v8i b = load_op32(xq + g * 128 + q * 32);
-        const v4f z = {0.f, 0.f, 0.f, 0.f};
-        const v4f d = mfma_e4m3_16x16x128(a[c], b, z);
-        const float sc = sw[c] * xs[g];
-        block_fma(acc, d, sc);
+      for (int c = 0; c < kGateUpChunk; ++c) {
+        const int k = k0 + c;
+        if (k < gn) {
+          const int g = gb + k;
+          const v8i b = load_op32(xq + g * 128 + q * 32);
+          const v4f z = {0.f, 0.f, 0.f, 0.f};
+          const v4f d = mfma_e4m3_16x16x128(a[c], b, z);
+          // Every lane stores: the 16 lanes of a row group hold the same
+          // four values (B's columns are all x), and a store under a lane
+          // condition would let the compiler sink the MFMA into it, where
+          // it would run under a partial exec mask.
+          *reinterpret_cast<float4*>(&dpart[tile][g][4 * q]) = make_float4(d[0], d[1], d[2], d[3]);
+          spart[tile][g] = sw[c] * xs[g];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < kGateUpChunk; ++c) {
+        const int k = k0 + c;
+        if (k < gn) {
+          const int g = gb + k;
+          const v8i b = load_op32(xq + g * 128 + q * 32);
+          const v4f z = {0.f, 0.f, 0.f, 0.f};
+          const v4f d = mfma_e4m3_16x16x128(a[c], b, z);
+          block_fma(acc, d, sw[c] * xs[g]);
+        }
       }
     }
+  }
+  __syncthreads();
+  if (!owner) return;
+  for (int g = gn; g < G; ++g) {
+    const float4 d = *reinterpret_cast<const float4*>(&dpart[tile][g][4 * q]);
+    const v4f dv = {d.x, d.y, d.z, d.w};
+    block_fma(acc, dv, spart[tile][g]);
   }
   if ((lane & 15) == 0) {
     const int r = r0 + 4 * q;
@@ -225,7 +306,7 @@ __global__ __launch_bounds__(1024) void down_gemv_kernel(
   __shared__ float spart[SHARED ? 16 : 1];
   const int wave = threadIdx.x >> 6;   // == k; SHARED: wave top_k is the shared expert's
   const int lane = threadIdx.x & 63;
-  const int64_t t = blockIdx.y;
+  const int t = blockIdx.y;
   if (SHARED && wave == top_k) {
     // the shared expert's 16 down rows of this workgroup, token t
     const int r0 = blockIdx.x * 16;
@@ -233,8 +314,7 @@ __global__ __launch_bounds__(1024) void down_gemv_kernel(
 #pragma unroll
     for (int i = 0; i < 16; ++i) rows[i] = sh.wd + static_cast<int64_t>(r0 + i) * sh.inter;
     float acc[16][1];
-    rows_dot_bf16<16, 1, 1>(rows, sh.act, sh.inter, static_cast<int>(t),
-                            static_cast<int>(t) + 1, sh.inter >> 3, lane, acc);
+    rows_dot_bf16<16, 1, 1>(rows, sh.act, sh.inter, t, t + 1, sh.inter >> 3, lane, acc);
     if (lane == 0) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) spart[i] = acc[i][0];
@@ -243,7 +323,22 @@ __global__ __launch_bounds__(1024) void down_gemv_kernel(
     __syncthreads();                  // threads 0..15 then combine, spart included
     return;
   }
-  const int64_t p = t * top_k + wave;
+  // wave is uniform, so is p: the id reads below are scalar loads
+  const int p = t * top_k + __builtin_amdgcn_readfirstlane(wave);
+  // The pair's first 512 gate and up values are loaded before the weights
+  // (loads retire in issue order), so SiLU and the quantisation run while
+  // the weight tile is in flight; they do not depend on the expert and go
+  // out before the id.
+  // No load under a branch, for the reason given in the gate/up kernel.
+  const float* hp = h + static_cast<int64_t>(p) * (2 * inter);
+  const int j0 = lane * 8 < inter ? lane * 8 : 0;
+  float4 hraw[4];
+  hraw[0] = *reinterpret_cast<const float4*>(hp + j0);
+  hraw[1] = *reinterpret_cast<const float4*>(hp + j0 + 4);
+  hraw[2] = *reinterpret_cast<const float4*>(hp + inter + j0);
+  hraw[3] = *reinterpret_cast<const float4*>(hp + inter + j0 + 4);
+  // the pair's routing weight, combined only where it is used
+  const RouteHalves wr = load_route_halves(weights, wbf16, p);
   const int64_t e = load_id(ids, ids64, p);
   const bool valid = e >= 0 && e < n_experts;
   const int Gi = inter >> 7;
@@ -251,23 +346,11 @@ __global__ __launch_bounds__(1024) void down_gemv_kernel(
   const int q = lane >> 4;
   const uint8_t* wrow =
       w2 + (valid ? e : 0) * w2_es + static_cast<int64_t>(c0 + (lane & 15)) * inter + q * 32;
-  // The pair's first 512 gate and up values are loaded before the weights
-  // (loads retire in issue order), so SiLU and the quantisation run while
-  // the weight tile is in flight.
-  // No load under a branch, for the reason given in the gate/up kernel.
-  const float* hp = h + p * (2 * inter);
-  const int j0 = lane * 8 < inter ? lane * 8 : 0;
-  float4 hraw[4];
-  hraw[0] = *reinterpret_cast<const float4*>(hp + j0);
-  hraw[1] = *reinterpret_cast<const float4*>(hp + j0 + 4);
-  hraw[2] = *reinterpret_cast<const float4*>(hp + inter + j0);
-  hraw[3] = *reinterpret_cast<const float4*>(hp + inter + j0 + 4);
-  // block scales and the pair's routing weight go out before the weights
+  // block scales go out before the weights
   const float* srow = s2 + (valid ? e : 0) * s2_es + static_cast<int64_t>(c0 >> 7) * Gi;
   float sw[kDownChunk];
 #pragma unroll
   for (int c = 0; c < kDownChunk; ++c) sw[c] = srow[c < Gi ? c : Gi - 1];
-  const float wroute = load_w(weights, wbf16, p);
   __builtin_amdgcn_sched_barrier(0);
   v8i a[kDownChunk];
 #pragma unroll
@@ -316,13 +399,13 @@ __global__ __launch_bounds__(1024) void down_gemv_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) part[wave][4 * q + i] = valid ? acc[i] : nan;
   }
-  if (lane == 0) wpart[wave] = wroute;
+  if (lane == 0) wpart[wave] = route_weight(wr, wbf16);
   __syncthreads();
   if (threadIdx.x < 16) {
     // sum = fma(w_k, y_k, sum), k in order: the combine of the grouped path too
     float sum = 0.0f;
     for (int k = 0; k < top_k; ++k) sum = fmaf(wpart[k], part[k][threadIdx.x], sum);
-    const int64_t o = t * hidden + c0 + threadIdx.x;
+    const int64_t o = static_cast<int64_t>(t) * hidden + c0 + threadIdx.x;
     uint16_t y = f32_to_bf16(sum);
     if (SHARED) {
       // out = residual + (routed + sig * shared), as moe_shared_down on the routed output
@@ -345,14 +428,14 @@ static int launch_gemv(const uint16_t* x, const void* ids, int ids64, const void
   const unsigned gx = static_cast<unsigned>((2 * inter) / 16);
   if (sh) {
     // extra rows of workgroups for the shared expert's Is + 1 rows (the last: sigmoid gate)
-    const unsigned sy =
-        static_cast<unsigned>((sh->inter + 1 + kSharedJPW * gx - 1) / (kSharedJPW * gx));
-    hipLaunchKernelGGL(gateup_gemv_kernel<true>, dim3(gx / kGateUpWaves, pairs + sy),
+    const unsigned per_y = kSharedJPW * (gx / kGateUpTiles) * kGateUpWaves;
+    const unsigned sy = static_cast<unsigned>((sh->inter + 1 + per_y - 1) / per_y);
+    hipLaunchKernelGGL(gateup_gemv_kernel<true>, dim3(gx / kGateUpTiles, pairs + sy),
                        dim3(64 * kGateUpWaves), 0, s, x, ids,
                        ids64, top_k, w13, s13, es.w13, es.s13, n_experts, hidden, inter, h,
                        tokens, *sh);
   } else {
-    hipLaunchKernelGGL(gateup_gemv_kernel<false>, dim3(gx / kGateUpWaves, pairs),
+    hipLaunchKernelGGL(gateup_gemv_kernel<false>, dim3(gx / kGateUpTiles, pairs),
                        dim3(64 * kGateUpWaves), 0, s, x, ids, ids64,
                        top_k, w13, s13, es.w13, es.s13, n_experts, hidden, inter, h, tokens,
                        SharedRefs{});

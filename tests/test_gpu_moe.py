@@ -137,6 +137,38 @@ def test_out_of_range_expert_gives_nan_not_a_fault(lib, dev):
     assert torch.isfinite(got[0]).all() and torch.isnan(got[1].float()).all()
 
 
+def test_gemv_id_and_weight_dtypes(lib, dev):
+    """The decode kernels read ids (int32/int64) and routing weights
+    (float32/bf16) without a branch on the dtype: every combination gives
+    the same output as the grouped path; an int64 id whose low word names an
+    expert but whose high word is not zero is out of range (NaN row), as
+    is -1."""
+    import synth
+    E, H, I, K = 12, 2048, 512, 8
+    host, devt = _experts(17, E, H, I, "blockq", dev)
+    for T in (1, 2):
+        x = synth.hidden_states(17 + T, T).to(dev)
+        rng = np.random.default_rng(T)
+        ids = torch.tensor(np.stack([rng.choice(E, K, replace=False) for _ in range(T)]),
+                           dtype=torch.int64, device=dev)
+        w = torch.rand((T, K), generator=torch.Generator().manual_seed(T)).to(dev)
+        w = (w / w.sum(-1, keepdim=True)).to(torch.bfloat16)      # exact in float32 too
+        say(f"moe: GEMV dtypes, {T} token(s)")
+        outs = [_run(x, i, ww, devt, mode=1) for i in (ids, ids.int()) for ww in (w, w.float())]
+        want = _run(x, ids, w.float(), devt, mode=2)
+        torch.cuda.synchronize()
+        for o in outs:
+            assert torch.equal(o, want)
+    x = synth.hidden_states(18, 3).to(dev)
+    bad = torch.tensor([[0, (1 << 32) + 1], [-1, 3], [4, 5]], dtype=torch.int64, device=dev)
+    w = torch.full((3, 2), 0.5, device=dev)
+    got = _run(x, bad, w, devt, mode=1)
+    good = _run(x[2:], bad[2:], w[2:], devt, mode=1)
+    torch.cuda.synchronize()
+    assert torch.isnan(got[:2].float()).all()
+    assert torch.equal(got[2:], good) and torch.isfinite(good.float()).all()
+
+
 def test_rejects_cpu_inputs():
     from fp8_moe import fp8_moe_forward
     x = torch.zeros((1, 256), dtype=torch.bfloat16)
