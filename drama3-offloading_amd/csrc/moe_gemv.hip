@@ -301,7 +301,7 @@ __global__ __launch_bounds__(1024) void down_gemv_kernel(
     uint16_t* __restrict__ out, SharedRefs sh) {
   __shared__ __align__(16) uint8_t aq[kMaxK][kMaxInter];
   __shared__ float as_[kMaxK][kMaxInter / 128];
-  __shared__ float part[kMaxK][16];
+  __shared__ __align__(16) float part[kMaxK][16];
   __shared__ float wpart[kMaxK];
   __shared__ float spart[SHARED ? 16 : 1];
   const int wave = threadIdx.x >> 6;   // == k; SHARED: wave top_k is the shared expert's
@@ -319,9 +319,8 @@ __global__ __launch_bounds__(1024) void down_gemv_kernel(
 #pragma unroll
       for (int i = 0; i < 16; ++i) spart[i] = acc[i][0];
     }
-    __syncthreads();                  // pairs with the routed waves' two barriers;
-    __syncthreads();                  // threads 0..15 then combine, spart included
-    return;
+    __syncthreads();   // pairs with the routed waves' barrier: threads 0..15 then
+    return;            // combine, spart included
   }
   // wave is uniform, so is p: the id reads below are scalar loads
   const int p = t * top_k + __builtin_amdgcn_readfirstlane(wave);
@@ -368,7 +367,11 @@ __global__ __launch_bounds__(1024) void down_gemv_kernel(
     hr[3] = *reinterpret_cast<const float4*>(hp + inter + jj + 4);
     silu_quantize8(hr, j < inter, j, aq[wave], as_[wave]);
   }
-  __syncthreads();
+  // aq[wave] and as_[wave] are this wave's own: its LDS accesses complete in
+  // order, so a wave-scope fence (which keeps the compiler from moving the
+  // reads above the writes) replaces a workgroup barrier
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
 
   v4f acc = {0.f, 0.f, 0.f, 0.f};
   if (valid) {
@@ -394,17 +397,30 @@ __global__ __launch_bounds__(1024) void down_gemv_kernel(
       }
     }
   }
-  if ((lane & 15) == 0) {
+  {
+    // every lane stores: the 16 lanes of a row group hold the same values,
+    // and a store under a lane condition would let the compiler sink the
+    // MFMAs into it (a partial exec mask)
     const float nan = __builtin_nanf("");
-#pragma unroll
-    for (int i = 0; i < 4; ++i) part[wave][4 * q + i] = valid ? acc[i] : nan;
+    *reinterpret_cast<float4*>(&part[wave][4 * q]) =
+        valid ? make_float4(acc[0], acc[1], acc[2], acc[3]) : make_float4(nan, nan, nan, nan);
   }
-  if (lane == 0) wpart[wave] = route_weight(wr, wbf16);
+  wpart[wave] = route_weight(wr, wbf16);
   __syncthreads();
   if (threadIdx.x < 16) {
-    // sum = fma(w_k, y_k, sum), k in order: the combine of the grouped path too
+    // sum = fma(w_k, y_k, sum), k in order: the combine of the grouped path
+    // too.  All kMaxK partials are read at once (one LDS round trip); the
+    // slots past top_k are never folded in.
+    float wk[kMaxK], yk[kMaxK];
+#pragma unroll
+    for (int k = 0; k < kMaxK; ++k) {
+      wk[k] = wpart[k];
+      yk[k] = part[k][threadIdx.x];
+    }
     float sum = 0.0f;
-    for (int k = 0; k < top_k; ++k) sum = fmaf(wpart[k], part[k][threadIdx.x], sum);
+#pragma unroll
+    for (int k = 0; k < kMaxK; ++k)
+      if (k < top_k) sum = fmaf(wk[k], yk[k], sum);
     const int64_t o = static_cast<int64_t>(t) * hidden + c0 + threadIdx.x;
     uint16_t y = f32_to_bf16(sum);
     if (SHARED) {
