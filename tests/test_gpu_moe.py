@@ -169,6 +169,29 @@ def test_gemv_id_and_weight_dtypes(lib, dev):
     assert torch.equal(got[2:], good) and torch.isfinite(good.float()).all()
 
 
+@pytest.mark.parametrize("K", [1, 3, 7, 15, 16])
+def test_gemv_any_top_k_equals_grouped(lib, dev, K):
+    """The down kernel pairs experts two to a wave; an odd top_k leaves the
+    last wave one expert, and the output still equals the grouped path's
+    bit for bit (and the oracle within the bar)."""
+    import synth
+    E, H, I, T = 20, 2048, 512, 2
+    host, devt = _experts(40 + K, E, H, I, "blockq", dev)
+    x = synth.hidden_states(40 + K, T).to(dev)
+    rng = np.random.default_rng(K)
+    ids = torch.tensor(np.stack([rng.choice(E, K, replace=False) for _ in range(T)]), device=dev)
+    w = torch.rand((T, K), generator=torch.Generator().manual_seed(K)).to(dev)
+    w = w / w.sum(-1, keepdim=True)
+    say(f"moe: GEMV top_k {K}")
+    a = _run(x, ids, w, devt, mode=1)
+    b = _run(x, ids, w, devt, mode=2)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    want = omoe.forward_w8a8(_np(x), ids.cpu().numpy(), w.cpu().numpy().astype(np.float64),
+                             *(t.numpy() for t in host))
+    assert omoe.max_rel_err(_np(a), want) <= TOL
+
+
 def test_rejects_cpu_inputs():
     from fp8_moe import fp8_moe_forward
     x = torch.zeros((1, 256), dtype=torch.bfloat16)
