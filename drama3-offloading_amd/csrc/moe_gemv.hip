@@ -612,8 +612,8 @@ static int forward_impl(const void* x, const void* ids, int32_t ids_dtype, const
   }
   MOE_REQUIRE(pairs <= 65535LL, "moe_fp8_moe_forward: too many (token, expert) pairs (%lld)",
               (long long)pairs);
-  // the shared expert rides along when its extra wave fits the down workgroup
-  if (sh && top_k + 1 > kMaxK) sh = nullptr;
+  // the shared expert rides along (the down workgroup's ceil(top_k/2) + 1
+  // waves fit its launch bounds for every top_k)
   *fused = sh != nullptr;
   return launch_gemv(static_cast<const uint16_t*>(x), ids, ids64, weights, wbf16, tokens, top_k,
                      static_cast<const uint8_t*>(w13), s13, static_cast<const uint8_t*>(w2), s2,
@@ -689,11 +689,14 @@ extern "C" int moe_fp8_moe_block_forward(const void* x, const void* ids, int32_t
                       static_cast<const uint16_t*>(shared->w_up),
                       static_cast<const uint16_t*>(shared->w_down),
                       static_cast<const uint16_t*>(shared->w_sgate), Is, act, sig};
-  if (!use_grouped(tokens, hidden, mode) && top_k + 1 <= kMaxK) {
+  if (!use_grouped(tokens, hidden, mode)) {
     // decode: the shared expert rides in the two GEMV launches, residual last
-    return forward_impl(x, ids, ids_dtype, weights, w_dtype, tokens, top_k, w13, s13, w2, s2,
-                        n_experts, hidden, inter, strides, residual, out, workspace, base, mode,
-                        &sh, &fused, stream);
+    const int rc = forward_impl(x, ids, ids_dtype, weights, w_dtype, tokens, top_k, w13, s13,
+                                w2, s2, n_experts, hidden, inter, strides, residual, out,
+                                workspace, base, mode, &sh, &fused, stream);
+    MOE_REQUIRE(rc != MOE_OK || fused,
+                "moe_fp8_moe_block_forward: the GEMV launches did not carry the shared expert");
+    return rc;
   }
   // otherwise: routed experts into out, then the shared expert adds to it in place
   int rc = forward_impl(x, ids, ids_dtype, weights, w_dtype, tokens, top_k, w13, s13, w2, s2,

@@ -380,7 +380,7 @@ size_t moe_fp8_moe_block_workspace(int32_t tokens, int32_t top_k,
  * arguments and the shared terms those of moe_shared_gate_up/_down, bit for
  * bit.  On the per-pair GEMV path (decode) the shared expert is carried by
  * the two routed launches: extra workgroups of the gate/up launch and one
- * extra wave per workgroup of the down launch (needs top_k <= 15).  A
+ * extra wave per workgroup of the down launch.  A
  * grouped call runs the routed experts, then the two shared-expert kernels
  * on its output.  No counterpart in the reference: upstream's MoE block
  * calls the expert forward (bin/devcache.py:275-277) and the shared expert

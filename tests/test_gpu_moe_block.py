@@ -100,7 +100,7 @@ def _routed_experts(seed, E, H, I, dev):
                                       (3, 8, 1), (1, 8, 2)])
 def test_block_forward_equals_composition(lib, dev, T, K, mode):
     """moe_fp8_moe_block_forward (the shared expert carried by the decode
-    launches when T <= 2 and K <= 15) against the composition of the three
+    launches when T <= 2) against the composition of the three
     separate calls, bit for bit, with and without the residual."""
     E, H, I, Is = 24, 2048, 512, 512
     w13, s13, w2, s2 = _routed_experts(T * 31 + K, E, H, I, dev)
