@@ -45,6 +45,14 @@ __global__ __launch_bounds__(256) void e4m3_check_kernel(uint32_t first, uint32_
   if (e4m3x4(v[0], v[1], v[2], v[3]) != want) atomicAdd(mismatches, 1ull);
 }
 
+// out[i] = silu_mul(g[i], u[i]), the expert kernels' SiLU(gate) * up.
+__global__ __launch_bounds__(256) void silu_check_kernel(const float* __restrict__ g,
+                                                         const float* __restrict__ u,
+                                                         float* __restrict__ out, uint32_t n) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) out[i] = silu_mul(g[i], u[i]);
+}
+
 }  // namespace moe
 
 extern "C" {
@@ -58,6 +66,15 @@ int moe_e4m3_check(uint32_t first, uint32_t count, uint64_t* mismatches, void* s
                      static_cast<hipStream_t>(stream), first, count,
                      reinterpret_cast<unsigned long long*>(mismatches));
   return moe::check_launch("moe_e4m3_check");
+}
+
+int moe_silu_check(const float* g, const float* u, float* out, uint32_t n, void* stream) {
+  if (n == 0) return MOE_OK;
+  MOE_REQUIRE(g && u && out, "moe_silu_check: NULL pointer");
+  MOE_REQUIRE(n <= (1u << 30), "moe_silu_check: need n <= 2^30");
+  hipLaunchKernelGGL(moe::silu_check_kernel, dim3((n + 255) / 256), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), g, u, out, n);
+  return moe::check_launch("moe_silu_check");
 }
 
 const char* moe_last_error(void) { return moe::g_err; }

@@ -79,6 +79,7 @@ SIGNATURES = {
     "moe_shared_down": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "moe_all_finite": (C.c_int, [_vp, _i32, _i64, _vp, _vp]),
     "moe_e4m3_check": (C.c_int, [C.c_uint32, C.c_uint32, _vp, _vp]),
+    "moe_silu_check": (C.c_int, [_vp, _vp, _vp, C.c_uint32, _vp]),
     "moe_codec_histogram": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _i32]),
     "moe_codec_bound": (_i64, [_i64, _i64]),
     "moe_codec_encode": (_i64, [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i32]),
@@ -321,6 +322,18 @@ class Native:
         software encoder's (moe_e4m3_check)."""
         self._check(self.cdll.moe_e4m3_check(first, count, mismatches.data_ptr(), self.stream()),
                     "moe_e4m3_check")
+
+    def silu_check(self, g, u, out) -> None:
+        """out = the expert kernels' SiLU(g) * u, elementwise on float32
+        device tensors of one size (moe_silu_check)."""
+        import torch
+        if not (g.numel() == u.numel() == out.numel()):
+            raise ValueError("g, u and out must have one size")
+        for t in (g, u, out):
+            if t.dtype != torch.float32 or not t.is_contiguous():
+                raise ValueError("g, u and out must be contiguous float32")
+        self._check(self.cdll.moe_silu_check(g.data_ptr(), u.data_ptr(), out.data_ptr(),
+                                             g.numel(), self.stream()), "moe_silu_check")
 
     # ------------------------------------------------------------ coded pools
     def codec_histogram(self, records: np.ndarray, fp8_bytes: int, threads: int = 8):

@@ -59,6 +59,14 @@ const char* moe_hip_runtime_path(void);
  * torch's float8_e4m3fn cast inside fp8_moe_forward (bin/offload.py:239). */
 int moe_e4m3_check(uint32_t first, uint32_t count, uint64_t* mismatches, void* stream);
 
+/* Device self-check of the expert kernels' SiLU(gate) * up: out[i] =
+ * g[i] * rcp(1 + 2^(-g[i] log2 e)) * u[i] on the hardware exp2 and
+ * reciprocal, the float32 formula the decode and grouped kernels apply to
+ * h, for n <= 2^30 device floats (n == 0 does nothing).  No counterpart in
+ * the reference, whose SiLU runs inside fp8_moe_forward
+ * (bin/devcache.py:275-277). */
+int moe_silu_check(const float* g, const float* u, float* out, uint32_t n, void* stream);
+
 /* ------------------------------------------------------------- host pool */
 
 /* Page-locked, device-mapped host allocation for an expert pool.
