@@ -361,7 +361,7 @@ def resident_bench(lib, harness, batches=(1, 8, 32, 128), steps: int = 20, warmu
                        "distinct_experts_per_layer": round(float(distinct.mean()), 1),
                        "expert_GBps": round(wbytes / dt / 1e9, 1),
                        "expert_TFLOPs": round(flops / dt / 1e12, 3),
-                       "kernels": "GEMV" if B <= 2 else "grouped",
+                       "kernels": "GEMV" if B <= 16 else "grouped",
                        "finite_output": bool(torch.isfinite(x.float()).all())}
         del graph
     del recs, views

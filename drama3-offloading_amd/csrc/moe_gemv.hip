@@ -528,7 +528,16 @@ using namespace moe;
 
 // Calls of at most this many tokens take the per-pair GEMV kernels by default;
 // larger ones the grouped kernels, which read each expert's weights once.
-constexpr int32_t kGemvMaxTokens = 2;
+// Measured on MI355X (top-8 of 256 uniform, H 2048, I 512, resident
+// records, graph of back-to-back calls): GEMV 11 / 25 / 46 / 88 us against
+// grouped 50 / 78 / 104 / 116 us at 1 / 4 / 8 / 16 tokens, and 105 against
+// 99 us at 20: the GEMV's re-read of shared experts costs less than the
+// grouped path's six launches until about 16 tokens.
+constexpr int32_t kGemvMaxTokens = 16;
+// The block call carries the shared expert in the GEMV launches up to this
+// many tokens (its gate/up workgroups take the tokens one after another);
+// beyond, the routed call is followed by the two shared-expert kernels.
+constexpr int32_t kCarrySharedMaxTokens = 2;
 
 static bool use_grouped(int32_t tokens, int32_t hidden, int32_t mode) {
   if (mode == 1) return false;
@@ -689,7 +698,7 @@ extern "C" int moe_fp8_moe_block_forward(const void* x, const void* ids, int32_t
                       static_cast<const uint16_t*>(shared->w_up),
                       static_cast<const uint16_t*>(shared->w_down),
                       static_cast<const uint16_t*>(shared->w_sgate), Is, act, sig};
-  if (!use_grouped(tokens, hidden, mode)) {
+  if (!use_grouped(tokens, hidden, mode) && tokens <= kCarrySharedMaxTokens) {
     // decode: the shared expert rides in the two GEMV launches, residual last
     const int rc = forward_impl(x, ids, ids_dtype, weights, w_dtype, tokens, top_k, w13, s13,
                                 w2, s2, n_experts, hidden, inter, strides, residual, out,

@@ -212,8 +212,9 @@ typedef struct moe_expert_strides {
 /* moe_fp8_moe_forward with explicit expert strides (NULL = dense), an
  * optional bf16 residual [tokens, hidden] added to the bf16 result the way a
  * bf16 tensor add would (out = bf16(residual + bf16(sum_k w*y)); NULL =
- * none; it may be x itself, not out), and a kernel choice: mode 0 automatic,
- * 1 per-pair GEMV, 2 grouped. */
+ * none; it may be x itself, not out), and a kernel choice: mode 0 automatic
+ * (per-pair GEMV up to 16 tokens, grouped beyond), 1 per-pair GEMV, 2
+ * grouped. */
 int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t ids_dtype,
                            const void* weights, int32_t w_dtype,
                            int32_t tokens, int32_t top_k, const void* w13,
@@ -386,10 +387,10 @@ size_t moe_fp8_moe_block_workspace(int32_t tokens, int32_t top_k,
  *   out = bf16(residual + bf16(routed + bf16(sig * shared_down)))
  * with routed the bf16 result of moe_fp8_moe_forward_ex on the same
  * arguments and the shared terms those of moe_shared_gate_up/_down, bit for
- * bit.  On the per-pair GEMV path (decode) the shared expert is carried by
- * the two routed launches: extra workgroups of the gate/up launch and one
- * extra wave per workgroup of the down launch.  A
- * grouped call runs the routed experts, then the two shared-expert kernels
+ * bit.  On the per-pair GEMV path with at most 2 tokens (decode) the shared
+ * expert is carried by the two routed launches: extra workgroups of the
+ * gate/up launch and one extra wave per workgroup of the down launch.  Any
+ * other call runs the routed experts, then the two shared-expert kernels
  * on its output.  No counterpart in the reference: upstream's MoE block
  * calls the expert forward (bin/devcache.py:275-277) and the shared expert
  * separately. */
