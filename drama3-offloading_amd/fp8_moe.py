@@ -15,6 +15,8 @@ import torch
 
 import hipfetch
 
+# kernel choice: automatic (per-pair GEMV up to 16 tokens, grouped beyond),
+# per-pair GEMV, grouped
 MODE_AUTO, MODE_GEMV, MODE_GROUPED = 0, 1, 2
 
 
