@@ -28,40 +28,6 @@
 
 namespace moe {
 
-// --------------------------------------------------------------- quant x
-
-__global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restrict__ x,
-                                                         int32_t hidden, uint8_t* __restrict__ xq,
-                                                         float* __restrict__ xs) {
-  // one workgroup per token; 16 threads x 8 values per 128-group
-  const int64_t t = blockIdx.x;
-  const uint16_t* xr = x + t * hidden;
-  for (int base = 0; base < hidden; base += 2048) {
-    const int i = base + threadIdx.x * 8;
-    float v[8];
-    float amax = 0.0f;
-    if (i < hidden) {
-      const uint4 raw = *reinterpret_cast<const uint4*>(xr + i);
-      const uint32_t r[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[2 * j] = __uint_as_float(r[j] << 16);
-        v[2 * j + 1] = __uint_as_float(r[j] & 0xffff0000u);
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
-    }
-    amax = row16_max_f32(amax);
-    if (i < hidden) {
-      const float s = act_scale(amax);
-      *reinterpret_cast<uint2*>(xq + t * hidden + i) =
-          make_uint2(quant4_e4m3(v, s), quant4_e4m3(v + 4, s));
-      if ((threadIdx.x & 15) == 0) xs[t * (hidden >> 7) + (i >> 7)] = s;
-    }
-  }
-}
-
-
 // ---------------------------------------------------- streamed expert GEMM
 //
 // One kernel computes both projections.  For the weight rows r of one expert
@@ -417,11 +383,10 @@ int launch_grouped(const uint16_t* x, const void* ids, int ids64, const void* we
   int32_t* n_tiles = reinterpret_cast<int32_t*>(ws + L.n_tiles);
   const int64_t P = static_cast<int64_t>(tokens) * top_k;
   const int64_t max_tiles = (P + kTileTok - 1) / kTileTok + n_experts;
+  // the permutation and the activation rows' quantisation in one launch
+  const QuantRowsJob quant{x, hidden, xq, xs, tokens};
   int rc = launch_permute(ids, ids64, P, n_experts, counts, offsets, sorted, pos, s, tiles, n_tiles,
-                          kTileTok);
-  if (rc) return rc;
-  hipLaunchKernelGGL(quant_rows_kernel, dim3(tokens), dim3(256), 0, s, x, hidden, xq, xs);
-  rc = check_launch("moe_fp8_moe_forward(quant)");
+                          kTileTok, &quant);
   if (rc) return rc;
   StreamArgs gu{};
   gu.act = xq;  gu.act_s = xs;  gu.sorted = sorted;

@@ -81,11 +81,18 @@ __global__ __launch_bounds__(kPlaceThreads) void permute_kernel(
     const void* __restrict__ ids, int ids64, int64_t P, int32_t n_experts,
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ sorted_pairs,
     int32_t* __restrict__ pair_pos, int32_t* __restrict__ tiles, int32_t* __restrict__ n_tiles,
-    int32_t tile_tokens) {
+    int32_t tile_tokens, QuantRowsJob quant) {
   __shared__ int32_t cursor[kPermMaxExperts];
   __shared__ uint64_t fields[kPermMaxExperts];
   __shared__ int32_t scratch[40];
   const int tid = threadIdx.x;
+  if (blockIdx.x > 0) {
+    // the activation rows, two tokens per workgroup (a 256-thread half each,
+    // whole waves), beside workgroup 0's permutation; no barrier here
+    const int64_t t = 2 * static_cast<int64_t>(blockIdx.x - 1) + (tid >> 8);
+    if (t < quant.tokens) quant_row(quant, t, tid & 255);
+    return;
+  }
   const int lane = tid & 63, wave = tid >> 6;
   // ids of the first kHoldRounds rounds, read once with all loads in flight
   // (-1: id out of range, -2: past the last pair)
@@ -328,9 +335,14 @@ __global__ __launch_bounds__(64) void gather_plan_kernel(
 
 int launch_permute(const void* ids, int ids64, int64_t P, int32_t n_experts, int32_t* counts,
                    int32_t* offsets, int32_t* sorted_pairs, int32_t* pair_pos, hipStream_t s,
-                   int32_t* tiles, int32_t* n_tiles, int32_t tile_tokens) {
-  hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(kPlaceThreads), 0, s, ids, ids64, P, n_experts,
-                     counts, offsets, sorted_pairs, pair_pos, tiles, n_tiles, tile_tokens);
+                   int32_t* tiles, int32_t* n_tiles, int32_t tile_tokens,
+                   const QuantRowsJob* quant) {
+  static_assert(kPlaceThreads == 512, "two 256-thread token slices per quantising workgroup");
+  const QuantRowsJob q = quant ? *quant : QuantRowsJob{nullptr, 0, nullptr, nullptr, 0};
+  const unsigned grid = 1 + static_cast<unsigned>((q.tokens + 1) / 2);
+  hipLaunchKernelGGL(permute_kernel, dim3(grid), dim3(kPlaceThreads), 0, s, ids, ids64, P,
+                     n_experts, counts, offsets, sorted_pairs, pair_pos, tiles, n_tiles,
+                     tile_tokens, q);
   return check_launch("moe_permute");
 }
 
