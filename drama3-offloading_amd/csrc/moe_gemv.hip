@@ -275,6 +275,8 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
   }
   __syncthreads();
   if (!owner) return;
+  // unrolled so that the LDS reads of several blocks are in flight at once
+#pragma unroll 8
   for (int g = gn; g < G; ++g) {
     const float4 d = *reinterpret_cast<const float4*>(&dpart[tile][g][4 * q]);
     const v4f dv = {d.x, d.y, d.z, d.w};
