@@ -285,6 +285,9 @@ extern "C" int moe_route_resolve(const void* x, const void* w, const float* bias
   MOE_REQUIRE(top_k >= 1 && top_k <= kMaxTopK && top_k <= n_experts && n_experts <= 4096,
               "moe_route_resolve: need 1 <= top_k <= min(32, n_experts), n_experts <= 4096");
   MOE_REQUIRE(cap >= 1 && cap <= kMaxCap, "moe_route_resolve: need 1 <= cap <= %d", kMaxCap);
+  // more ids than slots would hand one slot to two ids of this call
+  MOE_REQUIRE(top_k <= cap, "moe_route_resolve: top_k (%d) exceeds the cache capacity (%d)",
+              top_k, cap);
   MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0,
               "moe_route_resolve: x and w must be 16-byte aligned");
   hipStream_t s = as_stream(stream);

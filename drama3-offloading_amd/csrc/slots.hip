@@ -72,6 +72,8 @@ int moe_resolve_slots(const void* ids, int32_t ids_dtype, int32_t k, int32_t* sl
   MOE_REQUIRE(n_experts >= 1 && cap >= 1 && cap <= moe::kMaxCap,
               "moe_resolve_slots: need n_experts >= 1 and 1 <= cap <= %d (got %d, %d)",
               moe::kMaxCap, n_experts, cap);
+  // more ids than slots would hand one slot to two ids of this call
+  MOE_REQUIRE(k <= cap, "moe_resolve_slots: k (%d) exceeds the cache capacity (%d)", k, cap);
   hipStream_t s = moe::as_stream(stream);
   const int ids64 = ids_dtype == MOE_I64;
 #define MOE_RS(PER)                                                                              \

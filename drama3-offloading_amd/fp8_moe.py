@@ -61,9 +61,11 @@ def fp8_moe_forward(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch
     if tuple(s13.shape[1:]) != (I2 // 128, H // 128) or tuple(s2.shape[1:]) != (H // 128, inter // 128):
         raise ValueError(f"scale shapes {tuple(s13.shape)} / {tuple(s2.shape)} do not match "
                          "128x128 blocks")
-    for t in (w13, s13, w2, s2):
+    # a host address handed to a kernel would fault the device
+    for t in (topk_ids, topk_weights, w13, s13, w2, s2):
         if t.device != x.device:
-            raise ValueError(f"expert buffers must be on {x.device}, got {t.device}")
+            raise ValueError(f"ids, weights and expert buffers must be on {x.device}, "
+                             f"got one on {t.device}")
     if out is None:
         out = torch.empty((T, H), dtype=torch.bfloat16, device=x.device)
     need = lib.fp8_moe_workspace(T, K, n, H, inter)

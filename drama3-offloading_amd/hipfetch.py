@@ -133,6 +133,22 @@ class Native:
         return None if t is None else t.data_ptr()
 
     @staticmethod
+    def _on_gpu(what: str, *tensors) -> None:
+        """Every tensor argument must live on one GPU: a host address handed
+        to a kernel would fault the device, so it is refused here."""
+        dev = None
+        for t in tensors:
+            if t is None:
+                continue
+            if not t.is_cuda:
+                raise ValueError(f"{what}: every tensor argument must be on the GPU, "
+                                 f"got one on {t.device}")
+            if dev is None:
+                dev = t.device
+            elif t.device != dev:
+                raise ValueError(f"{what}: tensor arguments on {dev} and {t.device}")
+
+    @staticmethod
     def _dtype_code(t) -> int:
         import torch
         return {torch.int32: MOE_I32, torch.int64: MOE_I64, torch.float32: MOE_F32,
@@ -168,6 +184,8 @@ class Native:
 
     def resolve_slots(self, ids, slot_of, slot_expert, stamp, step, out_slot, fetch_slot,
                       fetch_expert, nmiss, stats=None) -> None:
+        self._on_gpu("moe_resolve_slots", ids, slot_of, slot_expert, stamp, step, out_slot,
+                     fetch_slot, fetch_expert, nmiss, stats)
         self._check(self.cdll.moe_resolve_slots(
             ids.data_ptr(), self._dtype_code(ids), ids.numel(), slot_of.data_ptr(),
             slot_of.numel(), slot_expert.data_ptr(), stamp.data_ptr(), slot_expert.numel(),
@@ -178,6 +196,7 @@ class Native:
     def fetch(self, pairs, fetch_expert, fetch_slot, nmiss, max_jobs: int,
               blocks_per_job: int) -> None:
         """pairs: [(src_device_addr, dst_device_addr, bytes_per_record), ...]"""
+        self._on_gpu("moe_fetch", fetch_expert, fetch_slot, nmiss)
         arr = (FetchPair * len(pairs))(*[FetchPair(s, d, b) for s, d, b in pairs])
         self._check(self.cdll.moe_fetch(arr, len(pairs), fetch_expert.data_ptr(),
                                         fetch_slot.data_ptr(), nmiss.data_ptr(), max_jobs,
@@ -185,6 +204,7 @@ class Native:
 
     # ------------------------------------------------------------ router
     def router_topk(self, x, w, bias, top_k: int, logits, ids, weights) -> None:
+        self._on_gpu("moe_router_topk", x, w, bias, logits, ids, weights)
         T, H = x.shape
         E = w.shape[0]
         self._check(self.cdll.moe_router_topk(
@@ -197,6 +217,8 @@ class Native:
         """Router + slot resolve of one token (ids int32, weights float32)."""
         if x.shape[0] != 1:
             raise ValueError("route_resolve takes exactly one token")
+        self._on_gpu("moe_route_resolve", x, w, bias, logits, ids, weights, slot_of, slot_expert,
+                     stamp, step, out_slot, fetch_slot, fetch_expert, nmiss, stats)
         H = x.shape[1]
         E = w.shape[0]
         self._check(self.cdll.moe_route_resolve(
@@ -214,6 +236,8 @@ class Native:
                         mode: int = 0, residual=None) -> None:
         """w13/s13/w2/s2 may be strided along the expert axis (views into a
         packed record pool); every other dimension must be contiguous."""
+        self._on_gpu("moe_fp8_moe_forward", x, ids, weights, w13, s13, w2, s2, out, workspace,
+                     residual)
         T, H = x.shape
         K = ids.shape[-1]
         n = w13.shape[0]
@@ -240,6 +264,8 @@ class Native:
         """The MoE block: routed experts plus the gated shared expert,
         shared = (w_gate [Is, H], w_up [Is, H], w_down [H, Is], w_sgate [H]) bf16;
         out = residual + (routed + sigmoid-gated shared), each sum rounded to bf16."""
+        self._on_gpu("moe_fp8_moe_block_forward", x, ids, weights, w13, s13, w2, s2, *shared, out,
+                     workspace, residual)
         T, H = x.shape
         K = ids.shape[-1]
         n = w13.shape[0]
@@ -262,6 +288,7 @@ class Native:
 
     # ------------------------------------------------------------ permute
     def permute(self, ids, n_experts: int, counts, offsets, sorted_pairs, pair_pos) -> None:
+        self._on_gpu("moe_permute", ids, counts, offsets, sorted_pairs, pair_pos)
         T, K = ids.shape
         self._check(self.cdll.moe_permute(ids.data_ptr(), self._dtype_code(ids), T, K, n_experts,
                                           counts.data_ptr(), offsets.data_ptr(),
@@ -270,6 +297,7 @@ class Native:
 
     def unique_inverse(self, ids, n_experts: int, counts, n_unique, uniq, rank_of,
                        inverse) -> None:
+        self._on_gpu("moe_unique_inverse", ids, counts, n_unique, uniq, rank_of, inverse)
         T, K = ids.shape
         self._check(self.cdll.moe_unique_inverse(
             ids.data_ptr(), self._dtype_code(ids), T, K, n_experts, counts.data_ptr(),
@@ -278,6 +306,8 @@ class Native:
 
     def gather_plan(self, uniq, n_unique, slot_of, cap: int, host_expert, host_dst, n_host,
                     cache_src, cache_dst, n_cache, stats=None) -> None:
+        self._on_gpu("moe_gather_plan", uniq, n_unique, slot_of, host_expert, host_dst, n_host,
+                     cache_src, cache_dst, n_cache, stats)
         self._check(self.cdll.moe_gather_plan(
             uniq.data_ptr(), n_unique.data_ptr(), self._ptr(slot_of), uniq.numel(), cap,
             host_expert.data_ptr(), host_dst.data_ptr(), n_host.data_ptr(), cache_src.data_ptr(),
@@ -293,6 +323,7 @@ class Native:
             raise ValueError("shared expert weights do not match x")
         if act.shape != (T, Is) or sig.numel() < T:
             raise ValueError("shared expert scratch too small")
+        self._on_gpu("moe_shared_gate_up", x, w_gate, w_up, w_sgate, act, sig)
         self._check(self.cdll.moe_shared_gate_up(
             x.data_ptr(), w_gate.data_ptr(), w_up.data_ptr(), w_sgate.data_ptr(), T, H, Is,
             act.data_ptr(), sig.data_ptr(), self.stream()), "moe_shared_gate_up")
@@ -307,12 +338,14 @@ class Native:
         for t in (routed, residual):
             if t is not None and t.shape != (T, H):
                 raise ValueError("routed / residual must be [T, H]")
+        self._on_gpu("moe_shared_down", act, sig, w_down, out, routed, residual)
         self._check(self.cdll.moe_shared_down(
             act.data_ptr(), sig.data_ptr(), w_down.data_ptr(), T, H, Is, self._ptr(routed),
             self._ptr(residual), out.data_ptr(), self.stream()), "moe_shared_down")
 
     def all_finite(self, x, flag) -> None:
         """flag[0] (int32, device) = 1 if every element of x (f32 or bf16) is finite."""
+        self._on_gpu("moe_all_finite", x, flag)
         self._check(self.cdll.moe_all_finite(x.data_ptr(), self._dtype_code(x), x.numel(),
                                              flag.data_ptr(), self.stream()), "moe_all_finite")
 
@@ -382,6 +415,7 @@ class Native:
             self.stream()), "moe_fetch_coded")
 
     def unpermute(self, y, pair_pos, weights, out) -> None:
+        self._on_gpu("moe_unpermute", y, pair_pos, weights, out)
         T, K = weights.shape
         H = y.shape[-1]
         self._check(self.cdll.moe_unpermute(y.data_ptr(), pair_pos.data_ptr(),

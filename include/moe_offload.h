@@ -99,8 +99,10 @@ int moe_slots_init(int32_t* slot_of, int32_t n_experts, int32_t* slot_expert,
  * ids_dtype: MOE_I32 or MOE_I64.  stats (nullable) is int64[2]
  * {hits, misses} accumulated on the device -- the reference keeps no such
  * counter (bin/devcache.py:274).  Constraints: 1 <= cap <= 4096,
- * n_experts >= 1; ids must lie in [0, n_experts) (an out-of-range id is
- * ignored and reported as slot -1). */
+ * n_experts >= 1, k <= cap (more ids than slots would give one slot to two
+ * ids of the call; the reference's callers never pass more than 8 ids,
+ * bin/devcache.py:232-233); ids must lie in [0, n_experts) (an out-of-range
+ * id is ignored and reported as slot -1). */
 int moe_resolve_slots(const void* ids, int32_t ids_dtype, int32_t k,
                       int32_t* slot_of, int32_t n_experts,
                       int32_t* slot_expert, int64_t* slot_stamp, int32_t cap,
@@ -157,7 +159,8 @@ int moe_router_topk(const void* x, const void* w, const float* bias,
  * moe_router_topk (ids int32 [top_k], weights f32 [top_k], logits f32
  * [n_experts]) followed by moe_resolve_slots on those ids, in two launches
  * instead of three.  Outputs and table updates are exactly those of the two
- * entry points called in sequence.  It has no single counterpart in the
+ * entry points called in sequence, and top_k <= cap as there.  It has no
+ * single counterpart in the
  * reference: it fuses the router (moe.py:217-220) with _resolve_slots
  * (bin/devcache.py:45-98) as they occur back to back in the decode step
  * (bin/devcache.py:230-239). */

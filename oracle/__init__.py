@@ -19,7 +19,6 @@ it follows. Modules:
              LRU/LFU/static simulator
   permute    torch.unique-style id remap and the token->expert stable sort
   fetch      the self-identifying host pool pattern
-  workloads  seeded generators for the five Drama-3-shaped workloads
   cpu_moe    the timed CPU baseline (torch on host cores)
 
 Where a function's parity rests only on this restatement (no golden vector,

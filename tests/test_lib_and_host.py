@@ -44,6 +44,12 @@ def test_preconditions_are_rejected_without_launching(lib):
     assert c.moe_route_resolve(16, 16, None, 2048, 256, 8, 1, 1, 1, 1, 1, 1, 9999, 1, 1, 1, 1, 1,
                                None, None) == -1
     assert b"cap" in c.moe_last_error()
+    # more ids than slots: one slot would go to two ids of the call
+    assert c.moe_resolve_slots(1, 0, 9, 1, 256, 1, 1, 8, 1, 1, 1, 1, 1, None, None) == -1
+    assert b"exceeds the cache capacity" in c.moe_last_error()
+    assert c.moe_route_resolve(16, 16, None, 2048, 256, 8, 1, 1, 1, 1, 1, 1, 7, 1, 1, 1, 1, 1,
+                               None, None) == -1
+    assert b"exceeds the cache capacity" in c.moe_last_error()
 
 
 def test_shared_and_block_preconditions_are_rejected_without_launching(lib):
@@ -178,6 +184,21 @@ def test_fp8_moe_forward_has_no_cpu_path(lib):
                         torch.ones((1, 2, 2)),
                         torch.zeros((1, 256, 128), dtype=torch.float8_e4m3fn),
                         torch.ones((1, 2, 1)))
+
+
+def test_wrappers_refuse_host_tensors(lib):
+    # a CPU tensor's address handed to a kernel would fault the device
+    i32 = lambda n: torch.zeros(n, dtype=torch.int32)
+    with pytest.raises(ValueError, match="on the GPU"):
+        lib.resolve_slots(i32(8), i32(256), i32(64), torch.zeros(64, dtype=torch.int64),
+                          torch.zeros(1, dtype=torch.int64), i32(8), i32(8), i32(8), i32(1))
+    with pytest.raises(ValueError, match="on the GPU"):
+        lib.fetch([(16, 16, 256)], i32(8), i32(8), i32(1), max_jobs=8, blocks_per_job=2)
+    x = torch.zeros((1, 2048), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="on the GPU"):
+        lib.router_topk(x, torch.zeros((256, 2048), dtype=torch.bfloat16), None, 8,
+                        torch.zeros((1, 256)), torch.zeros((1, 8), dtype=torch.int64),
+                        torch.zeros((1, 8)))
 
 
 def test_moe_experts_surface():
