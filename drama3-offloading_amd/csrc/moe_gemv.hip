@@ -25,6 +25,8 @@
 #include "grouped.hpp"
 #include "shared.hpp"
 
+#include <mutex>
+
 namespace moe {
 
 // The MoE block's shared expert carried along by the two decode launches
@@ -558,6 +560,69 @@ extern "C" size_t moe_fp8_moe_workspace(int32_t tokens, int32_t top_k, int32_t n
   return need > g ? need : g;
 }
 
+// ---------------------------------------------------------------------------
+// The allocation-free forward: moe_fp8_moe_forward_ex with its workspace in
+// a file-scope device array instead of a caller's buffer.
+//
+// Each GPU the library runs on holds its own copy of `scratch` until the
+// process ends.  In host code the name `scratch` is only a stand-in for the
+// variable, not a device address: the address each device's copy has is
+// looked up with hipGetSymbolAddress, once per device with that device
+// current, and only that address ever reaches a kernel.  Every call on one
+// GPU uses the same copy, so calls that overlap on one GPU (two streams, two
+// threads) race on it.  No kernel of the forward reads a workspace byte it
+// has not written earlier in the same call, so nothing is cleared between
+// calls.
+
+static size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+constexpr size_t kNoAllocScratchBytes = MOE_NOALLOC_SCRATCH_BYTES;
+static_assert(kNoAllocScratchBytes % 256 == 0, "scratch size must keep 256-byte alignment");
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_dev[kMaxDevices];
+
+// This device's copy of `scratch`, looked up on the first call on it.
+static int scratch_address(hipStream_t s, void** addr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("moe_fp8_moe_forward_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    return static_cast<int>(e);
+  }
+  MOE_REQUIRE(dev >= 0 && dev < kMaxDevices,
+              "moe_fp8_moe_forward_noalloc: device %d beyond the %d this library tracks", dev,
+              kMaxDevices);
+  if (s != nullptr) {
+    // the address is per device: a stream of another device would get the
+    // current device's copy
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(s, &sdev);
+    if (e != hipSuccess) {
+      set_error("moe_fp8_moe_forward_noalloc: hipStreamGetDevice: %s", hipGetErrorString(e));
+      return static_cast<int>(e);
+    }
+    MOE_REQUIRE(static_cast<int>(sdev) == dev,
+                "moe_fp8_moe_forward_noalloc: the stream belongs to device %d, the current "
+                "device is %d", static_cast<int>(sdev), dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("moe_fp8_moe_forward_noalloc: hipGetSymbolAddress(scratch) on device %d: %s",
+                dev, hipGetErrorString(e));
+      return e != hipSuccess ? static_cast<int>(e) : MOE_EINVAL;
+    }
+    g_scratch_dev[dev] = p;
+  }
+  *addr = g_scratch_dev[dev];
+  return MOE_OK;
+}
+
 // The routed-expert call: preconditions, then the GEMV or grouped path.
 // `sh` (nullable) asks for the shared expert on the GEMV path; *fused tells
 // whether it was carried along (the caller runs it after a grouped call).
@@ -566,7 +631,8 @@ static int forward_impl(const void* x, const void* ids, int32_t ids_dtype, const
                         const float* s13, const void* w2, const float* s2, int32_t n_experts,
                         int32_t hidden, int32_t inter, const moe_expert_strides* strides,
                         const void* residual, void* out, void* workspace, size_t workspace_bytes,
-                        int32_t mode, const SharedRefs* sh, bool* fused, void* stream) {
+                        int32_t mode, const SharedRefs* sh, bool* fused, void* stream,
+                        bool static_scratch = false) {
   *fused = false;
   MOE_REQUIRE(tokens >= 0, "moe_fp8_moe_forward: tokens < 0");
   MOE_REQUIRE(top_k >= 1 && top_k <= kMaxK, "moe_fp8_moe_forward: need 1 <= top_k <= %d", kMaxK);
@@ -602,6 +668,16 @@ static int forward_impl(const void* x, const void* ids, int32_t ids_dtype, const
   MOE_REQUIRE(es.w13 % 16 == 0 && es.w2 % 16 == 0,
               "moe_fp8_moe_forward: w13/w2 expert strides must be multiples of 16 bytes");
   const size_t need = moe_fp8_moe_workspace(tokens, top_k, n_experts, hidden, inter);
+  if (static_scratch) {
+    // moe_fp8_moe_forward_noalloc: the library's per-GPU array is the workspace
+    MOE_REQUIRE(need <= kNoAllocScratchBytes,
+                "moe_fp8_moe_forward_noalloc: this call needs %zu bytes of scratch, more than "
+                "the %zu the library holds per GPU; use moe_fp8_moe_forward_ex with a workspace",
+                need, kNoAllocScratchBytes);
+    const int rc = scratch_address(as_stream(stream), &workspace);
+    if (rc) return rc;
+    workspace_bytes = kNoAllocScratchBytes;
+  }
   MOE_REQUIRE(workspace != nullptr && workspace_bytes >= need,
               "moe_fp8_moe_forward: workspace of %zu bytes needed, %zu given", need,
               workspace_bytes);
@@ -646,8 +722,6 @@ extern "C" int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t id
                       n_experts, hidden, inter, strides, residual, out, workspace, workspace_bytes,
                       mode, nullptr, &fused, stream);
 }
-
-static size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
 extern "C" size_t moe_fp8_moe_block_workspace(int32_t tokens, int32_t top_k, int32_t n_experts,
                                               int32_t hidden, int32_t inter,
@@ -731,4 +805,19 @@ extern "C" int moe_fp8_moe_forward(const void* x, const void* ids, int32_t ids_d
   return moe_fp8_moe_forward_ex(x, ids, ids_dtype, weights, w_dtype, tokens, top_k, w13, s13, w2,
                                 s2, n_experts, hidden, inter, nullptr, nullptr, out, workspace,
                                 workspace_bytes, 0, stream);
+}
+
+
+extern "C" int moe_fp8_moe_forward_noalloc(const void* x, const void* ids, int32_t ids_dtype,
+                                           const void* weights, int32_t w_dtype, int32_t tokens,
+                                           int32_t top_k, const void* w13, const float* s13,
+                                           const void* w2, const float* s2, int32_t n_experts,
+                                           int32_t hidden, int32_t inter,
+                                           const moe_expert_strides* strides,
+                                           const void* residual, void* out, int32_t mode,
+                                           void* stream) {
+  bool fused;
+  return forward_impl(x, ids, ids_dtype, weights, w_dtype, tokens, top_k, w13, s13, w2, s2,
+                      n_experts, hidden, inter, strides, residual, out, nullptr, 0, mode, nullptr,
+                      &fused, stream, /*static_scratch=*/true);
 }

@@ -70,6 +70,9 @@ SIGNATURES = {
     "moe_fp8_moe_forward_ex": (C.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp,
                                          _vp, _i32, _i32, _i32, C.POINTER(ExpertStrides), _vp,
                                          _vp, _vp, _sz, _i32, _vp]),
+    "moe_fp8_moe_forward_noalloc": (C.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp,
+                                              _vp, _vp, _i32, _i32, _i32,
+                                              C.POINTER(ExpertStrides), _vp, _vp, _i32, _vp]),
     "moe_permute": (C.c_int, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp]),
     "moe_unpermute": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp]),
     "moe_unique_inverse": (C.c_int, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
@@ -253,6 +256,26 @@ class Native:
             workspace.data_ptr(),
             workspace.numel() * workspace.element_size(), mode, self.stream()),
             "moe_fp8_moe_forward")
+
+    def fp8_moe_forward_noalloc(self, x, ids, weights, w13, s13, w2, s2, out, mode: int = 0,
+                                residual=None) -> None:
+        """fp8_moe_forward with the library's per-GPU scratch array as the
+        workspace: allocates nothing (moe_fp8_moe_forward_noalloc)."""
+        self._on_gpu("moe_fp8_moe_forward_noalloc", x, ids, weights, w13, s13, w2, s2, out,
+                     residual)
+        T, H = x.shape
+        K = ids.shape[-1]
+        n = w13.shape[0]
+        inter = w2.shape[-1]
+        for t in (w13, s13, w2, s2):
+            if not t[0].is_contiguous():
+                raise ValueError("expert weights must be contiguous within an expert")
+        es = ExpertStrides(w13.stride(0), s13.stride(0), w2.stride(0), s2.stride(0))
+        self._check(self.cdll.moe_fp8_moe_forward_noalloc(
+            x.data_ptr(), ids.data_ptr(), self._dtype_code(ids), weights.data_ptr(),
+            self._dtype_code(weights), T, K, w13.data_ptr(), s13.data_ptr(), w2.data_ptr(),
+            s2.data_ptr(), n, H, inter, C.byref(es), self._ptr(residual), out.data_ptr(), mode,
+            self.stream()), "moe_fp8_moe_forward_noalloc")
 
     def fp8_moe_block_workspace(self, tokens, top_k, n_experts, hidden, inter,
                                 shared_inter) -> int:

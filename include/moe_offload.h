@@ -228,6 +228,30 @@ int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t ids_dtype,
                            void* workspace, size_t workspace_bytes,
                            int32_t mode, void* stream);
 
+/* Bytes of the per-GPU scratch array behind moe_fp8_moe_forward_noalloc. */
+#define MOE_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+
+/* moe_fp8_moe_forward_ex without a workspace argument and without any
+ * allocation: the workspace is a 16 MiB device array inside the library
+ * (MOE_NOALLOC_SCRATCH_BYTES), one copy per GPU, held until the process
+ * ends.  No counterpart in the reference: it is for callers that cannot
+ * allocate (code under hipGraph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Calls whose moe_fp8_moe_workspace exceeds the
+ * array are refused with MOE_EINVAL (decode, and batches up to about 160
+ * tokens at top-8 of 256 with hidden 2048 and inter 512, fit).  Every call
+ * on one GPU shares that GPU's array: calls that overlap on one GPU (two
+ * streams or threads) race.  `stream` must belong to the current device,
+ * on which the first call looks the array's address up.  Outputs are those
+ * of moe_fp8_moe_forward_ex with the same arguments, bit for bit. */
+int moe_fp8_moe_forward_noalloc(const void* x, const void* ids, int32_t ids_dtype,
+                                const void* weights, int32_t w_dtype,
+                                int32_t tokens, int32_t top_k, const void* w13,
+                                const float* s13, const void* w2, const float* s2,
+                                int32_t n_experts, int32_t hidden, int32_t inter,
+                                const moe_expert_strides* strides,
+                                const void* residual, void* out, int32_t mode,
+                                void* stream);
+
 /* ------------------------------------------------------ permute/unpermute */
 
 /* Stable token->expert grouping of ids [tokens, top_k]:

@@ -94,6 +94,32 @@ def test_shared_and_block_preconditions_are_rejected_without_launching(lib):
     assert b"shared inter" in c.moe_last_error()
 
 
+def test_noalloc_forward_refuses_calls_beyond_its_scratch(lib):
+    import ctypes as C
+    import hipfetch
+    c = lib.cdll
+    one = C.c_void_p(16)                   # never dereferenced: the size check fails first
+    es = hipfetch.ExpertStrides(2 * 512 * 2048, 8 * 16, 2048 * 512, 16 * 4)
+    cap = 16 << 20
+    # 512 tokens of top-8 (the prefill call) need about 35 MiB of workspace
+    assert c.moe_fp8_moe_workspace(512, 8, 256, 2048, 512) > cap
+    assert c.moe_fp8_moe_forward_noalloc(one, one, hipfetch.MOE_I32, one, hipfetch.MOE_F32, 512, 8,
+                                         one, one, one, one, 256, 2048, 512, C.byref(es), None,
+                                         one, 0, None) == -1
+    assert b"more than the 16777216" in c.moe_last_error()
+    # other preconditions are those of moe_fp8_moe_forward_ex
+    assert c.moe_fp8_moe_forward_noalloc(one, one, hipfetch.MOE_I32, one, hipfetch.MOE_F32, 1, 8,
+                                         one, one, one, one, 256, 2000, 512, None, None, one, 0,
+                                         None) == -1
+    assert b"hidden" in c.moe_last_error()
+    # an empty call does nothing and needs no scratch
+    assert c.moe_fp8_moe_forward_noalloc(None, None, hipfetch.MOE_I32, None, hipfetch.MOE_F32, 0,
+                                         8, None, None, None, None, 256, 2048, 512, None, None,
+                                         None, 0, None) == 0
+    # decode and batches up to ~160 tokens fit
+    assert c.moe_fp8_moe_workspace(128, 8, 256, 2048, 512) <= cap
+
+
 def test_workspace_size_formula(lib):
     def al(v):
         return (v + 255) // 256 * 256
