@@ -3,9 +3,11 @@
 // E then renormalise, upstream's norm_topk_prob).
 //
 // Logit arithmetic: a bf16 x bf16 product is exact in float32; products are
-// summed in float64 and rounded once to float32.  With float64 partial sums
-// exact for ordinary data, the rounded logit does not depend on the order of
-// summation, which is what lets expert ids match the oracle bit for bit.
+// summed in float64 and rounded once, to float32 or (the gate of a bf16
+// nn.Linear, whose output is a bf16 tensor) to bf16, before the optional
+// float32 bias.  With float64 partial sums exact for ordinary data, the
+// rounded logit does not depend on the order of summation, which is what
+// lets expert ids match the oracle bit for bit.
 //
 // Kernels:
 //   logits: grid (E/4, ceil(T/TB)), 4 waves, TB = 1 for one token else 4;
@@ -58,6 +60,19 @@ __device__ __forceinline__ double wave_sum_f64_dpp(double v) {
   return s;
 }
 
+// bf16 (round to nearest, ties to even) of a double, returned as a float.
+// The double is first rounded to odd into float32 (toward zero, then the
+// last bit set when anything was dropped); float32 keeps 24 significant
+// bits, at least two more than bf16's 8, so rounding that result to nearest
+// even gives the correctly rounded bf16 of the double itself.
+__device__ __forceinline__ float bf16_of_f64(double s) {
+  const float f = __double2float_rz(s);
+  uint32_t u = __float_as_uint(f);
+  if (static_cast<double>(f) != s) u |= 1u;
+  u = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
+  return __uint_as_float(u);
+}
+
 // One wave per (expert, block of TB tokens): the expert's gate row and the
 // tokens' rows are read in chunks of 4 x 16 bytes per lane, every load of a
 // chunk issued before any of it is used (no load under a branch: lanes and
@@ -65,7 +80,8 @@ __device__ __forceinline__ double wave_sum_f64_dpp(double v) {
 template <int TB>
 __global__ __launch_bounds__(256) void router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ bias,
-    int32_t tokens, int32_t hidden, int32_t n_experts, float* __restrict__ logits) {
+    int32_t tokens, int32_t hidden, int32_t n_experts, int bf16_logits,
+    float* __restrict__ logits) {
   constexpr int U = 4;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -113,7 +129,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   for (int tt = 0; tt < TB; ++tt) {
     const double s = wave_sum_f64_dpp(acc[tt]);
     if (lane == 0 && tt < nt) {
-      float l = static_cast<float>(s);
+      float l = bf16_logits ? bf16_of_f64(s) : static_cast<float>(s);
       if (bias) l += bias[e];
       logits[static_cast<int64_t>(t0 + tt) * n_experts + e] = l;
     }
@@ -232,11 +248,13 @@ __global__ __launch_bounds__(64) void topk_resolve_kernel(
 
 using namespace moe;
 
-extern "C" int moe_router_topk(const void* x, const void* w, const float* bias, int32_t tokens,
-                               int32_t hidden, int32_t n_experts, int32_t top_k, float* logits,
-                               void* ids, int32_t ids_dtype, void* weights, int32_t w_dtype,
-                               void* stream) {
+extern "C" int moe_router_topk(const void* x, const void* w, const float* bias,
+                               int32_t logit_dtype, int32_t tokens, int32_t hidden,
+                               int32_t n_experts, int32_t top_k, float* logits, void* ids,
+                               int32_t ids_dtype, void* weights, int32_t w_dtype, void* stream) {
   MOE_REQUIRE(tokens >= 0, "moe_router_topk: tokens < 0");
+  MOE_REQUIRE(logit_dtype == MOE_F32 || logit_dtype == MOE_BF16,
+              "moe_router_topk: logit_dtype must be MOE_F32 or MOE_BF16");
   MOE_REQUIRE(hidden > 0 && hidden % 8 == 0, "moe_router_topk: hidden %% 8 != 0 (%d)", hidden);
   MOE_REQUIRE(top_k >= 1 && top_k <= kMaxTopK && top_k <= n_experts && n_experts <= 4096,
               "moe_router_topk: need 1 <= top_k <= min(32, n_experts), n_experts <= 4096");
@@ -252,11 +270,11 @@ extern "C" int moe_router_topk(const void* x, const void* w, const float* bias, 
   if (tokens == 1)
     hipLaunchKernelGGL(router_logits_kernel<1>, grid, dim3(256), 0, s,
                        static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias,
-                       tokens, hidden, n_experts, logits);
+                       tokens, hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0, logits);
   else
     hipLaunchKernelGGL(router_logits_kernel<kTokBlock>, grid, dim3(256), 0, s,
                        static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias,
-                       tokens, hidden, n_experts, logits);
+                       tokens, hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0, logits);
   int rc = check_launch("moe_router_topk(logits)");
   if (rc) return rc;
   const int i64 = ids_dtype == MOE_I64 ? 1 : 0, bf = w_dtype == MOE_BF16 ? 1 : 0;
@@ -272,7 +290,8 @@ extern "C" int moe_router_topk(const void* x, const void* w, const float* bias, 
   return check_launch("moe_router_topk(topk)");
 }
 
-extern "C" int moe_route_resolve(const void* x, const void* w, const float* bias, int32_t hidden,
+extern "C" int moe_route_resolve(const void* x, const void* w, const float* bias,
+                                 int32_t logit_dtype, int32_t hidden,
                                  int32_t n_experts, int32_t top_k, float* logits, int32_t* ids,
                                  float* weights, int32_t* slot_of, int32_t* slot_expert,
                                  int64_t* slot_stamp, int32_t cap, int64_t* step,
@@ -281,6 +300,8 @@ extern "C" int moe_route_resolve(const void* x, const void* w, const float* bias
   MOE_REQUIRE(x && w && logits && ids && weights && slot_of && slot_expert && slot_stamp && step &&
                   out_slot && fetch_slot && fetch_expert && nmiss,
               "moe_route_resolve: NULL pointer");
+  MOE_REQUIRE(logit_dtype == MOE_F32 || logit_dtype == MOE_BF16,
+              "moe_route_resolve: logit_dtype must be MOE_F32 or MOE_BF16");
   MOE_REQUIRE(hidden > 0 && hidden % 8 == 0, "moe_route_resolve: hidden %% 8 != 0 (%d)", hidden);
   MOE_REQUIRE(top_k >= 1 && top_k <= kMaxTopK && top_k <= n_experts && n_experts <= 4096,
               "moe_route_resolve: need 1 <= top_k <= min(32, n_experts), n_experts <= 4096");
@@ -293,7 +314,7 @@ extern "C" int moe_route_resolve(const void* x, const void* w, const float* bias
   hipStream_t s = as_stream(stream);
   hipLaunchKernelGGL(router_logits_kernel<1>, dim3((n_experts + 3) / 4, 1), dim3(256), 0, s,
                      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias, 1,
-                     hidden, n_experts, logits);
+                     hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0, logits);
   int rc = check_launch("moe_route_resolve(logits)");
   if (rc) return rc;
 #define MOE_TR(PE, PC)                                                                          \

@@ -67,6 +67,7 @@ class DecodeConfig:
     shared_inter: int = 512
     coded_pool: bool = False        # fetch from entropy-coded host records
     coded_workgroups: int = 32
+    router_logits: str = "bf16"     # the gate's output dtype: "bf16" (a bf16 Linear) or "f32"
 
 
 def fill_pool_on_gpu(pool: HostPool, seed: int, layer: int, device, chunk: int = 64,
@@ -190,12 +191,13 @@ class DecodeHarness:
             lib.route_resolve(self.h, self.gate[l], self.bias_live[l], cfg.top_k, self.logits[l],
                               self.ids[l], self.wts[l], self.slot_of[l], self.slot_expert[l],
                               self.stamp[l], self.step[l], self.out_slot[l], self.fslot[l],
-                              self.fexp[l], self.nmiss[l], self.stats[l])
+                              self.fexp[l], self.nmiss[l], self.stats[l],
+                              logit_dtype=cfg.router_logits)
             self.fetch(l, self.fexp[l], self.fslot[l], self.nmiss[l])
             slots = self.out_slot[l]
         else:
             lib.router_topk(self.h, self.gate[l], self.bias_live[l], cfg.top_k, self.logits[l],
-                            self.ids[l], self.wts[l])
+                            self.ids[l], self.wts[l], logit_dtype=cfg.router_logits)
             self.fetch(l, self.ids[l].view(-1), self.fixed_slots.view(-1), self.all_miss)
             slots = self.fixed_slots
         if cfg.shared_expert:

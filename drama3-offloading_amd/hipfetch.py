@@ -60,10 +60,10 @@ SIGNATURES = {
     "moe_resolve_slots": (C.c_int, [_vp, _i32, _i32, _vp, _i32, _vp, _vp, _i32, _vp, _vp, _vp,
                                     _vp, _vp, _vp, _vp]),
     "moe_fetch": (C.c_int, [C.POINTER(FetchPair), _i32, _vp, _vp, _vp, _i32, _i32, _vp]),
-    "moe_router_topk": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _i32, _vp,
-                                  _i32, _vp]),
-    "moe_route_resolve": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp,
-                                    _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "moe_router_topk": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _i32,
+                                  _vp, _i32, _vp]),
+    "moe_route_resolve": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
+                                    _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "moe_fp8_moe_workspace": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "moe_fp8_moe_forward": (C.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
                                       _i32, _i32, _i32, _vp, _vp, _sz, _vp]),
@@ -206,17 +206,29 @@ class Native:
                                         blocks_per_job, self.stream()), "moe_fetch")
 
     # ------------------------------------------------------------ router
-    def router_topk(self, x, w, bias, top_k: int, logits, ids, weights) -> None:
+    @staticmethod
+    def _logit_code(logit_dtype: str) -> int:
+        codes = {"bf16": MOE_BF16, "f32": MOE_F32}
+        if logit_dtype not in codes:
+            raise ValueError(f"logit_dtype must be 'bf16' or 'f32', got {logit_dtype!r}")
+        return codes[logit_dtype]
+
+    def router_topk(self, x, w, bias, top_k: int, logits, ids, weights,
+                    logit_dtype: str = "bf16") -> None:
+        """logits = x . W^T rounded to logit_dtype ('bf16': the bf16 gate's
+        output, or 'f32'), + bias; top-k, softmax over the picks."""
         self._on_gpu("moe_router_topk", x, w, bias, logits, ids, weights)
         T, H = x.shape
         E = w.shape[0]
         self._check(self.cdll.moe_router_topk(
-            x.data_ptr(), w.data_ptr(), self._ptr(bias), T, H, E, top_k, logits.data_ptr(),
+            x.data_ptr(), w.data_ptr(), self._ptr(bias), self._logit_code(logit_dtype), T, H, E,
+            top_k, logits.data_ptr(),
             ids.data_ptr(), self._dtype_code(ids), weights.data_ptr(), self._dtype_code(weights),
             self.stream()), "moe_router_topk")
 
     def route_resolve(self, x, w, bias, top_k: int, logits, ids, weights, slot_of, slot_expert,
-                      stamp, step, out_slot, fetch_slot, fetch_expert, nmiss, stats=None) -> None:
+                      stamp, step, out_slot, fetch_slot, fetch_expert, nmiss, stats=None,
+                      logit_dtype: str = "bf16") -> None:
         """Router + slot resolve of one token (ids int32, weights float32)."""
         if x.shape[0] != 1:
             raise ValueError("route_resolve takes exactly one token")
@@ -225,7 +237,8 @@ class Native:
         H = x.shape[1]
         E = w.shape[0]
         self._check(self.cdll.moe_route_resolve(
-            x.data_ptr(), w.data_ptr(), self._ptr(bias), H, E, top_k, logits.data_ptr(),
+            x.data_ptr(), w.data_ptr(), self._ptr(bias), self._logit_code(logit_dtype), H, E,
+            top_k, logits.data_ptr(),
             ids.data_ptr(), weights.data_ptr(), slot_of.data_ptr(), slot_expert.data_ptr(),
             stamp.data_ptr(), slot_expert.numel(), step.data_ptr(), out_slot.data_ptr(),
             fetch_slot.data_ptr(), fetch_expert.data_ptr(), nmiss.data_ptr(), self._ptr(stats),

@@ -73,12 +73,14 @@ class MoEExperts(nn.Module):
 
 def route(x: torch.Tensor, gate_weight: torch.Tensor, top_k: int = 8,
           bias: torch.Tensor | None = None, ids_dtype=torch.int64,
-          weights_dtype=torch.float32, out=None):
+          weights_dtype=torch.float32, out=None, logit_dtype: str = "bf16"):
     """Router on the GPU: logits = x . W^T (+bias), top-k, renormalised softmax.
 
-    x [T, H] bf16, gate_weight [E, H] bf16.  Returns (topk_ids [T, k],
-    topk_weights [T, k], logits [T, E] float32).  `out` may be a preallocated
-    (ids, weights, logits) triple (graph capture)."""
+    x [T, H] bf16, gate_weight [E, H] bf16.  The logits are rounded to bf16
+    as the output of the model's bf16 nn.Linear gate is (logit_dtype "f32"
+    keeps float32 logits).  Returns (topk_ids [T, k], topk_weights [T, k],
+    logits [T, E] float32).  `out` may be a preallocated (ids, weights,
+    logits) triple (graph capture)."""
     lib = hipfetch.require()
     T = x.shape[0]
     E = gate_weight.shape[0]
@@ -88,7 +90,8 @@ def route(x: torch.Tensor, gate_weight: torch.Tensor, top_k: int = 8,
         logits = torch.empty((T, E), dtype=torch.float32, device=x.device)
     else:
         ids, wts, logits = out
-    lib.router_topk(x.contiguous(), gate_weight.contiguous(), bias, top_k, logits, ids, wts)
+    lib.router_topk(x.contiguous(), gate_weight.contiguous(), bias, top_k, logits, ids, wts,
+                    logit_dtype=logit_dtype)
     return ids, wts, logits
 
 

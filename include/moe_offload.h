@@ -145,13 +145,16 @@ int moe_fetch(const moe_fetch_pair* pairs, int32_t npairs,
  * f32 or NULL.  Writes ids [tokens, top_k] (ids_dtype MOE_I32/MOE_I64),
  * weights [tokens, top_k] (w_dtype MOE_F32/MOE_BF16), and the f32 logits
  * [tokens, n_experts] to `logits` (caller-provided, also the workspace).
- * Logits are float32 roundings of float64-accumulated exact products;
- * selection is by descending logit, ties to the lower index.
+ * Each logit is the float64-accumulated sum of exact bf16 x bf16 products
+ * rounded once to logit_dtype: MOE_BF16 (the output of upstream's bf16
+ * nn.Linear gate, round to nearest even) or MOE_F32; the bias is then added
+ * in float32.  Selection is by descending logit, ties to the lower index;
+ * weights are the softmax over the selected logits.
  * Replaces upstream's gate + softmax + topk + norm_topk_prob
  * (moe.py:217-220 per notes/01-static-findings.md:133-138).
  * Constraints: hidden % 8 == 0, 1 <= top_k <= 32, top_k <= n_experts <= 4096. */
 int moe_router_topk(const void* x, const void* w, const float* bias,
-                    int32_t tokens, int32_t hidden, int32_t n_experts,
+                    int32_t logit_dtype, int32_t tokens, int32_t hidden, int32_t n_experts,
                     int32_t top_k, float* logits, void* ids, int32_t ids_dtype,
                     void* weights, int32_t w_dtype, void* stream);
 
@@ -165,7 +168,7 @@ int moe_router_topk(const void* x, const void* w, const float* bias,
  * (bin/devcache.py:45-98) as they occur back to back in the decode step
  * (bin/devcache.py:230-239). */
 int moe_route_resolve(const void* x, const void* w, const float* bias,
-                      int32_t hidden, int32_t n_experts, int32_t top_k,
+                      int32_t logit_dtype, int32_t hidden, int32_t n_experts, int32_t top_k,
                       float* logits, int32_t* ids, float* weights,
                       int32_t* slot_of, int32_t* slot_expert,
                       int64_t* slot_stamp, int32_t cap, int64_t* step,

@@ -11,16 +11,18 @@ from oracle import router as orouter
 pytestmark = pytest.mark.gpu
 
 
+@pytest.mark.parametrize("logit_dtype", ["bf16", "f32"])
 @pytest.mark.parametrize("T", [1, 7, 64, 512])
-def test_router_ids_bit_exact(lib, dev, T):
+def test_router_ids_bit_exact(lib, dev, T, logit_dtype):
     import moe
     import synth
     x = synth.hidden_states(T, T).to(dev)
     w = synth.router_weight(T).to(dev)
-    say(f"router: T={T}")
-    ids, wts, logits = moe.route(x, w, 8)
+    say(f"router: T={T}, {logit_dtype} logits")
+    ids, wts, logits = moe.route(x, w, 8, logit_dtype=logit_dtype)
     torch.cuda.synchronize()
-    o_ids, o_w, o_lg = orouter.route(x.float().cpu().numpy(), w.float().cpu().numpy(), 8)
+    o_ids, o_w, o_lg = orouter.route(x.float().cpu().numpy(), w.float().cpu().numpy(), 8,
+                                     logit_dtype=logit_dtype)
     assert np.array_equal(logits.cpu().numpy(), o_lg)
     assert np.array_equal(ids.cpu().numpy(), o_ids)
     np.testing.assert_allclose(wts.cpu().numpy(), o_w, rtol=2e-6, atol=1e-7)
@@ -41,6 +43,25 @@ def test_router_with_bias_int32_bf16_outputs(lib, dev):
                                      bias.cpu().numpy())
     assert np.array_equal(ids.cpu().numpy(), o_ids)
     np.testing.assert_allclose(wts.float().cpu().numpy(), o_w, rtol=8e-3)
+
+
+def test_router_bf16_tie_goes_to_the_lower_expert(lib, dev):
+    """Logits 1 + 2^-10 (expert 3) and 1 + 2^-11 (expert 1) round to the
+    same bf16 value: expert 1 ranks first; with float32 logits expert 3."""
+    import moe
+    H, E = 128, 64
+    x = torch.zeros((1, H), dtype=torch.bfloat16, device=dev)
+    x[0, 0], x[0, 1], x[0, 2] = 1.0, 2.0 ** -10, 2.0 ** -11
+    w = torch.zeros((E, H), dtype=torch.bfloat16, device=dev)
+    w[3, 0], w[3, 1] = 1.0, 1.0
+    w[1, 0], w[1, 2] = 1.0, 1.0
+    w[5, 0] = 0.5
+    say("router: bf16 tie")
+    ids, _, lg = moe.route(x, w, 2)
+    ids32, _, lg32 = moe.route(x, w, 2, logit_dtype="f32")
+    torch.cuda.synchronize()
+    assert lg[0, 1].item() == lg[0, 3].item() == 1.0 and ids.tolist() == [[1, 3]]
+    assert lg32[0, 3].item() == 1.0 + 2.0 ** -10 and ids32.tolist() == [[3, 1]]
 
 
 def test_router_tie_break_lower_index(lib, dev):
@@ -111,7 +132,8 @@ def test_unpermute_matches_oracle(lib, dev):
     assert np.abs(got - want).max() <= np.abs(want).max() * 2 ** -8
 
 
-def test_route_resolve_equals_router_then_resolve(lib, dev):
+@pytest.mark.parametrize("logit_dtype", ["bf16", "f32"])
+def test_route_resolve_equals_router_then_resolve(lib, dev, logit_dtype):
     """The fused decode entry gives the oracle's router ids/weights and the
     oracle's slot decisions, step after step, tables included."""
     import synth
@@ -138,10 +160,10 @@ def test_route_resolve_equals_router_then_resolve(lib, dev):
         x = synth.hidden_states(500 + s, 1).to(dev)
         bias = torch.from_numpy((rng.gumbel(size=E) * 2).astype(np.float32)).to(dev)
         lib.route_resolve(x, w, bias, K, logits, ids, wts, slot_of, slot_expert, stamp, step,
-                          out_slot, fs, fe, nm, stats)
+                          out_slot, fs, fe, nm, stats, logit_dtype=logit_dtype)
         torch.cuda.synchronize()
         o_ids, o_w, o_lg = orouter.route(x.float().cpu().numpy(), w.float().cpu().numpy(), K,
-                                         bias.cpu().numpy())
+                                         bias.cpu().numpy(), logit_dtype=logit_dtype)
         assert np.array_equal(ids.cpu().numpy(), o_ids), f"step {s}"
         np.testing.assert_allclose(wts.cpu().numpy(), o_w, rtol=2e-6, atol=1e-7)
         want = oslots.resolve(tab, o_ids[0].tolist())

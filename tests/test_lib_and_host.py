@@ -40,15 +40,18 @@ def test_preconditions_are_rejected_without_launching(lib):
     assert c.moe_fp8_moe_forward(1, 1, 0, 1, 2, 1, 8, 16, 1, 16, 1, 4, 2000, 512, 1, 16, 1 << 30,
                                  None) == -1
     assert b"hidden" in c.moe_last_error()
-    assert c.moe_router_topk(16, 16, None, 1, 2048, 256, 40, 1, 1, 0, 1, 2, None) == -1
-    assert c.moe_route_resolve(16, 16, None, 2048, 256, 8, 1, 1, 1, 1, 1, 1, 9999, 1, 1, 1, 1, 1,
-                               None, None) == -1
+    bf16 = 3                                   # MOE_BF16 logits
+    assert c.moe_router_topk(16, 16, None, bf16, 1, 2048, 256, 40, 1, 1, 0, 1, 2, None) == -1
+    assert c.moe_router_topk(16, 16, None, 0, 1, 2048, 256, 8, 1, 1, 0, 1, 2, None) == -1
+    assert b"logit_dtype" in c.moe_last_error()
+    assert c.moe_route_resolve(16, 16, None, bf16, 2048, 256, 8, 1, 1, 1, 1, 1, 1, 9999, 1, 1, 1,
+                               1, 1, None, None) == -1
     assert b"cap" in c.moe_last_error()
     # more ids than slots: one slot would go to two ids of the call
     assert c.moe_resolve_slots(1, 0, 9, 1, 256, 1, 1, 8, 1, 1, 1, 1, 1, None, None) == -1
     assert b"exceeds the cache capacity" in c.moe_last_error()
-    assert c.moe_route_resolve(16, 16, None, 2048, 256, 8, 1, 1, 1, 1, 1, 1, 7, 1, 1, 1, 1, 1,
-                               None, None) == -1
+    assert c.moe_route_resolve(16, 16, None, bf16, 2048, 256, 8, 1, 1, 1, 1, 1, 1, 7, 1, 1, 1, 1,
+                               1, None, None) == -1
     assert b"exceeds the cache capacity" in c.moe_last_error()
 
 
