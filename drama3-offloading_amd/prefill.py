@@ -132,7 +132,11 @@ class DevicePrefill:
                           blocks_per_job=HOST_BLOCKS_PER_JOB)
 
         if cache is None:
-            from_host(self.uniq, self.rows, self.n_unique)
+            # no cache: the plan sends every expert to the host list (and
+            # counts them in self.stats)
+            lib.gather_plan(self.uniq, self.n_unique, None, 0, self.host_expert,
+                            self.host_dst, self.n_host, self.cache_src, self.cache_dst,
+                            self.n_cache, self.stats)
         else:
             slot_of, cap, cache_src = cache
             if len(cache_src) != len(self.gather):
@@ -143,7 +147,7 @@ class DevicePrefill:
             cache_pairs = [(s, d, b) for s, d, b in zip(cache_src, dst, self.row_bytes)]
             lib.fetch(cache_pairs, self.cache_src, self.cache_dst, self.n_cache,
                       max_jobs=self.E, blocks_per_job=CACHE_BLOCKS_PER_JOB)
-            from_host(self.host_expert, self.host_dst, self.n_host)
+        from_host(self.host_expert, self.host_dst, self.n_host)
         return self.inverse[:P].view(T, K)
 
     def forward(self, x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,

@@ -1,7 +1,7 @@
 """Device-side prefill gather on the GPU: the gather plan against the
 oracle, gathered bytes against the host records, hybrid (cache + host) equal
 to host-only byte for byte, and the MoE output through the device path equal
-to the reference-form gather path (bin/offload.py:137-239) bit for bit."""
+to the resident kernel bit for bit."""
 import numpy as np
 import pytest
 import torch
@@ -53,6 +53,7 @@ def layer(dev):
     host = moe.MoEExperts(E, H, I, device="cpu")
     for n in ("w13_weight", "w2_weight", "w13_scale_inv", "w2_scale_inv"):
         setattr(host, n, getattr(ref, n).cpu().pin_memory())
+    host._layer_index = 0
     return ref, host
 
 
@@ -119,26 +120,29 @@ def test_hybrid_gather_equals_host_gather(lib, dev, layer):
         assert torch.equal(t0, t1)               # the table is only read
 
 
-def test_dev_cached_forward_device_prefill_equals_reference_form(lib, dev, layer):
+def test_dev_cached_forward_prefill_equals_resident(lib, dev, layer):
+    """A multi-token call on a layer with a device cache goes to offload's
+    direct gather (device-side, borrowing the cache) in every copy mode's
+    default; its output equals the resident forward's, and the cache table
+    is only read."""
     import devcache
     import offload
+    from fp8_moe import fp8_moe_forward
     ref, host = layer
     devcache.init_dev_cache(host, dev, 16)
     devcache.dev_resolve_and_fetch(host, _routing(1, 7, dev)[0])
     T = 33
     x = torch.randn((T, H), device=dev).to(torch.bfloat16)
     ids, w = _routing(T, 3, dev)
-    assert devcache.DEVICE_PREFILL is False
-    say("prefill: dev_cached_forward, reference-form then device path")
-    want = devcache.dev_cached_forward(host, x, ids, w)
-    devcache.DEVICE_PREFILL = True
-    try:
-        got = devcache.dev_cached_forward(host, x, ids, w)
-    finally:
-        devcache.DEVICE_PREFILL = False
+    stamp = host._dc_stamp.clone()
+    say("prefill: dev_cached_forward of 33 tokens")
+    assert offload.HYBRID_GATHER and offload.COPY_MODE == "direct"
+    got = devcache.dev_cached_forward(host, x, ids, w)
+    want = fp8_moe_forward(x, ids, w, ref.w13_weight, ref.w13_scale_inv, ref.w2_weight,
+                           ref.w2_scale_inv)
     torch.cuda.synchronize()
-    assert offload.HYBRID_GATHER
     assert torch.equal(got, want)
+    assert torch.equal(stamp, host._dc_stamp)
 
 
 def test_device_prefill_is_capturable_and_dynamic(lib, dev, layer):

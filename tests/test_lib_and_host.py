@@ -184,26 +184,6 @@ def test_capacity_sizing_arithmetic():
                                           cap_per_layer=96) == 96
 
 
-def test_router_trace_and_census_host_logic():
-    import offload
-    offload.enable_census(2, 8)
-    offload.TRACE.enabled = True
-    offload.TRACE.records.clear()
-    try:
-        offload._count(1, torch.tensor([[1, 2, 3]]))
-        offload._count(1, torch.tensor([[1, 2, 3], [3, 4, 5]]))
-        offload.TRACE.add(1, torch.tensor([[1, 2, 3]]))
-        offload.TRACE.add(0, torch.tensor([[1, 2], [3, 4]]))
-        assert offload.CENSUS[1].tolist() == [0, 2, 2, 3, 1, 1, 0, 0]
-        assert offload.CENSUS_DECODE[1].tolist() == [0, 1, 1, 1, 0, 0, 0, 0]
-        assert [r["phase"] for r in offload.TRACE.records] == ["decode", "prefill"]
-    finally:
-        offload.CENSUS = None
-        offload.CENSUS_DECODE = None
-        offload.TRACE.enabled = False
-        offload.TRACE.records.clear()
-
-
 def test_fp8_moe_forward_has_no_cpu_path(lib):
     from fp8_moe import fp8_moe_forward
     x = torch.zeros((1, 256), dtype=torch.bfloat16)
