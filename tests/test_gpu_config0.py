@@ -77,5 +77,6 @@ def test_single_layer_decode_all_miss(lib, dev):
         print(f"config 0: ids {ids[0].tolist()}, max rel err vs W8A8 {err:.2e}, "
               f"vs dequantise path {gap:.2e}")
         assert err <= 1e-2
+        assert gap <= 6e-2          # the activation quantisation error, 4.5e-2 measured
     finally:
         pool.close()

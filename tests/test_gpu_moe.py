@@ -3,7 +3,8 @@
 Tolerance: max |got - want| / max |want| <= 1e-2 against oracle.moe.forward_w8a8
 (the stated bf16/fp8 bar is 2e-2, bin/test_cache.py:51).  The distance to the
 dequantise-then-matmul path (oracle.moe.forward_w8a16) is the activation
-quantisation error and is reported, bounded at 0.1.
+quantisation error (4.2-4.5 % on these inputs, computed oracle to oracle)
+and is reported, bounded at 6e-2.
 """
 import numpy as np
 import pytest
@@ -61,7 +62,7 @@ def test_decode_one_token_eight_experts(lib, dev, recipe):
     gap = omoe.max_rel_err(_np(got), omoe.forward_w8a16(*args))
     print(f"{recipe}: max rel err vs W8A8 oracle {err:.2e}, vs W8A16 {gap:.2e}")
     assert err <= TOL
-    assert gap <= 0.1
+    assert gap <= 6e-2
 
 
 def test_several_tokens_and_dtypes(lib, dev):
