@@ -56,6 +56,56 @@ def timed_replays(h, n: int):
     return a.elapsed_time(b) / 1000.0
 
 
+def timed_window(h, steps: int, split: int):
+    """Time `steps` replays with events on the replay stream; after replay
+    `split` an event and a device-side copy of the hit/miss counters mark
+    the popularity drift inside the window (no host sync in the window).
+    Returns (seconds, seconds of the first `split` replays, counters at the
+    split, counters at the end)."""
+    import torch
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    at_split = torch.empty_like(h.stats)
+    start = h.stats.clone()
+    ev[0].record()
+    h.replay(split)
+    at_split.copy_(h.stats)
+    ev[1].record()
+    h.replay(steps - split)
+    ev[2].record()
+    torch.cuda.synchronize()
+    return (ev[0].elapsed_time(ev[2]) / 1000.0, ev[0].elapsed_time(ev[1]) / 1000.0,
+            (at_split - start).sum(0).tolist(), (h.stats - at_split).sum(0).tolist())
+
+
+def router_contracts(lib, hc, steps: int = 25) -> dict:
+    """On the decode workload's own hidden states (eager steps, layer by
+    layer): how often the top-8 expert set under bf16 gate logits differs
+    from the one under float32 logits.  Runs after the timed steps (it
+    advances the caches)."""
+    import torch
+    cfg, dev = hc.cfg, hc.dev
+    K, E = cfg.top_k, cfg.n_experts
+    ids = [torch.empty((1, K), dtype=torch.int32, device=dev) for _ in range(2)]
+    wts = torch.empty((1, K), device=dev)
+    logits = torch.empty((1, E), device=dev)
+    differ = torch.zeros((), dtype=torch.int64, device=dev)
+    for s in range(steps):
+        hc.stage(s)
+        hc.x.copy_(hc.x0)
+        for l in range(cfg.layers):
+            hc.layer(l)                      # leaves layer l's hidden state in hc.h
+            for dt_, out in zip(("bf16", "f32"), ids):
+                lib.router_topk(hc.h, hc.gate[l], hc.bias_live[l], K, logits, out, wts,
+                                logit_dtype=dt_)
+            differ += (ids[0].sort().values != ids[1].sort().values).any()
+    n = steps * cfg.layers
+    return {"decisions": n, "sets_differing": int(differ.item()),
+            "rate": round(int(differ.item()) / n, 5),
+            "what": "top-8 sets under bf16 vs float32 gate logits, each layer's own hidden "
+                    "state, the workload's routing bias included"}
+
+
 def size_capacity(cfg, target: float, warm_steps: int):
     """Smallest per-layer capacity with >= target LRU hit over the schedule
     (routing approximated by top-8 of the bias, the dominant logit term)."""
@@ -438,6 +488,60 @@ def hbm_stream(dev, gib: int = 4, reps: int = 10) -> dict:
     return res
 
 
+def hbm_probe(lib, dev, gib: int = 4, calls: int = 200) -> dict:
+    """Read-only HBM floors from the library's streaming-read kernel
+    (moe_stream_read: nontemporal 16-byte loads, each word read once):
+
+      stream_GBps   one read of `gib` GiB (far past the 256 MB Infinity
+                    Cache), best over grid sizes;
+      one_pass_us   one launch reading N bytes once, for the decode FFN's
+                    25,180,160 B and its two kernels' shares (gate/up 16.8 MB,
+                    down 8.4 MB): `calls` back-to-back launches in a hipGraph,
+                    each on a different slice of the `gib` GiB region, best
+                    over grid sizes;
+      empty_us      a launch that reads 16 bytes (the launch floor in a graph);
+      two_launch_floor_us  gate/up share + down share: what two dependent
+                    one-pass launches of the decode FFN's bytes cost at best."""
+    import torch
+    n = gib << 30
+    buf = torch.empty(n, dtype=torch.uint8, device=dev)
+    buf.fill_(1)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = {"stream_GBps": 0.0, "stream_workgroups": 0}
+    for wg in (1024, 2048, 4096, 8192):
+        lib.stream_read(buf, n, wg, sink)
+        torch.cuda.synchronize(dev)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(5):
+            lib.stream_read(buf, n, wg, sink)
+        b.record()
+        torch.cuda.synchronize(dev)
+        gbs = n / (a.elapsed_time(b) / 1000.0 / 5) / 1e9
+        if gbs > out["stream_GBps"]:
+            out["stream_GBps"], out["stream_workgroups"] = round(gbs, 1), wg
+    sizes = {"ffn_25180160": 25_180_160, "gateup_16777216": 16_777_216 + 4096,
+             "down_8388608": 8_388_608 + 2048}
+    one = {}
+    for name, nbytes in sizes.items():
+        step = (nbytes + 4095) // 4096 * 4096
+        slices = n // step
+        best = None
+        for wg in (256, 512, 1024, 1536, 2048):
+            dt = graph_time(dev, lambda r: lib.stream_read(buf, nbytes, wg, sink,
+                                                           offset=(r % slices) * step), calls)
+            if best is None or dt < best[0]:
+                best = (dt, wg)
+        one[name] = {"bytes": nbytes, "us": round(1e6 * best[0], 3), "workgroups": best[1],
+                     "GBps": round(nbytes / best[0] / 1e9, 1)}
+    out["one_pass_us"] = one
+    dt = graph_time(dev, lambda r: lib.stream_read(buf, 16, 1, sink), calls)
+    out["empty_us"] = round(1e6 * dt, 3)
+    out["two_launch_floor_us"] = round(one["gateup_16777216"]["us"] + one["down_8388608"]["us"], 3)
+    del buf
+    return out
+
+
 def fill_pool_bytes(pool, dev, seed: int, chunk: int = 64) -> None:
     """Seeded random bytes in every record of a page-locked pool (fetch
     timing and byte-exact checks need distinct records, not weights)."""
@@ -451,8 +555,8 @@ def fill_pool_bytes(pool, dev, seed: int, chunk: int = 64) -> None:
 
 
 def run_probe(args) -> int:
-    """--probe gemv|fetch|codec|copy|grouped|shared: the named kernel(s) alone, many launches,
-    one JSON line."""
+    """--probe gemv|fetch|codec|copy|grouped|shared|hbm: the named kernel(s) alone, many
+    launches, one JSON line."""
     import torch
     import hipfetch
     from hostpool import DRAMA3, HostPool
@@ -521,6 +625,8 @@ def run_probe(args) -> int:
         res = {"probe": "shared", "what": "shared expert gate/up + down, 1 token, graph of "
                "back-to-back calls over 40 layers' bf16 weights", "us_per_call": round(1e6 * dt, 3),
                "bytes_per_call": nbytes, "GBps": round(nbytes / dt / 1e9, 1)}
+    elif args.probe == "hbm":
+        res = {"probe": "hbm", **hbm_probe(lib, dev, calls=args.steps)}
     elif args.probe == "copy":
         # a plain elementwise copy of known size: reads and writes 256 MiB,
         # the calibration for the HBM traffic counters
@@ -574,7 +680,8 @@ def shared_resident(lib, dev, weights, calls: int = 200):
 def moe_block_bench(lib, cfg, pools, dev, steps: int, warmup: int):
     """The decode step with the full MoE block: routed experts through the
     cache plus the gated shared expert, and the finiteness guard, in one
-    hipGraph (same schedule and cache size as the headline step)."""
+    hipGraph (same schedule, cache size and timed window as the headline
+    step)."""
     import torch
     import decode
     cfgb = decode.DecodeConfig(**{**cfg.__dict__, "shared_expert": True})
@@ -728,7 +835,8 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the prefill and all-resident measurements")
     ap.add_argument("--tokens", type=int, default=512, help="tokens per call of --probe grouped")
-    ap.add_argument("--probe", choices=["gemv", "fetch", "codec", "copy", "grouped", "shared"],
+    ap.add_argument("--probe", choices=["gemv", "fetch", "codec", "copy", "grouped", "shared",
+                                        "hbm"],
                     help="time one kernel alone (--steps launches) instead of the decode step")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -745,7 +853,13 @@ def main() -> int:
     dev = torch.device("cuda:0")
     t_start = time.perf_counter()
 
-    cfg = decode.DecodeConfig(layers=args.layers, schedule_steps=max(200, args.warmup + args.steps),
+    # The timed window straddles a popularity drift whatever --steps is: it
+    # starts up to half a window before the first drift after the warm-up
+    # (the replays before it are untimed warm-up too).
+    drift_every = decode.DecodeConfig().drift_every
+    boundary = drift_every * (args.warmup // drift_every + 1)
+    start = max(args.warmup, boundary - args.steps // 2)
+    cfg = decode.DecodeConfig(layers=args.layers, schedule_steps=max(200, start + args.steps),
                               noncoherent_pool=args.noncoherent_pool)
     if args.capacity:
         cfg.capacity, sim_hit = args.capacity, float("nan")
@@ -758,17 +872,22 @@ def main() -> int:
     pools = hc.pools
     log(f"pools ready ({time.perf_counter() - t_start:.1f}s); capturing the cached step")
     hc.capture()
-    hc.replay(args.warmup)
-    torch.cuda.synchronize()
-    h0, m0 = hc.hit_rate()
-    dt = timed_replays(hc, args.steps)
-    h1, m1 = hc.hit_rate()
-    hits, misses = h1 - h0, m1 - m0
+    hc.replay(start)
+    split = min(max(boundary - start, 0), args.steps)
+    dt, dt_before, (hb, mb), (ha, ma) = timed_window(hc, args.steps, split)
+    hits, misses = hb + ha, mb + ma
     hit = hits / max(1, hits + misses)
     tps_cached = args.steps / dt
+    drift = {"drift_every": drift_every, "drift_at_step": boundary,
+             "timed_steps": [start, start + args.steps],
+             "hit_before": round(hb / max(1, hb + mb), 4) if split else None,
+             "hit_from_drift": round(ha / max(1, ha + ma), 4) if split < args.steps else None,
+             "tokens_per_s_before": round(split / dt_before, 3) if split else None,
+             "tokens_per_s_from_drift": round((args.steps - split) / (dt - dt_before), 3)
+             if split < args.steps else None}
     x_ok = bool(torch.isfinite(hc.x.float()).all())
     log(f"cached: {tps_cached:.2f} tok/s, {1e3 * dt / args.steps:.3f} ms/step, hit {hit:.3f}, "
-        f"finite={x_ok}")
+        f"finite={x_ok}; drift at step {boundary}: {drift}")
 
     log("standalone kernel timing")
     link = link_peak(pools, dev)
@@ -778,8 +897,9 @@ def main() -> int:
     gemv_gbs = g_bytes / g_dt / 1e9
     lists = fetch_lists(lib, pools, dev)
     streams = hbm_stream(dev)
-    stream = max(streams.values())
-    log(f"fetch lists {lists} GB/s; HBM streaming {streams} GB/s")
+    floors = hbm_probe(lib, dev)
+    stream = floors["stream_GBps"]
+    log(f"fetch lists {lists} GB/s; HBM streaming {streams} GB/s (torch); read floors {floors}")
     log(f"link (copy engine) {link:.2f} GB/s; fetch {fetch_gbs:.2f} GB/s "
         f"({1e6 * f_dt:.1f} us/launch); GEMV {gemv_gbs:.1f} GB/s ({1e6 * g_dt:.2f} us/call)")
 
@@ -792,12 +912,16 @@ def main() -> int:
     coded = coded_pools = None
     if not args.no_extra:
         log("entropy-coded pools: encoding 40 layers")
-        coded, coded_pools = coded_bench(lib, cfg, hc, dev, args.steps, args.warmup, link)
+        coded, coded_pools = coded_bench(lib, cfg, hc, dev, args.steps, start, link)
         log(f"coded: {coded['tokens_per_s']} tok/s, {coded['ms_per_step']} ms/step "
             f"({coded['tokens_per_s_0pct_hit']} tok/s at 0 % hit), ratio "
             f"{coded['ratio']}, fetch {coded['fetch']['us_per_launch']} us/launch "
             f"({coded['fetch']['GBps_decoded']} GB/s decoded, {coded['fetch']['GBps_link']} GB/s "
             f"link), output equal to the raw-pool step: {coded['x_equal_raw_pool_step']}")
+
+    log("router contracts on the workload's hidden states")
+    contracts = router_contracts(lib, hc)
+    log(f"top-8 sets differing between bf16 and float32 logits: {contracts}")
 
     hc.graph = None
     del hc.cache, hc.views
@@ -806,7 +930,7 @@ def main() -> int:
     block = None
     if not args.no_extra:
         log("MoE block step (routed + shared expert + finiteness guard)")
-        block = moe_block_bench(lib, cfg, pools, dev, args.steps, args.warmup)
+        block = moe_block_bench(lib, cfg, pools, dev, args.steps, start)
         log(f"MoE block: {block['tokens_per_s']} tok/s, {block['ms_per_step']} ms/step, "
             f"finite flag {block['finite_flag']}, shared expert alone "
             f"{block['shared_expert_alone']['us_per_layer']} us/layer")
@@ -883,7 +1007,11 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
             "measured_stream_peak": round(stream, 1),
+            "measured_stream_peak_kind": "moe_stream_read over 4 GiB, nontemporal 16-byte "
+                                         "loads, best grid",
             "frac_of_measured_stream": round(gemv_gbs / stream, 4),
+            "one_pass_read_floor_us": floors["one_pass_us"]["ffn_25180160"]["us"],
+            "two_launch_read_floor_us": floors["two_launch_floor_us"],
             "traffic": TRAFFIC_GEMV_BYTES,
             "traffic_note": "HBM bytes per call, PMC, algorithmic 25,180,160",
             "call_us": round(1e6 * g_dt, 3),
@@ -893,6 +1021,9 @@ def main() -> int:
                                           "128-slot cache, 8 trials each, byte-exact; 256 "
                                           "as two 128-job launches"},
         "hbm_measured_GBps": streams,
+        "hbm_read_floors": floors,
+        "drift": drift,
+        "router_contracts": contracts,
         "cpu_baseline": cpu,
         "moe_block": block,
         "coded_pool": coded,

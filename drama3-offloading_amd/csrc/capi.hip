@@ -53,9 +53,49 @@ __global__ __launch_bounds__(256) void silu_check_kernel(const float* __restrict
   if (i < n) out[i] = silu_mul(g[i], u[i]);
 }
 
+// Read n16 16-byte words of src once each (grid-stride, U nontemporal loads
+// in flight per lane) and fold them into one XOR per lane; a lane writes only
+// if its XOR equals `never`, so the loads cannot be dropped and almost
+// nothing is written.
+template <int U>
+__global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restrict__ src,
+                                                          int64_t n16, uint32_t never,
+                                                          uint32_t* __restrict__ sink) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  uint32_t acc = 0;
+  for (; i + (U - 1) * stride < n16; i += U * stride) {
+    u32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(src + i + u * stride);
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  for (; i < n16; i += stride) {
+    const u32x4 v = __builtin_nontemporal_load(src + i);
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  if (acc == never) sink[0] = acc;
+}
+
 }  // namespace moe
 
 extern "C" {
+
+int moe_stream_read(const void* src, int64_t bytes, int32_t workgroups, uint32_t* sink,
+                    void* stream) {
+  MOE_REQUIRE(src && sink, "moe_stream_read: NULL pointer");
+  MOE_REQUIRE(bytes > 0 && bytes % 16 == 0, "moe_stream_read: bytes must be a positive multiple "
+              "of 16");
+  MOE_REQUIRE(reinterpret_cast<uintptr_t>(src) % 16 == 0, "moe_stream_read: src must be 16-byte "
+              "aligned");
+  MOE_REQUIRE(workgroups >= 1 && workgroups <= 65535, "moe_stream_read: need 1 <= workgroups "
+              "<= 65535");
+  hipLaunchKernelGGL(moe::stream_read_kernel<4>, dim3(workgroups), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const moe::u32x4*>(src),
+                     bytes / 16, 0x9e3779b9u, sink);
+  return moe::check_launch("moe_stream_read");
+}
 
 int moe_e4m3_check(uint32_t first, uint32_t count, uint64_t* mismatches, void* stream) {
   MOE_REQUIRE(mismatches != nullptr, "moe_e4m3_check: mismatches is NULL");

@@ -101,6 +101,22 @@ __device__ __forceinline__ void silu_quantize8(const float4 (&hr)[4], bool live,
 }
 
 
+// 8 float32 activations j..j+7 held by one lane -> e4m3 codes and the group
+// scale in LDS; 16 consecutive lanes form one 128-group.
+__device__ __forceinline__ void quantize8_f32(const float4 (&vr)[2], bool live, int j,
+                                              uint8_t* __restrict__ aq, float* __restrict__ as) {
+  const float av[8] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w, vr[1].x, vr[1].y, vr[1].z, vr[1].w};
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(av[i]));
+  amax = row16_max_f32(amax);
+  if (live) {
+    const float sc = act_scale(amax);
+    *reinterpret_cast<uint2*>(aq + j) = make_uint2(quant4_e4m3(av, sc), quant4_e4m3(av + 4, sc));
+    if ((threadIdx.x & 15) == 0) as[j >> 7] = sc;
+  }
+}
+
 template <typename T>
 __device__ __forceinline__ T wave_bcast(T v, int lane) { return __shfl(v, lane, 64); }
 

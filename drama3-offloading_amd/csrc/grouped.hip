@@ -314,8 +314,9 @@ static void launch_stream(const StreamArgs& A, int shape, int64_t max_tiles, hip
 
 // ------------------------------------------------------ SiLU * up -> e4m3
 
-// One wave per permuted row: a = SiLU(gate) * up quantised per 128, the
-// decode GEMV's silu_quantize8 on the same h values.
+// One wave per permuted row: a = SiLU(gate) * up quantised per 128, with the
+// decode GEMV's arithmetic (its gate/up kernel's silu_mul, its down kernel's
+// quantize8_f32) on the same row sums, so both paths give the same codes.
 __global__ __launch_bounds__(512) void grouped_silu_kernel(const float* __restrict__ h,
                                                            const int32_t* __restrict__ offsets,
                                                            int32_t n_experts, int32_t inter,

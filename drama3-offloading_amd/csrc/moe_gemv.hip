@@ -15,12 +15,14 @@
 // whole cache lines.  The block scales multiply the fp32 block result, so the
 // scale of every 128x128 weight block is applied exactly once per block.
 //
-// Kernel 1 (gate/up): grid (2I/32, pairs), four waves per workgroup: two
-// 16-row tiles, each split over K between two waves, x quantised into LDS by
-// the four together.  Kernel 2 (down + combine): grid (H/8, tokens), one
-// wave per two experts; each wave turns its two h rows into aq in LDS, does
-// the 8 output rows of w2 of both in one MFMA per K-block, and the
-// workgroup sums the k partials in order.
+// Kernel 1 (gate/up + SiLU): grid (I/16, pairs), four waves per workgroup:
+// gate rows 16j..16j+15 and the up rows I+16j.. of the same intermediate
+// columns, each tile split over K between two waves, x quantised into LDS by
+// the four together; the workgroup ends with a = SiLU(gate) * up of its 16
+// columns (float32, the pair's row of the workspace).  Kernel 2 (down +
+// combine): grid (H/8, tokens), one wave per two experts; each wave
+// quantises its two a rows into LDS, does the 8 output rows of w2 of both in
+// one MFMA per K-block, and the workgroup sums the k partials in order.
 #include "common.hpp"
 #include "grouped.hpp"
 #include "shared.hpp"
@@ -127,18 +129,20 @@ __device__ __forceinline__ void quantize_x8(uint4 raw, bool live, int i,
 constexpr int kGateUpTiles = 2;                  // 16-row tiles per workgroup
 constexpr int kGateUpSplit = 2;                  // waves per tile
 constexpr int kGateUpWaves = kGateUpSplit * kGateUpTiles;
+static_assert(kGateUpTiles == 2, "a workgroup pairs one gate tile with the up tile of its columns");
 constexpr int kGateUpChunk = 8;                  // K-blocks in flight per lane
 
 template <bool SHARED>
 __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
     const uint16_t* __restrict__ x, const void* __restrict__ ids, int ids64, int32_t top_k,
     const uint8_t* __restrict__ w13, const float* __restrict__ s13, int64_t w13_es,
-    int64_t s13_es, int32_t n_experts, int32_t hidden, int32_t inter, float* __restrict__ h,
+    int64_t s13_es, int32_t n_experts, int32_t hidden, int32_t inter, float* __restrict__ act,
     int32_t tokens, SharedRefs sh) {
   __shared__ __align__(16) uint8_t xq[kMaxHidden];
   __shared__ float xs[kMaxHidden / 128];
   __shared__ __align__(16) float dpart[kGateUpTiles][kMaxHidden / 128][16];
   __shared__ float spart[kGateUpTiles][kMaxHidden / 128];
+  __shared__ __align__(16) float upsum[16];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   if (SHARED && blockIdx.y >= static_cast<unsigned>(tokens * top_k)) {
@@ -189,7 +193,6 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
   const uint4 xraw = *reinterpret_cast<const uint4*>(xr + (i0 < hidden ? i0 : 0));
   const int64_t e = load_id(ids, ids64, p);
   const bool valid = e >= 0 && e < n_experts;
-  const int rows2 = 2 * inter;
   const int G = hidden >> 7;
   // wave is uniform: so are the tile, the K range and the scale row, which
   // is read with scalar loads
@@ -200,7 +203,9 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
   const int Gs = (G + kGateUpSplit - 1) / kGateUpSplit;   // K-blocks per part
   const int gb = min(part * Gs, G);      // this wave's first K-block
   const int gn = min(gb + Gs, G) - gb;   // and its count (0 for a part past the end)
-  const int r0 = (blockIdx.x * kGateUpTiles + tile) * 16;
+  // tile 0: gate rows j0..j0+15; tile 1: the up rows of the same columns
+  const int j0 = blockIdx.x * 16;
+  const int r0 = tile * inter + j0;
   const int q = lane >> 4;
   const uint8_t* wrow =
       w13 + (valid ? e : 0) * w13_es + static_cast<int64_t>(r0 + (lane & 15)) * hidden + q * 32;
@@ -225,9 +230,9 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
     quantize_x8(raw, i < hidden, i, xq, xs);
   }
   __syncthreads();
-  float* hp = h + static_cast<int64_t>(p) * rows2;
-  if (!valid) {   // no such expert (the whole workgroup): poison the rows, read nothing
-    if (owner && lane < 16) hp[r0 + lane] = __builtin_nanf("");
+  float* ap = act + static_cast<int64_t>(p) * inter;
+  if (!valid) {   // no such expert (the whole workgroup): poison the columns, read nothing
+    if (wu == 0 && lane < 16) ap[j0 + lane] = __builtin_nanf("");
     return;
   }
   // The block product d of K-block g (z = 0) times its scale product sc.
@@ -276,17 +281,27 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
     }
   }
   __syncthreads();
-  if (!owner) return;
-  // unrolled so that the LDS reads of several blocks are in flight at once
+  if (owner) {
+    // unrolled so that the LDS reads of several blocks are in flight at once
 #pragma unroll 8
-  for (int g = gn; g < G; ++g) {
-    const float4 d = *reinterpret_cast<const float4*>(&dpart[tile][g][4 * q]);
-    const v4f dv = {d.x, d.y, d.z, d.w};
-    block_fma(acc, dv, spart[tile][g]);
+    for (int g = gn; g < G; ++g) {
+      const float4 d = *reinterpret_cast<const float4*>(&dpart[tile][g][4 * q]);
+      const v4f dv = {d.x, d.y, d.z, d.w};
+      block_fma(acc, dv, spart[tile][g]);
+    }
+    // the up tile's owner hands its row sums over; every lane of a row
+    // group stores its (identical) four values
+    if (tile == 1)
+      *reinterpret_cast<float4*>(&upsum[4 * q]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
   }
-  if ((lane & 15) == 0) {
-    const int r = r0 + 4 * q;
-    *reinterpret_cast<float4*>(hp + r) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  __syncthreads();
+  if (owner && tile == 0 && (lane & 15) == 0) {
+    // a = SiLU(gate) * up of columns j0 + 4q .. +3, as the grouped path's
+    // SiLU kernel computes it from the same row sums
+    const float4 u = *reinterpret_cast<const float4*>(&upsum[4 * q]);
+    *reinterpret_cast<float4*>(ap + j0 + 4 * q) =
+        make_float4(silu_mul(acc[0], u.x), silu_mul(acc[1], u.y), silu_mul(acc[2], u.z),
+                    silu_mul(acc[3], u.w));
   }
 }
 
@@ -314,7 +329,7 @@ constexpr int kDownRows = 8;    // output rows per workgroup
 
 template <bool SHARED>
 __global__ __launch_bounds__(64 * (kMaxK / 2 + 1)) void down_gemv_kernel(
-    const float* __restrict__ h, const void* __restrict__ ids, int ids64,
+    const float* __restrict__ act, const void* __restrict__ ids, int ids64,
     const void* __restrict__ weights, int wbf16, int32_t top_k, const uint8_t* __restrict__ w2,
     const float* __restrict__ s2, int64_t w2_es, int64_t s2_es, int32_t n_experts,
     int32_t hidden, int32_t inter, const uint16_t* __restrict__ residual,
@@ -355,23 +370,19 @@ __global__ __launch_bounds__(64 * (kMaxK / 2 + 1)) void down_gemv_kernel(
   const int k1 = min(2 * wu + 1, top_k - 1);
   const int p0 = t * top_k + k0;
   const int p1 = t * top_k + k1;
-  // Both pairs' first 512 gate and up values are loaded before the weights
-  // (loads retire in issue order), so SiLU and the quantisation run while
-  // the weight tile is in flight; they do not depend on the experts and go
-  // out before the ids.
+  // Both pairs' first 512 activations are loaded before the weights (loads
+  // retire in issue order), so their quantisation runs while the weight
+  // tile is in flight; they do not depend on the experts and go out before
+  // the ids.
   // No load under a branch, for the reason given in the gate/up kernel.
   const int j0 = lane * 8 < inter ? lane * 8 : 0;
-  const float* hp0 = h + static_cast<int64_t>(p0) * (2 * inter);
-  const float* hp1 = h + static_cast<int64_t>(p1) * (2 * inter);
-  float4 hraw0[4], hraw1[4];
-  hraw0[0] = *reinterpret_cast<const float4*>(hp0 + j0);
-  hraw0[1] = *reinterpret_cast<const float4*>(hp0 + j0 + 4);
-  hraw0[2] = *reinterpret_cast<const float4*>(hp0 + inter + j0);
-  hraw0[3] = *reinterpret_cast<const float4*>(hp0 + inter + j0 + 4);
-  hraw1[0] = *reinterpret_cast<const float4*>(hp1 + j0);
-  hraw1[1] = *reinterpret_cast<const float4*>(hp1 + j0 + 4);
-  hraw1[2] = *reinterpret_cast<const float4*>(hp1 + inter + j0);
-  hraw1[3] = *reinterpret_cast<const float4*>(hp1 + inter + j0 + 4);
+  const float* ap0 = act + static_cast<int64_t>(p0) * inter;
+  const float* ap1 = act + static_cast<int64_t>(p1) * inter;
+  float4 araw0[2], araw1[2];
+  araw0[0] = *reinterpret_cast<const float4*>(ap0 + j0);
+  araw0[1] = *reinterpret_cast<const float4*>(ap0 + j0 + 4);
+  araw1[0] = *reinterpret_cast<const float4*>(ap1 + j0);
+  araw1[1] = *reinterpret_cast<const float4*>(ap1 + j0 + 4);
   // the pairs' routing weights, combined only where they are used
   const RouteHalves wr0 = load_route_halves(weights, wbf16, p0);
   const RouteHalves wr1 = load_route_halves(weights, wbf16, p1);
@@ -395,23 +406,19 @@ __global__ __launch_bounds__(64 * (kMaxK / 2 + 1)) void down_gemv_kernel(
 #pragma unroll
   for (int c = 0; c < kDownChunk; ++c) a[c] = load_op32_nt(wrow + (c < Gi ? c : Gi - 1) * 128);
   __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the math below
-  // SiLU(gate) * up of both pairs, quantised per 128 into LDS: 16 lanes x 8
-  silu_quantize8(hraw0, lane * 8 < inter, lane * 8, aq[k0], as_[k0]);
-  silu_quantize8(hraw1, lane * 8 < inter, lane * 8, aq[k0 + 1], as_[k0 + 1]);
+  // both pairs' activations, quantised per 128 into LDS: 16 lanes x 8
+  quantize8_f32(araw0, lane * 8 < inter, lane * 8, aq[k0], as_[k0]);
+  quantize8_f32(araw1, lane * 8 < inter, lane * 8, aq[k0 + 1], as_[k0 + 1]);
   for (int base = 512; base < inter; base += 512) {
     const int j = base + lane * 8;
     const int jj = j < inter ? j : 0;
-    float4 hr[4];
-    hr[0] = *reinterpret_cast<const float4*>(hp0 + jj);
-    hr[1] = *reinterpret_cast<const float4*>(hp0 + jj + 4);
-    hr[2] = *reinterpret_cast<const float4*>(hp0 + inter + jj);
-    hr[3] = *reinterpret_cast<const float4*>(hp0 + inter + jj + 4);
-    silu_quantize8(hr, j < inter, j, aq[k0], as_[k0]);
-    hr[0] = *reinterpret_cast<const float4*>(hp1 + jj);
-    hr[1] = *reinterpret_cast<const float4*>(hp1 + jj + 4);
-    hr[2] = *reinterpret_cast<const float4*>(hp1 + inter + jj);
-    hr[3] = *reinterpret_cast<const float4*>(hp1 + inter + jj + 4);
-    silu_quantize8(hr, j < inter, j, aq[k0 + 1], as_[k0 + 1]);
+    float4 ar[2];
+    ar[0] = *reinterpret_cast<const float4*>(ap0 + jj);
+    ar[1] = *reinterpret_cast<const float4*>(ap0 + jj + 4);
+    quantize8_f32(ar, j < inter, j, aq[k0], as_[k0]);
+    ar[0] = *reinterpret_cast<const float4*>(ap1 + jj);
+    ar[1] = *reinterpret_cast<const float4*>(ap1 + jj + 4);
+    quantize8_f32(ar, j < inter, j, aq[k0 + 1], as_[k0 + 1]);
   }
   // aq[k0..k0+1] and as_[k0..k0+1] are this wave's own: its LDS accesses
   // complete in order, so a wave-scope fence (which keeps the compiler from

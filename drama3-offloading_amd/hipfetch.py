@@ -83,6 +83,7 @@ SIGNATURES = {
     "moe_all_finite": (C.c_int, [_vp, _i32, _i64, _vp, _vp]),
     "moe_e4m3_check": (C.c_int, [C.c_uint32, C.c_uint32, _vp, _vp]),
     "moe_silu_check": (C.c_int, [_vp, _vp, _vp, C.c_uint32, _vp]),
+    "moe_stream_read": (C.c_int, [_vp, _i64, _i32, _vp, _vp]),
     "moe_codec_histogram": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _i32]),
     "moe_codec_bound": (_i64, [_i64, _i64]),
     "moe_codec_encode": (_i64, [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i32]),
@@ -403,6 +404,16 @@ class Native:
                 raise ValueError("g, u and out must be contiguous float32")
         self._check(self.cdll.moe_silu_check(g.data_ptr(), u.data_ptr(), out.data_ptr(),
                                              g.numel(), self.stream()), "moe_silu_check")
+
+    def stream_read(self, src, nbytes: int, workgroups: int, sink, offset: int = 0) -> None:
+        """Read nbytes of the device tensor src from byte `offset` once
+        (moe_stream_read); sink: device uint32/int32 [>= 1]."""
+        self._on_gpu("moe_stream_read", src, sink)
+        if offset < 0 or offset + nbytes > src.numel() * src.element_size():
+            raise ValueError("stream_read range past the end of src")
+        self._check(self.cdll.moe_stream_read(src.data_ptr() + offset, nbytes, workgroups,
+                                               sink.data_ptr(), self.stream()),
+                    "moe_stream_read")
 
     # ------------------------------------------------------------ coded pools
     def codec_histogram(self, records: np.ndarray, fp8_bytes: int, threads: int = 8):

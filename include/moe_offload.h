@@ -67,6 +67,16 @@ int moe_e4m3_check(uint32_t first, uint32_t count, uint64_t* mismatches, void* s
  * (bin/devcache.py:275-277). */
 int moe_silu_check(const float* g, const float* u, float* out, uint32_t n, void* stream);
 
+/* HBM read floor: every 16-byte word of src[0, bytes) (bytes a multiple of
+ * 16, src 16-byte aligned) is read once with nontemporal loads by
+ * `workgroups` workgroups of 256 threads (1..65535), four loads in flight
+ * per lane; nothing is written unless the XOR of a lane's words equals a
+ * fixed constant (then to sink[0], device uint32).  No counterpart in the
+ * reference: it measures the read-only floor that the decode GEMV and the
+ * HBM roofline are judged against. */
+int moe_stream_read(const void* src, int64_t bytes, int32_t workgroups, uint32_t* sink,
+                    void* stream);
+
 /* ------------------------------------------------------------- host pool */
 
 /* Page-locked, device-mapped host allocation for an expert pool.
