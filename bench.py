@@ -358,6 +358,7 @@ def resident_bench(lib, harness, batches=(1, 8, 32, 128), steps: int = 20, warmu
     non-expert stub per layer, the whole step in one hipGraph."""
     import numpy as np
     import torch
+    import decode
     dev, cfg = harness.dev, harness.cfg
     L, E, K, H, I = cfg.layers, cfg.n_experts, cfg.top_k, cfg.hidden, cfg.inter
     lay = harness.layout
@@ -381,7 +382,7 @@ def resident_bench(lib, harness, batches=(1, 8, 32, 128), steps: int = 20, warmu
         def step(_r=0):
             x.copy_(x0)
             for l in range(L):
-                torch.mm(x, harness.w_stub[l], out=h)
+                decode.stub_linear(x, harness.w_stub[l], h)
                 lib.router_topk(h, gate[l], None, K, logits, ids[l], wts[l])
                 lib.fp8_moe_forward(h, ids[l], wts[l], *views[l], x, ws, residual=h)
 
@@ -555,8 +556,8 @@ def fill_pool_bytes(pool, dev, seed: int, chunk: int = 64) -> None:
 
 
 def run_probe(args) -> int:
-    """--probe gemv|fetch|codec|copy|grouped|shared|hbm: the named kernel(s) alone, many
-    launches, one JSON line."""
+    """--probe gemv|fetch|codec|copy|grouped|shared|hbm|step: the named kernel(s) alone (or
+    the captured decode step), many launches, one JSON line."""
     import torch
     import hipfetch
     from hostpool import DRAMA3, HostPool
@@ -625,6 +626,23 @@ def run_probe(args) -> int:
         res = {"probe": "shared", "what": "shared expert gate/up + down, 1 token, graph of "
                "back-to-back calls over 40 layers' bf16 weights", "us_per_call": round(1e6 * dt, 3),
                "bytes_per_call": nbytes, "GBps": round(nbytes / dt / 1e9, 1)}
+    elif args.probe == "step":
+        # the headline decode step alone (cached, ~60 % hit), --steps replays
+        # after --warmup, for kernel traces of the captured step
+        import decode
+        cfg = decode.DecodeConfig(layers=args.layers,
+                                  schedule_steps=max(200, args.warmup + args.steps))
+        cfg.capacity = args.capacity or size_capacity(cfg, args.target_hit, args.warmup)[0]
+        hc = decode.DecodeHarness(cfg, dev)
+        hc.capture()
+        hc.replay(args.warmup)
+        h0, m0 = hc.hit_rate()
+        dt = timed_replays(hc, args.steps)
+        h1, m1 = hc.hit_rate()
+        res = {"probe": "step", "capacity": cfg.capacity, "ms_per_step": round(1e3 * dt / args.steps, 4),
+               "tokens_per_s": round(args.steps / dt, 3),
+               "hit_rate": round((h1 - h0) / max(1, h1 - h0 + m1 - m0), 4)}
+        hc.close()
     elif args.probe == "hbm":
         res = {"probe": "hbm", **hbm_probe(lib, dev, calls=args.steps)}
     elif args.probe == "copy":
@@ -836,7 +854,7 @@ def main() -> int:
                     help="skip the prefill and all-resident measurements")
     ap.add_argument("--tokens", type=int, default=512, help="tokens per call of --probe grouped")
     ap.add_argument("--probe", choices=["gemv", "fetch", "codec", "copy", "grouped", "shared",
-                                        "hbm"],
+                                        "hbm", "step"],
                     help="time one kernel alone (--steps launches) instead of the decode step")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

@@ -161,6 +161,24 @@ __device__ __forceinline__ uint64_t wave_reduce_u64(uint64_t v) {
 }
 
 // Value of lane `src` (uniform) as a scalar.
+// Sum over the wave, uniform in every lane: DPP butterfly within each row of
+// 16 lanes, then the four row sums read as scalars and added in row order.
+__device__ __forceinline__ float wave_sum_f32_dpp(float v) {
+#define MOE_DPP_ADD(CTRL)                                                                  \
+  v += __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, \
+                                                  0xf, 0xf, false));
+  MOE_DPP_ADD(0x0B1)   // quad_perm [1,0,3,2]
+  MOE_DPP_ADD(0x04E)   // quad_perm [2,3,0,1]
+  MOE_DPP_ADD(0x141)   // row_half_mirror
+  MOE_DPP_ADD(0x140)   // row_mirror
+#undef MOE_DPP_ADD
+  float s = 0.0f;
+#pragma unroll
+  for (int row = 0; row < 4; ++row)
+    s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), row * 16));
+  return s;
+}
+
 __device__ __forceinline__ int32_t lane_value(int32_t v, int src) {
   return __builtin_amdgcn_readlane(v, src);
 }

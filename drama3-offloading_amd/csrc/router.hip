@@ -150,10 +150,16 @@ __device__ __forceinline__ float key_logit(uint32_t k) {
 
 // Top-k of one token's logits by one wave.  Lane r < k ends up holding the
 // r-th pick (*id, *wt = its renormalised softmax weight).  Each candidate is
-// one 64-bit key, logit key above (~index) below, so a single wave-wide max
-// gives the largest logit with ties to the lower index; the pick's key is
-// then cleared.  Experts past n_experts get key 0 and are never picked
-// (top_k <= n_experts).
+// one 64-bit key, logit key above (~index) below, so a wave-wide max gives
+// the largest logit with ties to the lower index.  Experts past n_experts
+// get key 0 and are never picked (top_k <= n_experts).
+//   PER <= 4: each lane sorts its keys once; a round takes the wave maximum
+//             of the lanes' leading keys, and the winning lane (keys are
+//             distinct) moves to its next key.
+//   PER > 4:  a round takes the wave maximum of each lane's largest key,
+//             which is then cleared.
+// The weights are one exp per lane after the picks: exp(l_r - l_0) over
+// their wave-wide sum.
 template <int PER>
 __device__ __forceinline__ void wave_topk(const float* __restrict__ row, int32_t n_experts,
                                           int32_t top_k, int32_t* id, float* wt) {
@@ -166,28 +172,47 @@ __device__ __forceinline__ void wave_topk(const float* __restrict__ row, int32_t
                  ? (static_cast<uint64_t>(logit_key(row[e])) << 32) | (0xffffffffu - static_cast<uint32_t>(e))
                  : 0ull;
   }
-  float m = 0.0f, sum = 0.0f, myv = 0.0f;
-  int myi = -1;
-  for (int r = 0; r < top_k; ++r) {
-    uint64_t b = key[0];
+  uint64_t pick = 0;
+  if constexpr (PER <= 4) {
+    // descending sorting network over the lane's PER keys
+    auto cswap = [](uint64_t& a, uint64_t& b) {
+      const uint64_t hi = a > b ? a : b, lo = a > b ? b : a;
+      a = hi;
+      b = lo;
+    };
+    if constexpr (PER == 2) cswap(key[0], key[1]);
+    if constexpr (PER == 3) { cswap(key[0], key[1]); cswap(key[1], key[2]); cswap(key[0], key[1]); }
+    if constexpr (PER == 4) {
+      cswap(key[0], key[1]); cswap(key[2], key[3]);
+      cswap(key[0], key[2]); cswap(key[1], key[3]);
+      cswap(key[1], key[2]);
+    }
+    for (int r = 0; r < top_k; ++r) {
+      const uint64_t best = wave_reduce_u64<true>(key[0]);
+      if (lane == r) pick = best;
+      if (key[0] == best) {
 #pragma unroll
-    for (int j = 1; j < PER; ++j) b = key[j] > b ? key[j] : b;
-    const uint64_t best = wave_reduce_u64<true>(b);
-    const int bi = static_cast<int>(0xffffffffu - static_cast<uint32_t>(best));
+        for (int j = 0; j + 1 < PER; ++j) key[j] = key[j + 1];
+        key[PER - 1] = 0ull;
+      }
+    }
+  } else {
+    for (int r = 0; r < top_k; ++r) {
+      uint64_t b = key[0];
 #pragma unroll
-    for (int j = 0; j < PER; ++j)
-      if (key[j] == best) key[j] = 0ull;
-    const float bv = key_logit(static_cast<uint32_t>(best >> 32));
-    if (r == 0) m = bv;
-    const float ex = expf(bv - m);
-    sum += ex;
-    if (lane == r) {
-      myv = ex;
-      myi = bi;
+      for (int j = 1; j < PER; ++j) b = key[j] > b ? key[j] : b;
+      const uint64_t best = wave_reduce_u64<true>(b);
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        if (key[j] == best) key[j] = 0ull;
+      if (lane == r) pick = best;
     }
   }
-  *id = myi;
-  *wt = myv / sum;
+  const float v = key_logit(static_cast<uint32_t>(pick >> 32));
+  const float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float ex = lane < top_k ? expf(v - m) : 0.0f;
+  *id = lane < top_k ? static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(pick)) : -1;
+  *wt = ex / wave_sum_f32_dpp(ex);
 }
 
 template <int PER>

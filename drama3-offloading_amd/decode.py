@@ -3,7 +3,7 @@ hipGraph.
 
 Per layer, all on one stream, nothing synchronising and nothing allocating:
 
-    h     = x @ W_stub[l]                     non-expert compute (bf16 matmul stub)
+    h     = x W_stub[l]^T                     non-expert compute (bf16 matmul stub)
     ids,w = router(h, gate[l], bias[l])       top-8 of 256 (HIP)
     slots = resolve(ids, table[l])            device LRU, misses queued (HIP)
     fetch(pool[l] -> cache[l], misses)        zero-copy host -> HBM (HIP)
@@ -45,6 +45,17 @@ import torch
 import hipfetch
 import synth
 from hostpool import DRAMA3, HostPool, RecordLayout
+
+
+def stub_linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor) -> None:
+    """The non-expert stand-in, out = x w^T with w [out, in] bf16 (an
+    nn.Linear without bias).  One token takes torch's matrix-vector product
+    (6.8 us for 2048 x 2048 on MI355X against 12.0 us for the same product
+    as a 1-row torch.mm); more tokens a matrix product."""
+    if x.shape[0] == 1:
+        torch.mv(w, x[0], out=out[0])
+    else:
+        torch.mm(x, w.t(), out=out)
 
 
 @dataclass
@@ -127,7 +138,8 @@ class DecodeHarness:
         self.reset_tables()
         # non-expert stub, router gates, routing schedule
         g = torch.Generator(device=dev).manual_seed(cfg.seed + 1)
-        # std 1/sqrt(H) keeps the residual stream's scale from layer to layer
+        # std 1/sqrt(H) keeps the residual stream's scale from layer to layer;
+        # [out, in] per layer, the layout of an nn.Linear weight
         self.w_stub = (torch.randn((L, H, H), generator=g, device=dev) * (1.0 / H ** 0.5)).to(torch.bfloat16)
         self.gate = (torch.randn((L, E, H), generator=g, device=dev) * cfg.gate_std).to(torch.bfloat16)
         rng = np.random.default_rng(cfg.seed)
@@ -184,7 +196,7 @@ class DecodeHarness:
     # -------------------------------------------------------------- step
     def layer(self, l: int) -> None:
         cfg, lib = self.cfg, self.lib
-        torch.mm(self.x, self.w_stub[l], out=self.h)
+        stub_linear(self.x, self.w_stub[l], self.h)
         w13, s13, w2, s2 = self.views[l]
         if cfg.mode == "cached":
             # router + slot resolve (two launches), then the miss fetch

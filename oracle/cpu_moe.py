@@ -49,10 +49,11 @@ def moe_forward_cpu(x: torch.Tensor, ids: torch.Tensor, wts: torch.Tensor,
 
 
 def decode_step_cpu(x, w_stub, gate, bias, records, layout, top_k=8, layers=None):
-    """One batch-1 decode step over `layers` layers (all by default)."""
+    """One batch-1 decode step over `layers` layers (all by default);
+    w_stub [L, out, in] as the GPU harness holds it: h = x w_stub[l]^T."""
     L = w_stub.shape[0] if layers is None else layers
     for l in range(L):
-        h = x @ w_stub[l]
+        h = x @ w_stub[l].T
         logits = h @ gate[l].T + bias[l]
         val, ids = torch.topk(logits, top_k, dim=-1)
         wts = torch.softmax(val, dim=-1)

@@ -54,7 +54,7 @@ def test_decode_step_cpu_equals_float64_composition():
                                   hostpool.DRAMA3, top_k=K).numpy()
     xv = x.numpy().astype(np.float64)
     for l in range(L):
-        h = xv @ w_stub[l].numpy().astype(np.float64)
+        h = xv @ w_stub[l].numpy().astype(np.float64).T
         logits = h @ gate[l].numpy().astype(np.float64).T + bias[l].numpy()
         ids = np.argsort(-logits[0], kind="stable")[:K]
         sel = logits[0, ids]
