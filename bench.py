@@ -268,6 +268,105 @@ def gemv_resident(lib, dev, layout, n_records: int = 2048, calls: int = 200, top
     return dt, top_k * layout.record_bytes + 2 * 2 * layout.hidden
 
 
+def contention(lib, pools, dev, gemv_calls: int = 2000, fetches: int = 40,
+               jobs: int = 8) -> dict:
+    """The reference's open question (notes/06-cuda-graphs-plan.md:216-225):
+    does a fetch KERNEL, which occupies compute units, slow the expert GEMM
+    beside it where the copy engine would not?  Three streams of the same
+    priority: the decode expert FFN (graph of `gemv_calls` calls over 2048
+    resident records), the fetch kernel (graph of `fetches` launches of
+    `jobs` records), the copy engine (hipMemcpyAsync of the same bytes).
+    Each runs alone, then the FFN beside the fetch kernel and beside the
+    copy engine; every stream is timed with events on itself."""
+    import numpy as np
+    import torch
+    from hostpool import DRAMA3
+    L = len(pools)
+    RB = DRAMA3.record_bytes
+    rec = resident_records(dev, 2048, DRAMA3)
+    views = DRAMA3.views(rec)
+    rng = np.random.default_rng(12)
+    ids = torch.tensor(np.stack([rng.choice(2048, 8, replace=False)
+                                 for _ in range(gemv_calls)])[:, None, :], dtype=torch.int32,
+                       device=dev)
+    x = torch.randn((1, DRAMA3.hidden), device=dev).to(torch.bfloat16)
+    w = torch.full((1, 8), 1.0 / 8, device=dev)
+    out = torch.empty_like(x)
+    ws = torch.empty(lib.fp8_moe_workspace(1, 8, 2048, DRAMA3.hidden, DRAMA3.inter),
+                     dtype=torch.uint8, device=dev)
+    cache = torch.zeros((jobs, RB), dtype=torch.uint8, device=dev)
+    lists = torch.tensor(np.stack([rng.choice(pools[0].n, jobs, replace=False)
+                                   for _ in range(fetches)]), dtype=torch.int32, device=dev)
+    fslot = torch.arange(jobs, dtype=torch.int32, device=dev)
+    nmiss = torch.tensor([jobs], dtype=torch.int32, device=dev)
+    pairs = [p.fetch_pair(cache) for p in pools]
+    # the copy engine moves `jobs` consecutive records per copy (one hipMemcpyAsync)
+    srcs = [pools[r % L].tensor[(r * jobs) % (pools[0].n - jobs):][:jobs] for r in range(fetches)]
+    streams = {k: torch.cuda.Stream(device=dev) for k in ("gemv", "fetch", "copy")}
+
+    def capture(body, n):
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream(device=dev)
+        s.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(s):
+            body(0)
+        torch.cuda.synchronize(dev)
+        with torch.cuda.graph(g, stream=s):
+            for r in range(n):
+                body(r)
+        torch.cuda.synchronize(dev)
+        return g
+
+    graphs = {
+        "gemv": capture(lambda r: lib.fp8_moe_forward(x, ids[r], w, *views, out, ws, mode=1),
+                        gemv_calls),
+        "fetch": capture(lambda r: lib.fetch([pairs[r % L]], lists[r], fslot, nmiss, jobs, 2),
+                         fetches),
+    }
+
+    def run(which):
+        ev = {k: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for k in which}
+        torch.cuda.synchronize(dev)
+        for k in which:
+            with torch.cuda.stream(streams[k]):
+                ev[k][0].record()
+                if k == "copy":
+                    for r in range(fetches):
+                        cache.copy_(srcs[r], non_blocking=True)
+                else:
+                    graphs[k].replay()
+                ev[k][1].record()
+        torch.cuda.synchronize(dev)
+        return {k: ev[k][0].elapsed_time(ev[k][1]) / 1000.0 for k in which}
+
+    for k in ("gemv", "fetch", "copy"):
+        run([k])                                        # warm-up
+    alone = {k: run([k])[k] for k in ("gemv", "fetch", "copy")}
+    with_fetch = run(["gemv", "fetch"])
+    with_copy = run(["gemv", "copy"])
+    moved = fetches * jobs * RB
+    res = {
+        "gemv_us_per_call": {"alone": round(1e6 * alone["gemv"] / gemv_calls, 3),
+                             "beside_fetch_kernel": round(1e6 * with_fetch["gemv"] / gemv_calls, 3),
+                             "beside_copy_engine": round(1e6 * with_copy["gemv"] / gemv_calls, 3)},
+        "fetch_kernel_GBps": {"alone": round(moved / alone["fetch"] / 1e9, 3),
+                              "beside_gemv": round(moved / with_fetch["fetch"] / 1e9, 3)},
+        "copy_engine_GBps": {"alone": round(moved / alone["copy"] / 1e9, 3),
+                             "beside_gemv": round(moved / with_copy["copy"] / 1e9, 3)},
+        "what": f"decode expert FFN ({gemv_calls} calls, graph) on one stream beside "
+                f"{fetches} fetches of {jobs} records (fetch kernel: graph; copy engine: "
+                "hipMemcpyAsync) on another, same priority, events per stream",
+    }
+    res["gemv_slowdown_beside_fetch_kernel"] = round(
+        res["gemv_us_per_call"]["beside_fetch_kernel"] / res["gemv_us_per_call"]["alone"], 4)
+    res["gemv_slowdown_beside_copy_engine"] = round(
+        res["gemv_us_per_call"]["beside_copy_engine"] / res["gemv_us_per_call"]["alone"], 4)
+    del graphs, rec
+    torch.cuda.empty_cache()
+    return res
+
+
 def prefill_bench(lib, harness, tokens: int = 512, passes: int = 2, coded=None):
     """512-token prefill through all layers: router, distinct experts, one
     fetch of their records from the page-locked pool (no host sync), grouped
@@ -645,6 +744,13 @@ def run_probe(args) -> int:
         hc.close()
     elif args.probe == "hbm":
         res = {"probe": "hbm", **hbm_probe(lib, dev, calls=args.steps)}
+    elif args.probe == "contention":
+        pools = [HostPool(256, DRAMA3) for _ in range(4)]
+        for i, p in enumerate(pools):
+            fill_pool_bytes(p, dev, i)
+        res = {"probe": "contention", **contention(lib, pools, dev)}
+        for p in pools:
+            p.close()
     elif args.probe == "copy":
         # a plain elementwise copy of known size: reads and writes 256 MiB,
         # the calibration for the HBM traffic counters
@@ -854,7 +960,7 @@ def main() -> int:
                     help="skip the prefill and all-resident measurements")
     ap.add_argument("--tokens", type=int, default=512, help="tokens per call of --probe grouped")
     ap.add_argument("--probe", choices=["gemv", "fetch", "codec", "copy", "grouped", "shared",
-                                        "hbm", "step"],
+                                        "hbm", "step", "contention"],
                     help="time one kernel alone (--steps launches) instead of the decode step")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -914,6 +1020,8 @@ def main() -> int:
     fetch_gbs = f_bytes / f_dt / 1e9
     gemv_gbs = g_bytes / g_dt / 1e9
     lists = fetch_lists(lib, pools, dev)
+    contended = contention(lib, pools, dev)
+    log(f"fetch beside the GEMV: {contended}")
     streams = hbm_stream(dev)
     floors = hbm_probe(lib, dev)
     stream = floors["stream_GBps"]
@@ -1040,6 +1148,7 @@ def main() -> int:
                                           "as two 128-job launches"},
         "hbm_measured_GBps": streams,
         "hbm_read_floors": floors,
+        "fetch_compute_contention": contended,
         "drift": drift,
         "router_contracts": contracts,
         "cpu_baseline": cpu,
