@@ -324,12 +324,21 @@ def contention(lib, pools, dev, gemv_calls: int = 2000, fetches: int = 40,
                          fetches),
     }
 
+    gate = torch.cuda.Stream(device=dev)
+
     def run(which):
+        """Both streams wait on one event behind a ~40 ms sleep kernel, so
+        their work (enqueued meanwhile) starts together on the GPU."""
         ev = {k: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for k in which}
+        go = torch.cuda.Event()
         torch.cuda.synchronize(dev)
+        with torch.cuda.stream(gate):
+            torch.cuda._sleep(100_000_000)
+            go.record()
         for k in which:
             with torch.cuda.stream(streams[k]):
+                streams[k].wait_event(go)
                 ev[k][0].record()
                 if k == "copy":
                     for r in range(fetches):
@@ -338,7 +347,12 @@ def contention(lib, pools, dev, gemv_calls: int = 2000, fetches: int = 40,
                     graphs[k].replay()
                 ev[k][1].record()
         torch.cuda.synchronize(dev)
-        return {k: ev[k][0].elapsed_time(ev[k][1]) / 1000.0 for k in which}
+        t = {k: ev[k][0].elapsed_time(ev[k][1]) / 1000.0 for k in which}
+        if len(which) == 2:
+            a, b = which
+            t["wall"] = max(ev[a][0].elapsed_time(ev[b][1]), ev[b][0].elapsed_time(ev[a][1]),
+                            t[a] * 1000.0, t[b] * 1000.0) / 1000.0
+        return t
 
     for k in ("gemv", "fetch", "copy"):
         run([k])                                        # warm-up
@@ -346,6 +360,8 @@ def contention(lib, pools, dev, gemv_calls: int = 2000, fetches: int = 40,
     with_fetch = run(["gemv", "fetch"])
     with_copy = run(["gemv", "copy"])
     moved = fetches * jobs * RB
+    overlap = lambda t, o: round((alone["gemv"] + alone[o] - t["wall"]) /
+                                 min(alone["gemv"], alone[o]), 3)
     res = {
         "gemv_us_per_call": {"alone": round(1e6 * alone["gemv"] / gemv_calls, 3),
                              "beside_fetch_kernel": round(1e6 * with_fetch["gemv"] / gemv_calls, 3),
@@ -354,9 +370,13 @@ def contention(lib, pools, dev, gemv_calls: int = 2000, fetches: int = 40,
                               "beside_gemv": round(moved / with_fetch["fetch"] / 1e9, 3)},
         "copy_engine_GBps": {"alone": round(moved / alone["copy"] / 1e9, 3),
                              "beside_gemv": round(moved / with_copy["copy"] / 1e9, 3)},
+        "overlap_with_fetch_kernel": overlap(with_fetch, "fetch"),
+        "overlap_with_copy_engine": overlap(with_copy, "copy"),
         "what": f"decode expert FFN ({gemv_calls} calls, graph) on one stream beside "
                 f"{fetches} fetches of {jobs} records (fetch kernel: graph; copy engine: "
-                "hipMemcpyAsync) on another, same priority, events per stream",
+                "hipMemcpyAsync) on another, same priority, both released together by one "
+                "event; events per stream; overlap = (sum of the two alone - wall) / the "
+                "shorter alone, 1 = fully concurrent",
     }
     res["gemv_slowdown_beside_fetch_kernel"] = round(
         res["gemv_us_per_call"]["beside_fetch_kernel"] / res["gemv_us_per_call"]["alone"], 4)

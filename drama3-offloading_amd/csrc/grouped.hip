@@ -80,9 +80,15 @@ struct StreamArgs {
   const int32_t* n_tiles;  // tile count, written by the permute kernel
   const uint8_t* w;        // [E][rows][G*128] e4m3, expert stride w_es bytes
   const float* ws;         // [E][rows/128][G] f32, expert stride s_es floats
-  float* out;              // [pairs][rows] f32, permuted order
+  float* out;              // [pairs][rows] f32, permuted order (not in the GLU form)
   int64_t w_es, s_es;
   int32_t top_k, rows, G;
+  // GLU form (gate/up only): rows = 2 * inter, and instead of `out` the
+  // item writes a = SiLU(gate) * up quantised per 128: aq [pairs][inter]
+  // e4m3, as [pairs][inter / 128]
+  uint8_t* aq;
+  float* as;
+  int32_t inter;
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -94,9 +100,20 @@ __device__ __forceinline__ v8i lds_op32(const uint8_t* p0, const uint8_t* p1) {
   return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
 }
 
-template <int RING, int GPW, bool GATHER>
+// The GLU form of the gate/up projection.  An item takes intermediate
+// columns [c, c + 32*GPW) -- whole 128-column groups, GPW >= 4 -- with their
+// gate rows (waves 0-1) and their up rows (waves 2-3), so it holds every
+// value that SiLU(gate) * up and its per-128 quantisation of those columns
+// need.  The row sums go through LDS once (the staging area, free after the
+// K loop) and leave as e4m3 codes and scales: no float32 h round trip, no
+// separate SiLU launch.  The arithmetic is the decode GEMV's: silu_mul on
+// the same row sums, then quantize8_f32, so the codes are identical.
+constexpr int kGluPad = 4;            // LDS row padding (floats) of the epilogue tile
+
+template <int RING, int GPW, bool GATHER, bool GLU>
 __global__ __launch_bounds__(64 * kWaves) void grouped_stream_kernel(StreamArgs A) {
   static_assert(RING % GPW == 0 && RING <= kRing && GPW <= kMaxGPW, "ring slots per group");
+  static_assert(!GLU || GPW >= 4, "the GLU form needs whole 128-column groups per item");
   constexpr int KPP = RING / GPW;                   // K-blocks per pass of the ring
   __shared__ __align__(16) uint8_t smem[kLdsBytes];
   uint8_t* xt = smem;
@@ -125,9 +142,23 @@ __global__ __launch_bounds__(64 * kWaves) void grouped_stream_kernel(StreamArgs 
   const int32_t ncols = min(kTileTok, A.counts[e] - m0);
   const int nct = (ncols + 15) >> 4;                // column tiles in use
   const int row0 = static_cast<int>(item % ipt) * (64 * GPW);
-  const int rw = row0 + wave * (16 * GPW);          // the wave's first row
-  const int sb0 = row0 >> 7;                        // the item's first scale row
-  const int nsb = ((row0 + 64 * GPW - 1) >> 7) - sb0 + 1;
+  // GLU: the item's columns c0..c0+32*GPW-1; waves 0-1 take their gate rows,
+  // waves 2-3 their up rows (row inter + c)
+  const int c0 = row0 >> 1;
+  const int rw = GLU ? (wave >> 1) * A.inter + c0 + (wave & 1) * (16 * GPW)
+                     : row0 + wave * (16 * GPW);    // the wave's first row
+  // weight-scale rows staged for the item: one contiguous band, or (GLU)
+  // the gate band then the up band of nb rows each
+  const int nb = GLU ? (32 * GPW + 127) >> 7 : 0;
+  const int sb0 = GLU ? c0 >> 7 : row0 >> 7;        // the item's first scale row
+  const int nsb = GLU ? 2 * nb : ((row0 + 64 * GPW - 1) >> 7) - sb0 + 1;
+  auto scale_row = [&](int slot) {                  // staged slot -> scale row
+    return GLU ? (slot < nb ? sb0 + slot : ((A.inter + c0) >> 7) + slot - nb) : sb0 + slot;
+  };
+  auto scale_slot = [&](int j) {                    // group j of this wave -> staged slot
+    return GLU ? (wave >> 1) * nb + (((wave & 1) * (16 * GPW) + 16 * j) >> 7)
+               : ((rw + 16 * j) >> 7) - sb0;
+  };
   const int Gs = min(G, kStageBlocks);              // K-blocks per staged row
   const int upr = Gs * 8;                           // 16-byte units per staged row
   const int swz = (Gs & 1) ? 7 : 15;                // unit XOR mask (within the row)
@@ -176,7 +207,7 @@ __global__ __launch_bounds__(64 * kWaves) void grouped_stream_kernel(StreamArgs 
     for (int i = threadIdx.x; i < nsb * Gs; i += 64 * kWaves) {
       const int kb = kb0 + i % Gs;
       wsc[i] = kb < G ? A.ws[static_cast<int64_t>(e) * A.s_es +
-                             static_cast<int64_t>(sb0 + i / Gs) * G + kb]
+                             static_cast<int64_t>(scale_row(i / Gs)) * G + kb]
                       : 0.0f;
     }
     __builtin_amdgcn_s_waitcnt(0);                  // this wave's direct loads landed
@@ -218,7 +249,7 @@ __global__ __launch_bounds__(64 * kWaves) void grouped_stream_kernel(StreamArgs 
         }
 #pragma unroll
         for (int j = 0; j < GPW; ++j) {
-          const float wsj = wsc[(((rw + 16 * j) >> 7) - sb0) * Gs + kl];
+          const float wsj = wsc[scale_slot(j) * Gs + kl];
 #pragma unroll
           for (int m = 0; m < kColTiles; ++m) {
             if (m < nct) {
@@ -241,16 +272,62 @@ __global__ __launch_bounds__(64 * kWaves) void grouped_stream_kernel(StreamArgs 
   for (int p = 0; p + 1 < npass; ++p) pass(p, std::true_type{});
   pass(npass - 1, std::false_type{});
 
+  if constexpr (!GLU) {
 #pragma unroll
-  for (int j = 0; j < GPW; ++j)
+    for (int j = 0; j < GPW; ++j)
 #pragma unroll
-    for (int m = 0; m < kColTiles; ++m) {
-      const int cc = m * 16 + col;
-      if (m < nct && cc < ncols)
-        *reinterpret_cast<float4*>(A.out + static_cast<int64_t>(seg + cc) * A.rows + rw + 16 * j +
-                                   4 * q) = make_float4(acc[j][m][0], acc[j][m][1], acc[j][m][2],
-                                                        acc[j][m][3]);
+      for (int m = 0; m < kColTiles; ++m) {
+        const int cc = m * 16 + col;
+        if (m < nct && cc < ncols)
+          *reinterpret_cast<float4*>(A.out + static_cast<int64_t>(seg + cc) * A.rows + rw +
+                                     16 * j + 4 * q) =
+              make_float4(acc[j][m][0], acc[j][m][1], acc[j][m][2], acc[j][m][3]);
+      }
+  } else {
+    // row sums -> LDS as [gate | up][token][column] (the staging area is
+    // free once every wave is past its last K-block)
+    constexpr int kCols = 32 * GPW;                 // columns of the item
+    constexpr int kStride = kCols + kGluPad;
+    static_assert(2 * kTileTok * kStride * 4 <= kLdsBytes, "GLU epilogue tile fits the LDS");
+    float* ep = reinterpret_cast<float*>(smem);
+    __syncthreads();
+    const int half = wave >> 1;
+    const int cw = (wave & 1) * (16 * GPW);         // the wave's first column of the item
+#pragma unroll
+    for (int j = 0; j < GPW; ++j)
+#pragma unroll
+      for (int m = 0; m < kColTiles; ++m)
+        if (m < nct)
+          *reinterpret_cast<float4*>(ep + (half * kTileTok + m * 16 + col) * kStride + cw +
+                                     16 * j + 4 * q) =
+              make_float4(acc[j][m][0], acc[j][m][1], acc[j][m][2], acc[j][m][3]);
+    __syncthreads();
+    // 16 lanes per (token, 128-column group): 8 columns per lane
+    constexpr int kGroups = kCols / 128;
+    const int sub = threadIdx.x >> 4;               // 16 rows of 16 lanes
+    const int li = threadIdx.x & 15;
+    for (int u = sub; u < kTileTok * kGroups; u += 16) {
+      const int tt = u / kGroups;
+      const int cg = u - tt * kGroups;
+      const int cl = cg * 128 + li * 8;             // column within the item
+      const float* gp = ep + tt * kStride + cl;
+      const float* up = ep + (kTileTok + tt) * kStride + cl;
+      const float4 g0 = *reinterpret_cast<const float4*>(gp);
+      const float4 g1 = *reinterpret_cast<const float4*>(gp + 4);
+      const float4 u0 = *reinterpret_cast<const float4*>(up);
+      const float4 u1 = *reinterpret_cast<const float4*>(up + 4);
+      const float4 av[2] = {
+          make_float4(silu_mul(g0.x, u0.x), silu_mul(g0.y, u0.y), silu_mul(g0.z, u0.z),
+                      silu_mul(g0.w, u0.w)),
+          make_float4(silu_mul(g1.x, u1.x), silu_mul(g1.y, u1.y), silu_mul(g1.z, u1.z),
+                      silu_mul(g1.w, u1.w))};
+      const int64_t prow = seg + tt;                // this token's permuted row
+      // every lane of the 16 takes part in the group maximum; rows past the
+      // tile's tokens store nothing
+      quantize8_f32(av, tt < ncols, c0 + cl, A.aq + prow * A.inter,
+                    A.as + prow * (A.inter >> 7));
     }
+  }
 }
 
 // Work-item shapes, in increasing rows per item: (ring slots, groups of 16
@@ -299,16 +376,30 @@ static int pick_shape(int64_t P, int32_t n_experts, int32_t rows) {
   return best;
 }
 
-template <bool GATHER>
+// Whether the GLU form serves a gate/up projection of this shape: items of
+// whole 128-column groups (GPW >= 4) that tile the intermediate columns.
+static bool glu_shape(int shape, int32_t inter) {
+  const int g = kShapes[shape].gpw;
+  return g >= 4 && inter % (32 * g) == 0;
+}
+
+template <bool GATHER, bool GLU = false>
 static void launch_stream(const StreamArgs& A, int shape, int64_t max_tiles, hipStream_t s) {
   const int64_t items = max_tiles * (A.rows / (64 * kShapes[shape].gpw));
   const dim3 grid(static_cast<unsigned>((items + 7) & ~int64_t{7}));
   const dim3 block(64 * kWaves);
+  if constexpr (GLU) {
+    if (shape == 2)
+      hipLaunchKernelGGL((grouped_stream_kernel<16, 4, GATHER, true>), grid, block, 0, s, A);
+    else
+      hipLaunchKernelGGL((grouped_stream_kernel<8, 8, GATHER, true>), grid, block, 0, s, A);
+    return;
+  }
   switch (shape) {
-    case 0: hipLaunchKernelGGL((grouped_stream_kernel<16, 1, GATHER>), grid, block, 0, s, A); break;
-    case 1: hipLaunchKernelGGL((grouped_stream_kernel<16, 2, GATHER>), grid, block, 0, s, A); break;
-    case 2: hipLaunchKernelGGL((grouped_stream_kernel<16, 4, GATHER>), grid, block, 0, s, A); break;
-    default: hipLaunchKernelGGL((grouped_stream_kernel<8, 8, GATHER>), grid, block, 0, s, A); break;
+    case 0: hipLaunchKernelGGL((grouped_stream_kernel<16, 1, GATHER, false>), grid, block, 0, s, A); break;
+    case 1: hipLaunchKernelGGL((grouped_stream_kernel<16, 2, GATHER, false>), grid, block, 0, s, A); break;
+    case 2: hipLaunchKernelGGL((grouped_stream_kernel<16, 4, GATHER, false>), grid, block, 0, s, A); break;
+    default: hipLaunchKernelGGL((grouped_stream_kernel<8, 8, GATHER, false>), grid, block, 0, s, A); break;
   }
 }
 
@@ -394,13 +485,22 @@ int launch_grouped(const uint16_t* x, const void* ids, int ids64, const void* we
   gu.counts = counts;  gu.offsets = offsets;  gu.tiles = tiles;  gu.n_tiles = n_tiles;
   gu.w = w13;  gu.ws = s13;  gu.out = h;  gu.w_es = es.w13;  gu.s_es = es.s13;
   gu.top_k = top_k;  gu.rows = 2 * inter;  gu.G = hidden / 128;
-  launch_stream<true>(gu, pick_shape(P, n_experts, gu.rows), max_tiles, s);
-  rc = check_launch("moe_fp8_moe_forward(grouped gate/up)");
-  if (rc) return rc;
-  hipLaunchKernelGGL(grouped_silu_kernel, dim3(static_cast<unsigned>((P + 7) / 8)), dim3(512), 0, s,
-                     h, offsets, n_experts, inter, aq, as_);
-  rc = check_launch("moe_fp8_moe_forward(grouped silu)");
-  if (rc) return rc;
+  gu.aq = aq;  gu.as = as_;  gu.inter = inter;
+  const int gu_shape = pick_shape(P, n_experts, gu.rows);
+  if (glu_shape(gu_shape, inter)) {
+    // gate/up, SiLU * up and its quantisation in one launch
+    launch_stream<true, true>(gu, gu_shape, max_tiles, s);
+    rc = check_launch("moe_fp8_moe_forward(grouped gate/up + SiLU)");
+    if (rc) return rc;
+  } else {
+    launch_stream<true>(gu, gu_shape, max_tiles, s);
+    rc = check_launch("moe_fp8_moe_forward(grouped gate/up)");
+    if (rc) return rc;
+    hipLaunchKernelGGL(grouped_silu_kernel, dim3(static_cast<unsigned>((P + 7) / 8)), dim3(512), 0,
+                       s, h, offsets, n_experts, inter, aq, as_);
+    rc = check_launch("moe_fp8_moe_forward(grouped silu)");
+    if (rc) return rc;
+  }
   StreamArgs dn{};
   dn.act = aq;  dn.act_s = as_;  dn.sorted = nullptr;
   dn.counts = counts;  dn.offsets = offsets;  dn.tiles = tiles;  dn.n_tiles = n_tiles;
