@@ -261,7 +261,8 @@ def gemv_resident(lib, dev, layout, n_records: int = 2048, calls: int = 200, top
     out = torch.empty_like(x)
     ws = torch.empty(lib.fp8_moe_workspace(1, top_k, n_records, layout.hidden, layout.inter),
                      dtype=torch.uint8, device=dev)
-    dt = graph_time(dev, lambda r: lib.fp8_moe_forward(x, ids[r], w, *views, out, ws, mode=1), calls)
+    dt = graph_time(dev, lambda r: lib.fp8_moe_forward(x, ids[r], w, *views, out, ws, mode=1,
+                                                      layout=layout.code), calls)
     if not bool(torch.isfinite(out.float()).all()):
         raise RuntimeError("GEMV probe produced non-finite output")
     del rec
@@ -318,8 +319,8 @@ def contention(lib, pools, dev, gemv_calls: int = 2000, fetches: int = 40,
         return g
 
     graphs = {
-        "gemv": capture(lambda r: lib.fp8_moe_forward(x, ids[r], w, *views, out, ws, mode=1),
-                        gemv_calls),
+        "gemv": capture(lambda r: lib.fp8_moe_forward(x, ids[r], w, *views, out, ws, mode=1,
+                                                      layout=DRAMA3.code), gemv_calls),
         "fetch": capture(lambda r: lib.fetch([pairs[r % L]], lists[r], fslot, nmiss, jobs, 2),
                          fetches),
     }
@@ -448,7 +449,7 @@ def prefill_bench(lib, harness, tokens: int = 512, passes: int = 2, coded=None):
     local = pf.inverse[:tokens * K].view(tokens, K).clone()
     out = torch.empty_like(x)
     g_dt = graph_time(dev, lambda r: lib.fp8_moe_forward(x0, local, wts, w13, s13, w2, s2, out,
-                                                         pf.ws, mode=2), 20)
+                                                         pf.ws, mode=2, layout=pf.layout), 20)
     n_last = int(n_unique[L - 1])
     g_bytes = n_last * harness.layout.record_bytes + tokens * H * 2 * 2
     g_flops = tokens * K * 2 * (2 * cfg.inter * H + H * cfg.inter)
@@ -503,7 +504,8 @@ def resident_bench(lib, harness, batches=(1, 8, 32, 128), steps: int = 20, warmu
             for l in range(L):
                 decode.stub_linear(x, harness.w_stub[l], h)
                 lib.router_topk(h, gate[l], None, K, logits, ids[l], wts[l])
-                lib.fp8_moe_forward(h, ids[l], wts[l], *views[l], x, ws, residual=h)
+                lib.fp8_moe_forward(h, ids[l], wts[l], *views[l], x, ws, residual=h,
+                                    layout=harness.layout.code)
 
         s = torch.cuda.Stream(device=dev)
         s.wait_stream(torch.cuda.current_stream(dev))
@@ -732,7 +734,7 @@ def run_probe(args) -> int:
         ws = torch.empty(lib.fp8_moe_workspace(T, K, E, DRAMA3.hidden, DRAMA3.inter),
                          dtype=torch.uint8, device=dev)
         dt = graph_time(dev, lambda r: lib.fp8_moe_forward(x, ids, wts, w13, s13, w2, s2, out, ws,
-                                                          mode=2), args.steps)
+                                                          mode=2, layout=DRAMA3.code), args.steps)
         distinct = int(torch.unique(ids).numel())
         nbytes = distinct * DRAMA3.record_bytes
         res = {"probe": "grouped", "what": f"grouped FFN, {T} tokens x top-{K} uniform over {E} "

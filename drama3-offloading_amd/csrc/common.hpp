@@ -196,17 +196,39 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // 32 bytes (two 16-byte loads) as an MFMA operand; `p` 16-byte aligned.
-// The _nt form streams from HBM without keeping the lines in the caches.
-__device__ __forceinline__ v8i load_op32_nt(const uint8_t* p) {
-  const u32x4* s = reinterpret_cast<const u32x4*>(p);
-  u32x4 lo = __builtin_nontemporal_load(s);
-  u32x4 hi = __builtin_nontemporal_load(s + 1);
-  return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-}
 __device__ __forceinline__ v8i load_op32(const uint8_t* p) {
   const u32x4* s = reinterpret_cast<const u32x4*>(p);
   u32x4 lo = s[0];
   u32x4 hi = s[1];
+  return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+}
+
+// Where a lane finds its MFMA A operand in an expert's [R, K] e4m3 weight
+// matrix: the 32 bytes of row `row`, reduction indices [32q, 32q + 32) of
+// K-block 0, as two 16-byte halves `half` bytes apart; K-block b is b *
+// `kstep` further on, and the row 16 below is 16 * K further on in both
+// orders.
+//   row-major:   row * K + 32q;                          kstep 128,  half 16
+//   MFMA tiles:  (row & ~15) * K + (16q + row % 16) * 16; kstep 2048, half 1024
+// In tile order the 64 lanes of a wave loading rows 16g..16g+15 read 1 KiB
+// contiguous per 16-byte load (8 whole 128-byte lines); row-major, the same
+// load touches 16 lines, half of each.  The bytes each lane receives are
+// the same, so are the products.
+struct OperandWalk {
+  int64_t off;
+  int32_t kstep;
+  int32_t half;
+};
+__device__ __forceinline__ OperandWalk operand_walk(int row, int q, int64_t K, bool tiled) {
+  if (tiled)
+    return {static_cast<int64_t>(row & ~15) * K + (16 * q + (row & 15)) * 16, 2048, 1024};
+  return {static_cast<int64_t>(row) * K + 32 * q, 128, 16};
+}
+// The weight operand: nontemporal, streamed from HBM without keeping the
+// lines in the caches.
+__device__ __forceinline__ v8i load_op_nt(const uint8_t* p, int half) {
+  u32x4 lo = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  u32x4 hi = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + half));
   return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
 }
 

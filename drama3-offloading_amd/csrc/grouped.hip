@@ -83,6 +83,7 @@ struct StreamArgs {
   float* out;              // [pairs][rows] f32, permuted order (not in the GLU form)
   int64_t w_es, s_es;
   int32_t top_k, rows, G;
+  int32_t tiled;           // w in MFMA tile order (MOE_LAYOUT_TILES), else row-major
   // GLU form (gate/up only): rows = 2 * inter, and instead of `out` the
   // item writes a = SiLU(gate) * up quantised per 128: aq [pairs][inter]
   // e4m3, as [pairs][inter / 128]
@@ -170,13 +171,13 @@ __global__ __launch_bounds__(64 * kWaves) void grouped_stream_kernel(StreamArgs 
   __builtin_amdgcn_sched_barrier(0);
 
   // fill the ring: unit s = (K-block s / GPW, group s % GPW)
-  const uint8_t* wl = A.w + static_cast<int64_t>(e) * A.w_es +
-                      static_cast<int64_t>(rw + col) * K + q * 32;
+  const OperandWalk ow = operand_walk(rw + col, q, K, A.tiled);
+  const uint8_t* wl = A.w + static_cast<int64_t>(e) * A.w_es + ow.off;
   v8i a[RING];
 #pragma unroll
   for (int s = 0; s < RING; ++s) {
     const int kb = min(s / GPW, G - 1);
-    a[s] = load_op32_nt(wl + static_cast<int64_t>(s % GPW) * 16 * K + kb * 128);
+    a[s] = load_op_nt(wl + static_cast<int64_t>(s % GPW) * 16 * K + kb * ow.kstep, ow.half);
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -264,7 +265,8 @@ __global__ __launch_bounds__(64 * kWaves) void grouped_stream_kernel(StreamArgs 
         const int kn = min(kb + KPP, G - 1);
 #pragma unroll
         for (int j = 0; j < GPW; ++j)
-          a[i * GPW + j] = load_op32_nt(wl + static_cast<int64_t>(j) * 16 * K + kn * 128);
+          a[i * GPW + j] = load_op_nt(wl + static_cast<int64_t>(j) * 16 * K + kn * ow.kstep,
+                                      ow.half);
       }
     }
   };
@@ -485,6 +487,7 @@ int launch_grouped(const uint16_t* x, const void* ids, int ids64, const void* we
   gu.counts = counts;  gu.offsets = offsets;  gu.tiles = tiles;  gu.n_tiles = n_tiles;
   gu.w = w13;  gu.ws = s13;  gu.out = h;  gu.w_es = es.w13;  gu.s_es = es.s13;
   gu.top_k = top_k;  gu.rows = 2 * inter;  gu.G = hidden / 128;
+  gu.tiled = es.layout == MOE_LAYOUT_TILES;
   gu.aq = aq;  gu.as = as_;  gu.inter = inter;
   const int gu_shape = pick_shape(P, n_experts, gu.rows);
   if (glu_shape(gu_shape, inter)) {
@@ -506,6 +509,7 @@ int launch_grouped(const uint16_t* x, const void* ids, int ids64, const void* we
   dn.counts = counts;  dn.offsets = offsets;  dn.tiles = tiles;  dn.n_tiles = n_tiles;
   dn.w = w2;  dn.ws = s2;  dn.out = y;  dn.w_es = es.w2;  dn.s_es = es.s2;
   dn.top_k = top_k;  dn.rows = hidden;  dn.G = inter / 128;
+  dn.tiled = es.layout == MOE_LAYOUT_TILES;
   launch_stream<false>(dn, pick_shape(P, n_experts, dn.rows), max_tiles, s);
   rc = check_launch("moe_fp8_moe_forward(grouped down)");
   if (rc) return rc;

@@ -136,8 +136,8 @@ template <bool SHARED>
 __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
     const uint16_t* __restrict__ x, const void* __restrict__ ids, int ids64, int32_t top_k,
     const uint8_t* __restrict__ w13, const float* __restrict__ s13, int64_t w13_es,
-    int64_t s13_es, int32_t n_experts, int32_t hidden, int32_t inter, float* __restrict__ act,
-    int32_t tokens, SharedRefs sh) {
+    int64_t s13_es, int tiled, int32_t n_experts, int32_t hidden, int32_t inter,
+    float* __restrict__ act, int32_t tokens, SharedRefs sh) {
   __shared__ __align__(16) uint8_t xq[kMaxHidden];
   __shared__ float xs[kMaxHidden / 128];
   __shared__ __align__(16) float dpart[kGateUpTiles][kMaxHidden / 128][16];
@@ -207,8 +207,8 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
   const int j0 = blockIdx.x * 16;
   const int r0 = tile * inter + j0;
   const int q = lane >> 4;
-  const uint8_t* wrow =
-      w13 + (valid ? e : 0) * w13_es + static_cast<int64_t>(r0 + (lane & 15)) * hidden + q * 32;
+  const OperandWalk ow = operand_walk(r0 + (lane & 15), q, hidden, tiled);
+  const uint8_t* wrow = w13 + (valid ? e : 0) * w13_es + ow.off;
   // the tile's block scales go out before the weights (loaded after them,
   // they would add a round trip between the weights' arrival and the MFMAs)
   const float* srow =
@@ -219,7 +219,8 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
   __builtin_amdgcn_sched_barrier(0);
   v8i a[kGateUpChunk];
 #pragma unroll
-  for (int c = 0; c < kGateUpChunk; ++c) a[c] = load_op32_nt(wrow + min(gb + c, G - 1) * 128);
+  for (int c = 0; c < kGateUpChunk; ++c)
+    a[c] = load_op_nt(wrow + min(gb + c, G - 1) * ow.kstep, ow.half);
   __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the math below
   // x[t] -> e4m3 codes + per-128 scales in LDS: 8 values per lane, 16 lanes
   // per group, the workgroup's waves taking 512-value slices in turn
@@ -245,7 +246,7 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
 #pragma unroll
       for (int c = 0; c < kGateUpChunk; ++c)
         if (k0 + c < gn) {
-          a[c] = load_op32_nt(wrow + (gb + k0 + c) * 128);
+          a[c] = load_op_nt(wrow + (gb + k0 + c) * ow.kstep, ow.half);
           sw[c] = srow[gb + k0 + c];
         }
     }
@@ -331,7 +332,7 @@ template <bool SHARED>
 __global__ __launch_bounds__(64 * (kMaxK / 2 + 1)) void down_gemv_kernel(
     const float* __restrict__ act, const void* __restrict__ ids, int ids64,
     const void* __restrict__ weights, int wbf16, int32_t top_k, const uint8_t* __restrict__ w2,
-    const float* __restrict__ s2, int64_t w2_es, int64_t s2_es, int32_t n_experts,
+    const float* __restrict__ s2, int64_t w2_es, int64_t s2_es, int tiled, int32_t n_experts,
     int32_t hidden, int32_t inter, const uint16_t* __restrict__ residual,
     uint16_t* __restrict__ out, SharedRefs sh) {
   __shared__ __align__(16) uint8_t aq[kMaxK][kMaxInter];
@@ -393,8 +394,8 @@ __global__ __launch_bounds__(64 * (kMaxK / 2 + 1)) void down_gemv_kernel(
   const int Gi = inter >> 7;
   // A operand: this lane's row of its slot's expert
   const int64_t ea = half ? (valid1 ? e1 : 0) : (valid0 ? e0 : 0);
-  const uint8_t* wrow =
-      w2 + ea * w2_es + static_cast<int64_t>(c0 + (lane & 7)) * inter + q * 32;
+  const OperandWalk ow = operand_walk(c0 + (lane & 7), q, inter, tiled);
+  const uint8_t* wrow = w2 + ea * w2_es + ow.off;
   // block scales of the slot that owns this lane's D rows, before the weights
   const int64_t ed = dhalf ? (valid1 ? e1 : 0) : (valid0 ? e0 : 0);
   const float* srow = s2 + ed * s2_es + static_cast<int64_t>(c0 >> 7) * Gi;
@@ -404,7 +405,8 @@ __global__ __launch_bounds__(64 * (kMaxK / 2 + 1)) void down_gemv_kernel(
   __builtin_amdgcn_sched_barrier(0);
   v8i a[kDownChunk];
 #pragma unroll
-  for (int c = 0; c < kDownChunk; ++c) a[c] = load_op32_nt(wrow + (c < Gi ? c : Gi - 1) * 128);
+  for (int c = 0; c < kDownChunk; ++c)
+    a[c] = load_op_nt(wrow + (c < Gi ? c : Gi - 1) * ow.kstep, ow.half);
   __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the math below
   // both pairs' activations, quantised per 128 into LDS: 16 lanes x 8
   quantize8_f32(araw0, lane * 8 < inter, lane * 8, aq[k0], as_[k0]);
@@ -436,7 +438,7 @@ __global__ __launch_bounds__(64 * (kMaxK / 2 + 1)) void down_gemv_kernel(
 #pragma unroll
       for (int c = 0; c < kDownChunk; ++c)
         if (g0 + c < Gi) {
-          a[c] = load_op32_nt(wrow + (g0 + c) * 128);
+          a[c] = load_op_nt(wrow + (g0 + c) * ow.kstep, ow.half);
           sw[c] = srow[g0 + c];
         }
     }
@@ -509,13 +511,13 @@ static int launch_gemv(const uint16_t* x, const void* ids, int ids64, const void
     const unsigned sy = static_cast<unsigned>((sh->inter + 1 + per_y - 1) / per_y);
     hipLaunchKernelGGL(gateup_gemv_kernel<true>, dim3(gx / kGateUpTiles, pairs + sy),
                        dim3(64 * kGateUpWaves), 0, s, x, ids,
-                       ids64, top_k, w13, s13, es.w13, es.s13, n_experts, hidden, inter, h,
-                       tokens, *sh);
+                       ids64, top_k, w13, s13, es.w13, es.s13, static_cast<int>(es.layout),
+                       n_experts, hidden, inter, h, tokens, *sh);
   } else {
     hipLaunchKernelGGL(gateup_gemv_kernel<false>, dim3(gx / kGateUpTiles, pairs),
                        dim3(64 * kGateUpWaves), 0, s, x, ids, ids64,
-                       top_k, w13, s13, es.w13, es.s13, n_experts, hidden, inter, h, tokens,
-                       SharedRefs{});
+                       top_k, w13, s13, es.w13, es.s13, static_cast<int>(es.layout), n_experts,
+                       hidden, inter, h, tokens, SharedRefs{});
   }
   int rc = check_launch("moe_fp8_moe_forward(gate/up)");
   if (rc) return rc;
@@ -523,12 +525,13 @@ static int launch_gemv(const uint16_t* x, const void* ids, int ids64, const void
     hipLaunchKernelGGL(down_gemv_kernel<true>, dim3(hidden / kDownRows, tokens),
                        dim3(64 * ((top_k + 1) / 2 + 1)),
                        0, s, h, ids, ids64, weights, wbf16, top_k, w2, s2, es.w2, es.s2,
-                       n_experts, hidden, inter, residual, out, *sh);
+                       static_cast<int>(es.layout), n_experts, hidden, inter, residual, out, *sh);
   } else {
     hipLaunchKernelGGL(down_gemv_kernel<false>, dim3(hidden / kDownRows, tokens),
                        dim3(64 * ((top_k + 1) / 2)), 0, s,
-                       h, ids, ids64, weights, wbf16, top_k, w2, s2, es.w2, es.s2, n_experts,
-                       hidden, inter, residual, out, SharedRefs{});
+                       h, ids, ids64, weights, wbf16, top_k, w2, s2, es.w2, es.s2,
+                       static_cast<int>(es.layout), n_experts, hidden, inter, residual, out,
+                       SharedRefs{});
   }
   return check_launch("moe_fp8_moe_forward(down)");
 }
@@ -667,7 +670,10 @@ static int forward_impl(const void* x, const void* ids, int32_t ids_dtype, const
     es.s13 = (2LL * inter / 128) * (hidden / 128);
     es.w2 = static_cast<int64_t>(hidden) * inter;
     es.s2 = (static_cast<int64_t>(hidden) / 128) * (inter / 128);
+    es.layout = MOE_LAYOUT_ROWS;
   }
+  MOE_REQUIRE(es.layout == MOE_LAYOUT_ROWS || es.layout == MOE_LAYOUT_TILES,
+              "moe_fp8_moe_forward: strides->layout must be MOE_LAYOUT_ROWS or MOE_LAYOUT_TILES");
   MOE_REQUIRE(es.w13 >= 2LL * inter * hidden && es.w2 >= static_cast<int64_t>(hidden) * inter &&
                   es.s13 >= (2LL * inter / 128) * (hidden / 128) &&
                   es.s2 >= (static_cast<int64_t>(hidden) / 128) * (inter / 128),

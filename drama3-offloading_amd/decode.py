@@ -102,7 +102,9 @@ class DecodeHarness:
         self.cfg = cfg
         self.lib = hipfetch.require()
         self.dev = torch.device(device or "cuda:0")
-        self.layout = RecordLayout(cfg.hidden, cfg.inter)
+        self.layout = pools[0].layout if pools else RecordLayout(cfg.hidden, cfg.inter)
+        if (self.layout.hidden, self.layout.inter) != (cfg.hidden, cfg.inter):
+            raise ValueError("the pools' record layout does not match the config's shapes")
         L, E, K, H = cfg.layers, cfg.n_experts, cfg.top_k, cfg.hidden
         dev = self.dev
         if pools is None:
@@ -215,11 +217,12 @@ class DecodeHarness:
         if cfg.shared_expert:
             # x = h + (routed + shared): the whole block in the two decode launches
             lib.fp8_moe_block_forward(self.h, slots, self.wts[l], w13, s13, w2, s2,
-                                      self.shared(l), self.x, self.ws_block, residual=self.h)
+                                      self.shared(l), self.x, self.ws_block, residual=self.h,
+                                      layout=self.layout.code)
         else:
             # x = h + MoE(h), the residual add fused into the down kernel
             lib.fp8_moe_forward(self.h, slots, self.wts[l], w13, s13, w2, s2, self.x, self.ws,
-                                residual=self.h)
+                                residual=self.h, layout=self.layout.code)
 
     def fetch(self, l: int, experts, slots, nmiss) -> None:
         """Layer l's miss fetch: records experts[j] into cache slots slots[j],

@@ -27,13 +27,15 @@ def workspace_bytes(tokens: int, top_k: int, n_experts: int, hidden: int, inter:
 def fp8_moe_forward(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
                     w13: torch.Tensor, s13: torch.Tensor, w2: torch.Tensor, s2: torch.Tensor,
                     *, out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
-                    mode: int = MODE_AUTO) -> torch.Tensor:
+                    mode: int = MODE_AUTO, layout: int = hipfetch.LAYOUT_ROWS) -> torch.Tensor:
     """x [T, H] bf16; topk_ids [T, K] int32/int64; topk_weights [T, K] f32/bf16;
     w13 [n, 2I, H] and w2 [n, H, I] float8_e4m3fn (or uint8 views of them);
     s13 [n, 2I/128, H/128], s2 [n, H/128, I/128] float32.  Returns [T, H] bf16.
 
     `out` and `workspace` may be passed in (preallocated, e.g. for graph
-    capture); otherwise they are allocated from torch's caching allocator."""
+    capture); otherwise they are allocated from torch's caching allocator.
+    `layout`: byte order of w13/w2 -- row-major as in the checkpoint
+    (default), or hipfetch.LAYOUT_TILES for views of packed records."""
     lib = hipfetch.require()
     if not x.is_cuda:
         raise RuntimeError("fp8_moe_forward runs on the GPU only; x is on "
@@ -71,5 +73,5 @@ def fp8_moe_forward(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch
     need = lib.fp8_moe_workspace(T, K, n, H, inter)
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
-    lib.fp8_moe_forward(x, ids, wts, w13, s13, w2, s2, out, workspace, mode)
+    lib.fp8_moe_forward(x, ids, wts, w13, s13, w2, s2, out, workspace, mode, layout=layout)
     return out

@@ -30,9 +30,26 @@ _lib = None
 _err: str | None = None
 
 
+# byte order of the e4m3 expert matrices (moe_expert_strides.layout)
+LAYOUT_ROWS = 0    # row-major, the checkpoint's nn.Linear layout
+LAYOUT_TILES = 1   # MFMA tile order, the packed host records' layout
+
+
 class ExpertStrides(C.Structure):
     """moe_expert_strides (include/moe_offload.h)."""
-    _fields_ = [("w13", C.c_int64), ("s13", C.c_int64), ("w2", C.c_int64), ("s2", C.c_int64)]
+    _fields_ = [("w13", C.c_int64), ("s13", C.c_int64), ("w2", C.c_int64), ("s2", C.c_int64),
+                ("layout", C.c_int64)]
+
+
+def _expert_strides(w13, s13, w2, s2, layout: int) -> ExpertStrides:
+    """Expert-axis strides of the four weight buffers (every other dimension
+    contiguous) and their byte order."""
+    for t in (w13, s13, w2, s2):
+        if not t[0].is_contiguous():
+            raise ValueError("expert weights must be contiguous within an expert")
+    if layout not in (LAYOUT_ROWS, LAYOUT_TILES):
+        raise ValueError(f"layout must be LAYOUT_ROWS or LAYOUT_TILES, got {layout!r}")
+    return ExpertStrides(w13.stride(0), s13.stride(0), w2.stride(0), s2.stride(0), layout)
 
 
 class SharedExpert(C.Structure):
@@ -250,19 +267,17 @@ class Native:
         return int(self.cdll.moe_fp8_moe_workspace(tokens, top_k, n_experts, hidden, inter))
 
     def fp8_moe_forward(self, x, ids, weights, w13, s13, w2, s2, out, workspace,
-                        mode: int = 0, residual=None) -> None:
+                        mode: int = 0, residual=None, layout: int = LAYOUT_ROWS) -> None:
         """w13/s13/w2/s2 may be strided along the expert axis (views into a
-        packed record pool); every other dimension must be contiguous."""
+        packed record pool); every other dimension must be contiguous.
+        `layout`: byte order of w13/w2 (LAYOUT_TILES for record views)."""
         self._on_gpu("moe_fp8_moe_forward", x, ids, weights, w13, s13, w2, s2, out, workspace,
                      residual)
         T, H = x.shape
         K = ids.shape[-1]
         n = w13.shape[0]
         inter = w2.shape[-1]
-        for t in (w13, s13, w2, s2):
-            if not t[0].is_contiguous():
-                raise ValueError("expert weights must be contiguous within an expert")
-        es = ExpertStrides(w13.stride(0), s13.stride(0), w2.stride(0), s2.stride(0))
+        es = _expert_strides(w13, s13, w2, s2, layout)
         self._check(self.cdll.moe_fp8_moe_forward_ex(
             x.data_ptr(), ids.data_ptr(), self._dtype_code(ids), weights.data_ptr(),
             self._dtype_code(weights), T, K, w13.data_ptr(), s13.data_ptr(), w2.data_ptr(),
@@ -272,7 +287,7 @@ class Native:
             "moe_fp8_moe_forward")
 
     def fp8_moe_forward_noalloc(self, x, ids, weights, w13, s13, w2, s2, out, mode: int = 0,
-                                residual=None) -> None:
+                                residual=None, layout: int = LAYOUT_ROWS) -> None:
         """fp8_moe_forward with the library's per-GPU scratch array as the
         workspace: allocates nothing (moe_fp8_moe_forward_noalloc)."""
         self._on_gpu("moe_fp8_moe_forward_noalloc", x, ids, weights, w13, s13, w2, s2, out,
@@ -281,10 +296,7 @@ class Native:
         K = ids.shape[-1]
         n = w13.shape[0]
         inter = w2.shape[-1]
-        for t in (w13, s13, w2, s2):
-            if not t[0].is_contiguous():
-                raise ValueError("expert weights must be contiguous within an expert")
-        es = ExpertStrides(w13.stride(0), s13.stride(0), w2.stride(0), s2.stride(0))
+        es = _expert_strides(w13, s13, w2, s2, layout)
         self._check(self.cdll.moe_fp8_moe_forward_noalloc(
             x.data_ptr(), ids.data_ptr(), self._dtype_code(ids), weights.data_ptr(),
             self._dtype_code(weights), T, K, w13.data_ptr(), s13.data_ptr(), w2.data_ptr(),
@@ -297,7 +309,7 @@ class Native:
                                                          shared_inter))
 
     def fp8_moe_block_forward(self, x, ids, weights, w13, s13, w2, s2, shared, out, workspace,
-                              mode: int = 0, residual=None) -> None:
+                              mode: int = 0, residual=None, layout: int = LAYOUT_ROWS) -> None:
         """The MoE block: routed experts plus the gated shared expert,
         shared = (w_gate [Is, H], w_up [Is, H], w_down [H, Is], w_sgate [H]) bf16;
         out = residual + (routed + sigmoid-gated shared), each sum rounded to bf16."""
@@ -311,10 +323,7 @@ class Native:
         Is = wg.shape[0]
         if wg.shape != (Is, H) or wu.shape != (Is, H) or wd.shape != (H, Is) or wsg.numel() != H:
             raise ValueError("shared expert weights do not match x")
-        for t in (w13, s13, w2, s2):
-            if not t[0].is_contiguous():
-                raise ValueError("expert weights must be contiguous within an expert")
-        es = ExpertStrides(w13.stride(0), s13.stride(0), w2.stride(0), s2.stride(0))
+        es = _expert_strides(w13, s13, w2, s2, layout)
         se = SharedExpert(wg.data_ptr(), wu.data_ptr(), wd.data_ptr(), wsg.data_ptr(), Is)
         self._check(self.cdll.moe_fp8_moe_block_forward(
             x.data_ptr(), ids.data_ptr(), self._dtype_code(ids), weights.data_ptr(),

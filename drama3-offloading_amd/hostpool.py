@@ -12,6 +12,11 @@ scattered bases are noted at bin/bench_hostread.py:262-269).  Here a layer's
 starts 256-byte aligned), and a miss is ONE contiguous copy of one record.
 The device cache holds records in the same layout, and the expert FFN reads
 them in place through strided views (moe_expert_strides).
+
+The two e4m3 matrices are stored in MFMA tile order (MOE_LAYOUT_TILES, see
+to_tiles): each 16-row x 128-column block is 2 KiB laid out as the 64 lanes
+of a wave load it, so every 16-byte load of the expert kernels reads 1 KiB
+contiguous.  The scales are row-major.
 """
 from __future__ import annotations
 
@@ -24,10 +29,47 @@ import torch
 import hipfetch
 
 
+def _order(t, perm):
+    """permute for torch tensors, transpose for numpy arrays, made contiguous."""
+    if isinstance(t, np.ndarray):
+        return np.ascontiguousarray(t.transpose(perm))
+    return t.permute(*perm).contiguous()
+
+
+def to_tiles(w):
+    """[..., R, K] row-major e4m3 bytes (R % 16 == 0, K % 128 == 0; torch or
+    numpy, any 1-byte dtype) -> the same shape in MFMA tile order: row group
+    g = row // 16, then K-block b = col // 128, then 1 KiB half h, then
+    16-byte unit 16q + r, then byte i, where row = 16g + r and col = 128b +
+    32q + 16h + i.  Unit 16q + r of half h is what lane 16q + r of a wave
+    loads for the 16x16x128 MFMA's A operand (row r, reduction indices
+    32q + 16h ..)."""
+    *lead, R, K = w.shape
+    n = len(lead)
+    t = w.reshape(*lead, R // 16, 16, K // 128, 4, 2, 16)            # g r b q h i
+    perm = list(range(n)) + [n + 0, n + 2, n + 4, n + 3, n + 1, n + 5]   # g b h q r i
+    return _order(t, perm).reshape(*lead, R, K)
+
+
+def from_tiles(w):
+    """Inverse of to_tiles."""
+    *lead, R, K = w.shape
+    n = len(lead)
+    t = w.reshape(*lead, R // 16, K // 128, 2, 4, 16, 16)            # g b h q r i
+    perm = list(range(n)) + [n + 0, n + 4, n + 1, n + 3, n + 2, n + 5]   # g r b q h i
+    return _order(t, perm).reshape(*lead, R, K)
+
+
 @dataclass(frozen=True)
 class RecordLayout:
     hidden: int = 2048
     inter: int = 512
+    tiled: bool = True          # w13/w2 in MFMA tile order (else row-major)
+
+    @property
+    def code(self) -> int:
+        """moe_expert_strides.layout of this layout's records."""
+        return hipfetch.LAYOUT_TILES if self.tiled else hipfetch.LAYOUT_ROWS
 
     @property
     def w13_bytes(self) -> int:
@@ -70,7 +112,8 @@ class RecordLayout:
 
     def views(self, rec: torch.Tensor):
         """uint8 [n, record_bytes] -> (w13 e4m3 [n,2I,H], s13 f32, w2 e4m3 [n,H,I], s2 f32),
-        strided views along the expert axis."""
+        strided views along the expert axis.  w13/w2 hold the record's bytes
+        as stored: pass `layout=self.code` to the expert FFN."""
         n = rec.shape[0]
         H, I = self.hidden, self.inter
         w13 = rec[:, :self.off_w2].view(torch.float8_e4m3fn).view(n, 2 * I, H)
@@ -81,14 +124,38 @@ class RecordLayout:
 
     def pack(self, w13: torch.Tensor, s13: torch.Tensor, w2: torch.Tensor,
              s2: torch.Tensor) -> torch.Tensor:
-        """Dense per-buffer tensors [n, ...] -> packed uint8 records [n, record_bytes]."""
+        """Dense row-major per-buffer tensors [n, ...] (the checkpoint's
+        layout) -> packed uint8 records [n, record_bytes]."""
         n = w13.shape[0]
         rec = torch.zeros((n, self.record_bytes), dtype=torch.uint8, device=w13.device)
-        rec[:, :self.off_w2] = w13.reshape(n, -1).view(torch.uint8)
-        rec[:, self.off_w2:self.off_s13] = w2.reshape(n, -1).view(torch.uint8)
+        w13b, w2b = w13.view(torch.uint8), w2.view(torch.uint8)
+        if self.tiled:
+            w13b, w2b = to_tiles(w13b), to_tiles(w2b)
+        rec[:, :self.off_w2] = w13b.reshape(n, -1)
+        rec[:, self.off_w2:self.off_s13] = w2b.reshape(n, -1)
         rec[:, self.off_s13:self.off_s2] = s13.reshape(n, -1).contiguous().view(torch.uint8)
         rec[:, self.off_s2:self.payload_bytes] = s2.reshape(n, -1).contiguous().view(torch.uint8)
         return rec
+
+    def unpack(self, rec):
+        """Packed records [n, record_bytes] (torch or numpy uint8) -> dense
+        row-major (w13 uint8 [n,2I,H], s13 f32, w2 uint8 [n,H,I], s2 f32),
+        the inverse of pack; copies."""
+        n = rec.shape[0]
+        H, I = self.hidden, self.inter
+        w13 = rec[:, :self.off_w2].reshape(n, 2 * I, H)
+        w2 = rec[:, self.off_w2:self.off_s13].reshape(n, H, I)
+        if self.tiled:
+            w13, w2 = from_tiles(w13), from_tiles(w2)
+        if isinstance(rec, np.ndarray):
+            f32 = lambda b: np.ascontiguousarray(b).view(np.float32)
+            w13, w2 = np.array(w13), np.array(w2)
+        else:
+            f32 = lambda b: b.contiguous().view(torch.float32)
+            w13, w2 = w13.contiguous(), w2.contiguous()
+        s13 = f32(rec[:, self.off_s13:self.off_s2]).reshape(n, 2 * I // 128, H // 128)
+        s2 = f32(rec[:, self.off_s2:self.payload_bytes]).reshape(n, H // 128, I // 128)
+        return w13, s13, w2, s2
 
 
 DRAMA3 = RecordLayout()

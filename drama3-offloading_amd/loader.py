@@ -30,7 +30,7 @@ from pathlib import Path
 
 import numpy as np
 
-from hostpool import RecordLayout
+from hostpool import RecordLayout, to_tiles
 
 EXPERT = "model.language_model.layers.{layer}.mlp.experts.{expert}.{proj}.{what}"
 ROUTER_GATE = "model.language_model.layers.{layer}.mlp.gate.weight"
@@ -163,7 +163,12 @@ def fill_records(index: ShardIndex, layer: int, dst: np.ndarray, layout: RecordL
     def one(e: int) -> int:
         row = dst[e]
         for t, off in plan[e]:
-            row[off:off + t.nbytes] = maps(t.shard)[t.start:t.start + t.nbytes]
+            src = maps(t.shard)[t.start:t.start + t.nbytes]
+            if layout.tiled and t.dtype == "F8_E4M3":
+                # gate, up and down each tile on their own: gate's and up's
+                # 16-row groups do not mix, so gate | up tiled is w13 tiled
+                src = to_tiles(src.reshape(t.shape)).reshape(-1)
+            row[off:off + t.nbytes] = src
         row[layout.payload_bytes:] = 0          # alignment padding, if any
         return layout.payload_bytes
 

@@ -45,13 +45,15 @@ class DevicePrefill:
              one per storage buffer (packed: one uint8 [n, record]; the
              reference's layout: w13, w2, s13, s2)
     views:   (w13, s13, w2, s2) over the gather buffers, as fp8_moe_forward
-             takes them."""
+             takes them
+    layout:  byte order of the gathered w13/w2 (hipfetch.LAYOUT_*)."""
 
     def __init__(self, gather: list[torch.Tensor], views, top_k: int, max_tokens: int,
-                 hidden: int, inter: int):
+                 hidden: int, inter: int, layout: int = hipfetch.LAYOUT_ROWS):
         self.lib = hipfetch.require()
         self.gather = gather
         self.views = views
+        self.layout = layout
         self.E = gather[0].shape[0]
         self.K, self.max_tokens = top_k, max_tokens
         self.dev = gather[0].device
@@ -84,7 +86,8 @@ class DevicePrefill:
                     layout: RecordLayout = DRAMA3) -> "DevicePrefill":
         """Gather buffer of packed records (805 MB at Drama-3 shapes)."""
         g = torch.empty((n_experts, layout.record_bytes), dtype=torch.uint8, device=device)
-        return cls([g], layout.views(g), top_k, max_tokens, layout.hidden, layout.inter)
+        return cls([g], layout.views(g), top_k, max_tokens, layout.hidden, layout.inter,
+                   layout.code)
 
     @classmethod
     def for_experts(cls, experts, top_k: int, max_tokens: int, device) -> "DevicePrefill":
@@ -160,7 +163,7 @@ class DevicePrefill:
             out = torch.empty_like(x)
         w13, s13, w2, s2 = self.views
         self.lib.fp8_moe_forward(x, local, weights, w13, s13, w2, s2, out, self.ws, mode=2,
-                                 residual=residual)
+                                 residual=residual, layout=self.layout)
         return out
 
     def copy_stats(self) -> tuple[int, int]:

@@ -214,15 +214,33 @@ int moe_fp8_moe_forward(const void* x, const void* ids, int32_t ids_dtype,
                         int32_t hidden, int32_t inter, void* out,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* Byte order of each expert's e4m3 matrices w13 [2*inter, hidden] and w2
+ * [hidden, inter] (the scales are row-major in both):
+ *   MOE_LAYOUT_ROWS   row-major, the checkpoint's nn.Linear layout (what
+ *                     upstream fp8_moe_forward takes);
+ *   MOE_LAYOUT_TILES  MFMA operand order: an [R, K] matrix is R/16 row
+ *                     groups, each K/128 tiles of 2048 bytes in K order;
+ *                     byte (16g + r, 128b + 32q + 16h + i) of the matrix
+ *                     (r < 16, q < 4, h < 2, i < 16) sits at
+ *                     (g*K/128 + b)*2048 + h*1024 + (16q + r)*16 + i.
+ *                     A wave's 16-byte load of an MFMA A operand then reads
+ *                     1 KiB contiguous (8 whole 128-byte lines) instead of
+ *                     16 half lines; the packed host records use it.
+ * Both orders give bit-identical results. */
+#define MOE_LAYOUT_ROWS 0
+#define MOE_LAYOUT_TILES 1
+
 /* Distance between consecutive experts of each weight buffer, in elements
  * of that buffer (e4m3 bytes for w13/w2, floats for s13/s2).  Dense
  * [n, ...] buffers use the product of the trailing dimensions; a packed
- * record pool (w13|w2|s13|s2 per record) uses the record size. */
+ * record pool (w13|w2|s13|s2 per record) uses the record size.  `layout`
+ * is MOE_LAYOUT_ROWS or MOE_LAYOUT_TILES (NULL strides: dense, rows). */
 typedef struct moe_expert_strides {
   int64_t w13;
   int64_t s13;
   int64_t w2;
   int64_t s2;
+  int64_t layout;
 } moe_expert_strides;
 
 /* moe_fp8_moe_forward with explicit expert strides (NULL = dense), an

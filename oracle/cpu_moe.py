@@ -10,6 +10,12 @@ torch on the host cores in float32, reading the packed records straight out
 of the page-locked pool the GPU fetches from.  One decode step mirrors the
 GPU harness: per layer a [2048, 2048] stub matmul, the router, then the
 8 routed experts.
+
+The pool stores w13/w2 in the GPU kernels' MFMA tile order; the reference's
+host tensors are row-major.  The selected records are put back in row order
+before dequantisation and that permutation is timed apart (UNTILE_SECONDS)
+and left out of the reported times: it is a cost of this storage format,
+not of the reference's CPU path.
 """
 from __future__ import annotations
 
@@ -26,19 +32,37 @@ def dequantize_fp8_blocks(q_u8: torch.Tensor, scale_inv: torch.Tensor,
     return w * s
 
 
+# Seconds spent putting tile-ordered records back in row order (excluded
+# from the timings below); reset by each timing function.
+UNTILE_SECONDS = 0.0
+
+
+def _row_order(b: torch.Tensor) -> torch.Tensor:
+    """[n, R, K] uint8 in MFMA tile order (row group, K-block, 1 KiB half,
+    16-byte unit 16q + r, byte; hostpool.to_tiles) -> row-major."""
+    n, R, K = b.shape
+    return (b.reshape(n, R // 16, K // 128, 2, 4, 16, 16)
+            .permute(0, 1, 5, 2, 4, 3, 6).reshape(n, R, K))
+
+
 def moe_forward_cpu(x: torch.Tensor, ids: torch.Tensor, wts: torch.Tensor,
                     records: torch.Tensor, layout) -> torch.Tensor:
     """x [T, H] float32, ids/wts [T, K], records uint8 [E, record_bytes]."""
+    global UNTILE_SECONDS
     T, K = ids.shape
     H, I = layout.hidden, layout.inter
     uniq, inv = torch.unique(ids, return_inverse=True)
     rec = records[uniq]                                          # CPU gather (select_fp8)
     n = rec.shape[0]
-    w13 = dequantize_fp8_blocks(rec[:, :layout.off_w2].view(n, 2 * I, H),
-                                rec[:, layout.off_s13:layout.off_s2].contiguous()
+    q13 = rec[:, :layout.off_w2].view(n, 2 * I, H)
+    q2 = rec[:, layout.off_w2:layout.off_s13].view(n, H, I)
+    if getattr(layout, "tiled", False):
+        t0 = time.perf_counter()
+        q13, q2 = _row_order(q13), _row_order(q2)
+        UNTILE_SECONDS += time.perf_counter() - t0
+    w13 = dequantize_fp8_blocks(q13, rec[:, layout.off_s13:layout.off_s2].contiguous()
                                 .view(torch.float32).view(n, 2 * I // 128, H // 128))
-    w2 = dequantize_fp8_blocks(rec[:, layout.off_w2:layout.off_s13].view(n, H, I),
-                               rec[:, layout.off_s2:layout.payload_bytes].contiguous()
+    w2 = dequantize_fp8_blocks(q2, rec[:, layout.off_s2:layout.payload_bytes].contiguous()
                                .view(torch.float32).view(n, H // 128, I // 128))
     flat = inv.reshape(-1)
     xs = x.repeat_interleave(K, dim=0).unsqueeze(-1)             # [T*K, H, 1]
@@ -65,10 +89,12 @@ def time_decode(w_stub, gate, bias, records, layout, x0, budget_s: float = 12.0,
                 top_k: int = 8):
     """Run whole layers until ~budget_s of CPU work; returns
     (seconds per token, layers run, threads)."""
+    global UNTILE_SECONDS
     L = w_stub.shape[0]
     x = x0
     # warm-up one layer
     decode_step_cpu(x, w_stub[:1], gate[:1], bias[:1], records[:1], layout, top_k)
+    UNTILE_SECONDS = 0.0
     t0 = time.perf_counter()
     done = 0
     while True:
@@ -76,7 +102,7 @@ def time_decode(w_stub, gate, bias, records, layout, x0, budget_s: float = 12.0,
         x = decode_step_cpu(x, w_stub[l:l + 1], gate[l:l + 1], bias[l:l + 1],
                             records[l:l + 1], layout, top_k)
         done += 1
-        el = time.perf_counter() - t0
+        el = time.perf_counter() - t0 - UNTILE_SECONDS
         if (el >= budget_s and done >= 4) or done >= 4 * L:
             break
     per_layer = el / done
@@ -84,14 +110,17 @@ def time_decode(w_stub, gate, bias, records, layout, x0, budget_s: float = 12.0,
 
 
 def median_seconds(fn, iters: int = 20, warmup: int = 3) -> float:
-    """Median wall time of fn() over `iters` runs after `warmup` runs."""
+    """Median wall time of fn() over `iters` runs after `warmup` runs, less
+    the record untiling each run did."""
+    global UNTILE_SECONDS
     for _ in range(warmup):
         fn()
     ts = []
     for _ in range(iters):
+        UNTILE_SECONDS = 0.0
         t0 = time.perf_counter()
         fn()
-        ts.append(time.perf_counter() - t0)
+        ts.append(time.perf_counter() - t0 - UNTILE_SECONDS)
     ts.sort()
     return ts[len(ts) // 2]
 

@@ -48,7 +48,8 @@ def test_single_layer_decode_all_miss(lib, dev):
                   blocks_per_job=2)
         out = torch.empty_like(x)
         ws = torch.empty(lib.fp8_moe_workspace(1, K, C, H, I), dtype=torch.uint8, device=dev)
-        lib.fp8_moe_forward(x, out_slot.view(1, K), wts, *lay.views(cache), out, ws)
+        lib.fp8_moe_forward(x, out_slot.view(1, K), wts, *lay.views(cache), out, ws,
+                            layout=lay.code)
         torch.cuda.synchronize()
 
         o_ids, o_w, _ = orouter.route(x.float().cpu().numpy(), gate.float().cpu().numpy(), K)
@@ -67,10 +68,9 @@ def test_single_layer_decode_all_miss(lib, dev):
 
         # the oracle gets the 8 routed records only, ids renumbered 0..7
         sel = recs[torch.from_numpy(o_ids[0].astype(np.int64))].clone()
-        v13, vs13, v2, vs2 = lay.views(sel)
+        d13, ds13, d2, ds2 = lay.unpack(sel.numpy())
         args = (x.float().cpu().numpy(), np.arange(K)[None, :],
-                wts.cpu().numpy().astype(np.float64), v13.view(torch.uint8).numpy(),
-                vs13.numpy(), v2.view(torch.uint8).numpy(), vs2.numpy())
+                wts.cpu().numpy().astype(np.float64), d13, ds13, d2, ds2)
         got = out.float().cpu().numpy()
         err = omoe.max_rel_err(got, omoe.forward_w8a8(*args))
         gap = omoe.max_rel_err(got, omoe.forward_w8a16(*args))

@@ -43,13 +43,9 @@ STEPS = 6
 TOL = 1e-2
 
 
-def _unpack(layout, rec: np.ndarray):
-    """One packed record -> (w13 codes [2I,H], s13, w2 codes [H,I], s2)."""
-    w13 = rec[:layout.off_w2].reshape(2 * I, H)
-    w2 = rec[layout.off_w2:layout.off_s13].reshape(H, I)
-    s13 = rec[layout.off_s13:layout.off_s2].view(np.float32).reshape(2 * I // 128, H // 128)
-    s2 = rec[layout.off_s2:layout.payload_bytes].view(np.float32).reshape(H // 128, I // 128)
-    return w13, s13, w2, s2
+def _unpack(layout, recs: np.ndarray):
+    """Packed records [n, record] -> dense (w13 codes [n,2I,H], s13, w2 codes [n,H,I], s2)."""
+    return layout.unpack(recs)
 
 
 def _tables(hx, l):
@@ -106,15 +102,15 @@ def test_full_shape_decode_step_eager_and_graph(lib, dev):
                         f"step {s} layer {l}: slot {sl} does not hold expert {e}"
                 # the layer's output is h + FFN(h), the add exact in bf16
                 w13, s13, w2, s2 = hx.views[l]
-                lib.fp8_moe_forward(h, hx.out_slot[l], hx.wts[l], w13, s13, w2, s2, y, ws)
+                lib.fp8_moe_forward(h, hx.out_slot[l], hx.wts[l], w13, s13, w2, s2, y, ws,
+                                    layout=lay.code)
                 torch.cuda.synchronize(dev)
                 assert torch.equal((h + y).view(torch.int16), hx.x.view(torch.int16)), \
                     f"step {s} layer {l}: fused residual"
                 if l in sampled:
-                    recs = [_unpack(lay, hx.pools[l].array[e]) for e in o_ids[0]]
+                    dense = _unpack(lay, hx.pools[l].array[np.asarray(o_ids[0])])
                     want = omoe.forward_w8a8(h.float().cpu().numpy(), np.arange(K)[None, :],
-                                             hx.wts[l].cpu().numpy().astype(np.float64),
-                                             *[np.stack(t) for t in zip(*recs)])
+                                             hx.wts[l].cpu().numpy().astype(np.float64), *dense)
                     err = omoe.max_rel_err(y.float().cpu().numpy(), want)
                     say(f"decode-full: step {s} layer {l}: FFN max rel err {err:.2e}")
                     assert err <= TOL

@@ -116,10 +116,13 @@ def test_grouped_residual_and_bad_ids(lib, dev):
     assert torch.equal(torch.cat([nanrow[:4], nanrow[5:]]), torch.cat([plain[:4], plain[5:]]))
 
 
-def test_grouped_packed_record_views(lib, dev):
+@pytest.mark.parametrize("mode", [1, 2])
+def test_grouped_packed_record_views(lib, dev, mode):
+    """Tile-ordered packed records against the same experts as dense
+    row-major buffers: bit for bit, on the GEMV and the grouped path."""
     import hostpool
     import synth
-    T, E = 33, 24
+    T, E = 33 if mode == 2 else 5, 24
     lay = hostpool.DRAMA3
     host, devt = _experts(31, E, lay.hidden, lay.inter, dev)
     rec = lay.pack(devt[0].view(torch.float8_e4m3fn), devt[1], devt[2].view(torch.float8_e4m3fn),
@@ -128,8 +131,9 @@ def test_grouped_packed_record_views(lib, dev):
     x = synth.hidden_states(31, T).to(dev)
     ids, w = _routing(T, E, 8, 31, dev)
     from fp8_moe import fp8_moe_forward
-    a = fp8_moe_forward(x, ids, w, v13, vs13, v2, vs2, mode=2)
-    b = _fwd(x, ids, w, devt, mode=2)
+    say(f"packed record views: tile order, mode {mode}")
+    a = fp8_moe_forward(x, ids, w, v13, vs13, v2, vs2, mode=mode, layout=lay.code)
+    b = _fwd(x, ids, w, devt, mode=mode)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
 

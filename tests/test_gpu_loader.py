@@ -44,7 +44,8 @@ def test_pools_from_shards_feed_the_fetch_and_ffn(lib, dev, tmp_path):
         # slot s of the cache holds expert order[s]
         slot_of = torch.empty(E, dtype=torch.long, device=dev)
         slot_of[order.long()] = torch.arange(E, device=dev)
-        got = fp8_moe_forward(x, slot_of[ids], w, *lay.views(cache))
+        # tile-ordered records against the module's row-major buffers: bit for bit
+        got = fp8_moe_forward(x, slot_of[ids], w, *lay.views(cache), layout=lay.code)
         torch.cuda.synchronize()
         assert torch.equal(got, want)
     finally:

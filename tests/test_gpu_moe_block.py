@@ -44,7 +44,8 @@ def test_block_layers_match_oracle(lib, dev):
             say(f"moe block layer {l}")
             h.layer(l)
             w13, s13, w2, s2 = h.views[l]
-            lib.fp8_moe_forward(h.h, h.out_slot[l], h.wts[l], w13, s13, w2, s2, routed, h.ws)
+            lib.fp8_moe_forward(h.h, h.out_slot[l], h.wts[l], w13, s13, w2, s2, routed, h.ws,
+                                layout=h.layout.code)
             torch.cuda.synchronize()
             want = shared.shared_expert(_np(h.h), _np(h.sh_wg[l]), _np(h.sh_wu[l]),
                                         _np(h.sh_wd[l]), _np(h.sh_wsg[l]), routed=_np(routed),

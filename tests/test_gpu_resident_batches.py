@@ -37,12 +37,8 @@ def resident(dev):
 
 
 def _unpack(rec_np):
-    from hostpool import DRAMA3 as L
-    w13 = rec_np[:, :L.off_w2].reshape(-1, 2 * I, H)
-    w2 = rec_np[:, L.off_w2:L.off_s13].reshape(-1, H, I)
-    s13 = rec_np[:, L.off_s13:L.off_s2].copy().view(np.float32).reshape(-1, 2 * I // 128, H // 128)
-    s2 = rec_np[:, L.off_s2:L.payload_bytes].copy().view(np.float32).reshape(-1, H // 128, I // 128)
-    return w13, s13, w2, s2
+    from hostpool import DRAMA3
+    return DRAMA3.unpack(rec_np)
 
 
 @pytest.mark.parametrize("B", [8, 32, 128])
@@ -64,10 +60,10 @@ def test_resident_batch_against_oracle(lib, dev, resident, B):
     outs = {}
     for mode in (0, 1, 2):
         y = torch.empty_like(x)
-        lib.fp8_moe_forward(x, ids, wts, *views, y, ws, mode=mode)
+        lib.fp8_moe_forward(x, ids, wts, *views, y, ws, mode=mode, layout=DRAMA3.code)
         outs[mode] = y
     res = torch.empty_like(x)
-    lib.fp8_moe_forward(x, ids, wts, *views, res, ws, residual=x)
+    lib.fp8_moe_forward(x, ids, wts, *views, res, ws, residual=x, layout=DRAMA3.code)
     torch.cuda.synchronize()
     assert torch.equal(outs[1].view(torch.int16), outs[2].view(torch.int16)), "GEMV != grouped"
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))

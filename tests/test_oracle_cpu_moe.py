@@ -39,6 +39,10 @@ def test_moe_forward_cpu_equals_float64_w8a16_on_packed_records():
     bad[:, off:off + 256], bad[:, off + 256:off + 512] = rec[:, off + 256:off + 512], rec[:, off:off + 256]
     wrong = cpu_moe.moe_forward_cpu(x, ids, w, bad, hostpool.DRAMA3).numpy()
     assert np.abs(wrong - want).max() > 0.05 * np.abs(want).max()
+    # and so does a tile-ordered record read as row-major
+    rows = hostpool.RecordLayout(H, I, tiled=False)
+    wrong = cpu_moe.moe_forward_cpu(x, ids, w, rec, rows).numpy()
+    assert np.abs(wrong - want).max() > 0.05 * np.abs(want).max()
 
 
 def test_decode_step_cpu_equals_float64_composition():
