@@ -1,7 +1,8 @@
 // Token -> expert grouping (permute), its inverse (unpermute), and the
 // torch.unique-style renumbering the reference uses for its gathered subsets.
 //
-// permute: one workgroup, O(pairs) work, stable and deterministic:
+// permute (n_experts > 1024; permute_fast_kernel below otherwise): one
+// workgroup, O(pairs) work, stable and deterministic:
 //   1. histogram of expert ids in LDS (atomic adds; counts do not depend on
 //      the order they land in);
 //   2. block-wide exclusive scan -> offsets, and a cursor per expert;
@@ -214,6 +215,146 @@ __global__ __launch_bounds__(kPlaceThreads) void permute_kernel(
   }
 }
 
+// permute for n_experts <= kFastExperts: 16 waves, and 4096 pairs per
+// placement pass instead of 512, so one pass serves a 512-token top-8 call.
+// Wave w takes pairs [4096c + 256w, +256) of pass c in 4 rounds of 64 (lane
+// l of round j: pair 4096c + 256w + 64j + l).  In a round each lane finds
+// the lanes of its expert (ballot matching, as above); its rank in the wave
+// is the wave's count of that expert from earlier rounds, kept in LDS as one
+// 16-bit word per (wave, expert) and advanced by the expert's lowest lane,
+// plus its rank in the round.  Then one thread per expert turns the 16
+// waves' counts into exclusive prefixes, and a pair's position is
+//   cursor[e] + (its wave's prefix) + (its rank in the wave)
+// -- its rank in a stable sort.  Four barriers per pass.
+constexpr int kFastThreads = 1024;
+constexpr int kFastWaves = kFastThreads / 64;
+constexpr int kFastRounds = 4;
+constexpr int kFastPass = kFastThreads * kFastRounds;   // pairs per placement pass
+constexpr int kFastExperts = 1024;                      // one thread per expert
+
+__global__ __launch_bounds__(kFastThreads) void permute_fast_kernel(
+    const void* __restrict__ ids, int ids64, int64_t P, int32_t n_experts,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ sorted_pairs,
+    int32_t* __restrict__ pair_pos, int32_t* __restrict__ tiles, int32_t* __restrict__ n_tiles,
+    int32_t tile_tokens, QuantRowsJob quant) {
+  __shared__ int32_t cursor[kFastExperts];
+  __shared__ uint16_t wcount[kFastWaves * kFastExperts];   // [wave][expert]
+  __shared__ int32_t scratch[40];
+  const int tid = threadIdx.x;
+  if (blockIdx.x > 0) {
+    // the activation rows, four tokens per workgroup (a 256-thread quarter
+    // each, whole waves), beside workgroup 0's permutation; no barrier here
+    const int64_t t = 4 * static_cast<int64_t>(blockIdx.x - 1) + (tid >> 8);
+    if (t < quant.tokens) quant_row(quant, t, tid & 255);
+    return;
+  }
+  const int lane = tid & 63, wave = tid >> 6;
+  const int E = n_experts;
+  // expert codes of this lane's pairs in a pass (-1: id out of range, -2:
+  // past the last pair)
+  auto load_pass = [&](int64_t c0, int32_t (&e)[kFastRounds]) {
+#pragma unroll
+    for (int j = 0; j < kFastRounds; ++j) {
+      const int64_t p = c0 + wave * (64 * kFastRounds) + j * 64 + lane;
+      const int32_t v = read_id(ids, ids64, p < P ? p : P - 1);
+      e[j] = p < P ? ((v >= 0 && v < E) ? v : -1) : -2;
+    }
+  };
+  int32_t held[kFastRounds];
+#pragma unroll
+  for (int j = 0; j < kFastRounds; ++j) held[j] = -2;
+  if (P > 0) load_pass(0, held);
+  if (tid < E) {
+    cursor[tid] = 0;
+#pragma unroll
+    for (int w = 0; w < kFastWaves; ++w) wcount[w * kFastExperts + tid] = 0;
+  }
+  __syncthreads();
+  // histogram (LDS atomics; the counts do not depend on the order)
+#pragma unroll
+  for (int j = 0; j < kFastRounds; ++j)
+    if (held[j] >= 0) atomicAdd(&cursor[held[j]], 1);
+  for (int64_t p = kFastPass + tid; p < P; p += kFastThreads) {
+    const int32_t v = read_id(ids, ids64, p);
+    if (v >= 0 && v < E) atomicAdd(&cursor[v], 1);
+  }
+  __syncthreads();
+  // thread t owns expert t: counts, offsets, and the placement cursor
+  const int32_t mine = tid < E ? cursor[tid] : 0;
+  int32_t base;
+  const int32_t total = block_exclusive_scan<kFastWaves>(mine, scratch, &base);
+  if (tid < E) {
+    counts[tid] = mine;
+    offsets[tid] = base;
+    cursor[tid] = base;
+  }
+  if (tid == 0) offsets[E] = total;
+  if (tiles) {
+    // work tiles of the grouped kernels: (expert, first row of the segment)
+    // for every tile_tokens rows of every expert's segment, in expert order
+    const int32_t nt = (mine + tile_tokens - 1) / tile_tokens;
+    int32_t tbase;
+    const int32_t ttotal = block_exclusive_scan<kFastWaves>(nt, scratch, &tbase);
+    for (int32_t i = 0; i < nt; ++i) {
+      tiles[2 * (tbase + i)] = tid;
+      tiles[2 * (tbase + i) + 1] = i * tile_tokens;
+    }
+    if (tid == 0) *n_tiles = ttotal;
+  }
+  __syncthreads();
+  const uint64_t below_lane = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int nbits = E > 1 ? 32 - __clz(E - 1) : 0;
+  uint16_t* wc = wcount + wave * kFastExperts;
+  for (int64_t c0 = 0; c0 < P; c0 += kFastPass) {
+    if (c0 > 0) load_pass(c0, held);
+    // rank of each pair among its wave's pairs of the same expert
+    int32_t rank[kFastRounds];
+#pragma unroll
+    for (int j = 0; j < kFastRounds; ++j) {
+      const int32_t e = held[j];
+      int r, n;
+      wave_match_rank(e, nbits, below_lane, r, n);
+      const int32_t prior = e >= 0 ? wc[e] : 0;    // earlier rounds of this wave
+      rank[j] = prior + r;
+      if (e >= 0 && r == 0) wc[e] = static_cast<uint16_t>(prior + n);
+    }
+    __syncthreads();
+    // per expert: the waves' counts -> exclusive prefixes, and the pass total
+    int32_t pass_total = 0;
+    if (tid < E) {
+      uint16_t v[kFastWaves];
+#pragma unroll
+      for (int w = 0; w < kFastWaves; ++w) v[w] = wcount[w * kFastExperts + tid];
+#pragma unroll
+      for (int w = 0; w < kFastWaves; ++w) {
+        wcount[w * kFastExperts + tid] = static_cast<uint16_t>(pass_total);
+        pass_total += v[w];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kFastRounds; ++j) {
+      const int64_t p = c0 + wave * (64 * kFastRounds) + j * 64 + lane;
+      const int32_t e = held[j];
+      if (e >= 0) {
+        const int32_t pos = cursor[e] + wc[e] + rank[j];
+        sorted_pairs[pos] = static_cast<int32_t>(p);
+        pair_pos[p] = pos;
+      } else if (e == -1) {
+        pair_pos[p] = -1;                        // no such expert: no position
+      }
+    }
+    __syncthreads();
+    // the next pass starts after this one's pairs, with its counts cleared
+    if (tid < E) {
+      cursor[tid] += pass_total;
+#pragma unroll
+      for (int w = 0; w < kFastWaves; ++w) wcount[w * kFastExperts + tid] = 0;
+    }
+    __syncthreads();
+  }
+}
+
 __global__ __launch_bounds__(kPermThreads) void unique_inverse_kernel(
     const void* __restrict__ ids, int ids64, int64_t P, int32_t n_experts,
     const int32_t* __restrict__ counts, int32_t* __restrict__ n_unique, int32_t* __restrict__ uniq,
@@ -338,11 +479,19 @@ int launch_permute(const void* ids, int ids64, int64_t P, int32_t n_experts, int
                    int32_t* tiles, int32_t* n_tiles, int32_t tile_tokens,
                    const QuantRowsJob* quant) {
   static_assert(kPlaceThreads == 512, "two 256-thread token slices per quantising workgroup");
+  static_assert(kFastThreads == 1024, "four 256-thread token slices per quantising workgroup");
   const QuantRowsJob q = quant ? *quant : QuantRowsJob{nullptr, 0, nullptr, nullptr, 0};
-  const unsigned grid = 1 + static_cast<unsigned>((q.tokens + 1) / 2);
-  hipLaunchKernelGGL(permute_kernel, dim3(grid), dim3(kPlaceThreads), 0, s, ids, ids64, P,
-                     n_experts, counts, offsets, sorted_pairs, pair_pos, tiles, n_tiles,
-                     tile_tokens, q);
+  if (n_experts <= kFastExperts) {
+    const unsigned grid = 1 + static_cast<unsigned>((q.tokens + 3) / 4);
+    hipLaunchKernelGGL(permute_fast_kernel, dim3(grid), dim3(kFastThreads), 0, s, ids, ids64, P,
+                       n_experts, counts, offsets, sorted_pairs, pair_pos, tiles, n_tiles,
+                       tile_tokens, q);
+  } else {
+    const unsigned grid = 1 + static_cast<unsigned>((q.tokens + 1) / 2);
+    hipLaunchKernelGGL(permute_kernel, dim3(grid), dim3(kPlaceThreads), 0, s, ids, ids64, P,
+                       n_experts, counts, offsets, sorted_pairs, pair_pos, tiles, n_tiles,
+                       tile_tokens, q);
+  }
   return check_launch("moe_permute");
 }
 
