@@ -340,42 +340,50 @@ struct StreamShape {
 };
 constexpr StreamShape kShapes[] = {{16, 1}, {16, 2}, {16, 4}, {8, 8}};
 constexpr int kNumShapes = sizeof(kShapes) / sizeof(kShapes[0]);
+constexpr int kGateUpShape = 2;       // (16, 4): whole 128-column groups, the GLU form
+constexpr int kDownShape = 3;         // (8, 8)
+static_assert(kGateUpShape < kNumShapes && kDownShape < kNumShapes, "shape index");
 
-// Resident workgroups of the streamed kernel (2 per CU).
-static int resident_slots() {
-  static int slots = 0;
-  if (slots == 0) {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        cus <= 0)
-      cus = 256;
-    slots = 2 * cus;
+// Expected tile count of P uniform picks over n_experts: each expert's
+// pair count n is Poisson(P / n_experts) and takes ceil(n / 32) tiles,
+// E[ceil(n / 32)] = sum over j >= 0 of P(n > 32 j).
+static double expected_tiles(int64_t P, int32_t n_experts) {
+  if (P <= 0) return 0.0;
+  const double lam = static_cast<double>(P) / n_experts;
+  if (lam > 1000.0) return n_experts * (lam / kTileTok + 0.5);
+  double tiles = 0.0, cdf = 0.0, logp = -lam;   // log P(n = 0)
+  int n = 0;
+  for (int j = 0;; ++j) {
+    const int m = kTileTok * j;
+    for (; n <= m; ++n) {
+      cdf += exp(logp);
+      logp += log(lam) - log(static_cast<double>(n + 1));
+    }
+    const double tail = 1.0 - cdf;
+    if (m > lam && tail < 1e-9) break;
+    tiles += tail;
   }
-  return slots;
+  return n_experts * tiles;
 }
 
-// Shape for a projection of `rows` weight rows.  Bigger items amortise each
-// workgroup's start (tile look-up, staging, first loads), but items run in
-// rounds of the resident slots, and an item count just past a whole round
-// leaves most CUs idle in the last one.  So: the biggest shape whose item
-// count, at the expected tile count (distinct experts of P uniform picks,
-// plus partial tiles), is at least kMinItems and fills at least 80 % of its
-// last round.
-static int pick_shape(int64_t P, int32_t n_experts, int32_t rows) {
-  const double E = n_experts;
-  const double tiles = E * (1.0 - exp(-static_cast<double>(P) / E)) +
-                       static_cast<double>(P) / kTileTok;
-  const double slots = resident_slots();
-  int best = 0;
-  for (int i = 1; i < kNumShapes; ++i) {
+// Shape for a projection of `rows` weight rows: the biggest up to `target`
+// that tiles the rows and still gives kMinItems work items at the expected
+// tile count (fewer items than that leave CUs idle: small calls over few
+// experts take smaller items).  Bigger items amortise each workgroup's start
+// (tile look-up, staging, first loads) and drain; the GLU form needs
+// GPW >= 4.  Measured on MI355X over 256 resident experts, top-8, H 2048,
+// I 512, T = 17 .. 1024 tokens and every pair of shapes: gate/up (16, 4)
+// with down (8, 8) was the fastest pair or within 1.5 % of it at every T.
+static int pick_shape(int64_t P, int32_t n_experts, int32_t rows, int target) {
+  const double tiles = expected_tiles(P, n_experts);
+  int fallback = -1;
+  for (int i = target; i >= 0; --i) {
     const int g = kShapes[i].gpw;
     if (rows % (64 * g) != 0) continue;
-    const double items = tiles * rows / (64.0 * g);
-    const double fill = items / (ceil(items / slots) * slots);
-    if (items >= kMinItems && fill >= 0.8) best = i;
+    fallback = i;
+    if (tiles * rows / (64.0 * g) >= kMinItems) return i;
   }
-  return best;
+  return fallback < 0 ? 0 : fallback;
 }
 
 // Whether the GLU form serves a gate/up projection of this shape: items of
@@ -489,7 +497,7 @@ int launch_grouped(const uint16_t* x, const void* ids, int ids64, const void* we
   gu.top_k = top_k;  gu.rows = 2 * inter;  gu.G = hidden / 128;
   gu.tiled = es.layout == MOE_LAYOUT_TILES;
   gu.aq = aq;  gu.as = as_;  gu.inter = inter;
-  const int gu_shape = pick_shape(P, n_experts, gu.rows);
+  const int gu_shape = pick_shape(P, n_experts, gu.rows, kGateUpShape);
   if (glu_shape(gu_shape, inter)) {
     // gate/up, SiLU * up and its quantisation in one launch
     launch_stream<true, true>(gu, gu_shape, max_tiles, s);
@@ -510,7 +518,7 @@ int launch_grouped(const uint16_t* x, const void* ids, int ids64, const void* we
   dn.w = w2;  dn.ws = s2;  dn.out = y;  dn.w_es = es.w2;  dn.s_es = es.s2;
   dn.top_k = top_k;  dn.rows = hidden;  dn.G = inter / 128;
   dn.tiled = es.layout == MOE_LAYOUT_TILES;
-  launch_stream<false>(dn, pick_shape(P, n_experts, dn.rows), max_tiles, s);
+  launch_stream<false>(dn, pick_shape(P, n_experts, dn.rows, kDownShape), max_tiles, s);
   rc = check_launch("moe_fp8_moe_forward(grouped down)");
   if (rc) return rc;
   return launch_unpermute(y, pos, weights, wbf16, tokens, top_k, hidden, residual, out, s);

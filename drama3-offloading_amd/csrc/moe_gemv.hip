@@ -542,11 +542,12 @@ using namespace moe;
 
 // Calls of at most this many tokens take the per-pair GEMV kernels by default;
 // larger ones the grouped kernels, which read each expert's weights once.
-// Measured on MI355X (top-8 of 256 uniform, H 2048, I 512, resident
-// records, graph of back-to-back calls): GEMV 11 / 25 / 46 / 88 us against
-// grouped 50 / 78 / 104 / 116 us at 1 / 4 / 8 / 16 tokens, and 105 against
-// 99 us at 20: the GEMV's re-read of shared experts costs less than the
-// grouped path's six launches until about 16 tokens.
+// Measured on MI355X (top-8 of 256 uniform, H 2048, I 512, tile-ordered
+// records rotating over 2048 of them, graph of back-to-back calls): GEMV
+// 9.7 / 20.9 / 37.3 / 68.7 us against grouped 47.4 / 56.1 / 54.8 / 68.7 us
+// at 1 / 4 / 8 / 16 tokens, and 82.4 against 77.5 us at 20: the GEMV's
+// re-read of shared experts costs less than the grouped path's four
+// launches up to 16 tokens.
 constexpr int32_t kGemvMaxTokens = 16;
 // The block call carries the shared expert in the GEMV launches up to this
 // many tokens (its gate/up workgroups take the tokens one after another);
