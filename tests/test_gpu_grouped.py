@@ -116,22 +116,24 @@ def test_grouped_residual_and_bad_ids(lib, dev):
     assert torch.equal(torch.cat([nanrow[:4], nanrow[5:]]), torch.cat([plain[:4], plain[5:]]))
 
 
+@pytest.mark.parametrize("H,I", [(2048, 512), (4096, 384), (2560, 256), (1024, 1024)])
 @pytest.mark.parametrize("mode", [1, 2])
-def test_grouped_packed_record_views(lib, dev, mode):
+def test_grouped_packed_record_views(lib, dev, mode, H, I):
     """Tile-ordered packed records against the same experts as dense
-    row-major buffers: bit for bit, on the GEMV and the grouped path."""
+    row-major buffers: bit for bit, on the GEMV and the grouped path, at
+    several hidden / intermediate sizes (K-block counts 2 to 32)."""
     import hostpool
     import synth
     T, E = 33 if mode == 2 else 5, 24
-    lay = hostpool.DRAMA3
+    lay = hostpool.RecordLayout(H, I)
     host, devt = _experts(31, E, lay.hidden, lay.inter, dev)
     rec = lay.pack(devt[0].view(torch.float8_e4m3fn), devt[1], devt[2].view(torch.float8_e4m3fn),
                    devt[3])
     v13, vs13, v2, vs2 = lay.views(rec)
-    x = synth.hidden_states(31, T).to(dev)
+    x = synth.hidden_states(31, T, H).to(dev)
     ids, w = _routing(T, E, 8, 31, dev)
     from fp8_moe import fp8_moe_forward
-    say(f"packed record views: tile order, mode {mode}")
+    say(f"packed record views: tile order, mode {mode}, H {H} I {I}")
     a = fp8_moe_forward(x, ids, w, v13, vs13, v2, vs2, mode=mode, layout=lay.code)
     b = _fwd(x, ids, w, devt, mode=mode)
     torch.cuda.synchronize()
