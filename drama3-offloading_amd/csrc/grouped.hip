@@ -3,15 +3,22 @@
 // cut into tiles of up to 32 rows, every expert's weights are read from HBM
 // once per tile, and the results are un-permuted with the routing weights.
 //
-//   quant_rows:  x [T, H] bf16 -> xq [T, H] e4m3, xs [T, H/128]   (per token)
+//   permute:     the token -> expert grouping and the tile list, and in the
+//                same launch x [T, H] bf16 -> xq [T, H] e4m3, xs [T, H/128]
+//                (per token; permute.hip).
 //   gate/up:     grouped_stream_kernel over (tile, rows of w13) work items,
-//                the tile's xq rows gathered by token: h [pos, 2I] float32 in
-//                permuted order.
-//   silu:        one wave per permuted row: a = SiLU(gate) * up, quantised
-//                per 128 (aq, as) -- the decode GEMV's own function.
+//                the tile's xq rows gathered by token.  In the GLU form (the
+//                default: items of whole 128-column groups) the epilogue
+//                forms a = SiLU(gate) * up and quantises it per 128 (aq, as);
+//                otherwise it writes h [pos, 2I] float32 in permuted order
+//                and a SiLU launch (one wave per permuted row) does the rest.
 //   down:        grouped_stream_kernel over (tile, rows of w2) work items on
 //                the tile's aq rows: y [pos, H] float32.
 //   unpermute:   out[t] = sum_k w[t,k] * y[pos[t,k]] (permute.hip).
+//
+// The weights are read in either byte order (moe_expert_strides.layout);
+// in the MFMA tile order of the packed records each 16-byte load of a wave
+// reads 1 KiB contiguous.
 //
 // MFMA 16x16x128 e4m3 with the same operand roles as the decode GEMV:
 // weight rows are the A operand, activations the B operand (one token per B
@@ -42,15 +49,18 @@ namespace moe {
 //
 // A work item is (tile, 64*GPW consecutive weight rows).  One workgroup of 4
 // waves takes one item; wave w owns GPW groups of 16 rows.  The wave's
-// (K-block, group) units, K-block-major, stream through a ring of 16
-// operand registers per lane: unit u+16 is loaded as soon as the MFMA of
-// unit u has read its slot, so 16 K-blocks (32 KiB per wave) stay in flight
-// from the item's first load to its last.  The tile's activation rows are
+// (K-block, group) units, K-block-major, stream through a ring of RING
+// operand registers per lane (16, or 8 for the 8-group shape): unit u+RING
+// is loaded as soon as the MFMA of unit u has read its slot, so RING units
+// (2 KiB each per wave) stay in flight from the item's first load to its
+// last.  The tile's activation rows are
 // copied once into LDS by direct global->LDS loads, 16-byte units
 // XOR-swizzled by row against bank conflicts, together with their scales and
 // the item's weight scales; K beyond 16 blocks is staged 16 blocks at a time.
 // Items are dealt to the 8 XCDs in contiguous ranges, so the items of one
-// tile mostly share an L2.
+// tile mostly share an L2.  Gate/up takes 4 groups per wave (the GLU form),
+// down 8 with a ring of 8, each stepping down only for calls too small to
+// fill the chip (pick_shape).
 
 constexpr int kTileTok = 32;          // permuted rows per tile (two MFMA column tiles)
 constexpr int kColTiles = kTileTok / 16;
