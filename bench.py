@@ -36,7 +36,7 @@ FP8_PEAK_TFLOPS = 5000.0      # dense e4m3 MFMA, MI355X
 # known size (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); the passes and the
 # calibration are recorded in profiles/hbm_traffic.md.
 TRAFFIC_FETCH_BYTES = (24630 + 24582) * 1024          # host reads + HBM writes, 8 records
-TRAFFIC_GEMV_BYTES = (16571 + 8600 + 32 + 8) * 1024   # gate/up + down, 8 experts x 1 token
+TRAFFIC_GEMV_BYTES = (16614 + 8463 + 16 + 8) * 1024   # gate/up + down, 8 experts x 1 token
 TRAFFIC_CODED_BYTES = (21530 + 24582) * 1024          # coded host reads + HBM writes, 8 records
 PCIE5_X16_GBS = 64.0
 
