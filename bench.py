@@ -151,7 +151,7 @@ def link_peak(pools, dev, chunk_mib: int = 256, reps: int = 8) -> float:
     return len(srcs) * nb / (a.elapsed_time(b) / 1000.0) / 1e9
 
 
-def fetch_standalone(lib, pools, dev, jobs: int = 8, reps: int = 160, bpj: int = 2,
+def fetch_standalone(lib, pools, dev, jobs: int = 8, reps: int = 160, bpj: int = 3,
                      coded=None, workgroups: int = 32):
     """Average duration of one fetch launch moving `jobs` distinct records,
     rotating over every layer's pool (HIP events on the launch stream).

@@ -11,16 +11,31 @@
 // buffer pair, and the pieces are dealt round-robin to every workgroup of the
 // grid, whatever the miss count.  The grid is deliberately small:
 // blocks_per_job * min(max_jobs, 8) workgroups of 128 threads keep about
-// 128 KiB of host reads in flight at the default of 2, which is the host
-// link's bandwidth-delay product (~57 GB/s x ~2 us).  Measured on MI355X, more
-// outstanding reads lower the throughput (51 GB/s with 64 x 256-thread
-// workgroups per job against 56.5 GB/s here at 8 misses, 53.9 at 1 miss; the
-// copy engine's H2D rate on the same pool is 57.2 GB/s).
+// 192 KiB of host reads in flight at the default of 3, about the host link's
+// bandwidth-delay product (~57 GB/s x ~2-3 us).  Measured on MI355X (Drama-3
+// records, 1 / 3 / 8 misses): 53.6 / 56.1 / 56.8 GB/s at 3 workgroups per
+// job, 53.6 / 55.8 / 56.4 at 2, 53.1 / 55.9 / 56.8 at 4, 50.9 / 53.4 / 54.0
+// at 6, and 51 GB/s with 64 x 256-thread workgroups at 8; the copy engine's
+// H2D rate on the same pool is 57.2 GB/s.
 //
 // Each lane issues kFetchUnroll 16-byte loads, wave-contiguous (one wave
 // instruction covers 1 KiB of one record), before the matching stores.
 // Pairs whose sizes or addresses are not 16-byte aligned (tiny scale blocks
 // of toy shapes) are copied in 4-byte words by whole workgroups.
+//
+// A pair with tile_k = K > 0 holds row-major [rows, K] e4m3 matrices on the
+// host and writes them in MFMA tile order: the unit (16 bytes) of row
+// 16g + r, column unit c goes to unit
+//   ((g * K/128 + c/8) * 2 + c % 2) * 64 + ((c / 2) % 4) * 16 + r
+// of the record, which is byte (g*K/128 + b)*2048 + h*1024 + (16q + r)*16 of
+// the tile layout (b = c/8, q = (c/2) % 4, h = c % 2).  A piece of such a
+// pair is 16 rows x W column units (W = 32, 16 or 8, dividing K/16), whose
+// units fill one contiguous run of 16W units of the cache: the piece is read
+// as 16 row runs of 16W bytes, transposed through LDS (rows padded by one
+// unit, so the 16 rows a wave reads fall in distinct banks) and stored
+// contiguously.  Storing the units straight to their scattered places
+// writes 64 distinct 128-byte lines per wave instruction and measured 6 %
+// below the byte copy's rate.
 #include "common.hpp"
 
 namespace moe {
@@ -35,6 +50,8 @@ struct FetchArgs {
   int64_t bytes[4];
   int64_t pieces[4];      // pieces of this pair per record
   int32_t vec16[4];       // 1 if the pair takes the 16-byte path
+  uint32_t tile_upr[4];   // tile order: 16-byte units per row (K / 16), 0 for a byte copy
+  uint32_t tile_wlog[4];  // tile order: log2 of the column units per piece (5, 4 or 3)
   int32_t npairs;
   int64_t pieces_per_job; // sum of pieces over pairs
 };
@@ -44,6 +61,7 @@ __global__ __launch_bounds__(kFetchThreads) void fetch_kernel(FetchArgs a,
                                                               const int32_t* __restrict__ fslot,
                                                               const int32_t* __restrict__ nmiss,
                                                               int32_t max_jobs) {
+  __shared__ u32x4 stage[16 * 33];   // one tile-order piece, rows padded by one unit
   const int32_t nm = min(*nmiss, max_jobs);
   const int64_t total = static_cast<int64_t>(nm) * a.pieces_per_job;
   const int64_t row = static_cast<int64_t>(kFetchThreads) * kFetchUnroll;   // vectors per piece
@@ -60,7 +78,43 @@ __global__ __launch_bounds__(kFetchThreads) void fetch_kernel(FetchArgs a,
     const int64_t bytes = a.bytes[p];
     const char* src = a.src[p] + e * bytes;
     char* dst = a.dst[p] + s * bytes;
-    if (a.vec16[p]) {
+    const uint32_t upr = a.tile_upr[p];
+    if (upr != 0) {
+      // piece k = (row group g, column units [jW, jW + W)); its destination
+      // is the contiguous run of 16W units at unit (g * upr + jW) * 16
+      const uint32_t wl = a.tile_wlog[p];
+      const uint32_t W = 1u << wl;
+      const uint32_t per_g = upr >> wl;
+      const uint32_t g = static_cast<uint32_t>(k) / per_g;
+      const uint32_t jw = (static_cast<uint32_t>(k) - g * per_g) * W;
+      const u32x4* sv = reinterpret_cast<const u32x4*>(src) + (static_cast<int64_t>(g) * 16 * upr + jw);
+      u32x4* dv = reinterpret_cast<u32x4*>(dst) + (static_cast<int64_t>(g) * upr + jw) * 16;
+      const uint32_t n = 16 * W;   // <= kFetchThreads * kFetchUnroll
+      u32x4 v[kFetchUnroll];
+      // every lane loads (slots past n repeat the last unit), so the loads
+      // issue back to back and no branch splits them
+#pragma unroll
+      for (int u = 0; u < kFetchUnroll; ++u) {
+        const uint32_t i = min(threadIdx.x + u * kFetchThreads, n - 1);
+        v[u] = __builtin_nontemporal_load(sv + (i >> wl) * upr + (i & (W - 1)));
+      }
+#pragma unroll
+      for (int u = 0; u < kFetchUnroll; ++u) {
+        const uint32_t i = threadIdx.x + u * kFetchThreads;
+        if (i < n) stage[(i >> wl) * (W + 1) + (i & (W - 1))] = v[u];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < kFetchUnroll; ++u) {
+        // destination unit d = (2 * bb + h) * 64 + 16q + r holds row r, column unit 8bb + 2q + h
+        const uint32_t d = threadIdx.x + u * kFetchThreads;
+        if (d < n) {
+          const uint32_t bh = d >> 6, q = (d >> 4) & 3, r = d & 15;
+          dv[d] = stage[r * (W + 1) + (bh >> 1) * 8 + 2 * q + (bh & 1)];
+        }
+      }
+      __syncthreads();
+    } else if (a.vec16[p]) {
       const int64_t n = bytes >> 4;
       const u32x4* sv = reinterpret_cast<const u32x4*>(src);
       u32x4* dv = reinterpret_cast<u32x4*>(dst);
@@ -113,7 +167,23 @@ extern "C" int moe_fetch(const moe_fetch_pair* pairs, int32_t npairs,
     a.dst[p] = static_cast<char*>(pairs[p].dst);
     a.bytes[p] = b;
     a.vec16[p] = (b % 16 == 0 && sa % 16 == 0 && da % 16 == 0) ? 1 : 0;
-    a.pieces[p] = a.vec16[p] ? ((b >> 4) + row - 1) / row : 1;
+    const int64_t tk = pairs[p].tile_k;
+    MOE_REQUIRE(tk >= 0, "moe_fetch: pair %d has tile_k %lld", p, (long long)tk);
+    if (tk > 0) {
+      MOE_REQUIRE(tk % 128 == 0 && b % (16 * tk) == 0,
+                  "moe_fetch: pair %d: tile_k %lld must be a multiple of 128 and the record "
+                  "(%lld bytes) whole groups of 16 rows of it", p, (long long)tk, (long long)b);
+      MOE_REQUIRE(a.vec16[p] && (b >> 4) < (1LL << 32),
+                  "moe_fetch: pair %d in tile order must be 16-byte aligned with records "
+                  "under 64 GiB", p);
+    }
+    const uint32_t upr = static_cast<uint32_t>(tk / 16);
+    a.tile_upr[p] = upr;
+    a.tile_wlog[p] = upr % 32 == 0 ? 5 : upr % 16 == 0 ? 4 : 3;
+    if (tk > 0)
+      a.pieces[p] = (b / tk / 16) * (upr >> a.tile_wlog[p]);
+    else
+      a.pieces[p] = a.vec16[p] ? ((b >> 4) + row - 1) / row : 1;
     a.pieces_per_job += a.pieces[p];
   }
   const int grid = blocks_per_job * (max_jobs < moe::kFetchMaxJobsInGrid ? max_jobs

@@ -72,7 +72,7 @@ class DecodeConfig:
     drift_every: int = 50
     zipf_s: float = 1.1
     gate_std: float = 0.002
-    blocks_per_job: int = 2
+    blocks_per_job: int = 3
     noncoherent_pool: bool = False
     shared_expert: bool = False     # the MoE block's gated bf16 shared expert
     shared_inter: int = 512

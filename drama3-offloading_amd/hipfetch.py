@@ -60,7 +60,8 @@ class SharedExpert(C.Structure):
 
 class FetchPair(C.Structure):
     """moe_fetch_pair (include/moe_offload.h)."""
-    _fields_ = [("src", C.c_void_p), ("dst", C.c_void_p), ("bytes", C.c_int64)]
+    _fields_ = [("src", C.c_void_p), ("dst", C.c_void_p), ("bytes", C.c_int64),
+                ("tile_k", C.c_int64)]
 
 
 _vp, _i32, _i64, _sz = C.c_void_p, C.c_int32, C.c_int64, C.c_size_t
@@ -216,9 +217,12 @@ class Native:
     # ------------------------------------------------------------ fetch
     def fetch(self, pairs, fetch_expert, fetch_slot, nmiss, max_jobs: int,
               blocks_per_job: int) -> None:
-        """pairs: [(src_device_addr, dst_device_addr, bytes_per_record), ...]"""
+        """pairs: [(src_device_addr, dst_device_addr, bytes_per_record[, tile_k]), ...]
+
+        tile_k = K > 0 writes each record, a row-major [rows, K] e4m3 matrix on
+        the host, to the cache in MFMA tile order; 0 (the default) copies bytes."""
         self._on_gpu("moe_fetch", fetch_expert, fetch_slot, nmiss)
-        arr = (FetchPair * len(pairs))(*[FetchPair(s, d, b) for s, d, b in pairs])
+        arr = (FetchPair * len(pairs))(*[FetchPair(*((tuple(p) + (0,))[:4])) for p in pairs])
         self._check(self.cdll.moe_fetch(arr, len(pairs), fetch_expert.data_ptr(),
                                         fetch_slot.data_ptr(), nmiss.data_ptr(), max_jobs,
                                         blocks_per_job, self.stream()), "moe_fetch")

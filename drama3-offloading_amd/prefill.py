@@ -32,9 +32,9 @@ import torch
 import hipfetch
 from hostpool import DRAMA3, RecordLayout
 
-# Fetch workgroups per job: the host link saturates at 2 (~128 KiB in
+# Fetch workgroups per job: the host link saturates at 3 (~192 KiB in
 # flight); device-to-device copies from the cache want many more.
-HOST_BLOCKS_PER_JOB = 2
+HOST_BLOCKS_PER_JOB = 3
 CACHE_BLOCKS_PER_JOB = 64
 
 
@@ -46,14 +46,19 @@ class DevicePrefill:
              reference's layout: w13, w2, s13, s2)
     views:   (w13, s13, w2, s2) over the gather buffers, as fp8_moe_forward
              takes them
-    layout:  byte order of the gathered w13/w2 (hipfetch.LAYOUT_*)."""
+    layout:  byte order of the gathered w13/w2 (hipfetch.LAYOUT_*)
+    tile_k:  per gather buffer, the fetch's tile_k for copies from the host
+             (K of a row-major host matrix written in tile order; 0 copies
+             bytes).  Copies between device buffers always copy bytes."""
 
     def __init__(self, gather: list[torch.Tensor], views, top_k: int, max_tokens: int,
-                 hidden: int, inter: int, layout: int = hipfetch.LAYOUT_ROWS):
+                 hidden: int, inter: int, layout: int = hipfetch.LAYOUT_ROWS,
+                 tile_k: list[int] | None = None):
         self.lib = hipfetch.require()
         self.gather = gather
         self.views = views
         self.layout = layout
+        self.tile_k = list(tile_k) if tile_k is not None else [0] * len(gather)
         self.E = gather[0].shape[0]
         self.K, self.max_tokens = top_k, max_tokens
         self.dev = gather[0].device
@@ -90,13 +95,19 @@ class DevicePrefill:
                    layout.code)
 
     @classmethod
-    def for_experts(cls, experts, top_k: int, max_tokens: int, device) -> "DevicePrefill":
-        """Gather buffers shaped like an experts module's four host buffers."""
+    def for_experts(cls, experts, top_k: int, max_tokens: int, device,
+                    tiles: bool = False) -> "DevicePrefill":
+        """Gather buffers shaped like an experts module's four host buffers.
+        tiles: the host's row-major w13/w2 land in MFMA tile order, which the
+        FFN then reads as LAYOUT_TILES (the scales are copied as they are)."""
         bufs = [torch.empty_like(getattr(experts, n), device=device)
                 for n in ("w13_weight", "w2_weight", "w13_scale_inv", "w2_scale_inv")]
         views = (bufs[0], bufs[2], bufs[1], bufs[3])
-        return cls(bufs, views, top_k, max_tokens, experts.w13_weight.shape[2],
-                   experts.w2_weight.shape[2])
+        hidden, inter = experts.w13_weight.shape[2], experts.w2_weight.shape[2]
+        if tiles:
+            return cls(bufs, views, top_k, max_tokens, hidden, inter, hipfetch.LAYOUT_TILES,
+                       [hidden, inter, 0, 0])
+        return cls(bufs, views, top_k, max_tokens, hidden, inter)
 
     def gather_experts(self, ids: torch.Tensor, host_src: list[int] | None, cache=None,
                        coded=None) -> torch.Tensor:
@@ -130,7 +141,7 @@ class DevicePrefill:
             if coded is not None:
                 coded.fetch(self.gather[0], experts, rows, n, max_jobs=self.E)
             else:
-                pairs = [(s, d, b) for s, d, b in zip(host_src, dst, self.row_bytes)]
+                pairs = list(zip(host_src, dst, self.row_bytes, self.tile_k))
                 lib.fetch(pairs, experts, rows, n, max_jobs=self.E,
                           blocks_per_job=HOST_BLOCKS_PER_JOB)
 

@@ -129,6 +129,10 @@ typedef struct moe_fetch_pair {
   const void* src;   /* device-side address of the page-locked host buffer */
   void* dst;         /* HBM cache buffer */
   int64_t bytes;     /* bytes per expert record in this buffer */
+  int64_t tile_k;    /* 0: a byte copy.  K > 0: each record of this buffer is
+                        a row-major [bytes / K, K] e4m3 matrix (K % 128 == 0,
+                        bytes / K a multiple of 16) written to the cache in
+                        MFMA tile order (MOE_LAYOUT_TILES) */
 } moe_fetch_pair;
 
 /* Copy the queued misses host -> HBM with a zero-copy gather kernel.
@@ -136,13 +140,16 @@ typedef struct moe_fetch_pair {
  * fetch_slot[j] for every pair; *nmiss is read on the device at run time,
  * so later jobs cost nothing.  The grid is blocks_per_job * min(max_jobs, 8)
  * workgroups of 128 threads over which the queued records are dealt in
- * 8 KiB pieces (default 2 per job: ~128 KiB of host reads in flight, the
- * link's bandwidth-delay product; more outstanding reads measured slower).
+ * 8 KiB pieces (default 3 per job: ~192 KiB of host reads in flight, about
+ * the link's bandwidth-delay product; more outstanding reads measured
+ * slower).  A tile-order pair's pieces are 16 rows x up to 512 bytes,
+ * transposed through LDS into one contiguous 8 KiB run of the slot.
  * Replaces fetch_experts/fetch_kernel (csrc/fetch_experts.cu:49-94) and the
  * four per-buffer launches of _cpp_fetch (bin/devcache.py:197-220) with one
  * launch.  Preconditions: 1 <= npairs <= 4; each pair's src, dst and bytes
- * are 4-byte aligned (16-byte aligned pairs take the 16-byte path);
- * 1 <= max_jobs <= 65535; 1 <= blocks_per_job <= 65535. */
+ * are 4-byte aligned (16-byte aligned pairs take the 16-byte path), and a
+ * pair with tile_k > 0 is 16-byte aligned with records under 64 GiB;
+ * 1 <= max_jobs <= 65535; 1 <= blocks_per_job <= 4096. */
 int moe_fetch(const moe_fetch_pair* pairs, int32_t npairs,
               const int32_t* fetch_expert, const int32_t* fetch_slot,
               const int32_t* nmiss, int32_t max_jobs, int32_t blocks_per_job,

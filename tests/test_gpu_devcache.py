@@ -1,7 +1,9 @@
 """The device cache end to end (bin/test_devcache.py, restated): outputs
 through the cache equal the all-resident outputs EXACTLY over 40 steps at
-capacities 16/32/64 of 64 experts with real shapes, eviction exercised, and a
-captured step replays DYNAMIC with the right bytes."""
+capacities 16/32/64 of 64 experts with real shapes, eviction exercised, with
+the slots in MFMA tile order (the fetch tiling the row-major host buffers as
+it stores; every occupied slot holds hostpool.to_tiles of its expert) and in
+row-major order, and a captured step replays DYNAMIC with the right bytes."""
 import numpy as np
 import pytest
 import torch
@@ -24,14 +26,19 @@ def pair(dev):
     return ref, host
 
 
-@pytest.mark.parametrize("cap", [16, 32, E])
-def test_cache_is_bit_exact_against_resident(lib, dev, pair, cap):
+@pytest.mark.parametrize("cap,tiles", [(16, True), (32, False), (E, True)])
+def test_cache_is_bit_exact_against_resident(lib, dev, pair, cap, tiles, monkeypatch):
     import devcache
+    import hipfetch
+    import offload
     from fp8_moe import fp8_moe_forward
+    from hostpool import to_tiles
     ref, host = pair
+    monkeypatch.setattr(offload, "DEVICE_TILES", tiles)
     devcache.init_dev_cache(host, dev, cap)
+    assert devcache.cache_layout(host) == (hipfetch.LAYOUT_TILES if tiles else hipfetch.LAYOUT_ROWS)
     torch.manual_seed(cap)
-    say(f"devcache: capacity {cap}")
+    say(f"devcache: capacity {cap}, tiles {tiles}")
     for step in range(40):
         x = torch.randn(1, H, device=dev).to(torch.bfloat16)
         ids = torch.randperm(E, device=dev)[:K].unsqueeze(0)
@@ -41,10 +48,15 @@ def test_cache_is_bit_exact_against_resident(lib, dev, pair, cap):
                                ref.w2_scale_inv)
         slots = devcache.dev_resolve_and_fetch(host, ids)
         got = fp8_moe_forward(x, slots.reshape(ids.shape), w, host._dc_w13, host._dc_s13,
-                              host._dc_w2, host._dc_s2)
+                              host._dc_w2, host._dc_s2, layout=devcache.cache_layout(host))
         assert torch.equal(want, got), f"step {step}"
     occupied = int((host._dc_slot_expert >= 0).sum())
     assert occupied == cap
+    order = to_tiles if tiles else (lambda t: t)
+    for s_, e in enumerate(host._dc_slot_expert.tolist()):
+        for c, h in ((host._dc_w13, host.w13_weight), (host._dc_w2, host.w2_weight)):
+            assert torch.equal(c[s_].view(torch.uint8).cpu(), order(h[e].view(torch.uint8))), (s_, e)
+        assert torch.equal(host._dc_s13[s_].cpu(), host.w13_scale_inv[e])
     hits, misses = devcache.cache_stats(host)
     assert hits + misses == 40 * K and (cap >= E or misses > cap)
 
@@ -85,7 +97,7 @@ def test_capture_dynamic_and_bytes(lib, dev, pair):
     want = fp8_moe_forward(x, ids_rep, w, ref.w13_weight, ref.w13_scale_inv, ref.w2_weight,
                            ref.w2_scale_inv)
     got = fp8_moe_forward(x, slots.reshape(1, K), w, host._dc_w13, host._dc_s13, host._dc_w2,
-                          host._dc_s2)
+                          host._dc_s2, layout=devcache.cache_layout(host))
     assert torch.equal(want, got)
 
 
@@ -123,7 +135,7 @@ def test_whole_decode_layer_graph_replays_match_eager(lib, dev, pair, coded):
         moe.route(x_live, gate, K, bias=bias, out=(rids, rw, rl))
         sl = devcache.dev_resolve_and_fetch(hmod, rids)
         fp8_moe_forward(x_live, sl.reshape(1, K), rw, hmod._dc_w13, hmod._dc_s13, hmod._dc_w2,
-                        hmod._dc_s2, out=o, workspace=ws)
+                        hmod._dc_s2, out=o, workspace=ws, layout=devcache.cache_layout(hmod))
 
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -179,7 +191,7 @@ def test_coded_pool_through_the_hooks_equals_raw(lib, dev, pair):
         for m in (host, twin):
             slots = devcache.dev_resolve_and_fetch(m, ids)
             outs.append(fp8_moe_forward(x, slots.reshape(ids.shape), w, m._dc_w13, m._dc_s13,
-                                        m._dc_w2, m._dc_s2))
+                                        m._dc_w2, m._dc_s2, layout=devcache.cache_layout(m)))
         torch.cuda.synchronize()
         assert torch.equal(outs[0], outs[1]), f"step {step}"
     for a in ("_dc_w13", "_dc_w2", "_dc_s13", "_dc_s2", "_dc_slot_of", "_dc_stamp"):

@@ -117,6 +117,56 @@ def test_fetch_four_pairs_including_unaligned(lib, dev):
         assert torch.all(cv[1] == 0) and torch.all(cv[4] == 0)
 
 
+def test_fetch_tile_order_pairs(lib, dev):
+    """tile_k = K: each row-major [R, K] host matrix lands in MFMA tile
+    order (hostpool.to_tiles), beside a byte pair in the same launch.
+    Shapes: the Drama-3 w13 [1024, 2048] and w2 [2048, 512], K = 384 with
+    1.5 pieces of 8 KiB per record (a partial piece), and one 16 x 128 tile
+    (less than a piece)."""
+    from hostpool import to_tiles
+    n, C = 12, 5
+    mats = [(1024, 2048), (2048, 512), (32, 384), (16, 128)]
+    g = torch.Generator().manual_seed(3)
+    ids, slots = [7, 0, 11, 4], [3, 0, 4, 1]
+    fexp = torch.tensor(ids, dtype=torch.int32, device=dev)
+    fslot = torch.tensor(slots, dtype=torch.int32, device=dev)
+    nmiss = torch.tensor([len(ids)], dtype=torch.int32, device=dev)
+    for first, second in ((0, 1), (2, 3)):
+        hosts, caches, pairs = [], [], []
+        for R, Kd in (mats[first], mats[second]):
+            h = torch.randint(0, 256, (n, R, Kd), dtype=torch.uint8, generator=g).pin_memory()
+            c = torch.zeros((C, R, Kd), dtype=torch.uint8, device=dev)
+            hosts.append(h)
+            caches.append(c)
+            pairs.append((lib.device_ptr_of(h.data_ptr()), c.data_ptr(), R * Kd, Kd))
+        hs = torch.randint(0, 256, (n, 48), dtype=torch.uint8, generator=g).pin_memory()
+        cs = torch.zeros((C, 48), dtype=torch.uint8, device=dev)
+        pairs.append((lib.device_ptr_of(hs.data_ptr()), cs.data_ptr(), 48, 0))
+        say(f"fetch: tile order {mats[first]} {mats[second]} + 48-byte pair")
+        lib.fetch(pairs, fexp, fslot, nmiss, max_jobs=4, blocks_per_job=3)
+        torch.cuda.synchronize()
+        for h, c in zip(hosts, caches):
+            got = c.cpu()
+            for e, s_ in zip(ids, slots):
+                assert torch.equal(got[s_], to_tiles(h[e])), (tuple(h.shape[1:]), e)
+            assert torch.all(got[2] == 0)
+        for e, s_ in zip(ids, slots):
+            assert torch.equal(cs[s_].cpu(), hs[e])
+
+
+def test_fetch_tile_order_preconditions(lib, dev):
+    """tile_k must be a multiple of 128 dividing the record into whole groups
+    of 16 rows, on a 16-byte aligned pair; rejected before any launch."""
+    import hipfetch
+    h = torch.zeros(4 * 16 * 256, dtype=torch.uint8, pin_memory=True)
+    c = torch.zeros(4 * 16 * 256 + 16, dtype=torch.uint8, device=dev)
+    src = lib.device_ptr_of(h.data_ptr())
+    j = torch.zeros(1, dtype=torch.int32, device=dev)
+    for tk, b, d in ((192, 16 * 256, 0), (256, 8 * 256, 0), (256, 16 * 256, 4), (-128, 4096, 0)):
+        with pytest.raises(hipfetch.NativeError, match="tile"):
+            lib.fetch([(src, c.data_ptr() + d, b, tk)], j, j, j, max_jobs=1, blocks_per_job=1)
+
+
 @pytest.mark.parametrize("noncoherent", [False, True])
 def test_fetch_from_library_host_pool(lib, dev, noncoherent):
     n = 8

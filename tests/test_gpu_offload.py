@@ -4,10 +4,12 @@ all-resident kernel on the same inputs, exactly).
 
   * direct (page-locked and pageable host buffers), gather, and the
     host-managed cache give outputs identical to the resident forward, at
-    decode- and prefill-shaped calls;
+    decode- and prefill-shaped calls, with the device rows in MFMA tile
+    order (offload.DEVICE_TILES, the default) and row-major;
   * the host-managed cache holds, after every call, exactly the experts its
-    decisions put in each slot (the decisions themselves are checked against
-    the oracle on the CPU, tests/test_offload_host.py);
+    decisions put in each slot, in the cache's order (the decisions
+    themselves are checked against the oracle on the CPU,
+    tests/test_offload_host.py);
   * the direct gather borrows resident experts from the device cache without
     touching its table, counts on the device, and runs without a host sync:
     it is captured in a graph and replayed with new ids.
@@ -51,17 +53,24 @@ def _call(ref, tokens, seed, dev):
     return x, ids, w, want
 
 
+def _order(tiles):
+    from hostpool import to_tiles
+    return to_tiles if tiles else (lambda t: t)
+
+
+@pytest.mark.parametrize("tiles", [True, False])
 @pytest.mark.parametrize("mode,which", [("direct", "pinned"), ("direct", "pageable"),
                                         ("gather", "pinned"), ("gather", "pageable")])
-def test_copy_modes_match_resident(lib, dev, models, mode, which):
+def test_copy_modes_match_resident(lib, dev, models, mode, which, tiles, monkeypatch):
     import offload
     ref, host, pageable = models
     layer = host if which == "pinned" else pageable
+    monkeypatch.setattr(offload, "DEVICE_TILES", tiles)
     offload.COPY_MODE = mode
     try:
         for step, tokens in enumerate([1, 5, 1, 17, 64]):
             x, ids, w, want = _call(ref, tokens, step, dev)
-            say(f"offload: {mode} {which} tokens={tokens}")
+            say(f"offload: {mode} {which} tiles={tiles} tokens={tokens}")
             before = offload.STATS["experts_copied"]
             got = offload.offloaded_forward(layer, x, ids, w)
             assert torch.equal(got, want)
@@ -71,11 +80,15 @@ def test_copy_modes_match_resident(lib, dev, models, mode, which):
         offload.COPY_MODE = "direct"
 
 
-def test_hybrid_gather_borrows_device_cache(lib, dev, models):
+@pytest.mark.parametrize("tiles", [True, False])
+def test_hybrid_gather_borrows_device_cache(lib, dev, models, tiles, monkeypatch):
     import devcache
     import offload
     ref, host, _ = models
+    monkeypatch.setattr(offload, "DEVICE_TILES", tiles)
     devcache.init_dev_cache(host, dev, 16)
+    # the gather rows follow the cache's order whatever the knob says later
+    monkeypatch.setattr(offload, "DEVICE_TILES", not tiles)
     try:
         for step in range(6):                      # populate the device cache
             _, ids, _, _ = _call(ref, 1, 50 + step, dev)
@@ -86,7 +99,7 @@ def test_hybrid_gather_borrows_device_cache(lib, dev, models):
             table = [t.clone() for t in (host._dc_slot_of, host._dc_slot_expert, host._dc_stamp,
                                          host._dc_step)]
             x, ids, w, want = _call(ref, 9, 99, dev)
-            say(f"offload: hybrid {mode}")
+            say(f"offload: hybrid {mode} tiles={tiles}")
             got = offload.offloaded_forward(host, x, ids, w)
             assert torch.equal(got, want)
             resident = set(host._dc_slot_expert.tolist()) - {-1}
@@ -133,12 +146,15 @@ def test_direct_gather_is_capturable_and_dynamic(lib, dev, models):
         assert torch.equal(out, want), f"replay {r}"
 
 
-def test_host_lru_and_fallbacks(lib, dev, models):
+@pytest.mark.parametrize("tiles", [True, False])
+def test_host_lru_and_fallbacks(lib, dev, models, tiles, monkeypatch):
     import offload
     ref, host, _ = models
+    monkeypatch.setattr(offload, "DEVICE_TILES", tiles)
+    order = _order(tiles)
     for cap in (8, 12, E):
         offload._init_cache(host, dev, cap)
-        say(f"offload: host LRU cap {cap}")
+        say(f"offload: host LRU cap {cap} tiles={tiles}")
         for step in range(12):
             tokens = 1 if step % 3 else 5
             x, ids, w, want = _call(ref, tokens, 1000 + step, dev)
@@ -150,10 +166,13 @@ def test_host_lru_and_fallbacks(lib, dev, models):
                 e = int(lru.slot_expert[slot])
                 for cache, name in zip((host._cache_w13, host._cache_w2, host._cache_s13,
                                         host._cache_s2), _BUFS):
-                    assert torch.equal(cache[slot].cpu().view(torch.uint8),
-                                       getattr(host, name)[e].view(torch.uint8)), \
+                    want = getattr(host, name)[e].view(torch.uint8)
+                    if name.endswith("weight"):
+                        want = order(want)
+                    assert torch.equal(cache[slot].cpu().view(torch.uint8), want), \
                         f"cap {cap} step {step}: slot {slot} {name}"
-    for a in ("_cap", "_cache_w13", "_cache_w2", "_cache_s13", "_cache_s2", "_lru_state"):
+    for a in ("_cap", "_cache_w13", "_cache_w2", "_cache_s13", "_cache_s2", "_lru_state",
+              "_cache_tiles"):
         delattr(host, a)
 
 
@@ -194,9 +213,10 @@ def test_pin_experts_and_device_census(lib, dev):
     ids = torch.tensor([[3, 1, 4, 15, 9, 2, 6, 5]], device=dev)
     devcache.dev_resolve_and_fetch(ex, ids)
     torch.cuda.synchronize(dev)
+    order = _order(ex._dc_tiles)
     for j, e in enumerate(ids[0].tolist()):
         s = int(ex._dc_out[j].item())
-        assert torch.equal(ex._dc_w13[s].cpu().view(torch.uint8), want[0][e].view(torch.uint8))
+        assert torch.equal(ex._dc_w13[s].cpu().view(torch.uint8), order(want[0][e].view(torch.uint8)))
     offload.enable_census(2, E)
     try:
         ex._layer_index = 1

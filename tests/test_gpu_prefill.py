@@ -64,18 +64,25 @@ def _routing(T, seed, dev):
     return ids, w / w.sum(-1, keepdim=True)
 
 
-def test_device_prefill_equals_resident_and_gathers_exact_bytes(lib, dev, layer):
+@pytest.mark.parametrize("tiles", [False, True])
+def test_device_prefill_equals_resident_and_gathers_exact_bytes(lib, dev, layer, tiles):
+    """The gather rows hold the host's bytes (tiles: w13/w2 in MFMA tile
+    order, hostpool.to_tiles of the host's row-major matrices) and the FFN
+    over them equals the resident forward."""
     import devcache
     from fp8_moe import fp8_moe_forward
+    import hipfetch
+    from hostpool import to_tiles
     from prefill import DevicePrefill
     ref, host = layer
     T = 55
     x = torch.randn((T, H), device=dev).to(torch.bfloat16)
     ids, w = _routing(T, 1, dev)
-    pf = DevicePrefill.for_experts(host, K, 64, dev)
+    pf = DevicePrefill.for_experts(host, K, 64, dev, tiles=tiles)
+    assert pf.layout == (hipfetch.LAYOUT_TILES if tiles else hipfetch.LAYOUT_ROWS)
     src = [devcache._device_ptr(lib, getattr(host, n)) for n in
            ("w13_weight", "w2_weight", "w13_scale_inv", "w2_scale_inv")]
-    say("prefill: host-only gather")
+    say(f"prefill: host-only gather, tiles={tiles}")
     got = pf.forward(x, ids, w, src)
     want = fp8_moe_forward(x, ids, w, ref.w13_weight, ref.w13_scale_inv, ref.w2_weight,
                            ref.w2_scale_inv)
@@ -84,8 +91,11 @@ def test_device_prefill_equals_resident_and_gathers_exact_bytes(lib, dev, layer)
     uniq = torch.unique(ids).cpu()
     n = int(pf.n_unique)
     assert n == uniq.numel() and torch.equal(pf.uniq[:n].cpu(), uniq.to(torch.int32))
+    order = to_tiles if tiles else (lambda t: t)
     assert torch.equal(pf.gather[0][:n].view(torch.uint8).cpu(),
-                       host.w13_weight.view(torch.uint8)[uniq])
+                       order(host.w13_weight.view(torch.uint8)[uniq]))
+    assert torch.equal(pf.gather[1][:n].view(torch.uint8).cpu(),
+                       order(host.w2_weight.view(torch.uint8)[uniq]))
     assert torch.equal(pf.gather[3][:n].cpu(), host.w2_scale_inv[uniq])
 
 
@@ -103,8 +113,9 @@ def test_hybrid_gather_equals_host_gather(lib, dev, layer):
     ids, w = _routing(T, 2, dev)
     pairs = devcache._copy_pairs(host)
     src = [devcache._device_ptr(lib, h) for h, _ in pairs]
-    a = DevicePrefill.for_experts(host, K, 64, dev)
-    b = DevicePrefill.for_experts(host, K, 64, dev)
+    # gather rows in the cache's order (rows borrowed from it are copied as bytes)
+    a = DevicePrefill.for_experts(host, K, 64, dev, tiles=host._dc_tiles)
+    b = DevicePrefill.for_experts(host, K, 64, dev, tiles=host._dc_tiles)
     say("prefill: hybrid vs host-only gather")
     out_a = a.forward(x, ids, w, src)
     out_b = b.forward(x, ids, w, src, cache=(host._dc_slot_of, host._dc_cap,
@@ -162,7 +173,7 @@ def test_device_prefill_is_capturable_and_dynamic(lib, dev, layer):
     pairs = devcache._copy_pairs(host)
     src = [devcache._device_ptr(lib, h) for h, _ in pairs]
     cache = (host._dc_slot_of, host._dc_cap, [c.data_ptr() for _, c in pairs])
-    pf = DevicePrefill.for_experts(host, K, T, dev)
+    pf = DevicePrefill.for_experts(host, K, T, dev, tiles=host._dc_tiles)
     out = torch.empty_like(x)
 
     def body():
@@ -180,7 +191,7 @@ def test_device_prefill_is_capturable_and_dynamic(lib, dev, layer):
     say("prefill: capture")
     with torch.cuda.graph(g):
         body()
-    eager = DevicePrefill.for_experts(host, K, T, dev)
+    eager = DevicePrefill.for_experts(host, K, T, dev, tiles=host._dc_tiles)
     for r in range(4):
         ids_r, w_r = _routing(T, 60 + r, dev)
         ids_live.copy_(ids_r)
