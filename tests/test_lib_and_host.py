@@ -53,6 +53,15 @@ def test_preconditions_are_rejected_without_launching(lib):
     assert c.moe_route_resolve(16, 16, None, bf16, 2048, 256, 8, 1, 1, 1, 1, 1, 1, 7, 1, 1, 1, 1,
                                1, None, None) == -1
     assert b"exceeds the cache capacity" in c.moe_last_error()
+    # tile-order pairs: K a multiple of 128, whole 16-row groups, 16-byte aligned
+    FetchPair = __import__("hipfetch").FetchPair
+    for src, dst, nbytes, tile_k, msg in ((0x1000, 0x2000, 16 * 256, 192, b"multiple of 128"),
+                                          (0x1000, 0x2000, 8 * 256, 256, b"16 rows"),
+                                          (0x1000, 0x2004, 16 * 256, 256, b"16-byte aligned"),
+                                          (0x1000, 0x2000, 4096, -128, b"tile_k -128")):
+        pair = FetchPair(src, dst, nbytes, tile_k)
+        assert c.moe_fetch(ctypes.byref(pair), 1, 1, 1, 1, 8, 3, None) == -1, msg
+        assert msg in c.moe_last_error(), c.moe_last_error()
 
 
 def test_shared_and_block_preconditions_are_rejected_without_launching(lib):
