@@ -388,13 +388,18 @@ def contention(lib, pools, dev, gemv_calls: int = 2000, fetches: int = 40,
     return res
 
 
-def prefill_bench(lib, harness, tokens: int = 512, passes: int = 2, coded=None):
+def prefill_bench(lib, harness, tokens: int = 512, passes: int = 2, coded=None, hybrid=None):
     """512-token prefill through all layers: router, distinct experts, one
     fetch of their records from the page-locked pool (no host sync), grouped
     FFN with the residual fused; then the grouped FFN alone on resident
     gathered experts (HBM and MFMA figures).  With `coded` (one CodedPool
     per layer), the same passes again with the experts decoded from the
-    coded pools; their output must equal the raw passes'."""
+    coded pools; their output must equal the raw passes'.  With `hybrid`
+    ((slot_of, capacity, cache) per layer: the decode step's device caches
+    as the decode run left them), the same passes again with every expert
+    resident in a layer's cache copied from there instead of fetched over
+    the link (the table only read); their output must equal the raw
+    passes' too."""
     import torch
     import synth
     from prefill import DevicePrefill
@@ -412,35 +417,51 @@ def prefill_bench(lib, harness, tokens: int = 512, passes: int = 2, coded=None):
     logits = torch.zeros((tokens, E), dtype=torch.float32, device=dev)
     n_unique = torch.zeros(L, dtype=torch.int32, device=dev)
 
-    def one_pass(from_coded=False):
+    def one_pass(from_coded=False, from_cache=False):
         x.copy_(x0)
         for l in range(L):
             lib.router_topk(x, gate[l], None, K, logits, ids, wts)
             if from_coded:
                 pf.forward(x, ids, wts, None, out=y, residual=x, coded=coded[l])
+            elif from_cache:
+                slot_of, cap, cache = hybrid[l]
+                pf.forward(x, ids, wts, [harness.pools[l].dev_ptr], out=y, residual=x,
+                           cache=(slot_of, cap, [cache.data_ptr()]))
             else:
                 pf.forward(x, ids, wts, [harness.pools[l].dev_ptr], out=y, residual=x)
             n_unique[l:l + 1].copy_(pf.n_unique)
             x.copy_(y)
 
-    def timed(from_coded):
-        one_pass(from_coded)                     # warm-up
+    def timed(from_coded, from_cache=False):
+        one_pass(from_coded, from_cache)         # warm-up
         torch.cuda.synchronize(dev)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
         for _ in range(passes):
-            one_pass(from_coded)
+            one_pass(from_coded, from_cache)
         b.record()
         torch.cuda.synchronize(dev)
         return a.elapsed_time(b) / 1000.0 / passes
 
     dt = timed(False)
-    coded_res = None
+    x_raw = x.clone()
+    coded_res = hybrid_res = None
     if coded is not None:
-        x_raw = x.clone()
         c_dt = timed(True)
         coded_res = {"ms_per_pass": round(1e3 * c_dt, 3), "tokens_per_s": round(tokens / c_dt, 1),
                      "output_equal_raw_pool_pass": bool(torch.equal(x, x_raw))}
+    if hybrid is not None:
+        before = pf.copy_stats()
+        h_dt = timed(False, True)
+        after = pf.copy_stats()
+        borrowed, fetched_h = after[0] - before[0], after[1] - before[1]
+        hybrid_res = {
+            "what": "the same passes with each layer's experts resident in the decode step's "
+                    f"device cache ({hybrid[0][1]} slots per layer, as the decode run left it) "
+                    "copied from there, the rest fetched over the link; the table is only read",
+            "ms_per_pass": round(1e3 * h_dt, 3), "tokens_per_s": round(tokens / h_dt, 1),
+            "experts_from_cache": round(borrowed / (borrowed + fetched_h), 4),
+            "output_equal_raw_pool_pass": bool(torch.equal(x, x_raw))}
     uniq = n_unique.float()
     fetched = float(uniq.sum()) * harness.layout.record_bytes
     finite = bool(torch.isfinite(x.float()).all())
@@ -469,6 +490,7 @@ def prefill_bench(lib, harness, tokens: int = 512, passes: int = 2, coded=None):
                         "fp8_dense_peak_TFLOPs": FP8_PEAK_TFLOPS},
         "finite_output": finite,
         "coded_pool": coded_res,
+        "hybrid_gather": hybrid_res,
     }
 
 
@@ -1072,6 +1094,9 @@ def main() -> int:
     log(f"top-8 sets differing between bf16 and float32 logits: {contracts}")
 
     hc.graph = None
+    # the decode caches as the run left them, for the prefill's hybrid gather
+    hybrid = [(hc.slot_of[l], cfg.capacity, hc.cache[l]) for l in range(cfg.layers)] \
+        if not args.no_extra and cfg.mode == "cached" else None
     del hc.cache, hc.views
     hc.pools = []
     torch.cuda.empty_cache()
@@ -1093,10 +1118,12 @@ def main() -> int:
     prefill = resident = None
     if not args.no_extra:
         log("prefill (512 tokens, 40 layers)")
-        prefill = prefill_bench(lib, h0c, coded=coded_pools)
+        prefill = prefill_bench(lib, h0c, coded=coded_pools, hybrid=hybrid)
+        hybrid = None
         log(f"prefill: {prefill['tokens_per_s']} tok/s, {prefill['ms_per_pass']} ms/pass, "
             f"{prefill['distinct_experts_per_layer']} experts/layer, grouped FFN "
-            f"{prefill['grouped_ffn']['us']} us; from coded pools {prefill['coded_pool']}")
+            f"{prefill['grouped_ffn']['us']} us; from coded pools {prefill['coded_pool']}; "
+            f"hybrid gather {prefill['hybrid_gather']}")
         log("all-resident batched decode")
         resident = resident_bench(lib, h0c)
         log("resident: " + ", ".join(f"B={b}: {v['tokens_per_s']} tok/s"
