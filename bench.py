@@ -698,9 +698,94 @@ def fill_pool_bytes(pool, dev, seed: int, chunk: int = 64) -> None:
     torch.cuda.synchronize(dev)
 
 
+def loader_probe(layers: int = 4, threads: int = 16) -> dict:
+    """Host-side load time at Drama-3 shapes: `layers` synthetic checkpoint
+    shards (one safetensors file per layer, 256 experts of e4m3 gate/up/down
+    and their block scales, in the page cache after writing) read into
+    page-locked packed pools (tile order and row-major), into the
+    reference's four buffers per layer, and the reference-layout buffers
+    re-homed into page-locked arenas (offload.pin_experts).  GB/s counts the
+    expert payload (3,146,496 B per expert)."""
+    import shutil
+    import tempfile
+    import types
+    import numpy as np
+    import torch
+    from safetensors.torch import save_file
+    import hipfetch
+    import loader
+    import moe
+    import offload
+    from hostpool import DRAMA3, RecordLayout
+    E, H, I = 256, DRAMA3.hidden, DRAMA3.inter
+    root = Path(tempfile.mkdtemp(prefix="moe_loader_"))
+    try:
+        g = torch.Generator().manual_seed(11)
+        t0 = time.perf_counter()
+        keep = {}
+        for l in range(layers):
+            tensors = {}
+            for e in range(E):
+                for proj, shape in (("gate_proj", (I, H)), ("up_proj", (I, H)),
+                                    ("down_proj", (H, I))):
+                    w = torch.randint(0, 256, shape, generator=g, dtype=torch.uint8)
+                    tensors[loader.EXPERT.format(layer=l, expert=e, proj=proj, what="weight")] = \
+                        w.view(torch.float8_e4m3fn)
+                    tensors[loader.EXPERT.format(layer=l, expert=e, proj=proj,
+                                                 what="weight_scale_inv")] = \
+                        torch.rand((shape[0] // 128, shape[1] // 128), generator=g)
+            for e in (0, E - 1):
+                keep[(l, e)] = [tensors[loader.EXPERT.format(layer=l, expert=e, proj=p, what=w)]
+                                for w in ("weight", "weight_scale_inv")
+                                for p in ("gate_proj", "up_proj", "down_proj")]
+            save_file(tensors, root / f"model-{l + 1:05d}-of-{layers:05d}.safetensors")
+            del tensors
+        write_s = time.perf_counter() - t0
+        payload = layers * E * DRAMA3.payload_bytes
+        res = {"layers": layers, "experts": E, "threads": threads,
+               "payload_bytes": payload, "shard_write_s": round(write_s, 2)}
+        for name, lay in (("pools_tiled", DRAMA3), ("pools_rows", RecordLayout(H, I, tiled=False))):
+            t0 = time.perf_counter()
+            pools, copied = loader.load_host_pools(root, range(layers), lay, threads=threads)
+            dt = time.perf_counter() - t0
+            ok = copied == payload
+            for (l, e), (g_, u_, d_, gs, us, ds) in keep.items():
+                want = lay.pack(torch.cat([g_, u_])[None], torch.cat([gs, us])[None], d_[None],
+                                ds[None])[0].numpy()
+                ok = ok and bool(np.array_equal(pools[l].array[e], want))
+            for p in pools:
+                p.close()
+            res[name] = {"s": round(dt, 3), "GBps": round(payload / dt / 1e9, 2), "exact": ok}
+        index = loader.ShardIndex.from_dir(root)
+        mods = [moe.MoEExperts(E, H, I, device="cpu") for _ in range(layers)]
+        t0 = time.perf_counter()
+        for l, m in enumerate(mods):
+            loader.fill_expert_buffers(index, l, m, threads=threads)
+        dt = time.perf_counter() - t0
+        g_, u_, d_ = keep[(0, E - 1)][:3]
+        ok = bool(torch.equal(mods[0].w13_weight[E - 1].view(torch.uint8),
+                              torch.cat([g_, u_]).view(torch.uint8)))
+        res["four_buffers_pageable"] = {"s": round(dt, 3), "GBps": round(payload / dt / 1e9, 2),
+                                        "exact": ok}
+        model = types.SimpleNamespace(backbone=types.SimpleNamespace(model=types.SimpleNamespace(
+            layers=[types.SimpleNamespace(mlp=types.SimpleNamespace(experts=m)) for m in mods])))
+        gib, dt = offload.pin_experts(model, torch.device("cuda:0"))
+        lib = hipfetch.require()
+        ok = bool(torch.equal(mods[0].w13_weight[E - 1].view(torch.uint8),
+                              torch.cat([g_, u_]).view(torch.uint8))) and \
+            all(lib.is_page_locked(m.w13_weight) for m in mods)
+        res["pin_experts"] = {"s": round(dt, 3), "GBps": round(gib * 2 ** 30 / dt / 1e9, 2),
+                              "exact": ok}
+        res["reference"] = ("pin_experts of 30 GiB in ~14 s, about 2.3 GB/s "
+                            "(notes/12-full-run.md:72)")
+        return res
+    finally:
+        shutil.rmtree(root, ignore_errors=True)
+
+
 def run_probe(args) -> int:
-    """--probe gemv|fetch|codec|copy|grouped|shared|hbm|step: the named kernel(s) alone (or
-    the captured decode step), many launches, one JSON line."""
+    """--probe gemv|fetch|codec|copy|grouped|shared|hbm|step|contention|loader: the named
+    kernel(s) alone (or the captured decode step, or the host-side load), one JSON line."""
     import torch
     import hipfetch
     from hostpool import DRAMA3, HostPool
@@ -788,6 +873,8 @@ def run_probe(args) -> int:
         hc.close()
     elif args.probe == "hbm":
         res = {"probe": "hbm", **hbm_probe(lib, dev, calls=args.steps)}
+    elif args.probe == "loader":
+        res = {"probe": "loader", **loader_probe(layers=args.layers if args.layers != 40 else 4)}
     elif args.probe == "contention":
         pools = [HostPool(256, DRAMA3) for _ in range(4)]
         for i, p in enumerate(pools):
@@ -1004,7 +1091,7 @@ def main() -> int:
                     help="skip the prefill and all-resident measurements")
     ap.add_argument("--tokens", type=int, default=512, help="tokens per call of --probe grouped")
     ap.add_argument("--probe", choices=["gemv", "fetch", "codec", "copy", "grouped", "shared",
-                                        "hbm", "step", "contention"],
+                                        "hbm", "step", "contention", "loader"],
                     help="time one kernel alone (--steps launches) instead of the decode step")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

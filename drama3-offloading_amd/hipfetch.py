@@ -197,6 +197,16 @@ class Native:
         self._check(self.cdll.moe_device_ptr_of(host_ptr, C.byref(d)), "moe_device_ptr_of")
         return d.value
 
+    def is_page_locked(self, t) -> bool:
+        """Whether tensor t's storage is page-locked host memory, as the HIP
+        runtime sees it.  torch's Tensor.is_pinned() answers False for every
+        tensor until torch itself has initialised the GPU, which a process
+        that only allocated through this library has not."""
+        if t.device.type != "cpu" or t.numel() == 0:
+            return False
+        d = C.c_void_p()
+        return self.cdll.moe_device_ptr_of(t.data_ptr(), C.byref(d)) == 0
+
     # ------------------------------------------------------------ slots
     def slots_init(self, slot_of, slot_expert, stamp, step) -> None:
         self._check(self.cdll.moe_slots_init(slot_of.data_ptr(), slot_of.numel(),

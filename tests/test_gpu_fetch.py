@@ -189,6 +189,24 @@ def test_fetch_from_library_host_pool(lib, dev, noncoherent):
         lib.host_free(ptr)
 
 
+def test_is_page_locked_asks_the_runtime(lib, dev):
+    """hipfetch.is_page_locked: page-locked torch tensors and the library's
+    own host regions (views at an offset too) are page-locked; pageable
+    memory, device tensors and empty tensors are not."""
+    import ctypes
+    assert lib.is_page_locked(torch.empty(1 << 20, dtype=torch.uint8, pin_memory=True))
+    assert not lib.is_page_locked(torch.empty(1 << 20, dtype=torch.uint8))
+    assert not lib.is_page_locked(torch.empty(1 << 20, dtype=torch.uint8, device=dev))
+    assert not lib.is_page_locked(torch.empty(0, dtype=torch.uint8, pin_memory=True))
+    n = 64 << 20
+    ptr = lib.host_alloc(n)
+    try:
+        flat = torch.from_numpy(np.ctypeslib.as_array((ctypes.c_uint8 * n).from_address(ptr)))
+        assert lib.is_page_locked(flat) and lib.is_page_locked(flat[n // 2 + 16:])
+    finally:
+        lib.host_free(ptr)
+
+
 def test_pageable_source_is_rejected(lib):
     import hipfetch
     t = torch.empty(1 << 20, dtype=torch.uint8)
