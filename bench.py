@@ -388,6 +388,118 @@ def contention(lib, pools, dev, gemv_calls: int = 2000, fetches: int = 40,
     return res
 
 
+def dropin_bench(lib, hc, steps: int, start: int, split: int, x_headline) -> dict:
+    """The headline step through the reference's own hook surface: one
+    MoEExperts module per layer holding the reference's four host buffers
+    (filled with the pools' experts, page-locked by offload.pin_experts),
+    devcache.install_dev_cache with the headline's capacity, and each layer
+    calling experts(h, ids, w), i.e. dev_cached_forward: moe_resolve_slots,
+    one moe_fetch of the four buffers (w13/w2 written in tile order), the
+    expert FFN on the cache.  Router, stub and routing schedule are the
+    headline's; the residual add is a separate torch add, as in a model
+    that calls the experts module.  The same replays, window and split as
+    the headline: the decisions are the same, so the hit/miss counts must
+    match the headline's and the step output must equal it bit for bit."""
+    import types
+    import torch
+    import decode
+    import devcache
+    import moe
+    import offload
+    cfg, dev = hc.cfg, hc.dev
+    L, E, K, H, I = cfg.layers, cfg.n_experts, cfg.top_k, cfg.hidden, cfg.inter
+    t0 = time.perf_counter()
+    mods = [moe.MoEExperts(E, H, I, device="cpu") for _ in range(L)]
+    model = types.SimpleNamespace(backbone=types.SimpleNamespace(model=types.SimpleNamespace(
+        layers=[types.SimpleNamespace(mlp=types.SimpleNamespace(experts=m)) for m in mods])))
+    gib, pin_s = offload.pin_experts(model, dev)
+    for l, m in enumerate(mods):
+        # the pool's packed (tile-ordered) records, unpacked on the GPU into
+        # the checkpoint's row-major buffers
+        w13, s13, w2, s2 = hc.layout.unpack(hc.pools[l].tensor.to(dev))
+        m.w13_weight.view(torch.uint8).copy_(w13)
+        m.w13_scale_inv.copy_(s13)
+        m.w2_weight.view(torch.uint8).copy_(w2)
+        m.w2_scale_inv.copy_(s2)
+        del w13, s13, w2, s2
+    torch.cuda.synchronize(dev)
+    stock = moe.MoEExperts.forward
+    try:
+        n = devcache.install_dev_cache(model, dev, cfg.capacity)
+        build_s = time.perf_counter() - t0
+        i32 = dict(dtype=torch.int32, device=dev)
+        ids = torch.zeros((L, 1, K), **i32)
+        wts = torch.zeros((L, 1, K), dtype=torch.float32, device=dev)
+        logits = torch.zeros((L, 1, E), dtype=torch.float32, device=dev)
+        x = hc.x0.clone()
+        h = torch.empty_like(x)
+
+        def step():
+            x.copy_(hc.x0)
+            for l in range(L):
+                decode.stub_linear(x, hc.w_stub[l], h)
+                lib.router_topk(h, hc.gate[l], hc.bias_live[l], K, logits[l], ids[l], wts[l],
+                                logit_dtype=cfg.router_logits)
+                y = mods[l](h, ids[l], wts[l])
+                torch.add(h, y, out=x)
+
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            hc.stage(0)
+            step()                                   # warm-up outside capture
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize(dev)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step()
+        for m in mods:
+            devcache.reset_dev_cache(m)
+        stats = lambda: torch.stack([m._dc_stats for m in mods]).sum(0)   # noqa: E731
+
+        def replay(first, count):
+            for c in range(first, first + count):
+                hc.stage(c)
+                g.replay()
+
+        replay(0, start)
+        torch.cuda.synchronize(dev)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        s0 = stats()
+        ev[0].record()
+        replay(start, split)
+        s1 = stats()
+        ev[1].record()
+        replay(start + split, steps - split)
+        ev[2].record()
+        torch.cuda.synchronize(dev)
+        s2_ = stats()
+        dt = ev[0].elapsed_time(ev[2]) / 1000.0
+        hits, misses = (s2_ - s0).tolist()
+        return {
+            "workload": "the headline step through the reference's hooks: MoEExperts modules "
+                        "with the four page-locked host buffers, devcache.install_dev_cache, "
+                        "experts(h, ids, w) per layer (resolve, one four-buffer fetch writing "
+                        "w13/w2 in tile order, expert FFN), residual add in torch; one hipGraph",
+            "layers_hooked": n, "pinned_GiB": round(gib, 2), "pin_experts_s": round(pin_s, 2),
+            "build_s": round(build_s, 1),
+            "tokens_per_s": round(steps / dt, 3), "ms_per_step": round(1e3 * dt / steps, 4),
+            "hit_rate": round(hits / max(1, hits + misses), 4),
+            "tokens_per_s_before_drift": round(split / (ev[0].elapsed_time(ev[1]) / 1000.0), 3)
+            if split else None,
+            "hits_misses": [int(hits), int(misses)],
+            "x_equal_headline_step": bool(torch.equal(x, x_headline)),
+        }
+    finally:
+        moe.MoEExperts.forward = stock
+        devcache._dev_ptr_cache.clear()          # the arenas are freed below
+        for m in mods:
+            for a in [a for a in vars(m) if a.startswith("_dc_")]:
+                delattr(m, a)
+        del mods, model
+        torch.cuda.empty_cache()
+
+
 def prefill_bench(lib, harness, tokens: int = 512, passes: int = 2, coded=None, hybrid=None):
     """512-token prefill through all layers: router, distinct experts, one
     fetch of their records from the page-locked pool (no host sync), grouped
@@ -1143,6 +1255,12 @@ def main() -> int:
     x_ok = bool(torch.isfinite(hc.x.float()).all())
     log(f"cached: {tps_cached:.2f} tok/s, {1e3 * dt / args.steps:.3f} ms/step, hit {hit:.3f}, "
         f"finite={x_ok}; drift at step {boundary}: {drift}")
+    dropin = None
+    if not args.no_extra:
+        log("the same step through the reference's hooks (MoEExperts + install_dev_cache)")
+        dropin = dropin_bench(lib, hc, args.steps, start, split, hc.x.clone())
+        dropin["hits_misses_equal_headline"] = dropin["hits_misses"] == [int(hits), int(misses)]
+        log(f"drop-in: {dropin}")
 
     log("standalone kernel timing")
     link = link_peak(pools, dev)
@@ -1290,6 +1408,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "moe_block": block,
         "coded_pool": coded,
+        "dropin_decode": dropin,
         "prefill": prefill,
         "all_resident": resident,
         "finite_output": x_ok,
