@@ -413,15 +413,8 @@ def dropin_bench(lib, hc, steps: int, start: int, split: int, x_headline) -> dic
     model = types.SimpleNamespace(backbone=types.SimpleNamespace(model=types.SimpleNamespace(
         layers=[types.SimpleNamespace(mlp=types.SimpleNamespace(experts=m)) for m in mods])))
     gib, pin_s = offload.pin_experts(model, dev)
-    for l, m in enumerate(mods):
-        # the pool's packed (tile-ordered) records, unpacked on the GPU into
-        # the checkpoint's row-major buffers
-        w13, s13, w2, s2 = hc.layout.unpack(hc.pools[l].tensor.to(dev))
-        m.w13_weight.view(torch.uint8).copy_(w13)
-        m.w13_scale_inv.copy_(s13)
-        m.w2_weight.view(torch.uint8).copy_(w2)
-        m.w2_scale_inv.copy_(s2)
-        del w13, s13, w2, s2
+    for pool, m in zip(hc.pools, mods):
+        pool.to_experts(m, dev)             # packed records -> the checkpoint's buffers
     torch.cuda.synchronize(dev)
     stock = moe.MoEExperts.forward
     try:

@@ -182,6 +182,22 @@ class HostPool:
         n = records.shape[0]
         self.tensor[first:first + n].copy_(records)
 
+    def to_experts(self, experts, device, chunk: int = 64) -> None:
+        """Fill an experts module's four host buffers (w13_weight [E, 2I, H],
+        w13_scale_inv, w2_weight, w2_scale_inv: the reference's layout,
+        row-major) with this pool's experts, unpacking `chunk` records at a
+        time on `device`."""
+        if experts.w13_weight.shape[0] != self.n:
+            raise ValueError(f"{experts.w13_weight.shape[0]} experts in the module, "
+                             f"{self.n} in the pool")
+        for first in range(0, self.n, chunk):
+            last = min(self.n, first + chunk)
+            w13, s13, w2, s2 = self.layout.unpack(self.tensor[first:last].to(device))
+            experts.w13_weight.view(torch.uint8)[first:last].copy_(w13)
+            experts.w13_scale_inv[first:last].copy_(s13)
+            experts.w2_weight.view(torch.uint8)[first:last].copy_(w2)
+            experts.w2_scale_inv[first:last].copy_(s2)
+
     def fetch_pair(self, cache: torch.Tensor):
         """(src device address, dst address, bytes per record) for moe_fetch."""
         return (self.dev_ptr, cache.data_ptr(), self.layout.record_bytes)

@@ -226,3 +226,29 @@ def test_pin_experts_and_device_census(lib, dev):
         assert c[3] == 4 and c[0] == 0 and offload.CENSUS_DECODE[1][3] == 1
     finally:
         offload.disable_census()
+
+
+def test_freed_arena_leaves_no_cached_answers(lib, dev):
+    """The device address and the page-locked answer remembered for an
+    arena's buffers are dropped when the arena is freed, so an address the
+    allocator hands out again is asked afresh."""
+    import gc
+    import types
+    import devcache
+    import moe
+    import offload
+    ex = moe.MoEExperts(8, 256, 128, device="cpu")
+    layer = types.SimpleNamespace(mlp=types.SimpleNamespace(experts=ex))
+    model = types.SimpleNamespace(backbone=types.SimpleNamespace(
+        model=types.SimpleNamespace(layers=[layer])))
+    offload.pin_experts(model, dev)
+    bufs = [getattr(ex, n) for n in _BUFS]
+    addrs = [b.data_ptr() for b in bufs]
+    devcache._device_ptr(lib, bufs[0])
+    assert offload._all_pinned(bufs)
+    assert addrs[0] in devcache._dev_ptr_cache and tuple(addrs) in offload._pinned_memo
+    del bufs, layer, model
+    del ex
+    gc.collect()
+    assert addrs[0] not in devcache._dev_ptr_cache
+    assert tuple(addrs) not in offload._pinned_memo
