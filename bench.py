@@ -406,6 +406,7 @@ def dropin_bench(lib, hc, steps: int, start: int, split: int, x_headline) -> dic
     import devcache
     import moe
     import offload
+    import synth
     cfg, dev = hc.cfg, hc.dev
     L, E, K, H, I = cfg.layers, cfg.n_experts, cfg.top_k, cfg.hidden, cfg.inter
     t0 = time.perf_counter()
@@ -469,6 +470,48 @@ def dropin_bench(lib, hc, steps: int, start: int, split: int, x_headline) -> dic
         s2_ = stats()
         dt = ev[0].elapsed_time(ev[2]) / 1000.0
         hits, misses = (s2_ - s0).tolist()
+        x_step = x.clone()
+        del g
+
+        # prefill through the same hooks: a call of 512 rows goes to
+        # offloaded_forward's direct gather, which borrows the experts
+        # resident in the layer's device cache; the prefill measurement's
+        # router and input, so the output can be compared with its passes
+        tokens, passes = 512, 2
+        gen = torch.Generator(device=dev).manual_seed(cfg.seed + 5)
+        pgate = (torch.randn((L, E, H), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+        xp0 = synth.hidden_states(cfg.seed + 7, tokens, H).to(dev)
+        xp = xp0.clone()
+        pids = torch.zeros((tokens, K), **i32)
+        pw = torch.zeros((tokens, K), dtype=torch.float32, device=dev)
+        plog = torch.zeros((tokens, E), dtype=torch.float32, device=dev)
+
+        def prefill_pass():
+            xp.copy_(xp0)
+            for l in range(L):
+                lib.router_topk(xp, pgate[l], None, K, plog, pids, pw)
+                y = mods[l](xp, pids, pw)
+                torch.add(xp, y, out=xp)
+
+        before = offload.STATS.copy()
+        prefill_pass()                                  # warm-up: gather rows, plans
+        torch.cuda.synchronize(dev)
+        pa, pb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        pa.record()
+        for _ in range(passes):
+            prefill_pass()
+        pb.record()
+        torch.cuda.synchronize(dev)
+        p_dt = pa.elapsed_time(pb) / 1000.0 / passes
+        after = offload.STATS.copy()
+        borrowed = after["gather_hits"] - before["gather_hits"]
+        fetched = after["gather_misses"] - before["gather_misses"]
+        prefill_hooks = {
+            "what": f"{tokens}-token prefill through the same hooks (offloaded_forward, direct "
+                    "gather borrowing each layer's device-cache residents, grouped FFN), the "
+                    "prefill measurement's router and input",
+            "ms_per_pass": round(1e3 * p_dt, 3), "tokens_per_s": round(tokens / p_dt, 1),
+            "experts_from_cache": round(borrowed / max(1, borrowed + fetched), 4)}
         return {
             "workload": "the headline step through the reference's hooks: MoEExperts modules "
                         "with the four page-locked host buffers, devcache.install_dev_cache, "
@@ -481,10 +524,12 @@ def dropin_bench(lib, hc, steps: int, start: int, split: int, x_headline) -> dic
             "tokens_per_s_before_drift": round(split / (ev[0].elapsed_time(ev[1]) / 1000.0), 3)
             if split else None,
             "hits_misses": [int(hits), int(misses)],
-            "x_equal_headline_step": bool(torch.equal(x, x_headline)),
-        }
+            "x_equal_headline_step": bool(torch.equal(x_step, x_headline)),
+            "prefill": prefill_hooks,
+        }, xp.clone()
     finally:
         moe.MoEExperts.forward = stock
+        offload._DeviceGather._by_key.clear()
         devcache._dev_ptr_cache.clear()          # the arenas are freed below
         for m in mods:
             for a in [a for a in vars(m) if a.startswith("_dc_")]:
@@ -493,7 +538,8 @@ def dropin_bench(lib, hc, steps: int, start: int, split: int, x_headline) -> dic
         torch.cuda.empty_cache()
 
 
-def prefill_bench(lib, harness, tokens: int = 512, passes: int = 2, coded=None, hybrid=None):
+def prefill_bench(lib, harness, tokens: int = 512, passes: int = 2, coded=None, hybrid=None,
+                  x_hooks=None):
     """512-token prefill through all layers: router, distinct experts, one
     fetch of their records from the page-locked pool (no host sync), grouped
     FFN with the residual fused; then the grouped FFN alone on resident
@@ -504,7 +550,8 @@ def prefill_bench(lib, harness, tokens: int = 512, passes: int = 2, coded=None, 
     as the decode run left them), the same passes again with every expert
     resident in a layer's cache copied from there instead of fetched over
     the link (the table only read); their output must equal the raw
-    passes' too."""
+    passes' too.  `x_hooks`: the output of the same passes run through the
+    reference's hooks (dropin_bench), compared with the raw passes'."""
     import torch
     import synth
     from prefill import DevicePrefill
@@ -596,6 +643,8 @@ def prefill_bench(lib, harness, tokens: int = 512, passes: int = 2, coded=None, 
         "finite_output": finite,
         "coded_pool": coded_res,
         "hybrid_gather": hybrid_res,
+        "hooks_output_equal_raw_pool_pass": None if x_hooks is None else
+        bool(torch.equal(x_hooks, x_raw)),
     }
 
 
@@ -1248,10 +1297,10 @@ def main() -> int:
     x_ok = bool(torch.isfinite(hc.x.float()).all())
     log(f"cached: {tps_cached:.2f} tok/s, {1e3 * dt / args.steps:.3f} ms/step, hit {hit:.3f}, "
         f"finite={x_ok}; drift at step {boundary}: {drift}")
-    dropin = None
+    dropin = x_hooks = None
     if not args.no_extra:
         log("the same step through the reference's hooks (MoEExperts + install_dev_cache)")
-        dropin = dropin_bench(lib, hc, args.steps, start, split, hc.x.clone())
+        dropin, x_hooks = dropin_bench(lib, hc, args.steps, start, split, hc.x.clone())
         dropin["hits_misses_equal_headline"] = dropin["hits_misses"] == [int(hits), int(misses)]
         log(f"drop-in: {dropin}")
 
@@ -1316,8 +1365,8 @@ def main() -> int:
     prefill = resident = None
     if not args.no_extra:
         log("prefill (512 tokens, 40 layers)")
-        prefill = prefill_bench(lib, h0c, coded=coded_pools, hybrid=hybrid)
-        hybrid = None
+        prefill = prefill_bench(lib, h0c, coded=coded_pools, hybrid=hybrid, x_hooks=x_hooks)
+        hybrid = x_hooks = None
         log(f"prefill: {prefill['tokens_per_s']} tok/s, {prefill['ms_per_pass']} ms/pass, "
             f"{prefill['distinct_experts_per_layer']} experts/layer, grouped FFN "
             f"{prefill['grouped_ffn']['us']} us; from coded pools {prefill['coded_pool']}; "
