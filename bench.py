@@ -437,6 +437,24 @@ def dropin_bench(lib, hc, steps: int, start: int, split: int, x_headline) -> dic
                 y = mods[l](h, ids[l], wts[l])
                 torch.add(h, y, out=x)
 
+        # the window run eagerly first (no graph: one launch at a time)
+        for c in range(start):
+            hc.stage(c)
+            step()
+        torch.cuda.synchronize(dev)
+        ea, eb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ea.record()
+        for c in range(start, start + steps):
+            hc.stage(c)
+            step()
+        eb.record()
+        torch.cuda.synchronize(dev)
+        e_dt = ea.elapsed_time(eb) / 1000.0
+        eager = {"tokens_per_s": round(steps / e_dt, 3), "ms_per_step": round(1e3 * e_dt / steps, 4),
+                 "x_equal_headline_step": bool(torch.equal(x, x_headline))}
+        for m in mods:
+            devcache.reset_dev_cache(m)
+
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):
@@ -512,6 +530,35 @@ def dropin_bench(lib, hc, steps: int, start: int, split: int, x_headline) -> dic
                     "prefill measurement's router and input",
             "ms_per_pass": round(1e3 * p_dt, 3), "tokens_per_s": round(tokens / p_dt, 1),
             "experts_from_cache": round(borrowed / max(1, borrowed + fetched), 4)}
+
+        # the same decode steps through the host-managed cache instead
+        # (offload.cached_forward: decisions on the host, one sync per layer,
+        # so eager): the device caches are switched off, each layer gets a
+        # host-managed cache of the same capacity
+        for m in mods:
+            m._dc_cap = 0
+            offload._init_cache(m, dev, cfg.capacity)
+        for c in range(start):
+            hc.stage(c)
+            step()
+        torch.cuda.synchronize(dev)
+        before = offload.STATS.copy()
+        la, lb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        la.record()
+        for c in range(start, start + steps):
+            hc.stage(c)
+            step()
+        lb.record()
+        torch.cuda.synchronize(dev)
+        after = offload.STATS.copy()
+        l_dt = la.elapsed_time(lb) / 1000.0
+        lh, lm = after["hits"] - before["hits"], after["misses"] - before["misses"]
+        host_lru = {
+            "what": "the same window through offload.cached_forward (host-managed LRU cache of "
+                    "the same capacity, eager: the decisions need the ids on the host)",
+            "tokens_per_s": round(steps / l_dt, 3), "ms_per_step": round(1e3 * l_dt / steps, 4),
+            "hit_rate": round(lh / max(1, lh + lm), 4),
+            "x_equal_headline_step": bool(torch.equal(x, x_headline))}
         return {
             "workload": "the headline step through the reference's hooks: MoEExperts modules "
                         "with the four page-locked host buffers, devcache.install_dev_cache, "
@@ -525,14 +572,17 @@ def dropin_bench(lib, hc, steps: int, start: int, split: int, x_headline) -> dic
             if split else None,
             "hits_misses": [int(hits), int(misses)],
             "x_equal_headline_step": bool(torch.equal(x_step, x_headline)),
+            "eager": eager,
             "prefill": prefill_hooks,
+            "host_lru": host_lru,
         }, xp.clone()
     finally:
         moe.MoEExperts.forward = stock
         offload._DeviceGather._by_key.clear()
         devcache._dev_ptr_cache.clear()          # the arenas are freed below
         for m in mods:
-            for a in [a for a in vars(m) if a.startswith("_dc_")]:
+            for a in [a for a in vars(m) if a.startswith("_dc_") or a.startswith("_cache_")
+                      or a in ("_cap", "_lru_state")]:
                 delattr(m, a)
         del mods, model
         torch.cuda.empty_cache()
