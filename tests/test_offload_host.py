@@ -111,6 +111,8 @@ def test_router_trace_and_census(tmp_path):
         assert offload.CENSUS[0].tolist() == [0] * 8
         offload._count(1, torch.tensor([[7, 7, 6]]))
         assert offload.CENSUS[1].tolist() == [0, 2, 2, 3, 1, 1, 1, 2]
+        offload._count(1, torch.tensor([[8, -1, 6]]))               # ids outside the census: dropped
+        assert offload.CENSUS[1].tolist() == [0, 2, 2, 3, 1, 1, 2, 2]
         recs = offload.TRACE.records
         assert [r["phase"] for r in recs] == ["decode", "prefill"]
         assert recs[1] == {"phase": "prefill", "layer": 0, "ids": [[1, 2], [3, 4]]}
