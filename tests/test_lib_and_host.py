@@ -191,6 +191,12 @@ def test_capacity_sizing_arithmetic():
     assert offload.capacity_for_free_vram(None, 40, 256, free_bytes=280 * GiB) == 256
     assert offload.capacity_for_free_vram(None, 40, 256, free_bytes=280 * GiB,
                                           cap_per_layer=96) == 96
+    # the experts' own size when they are not Drama-3's
+    assert offload.capacity_for_free_vram(None, 4, 32, free_bytes=4 * GiB,
+                                          expert_bytes=1 << 20) == 32
+    assert offload.capacity_for_free_vram(None, 4, 256, free_bytes=4 * GiB,
+                                          expert_bytes=1 << 20) == \
+        int((4 - 3.5) * GiB // (4 << 20))
 
 
 def test_fp8_moe_forward_has_no_cpu_path(lib):
