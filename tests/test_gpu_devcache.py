@@ -197,3 +197,24 @@ def test_coded_pool_through_the_hooks_equals_raw(lib, dev, pair):
     for a in ("_dc_w13", "_dc_w2", "_dc_s13", "_dc_s2", "_dc_slot_of", "_dc_stamp"):
         assert torch.equal(getattr(host, a).view(torch.uint8), getattr(twin, a).view(torch.uint8)), a
     assert devcache.cache_stats(host) == devcache.cache_stats(twin)
+
+
+def test_decode_row_wider_than_the_cache_takes_the_gather(lib, dev, pair):
+    """A one-row call with more ids than slots goes to offload's gather
+    (the table would give one slot to two ids); the table is not touched
+    and the output equals the resident forward's."""
+    import devcache
+    from fp8_moe import fp8_moe_forward
+    ref, host = pair
+    devcache.init_dev_cache(host, dev, 4)
+    before = [t.clone() for t in (host._dc_slot_of, host._dc_stamp, host._dc_step)]
+    x = torch.randn(1, H, device=dev).to(torch.bfloat16)
+    ids = torch.randperm(E, device=dev)[:K].unsqueeze(0)
+    w = torch.softmax(torch.rand(1, K, device=dev), -1)
+    got = devcache.dev_cached_forward(host, x, ids, w)
+    want = fp8_moe_forward(x, ids, w, ref.w13_weight, ref.w13_scale_inv, ref.w2_weight,
+                           ref.w2_scale_inv)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    for t0, t1 in zip(before, (host._dc_slot_of, host._dc_stamp, host._dc_step)):
+        assert torch.equal(t0, t1)
