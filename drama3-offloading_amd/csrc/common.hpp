@@ -160,7 +160,6 @@ __device__ __forceinline__ uint64_t wave_reduce_u64(uint64_t v) {
   return best;
 }
 
-// Value of lane `src` (uniform) as a scalar.
 // Sum over the wave, uniform in every lane: DPP butterfly within each row of
 // 16 lanes, then the four row sums read as scalars and added in row order.
 __device__ __forceinline__ float wave_sum_f32_dpp(float v) {
@@ -179,6 +178,7 @@ __device__ __forceinline__ float wave_sum_f32_dpp(float v) {
   return s;
 }
 
+// Value of lane `src` (uniform) as a scalar.
 __device__ __forceinline__ int32_t lane_value(int32_t v, int src) {
   return __builtin_amdgcn_readlane(v, src);
 }

@@ -377,7 +377,17 @@ __global__ __launch_bounds__(64 * (kMaxK / 2 + 1)) void down_gemv_kernel(
   // the ids.
   // No load under a branch, for the reason given in the gate/up kernel.
   const int j0 = lane * 8 < inter ? lane * 8 : 0;
+  // The residual element of the output this thread combines (threads
+  // 0..kDownRows-1) and the token's shared gate go out first: they do not
+  // depend on the sums, and loaded in the combine they would add a memory
+  // round trip after it.  Without a residual the load reads the first word
+  // of the wave's own activation row (loaded next anyway) and is ignored.
   const float* ap0 = act + static_cast<int64_t>(p0) * inter;
+  const int64_t o_mine =
+      static_cast<int64_t>(t) * hidden + c0 + min(static_cast<int>(threadIdx.x), kDownRows - 1);
+  const uint16_t res_v =
+      *(residual ? residual + o_mine : reinterpret_cast<const uint16_t*>(ap0));
+  const float sig_v = SHARED ? sh.sig[t] : 0.0f;
   const float* ap1 = act + static_cast<int64_t>(p1) * inter;
   float4 araw0[2], araw1[2];
   araw0[0] = *reinterpret_cast<const float4*>(ap0 + j0);
@@ -488,9 +498,9 @@ __global__ __launch_bounds__(64 * (kMaxK / 2 + 1)) void down_gemv_kernel(
     uint16_t y = f32_to_bf16(sum);
     if (SHARED) {
       // out = residual + (routed + sig * shared), as moe_shared_down on the routed output
-      y = shared_out(spart[threadIdx.x], sh.sig[t], &y, residual ? residual + o : nullptr);
+      y = shared_out(spart[threadIdx.x], sig_v, true, y, residual != nullptr, res_v);
     } else if (residual) {
-      y = f32_to_bf16(bf16_to_f32(residual[o]) + bf16_to_f32(y));
+      y = f32_to_bf16(bf16_to_f32(res_v) + bf16_to_f32(y));
     }
     out[o] = y;
   }

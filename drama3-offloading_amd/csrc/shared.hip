@@ -17,21 +17,25 @@
 // output and the residual added in its epilogue.  Both are GEMVs over
 // weights read once per 4 tokens (per token at decode): HBM-bound, 6 MiB per
 // layer at H = 2048, Is = 512.  Sums are f32 fused multiply-adds over each
-// lane's 16-byte slices in row order, then a butterfly over the 64 lanes.
+// lane's 16-byte slices in row order, then the 64 lane sums (wave_sum_f32).
 #include "shared.hpp"
 
 namespace moe {
 
 constexpr int kSharedTB = 4;   // tokens per pass over the weights (1 when there is one)
 constexpr int kUnroll = 4;     // 16-byte slices per lane in flight per row
+// Waves per workgroup: small workgroups spread the rows over every CU.  A
+// 1-token call (both kernels, 2048 x 512) measured 7.07 us at 2, 7.12 at 1
+// and 7.47 at 4 on MI355X.
+constexpr int kWavesPerWG = 2;
 
 template <int TB>
-__global__ __launch_bounds__(256) void shared_gate_up_kernel(
+__global__ __launch_bounds__(64 * kWavesPerWG) void shared_gate_up_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg, const uint16_t* __restrict__ wu,
     const uint16_t* __restrict__ wsg, int32_t tokens, int32_t hidden, int32_t inter,
     uint16_t* __restrict__ act, float* __restrict__ sig) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int j = blockIdx.x * 4 + wave;           // j == inter: the sigmoid gate row
+  const int j = blockIdx.x * kWavesPerWG + wave; // j == inter: the sigmoid gate row
   if (j > inter) return;                         // no barriers below
   const bool gate_row = j == inter;
   const uint16_t* const rows[2] = {gate_row ? wsg : wg + static_cast<int64_t>(j) * hidden,
@@ -53,30 +57,37 @@ __global__ __launch_bounds__(256) void shared_gate_up_kernel(
 }
 
 template <int TB, int U>
-__global__ __launch_bounds__(256) void shared_down_kernel(
+__global__ __launch_bounds__(64 * kWavesPerWG) void shared_down_kernel(
     const uint16_t* __restrict__ act, const float* __restrict__ sig,
     const uint16_t* __restrict__ wd, int32_t tokens, int32_t hidden, int32_t inter,
     const uint16_t* __restrict__ routed, const uint16_t* __restrict__ residual,
     uint16_t* __restrict__ out) {
   constexpr int kRows = 4;                        // output rows per wave
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int r0 = (blockIdx.x * 4 + wave) * kRows;
+  const int r0 = (blockIdx.x * kWavesPerWG + wave) * kRows;
   if (r0 >= hidden) return;                       // hidden % 16 == 0: all kRows rows exist
   const uint16_t* rows[kRows];
 #pragma unroll
   for (int i = 0; i < kRows; ++i) rows[i] = wd + static_cast<int64_t>(r0 + i) * inter;
   for (int t0 = 0; t0 < tokens; t0 += TB) {
+    // lane i * TB + t finishes (row r0 + i, token t0 + t): its routed and
+    // residual values and the token's gate go out before the weights (lanes
+    // past the outputs re-read the last output's; an absent buffer reads the
+    // first word of act, which the sums read anyway, and is ignored)
+    const int li = min(lane, kRows * TB - 1);
+    const int tt = min(t0 + li % TB, tokens - 1);
+    const int64_t oo = static_cast<int64_t>(tt) * hidden + r0 + li / TB;
+    const uint16_t rv = *(routed ? routed + oo : act);
+    const uint16_t sv = *(residual ? residual + oo : act);
+    const float sg = sig[tt];
     float acc[kRows][TB];
     rows_dot_bf16<kRows, TB, U>(rows, act, inter, t0, tokens, inter >> 3, lane, acc);
-    // lane i * TB + t finishes (row r0 + i, token t0 + t)
 #pragma unroll
     for (int i = 0; i < kRows; ++i)
 #pragma unroll
       for (int t = 0; t < TB; ++t) {
         if (lane != i * TB + t || t0 + t >= tokens) continue;
-        const int64_t o = static_cast<int64_t>(t0 + t) * hidden + r0 + i;
-        out[o] = shared_out(acc[i][t], sig[t0 + t], routed ? routed + o : nullptr,
-                            residual ? residual + o : nullptr);
+        out[oo] = shared_out(acc[i][t], sg, routed != nullptr, rv, residual != nullptr, sv);
       }
   }
 }
@@ -115,10 +126,10 @@ __global__ __launch_bounds__(1024) void all_finite_kernel(const void* __restrict
 int launch_shared_gate_up(const uint16_t* x, const uint16_t* wg, const uint16_t* wu,
                           const uint16_t* wsg, int32_t tokens, int32_t hidden, int32_t inter,
                           uint16_t* act, float* sig, hipStream_t s) {
-  const unsigned grid = static_cast<unsigned>((inter + 1 + 3) / 4);
+  const unsigned grid = static_cast<unsigned>((inter + 1 + kWavesPerWG - 1) / kWavesPerWG);
   auto kern = tokens == 1 ? shared_gate_up_kernel<1> : shared_gate_up_kernel<kSharedTB>;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, s, x, wg, wu, wsg, tokens, hidden, inter, act,
-                     sig);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kWavesPerWG), 0, s, x, wg, wu, wsg, tokens,
+                     hidden, inter, act, sig);
   return check_launch("moe_shared_gate_up");
 }
 
@@ -130,8 +141,9 @@ int launch_shared_down(const uint16_t* act, const float* sig, const uint16_t* wd
   auto kern = tokens == 1 ? (one ? shared_down_kernel<1, 1> : shared_down_kernel<1, kUnroll>)
                           : (one ? shared_down_kernel<kSharedTB, 1>
                                  : shared_down_kernel<kSharedTB, kUnroll>);
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(hidden / 16)), dim3(256), 0, s, act, sig,
-                     wd, tokens, hidden, inter, routed, residual, out);
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(hidden / (4 * kWavesPerWG))),
+                     dim3(64 * kWavesPerWG), 0, s, act, sig, wd, tokens, hidden, inter, routed,
+                     residual, out);
   return check_launch("moe_shared_down");
 }
 

@@ -23,11 +23,9 @@ __device__ __forceinline__ float dot8_bf16(u32x4 w, u32x4 x, float acc) {
   return acc;
 }
 
-__device__ __forceinline__ float wave_sum_f32(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
+// The 64 lane sums added: DPP within rows of 16 lanes, then the four rows in
+// order (no LDS round trips, which a shuffle butterfly takes six of).
+__device__ __forceinline__ float wave_sum_f32(float v) { return wave_sum_f32_dpp(v); }
 
 // bf16 rounding of an f32 value, returned as f32.
 __device__ __forceinline__ float rbf16(float v) { return bf16_to_f32(f32_to_bf16(v)); }
@@ -35,7 +33,7 @@ __device__ __forceinline__ float rbf16(float v) { return bf16_to_f32(f32_to_bf16
 // acc[i][t] = <row_i, x[t0 + t]> over n16 16-byte slices (8 bf16 each), the
 // one dot product every shared-expert product uses: lane l sums slices
 // l, l + 64, l + 128, ... in that order with one fma per product, then the 64
-// lane sums are added by a butterfly (every lane ends with the total).  U
+// lane sums are added by wave_sum_f32 (every lane ends with the total).  U
 // slices per lane are loaded before any is used; slices past the end load
 // the last slice again and are not summed.  Tokens past `tokens` repeat the
 // last token.  U changes only the load schedule, never the sums.
@@ -92,12 +90,15 @@ __device__ __forceinline__ float shared_sig(float zsum) {
   return rbf16(1.0f / (1.0f + expf(-z)));
 }
 
-// bf16(sig * bf16(d)), then + routed and + residual, each rounded to bf16.
-__device__ __forceinline__ uint16_t shared_out(float dsum, float sig, const uint16_t* routed,
-                                               const uint16_t* residual) {
+// bf16(sig * bf16(d)), then + routed and + residual (each when present),
+// each rounded to bf16.  The callers load routed and residual early: they do
+// not depend on the sums, and a load after them would add a memory round trip.
+__device__ __forceinline__ uint16_t shared_out(float dsum, float sig, bool has_routed,
+                                               uint16_t routed, bool has_residual,
+                                               uint16_t residual) {
   float v = rbf16(sig * rbf16(dsum));
-  if (routed) v = rbf16(bf16_to_f32(*routed) + v);
-  if (residual) v = rbf16(bf16_to_f32(*residual) + v);
+  if (has_routed) v = rbf16(bf16_to_f32(routed) + v);
+  if (has_residual) v = rbf16(bf16_to_f32(residual) + v);
   return f32_to_bf16(v);
 }
 
