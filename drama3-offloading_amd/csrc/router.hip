@@ -10,8 +10,8 @@
 // lets expert ids match the oracle bit for bit.
 //
 // Kernels:
-//   logits: grid (E/4, ceil(T/TB)), 4 waves, TB = 1 for one token else 4;
-//           wave w of workgroup (bx, by) computes expert 4*bx + w for the TB
+//   logits: grid (E, ceil(T/TB)) of one wave, TB = 1 for one token else 4;
+//           the wave of workgroup (bx, by) computes expert bx for the TB
 //           tokens of block by, reading its 4 KiB gate row once.
 //   topk:   one wave per token, logits in registers, k rounds of a wave-wide
 //           max of (logit, ~index) keys (DPP, no LDS shuffles).
@@ -28,6 +28,10 @@ namespace moe {
 
 constexpr int kMaxTopK = 32;
 constexpr int kTokBlock = 4;     // tokens per logits workgroup when tokens > 1
+// Experts (one per wave) per logits workgroup: one-wave workgroups spread the
+// gate rows over every CU.  The decode router's two launches measured
+// 8.95 us per call at 1 or 2, 9.10 at 4 (a graph over 40 gates, MI355X).
+constexpr int kLogitWaves = 1;
 
 // Wave-wide float64 sum, uniform in every lane: DPP butterfly inside each
 // row of 16 lanes, then the four row sums read as scalars and added in row
@@ -78,14 +82,14 @@ __device__ __forceinline__ float bf16_of_f64(double s) {
 // chunk issued before any of it is used (no load under a branch: lanes and
 // tokens past the end re-read an in-bounds address and add nothing).
 template <int TB>
-__global__ __launch_bounds__(256) void router_logits_kernel(
+__global__ __launch_bounds__(64 * kLogitWaves) void router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ bias,
     int32_t tokens, int32_t hidden, int32_t n_experts, int bf16_logits,
     float* __restrict__ logits) {
   constexpr int U = 4;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int e = blockIdx.x * 4 + wave;
+  const int e = blockIdx.x * kLogitWaves + wave;
   const int t0 = blockIdx.y * TB;
   const int nt = min(TB, tokens - t0);
   if (e >= n_experts) return;
@@ -289,15 +293,16 @@ extern "C" int moe_router_topk(const void* x, const void* w, const float* bias,
   MOE_REQUIRE(x && w && logits && ids && weights, "moe_router_topk: NULL pointer");
   MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0,
               "moe_router_topk: x and w must be 16-byte aligned");
-  const dim3 grid((n_experts + 3) / 4, (tokens + kTokBlock - 1) / kTokBlock);
+  const dim3 grid((n_experts + kLogitWaves - 1) / kLogitWaves,
+                  (tokens + kTokBlock - 1) / kTokBlock);
   MOE_REQUIRE(grid.y <= 65535, "moe_router_topk: too many tokens (%d)", tokens);
   hipStream_t s = as_stream(stream);
   if (tokens == 1)
-    hipLaunchKernelGGL(router_logits_kernel<1>, grid, dim3(256), 0, s,
+    hipLaunchKernelGGL(router_logits_kernel<1>, grid, dim3(64 * kLogitWaves), 0, s,
                        static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias,
                        tokens, hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0, logits);
   else
-    hipLaunchKernelGGL(router_logits_kernel<kTokBlock>, grid, dim3(256), 0, s,
+    hipLaunchKernelGGL(router_logits_kernel<kTokBlock>, grid, dim3(64 * kLogitWaves), 0, s,
                        static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias,
                        tokens, hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0, logits);
   int rc = check_launch("moe_router_topk(logits)");
@@ -337,7 +342,8 @@ extern "C" int moe_route_resolve(const void* x, const void* w, const float* bias
   MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0,
               "moe_route_resolve: x and w must be 16-byte aligned");
   hipStream_t s = as_stream(stream);
-  hipLaunchKernelGGL(router_logits_kernel<1>, dim3((n_experts + 3) / 4, 1), dim3(256), 0, s,
+  hipLaunchKernelGGL(router_logits_kernel<1>, dim3((n_experts + kLogitWaves - 1) / kLogitWaves, 1),
+                     dim3(64 * kLogitWaves), 0, s,
                      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias, 1,
                      hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0, logits);
   int rc = check_launch("moe_route_resolve(logits)");
