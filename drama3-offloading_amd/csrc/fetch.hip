@@ -53,7 +53,8 @@ struct FetchArgs {
   uint32_t tile_upr[4];   // tile order: 16-byte units per row (K / 16), 0 for a byte copy
   uint32_t tile_wlog[4];  // tile order: log2 of the column units per piece (5, 4 or 3)
   int32_t npairs;
-  int64_t pieces_per_job; // sum of pieces over pairs
+  int64_t pieces_per_job; // sum of pieces over pairs (< 2^32)
+  int32_t last_job;       // max_jobs - 1, beside pieces_per_job (one kernel-argument load)
 };
 
 __global__ __launch_bounds__(kFetchThreads) void fetch_kernel(FetchArgs a,
@@ -62,7 +63,21 @@ __global__ __launch_bounds__(kFetchThreads) void fetch_kernel(FetchArgs a,
                                                               const int32_t* __restrict__ nmiss,
                                                               int32_t max_jobs) {
   __shared__ u32x4 stage[16 * 33];   // one tile-order piece, rows padded by one unit
-  const int32_t nm = min(*nmiss, max_jobs);
+  // The job of this workgroup's first item is read with the miss count, not
+  // after it (the lists hold max_jobs entries), so the count and the first
+  // record's expert and slot arrive in one memory round trip.  The values
+  // are used only if that item exists.
+  const int32_t j_first = min(static_cast<int32_t>(blockIdx.x / static_cast<uint32_t>(a.pieces_per_job)),
+                              a.last_job);
+  const int32_t e_first = fexp[j_first];
+  const int32_t s_first = fslot[j_first];
+  int32_t n_raw = *nmiss;
+  // the count passes through this (empty) statement with the list values as
+  // inputs, so all three loads are issued before anything waits on one: the
+  // compiler would otherwise sink the list loads below the no-work branch,
+  // or issue one of them after waiting for the count, a second round trip
+  asm volatile("" : "+s"(n_raw) : "s"(e_first), "s"(s_first));
+  const int32_t nm = min(n_raw, max_jobs);
   const int64_t total = static_cast<int64_t>(nm) * a.pieces_per_job;
   const int64_t row = static_cast<int64_t>(kFetchThreads) * kFetchUnroll;   // vectors per piece
   for (int64_t item = blockIdx.x; item < total; item += gridDim.x) {
@@ -73,8 +88,8 @@ __global__ __launch_bounds__(kFetchThreads) void fetch_kernel(FetchArgs a,
       k -= a.pieces[p];
       ++p;
     }
-    const int64_t e = fexp[j];
-    const int64_t s = fslot[j];
+    const int64_t e = j == j_first ? e_first : fexp[j];
+    const int64_t s = j == j_first ? s_first : fslot[j];
     const int64_t bytes = a.bytes[p];
     const char* src = a.src[p] + e * bytes;
     char* dst = a.dst[p] + s * bytes;
@@ -153,6 +168,7 @@ extern "C" int moe_fetch(const moe_fetch_pair* pairs, int32_t npairs,
               "moe_fetch: need 1 <= blocks_per_job <= 4096");
   moe::FetchArgs a = {};
   a.npairs = npairs;
+  a.last_job = max_jobs - 1;
   const int64_t row = static_cast<int64_t>(moe::kFetchThreads) * moe::kFetchUnroll;
   for (int p = 0; p < npairs; ++p) {
     const uintptr_t sa = reinterpret_cast<uintptr_t>(pairs[p].src);

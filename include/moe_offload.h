@@ -146,10 +146,13 @@ typedef struct moe_fetch_pair {
  * transposed through LDS into one contiguous 8 KiB run of the slot.
  * Replaces fetch_experts/fetch_kernel (csrc/fetch_experts.cu:49-94) and the
  * four per-buffer launches of _cpp_fetch (bin/devcache.py:197-220) with one
- * launch.  Preconditions: 1 <= npairs <= 4; each pair's src, dst and bytes
- * are 4-byte aligned (16-byte aligned pairs take the 16-byte path), and a
- * pair with tile_k > 0 is 16-byte aligned with records under 64 GiB;
- * 1 <= max_jobs <= 65535; 1 <= blocks_per_job <= 4096. */
+ * launch.  fetch_expert and fetch_slot hold max_jobs entries (each
+ * workgroup reads its first job before the count is known; entries at or
+ * past *nmiss are read, never used).  Preconditions: 1 <= npairs <= 4;
+ * each pair's src, dst and bytes are 4-byte aligned (16-byte aligned pairs
+ * take the 16-byte path), and a pair with tile_k > 0 is 16-byte aligned
+ * with records under 64 GiB; 1 <= max_jobs <= 65535;
+ * 1 <= blocks_per_job <= 4096. */
 int moe_fetch(const moe_fetch_pair* pairs, int32_t npairs,
               const int32_t* fetch_expert, const int32_t* fetch_slot,
               const int32_t* nmiss, int32_t max_jobs, int32_t blocks_per_job,
