@@ -36,26 +36,9 @@
 // contiguously.  Storing the units straight to their scattered places
 // writes 64 distinct 128-byte lines per wave instruction and measured 6 %
 // below the byte copy's rate.
-#include "common.hpp"
+#include "fetch.hpp"
 
 namespace moe {
-
-constexpr int kFetchThreads = 128;
-constexpr int kFetchUnroll = 4;
-constexpr int kFetchMaxJobsInGrid = 8;
-
-struct FetchArgs {
-  const char* src[4];
-  char* dst[4];
-  int64_t bytes[4];
-  int64_t pieces[4];      // pieces of this pair per record
-  int32_t vec16[4];       // 1 if the pair takes the 16-byte path
-  uint32_t tile_upr[4];   // tile order: 16-byte units per row (K / 16), 0 for a byte copy
-  uint32_t tile_wlog[4];  // tile order: log2 of the column units per piece (5, 4 or 3)
-  int32_t npairs;
-  int64_t pieces_per_job; // sum of pieces over pairs (< 2^32)
-  int32_t last_job;       // max_jobs - 1, beside pieces_per_job (one kernel-argument load)
-};
 
 __global__ __launch_bounds__(kFetchThreads) void fetch_kernel(FetchArgs a,
                                                               const int32_t* __restrict__ fexp,
@@ -79,97 +62,21 @@ __global__ __launch_bounds__(kFetchThreads) void fetch_kernel(FetchArgs a,
   asm volatile("" : "+s"(n_raw) : "s"(e_first), "s"(s_first));
   const int32_t nm = min(n_raw, max_jobs);
   const int64_t total = static_cast<int64_t>(nm) * a.pieces_per_job;
-  const int64_t row = static_cast<int64_t>(kFetchThreads) * kFetchUnroll;   // vectors per piece
   for (int64_t item = blockIdx.x; item < total; item += gridDim.x) {
     const int64_t j = item / a.pieces_per_job;
-    int64_t k = item - j * a.pieces_per_job;
-    int p = 0;
-    while (p + 1 < a.npairs && k >= a.pieces[p]) {
-      k -= a.pieces[p];
-      ++p;
-    }
     const int64_t e = j == j_first ? e_first : fexp[j];
     const int64_t s = j == j_first ? s_first : fslot[j];
-    const int64_t bytes = a.bytes[p];
-    const char* src = a.src[p] + e * bytes;
-    char* dst = a.dst[p] + s * bytes;
-    const uint32_t upr = a.tile_upr[p];
-    if (upr != 0) {
-      // piece k = (row group g, column units [jW, jW + W)); its destination
-      // is the contiguous run of 16W units at unit (g * upr + jW) * 16
-      const uint32_t wl = a.tile_wlog[p];
-      const uint32_t W = 1u << wl;
-      const uint32_t per_g = upr >> wl;
-      const uint32_t g = static_cast<uint32_t>(k) / per_g;
-      const uint32_t jw = (static_cast<uint32_t>(k) - g * per_g) * W;
-      const u32x4* sv = reinterpret_cast<const u32x4*>(src) + (static_cast<int64_t>(g) * 16 * upr + jw);
-      u32x4* dv = reinterpret_cast<u32x4*>(dst) + (static_cast<int64_t>(g) * upr + jw) * 16;
-      const uint32_t n = 16 * W;   // <= kFetchThreads * kFetchUnroll
-      u32x4 v[kFetchUnroll];
-      // every lane loads (slots past n repeat the last unit), so the loads
-      // issue back to back and no branch splits them
-#pragma unroll
-      for (int u = 0; u < kFetchUnroll; ++u) {
-        const uint32_t i = min(threadIdx.x + u * kFetchThreads, n - 1);
-        v[u] = __builtin_nontemporal_load(sv + (i >> wl) * upr + (i & (W - 1)));
-      }
-#pragma unroll
-      for (int u = 0; u < kFetchUnroll; ++u) {
-        const uint32_t i = threadIdx.x + u * kFetchThreads;
-        if (i < n) stage[(i >> wl) * (W + 1) + (i & (W - 1))] = v[u];
-      }
-      __syncthreads();
-#pragma unroll
-      for (int u = 0; u < kFetchUnroll; ++u) {
-        // destination unit d = (2 * bb + h) * 64 + 16q + r holds row r, column unit 8bb + 2q + h
-        const uint32_t d = threadIdx.x + u * kFetchThreads;
-        if (d < n) {
-          const uint32_t bh = d >> 6, q = (d >> 4) & 3, r = d & 15;
-          dv[d] = stage[r * (W + 1) + (bh >> 1) * 8 + 2 * q + (bh & 1)];
-        }
-      }
-      __syncthreads();
-    } else if (a.vec16[p]) {
-      const int64_t n = bytes >> 4;
-      const u32x4* sv = reinterpret_cast<const u32x4*>(src);
-      u32x4* dv = reinterpret_cast<u32x4*>(dst);
-      const int64_t r0 = k * row;
-      const int64_t base = r0 + threadIdx.x;
-      if (r0 + row <= n) {
-        u32x4 v[kFetchUnroll];
-#pragma unroll
-        for (int u = 0; u < kFetchUnroll; ++u)
-          v[u] = __builtin_nontemporal_load(sv + base + u * kFetchThreads);
-#pragma unroll
-        for (int u = 0; u < kFetchUnroll; ++u) dv[base + u * kFetchThreads] = v[u];
-      } else {
-        for (int64_t i = base; i < n; i += kFetchThreads) dv[i] = sv[i];
-      }
-    } else {
-      const int64_t n = bytes >> 2;
-      const uint32_t* sw = reinterpret_cast<const uint32_t*>(src);
-      uint32_t* dw = reinterpret_cast<uint32_t*>(dst);
-      for (int64_t i = threadIdx.x; i < n; i += kFetchThreads) dw[i] = sw[i];
-    }
+    fetch_piece(a, item - j * a.pieces_per_job, e, s, stage);
   }
 }
 
-}  // namespace moe
-
-extern "C" int moe_fetch(const moe_fetch_pair* pairs, int32_t npairs,
-                         const int32_t* fetch_expert, const int32_t* fetch_slot,
-                         const int32_t* nmiss, int32_t max_jobs, int32_t blocks_per_job,
-                         void* stream) {
+int fetch_args(const moe_fetch_pair* pairs, int32_t npairs, int32_t max_jobs, FetchArgs* out) {
   MOE_REQUIRE(pairs != nullptr, "moe_fetch: pairs is NULL");
   MOE_REQUIRE(npairs >= 1 && npairs <= 4, "moe_fetch: need 1 <= npairs <= 4 (got %d)", npairs);
-  MOE_REQUIRE(fetch_expert && fetch_slot && nmiss, "moe_fetch: NULL job list");
-  MOE_REQUIRE(max_jobs >= 1 && max_jobs <= 65535, "moe_fetch: need 1 <= max_jobs <= 65535");
-  MOE_REQUIRE(blocks_per_job >= 1 && blocks_per_job <= 4096,
-              "moe_fetch: need 1 <= blocks_per_job <= 4096");
-  moe::FetchArgs a = {};
+  FetchArgs a = {};
   a.npairs = npairs;
   a.last_job = max_jobs - 1;
-  const int64_t row = static_cast<int64_t>(moe::kFetchThreads) * moe::kFetchUnroll;
+  const int64_t row = static_cast<int64_t>(kFetchThreads) * kFetchUnroll;
   for (int p = 0; p < npairs; ++p) {
     const uintptr_t sa = reinterpret_cast<uintptr_t>(pairs[p].src);
     const uintptr_t da = reinterpret_cast<uintptr_t>(pairs[p].dst);
@@ -202,6 +109,23 @@ extern "C" int moe_fetch(const moe_fetch_pair* pairs, int32_t npairs,
       a.pieces[p] = a.vec16[p] ? ((b >> 4) + row - 1) / row : 1;
     a.pieces_per_job += a.pieces[p];
   }
+  *out = a;
+  return MOE_OK;
+}
+
+}  // namespace moe
+
+extern "C" int moe_fetch(const moe_fetch_pair* pairs, int32_t npairs,
+                         const int32_t* fetch_expert, const int32_t* fetch_slot,
+                         const int32_t* nmiss, int32_t max_jobs, int32_t blocks_per_job,
+                         void* stream) {
+  MOE_REQUIRE(fetch_expert && fetch_slot && nmiss, "moe_fetch: NULL job list");
+  MOE_REQUIRE(max_jobs >= 1 && max_jobs <= 65535, "moe_fetch: need 1 <= max_jobs <= 65535");
+  MOE_REQUIRE(blocks_per_job >= 1 && blocks_per_job <= 4096,
+              "moe_fetch: need 1 <= blocks_per_job <= 4096");
+  moe::FetchArgs a;
+  const int rc = moe::fetch_args(pairs, npairs, max_jobs, &a);
+  if (rc != MOE_OK) return rc;
   const int grid = blocks_per_job * (max_jobs < moe::kFetchMaxJobsInGrid ? max_jobs
                                                                           : moe::kFetchMaxJobsInGrid);
   hipLaunchKernelGGL(moe::fetch_kernel, dim3(grid), dim3(moe::kFetchThreads), 0,

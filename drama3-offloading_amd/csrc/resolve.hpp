@@ -27,14 +27,23 @@ struct SlotRegs {
   int64_t st[PER];
   int32_t se[PER];
 
+  // Every lane loads (slots past cap read the last one again and drop it):
+  // no load under a branch, so all of them are in flight together.
   __device__ __forceinline__ void load(const int64_t* stamp, const int32_t* slot_expert,
                                        int32_t cap) {
     const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
-      const int c = lane + 64 * j;
-      st[j] = c < cap ? stamp[c] : INT64_MAX;
-      se[j] = c < cap ? slot_expert[c] : -1;
+      const int c = min(lane + 64 * j, cap - 1);
+      st[j] = stamp[c];
+      se[j] = slot_expert[c];
+    }
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      if (lane + 64 * j >= cap) {
+        st[j] = INT64_MAX;
+        se[j] = -1;
+      }
     }
   }
 };
@@ -48,10 +57,17 @@ struct ExpertRegs {
   __device__ __forceinline__ void load(const int32_t* slot_of, int32_t n_experts) {
     const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int x = lane + 64 * j;
-      so[j] = x < n_experts ? slot_of[x] : -1;
-    }
+    for (int j = 0; j < PER; ++j) so[j] = slot_of[min(lane + 64 * j, n_experts - 1)];
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      if (lane + 64 * j >= n_experts) so[j] = -1;
+  }
+  // entry x = v (held by lane x % 64)
+  __device__ __forceinline__ void set(int32_t x, int32_t v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      if ((x >> 6) == j && (x & 63) == lane) so[j] = v;
   }
   __device__ __forceinline__ int32_t lookup(int32_t x) const {
     int32_t r = -1;
@@ -63,6 +79,36 @@ struct ExpertRegs {
     return r;
   }
 };
+
+// The miss of id e: the victim slot (smallest stamp, lowest slot on a tie,
+// one wave-wide min of (stamp + 4096) << 12 | slot; stamps start at
+// -cap >= -4096 and grow by one per call, so they stay far below 2^51) is
+// returned with its previous owner (-1 when it was empty); e becomes its
+// owner in the registers.
+template <int PER>
+__device__ __forceinline__ int32_t take_victim(SlotRegs<PER>& t, int32_t e, int32_t cap,
+                                               int32_t* victim) {
+  const int lane = threadIdx.x & 63;
+  uint64_t mine = ~0ull;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int c = lane + 64 * j;
+    const uint64_t k =
+        c < cap ? (static_cast<uint64_t>(t.st[j] + kMaxCap) << 12) | static_cast<uint64_t>(c) : ~0ull;
+    mine = k < mine ? k : mine;
+  }
+  const int32_t s = static_cast<int32_t>(wave_reduce_u64<false>(mine) & 0xfffull);
+  int32_t vloc = -1;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    if (j == (s >> 6)) {
+      vloc = t.se[j];
+      if ((s & 63) == lane) t.se[j] = e;
+    }
+  }
+  *victim = lane_value(vloc, s & 63);
+  return s;
+}
 
 // Resolve one chunk of <= 64 ids (lane r: my_e = id r, my_s = its slot now).
 // Returns nothing; updates the registers, the table in memory (lane 0), the
@@ -85,27 +131,8 @@ __device__ __forceinline__ void resolve_chunk(SlotRegs<PER>& t, int32_t my_e, in
       continue;
     }
     if (s < 0) {
-      // victim = smallest stamp, lowest slot on a tie: one wave-wide min of
-      // (stamp + 4096) << 12 | slot.  Stamps start at -cap >= -4096 and grow
-      // by one per call, so they stay far below 2^51.
-      uint64_t mine = ~0ull;
-#pragma unroll
-      for (int j = 0; j < PER; ++j) {
-        const int c = lane + 64 * j;
-        const uint64_t k =
-            c < cap ? (static_cast<uint64_t>(t.st[j] + kMaxCap) << 12) | static_cast<uint64_t>(c) : ~0ull;
-        mine = k < mine ? k : mine;
-      }
-      s = static_cast<int32_t>(wave_reduce_u64<false>(mine) & 0xfffull);
-      int32_t vloc = -1;
-#pragma unroll
-      for (int j = 0; j < PER; ++j) {
-        if (j == (s >> 6)) {
-          vloc = t.se[j];
-          if ((s & 63) == lane) t.se[j] = e;
-        }
-      }
-      const int32_t victim = lane_value(vloc, s & 63);
+      int32_t victim;
+      s = take_victim(t, e, cap, &victim);
       if (lane > r) {                      // later ids see the table as it is now
         if (my_e == victim) my_s = -1;
         if (my_e == e) my_s = s;
@@ -125,6 +152,47 @@ __device__ __forceinline__ void resolve_chunk(SlotRegs<PER>& t, int32_t my_e, in
     for (int j = 0; j < PER; ++j)
       if (j == (s >> 6) && (s & 63) == lane) t.st[j] = step;
     if (lane == 0) out_slot[base + r] = s;
+  }
+}
+
+// The resolve of one chunk of <= 64 ids on register copies of the whole
+// table (slot_of in x, slots in t), for a kernel whose workgroups all make
+// the decisions and one of them writes the next table out: the decisions of
+// resolve_chunk, nothing written to the table in memory.  Lane r ends with
+// id r's slot in slot_r (-1 for an id out of range); the misses are appended
+// to job_e / job_s by lane 0.
+template <int PER, int PERC>
+__device__ __forceinline__ void resolve_regs(SlotRegs<PERC>& t, ExpertRegs<PER>& x, int32_t my_e,
+                                             int32_t my_s, int n, int64_t step, int32_t cap,
+                                             int32_t* job_e, int32_t* job_s, int32_t& nm,
+                                             int64_t& hits, int32_t& slot_r) {
+  const int lane = threadIdx.x & 63;
+  slot_r = -1;
+  for (int r = 0; r < n; ++r) {
+    const int32_t e = lane_value(my_e, r);
+    int32_t s = lane_value(my_s, r);
+    if (e < 0) continue;
+    if (s < 0) {
+      int32_t victim;
+      s = take_victim(t, e, cap, &victim);
+      if (lane > r) {                      // later ids see the table as it is now
+        if (my_e == victim) my_s = -1;
+        if (my_e == e) my_s = s;
+      }
+      if (victim >= 0) x.set(victim, -1);
+      x.set(e, s);
+      if (lane == 0) {
+        job_e[nm] = e;
+        job_s[nm] = s;
+      }
+      ++nm;
+    } else {
+      ++hits;
+    }
+#pragma unroll
+    for (int j = 0; j < PERC; ++j)
+      if (j == (s >> 6) && (s & 63) == lane) t.st[j] = step;
+    if (lane == r) slot_r = s;
   }
 }
 

@@ -22,6 +22,7 @@
 // XCD has its own L2, and a device-scope fence inside a kernel costs more
 // than a launch.
 #include "common.hpp"
+#include "fetch.hpp"
 #include "resolve.hpp"
 
 namespace moe {
@@ -85,10 +86,13 @@ template <int TB>
 __global__ __launch_bounds__(64 * kLogitWaves) void router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ bias,
     int32_t tokens, int32_t hidden, int32_t n_experts, int bf16_logits,
-    float* __restrict__ logits) {
+    float* __restrict__ logits, int64_t* __restrict__ step_inc) {
   constexpr int U = 4;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
+  // the route + fetch launch that follows reads the slot-table step already
+  // counted, so that none of its workgroups writes what another one reads
+  if (step_inc && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *step_inc += 1;
   const int e = blockIdx.x * kLogitWaves + wave;
   const int t0 = blockIdx.y * TB;
   const int nt = min(TB, tokens - t0);
@@ -164,16 +168,28 @@ __device__ __forceinline__ float key_logit(uint32_t k) {
 //             which is then cleared.
 // The weights are one exp per lane after the picks: exp(l_r - l_0) over
 // their wave-wide sum.
+// This lane's logits lane, lane + 64, ... of a row: every lane loads (past
+// the end: the last logit again, then ignored), so the PER loads go out
+// together; a load under the bound's branch would be waited for inside it,
+// one memory round trip per load.
 template <int PER>
-__device__ __forceinline__ void wave_topk(const float* __restrict__ row, int32_t n_experts,
-                                          int32_t top_k, int32_t* id, float* wt) {
+__device__ __forceinline__ void load_logits(const float* __restrict__ row, int32_t n_experts,
+                                            float (&lv)[PER]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) lv[j] = row[min(lane + 64 * j, n_experts - 1)];
+}
+
+template <int PER>
+__device__ __forceinline__ void wave_topk_of(const float (&lv)[PER], int32_t n_experts,
+                                             int32_t top_k, int32_t* id, float* wt) {
   const int lane = threadIdx.x & 63;
   uint64_t key[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int e = lane + 64 * j;
     key[j] = e < n_experts
-                 ? (static_cast<uint64_t>(logit_key(row[e])) << 32) | (0xffffffffu - static_cast<uint32_t>(e))
+                 ? (static_cast<uint64_t>(logit_key(lv[j])) << 32) | (0xffffffffu - static_cast<uint32_t>(e))
                  : 0ull;
   }
   uint64_t pick = 0;
@@ -220,6 +236,14 @@ __device__ __forceinline__ void wave_topk(const float* __restrict__ row, int32_t
 }
 
 template <int PER>
+__device__ __forceinline__ void wave_topk(const float* __restrict__ row, int32_t n_experts,
+                                          int32_t top_k, int32_t* id, float* wt) {
+  float lv[PER];
+  load_logits<PER>(row, n_experts, lv);
+  wave_topk_of<PER>(lv, n_experts, top_k, id, wt);
+}
+
+template <int PER>
 __global__ __launch_bounds__(64) void router_topk_kernel(const float* __restrict__ logits,
                                                          int32_t n_experts, int32_t top_k,
                                                          void* __restrict__ ids, int ids64,
@@ -254,10 +278,17 @@ __global__ __launch_bounds__(64) void topk_resolve_kernel(
   table.load(slot_of, n_experts);
   StatsPrefetch prev;
   prev.load(stats);
-  const int64_t step = *step_ptr + 1;
+  int64_t step_raw = *step_ptr;
+  float lv[PER];
+  load_logits<PER>(logits, n_experts, lv);
+  // the step passes through this (empty) statement once every load above is
+  // issued: the compiler would otherwise load it where the resolve needs it,
+  // after the top-k, a second memory round trip
+  asm volatile("" : "+s"(step_raw));
+  const int64_t step = step_raw + 1;
   int32_t id;
   float wt;
-  wave_topk<PER>(logits, n_experts, top_k, &id, &wt);
+  wave_topk_of<PER>(lv, n_experts, top_k, &id, &wt);
   if (lane < top_k) {
     ids[lane] = id;
     weights[lane] = wt;
@@ -271,6 +302,110 @@ __global__ __launch_bounds__(64) void topk_resolve_kernel(
   resolve_chunk<PERC>(t, my_e, my_s, top_k, 0, step, cap, slot_of, slot_expert, out_slot,
                       fetch_slot, fetch_expert, nm, hits);
   resolve_finish<PERC>(t, step, nm, hits, cap, stamp, step_ptr, nmiss_ptr, stats, prev);
+}
+
+// The decode step's route + fetch: the top-k and slot resolve of one token
+// (topk_resolve_kernel's decisions) and the fetch of its misses (fetch.hip's
+// pieces) in one launch, on the fetch's grid.  Every workgroup's first wave
+// makes the same decisions from the same inputs (the logits and the current
+// table, which no workgroup of this launch writes) and puts the miss list
+// in LDS; workgroup 0 also writes the outputs and the next table.  The slot
+// table is double-buffered: the call counted `step` (the logits launch before
+// it adds one) reads buffer (step - 1) & 1 and writes buffer step & 1, so no
+// workgroup can see a half-written table.  Saves the separate resolve launch
+// and the fetch's reload of the miss list.
+template <int PER, int PERC>
+__global__ __launch_bounds__(kFetchThreads) void route_fetch_kernel(
+    FetchArgs a, const float* __restrict__ logits, int32_t n_experts, int32_t top_k,
+    int32_t* __restrict__ ids, float* __restrict__ weights, int32_t* __restrict__ slot_of,
+    int32_t* __restrict__ slot_expert, int64_t* __restrict__ stamp, int32_t cap,
+    const int64_t* __restrict__ step_ptr, int32_t* __restrict__ out_slot,
+    int32_t* __restrict__ fetch_slot, int32_t* __restrict__ fetch_expert,
+    int32_t* __restrict__ nmiss_ptr, int64_t* __restrict__ stats) {
+  __shared__ u32x4 stage[16 * 33];
+  __shared__ int32_t job_e[kMaxTopK], job_s[kMaxTopK], job_n;
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    // both buffers, the step, the counters and the logits in one round trip
+    SlotRegs<PERC> ta, tb;
+    ta.load(stamp, slot_expert, cap);
+    tb.load(stamp + cap, slot_expert + cap, cap);
+    ExpertRegs<PER> xa, xb;
+    xa.load(slot_of, n_experts);
+    xb.load(slot_of + n_experts, n_experts);
+    StatsPrefetch prev;
+    prev.load(stats);
+    int64_t step = *step_ptr;
+    float lv[PER];
+    load_logits<PER>(logits, n_experts, lv);
+    // the step passes through this (empty) statement once every load above
+    // is issued, so it is not loaded late, after the top-k
+    asm volatile("" : "+s"(step));
+    int32_t id;
+    float wt;
+    wave_topk_of<PER>(lv, n_experts, top_k, &id, &wt);
+    const int cur = static_cast<int>((step - 1) & 1);
+    SlotRegs<PERC> t;
+    ExpertRegs<PER> x;
+#pragma unroll
+    for (int j = 0; j < PERC; ++j) {
+      t.st[j] = cur ? tb.st[j] : ta.st[j];
+      t.se[j] = cur ? tb.se[j] : ta.se[j];
+    }
+#pragma unroll
+    for (int j = 0; j < PER; ++j) x.so[j] = cur ? xb.so[j] : xa.so[j];
+    const int32_t my_e = lane < top_k ? id : -1;
+    const int32_t found = x.lookup(my_e < 0 ? 0 : my_e);
+    const int32_t my_s = my_e < 0 ? -1 : found;
+    int32_t nm = 0, slot_r;
+    int64_t hits = 0;
+    resolve_regs<PER, PERC>(t, x, my_e, my_s, top_k, step, cap, job_e, job_s, nm, hits, slot_r);
+    if (lane == 0) job_n = nm;
+    if (blockIdx.x == 0) {
+      if (lane < top_k) {
+        ids[lane] = id;
+        weights[lane] = wt;
+        out_slot[lane] = slot_r;
+      }
+      const int nxt = 1 - cur;
+      int32_t* so_n = slot_of + static_cast<int64_t>(nxt) * n_experts;
+      int32_t* se_n = slot_expert + static_cast<int64_t>(nxt) * cap;
+      int64_t* st_n = stamp + static_cast<int64_t>(nxt) * cap;
+#pragma unroll
+      for (int j = 0; j < PERC; ++j) {
+        const int c = lane + 64 * j;
+        if (c < cap) {
+          st_n[c] = t.st[j];
+          se_n[c] = t.se[j];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        const int e = lane + 64 * j;
+        if (e < n_experts) so_n[e] = x.so[j];
+      }
+      if (lane == 0) {
+        for (int j = 0; j < nm; ++j) {
+          fetch_expert[j] = job_e[j];
+          fetch_slot[j] = job_s[j];
+        }
+        *nmiss_ptr = nm;
+        if (stats) {
+          stats[0] = prev.hits + hits;
+          stats[1] = prev.misses + nm;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const int64_t total = static_cast<int64_t>(job_n) * a.pieces_per_job;
+  for (int64_t item = blockIdx.x; item < total; item += gridDim.x) {
+    const int64_t j = item / a.pieces_per_job;
+    // job_e/job_s are the same in every lane: made scalar, so the piece's
+    // addressing stays scalar as in the fetch kernel
+    fetch_piece(a, item - j * a.pieces_per_job, __builtin_amdgcn_readfirstlane(job_e[j]),
+                __builtin_amdgcn_readfirstlane(job_s[j]), stage);
+  }
 }
 
 }  // namespace moe
@@ -300,11 +435,11 @@ extern "C" int moe_router_topk(const void* x, const void* w, const float* bias,
   if (tokens == 1)
     hipLaunchKernelGGL(router_logits_kernel<1>, grid, dim3(64 * kLogitWaves), 0, s,
                        static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias,
-                       tokens, hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0, logits);
+                       tokens, hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0, logits, nullptr);
   else
     hipLaunchKernelGGL(router_logits_kernel<kTokBlock>, grid, dim3(64 * kLogitWaves), 0, s,
                        static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias,
-                       tokens, hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0, logits);
+                       tokens, hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0, logits, nullptr);
   int rc = check_launch("moe_router_topk(logits)");
   if (rc) return rc;
   const int i64 = ids_dtype == MOE_I64 ? 1 : 0, bf = w_dtype == MOE_BF16 ? 1 : 0;
@@ -345,7 +480,7 @@ extern "C" int moe_route_resolve(const void* x, const void* w, const float* bias
   hipLaunchKernelGGL(router_logits_kernel<1>, dim3((n_experts + kLogitWaves - 1) / kLogitWaves, 1),
                      dim3(64 * kLogitWaves), 0, s,
                      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias, 1,
-                     hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0, logits);
+                     hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0, logits, nullptr);
   int rc = check_launch("moe_route_resolve(logits)");
   if (rc) return rc;
 #define MOE_TR(PE, PC)                                                                          \
@@ -361,4 +496,51 @@ extern "C" int moe_route_resolve(const void* x, const void* w, const float* bias
   }
 #undef MOE_TR
   return check_launch("moe_route_resolve(topk+resolve)");
+}
+
+extern "C" int moe_route_fetch(const void* x, const void* w, const float* bias, int32_t logit_dtype,
+                               int32_t hidden, int32_t n_experts, int32_t top_k, float* logits,
+                               int32_t* ids, float* weights, int32_t* slot_of,
+                               int32_t* slot_expert, int64_t* slot_stamp, int32_t cap,
+                               int64_t* step, int32_t* out_slot, int32_t* fetch_slot,
+                               int32_t* fetch_expert, int32_t* nmiss, int64_t* stats,
+                               const moe_fetch_pair* pairs, int32_t npairs,
+                               int32_t blocks_per_job, void* stream) {
+  MOE_REQUIRE(x && w && logits && ids && weights && slot_of && slot_expert && slot_stamp && step &&
+                  out_slot && fetch_slot && fetch_expert && nmiss,
+              "moe_route_fetch: NULL pointer");
+  MOE_REQUIRE(logit_dtype == MOE_F32 || logit_dtype == MOE_BF16,
+              "moe_route_fetch: logit_dtype must be MOE_F32 or MOE_BF16");
+  MOE_REQUIRE(hidden > 0 && hidden % 8 == 0, "moe_route_fetch: hidden %% 8 != 0 (%d)", hidden);
+  MOE_REQUIRE(top_k >= 1 && top_k <= kMaxTopK && top_k <= n_experts && n_experts <= 1024,
+              "moe_route_fetch: need 1 <= top_k <= min(32, n_experts), n_experts <= 1024");
+  MOE_REQUIRE(cap >= 1 && cap <= 1024, "moe_route_fetch: need 1 <= cap <= 1024");
+  MOE_REQUIRE(top_k <= cap, "moe_route_fetch: top_k (%d) exceeds the cache capacity (%d)",
+              top_k, cap);
+  MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0,
+              "moe_route_fetch: x and w must be 16-byte aligned");
+  MOE_REQUIRE(blocks_per_job >= 1 && blocks_per_job <= 4096,
+              "moe_route_fetch: need 1 <= blocks_per_job <= 4096");
+  FetchArgs a;
+  const int rc0 = fetch_args(pairs, npairs, top_k, &a);
+  if (rc0 != MOE_OK) return rc0;
+  hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(router_logits_kernel<1>, dim3((n_experts + kLogitWaves - 1) / kLogitWaves, 1),
+                     dim3(64 * kLogitWaves), 0, s,
+                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias, 1,
+                     hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0, logits, step);
+  int rc = check_launch("moe_route_fetch(logits)");
+  if (rc) return rc;
+  const int grid = blocks_per_job * (top_k < kFetchMaxJobsInGrid ? top_k : kFetchMaxJobsInGrid);
+#define MOE_RF(PE, PC)                                                                          \
+  hipLaunchKernelGGL((route_fetch_kernel<PE, PC>), dim3(grid), dim3(kFetchThreads), 0, s, a,    \
+                     logits, n_experts, top_k, ids, weights, slot_of, slot_expert, slot_stamp,   \
+                     cap, step, out_slot, fetch_slot, fetch_expert, nmiss, stats)
+  if (n_experts <= 256) {
+    if (cap <= 256) MOE_RF(4, 4); else MOE_RF(4, 16);
+  } else {
+    if (cap <= 256) MOE_RF(16, 4); else MOE_RF(16, 16);
+  }
+#undef MOE_RF
+  return check_launch("moe_route_fetch(route+fetch)");
 }

@@ -10,6 +10,11 @@ Per layer, all on one stream, nothing synchronising and nothing allocating:
     y     = fp8_moe_forward(h, slots, w)      W8A8 expert FFN on the cache (HIP)
     x     = h + y
 
+The router, resolve and fetch are two launches (moe_route_fetch: the logits,
+then every fetch workgroup resolving the call itself from a double-buffered
+slot table and copying its share of the misses), or with fused_fetch=False
+(and always with coded pools) three (moe_route_resolve, then the fetch).
+
 With `shared_expert`, the step is the full MoE block, one call after the
 fetch: the gated bf16 shared expert rides in the two routed GEMV launches
 (moe_fp8_moe_block_forward), which also add the residual,
@@ -73,6 +78,7 @@ class DecodeConfig:
     zipf_s: float = 1.1
     gate_std: float = 0.002
     blocks_per_job: int = 3
+    fused_fetch: bool = True        # router + resolve + fetch in two launches (moe_route_fetch)
     noncoherent_pool: bool = False
     shared_expert: bool = False     # the MoE block's gated bf16 shared expert
     shared_inter: int = 512
@@ -123,9 +129,10 @@ class DecodeHarness:
         self.views = [self.layout.views(c) for c in self.cache]
         # slot tables and per-layer scratch
         i32 = dict(dtype=torch.int32, device=dev)
-        self.slot_of = [torch.empty(E, **i32) for _ in range(L)]
-        self.slot_expert = [torch.empty(C, **i32) for _ in range(L)]
-        self.stamp = [torch.empty(C, dtype=torch.int64, device=dev) for _ in range(L)]
+        # double-buffered slot tables (moe_route_fetch; buffer 0 only otherwise)
+        self.tab_slot_of = torch.empty((L, 2, E), **i32)
+        self.tab_slot_expert = torch.empty((L, 2, C), **i32)
+        self.tab_stamp = torch.empty((L, 2, C), dtype=torch.int64, device=dev)
         self.step = [torch.empty(1, dtype=torch.int64, device=dev) for _ in range(L)]
         self.stats = torch.zeros((L, 2), dtype=torch.int64, device=dev)
         self.ids = torch.zeros((L, 1, K), **i32)
@@ -162,6 +169,8 @@ class DecodeHarness:
             if len(coded) != L:
                 raise ValueError(f"{len(coded)} coded pools for {L} layers")
             self.coded = coded
+        # the step takes moe_route_fetch (router + resolve + fetch), decided once
+        self.fused = cfg.mode == "cached" and cfg.fused_fetch and self.coded is None
         if cfg.shared_expert:
             # seeded bf16 shared experts, resident (6 MiB per layer at 2048 x 512)
             g2 = torch.Generator(device=dev).manual_seed(cfg.seed + 3)
@@ -181,6 +190,30 @@ class DecodeHarness:
         self.graph = None
         self.cursor = 0
 
+    def _tables(self) -> tuple[list, list, list]:
+        """Each layer's current slot table (slot_of, slot_expert, stamp views;
+        one host sync): buffer step & 1 on the fused path, else buffer 0."""
+        L = self.cfg.layers
+        if self.fused:
+            buf = (torch.cat(self.step).cpu() & 1).tolist()
+        else:
+            buf = [0] * L
+        return ([self.tab_slot_of[l, b] for l, b in zip(range(L), buf)],
+                [self.tab_slot_expert[l, b] for l, b in zip(range(L), buf)],
+                [self.tab_stamp[l, b] for l, b in zip(range(L), buf)])
+
+    @property
+    def slot_of(self) -> list:
+        return self._tables()[0]
+
+    @property
+    def slot_expert(self) -> list:
+        return self._tables()[1]
+
+    @property
+    def stamp(self) -> list:
+        return self._tables()[2]
+
     def shared(self, l: int):
         """Layer l's shared expert (gate, up, down, sigmoid gate)."""
         return self.sh_wg[l], self.sh_wu[l], self.sh_wd[l], self.sh_wsg[l]
@@ -188,7 +221,8 @@ class DecodeHarness:
     # -------------------------------------------------------------- state
     def reset_tables(self) -> None:
         for l in range(self.cfg.layers):
-            self.lib.slots_init(self.slot_of[l], self.slot_expert[l], self.stamp[l], self.step[l])
+            self.lib.slots_init(self.tab_slot_of[l, 0], self.tab_slot_expert[l, 0],
+                                self.tab_stamp[l, 0], self.step[l])
         self.stats.zero_()
 
     def stage(self, s: int) -> None:
@@ -200,13 +234,22 @@ class DecodeHarness:
         cfg, lib = self.cfg, self.lib
         stub_linear(self.x, self.w_stub[l], self.h)
         w13, s13, w2, s2 = self.views[l]
-        if cfg.mode == "cached":
+        if self.fused:
+            # router, then resolve + miss fetch in one launch (double-buffered table)
+            lib.route_fetch(self.h, self.gate[l], self.bias_live[l], cfg.top_k, self.logits[l],
+                            self.ids[l], self.wts[l], self.tab_slot_of[l],
+                            self.tab_slot_expert[l], self.tab_stamp[l], self.step[l],
+                            self.out_slot[l], self.fslot[l], self.fexp[l], self.nmiss[l],
+                            [self.pairs[l]], cfg.blocks_per_job, stats=self.stats[l],
+                            logit_dtype=cfg.router_logits)
+            slots = self.out_slot[l]
+        elif cfg.mode == "cached":
             # router + slot resolve (two launches), then the miss fetch
             lib.route_resolve(self.h, self.gate[l], self.bias_live[l], cfg.top_k, self.logits[l],
-                              self.ids[l], self.wts[l], self.slot_of[l], self.slot_expert[l],
-                              self.stamp[l], self.step[l], self.out_slot[l], self.fslot[l],
-                              self.fexp[l], self.nmiss[l], self.stats[l],
-                              logit_dtype=cfg.router_logits)
+                              self.ids[l], self.wts[l], self.tab_slot_of[l, 0],
+                              self.tab_slot_expert[l, 0], self.tab_stamp[l, 0], self.step[l],
+                              self.out_slot[l], self.fslot[l], self.fexp[l], self.nmiss[l],
+                              self.stats[l], logit_dtype=cfg.router_logits)
             self.fetch(l, self.fexp[l], self.fslot[l], self.nmiss[l])
             slots = self.out_slot[l]
         else:

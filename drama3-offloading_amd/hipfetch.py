@@ -82,6 +82,9 @@ SIGNATURES = {
                                   _vp, _i32, _vp]),
     "moe_route_resolve": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
                                     _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "moe_route_fetch": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
+                                  _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
+                                  C.POINTER(FetchPair), _i32, _i32, _vp]),
     "moe_fp8_moe_workspace": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "moe_fp8_moe_forward": (C.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
                                       _i32, _i32, _i32, _vp, _vp, _sz, _vp]),
@@ -275,6 +278,33 @@ class Native:
             stamp.data_ptr(), slot_expert.numel(), step.data_ptr(), out_slot.data_ptr(),
             fetch_slot.data_ptr(), fetch_expert.data_ptr(), nmiss.data_ptr(), self._ptr(stats),
             self.stream()), "moe_route_resolve")
+
+    def route_fetch(self, x, w, bias, top_k: int, logits, ids, weights, slot_of, slot_expert,
+                    stamp, step, out_slot, fetch_slot, fetch_expert, nmiss, pairs,
+                    blocks_per_job: int, stats=None, logit_dtype: str = "bf16") -> None:
+        """Router + slot resolve + fetch of the misses, one token, on a
+        double-buffered table: slot_of [2, E], slot_expert and stamp [2, C]
+        (buffer 0 set up by slots_init; after a call leaving step = s the
+        table is buffer s & 1).  pairs as for fetch()."""
+        if x.shape[0] != 1:
+            raise ValueError("route_fetch takes exactly one token")
+        if slot_of.dim() != 2 or slot_of.shape[0] != 2 or slot_expert.dim() != 2 \
+                or slot_expert.shape[0] != 2 or tuple(stamp.shape) != tuple(slot_expert.shape):
+            raise ValueError("route_fetch takes double-buffered tables: slot_of [2, E], "
+                             "slot_expert and stamp [2, C]")
+        self._on_gpu("moe_route_fetch", x, w, bias, logits, ids, weights, slot_of, slot_expert,
+                     stamp, step, out_slot, fetch_slot, fetch_expert, nmiss, stats)
+        H = x.shape[1]
+        E = w.shape[0]
+        if slot_of.shape[1] != E:
+            raise ValueError(f"slot_of [2, {slot_of.shape[1]}] does not match {E} experts")
+        arr = (FetchPair * len(pairs))(*[FetchPair(*((tuple(p) + (0,))[:4])) for p in pairs])
+        self._check(self.cdll.moe_route_fetch(
+            x.data_ptr(), w.data_ptr(), self._ptr(bias), self._logit_code(logit_dtype), H, E,
+            top_k, logits.data_ptr(), ids.data_ptr(), weights.data_ptr(), slot_of.data_ptr(),
+            slot_expert.data_ptr(), stamp.data_ptr(), slot_expert.shape[1], step.data_ptr(),
+            out_slot.data_ptr(), fetch_slot.data_ptr(), fetch_expert.data_ptr(), nmiss.data_ptr(),
+            self._ptr(stats), arr, len(pairs), blocks_per_job, self.stream()), "moe_route_fetch")
 
     # ------------------------------------------------------------ experts
     def fp8_moe_workspace(self, tokens, top_k, n_experts, hidden, inter) -> int:

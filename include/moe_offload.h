@@ -196,6 +196,32 @@ int moe_route_resolve(const void* x, const void* w, const float* bias,
                       int32_t* fetch_expert, int32_t* nmiss, int64_t* stats,
                       void* stream);
 
+/* Decode-step fusion of the router, the slot-table resolve AND the fetch of
+ * the misses for ONE token, in two launches instead of four: the logits
+ * (which also count the step), then one launch on the fetch's grid whose
+ * every workgroup makes the resolve's decisions and copies its share of the
+ * misses, workgroup 0 writing the outputs.  Decisions, outputs (ids,
+ * weights, out_slot, fetch lists, nmiss, stats) and cache contents are those
+ * of moe_route_resolve followed by moe_fetch(pairs, npairs, fetch_expert,
+ * fetch_slot, nmiss, top_k, blocks_per_job).
+ * The slot table is double-buffered: slot_of [2, n_experts], slot_expert
+ * [2, cap] and slot_stamp [2, cap], with buffer 0 set up by moe_slots_init
+ * (step 0); after a call that leaves *step = s the table is buffer s & 1
+ * (the call reads buffer (s - 1) & 1 and writes the other, so no workgroup
+ * reads what another writes).
+ * No counterpart in the reference: it fuses the router (moe.py:217-220),
+ * _resolve_slots (bin/devcache.py:45-98) and the fetch
+ * (csrc/fetch_experts.cu:49-94) as they occur back to back in the decode
+ * step (bin/devcache.py:230-255).  Constraints: those of moe_route_resolve
+ * and moe_fetch, with n_experts <= 1024 and cap <= 1024. */
+int moe_route_fetch(const void* x, const void* w, const float* bias, int32_t logit_dtype,
+                    int32_t hidden, int32_t n_experts, int32_t top_k, float* logits,
+                    int32_t* ids, float* weights, int32_t* slot_of, int32_t* slot_expert,
+                    int64_t* slot_stamp, int32_t cap, int64_t* step, int32_t* out_slot,
+                    int32_t* fetch_slot, int32_t* fetch_expert, int32_t* nmiss, int64_t* stats,
+                    const moe_fetch_pair* pairs, int32_t npairs, int32_t blocks_per_job,
+                    void* stream);
+
 /* ------------------------------------------------------- expert compute */
 
 /* Workspace bytes moe_fp8_moe_forward needs for this shape. */

@@ -1,0 +1,86 @@
+"""moe_route_fetch, the decode step's router + resolve + fetch in two
+launches, against moe_route_resolve followed by moe_fetch (three launches),
+at Drama-3 shape (256 experts, top-8, H 2048, I 512) over 3 layers and
+popularity drifts: two harnesses on the same pools, one per path, step for
+step, eager and then replayed from their graphs.  Step outputs, router
+outputs, slot decisions, miss queues, hit/miss counters, the current slot
+tables (the fused path's double buffer read at step & 1) and every occupied
+cache slot are equal.  The tests of the full 40-layer step check the fused
+path against the oracle; this one pins it to the separate launches."""
+import pytest
+import torch
+
+from conftest import say
+
+pytestmark = pytest.mark.gpu
+
+
+def _same(a, b, tag):
+    assert torch.equal(a.x, b.x), f"{tag}: step output"
+    for name in ("ids", "wts", "out_slot", "stats", "step"):
+        ga, gb = getattr(a, name), getattr(b, name)
+        if isinstance(ga, list):
+            assert all(torch.equal(u, v) for u, v in zip(ga, gb)), f"{tag}: {name}"
+        else:
+            assert torch.equal(ga, gb), f"{tag}: {name}"
+    for l in range(a.cfg.layers):
+        n = int(a.nmiss[l])
+        assert n == int(b.nmiss[l]), f"{tag} layer {l}: nmiss"
+        assert torch.equal(a.fexp[l][:n], b.fexp[l][:n]) and torch.equal(a.fslot[l][:n], b.fslot[l][:n])
+    for ta, tb in zip(a._tables(), b._tables()):
+        assert all(torch.equal(u, v) for u, v in zip(ta, tb)), f"{tag}: table"
+    se = a._tables()[1]
+    for l in range(a.cfg.layers):
+        occ = (se[l] >= 0).nonzero().flatten()
+        assert torch.equal(a.cache[l][occ], b.cache[l][occ]), f"{tag} layer {l}: cache"
+
+
+def test_route_fetch_equals_route_resolve_then_fetch(lib, dev):
+    import decode
+    base = dict(layers=3, capacity=20, drift_every=3, schedule_steps=12)
+    fused = decode.DecodeHarness(decode.DecodeConfig(**base), dev)
+    plain = decode.DecodeHarness(decode.DecodeConfig(**base, fused_fetch=False), dev,
+                                 pools=fused.pools)
+    assert fused.fused and not plain.fused
+    for s in range(7):
+        for h in (fused, plain):
+            h.stage(s)
+            h.step_eager()
+        torch.cuda.synchronize(dev)
+        say(f"route_fetch: eager step {s}")
+        _same(fused, plain, f"eager {s}")
+    hits, misses = fused.hit_rate()
+    assert hits > 0 and misses > 0
+    for h in (fused, plain):
+        h.capture()
+    for s in range(9):
+        for h in (fused, plain):
+            h.replay(1)
+        torch.cuda.synchronize(dev)
+        say(f"route_fetch: replay {s}")
+        _same(fused, plain, f"replay {s}")
+    plain.pools = []                     # owned by the fused harness
+    fused.close()
+
+
+def test_route_fetch_preconditions(lib, dev):
+    import hipfetch
+    E, C, K, H = 256, 16, 8, 256
+    i32 = dict(dtype=torch.int32, device=dev)
+    x = torch.zeros((1, H), dtype=torch.bfloat16, device=dev)
+    w = torch.zeros((E, H), dtype=torch.bfloat16, device=dev)
+    logits = torch.zeros(E, device=dev)
+    ids, out_slot, fs, fe = (torch.zeros(K, **i32) for _ in range(4))
+    wts = torch.zeros(K, device=dev)
+    nm = torch.zeros(1, **i32)
+    step = torch.zeros(1, dtype=torch.int64, device=dev)
+    single = (torch.zeros(E, **i32), torch.zeros(C, **i32), torch.zeros(C, dtype=torch.int64, device=dev))
+    pair = [(16, 16, 4096)]
+    with pytest.raises(ValueError, match="double-buffered"):
+        lib.route_fetch(x, w, None, K, logits, ids, wts, *single, step, out_slot, fs, fe, nm, pair, 3)
+    so = torch.zeros((2, E), **i32)
+    se = torch.zeros((2, 4), **i32)
+    st = torch.zeros((2, 4), dtype=torch.int64, device=dev)
+    with pytest.raises(hipfetch.NativeError, match="exceeds the cache capacity"):
+        lib.route_fetch(x, w, None, K, logits, ids, wts, so, se, st, step, out_slot, fs, fe, nm,
+                        pair, 3)
