@@ -794,12 +794,12 @@ def fetch_lists(lib, pools, dev, lengths=(8, 32, 64, 256), slots: int = 128, tri
                                  torch.tensor(part, dtype=torch.int32, device=dev),
                                  torch.tensor([len(part)], dtype=torch.int32, device=dev)))
         p0, i0, n0 = launches[0]
-        lib.fetch([p0.fetch_pair(cache)], i0, fslot, n0, slots, 2)
+        lib.fetch([p0.fetch_pair(cache)], i0, fslot, n0, i0.numel(), 2)
         torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
         for pool, ids_t, n_t in launches:
-            lib.fetch([pool.fetch_pair(cache)], ids_t, fslot, n_t, slots, 2)
+            lib.fetch([pool.fetch_pair(cache)], ids_t, fslot, n_t, ids_t.numel(), 2)
         b.record()
         torch.cuda.synchronize()
         dt = a.elapsed_time(b) / 1000.0

@@ -176,8 +176,56 @@ class Native:
     @staticmethod
     def _dtype_code(t) -> int:
         import torch
-        return {torch.int32: MOE_I32, torch.int64: MOE_I64, torch.float32: MOE_F32,
-                torch.bfloat16: MOE_BF16}[t.dtype]
+        codes = {torch.int32: MOE_I32, torch.int64: MOE_I64, torch.float32: MOE_F32,
+                 torch.bfloat16: MOE_BF16}
+        if t.dtype not in codes:
+            raise ValueError(f"no library dtype code for {t.dtype}")
+        return codes[t.dtype]
+
+    @staticmethod
+    def _buf(what: str, name: str, t, n: int, *dtypes) -> None:
+        """Buffer `name` of `what` (None allowed) must be a contiguous tensor
+        of at least n elements of one of `dtypes`.  The kernels index it by
+        the sizes passed beside it, so a shorter or differently typed buffer
+        would be read or written past its end on the device."""
+        if t is None:
+            return
+        if dtypes and t.dtype not in dtypes:
+            want = " or ".join(str(d).replace("torch.", "") for d in dtypes)
+            raise ValueError(f"{what}: {name} must be {want}, got "
+                             f"{str(t.dtype).replace('torch.', '')}")
+        if not t.is_contiguous():
+            raise ValueError(f"{what}: {name} must be contiguous")
+        if t.numel() < n:
+            raise ValueError(f"{what}: {name} holds {t.numel()} elements, needs {n}")
+
+    def _slot_bufs(self, what, slot_of, n_experts, slot_expert, stamp, step, out_slot, k,
+                   fetch_slot, fetch_expert, nmiss, stats) -> None:
+        """The slot table and the per-call outputs of the resolve kernels."""
+        import torch
+        i32, i64 = torch.int32, torch.int64
+        cap = slot_expert.numel()
+        for name, t, n, dt in (("slot_of", slot_of, n_experts, i32),
+                               ("slot_expert", slot_expert, cap, i32),
+                               ("stamp", stamp, cap, i64), ("step", step, 1, i64),
+                               ("out_slot", out_slot, k, i32),
+                               ("fetch_slot", fetch_slot, k, i32),
+                               ("fetch_expert", fetch_expert, k, i32),
+                               ("nmiss", nmiss, 1, i32), ("stats", stats, 2, i64)):
+            self._buf(what, name, t, n, dt)
+
+    def _router_bufs(self, what, x, w, bias, logits, tokens, top_k) -> tuple[int, int]:
+        """x [tokens, H] and w [E, H] bf16, bias f32 [E], logits f32
+        [tokens, E]; returns (H, E)."""
+        import torch
+        if x.dim() != 2 or w.dim() != 2 or x.shape[1] != w.shape[1]:
+            raise ValueError(f"{what}: x [T, H] and w [E, H] must share H")
+        H, E = x.shape[1], w.shape[0]
+        self._buf(what, "x", x, x.numel(), torch.bfloat16)
+        self._buf(what, "w", w, w.numel(), torch.bfloat16)
+        self._buf(what, "bias", bias, E, torch.float32)
+        self._buf(what, "logits", logits, tokens * E, torch.float32)
+        return H, E
 
     def version(self) -> str:
         return self.cdll.moe_version().decode()
@@ -212,6 +260,12 @@ class Native:
 
     # ------------------------------------------------------------ slots
     def slots_init(self, slot_of, slot_expert, stamp, step) -> None:
+        import torch
+        self._on_gpu("moe_slots_init", slot_of, slot_expert, stamp, step)
+        self._buf("moe_slots_init", "slot_of", slot_of, 1, torch.int32)
+        self._buf("moe_slots_init", "slot_expert", slot_expert, 1, torch.int32)
+        self._buf("moe_slots_init", "stamp", stamp, slot_expert.numel(), torch.int64)
+        self._buf("moe_slots_init", "step", step, 1, torch.int64)
         self._check(self.cdll.moe_slots_init(slot_of.data_ptr(), slot_of.numel(),
                                              slot_expert.data_ptr(), stamp.data_ptr(),
                                              slot_expert.numel(), step.data_ptr(), self.stream()),
@@ -219,8 +273,12 @@ class Native:
 
     def resolve_slots(self, ids, slot_of, slot_expert, stamp, step, out_slot, fetch_slot,
                       fetch_expert, nmiss, stats=None) -> None:
+        import torch
         self._on_gpu("moe_resolve_slots", ids, slot_of, slot_expert, stamp, step, out_slot,
                      fetch_slot, fetch_expert, nmiss, stats)
+        self._buf("moe_resolve_slots", "ids", ids, 1, torch.int32, torch.int64)
+        self._slot_bufs("moe_resolve_slots", slot_of, slot_of.numel(), slot_expert, stamp, step,
+                        out_slot, ids.numel(), fetch_slot, fetch_expert, nmiss, stats)
         self._check(self.cdll.moe_resolve_slots(
             ids.data_ptr(), self._dtype_code(ids), ids.numel(), slot_of.data_ptr(),
             slot_of.numel(), slot_expert.data_ptr(), stamp.data_ptr(), slot_expert.numel(),
@@ -234,7 +292,11 @@ class Native:
 
         tile_k = K > 0 writes each record, a row-major [rows, K] e4m3 matrix on
         the host, to the cache in MFMA tile order; 0 (the default) copies bytes."""
+        import torch
         self._on_gpu("moe_fetch", fetch_expert, fetch_slot, nmiss)
+        self._buf("moe_fetch", "fetch_expert", fetch_expert, max_jobs, torch.int32)
+        self._buf("moe_fetch", "fetch_slot", fetch_slot, max_jobs, torch.int32)
+        self._buf("moe_fetch", "nmiss", nmiss, 1, torch.int32)
         arr = (FetchPair * len(pairs))(*[FetchPair(*((tuple(p) + (0,))[:4])) for p in pairs])
         self._check(self.cdll.moe_fetch(arr, len(pairs), fetch_expert.data_ptr(),
                                         fetch_slot.data_ptr(), nmiss.data_ptr(), max_jobs,
@@ -252,9 +314,12 @@ class Native:
                     logit_dtype: str = "bf16") -> None:
         """logits = x . W^T rounded to logit_dtype ('bf16': the bf16 gate's
         output, or 'f32'), + bias; top-k, softmax over the picks."""
+        import torch
         self._on_gpu("moe_router_topk", x, w, bias, logits, ids, weights)
-        T, H = x.shape
-        E = w.shape[0]
+        T = x.shape[0]
+        H, E = self._router_bufs("moe_router_topk", x, w, bias, logits, T, top_k)
+        self._buf("moe_router_topk", "ids", ids, T * top_k, torch.int32, torch.int64)
+        self._buf("moe_router_topk", "weights", weights, T * top_k, torch.float32, torch.bfloat16)
         self._check(self.cdll.moe_router_topk(
             x.data_ptr(), w.data_ptr(), self._ptr(bias), self._logit_code(logit_dtype), T, H, E,
             top_k, logits.data_ptr(),
@@ -267,10 +332,14 @@ class Native:
         """Router + slot resolve of one token (ids int32, weights float32)."""
         if x.shape[0] != 1:
             raise ValueError("route_resolve takes exactly one token")
+        import torch
         self._on_gpu("moe_route_resolve", x, w, bias, logits, ids, weights, slot_of, slot_expert,
                      stamp, step, out_slot, fetch_slot, fetch_expert, nmiss, stats)
-        H = x.shape[1]
-        E = w.shape[0]
+        H, E = self._router_bufs("moe_route_resolve", x, w, bias, logits, 1, top_k)
+        self._buf("moe_route_resolve", "ids", ids, top_k, torch.int32)
+        self._buf("moe_route_resolve", "weights", weights, top_k, torch.float32)
+        self._slot_bufs("moe_route_resolve", slot_of, E, slot_expert, stamp, step, out_slot,
+                        top_k, fetch_slot, fetch_expert, nmiss, stats)
         self._check(self.cdll.moe_route_resolve(
             x.data_ptr(), w.data_ptr(), self._ptr(bias), self._logit_code(logit_dtype), H, E,
             top_k, logits.data_ptr(),
@@ -292,12 +361,16 @@ class Native:
                 or slot_expert.shape[0] != 2 or tuple(stamp.shape) != tuple(slot_expert.shape):
             raise ValueError("route_fetch takes double-buffered tables: slot_of [2, E], "
                              "slot_expert and stamp [2, C]")
+        import torch
         self._on_gpu("moe_route_fetch", x, w, bias, logits, ids, weights, slot_of, slot_expert,
                      stamp, step, out_slot, fetch_slot, fetch_expert, nmiss, stats)
-        H = x.shape[1]
-        E = w.shape[0]
+        H, E = self._router_bufs("moe_route_fetch", x, w, bias, logits, 1, top_k)
         if slot_of.shape[1] != E:
             raise ValueError(f"slot_of [2, {slot_of.shape[1]}] does not match {E} experts")
+        self._buf("moe_route_fetch", "ids", ids, top_k, torch.int32)
+        self._buf("moe_route_fetch", "weights", weights, top_k, torch.float32)
+        self._slot_bufs("moe_route_fetch", slot_of, 2 * E, slot_expert, stamp, step, out_slot,
+                        top_k, fetch_slot, fetch_expert, nmiss, stats)
         arr = (FetchPair * len(pairs))(*[FetchPair(*((tuple(p) + (0,))[:4])) for p in pairs])
         self._check(self.cdll.moe_route_fetch(
             x.data_ptr(), w.data_ptr(), self._ptr(bias), self._logit_code(logit_dtype), H, E,
@@ -378,8 +451,13 @@ class Native:
 
     # ------------------------------------------------------------ permute
     def permute(self, ids, n_experts: int, counts, offsets, sorted_pairs, pair_pos) -> None:
+        import torch
         self._on_gpu("moe_permute", ids, counts, offsets, sorted_pairs, pair_pos)
         T, K = ids.shape
+        self._buf("moe_permute", "ids", ids, T * K, torch.int32, torch.int64)
+        for name, t, n in (("counts", counts, n_experts), ("offsets", offsets, n_experts + 1),
+                           ("sorted_pairs", sorted_pairs, T * K), ("pair_pos", pair_pos, T * K)):
+            self._buf("moe_permute", name, t, n, torch.int32)
         self._check(self.cdll.moe_permute(ids.data_ptr(), self._dtype_code(ids), T, K, n_experts,
                                           counts.data_ptr(), offsets.data_ptr(),
                                           sorted_pairs.data_ptr(), pair_pos.data_ptr(),
@@ -387,8 +465,14 @@ class Native:
 
     def unique_inverse(self, ids, n_experts: int, counts, n_unique, uniq, rank_of,
                        inverse) -> None:
+        import torch
         self._on_gpu("moe_unique_inverse", ids, counts, n_unique, uniq, rank_of, inverse)
         T, K = ids.shape
+        self._buf("moe_unique_inverse", "ids", ids, T * K, torch.int32, torch.int64)
+        for name, t, n in (("counts", counts, n_experts), ("n_unique", n_unique, 1),
+                           ("uniq", uniq, n_experts), ("rank_of", rank_of, n_experts),
+                           ("inverse", inverse, T * K)):
+            self._buf("moe_unique_inverse", name, t, n, torch.int32)
         self._check(self.cdll.moe_unique_inverse(
             ids.data_ptr(), self._dtype_code(ids), T, K, n_experts, counts.data_ptr(),
             n_unique.data_ptr(), uniq.data_ptr(), rank_of.data_ptr(), inverse.data_ptr(),
@@ -396,8 +480,17 @@ class Native:
 
     def gather_plan(self, uniq, n_unique, slot_of, cap: int, host_expert, host_dst, n_host,
                     cache_src, cache_dst, n_cache, stats=None) -> None:
+        import torch
         self._on_gpu("moe_gather_plan", uniq, n_unique, slot_of, host_expert, host_dst, n_host,
                      cache_src, cache_dst, n_cache, stats)
+        E = uniq.numel()
+        for name, t, n in (("uniq", uniq, E), ("n_unique", n_unique, 1),
+                           ("slot_of", slot_of, E if cap > 0 else 0),
+                           ("host_expert", host_expert, E), ("host_dst", host_dst, E),
+                           ("n_host", n_host, 1), ("cache_src", cache_src, E),
+                           ("cache_dst", cache_dst, E), ("n_cache", n_cache, 1)):
+            self._buf("moe_gather_plan", name, t, n, torch.int32)
+        self._buf("moe_gather_plan", "stats", stats, 2, torch.int64)
         self._check(self.cdll.moe_gather_plan(
             uniq.data_ptr(), n_unique.data_ptr(), self._ptr(slot_of), uniq.numel(), cap,
             host_expert.data_ptr(), host_dst.data_ptr(), n_host.data_ptr(), cache_src.data_ptr(),
@@ -435,7 +528,10 @@ class Native:
 
     def all_finite(self, x, flag) -> None:
         """flag[0] (int32, device) = 1 if every element of x (f32 or bf16) is finite."""
+        import torch
         self._on_gpu("moe_all_finite", x, flag)
+        self._buf("moe_all_finite", "x", x, x.numel(), torch.float32, torch.bfloat16)
+        self._buf("moe_all_finite", "flag", flag, 1, torch.int32)
         self._check(self.cdll.moe_all_finite(x.data_ptr(), self._dtype_code(x), x.numel(),
                                              flag.data_ptr(), self.stream()), "moe_all_finite")
 
@@ -443,6 +539,9 @@ class Native:
         """Add to mismatches[0] (int64, device) the bit patterns of
         [first, first + count) whose hardware e4m3 encoding differs from the
         software encoder's (moe_e4m3_check)."""
+        import torch
+        self._on_gpu("moe_e4m3_check", mismatches)
+        self._buf("moe_e4m3_check", "mismatches", mismatches, 1, torch.int64)
         self._check(self.cdll.moe_e4m3_check(first, count, mismatches.data_ptr(), self.stream()),
                     "moe_e4m3_check")
 
@@ -455,13 +554,16 @@ class Native:
         for t in (g, u, out):
             if t.dtype != torch.float32 or not t.is_contiguous():
                 raise ValueError("g, u and out must be contiguous float32")
+        self._on_gpu("moe_silu_check", g, u, out)
         self._check(self.cdll.moe_silu_check(g.data_ptr(), u.data_ptr(), out.data_ptr(),
                                              g.numel(), self.stream()), "moe_silu_check")
 
     def stream_read(self, src, nbytes: int, workgroups: int, sink, offset: int = 0) -> None:
         """Read nbytes of the device tensor src from byte `offset` once
         (moe_stream_read); sink: device uint32/int32 [>= 1]."""
+        import torch
         self._on_gpu("moe_stream_read", src, sink)
+        self._buf("moe_stream_read", "sink", sink, 1, torch.int32, torch.uint32)
         if offset < 0 or offset + nbytes > src.numel() * src.element_size():
             raise ValueError("stream_read range past the end of src")
         self._check(self.cdll.moe_stream_read(src.data_ptr() + offset, nbytes, workgroups,
@@ -508,6 +610,17 @@ class Native:
                     workgroups: int = 32) -> None:
         """Decode coded records fetch_expert[j] into cache slots fetch_slot[j],
         j < nmiss[0] (device tensors); cache uint8 [slots, >= record_bytes]."""
+        import torch
+        self._on_gpu("moe_fetch_coded", rec_off, blk_off, lut, fetch_expert, fetch_slot, nmiss,
+                     cache)
+        self._buf("moe_fetch_coded", "lut", lut, 4096, torch.uint16, torch.int16)
+        for name, t in (("fetch_expert", fetch_expert), ("fetch_slot", fetch_slot)):
+            self._buf("moe_fetch_coded", name, t, max_jobs, torch.int32)
+        self._buf("moe_fetch_coded", "nmiss", nmiss, 1, torch.int32)
+        if cache.dim() != 2 or cache.stride(1) != 1 or \
+                cache.shape[1] * cache.element_size() < record_bytes:
+            raise ValueError("moe_fetch_coded: cache must be [slots, >= record_bytes] with "
+                             "contiguous rows")
         self._check(self.cdll.moe_fetch_coded(
             pool_dev_ptr, rec_off.data_ptr(), blk_off.data_ptr(), record_bytes, fp8_bytes,
             lut.data_ptr(), fetch_expert.data_ptr(), fetch_slot.data_ptr(), nmiss.data_ptr(),
@@ -515,9 +628,14 @@ class Native:
             self.stream()), "moe_fetch_coded")
 
     def unpermute(self, y, pair_pos, weights, out) -> None:
+        import torch
         self._on_gpu("moe_unpermute", y, pair_pos, weights, out)
         T, K = weights.shape
         H = y.shape[-1]
+        self._buf("moe_unpermute", "y", y, T * K * H, torch.float32)
+        self._buf("moe_unpermute", "pair_pos", pair_pos, T * K, torch.int32)
+        self._buf("moe_unpermute", "weights", weights, T * K, torch.float32, torch.bfloat16)
+        self._buf("moe_unpermute", "out", out, T * H, torch.bfloat16)
         self._check(self.cdll.moe_unpermute(y.data_ptr(), pair_pos.data_ptr(),
                                             weights.data_ptr(), self._dtype_code(weights), T, K,
                                             H, out.data_ptr(), self.stream()), "moe_unpermute")

@@ -446,7 +446,8 @@ int64_t moe_codec_encode(const void* records, int64_t n_records,
 int moe_codec_table(const uint8_t* code_lengths, uint16_t* lut);
 
 /* moe_fetch for a coded pool: job j < min(*nmiss, max_jobs) decodes coded
- * record fetch_expert[j] into cache slot fetch_slot[j] (slot_bytes apart).
+ * record fetch_expert[j] into cache slot fetch_slot[j] (slot_bytes apart);
+ * the lists hold max_jobs entries, as for moe_fetch.
  * pool: device address of the page-locked coded pool (256-byte aligned);
  * rec_offset, blk_offset, lut: device copies of moe_codec_encode's and
  * moe_codec_table's outputs.  Job lists are read on the device, so a

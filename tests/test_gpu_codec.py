@@ -38,8 +38,11 @@ def test_coded_fetch_fills_slots_with_the_raw_records(lib, dev, H, I, n, workgro
             experts = rng.choice(n, jobs, replace=False)
             slots = rng.choice(C, jobs, replace=False)
             cache.fill_(0xAB)
-            fe = torch.tensor(experts, dtype=torch.int32, device=dev)
-            fs = torch.tensor(slots, dtype=torch.int32, device=dev)
+            # lists of max_jobs entries, the tail past the jobs never read
+            fe = torch.full((8,), -1, dtype=torch.int32, device=dev)
+            fs = torch.full((8,), -1, dtype=torch.int32, device=dev)
+            fe[:jobs] = torch.tensor(experts, dtype=torch.int32)
+            fs[:jobs] = torch.tensor(slots, dtype=torch.int32)
             nm = torch.tensor([jobs], dtype=torch.int32, device=dev)
             pool.fetch(cache, fe, fs, nm, max_jobs=8, workgroups=workgroups)
             torch.cuda.synchronize()

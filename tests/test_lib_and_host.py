@@ -225,6 +225,89 @@ def test_wrappers_refuse_host_tensors(lib):
                         torch.zeros((1, 8)))
 
 
+def test_wrappers_check_buffer_sizes_and_dtypes(lib, monkeypatch):
+    # The kernels index the table, list and output buffers by the sizes
+    # passed beside them: a short, strided or differently typed buffer is
+    # refused before anything reaches the library, and a well-formed call
+    # gets through (the stand-in library below raises when called).
+    class NoCall:
+        def __getattr__(self, name):
+            def f(*a):
+                raise AssertionError(f"{name} reached")
+            return f
+    monkeypatch.setattr(lib, "_on_gpu", lambda *a: None)
+    monkeypatch.setattr(lib, "cdll", NoCall())
+    monkeypatch.setattr(lib, "stream", lambda: 0)
+    i32 = lambda *n: torch.zeros(n, dtype=torch.int32)
+    i64 = lambda *n: torch.zeros(n, dtype=torch.int64)
+    E, C, K, H = 256, 64, 8, 2048
+
+    def resolve(**over):
+        a = dict(ids=i32(K), slot_of=i32(E), slot_expert=i32(C), stamp=i64(C), step=i64(1),
+                 out_slot=i32(K), fetch_slot=i32(K), fetch_expert=i32(K), nmiss=i32(1),
+                 stats=i64(2))
+        a.update(over)
+        lib.resolve_slots(**a)
+    with pytest.raises(AssertionError, match="moe_resolve_slots reached"):
+        resolve()
+    for over, msg in ((dict(stamp=i32(C)), "stamp must be int64"),
+                      (dict(stamp=i64(C - 1)), "stamp holds 63 elements, needs 64"),
+                      (dict(out_slot=i32(K - 1)), "out_slot holds 7"),
+                      (dict(fetch_expert=i64(K)), "fetch_expert must be int32"),
+                      (dict(nmiss=i32(0)), "nmiss holds 0"),
+                      (dict(stats=i64(1)), "stats holds 1"),
+                      (dict(ids=torch.zeros(K)), "ids must be int32 or int64"),
+                      (dict(slot_of=i32(2 * E)[::2]), "slot_of must be contiguous")):
+        with pytest.raises(ValueError, match=msg):
+            resolve(**over)
+
+    with pytest.raises(ValueError, match="fetch_slot holds 4 elements, needs 8"):
+        lib.fetch([(16, 16, 256)], i32(8), i32(4), i32(1), max_jobs=8, blocks_per_job=3)
+    with pytest.raises(ValueError, match="moe_slots_init: stamp holds"):
+        lib.slots_init(i32(E), i32(C), i64(C - 1), i64(1))
+
+    x, w = torch.zeros((1, H), dtype=torch.bfloat16), torch.zeros((E, H), dtype=torch.bfloat16)
+
+    def topk(**over):
+        a = dict(x=x, w=w, bias=None, top_k=K, logits=torch.zeros(1, E), ids=i32(1, K),
+                 weights=torch.zeros(1, K))
+        a.update(over)
+        lib.router_topk(**a)
+    with pytest.raises(AssertionError, match="moe_router_topk reached"):
+        topk()
+    for over, msg in ((dict(logits=torch.zeros(E - 1)), "logits holds 255"),
+                      (dict(x=x.float()), "x must be bfloat16"),
+                      (dict(w=torch.zeros((E, H + 8), dtype=torch.bfloat16)), "share H"),
+                      (dict(bias=torch.zeros(E, dtype=torch.bfloat16)), "bias must be float32"),
+                      (dict(ids=i32(1, K - 1)), "ids holds 7"),
+                      (dict(weights=torch.zeros(1, K, dtype=torch.float64)), "weights must be")):
+        with pytest.raises(ValueError, match=msg):
+            topk(**over)
+
+    def route_fetch(**over):
+        a = dict(x=x, w=w, bias=None, top_k=K, logits=torch.zeros(E), ids=i32(K),
+                 weights=torch.zeros(K), slot_of=i32(2, E), slot_expert=i32(2, C),
+                 stamp=i64(2, C), step=i64(1), out_slot=i32(K), fetch_slot=i32(K),
+                 fetch_expert=i32(K), nmiss=i32(1), pairs=[(16, 16, 4096)], blocks_per_job=3)
+        a.update(over)
+        lib.route_fetch(**a)
+    with pytest.raises(AssertionError, match="moe_route_fetch reached"):
+        route_fetch()
+    for over, msg in ((dict(ids=i64(K)), "ids must be int32"),
+                      (dict(stamp=i32(2, C)), "stamp must be int64"),
+                      (dict(fetch_slot=i32(K - 2)), "fetch_slot holds 6"),
+                      (dict(stats=i32(2)), "stats must be int64")):
+        with pytest.raises(ValueError, match=msg):
+            route_fetch(**over)
+
+    with pytest.raises(ValueError, match="offsets holds 256 elements, needs 257"):
+        lib.permute(i32(4, K), E, i32(E), i32(E), i32(4 * K), i32(4 * K))
+    with pytest.raises(ValueError, match="out must be bfloat16"):
+        lib.unpermute(torch.zeros(4 * K, H), i32(4 * K), torch.zeros(4, K), torch.zeros(4, H))
+    with pytest.raises(ValueError, match="uniq holds"):
+        lib.unique_inverse(i32(4, K), E, i32(E), i32(1), i32(E - 1), i32(E), i32(4 * K))
+
+
 def test_moe_experts_surface():
     import moe
     m = moe.MoEExperts(4, 256, 128)
