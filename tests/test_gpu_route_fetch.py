@@ -1,6 +1,7 @@
 """moe_route_fetch, the decode step's router + resolve + fetch in two
 launches, against moe_route_resolve followed by moe_fetch (three launches),
-at Drama-3 shape (256 experts, top-8, H 2048, I 512) over 3 layers and
+at Drama-3 shape (256 experts, top-8, H 2048, I 512) and two others (320
+experts, top-12, 272 slots; 64 experts, top-4, 5 slots) over 3 layers and
 popularity drifts: two harnesses on the same pools, one per path, step for
 step, eager and then replayed from their graphs.  Step outputs, router
 outputs, slot decisions, miss queues, hit/miss counters, the current slot
@@ -35,9 +36,17 @@ def _same(a, b, tag):
         assert torch.equal(a.cache[l][occ], b.cache[l][occ]), f"{tag} layer {l}: cache"
 
 
-def test_route_fetch_equals_route_resolve_then_fetch(lib, dev):
+@pytest.mark.parametrize("shape", [
+    dict(capacity=20),
+    # more jobs than the grid's 8 (each workgroup loops over jobs), the
+    # 16-per-lane expert and slot registers (E, cap > 256), 2 workgroups per job
+    dict(n_experts=320, top_k=12, hidden=512, inter=256, capacity=272, blocks_per_job=2),
+    # a cache one slot above top_k: evictions on almost every step, 1 workgroup per job
+    dict(n_experts=64, top_k=4, hidden=256, inter=128, capacity=5, blocks_per_job=1),
+], ids=["drama3", "wide", "tight"])
+def test_route_fetch_equals_route_resolve_then_fetch(lib, dev, shape):
     import decode
-    base = dict(layers=3, capacity=20, drift_every=3, schedule_steps=12)
+    base = dict(layers=3, drift_every=3, schedule_steps=12, **shape)
     fused = decode.DecodeHarness(decode.DecodeConfig(**base), dev)
     plain = decode.DecodeHarness(decode.DecodeConfig(**base, fused_fetch=False), dev,
                                  pools=fused.pools)
@@ -47,7 +56,7 @@ def test_route_fetch_equals_route_resolve_then_fetch(lib, dev):
             h.stage(s)
             h.step_eager()
         torch.cuda.synchronize(dev)
-        say(f"route_fetch: eager step {s}")
+        say(f"route_fetch {shape}: eager step {s}")
         _same(fused, plain, f"eager {s}")
     hits, misses = fused.hit_rate()
     assert hits > 0 and misses > 0
