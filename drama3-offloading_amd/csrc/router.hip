@@ -90,13 +90,14 @@ __global__ __launch_bounds__(64 * kLogitWaves) void router_logits_kernel(
   constexpr int U = 4;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  // the route + fetch launch that follows reads the slot-table step already
-  // counted, so that none of its workgroups writes what another one reads
-  if (step_inc && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *step_inc += 1;
-  const int e = blockIdx.x * kLogitWaves + wave;
+  // No early exit for a wave past the last expert (it computes the last
+  // expert's logit again and stores nothing): a branch on n_experts would
+  // wait for that argument before the other arguments are even requested.
+  const int e_raw = blockIdx.x * kLogitWaves + wave;
+  const bool live = e_raw < n_experts;
+  const int e = live ? e_raw : n_experts - 1;
   const int t0 = blockIdx.y * TB;
   const int nt = min(TB, tokens - t0);
-  if (e >= n_experts) return;
   const int nv = hidden >> 3;                 // 16-byte vectors per row
   const uint4* wr = reinterpret_cast<const uint4*>(w + static_cast<int64_t>(e) * hidden);
   const uint4* xr[TB];
@@ -106,8 +107,10 @@ __global__ __launch_bounds__(64 * kLogitWaves) void router_logits_kernel(
   double acc[TB];
 #pragma unroll
   for (int tt = 0; tt < TB; ++tt) acc[tt] = 0.0;
-  for (int i0 = 0; i0 < nv; i0 += 64 * U) {
-    uint4 b[U], a[TB][U];
+  uint4 b[U], a[TB][U];
+  // chunk i0 of the row: 64 * U vectors, every lane's loads issued together
+  // (lanes past the end re-read the last vector)
+  auto load_chunk = [&](int i0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int i = i0 + 64 * u + lane;
@@ -116,9 +119,15 @@ __global__ __launch_bounds__(64 * kLogitWaves) void router_logits_kernel(
 #pragma unroll
       for (int tt = 0; tt < TB; ++tt) a[tt][u] = xr[tt][ic];
     }
+  };
+  // Lanes past the end add +0.0, which leaves a partial sum as it is (a sum
+  // that starts at +0.0 never becomes -0.0).  No branch: under a lane
+  // condition the compiler moved a chunk's first loads into the branch and
+  // waited for each there.
+  auto add_chunk = [&](int i0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      if (i0 + 64 * u + lane >= nv) continue;
+      const bool in = i0 + 64 * u + lane < nv;
       const uint32_t bv[4] = {b[u].x, b[u].y, b[u].z, b[u].w};
 #pragma unroll
       for (int tt = 0; tt < TB; ++tt) {
@@ -127,21 +136,42 @@ __global__ __launch_bounds__(64 * kLogitWaves) void router_logits_kernel(
         for (int j = 0; j < 4; ++j) {
           const float a0 = __uint_as_float(av[j] << 16), a1 = __uint_as_float(av[j] & 0xffff0000u);
           const float b0 = __uint_as_float(bv[j] << 16), b1 = __uint_as_float(bv[j] & 0xffff0000u);
-          acc[tt] += static_cast<double>(a0 * b0);     // exact products
-          acc[tt] += static_cast<double>(a1 * b1);
+          acc[tt] += in ? static_cast<double>(a0 * b0) : 0.0;     // exact products
+          acc[tt] += in ? static_cast<double>(a1 * b1) : 0.0;
         }
       }
     }
+  };
+  // The first chunk (the whole row up to hidden 2048) outside any loop, so
+  // that no loop-carried wait holds its loads back; the bias goes out after
+  // them (from the first word of the gate row when there is none, read and
+  // ignored): loaded where it is added, it would put a memory round trip
+  // after the sum.
+  load_chunk(0);
+  __builtin_amdgcn_sched_barrier(0);
+  const float bias_raw = *(bias ? bias + e : reinterpret_cast<const float*>(wr));
+  __builtin_amdgcn_sched_barrier(0);
+  add_chunk(0);
+  for (int i0 = 64 * U; i0 < nv; i0 += 64 * U) {
+    load_chunk(i0);
+    add_chunk(i0);
   }
 #pragma unroll
   for (int tt = 0; tt < TB; ++tt) {
     const double s = wave_sum_f64_dpp(acc[tt]);
-    if (lane == 0 && tt < nt) {
+    if (lane == 0 && tt < nt && live) {
       float l = bf16_logits ? bf16_of_f64(s) : static_cast<float>(s);
-      if (bias) l += bias[e];
+      if (bias) l += bias_raw;
       logits[static_cast<int64_t>(t0 + tt) * n_experts + e] = l;
     }
   }
+  // The route + fetch launch that follows reads the slot-table step already
+  // counted, so that none of its workgroups writes what another one reads.
+  // An atomic add whose result is unused waits for nothing (a load and a
+  // store would add a memory round trip), and at the end it holds no
+  // argument loads back either.
+  if (step_inc && e_raw == 0 && blockIdx.y == 0 && lane == 0)
+    __hip_atomic_fetch_add(step_inc, int64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Order-preserving 32-bit key of a float logit: larger logit, larger key;
