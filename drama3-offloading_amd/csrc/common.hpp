@@ -101,6 +101,30 @@ __device__ __forceinline__ void silu_quantize8(const float4 (&hr)[4], bool live,
 }
 
 
+// 8 bf16 values of x held by one lane (16 bytes, elements i..i+7) -> e4m3
+// codes and the group scale in LDS.  Sixteen consecutive lanes form one
+// 128-column group; every lane of the wave calls this (the group maximum is
+// a cross-lane exchange), lanes past the end with live == false.
+__device__ __forceinline__ void quantize_x8(uint4 raw, bool live, int i,
+                                            uint8_t* __restrict__ xq, float* __restrict__ xs) {
+  const uint32_t rr[4] = {raw.x, raw.y, raw.z, raw.w};
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[2 * j] = __uint_as_float(rr[j] << 16);
+    v[2 * j + 1] = __uint_as_float(rr[j] & 0xffff0000u);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+  amax = row16_max_f32(amax);
+  if (live) {
+    const float sc = act_scale(amax);
+    *reinterpret_cast<uint2*>(xq + i) = make_uint2(quant4_e4m3(v, sc), quant4_e4m3(v + 4, sc));
+    if ((threadIdx.x & 15) == 0) xs[i >> 7] = sc;
+  }
+}
+
 // 8 float32 activations j..j+7 held by one lane -> e4m3 codes and the group
 // scale in LDS; 16 consecutive lanes form one 128-group.
 __device__ __forceinline__ void quantize8_f32(const float4 (&vr)[2], bool live, int j,

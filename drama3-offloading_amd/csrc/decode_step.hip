@@ -1,0 +1,393 @@
+// The decode step's MoE layer of one token from packed records in three
+// launches: the router's logits; the route (top-k + slot resolve), the
+// misses' fetch and the gate/up half of the expert FFN in one launch; the
+// down half.  The separate form is moe_route_fetch followed by
+// moe_fp8_moe_forward_ex (four launches); both give the same bytes.
+//
+// Records: w13 [2I, H] | w2 [H, I] in MFMA tile order | s13 [2I/128, H/128]
+// | s2 [H/128, I/128] f32, record_bytes apart in the host pool and in the
+// cache.  In tile order the 16 rows 16g..16g+15 of w13 are 16H contiguous
+// bytes, 2 KiB per 128-column K-block, each K-block holding the MFMA A
+// operands of a wave: lane 16q + r finds row r, columns 32q..32q+15 at
+// byte 16 * lane and columns 32q+16..32q+31 at 1024 + 16 * lane.
+//
+// The route + fetch + gate/up launch has two kinds of workgroups (128
+// threads each); all of them first make the route on their first wave
+// (route.hpp: the same decisions in every workgroup, workgroup 0 writing
+// the outputs and the next table buffer) while the second wave quantises x
+// into LDS.
+//   * fetch workgroups (the first nfetch): the misses' records, cut into
+//     units of 16 intermediate columns (the 16 gate rows and the 16 up rows
+//     of those columns, 2 * H/512 pieces of 8 KiB) and plain 8 KiB pieces
+//     (w2, the scales).  A unit's pieces go through one workgroup, which
+//     stores them to the cache slot as they arrive and runs the gate/up
+//     MFMAs on the bytes in its registers: the unit ends with the 16
+//     SiLU(gate) * up values of the miss's pick.  Units go round robin over
+//     the workgroups, and plain pieces fill the workgroups with one unit
+//     fewer first, so every workgroup moves the same bytes within a piece.
+//   * hit workgroups (top_k * I/16 of them, one per pick and unit): a hit's
+//     16 gate rows (first wave) and 16 up rows (second wave) from its cache
+//     slot; a pick that missed leaves its workgroup idle.
+// Every row sum is the in-order chain over its K-blocks of fma(block
+// product, weight scale * x scale, sum) that the gate/up GEMV kernel forms,
+// so the activations, and the down launch's output, are bit-identical to
+// the separate launches'.  The fetch's link time hides the hits' gate/up,
+// and the gate/up launch after the fetch goes away.
+#include "common.hpp"
+#include "fetch.hpp"
+#include "gemv.hpp"
+#include "resolve.hpp"
+#include "route.hpp"
+
+namespace moe {
+
+constexpr int kStepThreads = 128;
+constexpr int kPieceBytes = 8192;          // 128 threads x 4 x 16 bytes
+constexpr int kHitChunk = 16;              // K-blocks of a hit tile in flight per lane
+
+struct StepGeom {
+  const char* pool;        // device address of host record 0
+  char* cache;             // cache slot 0
+  int64_t rb;              // record bytes (pool and cache stride)
+  int64_t w13_bytes;       // 2 I H
+  int64_t off_s13;         // w13_bytes + H I
+  int32_t hidden, inter;
+  int32_t gb;              // K-blocks per row: H / 128
+  int32_t kq;              // pieces per 16-row group: H / 512
+  int32_t units;           // units per record: I / 16
+  int32_t plain;           // 8 KiB pieces from w13_bytes to the record's end
+  int32_t nfetch;          // fetch workgroups (the first of the grid)
+};
+
+__device__ __forceinline__ int32_t uniform(int32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+
+template <int PER, int PERC>
+__global__ __launch_bounds__(kStepThreads) void route_fetch_gateup_kernel(
+    StepGeom g, const uint16_t* __restrict__ x, const float* __restrict__ logits,
+    int32_t n_experts, int32_t top_k, int32_t* __restrict__ ids, float* __restrict__ weights,
+    int32_t* __restrict__ slot_of, int32_t* __restrict__ slot_expert,
+    int64_t* __restrict__ stamp, int32_t cap, const int64_t* __restrict__ step_ptr,
+    int32_t* __restrict__ out_slot, int32_t* __restrict__ fetch_slot,
+    int32_t* __restrict__ fetch_expert, int32_t* __restrict__ nmiss_ptr,
+    int64_t* __restrict__ stats, float* __restrict__ act) {
+  __shared__ __align__(16) uint8_t xq[kGemvMaxHidden];
+  __shared__ float xs[kGemvMaxHidden / 128];
+  __shared__ __align__(16) float dpart[2][kGemvMaxHidden / 128][16];
+  __shared__ __align__(16) float upsum[16];
+  __shared__ float swl[2][64];              // a unit's block scales, per wave
+  __shared__ int32_t job_e[kMaxTopK], job_s[kMaxTopK], job_k[kMaxTopK], job_n;
+  __shared__ int32_t pick_slot[kMaxTopK];   // a hit's slot, -1 for a miss
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int q = lane >> 4;
+  int32_t slot_r;
+  bool miss_r;
+  route_wave<PER, PERC>(logits, n_experts, top_k, ids, weights, slot_of, slot_expert, stamp, cap,
+                        step_ptr, out_slot, fetch_slot, fetch_expert, nmiss_ptr, stats, job_e,
+                        job_s, job_k, &job_n, slot_r, miss_r);
+  if (wave == 0 && lane < top_k) pick_slot[lane] = miss_r ? -1 : slot_r;
+  if (wave == 1) {
+    // x -> e4m3 codes + per-128 scales in LDS while the first wave routes:
+    // every chunk's load first (past the end: x[0] again, ignored)
+    constexpr int NC = kGemvMaxHidden / 512;
+    uint4 raw[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int i = c * 512 + lane * 8;
+      raw[c] = *reinterpret_cast<const uint4*>(x + (i < g.hidden ? i : 0));
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      if (c * 512 < g.hidden) quantize_x8(raw[c], c * 512 + lane * 8 < g.hidden, c * 512 + lane * 8, xq, xs);
+  }
+  __syncthreads();
+  const int I = g.inter;
+  if (static_cast<int>(blockIdx.x) >= g.nfetch) {
+    // hit workgroup (pick k, unit t): gate rows 16t.. (first wave), up rows
+    // I + 16t.. (second wave) from the pick's cache slot
+    const int hb = static_cast<int>(blockIdx.x) - g.nfetch;
+    const int k = hb / g.units;
+    const int t = hb - k * g.units;
+    if (k >= top_k) return;
+    const int32_t s = uniform(pick_slot[k]);
+    if (s < 0) return;                       // a miss: a fetch workgroup forms these rows
+    const char* rec = g.cache + s * g.rb;
+    const int gr = t + wave * g.units;       // the wave's 16-row group of w13
+    const uint8_t* base =
+        reinterpret_cast<const uint8_t*>(rec) + static_cast<int64_t>(gr) * 16 * g.hidden + lane * 16;
+    const float* srow = reinterpret_cast<const float*>(rec + g.off_s13) + (gr >> 3) * g.gb;
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    for (int b0 = 0; b0 < g.gb; b0 += kHitChunk) {
+      float sw[kHitChunk];
+      v8i a[kHitChunk];
+#pragma unroll
+      for (int c = 0; c < kHitChunk; ++c) sw[c] = srow[min(b0 + c, g.gb - 1)];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < kHitChunk; ++c) a[c] = load_op_nt(base + min(b0 + c, g.gb - 1) * 2048, 1024);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < kHitChunk; ++c) {
+        const int b = b0 + c;
+        if (b < g.gb) {
+          const v4f z = {0.f, 0.f, 0.f, 0.f};
+          const v4f d = mfma_e4m3_16x16x128(a[c], load_op32(xq + b * 128 + q * 32), z);
+          block_fma(acc, d, sw[c] * xs[b]);
+        }
+      }
+    }
+    // every lane of a row group stores its (identical) four up sums
+    if (wave == 1) *reinterpret_cast<float4*>(&upsum[4 * q]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    __syncthreads();
+    if (wave == 0 && (lane & 15) == 0) {
+      const float4 u = *reinterpret_cast<const float4*>(&upsum[4 * q]);
+      *reinterpret_cast<float4*>(act + static_cast<int64_t>(k) * I + 16 * t + 4 * q) =
+          make_float4(silu_mul(acc[0], u.x), silu_mul(acc[1], u.y), silu_mul(acc[2], u.z),
+                      silu_mul(acc[3], u.w));
+    }
+    return;
+  }
+
+  // fetch workgroup b of G.  Its work is one sequence of 8 KiB pieces:
+  // its units' pieces, unit after unit, then its plain pieces.  Units go
+  // round robin (u = b, b + G, ...); plain pieces go first 8 to each
+  // workgroup with one unit fewer (b >= r, r = U % G), then round robin.
+  const int nm = uniform(job_n);
+  const int G = g.nfetch;
+  const int b = static_cast<int>(blockIdx.x);
+  const int U = nm * g.units;
+  const int P = nm * g.plain;
+  const int r = U % G;
+  const int A = r > 0 ? min(P, 8 * (G - r)) : 0;
+  const int np = 2 * g.kq;                   // pieces per unit (even)
+  const int nu = U > b ? (U - 1 - b) / G + 1 : 0;
+  const int na = (r > 0 && b >= r && A > b - r) ? (A - 1 - (b - r)) / (G - r) + 1 : 0;
+  const int nb = P > A + b ? (P - 1 - A - b) / G + 1 : 0;
+  const int64_t plain_units = (g.rb - g.w13_bytes) >> 4;   // 16-byte units after w13
+  // One piece in flight per workgroup, as in the fetch kernel: the next
+  // piece's loads go out once this piece has arrived and its stores are
+  // issued, before its MFMAs (and a unit's fold), into the other of two
+  // register buffers (a copy between them would wait for the loads just
+  // issued).  Issuing them before this piece had arrived (two in flight)
+  // made the step 1.3 % slower on MI355X: more outstanding host reads lower
+  // the link's rate.
+  u32x4 va[4], vb[4];
+
+  // ---- unit pieces: unit u = b + ui * G, pieces p = 0 .. np - 1 (np even,
+  // so piece p always lands in buffer p & 1 and a unit's first piece in va)
+  auto unit_off = [&](int ui, int p, int& j, int& t) -> int64_t {
+    const int u = b + ui * G;
+    j = u / g.units;
+    t = u - j * g.units;
+    const int tw = p / g.kq;
+    const int q4 = p - tw * g.kq;
+    return static_cast<int64_t>(t + tw * g.units) * 16 * g.hidden +
+           static_cast<int64_t>(q4) * kPieceBytes + wave * 4096 + lane * 16;
+  };
+  // live == false: the same offsets in the device cache, read and ignored.
+  // Every load is issued unconditionally: behind a branch, the compiler's
+  // wait for the previous piece at the join also covered these loads.
+  auto unit_load = [&](int ui, int p, u32x4 (&v)[4], bool live) {
+    int j, t;
+    const int64_t o = unit_off(ui, p, j, t);
+    const char* src = live ? g.pool + uniform(job_e[min(j, nm - 1)]) * g.rb : g.cache;
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+      v[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + o + h * 1024));
+  };
+  auto unit_store = [&](int ui, int p, const u32x4 (&v)[4]) {
+    int j, t;
+    const int64_t o = unit_off(ui, p, j, t);
+    char* dst = g.cache + uniform(job_s[j]) * g.rb;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) *reinterpret_cast<u32x4*>(dst + o + h * 1024) = v[h];
+  };
+  auto unit_mfma = [&](int p, const u32x4 (&v)[4]) {
+    const int tw = p / g.kq;
+    const int q4 = p - tw * g.kq;
+#pragma unroll
+    for (int bl = 0; bl < 2; ++bl) {
+      const int gbk = 4 * q4 + 2 * wave + bl;
+      const v8i a = {(int)v[2 * bl].x, (int)v[2 * bl].y, (int)v[2 * bl].z, (int)v[2 * bl].w,
+                     (int)v[2 * bl + 1].x, (int)v[2 * bl + 1].y, (int)v[2 * bl + 1].z,
+                     (int)v[2 * bl + 1].w};
+      const v4f z = {0.f, 0.f, 0.f, 0.f};
+      const v4f d = mfma_e4m3_16x16x128(a, load_op32(xq + gbk * 128 + q * 32), z);
+      // every lane stores: the 16 lanes of a row group hold the same values
+      *reinterpret_cast<float4*>(&dpart[tw][gbk][4 * q]) = make_float4(d[0], d[1], d[2], d[3]);
+    }
+  };
+  if (nu > 0) unit_load(0, 0, va, true);
+  for (int ui = 0; ui < nu; ++ui) {
+    int j, t;
+    unit_off(ui, 0, j, t);
+    // the unit's block scales of this wave's row group (lane c: K-block c),
+    // from the host record, for the fold at the unit's end
+    const int grw = t + wave * g.units;
+    const float sw = reinterpret_cast<const float*>(g.pool + uniform(job_e[j]) * g.rb +
+                                                    g.off_s13)[(grw >> 3) * g.gb +
+                                                               min(lane, g.gb - 1)];
+    for (int p = 0; p < np; p += 2) {
+      unit_store(ui, p, va);
+      unit_load(ui, p + 1, vb, true);
+      unit_mfma(p, va);
+      unit_store(ui, p + 1, vb);
+      // the unit's next piece, else the next unit's first
+      const bool in_unit = p + 2 < np;
+      unit_load(in_unit ? ui : ui + 1, in_unit ? p + 2 : 0, va, in_unit || ui + 1 < nu);
+      unit_mfma(p + 1, vb);
+      if (p == 0) {
+        // the scales arrived before the second piece (loads complete in
+        // order): parked in LDS here, where no wait is added; read in the
+        // fold below, a wait there covers every load in flight
+        swl[wave][lane] = sw;
+      }
+    }
+    // wave w folds tile w (gate, up) in K order
+    __syncthreads();
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    for (int gbk = 0; gbk < g.gb; ++gbk) {
+      const float4 d = *reinterpret_cast<const float4*>(&dpart[wave][gbk][4 * q]);
+      const v4f dv = {d.x, d.y, d.z, d.w};
+      block_fma(acc, dv, swl[wave][gbk] * xs[gbk]);
+    }
+    if (wave == 1)
+      *reinterpret_cast<float4*>(&upsum[4 * q]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    __syncthreads();
+    if (wave == 0 && (lane & 15) == 0) {
+      const int kk = uniform(job_k[j]);
+      const float4 uu = *reinterpret_cast<const float4*>(&upsum[4 * q]);
+      *reinterpret_cast<float4*>(act + static_cast<int64_t>(kk) * I + 16 * t + 4 * q) =
+          make_float4(silu_mul(acc[0], uu.x), silu_mul(acc[1], uu.y), silu_mul(acc[2], uu.z),
+                      silu_mul(acc[3], uu.w));
+    }
+  }
+
+  // ---- plain pieces: the workgroup's n-th is global plain piece gi, of job
+  // gi / plain; 16-byte unit m * 512 + thread + 128 h after w13, the last
+  // unit again past the record's end (read, never stored)
+  const int npl = na + nb;
+  auto plain_gi = [&](int n) { return n < na ? (b - r) + n * (G - r) : A + b + (n - na) * G; };
+  auto plain_load = [&](int n, u32x4 (&v)[4]) {
+    const int gi = plain_gi(n);
+    const int j = gi / g.plain;
+    const int m = gi - j * g.plain;
+    const char* src = g.pool + uniform(job_e[j]) * g.rb + g.w13_bytes;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int64_t uidx = min(static_cast<int64_t>(m) * (kPieceBytes / 16) + threadIdx.x +
+                                   h * kStepThreads,
+                               plain_units - 1);
+      v[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + uidx * 16));
+    }
+  };
+  auto plain_store = [&](int n, const u32x4 (&v)[4]) {
+    const int gi = plain_gi(n);
+    const int j = gi / g.plain;
+    const int m = gi - j * g.plain;
+    char* dst = g.cache + uniform(job_s[j]) * g.rb + g.w13_bytes;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int64_t uidx = static_cast<int64_t>(m) * (kPieceBytes / 16) + threadIdx.x +
+                           h * kStepThreads;
+      if (uidx < plain_units) *reinterpret_cast<u32x4*>(dst + uidx * 16) = v[h];
+    }
+  };
+  // (one piece in flight per workgroup, as in the fetch kernel: with no
+  // MFMAs between a piece's arrival and the next piece's loads, the
+  // fetch's grid keeps the link busy this way)
+  for (int n = 0; n < npl; ++n) {
+    plain_load(n, va);
+    plain_store(n, va);
+  }
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" int moe_route_fetch_ffn(const void* x, const void* w, const float* bias,
+                                   int32_t logit_dtype, int32_t hidden, int32_t n_experts,
+                                   int32_t top_k, float* logits, int32_t* ids, float* weights,
+                                   int32_t* slot_of, int32_t* slot_expert, int64_t* slot_stamp,
+                                   int32_t cap, int64_t* step, int32_t* out_slot,
+                                   int32_t* fetch_slot, int32_t* fetch_expert, int32_t* nmiss,
+                                   int64_t* stats, const void* pool, void* cache,
+                                   int64_t record_bytes, int32_t inter, int32_t blocks_per_job,
+                                   const void* residual, void* out, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  MOE_REQUIRE(x && w && logits && ids && weights && slot_of && slot_expert && slot_stamp && step &&
+                  out_slot && fetch_slot && fetch_expert && nmiss && pool && cache && out &&
+                  workspace,
+              "moe_route_fetch_ffn: NULL pointer");
+  MOE_REQUIRE(logit_dtype == MOE_F32 || logit_dtype == MOE_BF16,
+              "moe_route_fetch_ffn: logit_dtype must be MOE_F32 or MOE_BF16");
+  MOE_REQUIRE(hidden >= 512 && hidden % 512 == 0 && hidden <= kGemvMaxHidden,
+              "moe_route_fetch_ffn: hidden must be a multiple of 512 up to %d (got %d)",
+              kGemvMaxHidden, hidden);
+  MOE_REQUIRE(inter >= 128 && inter % 128 == 0 && inter <= kGemvMaxInter,
+              "moe_route_fetch_ffn: inter must be a multiple of 128 up to %d (got %d)",
+              kGemvMaxInter, inter);
+  MOE_REQUIRE(top_k >= 1 && top_k <= kGemvMaxTopK && top_k <= n_experts && n_experts <= 1024,
+              "moe_route_fetch_ffn: need 1 <= top_k <= min(%d, n_experts), n_experts <= 1024",
+              kGemvMaxTopK);
+  MOE_REQUIRE(cap >= 1 && cap <= 1024, "moe_route_fetch_ffn: need 1 <= cap <= 1024");
+  MOE_REQUIRE(top_k <= cap, "moe_route_fetch_ffn: top_k (%d) exceeds the cache capacity (%d)",
+              top_k, cap);
+  const int64_t w13 = 2LL * inter * hidden;
+  const int64_t off_s13 = w13 + static_cast<int64_t>(hidden) * inter;
+  const int64_t off_s2 = off_s13 + (2LL * inter / 128) * (hidden / 128) * 4;
+  const int64_t payload = off_s2 + (static_cast<int64_t>(hidden) / 128) * (inter / 128) * 4;
+  MOE_REQUIRE(record_bytes >= payload && record_bytes % 256 == 0,
+              "moe_route_fetch_ffn: record_bytes (%lld) must hold the %lld-byte record and be a "
+              "multiple of 256",
+              (long long)record_bytes, (long long)payload);
+  MOE_REQUIRE(reinterpret_cast<uintptr_t>(pool) % 256 == 0 &&
+                  reinterpret_cast<uintptr_t>(cache) % 256 == 0,
+              "moe_route_fetch_ffn: pool and cache must be 256-byte aligned");
+  MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0,
+              "moe_route_fetch_ffn: x and w must be 16-byte aligned");
+  MOE_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
+                  workspace_bytes >= static_cast<size_t>(top_k) * inter * sizeof(float),
+              "moe_route_fetch_ffn: the workspace must be 16-byte aligned and hold top_k * inter "
+              "floats");
+  MOE_REQUIRE(blocks_per_job >= 1 && blocks_per_job <= 4096,
+              "moe_route_fetch_ffn: need 1 <= blocks_per_job <= 4096");
+  hipStream_t s = as_stream(stream);
+  int rc = launch_decode_logits(x, w, bias, hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0,
+                                logits, step, s);
+  if (rc) return rc;
+  StepGeom g;
+  g.pool = static_cast<const char*>(pool);
+  g.cache = static_cast<char*>(cache);
+  g.rb = record_bytes;
+  g.w13_bytes = w13;
+  g.off_s13 = off_s13;
+  g.hidden = hidden;
+  g.inter = inter;
+  g.gb = hidden / 128;
+  g.kq = hidden / 512;
+  g.units = inter / 16;
+  g.plain = static_cast<int32_t>((record_bytes - w13 + kPieceBytes - 1) / kPieceBytes);
+  g.nfetch = blocks_per_job * (top_k < kFetchMaxJobsInGrid ? top_k : kFetchMaxJobsInGrid);
+  const unsigned grid = static_cast<unsigned>(g.nfetch + top_k * g.units);
+  float* act = static_cast<float*>(workspace);
+#define MOE_RFG(PE, PC)                                                                        \
+  hipLaunchKernelGGL((route_fetch_gateup_kernel<PE, PC>), dim3(grid), dim3(kStepThreads), 0, s, \
+                     g, static_cast<const uint16_t*>(x), logits, n_experts, top_k, ids, weights, \
+                     slot_of, slot_expert, slot_stamp, cap, step, out_slot, fetch_slot,          \
+                     fetch_expert, nmiss, stats, act)
+  if (n_experts <= 256) {
+    if (cap <= 256) MOE_RFG(4, 4); else MOE_RFG(4, 16);
+  } else {
+    if (cap <= 256) MOE_RFG(16, 4); else MOE_RFG(16, 16);
+  }
+#undef MOE_RFG
+  rc = check_launch("moe_route_fetch_ffn(route+fetch+gate/up)");
+  if (rc) return rc;
+  const uint8_t* cb = static_cast<const uint8_t*>(cache);
+  return launch_down_gemv(act, out_slot, weights, 1, top_k, cb + w13,
+                          reinterpret_cast<const float*>(cb + off_s2), record_bytes,
+                          record_bytes / 4, MOE_LAYOUT_TILES, cap, hidden, inter,
+                          static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out), s);
+}

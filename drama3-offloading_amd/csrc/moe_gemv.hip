@@ -24,6 +24,7 @@
 // quantises its two a rows into LDS, does the 8 output rows of w2 of both in
 // one MFMA per K-block, and the workgroup sums the k partials in order.
 #include "common.hpp"
+#include "gemv.hpp"
 #include "grouped.hpp"
 #include "shared.hpp"
 
@@ -46,9 +47,9 @@ struct SharedRefs {
 };
 constexpr int kSharedJPW = 2;   // shared intermediate rows (gate + up) per kernel-1 wave
 
-constexpr int kMaxHidden = 8192;
-constexpr int kMaxInter = 2048;
-constexpr int kMaxK = 16;
+constexpr int kMaxHidden = kGemvMaxHidden;
+constexpr int kMaxInter = kGemvMaxInter;
+constexpr int kMaxK = kGemvMaxTopK;
 
 // The id and the routing weight of pair p are read without a branch on
 // their dtype: a load inside a branch is waited for inside it, and that wait
@@ -81,30 +82,6 @@ __device__ __forceinline__ float route_weight(RouteHalves r, int wbf16) {
 }
 
 // ------------------------------------------------------------ kernel 1
-
-// 8 bf16 values of x held by one lane (16 bytes, elements i..i+7) -> e4m3
-// codes and the group scale in LDS.  Sixteen consecutive lanes form one
-// 128-column group; every lane of the wave calls this (the group maximum is
-// a cross-lane exchange), lanes past the end with live == false.
-__device__ __forceinline__ void quantize_x8(uint4 raw, bool live, int i,
-                                            uint8_t* __restrict__ xq, float* __restrict__ xs) {
-  const uint32_t rr[4] = {raw.x, raw.y, raw.z, raw.w};
-  float v[8];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    v[2 * j] = __uint_as_float(rr[j] << 16);
-    v[2 * j + 1] = __uint_as_float(rr[j] & 0xffff0000u);
-  }
-  float amax = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
-  amax = row16_max_f32(amax);
-  if (live) {
-    const float sc = act_scale(amax);
-    *reinterpret_cast<uint2*>(xq + i) = make_uint2(quant4_e4m3(v, sc), quant4_e4m3(v + 4, sc));
-    if ((threadIdx.x & 15) == 0) xs[i >> 7] = sc;
-  }
-}
 
 // Two 16-row tiles of one (token, expert) pair per workgroup, each split
 // over K between kGateUpSplit waves (contiguous ranges of K-blocks).  Every
@@ -544,6 +521,17 @@ static int launch_gemv(const uint16_t* x, const void* ids, int ids64, const void
                        SharedRefs{});
   }
   return check_launch("moe_fp8_moe_forward(down)");
+}
+
+int launch_down_gemv(const float* act, const int32_t* slots, const float* weights,
+                     int32_t tokens, int32_t top_k, const uint8_t* w2, const float* s2,
+                     int64_t w2_es, int64_t s2_es, int tiled, int32_t n_slots, int32_t hidden,
+                     int32_t inter, const uint16_t* residual, uint16_t* out, hipStream_t s) {
+  hipLaunchKernelGGL(down_gemv_kernel<false>, dim3(hidden / kDownRows, tokens),
+                     dim3(64 * ((top_k + 1) / 2)), 0, s, act, slots, 0, weights, 0, top_k, w2,
+                     s2, w2_es, s2_es, tiled, n_slots, hidden, inter, residual, out,
+                     SharedRefs{});
+  return check_launch("down_gemv_kernel");
 }
 
 }  // namespace moe

@@ -159,15 +159,18 @@ __device__ __forceinline__ void resolve_chunk(SlotRegs<PER>& t, int32_t my_e, in
 // table (slot_of in x, slots in t), for a kernel whose workgroups all make
 // the decisions and one of them writes the next table out: the decisions of
 // resolve_chunk, nothing written to the table in memory.  Lane r ends with
-// id r's slot in slot_r (-1 for an id out of range); the misses are appended
-// to job_e / job_s by lane 0.
+// id r's slot in slot_r (-1 for an id out of range) and miss_r set when id r
+// missed; the misses are appended to job_e / job_s, and their positions r
+// to job_k when it is given, by lane 0.
 template <int PER, int PERC>
 __device__ __forceinline__ void resolve_regs(SlotRegs<PERC>& t, ExpertRegs<PER>& x, int32_t my_e,
                                              int32_t my_s, int n, int64_t step, int32_t cap,
-                                             int32_t* job_e, int32_t* job_s, int32_t& nm,
-                                             int64_t& hits, int32_t& slot_r) {
+                                             int32_t* job_e, int32_t* job_s, int32_t* job_k,
+                                             int32_t& nm, int64_t& hits, int32_t& slot_r,
+                                             bool& miss_r) {
   const int lane = threadIdx.x & 63;
   slot_r = -1;
+  miss_r = false;
   for (int r = 0; r < n; ++r) {
     const int32_t e = lane_value(my_e, r);
     int32_t s = lane_value(my_s, r);
@@ -184,7 +187,9 @@ __device__ __forceinline__ void resolve_regs(SlotRegs<PERC>& t, ExpertRegs<PER>&
       if (lane == 0) {
         job_e[nm] = e;
         job_s[nm] = s;
+        if (job_k) job_k[nm] = r;
       }
+      if (lane == r) miss_r = true;
       ++nm;
     } else {
       ++hits;

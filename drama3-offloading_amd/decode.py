@@ -10,10 +10,14 @@ Per layer, all on one stream, nothing synchronising and nothing allocating:
     y     = fp8_moe_forward(h, slots, w)      W8A8 expert FFN on the cache (HIP)
     x     = h + y
 
-The router, resolve and fetch are two launches (moe_route_fetch: the logits,
-then every fetch workgroup resolving the call itself from a double-buffered
-slot table and copying its share of the misses), or with fused_fetch=False
-(and always with coded pools) three (moe_route_resolve, then the fetch).
+The router, resolve, fetch and expert FFN are three launches
+(moe_route_fetch_ffn: the logits; the route, the misses' fetch and the gate/up
+half of the FFN, every workgroup resolving the call itself from a
+double-buffered slot table, the workgroups that fetch a miss's rows running
+its gate/up MFMAs on them as they arrive; the down half).  With
+fused_ffn=False the FFN is its own two launches after moe_route_fetch's two;
+with fused_fetch=False (and always with coded pools) the route is
+moe_route_resolve and the fetch a launch of its own.
 
 With `shared_expert`, the step is the full MoE block, one call after the
 fetch: the gated bf16 shared expert rides in the two routed GEMV launches
@@ -79,6 +83,7 @@ class DecodeConfig:
     gate_std: float = 0.002
     blocks_per_job: int = 3
     fused_fetch: bool = True        # router + resolve + fetch in two launches (moe_route_fetch)
+    fused_ffn: bool = True          # ... and the FFN's gate/up in the same launch (moe_route_fetch_ffn)
     noncoherent_pool: bool = False
     shared_expert: bool = False     # the MoE block's gated bf16 shared expert
     shared_inter: int = 512
@@ -171,6 +176,9 @@ class DecodeHarness:
             self.coded = coded
         # the step takes moe_route_fetch (router + resolve + fetch), decided once
         self.fused = cfg.mode == "cached" and cfg.fused_fetch and self.coded is None
+        # ... and the FFN with it (packed tile-ordered records, routed experts only)
+        self.fused_ffn = (self.fused and cfg.fused_ffn and not cfg.shared_expert and
+                          self.layout.tiled and cfg.hidden % 512 == 0 and cfg.top_k <= 16)
         if cfg.shared_expert:
             # seeded bf16 shared experts, resident (6 MiB per layer at 2048 x 512)
             g2 = torch.Generator(device=dev).manual_seed(cfg.seed + 3)
@@ -234,6 +242,16 @@ class DecodeHarness:
         cfg, lib = self.cfg, self.lib
         stub_linear(self.x, self.w_stub[l], self.h)
         w13, s13, w2, s2 = self.views[l]
+        if self.fused_ffn:
+            # the whole layer's MoE in three launches; x = h + MoE(h)
+            lib.route_fetch_ffn(self.h, self.gate[l], self.bias_live[l], cfg.top_k,
+                                self.logits[l], self.ids[l], self.wts[l], self.tab_slot_of[l],
+                                self.tab_slot_expert[l], self.tab_stamp[l], self.step[l],
+                                self.out_slot[l], self.fslot[l], self.fexp[l], self.nmiss[l],
+                                self.pools[l].dev_ptr, self.cache[l], cfg.inter,
+                                cfg.blocks_per_job, self.x, self.ws, residual=self.h,
+                                stats=self.stats[l], logit_dtype=cfg.router_logits)
+            return
         if self.fused:
             # router, then resolve + miss fetch in one launch (double-buffered table)
             lib.route_fetch(self.h, self.gate[l], self.bias_live[l], cfg.top_k, self.logits[l],

@@ -85,6 +85,9 @@ SIGNATURES = {
     "moe_route_fetch": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
                                   _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
                                   C.POINTER(FetchPair), _i32, _i32, _vp]),
+    "moe_route_fetch_ffn": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp,
+                                      _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                      _vp, C.c_int64, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
     "moe_fp8_moe_workspace": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "moe_fp8_moe_forward": (C.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
                                       _i32, _i32, _i32, _vp, _vp, _sz, _vp]),
@@ -378,6 +381,48 @@ class Native:
             slot_expert.data_ptr(), stamp.data_ptr(), slot_expert.shape[1], step.data_ptr(),
             out_slot.data_ptr(), fetch_slot.data_ptr(), fetch_expert.data_ptr(), nmiss.data_ptr(),
             self._ptr(stats), arr, len(pairs), blocks_per_job, self.stream()), "moe_route_fetch")
+
+    def route_fetch_ffn(self, x, w, bias, top_k: int, logits, ids, weights, slot_of,
+                        slot_expert, stamp, step, out_slot, fetch_slot, fetch_expert, nmiss,
+                        pool_dev_ptr: int, cache, inter: int, blocks_per_job: int, out,
+                        workspace, residual=None, stats=None, logit_dtype: str = "bf16") -> None:
+        """The decode step's MoE layer of one token (moe_route_fetch_ffn):
+        route_fetch's router, resolve and miss fetch from the packed pool at
+        device address pool_dev_ptr into cache (uint8 [cap, record_bytes]),
+        then the expert FFN on the slots; out [1, H] bf16 = residual + MoE(x)."""
+        import torch
+        if x.shape[0] != 1:
+            raise ValueError("route_fetch_ffn takes exactly one token")
+        if slot_of.dim() != 2 or slot_of.shape[0] != 2 or slot_expert.dim() != 2 \
+                or slot_expert.shape[0] != 2 or tuple(stamp.shape) != tuple(slot_expert.shape):
+            raise ValueError("route_fetch_ffn takes double-buffered tables: slot_of [2, E], "
+                             "slot_expert and stamp [2, C]")
+        what = "moe_route_fetch_ffn"
+        self._on_gpu(what, x, w, bias, logits, ids, weights, slot_of, slot_expert, stamp, step,
+                     out_slot, fetch_slot, fetch_expert, nmiss, stats, cache, out, workspace,
+                     residual)
+        H, E = self._router_bufs(what, x, w, bias, logits, 1, top_k)
+        if slot_of.shape[1] != E:
+            raise ValueError(f"slot_of [2, {slot_of.shape[1]}] does not match {E} experts")
+        C_ = slot_expert.shape[1]
+        self._buf(what, "ids", ids, top_k, torch.int32)
+        self._buf(what, "weights", weights, top_k, torch.float32)
+        self._slot_bufs(what, slot_of, 2 * E, slot_expert, stamp, step, out_slot, top_k,
+                        fetch_slot, fetch_expert, nmiss, stats)
+        if cache.dim() != 2 or cache.dtype != torch.uint8 or not cache.is_contiguous() \
+                or cache.shape[0] < C_:
+            raise ValueError(f"{what}: cache must be contiguous uint8 [>= {C_}, record_bytes]")
+        self._buf(what, "out", out, H, torch.bfloat16)
+        self._buf(what, "residual", residual, H, torch.bfloat16)
+        self._buf(what, "workspace", workspace, 0)
+        self._check(self.cdll.moe_route_fetch_ffn(
+            x.data_ptr(), w.data_ptr(), self._ptr(bias), self._logit_code(logit_dtype), H, E,
+            top_k, logits.data_ptr(), ids.data_ptr(), weights.data_ptr(), slot_of.data_ptr(),
+            slot_expert.data_ptr(), stamp.data_ptr(), C_, step.data_ptr(), out_slot.data_ptr(),
+            fetch_slot.data_ptr(), fetch_expert.data_ptr(), nmiss.data_ptr(), self._ptr(stats),
+            pool_dev_ptr, cache.data_ptr(), cache.shape[1], inter, blocks_per_job,
+            self._ptr(residual), out.data_ptr(), workspace.data_ptr(),
+            workspace.numel() * workspace.element_size(), self.stream()), what)
 
     # ------------------------------------------------------------ experts
     def fp8_moe_workspace(self, tokens, top_k, n_experts, hidden, inter) -> int:

@@ -222,6 +222,35 @@ int moe_route_fetch(const void* x, const void* w, const float* bias, int32_t log
                     const moe_fetch_pair* pairs, int32_t npairs, int32_t blocks_per_job,
                     void* stream);
 
+/* The decode step's whole MoE layer of one token from packed records:
+ * moe_route_fetch's router, slot resolve and miss fetch followed by
+ * moe_fp8_moe_forward_ex's expert FFN on the cache slots, in three launches
+ * instead of four, with the same outputs bit for bit.  The workgroups that
+ * fetch a miss's gate and up rows run that expert's gate/up MFMAs on the
+ * bytes as they arrive, and the hits' gate/up runs beside the fetch in the
+ * same launch; the down projection (with the routing weights, the residual
+ * and the bf16 output) is the last launch.  Records: w13 [2*inter, hidden] |
+ * w2 [hidden, inter], both in MFMA tile order (MOE_LAYOUT_TILES), | s13
+ * [2*inter/128, hidden/128] | s2 [hidden/128, inter/128] f32, record_bytes
+ * apart (>= their sum, a multiple of 256) in `pool` (the device address of
+ * the page-locked host pool, n_experts records) and in `cache` (cap slots),
+ * both 256-byte aligned.  out [hidden] bf16 = bf16(residual + bf16(MoE(x)))
+ * (residual nullable, may be x); the workspace holds top_k * inter floats.
+ * The table arguments are moe_route_fetch's (double-buffered).
+ * Constraints: hidden a multiple of 512 up to 8192, inter a multiple of 128
+ * up to 2048, 1 <= top_k <= min(16, n_experts) <= cap <= 1024, n_experts <=
+ * 1024.  Replaces, for the decode step, the router top-k + _resolve_slots +
+ * fetch_experts + fp8_moe_forward sequence of bin/devcache.py:230-277; no
+ * single counterpart. */
+int moe_route_fetch_ffn(const void* x, const void* w, const float* bias, int32_t logit_dtype,
+                        int32_t hidden, int32_t n_experts, int32_t top_k, float* logits,
+                        int32_t* ids, float* weights, int32_t* slot_of, int32_t* slot_expert,
+                        int64_t* slot_stamp, int32_t cap, int64_t* step, int32_t* out_slot,
+                        int32_t* fetch_slot, int32_t* fetch_expert, int32_t* nmiss,
+                        int64_t* stats, const void* pool, void* cache, int64_t record_bytes,
+                        int32_t inter, int32_t blocks_per_job, const void* residual, void* out,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------- expert compute */
 
 /* Workspace bytes moe_fp8_moe_forward needs for this shape. */

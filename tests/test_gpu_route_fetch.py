@@ -1,5 +1,7 @@
 """moe_route_fetch, the decode step's router + resolve + fetch in two
 launches, against moe_route_resolve followed by moe_fetch (three launches),
+and moe_route_fetch_ffn (the same with the expert FFN, three launches)
+against those and the FFN's own two,
 at Drama-3 shape (256 experts, top-8, H 2048, I 512) and two others (320
 experts, top-12, 272 slots; 64 experts, top-4, 5 slots) over 3 layers and
 popularity drifts: two harnesses on the same pools, one per path, step for
@@ -47,10 +49,10 @@ def _same(a, b, tag):
 def test_route_fetch_equals_route_resolve_then_fetch(lib, dev, shape):
     import decode
     base = dict(layers=3, drift_every=3, schedule_steps=12, **shape)
-    fused = decode.DecodeHarness(decode.DecodeConfig(**base), dev)
+    fused = decode.DecodeHarness(decode.DecodeConfig(**base, fused_ffn=False), dev)
     plain = decode.DecodeHarness(decode.DecodeConfig(**base, fused_fetch=False), dev,
                                  pools=fused.pools)
-    assert fused.fused and not plain.fused
+    assert fused.fused and not fused.fused_ffn and not plain.fused
     for s in range(7):
         for h in (fused, plain):
             h.stage(s)
@@ -67,6 +69,43 @@ def test_route_fetch_equals_route_resolve_then_fetch(lib, dev, shape):
             h.replay(1)
         torch.cuda.synchronize(dev)
         say(f"route_fetch: replay {s}")
+        _same(fused, plain, f"replay {s}")
+    plain.pools = []                     # owned by the fused harness
+    fused.close()
+
+
+@pytest.mark.parametrize("shape", [
+    dict(capacity=20),
+    dict(n_experts=320, top_k=12, hidden=512, inter=256, capacity=272, blocks_per_job=2),
+    dict(n_experts=64, top_k=4, hidden=512, inter=128, capacity=5, blocks_per_job=1),
+], ids=["drama3", "wide", "tight"])
+def test_route_fetch_ffn_equals_separate_launches(lib, dev, shape):
+    """moe_route_fetch_ffn (three launches: the misses' gate/up inside the
+    fetch, the hits' beside it) against moe_route_resolve + moe_fetch +
+    moe_fp8_moe_forward_ex (five): outputs, tables and cache bytes equal
+    step for step, eager and replayed."""
+    import decode
+    base = dict(layers=3, drift_every=3, schedule_steps=12, **shape)
+    fused = decode.DecodeHarness(decode.DecodeConfig(**base), dev)
+    plain = decode.DecodeHarness(decode.DecodeConfig(**base, fused_fetch=False), dev,
+                                 pools=fused.pools)
+    assert fused.fused_ffn and not plain.fused
+    for s in range(7):
+        for h in (fused, plain):
+            h.stage(s)
+            h.step_eager()
+        torch.cuda.synchronize(dev)
+        say(f"route_fetch_ffn {shape}: eager step {s}")
+        _same(fused, plain, f"eager {s}")
+    hits, misses = fused.hit_rate()
+    assert hits > 0 and misses > 0
+    for h in (fused, plain):
+        h.capture()
+    for s in range(9):
+        for h in (fused, plain):
+            h.replay(1)
+        torch.cuda.synchronize(dev)
+        say(f"route_fetch_ffn: replay {s}")
         _same(fused, plain, f"replay {s}")
     plain.pools = []                     # owned by the fused harness
     fused.close()
