@@ -76,8 +76,8 @@ def test_route_fetch_equals_route_resolve_then_fetch(lib, dev, shape):
 
 @pytest.mark.parametrize("shape", [
     dict(capacity=20),
-    dict(n_experts=320, top_k=12, hidden=512, inter=256, capacity=272, blocks_per_job=2),
-    dict(n_experts=64, top_k=4, hidden=512, inter=128, capacity=5, blocks_per_job=1),
+    dict(n_experts=320, top_k=12, hidden=512, inter=256, capacity=272, ffn_blocks_per_job=2),
+    dict(n_experts=64, top_k=4, hidden=512, inter=128, capacity=5, ffn_blocks_per_job=1),
 ], ids=["drama3", "wide", "tight"])
 def test_route_fetch_ffn_equals_separate_launches(lib, dev, shape):
     """moe_route_fetch_ffn (three launches: the misses' gate/up inside the
