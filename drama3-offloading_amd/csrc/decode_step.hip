@@ -28,6 +28,10 @@
 //   * hit workgroups (top_k * I/16 of them, one per pick and unit): a hit's
 //     16 gate rows (first wave) and 16 up rows (second wave) from its cache
 //     slot; a pick that missed leaves its workgroup idle.
+//   * with the MoE block's shared expert, workgroups for its gate/up rows
+//     and sigmoid gate (the gate/up GEMV kernel's shared workgroups, the
+//     same arithmetic); they need no route.  Its down rows then ride in the
+//     down launch, which adds residual + (routed + sigmoid-gated shared).
 // Every row sum is the in-order chain over its K-blocks of fma(block
 // product, weight scale * x scale, sum) that the gate/up GEMV kernel forms,
 // so the activations, and the down launch's output, are bit-identical to
@@ -38,6 +42,7 @@
 #include "gemv.hpp"
 #include "resolve.hpp"
 #include "route.hpp"
+#include "shared.hpp"
 
 namespace moe {
 
@@ -69,7 +74,35 @@ __global__ __launch_bounds__(kStepThreads) void route_fetch_gateup_kernel(
     int64_t* __restrict__ stamp, int32_t cap, const int64_t* __restrict__ step_ptr,
     int32_t* __restrict__ out_slot, int32_t* __restrict__ fetch_slot,
     int32_t* __restrict__ fetch_expert, int32_t* __restrict__ nmiss_ptr,
-    int64_t* __restrict__ stats, float* __restrict__ act) {
+    int64_t* __restrict__ stats, float* __restrict__ act, SharedRefs sh) {
+  const int first_shared = g.nfetch + top_k * g.units;
+  if (static_cast<int>(blockIdx.x) >= first_shared) {
+    // shared expert rows j0, j0 + 1 of this wave (gate and up each; row Is
+    // is the sigmoid gate), the token's x; no barrier on this branch
+    const int wv = threadIdx.x >> 6;
+    const int ln = threadIdx.x & 63;
+    const int j0 = ((static_cast<int>(blockIdx.x) - first_shared) * 2 + wv) * kSharedJPW;
+    if (j0 > sh.inter) return;
+    const uint16_t* rows[2 * kSharedJPW];
+#pragma unroll
+    for (int i = 0; i < kSharedJPW; ++i) {
+      const int j = min(j0 + i, sh.inter);
+      const bool gate_row = j == sh.inter;
+      rows[2 * i] = gate_row ? sh.wsg : sh.wg + static_cast<int64_t>(j) * g.hidden;
+      rows[2 * i + 1] = gate_row ? sh.wsg : sh.wu + static_cast<int64_t>(j) * g.hidden;
+    }
+    float sacc[2 * kSharedJPW][1];
+    rows_dot_bf16<2 * kSharedJPW, 1, 4>(rows, x, g.hidden, 0, 1, g.hidden >> 3, ln, sacc);
+    if (ln == 0) {
+#pragma unroll
+      for (int i = 0; i < kSharedJPW; ++i) {
+        const int j = j0 + i;
+        if (j < sh.inter) sh.act[j] = shared_act(sacc[2 * i][0], sacc[2 * i + 1][0]);
+        else if (j == sh.inter) *sh.sig = shared_sig(sacc[2 * i][0]);
+      }
+    }
+    return;
+  }
   __shared__ __align__(16) uint8_t xq[kGemvMaxHidden];
   __shared__ float xs[kGemvMaxHidden / 128];
   __shared__ __align__(16) float dpart[2][kGemvMaxHidden / 128][16];
@@ -314,8 +347,9 @@ extern "C" int moe_route_fetch_ffn(const void* x, const void* w, const float* bi
                                    int32_t* fetch_slot, int32_t* fetch_expert, int32_t* nmiss,
                                    int64_t* stats, const void* pool, void* cache,
                                    int64_t record_bytes, int32_t inter, int32_t blocks_per_job,
-                                   const void* residual, void* out, void* workspace,
-                                   size_t workspace_bytes, void* stream) {
+                                   const moe_shared_expert* shared, const void* residual,
+                                   void* out, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
   MOE_REQUIRE(x && w && logits && ids && weights && slot_of && slot_expert && slot_stamp && step &&
                   out_slot && fetch_slot && fetch_expert && nmiss && pool && cache && out &&
                   workspace,
@@ -347,10 +381,37 @@ extern "C" int moe_route_fetch_ffn(const void* x, const void* w, const float* bi
               "moe_route_fetch_ffn: pool and cache must be 256-byte aligned");
   MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0,
               "moe_route_fetch_ffn: x and w must be 16-byte aligned");
-  MOE_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
-                  workspace_bytes >= static_cast<size_t>(top_k) * inter * sizeof(float),
-              "moe_route_fetch_ffn: the workspace must be 16-byte aligned and hold top_k * inter "
-              "floats");
+  // workspace: act [top_k, inter] f32 from byte 0; with the shared expert,
+  // its act [Is] bf16 and sig f32 after it (moe_fp8_moe_block_forward's
+  // layout for one token)
+  const size_t base = (moe_fp8_moe_workspace(1, top_k, cap, hidden, inter) + 255) & ~size_t{255};
+  size_t need = static_cast<size_t>(top_k) * inter * sizeof(float);
+  SharedRefs sh{};
+  if (shared) {
+    const int32_t Is = shared->inter;
+    MOE_REQUIRE(Is >= 128 && Is % 128 == 0,
+                "moe_route_fetch_ffn: shared inter must be a positive multiple of 128");
+    MOE_REQUIRE(shared->w_gate && shared->w_up && shared->w_down && shared->w_sgate,
+                "moe_route_fetch_ffn: NULL shared expert weight");
+    MOE_REQUIRE(reinterpret_cast<uintptr_t>(shared->w_gate) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(shared->w_up) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(shared->w_down) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(shared->w_sgate) % 16 == 0,
+                "moe_route_fetch_ffn: shared expert weights must be 16-byte aligned");
+    need = moe_fp8_moe_block_workspace(1, top_k, cap, hidden, inter, Is);
+    char* ws = static_cast<char*>(workspace);
+    sh = SharedRefs{static_cast<const uint16_t*>(shared->w_gate),
+                    static_cast<const uint16_t*>(shared->w_up),
+                    static_cast<const uint16_t*>(shared->w_down),
+                    static_cast<const uint16_t*>(shared->w_sgate), Is,
+                    reinterpret_cast<uint16_t*>(ws + base),
+                    reinterpret_cast<float*>(ws + base + ((static_cast<size_t>(Is) * 2 + 255) &
+                                                          ~size_t{255}))};
+  }
+  MOE_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0 && workspace_bytes >= need,
+              "moe_route_fetch_ffn: the workspace must be 256-byte aligned and hold %zu bytes "
+              "(%zu given)",
+              need, workspace_bytes);
   MOE_REQUIRE(blocks_per_job >= 1 && blocks_per_job <= 4096,
               "moe_route_fetch_ffn: need 1 <= blocks_per_job <= 4096");
   hipStream_t s = as_stream(stream);
@@ -370,13 +431,14 @@ extern "C" int moe_route_fetch_ffn(const void* x, const void* w, const float* bi
   g.units = inter / 16;
   g.plain = static_cast<int32_t>((record_bytes - w13 + kPieceBytes - 1) / kPieceBytes);
   g.nfetch = blocks_per_job * (top_k < kFetchMaxJobsInGrid ? top_k : kFetchMaxJobsInGrid);
-  const unsigned grid = static_cast<unsigned>(g.nfetch + top_k * g.units);
+  const int nshared = shared ? (shared->inter + 1 + 2 * kSharedJPW - 1) / (2 * kSharedJPW) : 0;
+  const unsigned grid = static_cast<unsigned>(g.nfetch + top_k * g.units + nshared);
   float* act = static_cast<float*>(workspace);
 #define MOE_RFG(PE, PC)                                                                        \
   hipLaunchKernelGGL((route_fetch_gateup_kernel<PE, PC>), dim3(grid), dim3(kStepThreads), 0, s, \
                      g, static_cast<const uint16_t*>(x), logits, n_experts, top_k, ids, weights, \
                      slot_of, slot_expert, slot_stamp, cap, step, out_slot, fetch_slot,          \
-                     fetch_expert, nmiss, stats, act)
+                     fetch_expert, nmiss, stats, act, sh)
   if (n_experts <= 256) {
     if (cap <= 256) MOE_RFG(4, 4); else MOE_RFG(4, 16);
   } else {
@@ -389,5 +451,6 @@ extern "C" int moe_route_fetch_ffn(const void* x, const void* w, const float* bi
   return launch_down_gemv(act, out_slot, weights, 1, top_k, cb + w13,
                           reinterpret_cast<const float*>(cb + off_s2), record_bytes,
                           record_bytes / 4, MOE_LAYOUT_TILES, cap, hidden, inter,
-                          static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out), s);
+                          static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out),
+                          shared ? &sh : nullptr, s);
 }

@@ -32,21 +32,6 @@
 
 namespace moe {
 
-// The MoE block's shared expert carried along by the two decode launches
-// (moe_fp8_moe_block_forward): kernel 1 computes its act and sigmoid gate in
-// extra workgroups, kernel 2 its down rows in one extra wave per workgroup,
-// with the arithmetic of the standalone shared-expert kernels (shared.hpp).
-struct SharedRefs {
-  const uint16_t* wg;    // [Is, H] bf16
-  const uint16_t* wu;    // [Is, H]
-  const uint16_t* wd;    // [H, Is]
-  const uint16_t* wsg;   // [H]
-  int32_t inter;         // Is
-  uint16_t* act;         // [T, Is] bf16 scratch
-  float* sig;            // [T] scratch
-};
-constexpr int kSharedJPW = 2;   // shared intermediate rows (gate + up) per kernel-1 wave
-
 constexpr int kMaxHidden = kGemvMaxHidden;
 constexpr int kMaxInter = kGemvMaxInter;
 constexpr int kMaxK = kGemvMaxTopK;
@@ -526,11 +511,18 @@ static int launch_gemv(const uint16_t* x, const void* ids, int ids64, const void
 int launch_down_gemv(const float* act, const int32_t* slots, const float* weights,
                      int32_t tokens, int32_t top_k, const uint8_t* w2, const float* s2,
                      int64_t w2_es, int64_t s2_es, int tiled, int32_t n_slots, int32_t hidden,
-                     int32_t inter, const uint16_t* residual, uint16_t* out, hipStream_t s) {
-  hipLaunchKernelGGL(down_gemv_kernel<false>, dim3(hidden / kDownRows, tokens),
-                     dim3(64 * ((top_k + 1) / 2)), 0, s, act, slots, 0, weights, 0, top_k, w2,
-                     s2, w2_es, s2_es, tiled, n_slots, hidden, inter, residual, out,
-                     SharedRefs{});
+                     int32_t inter, const uint16_t* residual, uint16_t* out,
+                     const SharedRefs* sh, hipStream_t s) {
+  if (sh) {
+    hipLaunchKernelGGL(down_gemv_kernel<true>, dim3(hidden / kDownRows, tokens),
+                       dim3(64 * ((top_k + 1) / 2 + 1)), 0, s, act, slots, 0, weights, 0, top_k,
+                       w2, s2, w2_es, s2_es, tiled, n_slots, hidden, inter, residual, out, *sh);
+  } else {
+    hipLaunchKernelGGL(down_gemv_kernel<false>, dim3(hidden / kDownRows, tokens),
+                       dim3(64 * ((top_k + 1) / 2)), 0, s, act, slots, 0, weights, 0, top_k, w2,
+                       s2, w2_es, s2_es, tiled, n_slots, hidden, inter, residual, out,
+                       SharedRefs{});
+  }
   return check_launch("down_gemv_kernel");
 }
 

@@ -180,8 +180,8 @@ class DecodeHarness:
         # the step takes moe_route_fetch (router + resolve + fetch), decided once
         self.fused = cfg.mode == "cached" and cfg.fused_fetch and self.coded is None
         # ... and the FFN with it (packed tile-ordered records, routed experts only)
-        self.fused_ffn = (self.fused and cfg.fused_ffn and not cfg.shared_expert and
-                          self.layout.tiled and cfg.hidden % 512 == 0 and cfg.top_k <= 16)
+        self.fused_ffn = (self.fused and cfg.fused_ffn and self.layout.tiled and
+                          cfg.hidden % 512 == 0 and cfg.top_k <= 16)
         if cfg.shared_expert:
             # seeded bf16 shared experts, resident (6 MiB per layer at 2048 x 512)
             g2 = torch.Generator(device=dev).manual_seed(cfg.seed + 3)
@@ -246,14 +246,17 @@ class DecodeHarness:
         stub_linear(self.x, self.w_stub[l], self.h)
         w13, s13, w2, s2 = self.views[l]
         if self.fused_ffn:
-            # the whole layer's MoE in three launches; x = h + MoE(h)
+            # the whole layer's MoE (block) in three launches; x = h + MoE(h)
             lib.route_fetch_ffn(self.h, self.gate[l], self.bias_live[l], cfg.top_k,
                                 self.logits[l], self.ids[l], self.wts[l], self.tab_slot_of[l],
                                 self.tab_slot_expert[l], self.tab_stamp[l], self.step[l],
                                 self.out_slot[l], self.fslot[l], self.fexp[l], self.nmiss[l],
                                 self.pools[l].dev_ptr, self.cache[l], cfg.inter,
-                                cfg.ffn_blocks_per_job, self.x, self.ws, residual=self.h,
-                                stats=self.stats[l], logit_dtype=cfg.router_logits)
+                                cfg.ffn_blocks_per_job, self.x,
+                                self.ws_block if cfg.shared_expert else self.ws,
+                                residual=self.h, stats=self.stats[l],
+                                logit_dtype=cfg.router_logits,
+                                shared=self.shared(l) if cfg.shared_expert else None)
             return
         if self.fused:
             # router, then resolve + miss fetch in one launch (double-buffered table)

@@ -87,7 +87,8 @@ SIGNATURES = {
                                   C.POINTER(FetchPair), _i32, _i32, _vp]),
     "moe_route_fetch_ffn": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp,
                                       _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
-                                      _vp, C.c_int64, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
+                                      _vp, C.c_int64, _i32, _i32, C.POINTER(SharedExpert), _vp,
+                                      _vp, _vp, _sz, _vp]),
     "moe_fp8_moe_workspace": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "moe_fp8_moe_forward": (C.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
                                       _i32, _i32, _i32, _vp, _vp, _sz, _vp]),
@@ -385,11 +386,14 @@ class Native:
     def route_fetch_ffn(self, x, w, bias, top_k: int, logits, ids, weights, slot_of,
                         slot_expert, stamp, step, out_slot, fetch_slot, fetch_expert, nmiss,
                         pool_dev_ptr: int, cache, inter: int, blocks_per_job: int, out,
-                        workspace, residual=None, stats=None, logit_dtype: str = "bf16") -> None:
+                        workspace, residual=None, stats=None, logit_dtype: str = "bf16",
+                        shared=None) -> None:
         """The decode step's MoE layer of one token (moe_route_fetch_ffn):
         route_fetch's router, resolve and miss fetch from the packed pool at
         device address pool_dev_ptr into cache (uint8 [cap, record_bytes]),
-        then the expert FFN on the slots; out [1, H] bf16 = residual + MoE(x)."""
+        then the expert FFN on the slots; out [1, H] bf16 = residual + MoE(x).
+        shared = (w_gate [Is, H], w_up [Is, H], w_down [H, Is], w_sgate [H])
+        bf16 makes it the MoE block (fp8_moe_block_forward's output)."""
         import torch
         if x.shape[0] != 1:
             raise ValueError("route_fetch_ffn takes exactly one token")
@@ -415,12 +419,24 @@ class Native:
         self._buf(what, "out", out, H, torch.bfloat16)
         self._buf(what, "residual", residual, H, torch.bfloat16)
         self._buf(what, "workspace", workspace, 0)
+        se = None
+        if shared is not None:
+            wg, wu, wd, wsg = shared
+            self._on_gpu(what, x, *shared)
+            Is = wg.shape[0]
+            if wg.shape != (Is, H) or wu.shape != (Is, H) or wd.shape != (H, Is) \
+                    or wsg.numel() != H:
+                raise ValueError(f"{what}: shared expert weights do not match x")
+            for name, t in zip(("w_gate", "w_up", "w_down", "w_sgate"), shared):
+                self._buf(what, name, t, t.numel(), torch.bfloat16)
+            se = C.byref(SharedExpert(wg.data_ptr(), wu.data_ptr(), wd.data_ptr(),
+                                      wsg.data_ptr(), Is))
         self._check(self.cdll.moe_route_fetch_ffn(
             x.data_ptr(), w.data_ptr(), self._ptr(bias), self._logit_code(logit_dtype), H, E,
             top_k, logits.data_ptr(), ids.data_ptr(), weights.data_ptr(), slot_of.data_ptr(),
             slot_expert.data_ptr(), stamp.data_ptr(), C_, step.data_ptr(), out_slot.data_ptr(),
             fetch_slot.data_ptr(), fetch_expert.data_ptr(), nmiss.data_ptr(), self._ptr(stats),
-            pool_dev_ptr, cache.data_ptr(), cache.shape[1], inter, blocks_per_job,
+            pool_dev_ptr, cache.data_ptr(), cache.shape[1], inter, blocks_per_job, se,
             self._ptr(residual), out.data_ptr(), workspace.data_ptr(),
             workspace.numel() * workspace.element_size(), self.stream()), what)
 

@@ -235,8 +235,13 @@ int moe_route_fetch(const void* x, const void* w, const float* bias, int32_t log
  * apart (>= their sum, a multiple of 256) in `pool` (the device address of
  * the page-locked host pool, n_experts records) and in `cache` (cap slots),
  * both 256-byte aligned.  out [hidden] bf16 = bf16(residual + bf16(MoE(x)))
- * (residual nullable, may be x); the workspace holds top_k * inter floats.
- * The table arguments are moe_route_fetch's (double-buffered).
+ * (residual nullable, may be x), the workspace 256-byte aligned with
+ * top_k * inter floats.  With `shared` (nullable) the call is the MoE block
+ * of moe_fp8_moe_block_forward: the shared expert's gate/up rows ride in the
+ * fetch launch and its down rows in the down launch, out = bf16(residual +
+ * bf16(routed + sigmoid-gated shared)), and the workspace holds
+ * moe_fp8_moe_block_workspace(1, top_k, cap, hidden, inter, shared->inter)
+ * bytes.  The table arguments are moe_route_fetch's (double-buffered).
  * Constraints: hidden a multiple of 512 up to 8192, inter a multiple of 128
  * up to 2048, 1 <= top_k <= min(16, n_experts) <= cap <= 1024, n_experts <=
  * 1024.  Replaces, for the decode step, the router top-k + _resolve_slots +
@@ -248,7 +253,8 @@ int moe_route_fetch_ffn(const void* x, const void* w, const float* bias, int32_t
                         int64_t* slot_stamp, int32_t cap, int64_t* step, int32_t* out_slot,
                         int32_t* fetch_slot, int32_t* fetch_expert, int32_t* nmiss,
                         int64_t* stats, const void* pool, void* cache, int64_t record_bytes,
-                        int32_t inter, int32_t blocks_per_job, const void* residual, void* out,
+                        int32_t inter, int32_t blocks_per_job,
+                        const struct moe_shared_expert* shared, const void* residual, void* out,
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------- expert compute */

@@ -111,6 +111,41 @@ def test_route_fetch_ffn_equals_separate_launches(lib, dev, shape):
     fused.close()
 
 
+@pytest.mark.parametrize("shape", [
+    dict(capacity=20),
+    dict(n_experts=64, top_k=4, hidden=512, inter=128, capacity=5, ffn_blocks_per_job=1,
+         shared_inter=256),
+], ids=["drama3", "tight"])
+def test_route_fetch_ffn_block_equals_separate_launches(lib, dev, shape):
+    """The same with the MoE block's gated shared expert: its gate/up rows in
+    the fused launch and its down rows in the down launch, against
+    moe_route_resolve + moe_fetch + moe_fp8_moe_block_forward."""
+    import decode
+    base = dict(layers=3, drift_every=3, schedule_steps=12, shared_expert=True, **shape)
+    fused = decode.DecodeHarness(decode.DecodeConfig(**base), dev)
+    plain = decode.DecodeHarness(decode.DecodeConfig(**base, fused_fetch=False), dev,
+                                 pools=fused.pools)
+    assert fused.fused_ffn and not plain.fused
+    for s in range(5):
+        for h in (fused, plain):
+            h.stage(s)
+            h.step_eager()
+        torch.cuda.synchronize(dev)
+        say(f"route_fetch_ffn block {shape}: eager step {s}")
+        _same(fused, plain, f"eager {s}")
+        assert int(fused.finite) == int(plain.finite) == 1
+    for h in (fused, plain):
+        h.capture()
+    for s in range(6):
+        for h in (fused, plain):
+            h.replay(1)
+        torch.cuda.synchronize(dev)
+        say(f"route_fetch_ffn block: replay {s}")
+        _same(fused, plain, f"replay {s}")
+    plain.pools = []                     # owned by the fused harness
+    fused.close()
+
+
 def test_route_fetch_preconditions(lib, dev):
     import hipfetch
     E, C, K, H = 256, 16, 8, 256
