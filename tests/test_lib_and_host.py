@@ -53,6 +53,21 @@ def test_preconditions_are_rejected_without_launching(lib):
     assert c.moe_route_resolve(16, 16, None, bf16, 2048, 256, 8, 1, 1, 1, 1, 1, 1, 7, 1, 1, 1, 1,
                                1, None, None) == -1
     assert b"exceeds the cache capacity" in c.moe_last_error()
+    # the three-launch decode layer: packed records of hidden % 512 == 0, top_k <= 16,
+    # records that hold the layout, a workspace that holds the activations
+    def rff(hidden=2048, top_k=8, cap=50, record_bytes=3146496, inter=512, pool=256, ws=1 << 20,
+            wbytes=1 << 20):
+        return c.moe_route_fetch_ffn(16, 16, None, bf16, hidden, 256, top_k, 1, 1, 1, 1, 1, 1,
+                                     cap, 1, 1, 1, 1, 1, None, pool, 256, record_bytes, inter, 4,
+                                     None, None, 256, ws, wbytes, None)
+    for kw, msg in ((dict(hidden=1024 + 256), b"multiple of 512"),
+                    (dict(top_k=17, cap=64), b"top_k"),
+                    (dict(top_k=9, cap=8), b"exceeds the cache capacity"),
+                    (dict(record_bytes=3146496 - 256), b"must hold"),
+                    (dict(pool=264), b"256-byte aligned"),
+                    (dict(wbytes=8 * 512 * 4 - 4), b"workspace")):
+        assert rff(**kw) == -1, msg
+        assert msg in c.moe_last_error(), (msg, c.moe_last_error())
     # tile-order pairs: K a multiple of 128, whole 16-row groups, 16-byte aligned
     FetchPair = __import__("hipfetch").FetchPair
     for src, dst, nbytes, tile_k, msg in ((0x1000, 0x2000, 16 * 256, 192, b"multiple of 128"),
