@@ -335,6 +335,204 @@ __global__ __launch_bounds__(kStepThreads) void route_fetch_gateup_kernel(
   }
 }
 
+// The drop-in's fetch + gate/up (moe_fetch_ffn): the reference's four
+// buffers per expert (w13, w2 row-major on the host, written in tile order
+// to the cache; s13, s2 raw), the miss list from the resolve launch before
+// it.  Fetch workgroups take the misses' w13 as units (16 gate + 16 up rows
+// of 16 intermediate columns, 2 H/512 tile pieces, each transposed through
+// LDS as moe_fetch writes it) and run the gate/up MFMAs on the transposed
+// piece in LDS before it is overwritten; the other buffers' pieces are
+// plain moe_fetch pieces.  Hit workgroups do a hit's unit from its slot.
+// Same arithmetic as route_fetch_gateup_kernel.
+__global__ __launch_bounds__(kStepThreads) void fetch_gateup_kernel(
+    FetchArgs a, int32_t nfetch, const int32_t* __restrict__ fetch_expert,
+    const int32_t* __restrict__ fetch_slot, const int32_t* __restrict__ nmiss_ptr,
+    int32_t max_jobs, const int32_t* __restrict__ slots, int32_t top_k,
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ w13c,
+    const float* __restrict__ s13c, int64_t w13_es, int64_t s13_es, int32_t hidden,
+    int32_t inter, float* __restrict__ act) {
+  __shared__ u32x4 stage[16 * 33];
+  __shared__ __align__(16) uint8_t xq[kGemvMaxHidden];
+  __shared__ float xs[kGemvMaxHidden / 128];
+  __shared__ __align__(16) float dpart[2][kGemvMaxHidden / 128][16];
+  __shared__ __align__(16) float upsum[16];
+  __shared__ float swl[2][64];
+  __shared__ int32_t job_e[kMaxTopK], job_s[kMaxTopK], job_k[kMaxTopK], job_n;
+  __shared__ int32_t pick_slot[kMaxTopK];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int q = lane >> 4;
+  const int gb = hidden / 128;
+  const int kq = hidden / 512;
+  const int units = inter / 16;
+  if (wave == 0) {
+    // the miss list and the picks' slots; a pick missed when its slot is in
+    // the list (one call's slots are distinct)
+    const int nm = min(*nmiss_ptr, max_jobs);
+    const int32_t fe = fetch_expert[min(lane, max_jobs - 1)];
+    const int32_t fs = fetch_slot[min(lane, max_jobs - 1)];
+    const int32_t sl = slots[min(lane, top_k - 1)];
+    bool miss = false;
+    int32_t kk = 0;
+    for (int j = 0; j < nm; ++j) miss |= __builtin_amdgcn_readlane(fs, j) == sl;
+    for (int k = 0; k < top_k; ++k)
+      if (__builtin_amdgcn_readlane(sl, k) == fs) kk = k;
+    if (lane < nm) {
+      job_e[lane] = fe;
+      job_s[lane] = fs;
+      job_k[lane] = kk;
+    }
+    if (lane < top_k) pick_slot[lane] = miss ? -1 : sl;
+    if (lane == 0) job_n = nm;
+  } else {
+    constexpr int NC = kGemvMaxHidden / 512;
+    uint4 raw[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int i = c * 512 + lane * 8;
+      raw[c] = *reinterpret_cast<const uint4*>(x + (i < hidden ? i : 0));
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      if (c * 512 < hidden) quantize_x8(raw[c], c * 512 + lane * 8 < hidden, c * 512 + lane * 8, xq, xs);
+  }
+  __syncthreads();
+  if (static_cast<int>(blockIdx.x) >= nfetch) {
+    const int hb = static_cast<int>(blockIdx.x) - nfetch;
+    const int k = hb / units;
+    const int t = hb - k * units;
+    if (k >= top_k) return;
+    const int32_t s = uniform(pick_slot[k]);
+    if (s < 0) return;
+    const int gr = t + wave * units;
+    const uint8_t* base = w13c + s * w13_es + static_cast<int64_t>(gr) * 16 * hidden + lane * 16;
+    const float* srow = s13c + s * s13_es + (gr >> 3) * gb;
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    for (int b0 = 0; b0 < gb; b0 += kHitChunk) {
+      float sw[kHitChunk];
+      v8i av[kHitChunk];
+#pragma unroll
+      for (int c = 0; c < kHitChunk; ++c) sw[c] = srow[min(b0 + c, gb - 1)];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < kHitChunk; ++c) av[c] = load_op_nt(base + min(b0 + c, gb - 1) * 2048, 1024);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < kHitChunk; ++c) {
+        const int b = b0 + c;
+        if (b < gb) {
+          const v4f z = {0.f, 0.f, 0.f, 0.f};
+          const v4f dd = mfma_e4m3_16x16x128(av[c], load_op32(xq + b * 128 + q * 32), z);
+          block_fma(acc, dd, sw[c] * xs[b]);
+        }
+      }
+    }
+    if (wave == 1) *reinterpret_cast<float4*>(&upsum[4 * q]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    __syncthreads();
+    if (wave == 0 && (lane & 15) == 0) {
+      const float4 u = *reinterpret_cast<const float4*>(&upsum[4 * q]);
+      *reinterpret_cast<float4*>(act + static_cast<int64_t>(k) * inter + 16 * t + 4 * q) =
+          make_float4(silu_mul(acc[0], u.x), silu_mul(acc[1], u.y), silu_mul(acc[2], u.z),
+                      silu_mul(acc[3], u.w));
+    }
+    return;
+  }
+  // fetch workgroup b of G: its units (round robin), then its plain pieces
+  // (those of the buffers after w13: first 8 to each workgroup with one unit
+  // fewer, then round robin), as in route_fetch_gateup_kernel
+  const int nm = uniform(job_n);
+  const int G = nfetch;
+  const int b = static_cast<int>(blockIdx.x);
+  const int U = nm * units;
+  const int plain = static_cast<int>(a.pieces_per_job - a.pieces[0]);
+  const int P = nm * plain;
+  const int r = U % G;
+  const int A = r > 0 ? min(P, 8 * (G - r)) : 0;
+  const int np = 2 * kq;
+  const int nu = U > b ? (U - 1 - b) / G + 1 : 0;
+  const uint32_t upr = a.tile_upr[0];      // 16-byte units per w13 row: H / 16
+  const int64_t rec0 = a.bytes[0];
+  for (int ui = 0; ui < nu; ++ui) {
+    const int u = b + ui * G;
+    const int j = u / units;
+    const int t = u - j * units;
+    const int32_t e = uniform(job_e[j]);
+    const int32_t s = uniform(job_s[j]);
+    const int grw = t + wave * units;
+    const float sw = reinterpret_cast<const float*>(a.src[2] + e * a.bytes[2])[(grw >> 3) * gb +
+                                                                              min(lane, gb - 1)];
+    const u32x4* srcv = reinterpret_cast<const u32x4*>(a.src[0] + e * rec0);
+    u32x4* dstv = reinterpret_cast<u32x4*>(a.dst[0] + s * rec0);
+    for (int p = 0; p < np; ++p) {
+      const int tw = p / kq;
+      const int q4 = p - tw * kq;
+      const uint32_t g16 = static_cast<uint32_t>(t + tw * units);   // 16-row group of w13
+      const uint32_t jw = static_cast<uint32_t>(q4) * 32;            // first column unit
+      const u32x4* sv = srcv + static_cast<int64_t>(g16) * 16 * upr + jw;
+      u32x4* dv = dstv + (static_cast<int64_t>(g16) * upr + jw) * 16;
+      u32x4 v[4];
+#pragma unroll
+      for (int uu = 0; uu < 4; ++uu) {
+        const uint32_t i = threadIdx.x + uu * kStepThreads;
+        v[uu] = __builtin_nontemporal_load(sv + (i >> 5) * upr + (i & 31));
+      }
+#pragma unroll
+      for (int uu = 0; uu < 4; ++uu) {
+        const uint32_t i = threadIdx.x + uu * kStepThreads;
+        stage[(i >> 5) * 33 + (i & 31)] = v[uu];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int uu = 0; uu < 4; ++uu) {
+        // destination unit dd = (2 bb + h) * 64 + 16 qq + rr: row rr, column unit 8 bb + 2 qq + h
+        const uint32_t dd = threadIdx.x + uu * kStepThreads;
+        const uint32_t bh = dd >> 6, qq = (dd >> 4) & 3, rr = dd & 15;
+        dv[dd] = stage[rr * 33 + (bh >> 1) * 8 + 2 * qq + (bh & 1)];
+      }
+      // this wave's K-blocks 2 wave, 2 wave + 1 of the piece: A from the
+      // transposed rows in LDS (lane 16q + r: row r, units 8 bl + 2q, + 1)
+#pragma unroll
+      for (int bl2 = 0; bl2 < 2; ++bl2) {
+        const int bl = 2 * wave + bl2;
+        const u32x4 lo = stage[(lane & 15) * 33 + 8 * bl + 2 * q];
+        const u32x4 hi = stage[(lane & 15) * 33 + 8 * bl + 2 * q + 1];
+        const v8i av = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
+                        (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        const int gbk = 4 * q4 + bl;
+        const v4f z = {0.f, 0.f, 0.f, 0.f};
+        const v4f dd = mfma_e4m3_16x16x128(av, load_op32(xq + gbk * 128 + q * 32), z);
+        *reinterpret_cast<float4*>(&dpart[tw][gbk][4 * q]) = make_float4(dd[0], dd[1], dd[2], dd[3]);
+      }
+      if (p == 0) swl[wave][lane] = sw;
+      __syncthreads();
+    }
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    for (int gbk = 0; gbk < gb; ++gbk) {
+      const float4 dd = *reinterpret_cast<const float4*>(&dpart[wave][gbk][4 * q]);
+      const v4f dv = {dd.x, dd.y, dd.z, dd.w};
+      block_fma(acc, dv, swl[wave][gbk] * xs[gbk]);
+    }
+    if (wave == 1)
+      *reinterpret_cast<float4*>(&upsum[4 * q]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    __syncthreads();
+    if (wave == 0 && (lane & 15) == 0) {
+      const int kk = uniform(job_k[j]);
+      const float4 uu = *reinterpret_cast<const float4*>(&upsum[4 * q]);
+      *reinterpret_cast<float4*>(act + static_cast<int64_t>(kk) * inter + 16 * t + 4 * q) =
+          make_float4(silu_mul(acc[0], uu.x), silu_mul(acc[1], uu.y), silu_mul(acc[2], uu.z),
+                      silu_mul(acc[3], uu.w));
+    }
+    __syncthreads();
+  }
+  const int na = (r > 0 && b >= r && A > b - r) ? (A - 1 - (b - r)) / (G - r) + 1 : 0;
+  const int nb = P > A + b ? (P - 1 - A - b) / G + 1 : 0;
+  for (int n = 0; n < na + nb; ++n) {
+    const int gi = n < na ? (b - r) + n * (G - r) : A + b + (n - na) * G;
+    const int j = gi / plain;
+    fetch_piece(a, a.pieces[0] + (gi - j * plain), uniform(job_e[j]), uniform(job_s[j]), stage);
+  }
+}
+
 }  // namespace moe
 
 using namespace moe;
@@ -448,9 +646,76 @@ extern "C" int moe_route_fetch_ffn(const void* x, const void* w, const float* bi
   rc = check_launch("moe_route_fetch_ffn(route+fetch+gate/up)");
   if (rc) return rc;
   const uint8_t* cb = static_cast<const uint8_t*>(cache);
-  return launch_down_gemv(act, out_slot, weights, 1, top_k, cb + w13,
+  return launch_down_gemv(act, out_slot, weights, 0, 1, top_k, cb + w13,
                           reinterpret_cast<const float*>(cb + off_s2), record_bytes,
                           record_bytes / 4, MOE_LAYOUT_TILES, cap, hidden, inter,
                           static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out),
                           shared ? &sh : nullptr, s);
+}
+
+extern "C" int moe_fetch_ffn(const moe_fetch_pair* pairs, int32_t npairs,
+                             const int32_t* fetch_expert, const int32_t* fetch_slot,
+                             const int32_t* nmiss, int32_t max_jobs, int32_t blocks_per_job,
+                             const void* x, const int32_t* slots, const void* weights,
+                             int32_t w_dtype, int32_t top_k, const void* w13, const float* s13,
+                             const void* w2, const float* s2, int32_t n_slots, int32_t hidden,
+                             int32_t inter, const moe_expert_strides* strides,
+                             const void* residual, void* out, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  MOE_REQUIRE(pairs && fetch_expert && fetch_slot && nmiss && x && slots && weights && w13 &&
+                  s13 && w2 && s2 && strides && out && workspace,
+              "moe_fetch_ffn: NULL pointer");
+  MOE_REQUIRE(npairs == 4, "moe_fetch_ffn: takes the four buffers w13, w2, s13, s2 (got %d)",
+              npairs);
+  MOE_REQUIRE(w_dtype == MOE_F32 || w_dtype == MOE_BF16,
+              "moe_fetch_ffn: w_dtype must be MOE_F32 or MOE_BF16");
+  MOE_REQUIRE(hidden >= 512 && hidden % 512 == 0 && hidden <= kGemvMaxHidden,
+              "moe_fetch_ffn: hidden must be a multiple of 512 up to %d (got %d)", kGemvMaxHidden,
+              hidden);
+  MOE_REQUIRE(inter >= 128 && inter % 128 == 0 && inter <= kGemvMaxInter,
+              "moe_fetch_ffn: inter must be a multiple of 128 up to %d (got %d)", kGemvMaxInter,
+              inter);
+  MOE_REQUIRE(top_k >= 1 && top_k <= kGemvMaxTopK && top_k <= n_slots && n_slots >= 1,
+              "moe_fetch_ffn: need 1 <= top_k <= min(%d, n_slots)", kGemvMaxTopK);
+  MOE_REQUIRE(max_jobs >= top_k && max_jobs <= kMaxTopK,
+              "moe_fetch_ffn: need top_k <= max_jobs <= %d", kMaxTopK);
+  MOE_REQUIRE(strides->layout == MOE_LAYOUT_TILES,
+              "moe_fetch_ffn: the cache must hold w13/w2 in tile order");
+  const int64_t w13b = 2LL * inter * hidden;
+  const int64_t s13b = (2LL * inter / 128) * (hidden / 128) * 4;
+  MOE_REQUIRE(pairs[0].bytes == w13b && pairs[0].tile_k == hidden,
+              "moe_fetch_ffn: pair 0 must be w13 (%lld bytes, tile_k = hidden)", (long long)w13b);
+  MOE_REQUIRE(pairs[1].bytes == static_cast<int64_t>(hidden) * inter && pairs[1].tile_k == inter,
+              "moe_fetch_ffn: pair 1 must be w2 (tile_k = inter)");
+  MOE_REQUIRE(pairs[2].bytes == s13b && pairs[2].tile_k == 0,
+              "moe_fetch_ffn: pair 2 must be s13 (%lld bytes, a byte copy)", (long long)s13b);
+  MOE_REQUIRE(pairs[0].dst == w13 && pairs[2].dst == s13 && strides->w13 == w13b &&
+                  strides->s13 == s13b / 4,
+              "moe_fetch_ffn: the w13 and s13 pairs must fill the cache buffers w13 and s13 "
+              "(dense, one expert after another)");
+  MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0, "moe_fetch_ffn: x must be 16-byte aligned");
+  MOE_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
+                  workspace_bytes >= static_cast<size_t>(top_k) * inter * sizeof(float),
+              "moe_fetch_ffn: the workspace must be 16-byte aligned and hold top_k * inter "
+              "floats");
+  MOE_REQUIRE(blocks_per_job >= 1 && blocks_per_job <= 4096,
+              "moe_fetch_ffn: need 1 <= blocks_per_job <= 4096");
+  FetchArgs a;
+  const int rc0 = fetch_args(pairs, npairs, max_jobs, &a);
+  if (rc0 != MOE_OK) return rc0;
+  MOE_REQUIRE(a.tile_wlog[0] == 5, "moe_fetch_ffn: w13 pieces must be 32 column units wide");
+  hipStream_t s = as_stream(stream);
+  const int nfetch = blocks_per_job * (max_jobs < kFetchMaxJobsInGrid ? max_jobs : kFetchMaxJobsInGrid);
+  float* act = static_cast<float*>(workspace);
+  hipLaunchKernelGGL(fetch_gateup_kernel, dim3(nfetch + top_k * (inter / 16)), dim3(kStepThreads),
+                     0, s, a, nfetch, fetch_expert, fetch_slot, nmiss, max_jobs, slots, top_k,
+                     static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(w13), s13,
+                     strides->w13, strides->s13, hidden, inter, act);
+  const int rc = check_launch("moe_fetch_ffn(fetch+gate/up)");
+  if (rc) return rc;
+  return launch_down_gemv(act, slots, weights, w_dtype == MOE_BF16 ? 1 : 0, 1, top_k,
+                          static_cast<const uint8_t*>(w2), s2, strides->w2, strides->s2,
+                          MOE_LAYOUT_TILES, n_slots, hidden, inter,
+                          static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out),
+                          nullptr, s);
 }

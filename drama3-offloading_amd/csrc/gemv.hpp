@@ -29,12 +29,12 @@ constexpr int kGemvMaxTopK = 16;
 // down_gemv_kernel over `tokens` tokens of top_k pairs each: out[t] =
 // bf16(residual[t] + bf16(sum_k fma-in-order weights[t,k] * y_k)) (no
 // residual: the bf16 sum), y_k = W2[slots[t,k]] . quantised act[t*top_k+k];
-// act [pairs, inter] f32, slots int32, weights f32; w2 / s2 with expert
-// strides w2_es bytes / s2_es floats, tile order when `tiled`.  With `sh`,
+// act [pairs, inter] f32, slots int32, weights f32 (bf16 when wbf16); w2 /
+// s2 with expert strides w2_es bytes / s2_es floats, tile order when `tiled`.  With `sh`,
 // the shared expert's down rows ride along (its act and sig formed before)
 // and out = residual + (routed + sig * shared), as the block call gives.
 // Launch errors are returned (check_launch).
-int launch_down_gemv(const float* act, const int32_t* slots, const float* weights,
+int launch_down_gemv(const float* act, const int32_t* slots, const void* weights, int wbf16,
                      int32_t tokens, int32_t top_k, const uint8_t* w2, const float* s2,
                      int64_t w2_es, int64_t s2_es, int tiled, int32_t n_slots, int32_t hidden,
                      int32_t inter, const uint16_t* residual, uint16_t* out,

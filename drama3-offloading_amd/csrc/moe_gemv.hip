@@ -508,19 +508,20 @@ static int launch_gemv(const uint16_t* x, const void* ids, int ids64, const void
   return check_launch("moe_fp8_moe_forward(down)");
 }
 
-int launch_down_gemv(const float* act, const int32_t* slots, const float* weights,
+int launch_down_gemv(const float* act, const int32_t* slots, const void* weights, int wbf16,
                      int32_t tokens, int32_t top_k, const uint8_t* w2, const float* s2,
                      int64_t w2_es, int64_t s2_es, int tiled, int32_t n_slots, int32_t hidden,
                      int32_t inter, const uint16_t* residual, uint16_t* out,
                      const SharedRefs* sh, hipStream_t s) {
   if (sh) {
     hipLaunchKernelGGL(down_gemv_kernel<true>, dim3(hidden / kDownRows, tokens),
-                       dim3(64 * ((top_k + 1) / 2 + 1)), 0, s, act, slots, 0, weights, 0, top_k,
-                       w2, s2, w2_es, s2_es, tiled, n_slots, hidden, inter, residual, out, *sh);
+                       dim3(64 * ((top_k + 1) / 2 + 1)), 0, s, act, slots, 0, weights, wbf16,
+                       top_k, w2, s2, w2_es, s2_es, tiled, n_slots, hidden, inter, residual, out,
+                       *sh);
   } else {
     hipLaunchKernelGGL(down_gemv_kernel<false>, dim3(hidden / kDownRows, tokens),
-                       dim3(64 * ((top_k + 1) / 2)), 0, s, act, slots, 0, weights, 0, top_k, w2,
-                       s2, w2_es, s2_es, tiled, n_slots, hidden, inter, residual, out,
+                       dim3(64 * ((top_k + 1) / 2)), 0, s, act, slots, 0, weights, wbf16, top_k,
+                       w2, s2, w2_es, s2_es, tiled, n_slots, hidden, inter, residual, out,
                        SharedRefs{});
   }
   return check_launch("down_gemv_kernel");

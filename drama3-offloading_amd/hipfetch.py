@@ -89,6 +89,9 @@ SIGNATURES = {
                                       _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                       _vp, C.c_int64, _i32, _i32, C.POINTER(SharedExpert), _vp,
                                       _vp, _vp, _sz, _vp]),
+    "moe_fetch_ffn": (C.c_int, [C.POINTER(FetchPair), _i32, _vp, _vp, _vp, _i32, _i32, _vp,
+                                _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _i32,
+                                C.POINTER(ExpertStrides), _vp, _vp, _vp, _sz, _vp]),
     "moe_fp8_moe_workspace": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "moe_fp8_moe_forward": (C.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
                                       _i32, _i32, _i32, _vp, _vp, _sz, _vp]),
@@ -439,6 +442,39 @@ class Native:
             pool_dev_ptr, cache.data_ptr(), cache.shape[1], inter, blocks_per_job, se,
             self._ptr(residual), out.data_ptr(), workspace.data_ptr(),
             workspace.numel() * workspace.element_size(), self.stream()), what)
+
+    def fetch_ffn(self, pairs, fetch_expert, fetch_slot, nmiss, max_jobs: int,
+                  blocks_per_job: int, x, slots, weights, w13, s13, w2, s2, out, workspace,
+                  residual=None) -> None:
+        """moe_fetch of the four buffers (w13, w2, s13, s2 pairs, w13/w2 in tile
+        order) and the expert FFN of one token on the cache slots
+        (moe_fetch_ffn); out [1, H] bf16 = residual + MoE(x)."""
+        import torch
+        what = "moe_fetch_ffn"
+        self._on_gpu(what, fetch_expert, fetch_slot, nmiss, x, slots, weights, w13, s13, w2, s2,
+                     out, workspace, residual)
+        if x.dim() != 2 or x.shape[0] != 1:
+            raise ValueError(f"{what} takes exactly one token")
+        H = x.shape[1]
+        K = slots.numel()
+        self._buf(what, "x", x, H, torch.bfloat16)
+        self._buf(what, "slots", slots, K, torch.int32)
+        self._buf(what, "weights", weights, K, torch.float32, torch.bfloat16)
+        for name, t in (("fetch_expert", fetch_expert), ("fetch_slot", fetch_slot)):
+            self._buf(what, name, t, max_jobs, torch.int32)
+        self._buf(what, "nmiss", nmiss, 1, torch.int32)
+        self._buf(what, "out", out, H, torch.bfloat16)
+        self._buf(what, "residual", residual, H, torch.bfloat16)
+        self._buf(what, "workspace", workspace, 0)
+        es = _expert_strides(w13, s13, w2, s2, LAYOUT_TILES)
+        arr = (FetchPair * len(pairs))(*[FetchPair(*((tuple(p) + (0,))[:4])) for p in pairs])
+        self._check(self.cdll.moe_fetch_ffn(
+            arr, len(pairs), fetch_expert.data_ptr(), fetch_slot.data_ptr(), nmiss.data_ptr(),
+            max_jobs, blocks_per_job, x.data_ptr(), slots.data_ptr(), weights.data_ptr(),
+            self._dtype_code(weights), K, w13.data_ptr(), s13.data_ptr(), w2.data_ptr(),
+            s2.data_ptr(), w13.shape[0], H, w2.shape[-1], C.byref(es), self._ptr(residual),
+            out.data_ptr(), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+            self.stream()), what)
 
     # ------------------------------------------------------------ experts
     def fp8_moe_workspace(self, tokens, top_k, n_experts, hidden, inter) -> int:

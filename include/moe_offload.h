@@ -257,6 +257,32 @@ int moe_route_fetch_ffn(const void* x, const void* w, const float* bias, int32_t
                         const struct moe_shared_expert* shared, const void* residual, void* out,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* The drop-in's fetch and expert FFN of one token: moe_fetch of the four
+ * buffers (pairs in the order w13, w2, s13, s2, as the reference's
+ * _cpp_fetch copies them, w13 and w2 with tile_k set so the cache holds
+ * them in tile order) followed by moe_fp8_moe_forward_ex(x, slots, weights,
+ * w13, s13, w2, s2, strides) on the cache, in two launches instead of three,
+ * with the same outputs bit for bit.  The workgroups that fetch a miss's
+ * gate and up rows run its gate/up MFMAs on each piece while it sits
+ * transposed in LDS; the hits' gate/up runs beside the fetch.  slots
+ * [top_k] int32 are the resolve's out_slot (every slot below n_slots), the
+ * miss list its fetch_slot/fetch_expert/nmiss (max_jobs entries, top_k <=
+ * max_jobs <= 32), weights [top_k] w_dtype MOE_F32/MOE_BF16, out [hidden]
+ * bf16 = bf16(residual + bf16(MoE(x))) (residual nullable), the workspace
+ * top_k * inter floats.  Constraints: those of moe_route_fetch_ffn on
+ * hidden, inter and top_k; the w13/s13 pairs fill the cache buffers w13/s13
+ * (dense); strides->layout MOE_LAYOUT_TILES.  Replaces fetch_experts +
+ * fp8_moe_forward in dev_cached_forward (bin/devcache.py:270-277); no
+ * single counterpart. */
+int moe_fetch_ffn(const moe_fetch_pair* pairs, int32_t npairs, const int32_t* fetch_expert,
+                  const int32_t* fetch_slot, const int32_t* nmiss, int32_t max_jobs,
+                  int32_t blocks_per_job, const void* x, const int32_t* slots,
+                  const void* weights, int32_t w_dtype, int32_t top_k, const void* w13,
+                  const float* s13, const void* w2, const float* s2, int32_t n_slots,
+                  int32_t hidden, int32_t inter, const struct moe_expert_strides* strides,
+                  const void* residual, void* out, void* workspace, size_t workspace_bytes,
+                  void* stream);
+
 /* ------------------------------------------------------- expert compute */
 
 /* Workspace bytes moe_fp8_moe_forward needs for this shape. */

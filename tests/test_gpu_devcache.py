@@ -61,6 +61,39 @@ def test_cache_is_bit_exact_against_resident(lib, dev, pair, cap, tiles, monkeyp
     assert hits + misses == 40 * K and (cap >= E or misses > cap)
 
 
+@pytest.mark.parametrize("cap,wdtype", [(16, torch.bfloat16), (E, torch.float32), (9, torch.float32)])
+def test_hook_fetch_ffn_is_bit_exact_against_resident(lib, dev, pair, cap, wdtype, monkeypatch):
+    """dev_cached_forward through moe_fetch_ffn (the misses' gate/up run by
+    the workgroups that fetch them, the hits' beside them) against the
+    all-resident forward, bit for bit, and the slots' bytes in tile order."""
+    import devcache
+    import offload
+    from fp8_moe import fp8_moe_forward
+    from hostpool import to_tiles
+    ref, host = pair
+    monkeypatch.setattr(offload, "DEVICE_TILES", True)
+    monkeypatch.setattr(devcache, "FUSED_FFN", True)
+    devcache.init_dev_cache(host, dev, cap)
+    torch.manual_seed(100 + cap)
+    say(f"devcache fetch_ffn: capacity {cap}, weights {wdtype}")
+    for step in range(40):
+        x = torch.randn(1, H, device=dev).to(torch.bfloat16)
+        ids = torch.randperm(E, device=dev)[:K].unsqueeze(0)
+        w = torch.rand(1, K, device=dev).to(wdtype)
+        w = w / w.sum(-1, keepdim=True)
+        want = fp8_moe_forward(x, ids, w, ref.w13_weight, ref.w13_scale_inv, ref.w2_weight,
+                               ref.w2_scale_inv)
+        got = devcache.dev_cached_forward(host, x, ids, w)
+        assert torch.equal(want, got), f"step {step}"
+    for s_, e in enumerate(host._dc_slot_expert.tolist()):
+        for c, h in ((host._dc_w13, host.w13_weight), (host._dc_w2, host.w2_weight)):
+            assert torch.equal(c[s_].view(torch.uint8).cpu(), to_tiles(h[e].view(torch.uint8))), (s_, e)
+        assert torch.equal(host._dc_s13[s_].cpu(), host.w13_scale_inv[e])
+        assert torch.equal(host._dc_s2[s_].cpu(), host.w2_scale_inv[e])
+    hits, misses = devcache.cache_stats(host)
+    assert hits + misses == 40 * K and (cap >= E or misses > cap)
+
+
 def test_capture_dynamic_and_bytes(lib, dev, pair):
     import devcache
     from fp8_moe import fp8_moe_forward
