@@ -349,8 +349,8 @@ __global__ __launch_bounds__(kStepThreads) void fetch_gateup_kernel(
     const int32_t* __restrict__ fetch_slot, const int32_t* __restrict__ nmiss_ptr,
     int32_t max_jobs, const int32_t* __restrict__ slots, int32_t top_k,
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ w13c,
-    const float* __restrict__ s13c, int64_t w13_es, int64_t s13_es, int32_t hidden,
-    int32_t inter, float* __restrict__ act) {
+    const float* __restrict__ s13c, int64_t w13_es, int64_t s13_es, int32_t n_slots,
+    int32_t hidden, int32_t inter, float* __restrict__ act) {
   __shared__ u32x4 stage[16 * 33];
   __shared__ __align__(16) uint8_t xq[kGemvMaxHidden];
   __shared__ float xs[kGemvMaxHidden / 128];
@@ -403,7 +403,8 @@ __global__ __launch_bounds__(kStepThreads) void fetch_gateup_kernel(
     const int t = hb - k * units;
     if (k >= top_k) return;
     const int32_t s = uniform(pick_slot[k]);
-    if (s < 0) return;
+    // a miss, or no such slot (the down launch poisons that pick's output)
+    if (s < 0 || s >= n_slots) return;
     const int gr = t + wave * units;
     const uint8_t* base = w13c + s * w13_es + static_cast<int64_t>(gr) * 16 * hidden + lane * 16;
     const float* srow = s13c + s * s13_es + (gr >> 3) * gb;
@@ -710,7 +711,7 @@ extern "C" int moe_fetch_ffn(const moe_fetch_pair* pairs, int32_t npairs,
   hipLaunchKernelGGL(fetch_gateup_kernel, dim3(nfetch + top_k * (inter / 16)), dim3(kStepThreads),
                      0, s, a, nfetch, fetch_expert, fetch_slot, nmiss, max_jobs, slots, top_k,
                      static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(w13), s13,
-                     strides->w13, strides->s13, hidden, inter, act);
+                     strides->w13, strides->s13, n_slots, hidden, inter, act);
   const int rc = check_launch("moe_fetch_ffn(fetch+gate/up)");
   if (rc) return rc;
   return launch_down_gemv(act, slots, weights, w_dtype == MOE_BF16 ? 1 : 0, 1, top_k,
