@@ -453,6 +453,29 @@ __global__ __launch_bounds__(kStepThreads) void fetch_gateup_kernel(
   const int nu = U > b ? (U - 1 - b) / G + 1 : 0;
   const uint32_t upr = a.tile_upr[0];      // 16-byte units per w13 row: H / 16
   const int64_t rec0 = a.bytes[0];
+  // unit piece p of the workgroup's unit ui: its host rows (lane's loads) and
+  // its cache run; live == false reads the same offsets of the cache (the
+  // loads stay unconditional: behind a branch, the compiler's wait at the
+  // join would cover them)
+  auto piece_src = [&](int ui, int p, bool live) -> const u32x4* {
+    const int u = b + ui * G;
+    const int j = u / units;
+    const int t = u - j * units;
+    const int tw = p / kq;
+    const int q4 = p - tw * kq;
+    const uint32_t g16 = static_cast<uint32_t>(t + tw * units);
+    const char* base = live ? a.src[0] + uniform(job_e[min(j, nm - 1)]) * rec0 : a.dst[0];
+    return reinterpret_cast<const u32x4*>(base) + static_cast<int64_t>(g16) * 16 * upr + q4 * 32;
+  };
+  auto load_piece = [&](const u32x4* sv, u32x4 (&v)[4]) {
+#pragma unroll
+    for (int uu = 0; uu < 4; ++uu) {
+      const uint32_t i = threadIdx.x + uu * kStepThreads;
+      v[uu] = __builtin_nontemporal_load(sv + (i >> 5) * upr + (i & 31));
+    }
+  };
+  u32x4 v[4];
+  if (nu > 0) load_piece(piece_src(0, 0, true), v);
   for (int ui = 0; ui < nu; ++ui) {
     const int u = b + ui * G;
     const int j = u / units;
@@ -462,27 +485,26 @@ __global__ __launch_bounds__(kStepThreads) void fetch_gateup_kernel(
     const int grw = t + wave * units;
     const float sw = reinterpret_cast<const float*>(a.src[2] + e * a.bytes[2])[(grw >> 3) * gb +
                                                                               min(lane, gb - 1)];
-    const u32x4* srcv = reinterpret_cast<const u32x4*>(a.src[0] + e * rec0);
     u32x4* dstv = reinterpret_cast<u32x4*>(a.dst[0] + s * rec0);
     for (int p = 0; p < np; ++p) {
       const int tw = p / kq;
       const int q4 = p - tw * kq;
       const uint32_t g16 = static_cast<uint32_t>(t + tw * units);   // 16-row group of w13
-      const uint32_t jw = static_cast<uint32_t>(q4) * 32;            // first column unit
-      const u32x4* sv = srcv + static_cast<int64_t>(g16) * 16 * upr + jw;
-      u32x4* dv = dstv + (static_cast<int64_t>(g16) * upr + jw) * 16;
-      u32x4 v[4];
-#pragma unroll
-      for (int uu = 0; uu < 4; ++uu) {
-        const uint32_t i = threadIdx.x + uu * kStepThreads;
-        v[uu] = __builtin_nontemporal_load(sv + (i >> 5) * upr + (i & 31));
-      }
+      u32x4* dv = dstv + (static_cast<int64_t>(g16) * upr + q4 * 32) * 16;
 #pragma unroll
       for (int uu = 0; uu < 4; ++uu) {
         const uint32_t i = threadIdx.x + uu * kStepThreads;
         stage[(i >> 5) * 33 + (i & 31)] = v[uu];
       }
       __syncthreads();
+      // the piece is in LDS: the next one's loads go out now, into the same
+      // registers, while this one is stored and multiplied (one piece in
+      // flight per workgroup, as in the fetch kernel)
+      {
+        const bool in_unit = p + 1 < np;
+        load_piece(piece_src(in_unit ? ui : ui + 1, in_unit ? p + 1 : 0, in_unit || ui + 1 < nu),
+                   v);
+      }
 #pragma unroll
       for (int uu = 0; uu < 4; ++uu) {
         // destination unit dd = (2 bb + h) * 64 + 16 qq + rr: row rr, column unit 8 bb + 2 qq + h
