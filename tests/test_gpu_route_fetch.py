@@ -78,7 +78,9 @@ def test_route_fetch_equals_route_resolve_then_fetch(lib, dev, shape):
     dict(capacity=20),
     dict(n_experts=320, top_k=12, hidden=512, inter=256, capacity=272, ffn_blocks_per_job=2),
     dict(n_experts=64, top_k=4, hidden=512, inter=128, capacity=5, ffn_blocks_per_job=1),
-], ids=["drama3", "wide", "tight"])
+    # the limits: 1024 experts and slots, top-16 (16 jobs over the grid's 8)
+    dict(n_experts=1024, top_k=16, hidden=1024, inter=128, capacity=1024, ffn_blocks_per_job=2),
+], ids=["drama3", "wide", "tight", "limits"])
 def test_route_fetch_ffn_equals_separate_launches(lib, dev, shape):
     """moe_route_fetch_ffn (three launches: the misses' gate/up inside the
     fetch, the hits' beside it) against moe_route_resolve + moe_fetch +
