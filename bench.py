@@ -383,7 +383,11 @@ def contention(lib, pools, dev, gemv_calls: int = 2000, fetches: int = 40,
         res["gemv_us_per_call"]["beside_fetch_kernel"] / res["gemv_us_per_call"]["alone"], 4)
     res["gemv_slowdown_beside_copy_engine"] = round(
         res["gemv_us_per_call"]["beside_copy_engine"] / res["gemv_us_per_call"]["alone"], 4)
-    del graphs, rec
+    # nothing of the probe outlives it: the graphs (which address the
+    # pools), the views of the pools and the resident records go here,
+    # after the streams have drained, so the caller can free the pools
+    torch.cuda.synchronize(dev)
+    del graphs, rec, views, srcs, pairs, cache
     torch.cuda.empty_cache()
     return res
 
@@ -1086,6 +1090,7 @@ def run_probe(args) -> int:
         res = {"probe": "contention", **contention(lib, pools, dev)}
         for p in pools:
             p.close()
+        del pools
     elif args.probe == "copy":
         # a plain elementwise copy of known size: reads and writes 256 MiB,
         # the calibration for the HBM traffic counters
@@ -1105,6 +1110,7 @@ def run_probe(args) -> int:
                "GBps": round(8 * n / dt / 1e9, 1)}
     else:
         raise SystemExit(f"unknown probe {args.probe!r}")
+    torch.cuda.synchronize(dev)
     print(json.dumps(res), flush=True)
     return 0
 

@@ -79,7 +79,7 @@ class CodedPool:
                                                   scratch[:need], threads)
         self.coded_bytes = used
         self.raw_bytes = n * rb
-        self.ptr = lib.host_alloc(used, noncoherent=noncoherent)
+        self.ptr, self._host = lib.host_buffer(used, noncoherent=noncoherent)
         ctypes.memmove(self.ptr, scratch.ctypes.data, used)
         self.dev_ptr = lib.device_ptr_of(self.ptr)
         self.rec_off = torch.from_numpy(rec_off).to(device)
@@ -99,12 +99,8 @@ class CodedPool:
                              cache, workgroups)
 
     def close(self) -> None:
-        if self.ptr:
-            self.lib.host_free(self.ptr)
-            self.ptr = 0
-
-    def __del__(self):
-        try:
-            self.close()
-        except Exception:                                     # noqa: BLE001
-            pass
+        """Free the coded bytes (device addresses taken from the pool, such
+        as a captured graph's, are the caller's to retire first)."""
+        self._host = None
+        self.ptr = 0
+        self.dev_ptr = 0

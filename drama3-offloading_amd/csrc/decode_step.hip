@@ -359,7 +359,11 @@ __global__ __launch_bounds__(kStepThreads) void fetch_gateup_kernel(
   __shared__ __align__(16) float dpart[2][kGemvMaxHidden / 128][16];
   __shared__ __align__(16) float upsum[16];
   __shared__ float swl[2][64];
-  __shared__ int32_t job_e[kMaxTopK], job_s[kMaxTopK], job_k[kMaxTopK], job_n;
+  // job_km[j]: bit k set for every pick k whose slot is job j's (an expert
+  // repeated in the row takes one slot for all its picks, and its miss is
+  // queued once; every such pick reads the unit's activations)
+  __shared__ int32_t job_e[kMaxTopK], job_s[kMaxTopK], job_n;
+  __shared__ uint32_t job_km[kMaxTopK];
   __shared__ int32_t pick_slot[kMaxTopK];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -369,20 +373,20 @@ __global__ __launch_bounds__(kStepThreads) void fetch_gateup_kernel(
   const int units = inter / 16;
   if (wave == 0) {
     // the miss list and the picks' slots; a pick missed when its slot is in
-    // the list (one call's slots are distinct)
+    // the list (a repeated expert's picks all did)
     const int nm = min(*nmiss_ptr, max_jobs);
     const int32_t fe = fetch_expert[min(lane, max_jobs - 1)];
     const int32_t fs = fetch_slot[min(lane, max_jobs - 1)];
     const int32_t sl = slots[min(lane, top_k - 1)];
     bool miss = false;
-    int32_t kk = 0;
+    uint32_t km = 0;
     for (int j = 0; j < nm; ++j) miss |= __builtin_amdgcn_readlane(fs, j) == sl;
     for (int k = 0; k < top_k; ++k)
-      if (__builtin_amdgcn_readlane(sl, k) == fs) kk = k;
+      if (__builtin_amdgcn_readlane(sl, k) == fs) km |= 1u << k;
     if (lane < nm) {
       job_e[lane] = fe;
       job_s[lane] = fs;
-      job_k[lane] = kk;
+      job_km[lane] = km;
     }
     if (lane < top_k) pick_slot[lane] = miss ? -1 : sl;
     if (lane == 0) job_n = nm;
@@ -541,11 +545,16 @@ __global__ __launch_bounds__(kStepThreads) void fetch_gateup_kernel(
       *reinterpret_cast<float4*>(&upsum[4 * q]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
     __syncthreads();
     if (wave == 0 && (lane & 15) == 0) {
-      const int kk = uniform(job_k[j]);
+      uint32_t km = static_cast<uint32_t>(uniform(static_cast<int32_t>(job_km[j])));
       const float4 uu = *reinterpret_cast<const float4*>(&upsum[4 * q]);
-      *reinterpret_cast<float4*>(act + static_cast<int64_t>(kk) * inter + 16 * t + 4 * q) =
-          make_float4(silu_mul(acc[0], uu.x), silu_mul(acc[1], uu.y), silu_mul(acc[2], uu.z),
-                      silu_mul(acc[3], uu.w));
+      const float4 av = make_float4(silu_mul(acc[0], uu.x), silu_mul(acc[1], uu.y),
+                                    silu_mul(acc[2], uu.z), silu_mul(acc[3], uu.w));
+      // a queued slot no pick names (a caller's stale list) writes nothing
+      while (km) {
+        const int kk = __builtin_ctz(km);
+        km &= km - 1;
+        *reinterpret_cast<float4*>(act + static_cast<int64_t>(kk) * inter + 16 * t + 4 * q) = av;
+      }
     }
     __syncthreads();
   }
@@ -712,11 +721,19 @@ extern "C" int moe_fetch_ffn(const moe_fetch_pair* pairs, int32_t npairs,
               "moe_fetch_ffn: pair 0 must be w13 (%lld bytes, tile_k = hidden)", (long long)w13b);
   MOE_REQUIRE(pairs[1].bytes == static_cast<int64_t>(hidden) * inter && pairs[1].tile_k == inter,
               "moe_fetch_ffn: pair 1 must be w2 (tile_k = inter)");
+  const int64_t w2b = static_cast<int64_t>(hidden) * inter;
+  const int64_t s2b = (static_cast<int64_t>(hidden) / 128) * (inter / 128) * 4;
   MOE_REQUIRE(pairs[2].bytes == s13b && pairs[2].tile_k == 0,
               "moe_fetch_ffn: pair 2 must be s13 (%lld bytes, a byte copy)", (long long)s13b);
+  MOE_REQUIRE(pairs[3].bytes == s2b && pairs[3].tile_k == 0,
+              "moe_fetch_ffn: pair 3 must be s2 (%lld bytes, a byte copy)", (long long)s2b);
   MOE_REQUIRE(pairs[0].dst == w13 && pairs[2].dst == s13 && strides->w13 == w13b &&
                   strides->s13 == s13b / 4,
               "moe_fetch_ffn: the w13 and s13 pairs must fill the cache buffers w13 and s13 "
+              "(dense, one expert after another)");
+  MOE_REQUIRE(pairs[1].dst == w2 && pairs[3].dst == s2 && strides->w2 == w2b &&
+                  strides->s2 == s2b / 4,
+              "moe_fetch_ffn: the w2 and s2 pairs must fill the cache buffers w2 and s2 "
               "(dense, one expert after another)");
   MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0, "moe_fetch_ffn: x must be 16-byte aligned");
   MOE_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&

@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import weakref
 from pathlib import Path
 
 import numpy as np
@@ -28,6 +29,16 @@ MOE_I32, MOE_I64, MOE_F32, MOE_BF16 = 0, 1, 2, 3
 
 _lib = None
 _err: str | None = None
+
+
+def _free_host_buffer(lib, ptr: int, nbytes: int, hooks) -> None:
+    """Finaliser of Lib.host_buffer's memory: its last view is gone."""
+    for hook in hooks:
+        try:
+            hook(ptr, ptr + nbytes)
+        except Exception:                                     # noqa: BLE001
+            pass
+    lib.host_free(ptr)
 
 
 # byte order of the e4m3 expert matrices (moe_expert_strides.layout)
@@ -249,6 +260,20 @@ class Native:
 
     def host_free(self, ptr: int) -> None:
         self._check(self.cdll.moe_host_free(ptr), "moe_host_free")
+
+    def host_buffer(self, nbytes: int, noncoherent: bool = False, on_free=()):
+        """(address, uint8 array) of `nbytes` of page-locked, device-mapped host
+        memory (moe_host_alloc).  The memory belongs to its views: it is
+        freed when the last numpy array or torch.from_numpy tensor over it is
+        collected, after `on_free(lo, hi)` of each hook (callers drop cached
+        answers about the range there).  Memory still held when the
+        interpreter exits is left to the process's end: no HIP call is made
+        while the runtime may be shutting down."""
+        ptr = self.host_alloc(nbytes, noncoherent=noncoherent)
+        buf = (C.c_uint8 * nbytes).from_address(ptr)
+        fin = weakref.finalize(buf, _free_host_buffer, self, ptr, nbytes, tuple(on_free))
+        fin.atexit = False
+        return ptr, np.ctypeslib.as_array(buf)
 
     def device_ptr_of(self, host_ptr: int) -> int:
         d = C.c_void_p()

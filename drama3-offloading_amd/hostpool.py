@@ -20,7 +20,6 @@ contiguous.  The scales are row-major.
 """
 from __future__ import annotations
 
-import ctypes
 from dataclasses import dataclass
 
 import numpy as np
@@ -171,10 +170,11 @@ class HostPool:
         self.layout = layout
         self.n = n_experts
         self.nbytes = n_experts * layout.record_bytes
-        self.ptr = self.lib.host_alloc(self.nbytes, noncoherent=noncoherent)
+        # the memory lives as long as any view of it (self.array, self.tensor
+        # or a slice taken from them)
+        self.ptr, flat = self.lib.host_buffer(self.nbytes, noncoherent=noncoherent)
         self.dev_ptr = self.lib.device_ptr_of(self.ptr)
-        buf = (ctypes.c_uint8 * self.nbytes).from_address(self.ptr)
-        self.array = np.ctypeslib.as_array(buf).reshape(n_experts, layout.record_bytes)
+        self.array = flat.reshape(n_experts, layout.record_bytes)
         self.tensor = torch.from_numpy(self.array)          # CPU view, no copy
 
     def write(self, first: int, records: torch.Tensor) -> None:
@@ -203,14 +203,11 @@ class HostPool:
         return (self.dev_ptr, cache.data_ptr(), self.layout.record_bytes)
 
     def close(self) -> None:
-        if self.ptr:
-            self.tensor = None
-            self.array = None
-            self.lib.host_free(self.ptr)
-            self.ptr = 0
-
-    def __del__(self):
-        try:
-            self.close()
-        except Exception:                                     # noqa: BLE001
-            pass
+        """Drop the pool's views: the memory is freed now unless a slice of
+        it is still held elsewhere, then when that goes.  Device addresses
+        taken from the pool (dev_ptr, fetch_pair, a captured graph's) are
+        the caller's to retire first."""
+        self.tensor = None
+        self.array = None
+        self.ptr = 0
+        self.dev_ptr = 0

@@ -94,6 +94,69 @@ def test_hook_fetch_ffn_is_bit_exact_against_resident(lib, dev, pair, cap, wdtyp
     assert hits + misses == 40 * K and (cap >= E or misses > cap)
 
 
+def _rows_with_repeats(E_, K_, n, seed):
+    """Fixed rows that repeat an expert on a miss, on a hit and both in one
+    row (first on a cold cache), then `n` rows drawn with replacement."""
+    fixed = [[3, 3, 7, 9, 3, 11, 12, 13],       # 3 three times, all cold: a repeated miss
+             [3, 9, 9, 20, 21, 22, 23, 3],      # 3 and 9 resident: repeated hits, 4 misses
+             [40, 3, 40, 41, 41, 9, 42, 3]]     # repeated misses and a repeated hit
+    rng = np.random.default_rng(seed)
+    rows = [r[:K_] for r in fixed] + [list(rng.integers(0, E_, size=K_)) for _ in range(n)]
+    return [torch.tensor([r], dtype=torch.int64) for r in rows]
+
+
+@pytest.mark.parametrize("cap", [9, 16])
+def test_hook_fetch_ffn_repeated_expert_in_a_row(lib, dev, pair, cap, monkeypatch):
+    """A row that names an expert twice (bin/devcache.py:73-97: the second
+    occurrence is a hit on the slot the first one took; a miss is queued
+    once).  dev_cached_forward through moe_fetch_ffn must give every pick
+    of that expert its activations, whether the expert misses or hits:
+    the output equals the unfused path (resolve, fetch, forward on the
+    slots) on a twin cache and the all-resident forward bit for bit, and
+    the W8A8 oracle within 1e-2; the two caches' tables stay equal."""
+    import devcache
+    import moe
+    import offload
+    from fp8_moe import fp8_moe_forward
+    from oracle import moe as omoe
+    ref, host = pair
+    twin = moe.MoEExperts(E, H, I, device="cpu")
+    for n in ("w13_weight", "w2_weight", "w13_scale_inv", "w2_scale_inv"):
+        setattr(twin, n, getattr(host, n))          # the same pinned tensors
+    monkeypatch.setattr(offload, "DEVICE_TILES", True)
+    devcache.init_dev_cache(host, dev, cap)
+    devcache.init_dev_cache(twin, dev, cap)
+    w13q = ref.w13_weight.view(torch.uint8).cpu().numpy()
+    w2q = ref.w2_weight.view(torch.uint8).cpu().numpy()
+    s13 = ref.w13_scale_inv.cpu().numpy()
+    s2 = ref.w2_scale_inv.cpu().numpy()
+    g = torch.Generator().manual_seed(300 + cap)
+    for step, ids_cpu in enumerate(_rows_with_repeats(E, K, 20, cap)):
+        ids = ids_cpu.to(dev)
+        x = torch.randn((1, H), generator=g).to(torch.bfloat16).to(dev)
+        w = torch.softmax(torch.rand((1, K), generator=g), -1).to(dev)
+        say(f"devcache fetch_ffn repeats: capacity {cap}, step {step}, ids {ids_cpu.tolist()}")
+        monkeypatch.setattr(devcache, "FUSED_FFN", True)
+        fused = devcache.dev_cached_forward(host, x, ids, w)
+        monkeypatch.setattr(devcache, "FUSED_FFN", False)
+        unfused = devcache.dev_cached_forward(twin, x, ids, w)
+        want = fp8_moe_forward(x, ids, w, ref.w13_weight, ref.w13_scale_inv, ref.w2_weight,
+                               ref.w2_scale_inv)
+        torch.cuda.synchronize()
+        assert torch.equal(fused, unfused), f"step {step}: fused != unfused"
+        assert torch.equal(fused, want), f"step {step}: fused != resident"
+        assert torch.equal(host._dc_slot_of, twin._dc_slot_of), f"step {step}"
+        assert torch.equal(host._dc_stamp, twin._dc_stamp), f"step {step}"
+        if step < 3 or step % 5 == 0:
+            oracle_out = omoe.forward_w8a8(x.float().cpu().numpy(), ids_cpu.numpy(),
+                                           w.cpu().numpy().astype(np.float64), w13q, s13, w2q, s2)
+            err = omoe.max_rel_err(fused.float().cpu().numpy(), oracle_out)
+            assert err <= 1e-2, f"step {step}: max rel err {err:.2e} vs the W8A8 oracle"
+    hits, misses = devcache.cache_stats(host)
+    assert (hits, misses) == devcache.cache_stats(twin)
+    assert hits > 0 and misses > 0
+
+
 def test_capture_dynamic_and_bytes(lib, dev, pair):
     import devcache
     from fp8_moe import fp8_moe_forward

@@ -79,6 +79,46 @@ def test_preconditions_are_rejected_without_launching(lib):
         assert msg in c.moe_last_error(), c.moe_last_error()
 
 
+def test_fetch_ffn_refuses_pairs_that_miss_the_cache_buffers(lib):
+    """moe_fetch_ffn's down launch reads w2/s2 from the cache buffers it is
+    given: pairs that fill other buffers, or strides that disagree with
+    them, are refused before any launch (every case below fails a check
+    ahead of the launch; none is ever well formed)."""
+    import ctypes as C
+    import hipfetch
+    c = lib.cdll
+    H, I = 2048, 512
+    W13, W2, S13, S2 = 0x100000, 0x200000, 0x300000, 0x400000
+    good = [(0x10000, W13, 2 * I * H, H), (0x20000, W2, H * I, I), (0x30000, S13, 512, 0),
+            (0x40000, S2, 256, 0)]
+    good_es = (2 * I * H, 128, H * I, 64)
+
+    def call(pairs, es):
+        arr = (hipfetch.FetchPair * 4)(*[hipfetch.FetchPair(*p) for p in pairs])
+        st = hipfetch.ExpertStrides(*es, hipfetch.LAYOUT_TILES)
+        one = C.c_void_p(256)
+        return c.moe_fetch_ffn(arr, 4, one, one, one, 8, 3, one, one, one, hipfetch.MOE_F32, 8,
+                               W13, S13, W2, S2, 16, H, I, C.byref(st), None, one, one, 1 << 20,
+                               None)
+
+    def with_pair(i, **kw):
+        p = list(good[i])
+        for k, v in kw.items():
+            p[("src", "dst", "bytes", "tile_k").index(k)] = v
+        return good[:i] + [tuple(p)] + good[i + 1:]
+
+    cases = ((with_pair(1, dst=W2 + 256), good_es, b"w2 and s2"),
+             (with_pair(3, dst=S13), good_es, b"w2 and s2"),
+             (with_pair(3, bytes=512), good_es, b"pair 3 must be s2"),
+             (with_pair(3, tile_k=128), good_es, b"pair 3 must be s2"),
+             (good, (2 * I * H, 128, H * I + 256, 64), b"w2 and s2"),
+             (good, (2 * I * H, 128, H * I, 128), b"w2 and s2"),
+             (with_pair(0, dst=W2), good_es, b"w13 and s13"))
+    for pairs, es, msg in cases:
+        assert call(pairs, es) == -1, msg
+        assert msg in c.moe_last_error(), (msg, c.moe_last_error())
+
+
 def test_shared_and_block_preconditions_are_rejected_without_launching(lib):
     import ctypes as C
     import hipfetch

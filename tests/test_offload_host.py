@@ -147,3 +147,53 @@ def test_host_arena_layout():
     assert bases == sorted(bases) and bases[-1] - bases[0] < m._host_arena.nbytes
     assert m.w13_scale_inv.flatten().tolist() == list(range(m.w13_scale_inv.numel()))
     assert sorted(n for n, _ in m.named_buffers()) == sorted(offload._BUFFERS)
+
+
+class _StandInLib:
+    """host_alloc/host_free over memory this test owns, for Native.host_buffer
+    on the CPU: records what is freed, and when."""
+
+    def __init__(self):
+        import ctypes
+        self.blocks, self.freed = {}, []
+        self._ctypes = ctypes
+
+    def host_alloc(self, nbytes, noncoherent=False):
+        b = self._ctypes.create_string_buffer(nbytes + 256)
+        ptr = (self._ctypes.addressof(b) + 255) // 256 * 256
+        self.blocks[ptr] = b
+        return ptr
+
+    def host_free(self, ptr):
+        self.freed.append(ptr)
+        del self.blocks[ptr]
+
+
+def test_host_buffer_lives_as_long_as_its_views():
+    """Page-locked memory handed out by host_buffer is freed only when its
+    last view is gone (a slice of a pool outliving the pool, the module's
+    buffers outliving the arena object), after the range hooks; nothing is
+    freed at interpreter exit."""
+    import gc
+    import hipfetch
+    fake = _StandInLib()
+    seen = []
+    ptr, arr = hipfetch.Native.host_buffer(fake, 4096, on_free=(lambda lo, hi: seen.append((lo, hi)),))
+    t = torch.from_numpy(arr.reshape(4, 1024))
+    part = t[2:].view(torch.int32)
+    part.fill_(7)
+    del arr, t
+    gc.collect()
+    assert fake.freed == [] and seen == []
+    assert int(part.sum()) == 7 * 512              # the memory is still there
+    del part
+    gc.collect()
+    assert fake.freed == [ptr] and seen == [(ptr, ptr + 4096)]
+    # at exit: the finaliser is not one weakref runs then
+    _, keep = hipfetch.Native.host_buffer(fake, 256)
+    import weakref
+    ours = [f for f in list(weakref.finalize._registry)
+            if f.alive and f.peek()[1] is hipfetch._free_host_buffer]
+    assert len(ours) == 1 and not ours[0].atexit
+    del keep
+    gc.collect()
