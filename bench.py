@@ -38,6 +38,9 @@ FP8_PEAK_TFLOPS = 5000.0      # dense e4m3 MFMA, MI355X
 TRAFFIC_FETCH_BYTES = (24630 + 24582) * 1024          # host reads + HBM writes, 8 records
 TRAFFIC_GEMV_BYTES = (16614 + 8463 + 16 + 8) * 1024   # gate/up + down, 8 experts x 1 token
 TRAFFIC_CODED_BYTES = (21530 + 24582) * 1024          # coded host reads + HBM writes, 8 records
+# route_fetch_gateup_kernel at 8 misses (--probe routefetch --misses 8): host
+# reads + HBM writes, 8 records (profiles/route_fetch_gateup_kernel.md)
+TRAFFIC_ROUTEFETCH_BYTES = (25258 + 24599) * 1024
 PCIE5_X16_GBS = 64.0
 
 
@@ -195,6 +198,107 @@ def fetch_standalone(lib, pools, dev, jobs: int = 8, reps: int = 160, bpj: int =
     if coded is None:
         return dt, jobs * RB
     return dt, jobs * RB, read
+
+
+def route_fetch_probe(lib, pools, dev, misses=(0, 3, 8), reps: int = 40, capacity: int = 16,
+                      blocks_per_job: int = 4, seed: int = 9) -> dict:
+    """The decode step's dominant kernel alone: route_fetch_gateup_kernel,
+    the second of moe_route_fetch_ffn's three launches (route, the misses'
+    fetch and every pick's gate/up), timed by HIP events that
+    moe_time_fused_launch records around that one dispatch, on the stream it
+    runs on.  For each miss count m, `reps` calls rotate over the page-locked
+    pools (each pool with its own cache and double-buffered table); before
+    each timed call, untimed: the table is reset, a call routed to 8 experts
+    S0 fills the cache, and a 1 GiB streaming read evicts the Infinity Cache
+    (a hit's slot in the step was written long before); the timed call is
+    routed to a set S1 with exactly m experts outside S0 (a router bias of
+    +64 on S1's experts).  Verified: every timed call queued m misses, and
+    the last call's fetched slots equal their host records.  Bytes per call:
+    m records over the link into HBM, and the 8 - m hits' w13 + s13 read
+    from HBM."""
+    import numpy as np
+    import torch
+    lay = pools[0].layout
+    L, E, K, H, I = len(pools), pools[0].n, 8, lay.hidden, lay.inter
+    RB = lay.record_bytes
+    HIT_BYTES = 2 * I * H + (2 * I // 128) * (H // 128) * 4
+    i32 = dict(dtype=torch.int32, device=dev)
+    caches = [torch.zeros((capacity, RB), dtype=torch.uint8, device=dev) for _ in range(L)]
+    slot_of = torch.empty((L, 2, E), **i32)
+    slot_expert = torch.empty((L, 2, capacity), **i32)
+    stamp = torch.empty((L, 2, capacity), dtype=torch.int64, device=dev)
+    step = torch.empty((L, 1), dtype=torch.int64, device=dev)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    gate = (torch.randn((E, H), generator=g, device=dev) * 0.002).to(torch.bfloat16)
+    x = torch.randn((1, H), generator=g, device=dev).to(torch.bfloat16)
+    logits = torch.empty((1, E), dtype=torch.float32, device=dev)
+    ids = torch.empty((1, K), **i32)
+    wts = torch.empty((1, K), dtype=torch.float32, device=dev)
+    out_slot = torch.empty((1, K), **i32)
+    fslot, fexp = torch.empty(K, **i32), torch.empty(K, **i32)
+    nmiss = torch.empty(1, **i32)
+    out = torch.empty((1, H), dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(lib.fp8_moe_workspace(1, K, capacity, H, I), dtype=torch.uint8, device=dev)
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(1, **i32)
+    rng = np.random.default_rng(seed)
+
+    def call(l, bias):
+        lib.route_fetch_ffn(x, gate, bias, K, logits, ids, wts, slot_of[l], slot_expert[l],
+                            stamp[l], step[l], out_slot, fslot, fexp, nmiss, pools[l].dev_ptr,
+                            caches[l], I, blocks_per_job, out, ws, residual=x)
+
+    res = {}
+    for m in misses:
+        plans = []
+        for r in range(reps):
+            s0 = rng.choice(E, K, replace=False)
+            rest = np.setdiff1d(np.arange(E), s0)
+            s1 = np.concatenate([rng.choice(s0, K - m, replace=False),
+                                 rng.choice(rest, m, replace=False)])
+            b0 = torch.zeros(E, dtype=torch.float32)
+            b1 = torch.zeros(E, dtype=torch.float32)
+            b0[s0], b1[s1] = 64.0, 64.0
+            plans.append((r % L, b0.to(dev), b1.to(dev), s1))
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(reps)]
+        queued = torch.empty(reps, **i32)
+        for r, (l, b0, b1, _) in enumerate(plans + plans[:2]):
+            # the first two calls warm up; every call after is timed
+            lib.slots_init(slot_of[l, 0], slot_expert[l, 0], stamp[l, 0], step[l])
+            call(l, b0)
+            lib.stream_read(flush, flush.numel(), 4096, sink)
+            if r >= 2:
+                lib.time_fused_launch(*evs[r - 2])
+            call(l, b1)
+            if r >= 2:
+                queued[r - 2].copy_(nmiss[0])
+        torch.cuda.synchronize(dev)
+        if not bool((queued == m).all()):
+            raise RuntimeError(f"route_fetch probe: calls queued {queued.tolist()} misses, "
+                               f"expected {m}")
+        # the last call's fetched slots hold their host records
+        l_last, s1_last = plans[1][0], plans[1][3]
+        so = slot_of[l_last].cpu()
+        buf = int(step[l_last].item()) & 1
+        for e in s1_last:
+            s_ = int(so[buf][e])
+            if s_ < 0 or not torch.equal(caches[l_last][s_].cpu(), pools[l_last].tensor[e]):
+                raise RuntimeError(f"route_fetch probe: slot of expert {e} != its record")
+        us = np.array([a.elapsed_time(b) * 1e3 for a, b in evs])
+        t = float(us.mean()) / 1e6
+        link_bytes = m * RB
+        hbm_bytes = (K - m) * HIT_BYTES
+        res[str(m)] = {"misses": m, "us": round(float(us.mean()), 2),
+                       "us_min": round(float(us.min()), 2), "us_max": round(float(us.max()), 2),
+                       "link_bytes": link_bytes, "hit_bytes_from_hbm": hbm_bytes,
+                       "link_GBps": round(link_bytes / t / 1e9, 3) if m else None,
+                       "hbm_GBps": round(hbm_bytes / t / 1e9, 1) if m < K else None}
+    torch.cuda.synchronize(dev)
+    return {"kernel": "route_fetch_gateup_kernel (moe_route_fetch_ffn's route + fetch + gate/up "
+                      "launch), 8 picks, Drama-3 records",
+            "pools": L, "pool_bytes": L * E * RB, "capacity": capacity,
+            "blocks_per_job": blocks_per_job, "reps": reps, "by_misses": res}
 
 
 # ------------------------------------------------------------ kernel probes
@@ -992,7 +1096,7 @@ def loader_probe(layers: int = 4, threads: int = 16) -> dict:
 
 
 def run_probe(args) -> int:
-    """--probe gemv|fetch|codec|copy|grouped|shared|hbm|step|contention|loader: the named
+    """--probe gemv|fetch|codec|copy|grouped|shared|hbm|step|contention|loader|routefetch: the named
     kernel(s) alone (or the captured decode step, or the host-side load), one JSON line."""
     import torch
     import hipfetch
@@ -1083,6 +1187,17 @@ def run_probe(args) -> int:
         res = {"probe": "hbm", **hbm_probe(lib, dev, calls=args.steps)}
     elif args.probe == "loader":
         res = {"probe": "loader", **loader_probe(layers=args.layers if args.layers != 40 else 4)}
+    elif args.probe == "routefetch":
+        # the decode step's route + fetch + gate/up launch alone at --misses
+        # misses per call (events around the one dispatch), 4 pools of 256
+        pools = [HostPool(256, DRAMA3) for _ in range(4)]
+        for i, p in enumerate(pools):
+            fill_pool_bytes(p, dev, i)
+        res = {"probe": "routefetch",
+               **route_fetch_probe(lib, pools, dev, misses=(args.misses,), reps=args.steps)}
+        for p in pools:
+            p.close()
+        del pools
     elif args.probe == "contention":
         pools = [HostPool(256, DRAMA3) for _ in range(4)]
         for i, p in enumerate(pools):
@@ -1300,8 +1415,10 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the prefill and all-resident measurements")
     ap.add_argument("--tokens", type=int, default=512, help="tokens per call of --probe grouped")
+    ap.add_argument("--misses", type=int, default=8,
+                    help="misses per call of --probe routefetch (0..8)")
     ap.add_argument("--probe", choices=["gemv", "fetch", "codec", "copy", "grouped", "shared",
-                                        "hbm", "step", "contention", "loader"],
+                                        "hbm", "step", "contention", "loader", "routefetch"],
                     help="time one kernel alone (--steps launches) instead of the decode step")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -1367,6 +1484,8 @@ def main() -> int:
     fetch_gbs = f_bytes / f_dt / 1e9
     gemv_gbs = g_bytes / g_dt / 1e9
     lists = fetch_lists(lib, pools, dev)
+    rf = route_fetch_probe(lib, pools[:4], dev)
+    log(f"route + fetch + gate/up launch alone: {rf['by_misses']}")
     contended = contention(lib, pools, dev)
     log(f"fetch beside the GEMV: {contended}")
     streams = hbm_stream(dev)
@@ -1462,6 +1581,25 @@ def main() -> int:
         "fetch_bytes_per_step": int(miss_bytes_per_step),
         "effective_fetch_GBps_in_step": round(miss_bytes_per_step * tps_cached / 1e9, 3),
         "roofline": {
+            "kernel": "moe route_fetch_gateup_kernel (the decode step's route + fetch + gate/up "
+                      "launch; 8 misses of 3,146,496 B per launch, the 0 % hit case)",
+            "bound": "host-link",
+            "achieved": rf["by_misses"]["8"]["link_GBps"],
+            "peak": round(link, 3),
+            "peak_kind": "measured copy-engine H2D (hipMemcpyAsync, 8 x 256 MiB, page-locked)",
+            "published_link_peak": PCIE5_X16_GBS,
+            "unit": "GB/s",
+            "frac": round(rf["by_misses"]["8"]["link_GBps"] / link, 4),
+            "traffic": TRAFFIC_ROUTEFETCH_BYTES,
+            "traffic_note": "bytes per launch at 8 misses (host reads + HBM writes), PMC, "
+                            "algorithmic 50,343,936",
+            "launch_us": rf["by_misses"]["8"]["us"],
+            "timing": "HIP events recorded around the one dispatch (moe_time_fused_launch), "
+                      "mean of 40 launches rotating over 4 pools of 256 records (3.2 GB)",
+            "by_misses": rf["by_misses"],
+            "step_misses_per_layer": round(misses / (args.steps * cfg.layers), 3),
+        },
+        "roofline_fetch_kernel": {
             "kernel": "moe fetch_kernel (8 records of 3,146,496 B per launch)",
             "bound": "host-link",
             "achieved": round(fetch_gbs, 3),

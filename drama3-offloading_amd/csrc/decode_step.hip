@@ -39,6 +39,8 @@
 // so the activations, and the down launch's output, are bit-identical to
 // the separate launches'.  The fetch's link time hides the hits' gate/up,
 // and the gate/up launch after the fetch goes away.
+#include <hip/hip_ext.h>
+
 #include "common.hpp"
 #include "fetch.hpp"
 #include "gemv.hpp"
@@ -567,9 +569,30 @@ __global__ __launch_bounds__(kStepThreads) void fetch_gateup_kernel(
   }
 }
 
+// Events armed by moe_time_fused_launch for the calling thread's next fused
+// fetch + gate/up launch (hipExtLaunchKernel records them around that one
+// dispatch); taken, and so disarmed, by the next moe_route_fetch_ffn or
+// moe_fetch_ffn call whether or not it launches.
+thread_local hipEvent_t t_fused_start = nullptr;
+thread_local hipEvent_t t_fused_stop = nullptr;
+
+inline void take_fused_events(hipEvent_t& e0, hipEvent_t& e1) {
+  e0 = t_fused_start;
+  e1 = t_fused_stop;
+  t_fused_start = t_fused_stop = nullptr;
+}
+
 }  // namespace moe
 
 using namespace moe;
+
+extern "C" int moe_time_fused_launch(void* start, void* stop) {
+  MOE_REQUIRE((start == nullptr) == (stop == nullptr),
+              "moe_time_fused_launch: give both events or neither");
+  t_fused_start = static_cast<hipEvent_t>(start);
+  t_fused_stop = static_cast<hipEvent_t>(stop);
+  return MOE_OK;
+}
 
 extern "C" int moe_route_fetch_ffn(const void* x, const void* w, const float* bias,
                                    int32_t logit_dtype, int32_t hidden, int32_t n_experts,
@@ -582,6 +605,8 @@ extern "C" int moe_route_fetch_ffn(const void* x, const void* w, const float* bi
                                    const moe_shared_expert* shared, const void* residual,
                                    void* out, void* workspace, size_t workspace_bytes,
                                    void* stream) {
+  hipEvent_t ev0, ev1;
+  take_fused_events(ev0, ev1);
   MOE_REQUIRE(x && w && logits && ids && weights && slot_of && slot_expert && slot_stamp && step &&
                   out_slot && fetch_slot && fetch_expert && nmiss && pool && cache && out &&
                   workspace,
@@ -667,10 +692,10 @@ extern "C" int moe_route_fetch_ffn(const void* x, const void* w, const float* bi
   const unsigned grid = static_cast<unsigned>(g.nfetch + top_k * g.units + nshared);
   float* act = static_cast<float*>(workspace);
 #define MOE_RFG(PE, PC)                                                                        \
-  hipLaunchKernelGGL((route_fetch_gateup_kernel<PE, PC>), dim3(grid), dim3(kStepThreads), 0, s, \
-                     g, static_cast<const uint16_t*>(x), logits, n_experts, top_k, ids, weights, \
-                     slot_of, slot_expert, slot_stamp, cap, step, out_slot, fetch_slot,          \
-                     fetch_expert, nmiss, stats, act, sh)
+  hipExtLaunchKernelGGL((route_fetch_gateup_kernel<PE, PC>), dim3(grid), dim3(kStepThreads), 0,  \
+                        s, ev0, ev1, 0, g, static_cast<const uint16_t*>(x), logits, n_experts,   \
+                        top_k, ids, weights, slot_of, slot_expert, slot_stamp, cap, step,        \
+                        out_slot, fetch_slot, fetch_expert, nmiss, stats, act, sh)
   if (n_experts <= 256) {
     if (cap <= 256) MOE_RFG(4, 4); else MOE_RFG(4, 16);
   } else {
@@ -696,6 +721,8 @@ extern "C" int moe_fetch_ffn(const moe_fetch_pair* pairs, int32_t npairs,
                              int32_t inter, const moe_expert_strides* strides,
                              const void* residual, void* out, void* workspace,
                              size_t workspace_bytes, void* stream) {
+  hipEvent_t ev0, ev1;
+  take_fused_events(ev0, ev1);
   MOE_REQUIRE(pairs && fetch_expert && fetch_slot && nmiss && x && slots && weights && w13 &&
                   s13 && w2 && s2 && strides && out && workspace,
               "moe_fetch_ffn: NULL pointer");
@@ -749,10 +776,11 @@ extern "C" int moe_fetch_ffn(const moe_fetch_pair* pairs, int32_t npairs,
   hipStream_t s = as_stream(stream);
   const int nfetch = blocks_per_job * (max_jobs < kFetchMaxJobsInGrid ? max_jobs : kFetchMaxJobsInGrid);
   float* act = static_cast<float*>(workspace);
-  hipLaunchKernelGGL(fetch_gateup_kernel, dim3(nfetch + top_k * (inter / 16)), dim3(kStepThreads),
-                     0, s, a, nfetch, fetch_expert, fetch_slot, nmiss, max_jobs, slots, top_k,
-                     static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(w13), s13,
-                     strides->w13, strides->s13, n_slots, hidden, inter, act);
+  hipExtLaunchKernelGGL(fetch_gateup_kernel, dim3(nfetch + top_k * (inter / 16)),
+                        dim3(kStepThreads), 0, s, ev0, ev1, 0, a, nfetch, fetch_expert, fetch_slot,
+                        nmiss, max_jobs, slots, top_k, static_cast<const uint16_t*>(x),
+                        static_cast<const uint8_t*>(w13), s13, strides->w13, strides->s13, n_slots,
+                        hidden, inter, act);
   const int rc = check_launch("moe_fetch_ffn(fetch+gate/up)");
   if (rc) return rc;
   return launch_down_gemv(act, slots, weights, w_dtype == MOE_BF16 ? 1 : 0, 1, top_k,

@@ -123,6 +123,7 @@ SIGNATURES = {
     "moe_e4m3_check": (C.c_int, [C.c_uint32, C.c_uint32, _vp, _vp]),
     "moe_silu_check": (C.c_int, [_vp, _vp, _vp, C.c_uint32, _vp]),
     "moe_stream_read": (C.c_int, [_vp, _i64, _i32, _vp, _vp]),
+    "moe_time_fused_launch": (C.c_int, [_vp, _vp]),
     "moe_codec_histogram": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _i32]),
     "moe_codec_bound": (_i64, [_i64, _i64]),
     "moe_codec_encode": (_i64, [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i32]),
@@ -691,6 +692,21 @@ class Native:
         self._check(self.cdll.moe_stream_read(src.data_ptr() + offset, nbytes, workgroups,
                                                sink.data_ptr(), self.stream()),
                     "moe_stream_read")
+
+    def time_fused_launch(self, start, stop) -> None:
+        """Arm torch.cuda.Event start/stop (enable_timing=True) around this
+        thread's next fused fetch + gate/up launch (moe_time_fused_launch);
+        None, None disarms.  start.elapsed_time(stop) is then that kernel's
+        own duration.  Not during stream capture."""
+        handles = []
+        for ev in (start, stop):
+            if ev is None:
+                handles.append(None)
+                continue
+            if not ev.cuda_event:
+                ev.record()                 # torch creates the HIP event on first use
+            handles.append(ev.cuda_event)
+        self._check(self.cdll.moe_time_fused_launch(*handles), "moe_time_fused_launch")
 
     # ------------------------------------------------------------ coded pools
     def codec_histogram(self, records: np.ndarray, fp8_bytes: int, threads: int = 8):

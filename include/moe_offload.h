@@ -77,6 +77,15 @@ int moe_silu_check(const float* g, const float* u, float* out, uint32_t n, void*
 int moe_stream_read(const void* src, int64_t bytes, int32_t workgroups, uint32_t* sink,
                     void* stream);
 
+/* Measurement: the calling thread's next moe_route_fetch_ffn or
+ * moe_fetch_ffn call records `start` and `stop` (hipEvent_t, created by the
+ * caller) around its fetch + gate/up launch alone, through
+ * hipExtLaunchKernel, so hipEventElapsedTime gives that kernel's own
+ * duration.  The next such call disarms them, whether or not it launches;
+ * NULL, NULL disarms.  Not for stream capture.  No counterpart in the
+ * reference: it times the decode step's dominant kernel for its roofline. */
+int moe_time_fused_launch(void* start, void* stop);
+
 /* ------------------------------------------------------------- host pool */
 
 /* Page-locked, device-mapped host allocation for an expert pool.
