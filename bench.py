@@ -200,6 +200,84 @@ def fetch_standalone(lib, pools, dev, jobs: int = 8, reps: int = 160, bpj: int =
     return dt, jobs * RB, read
 
 
+def transfer_split(lib, pools, dev, reps: int = 20, warm: int = 4, seed: int = 5) -> dict:
+    """One layer's misses (8 records of 3,146,496 B, 24 MiB) moved to HBM
+    every way the reference compared (bin/bench_copy.py:36-96,
+    bin/bench_pin.py:31-61): the CPU gather alone; the gather plus a
+    pageable H2D copy (the naive offload); H2D alone from a gathered
+    pageable buffer and from a gathered page-locked one; per-expert DMA
+    (one copy per record straight from the 256-record pool into its slot)
+    from a pageable pool and from a page-locked pool; and the fetch kernel
+    (one launch, the same 8 records, from the page-locked pool).  Eager,
+    wall time with a device synchronise on both sides, median of `reps`
+    after `warm`.  The page-locked pools are the bench's own (30 GiB held at
+    once); the pageable pool is a copy of the first."""
+    import numpy as np
+    import torch
+    RB = pools[0].layout.record_bytes
+    n = pools[0].n
+    ids = np.random.default_rng(seed).choice(n, 8, replace=False).tolist()
+    ids_t = torch.tensor(ids)
+    pageable = pools[0].tensor.clone()                 # a pageable copy of layer 0's records
+    pinned = pools[0].tensor
+    stage_pg = torch.empty((8, RB), dtype=torch.uint8)
+    stage_pl = torch.empty((8, RB), dtype=torch.uint8, pin_memory=True)
+    stage_pl.copy_(pinned[ids_t])
+    stage_pg.copy_(pageable[ids_t])
+    dst = torch.empty((8, RB), dtype=torch.uint8, device=dev)
+    cache = torch.empty((8, RB), dtype=torch.uint8, device=dev)
+    fexp = torch.tensor(ids, dtype=torch.int32, device=dev)
+    fslot = torch.arange(8, dtype=torch.int32, device=dev)
+    nmiss = torch.tensor([8], dtype=torch.int32, device=dev)
+    pair = pools[0].fetch_pair(cache)
+
+    def timed(fn):
+        for _ in range(warm):
+            fn()
+        torch.cuda.synchronize(dev)
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize(dev)
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
+
+    def per_expert(src):
+        def go():
+            for i, e in enumerate(ids):
+                dst[i].copy_(src[e], non_blocking=True)
+        return go
+
+    rows = {
+        "cpu_gather_only": timed(lambda: torch.index_select(pageable, 0, ids_t)),
+        "gather_plus_pageable_h2d": timed(
+            lambda: torch.index_select(pageable, 0, ids_t).to(dev, non_blocking=True)),
+        "h2d_only_pageable": timed(lambda: dst.copy_(stage_pg, non_blocking=True)),
+        "h2d_only_page_locked": timed(lambda: dst.copy_(stage_pl, non_blocking=True)),
+        "per_expert_dma_pageable": timed(per_expert(pageable)),
+        "per_expert_dma_page_locked": timed(per_expert(pinned)),
+        "fetch_kernel_page_locked": timed(
+            lambda: lib.fetch([pair], fexp, fslot, nmiss, max_jobs=8, blocks_per_job=3)),
+    }
+    if not torch.equal(cache.cpu(), stage_pl):
+        raise RuntimeError("transfer split: the fetch kernel's slots differ from the records")
+    if not torch.equal(dst.cpu(), stage_pl):
+        raise RuntimeError("transfer split: the per-expert copies differ from the records")
+    nbytes = 8 * RB
+    out = {k: {"ms": round(1e3 * t, 3), "GiB_per_s": round(nbytes / t / 2 ** 30, 2),
+               "GB_per_s": round(nbytes / t / 1e9, 2),
+               "tokens_per_s_if_40_layers": round(1.0 / (40 * t), 1)} for k, t in rows.items()}
+    del pageable
+    return {"bytes_per_layer": nbytes,
+            "what": "8 records of one layer to HBM; eager, wall time between device syncs, "
+                    f"median of {reps}; page-locked pools of the bench (30 GiB pinned at once); "
+                    "GiB/s binary as the reference reports",
+            "page_locked_over_pageable_per_expert_dma": round(
+                rows["per_expert_dma_pageable"] / rows["per_expert_dma_page_locked"], 3),
+            "rows": out}
+
+
 def route_fetch_probe(lib, pools, dev, misses=(0, 3, 8), reps: int = 40, capacity: int = 16,
                       blocks_per_job: int = 4, seed: int = 9) -> dict:
     """The decode step's dominant kernel alone: route_fetch_gateup_kernel,
@@ -1096,7 +1174,7 @@ def loader_probe(layers: int = 4, threads: int = 16) -> dict:
 
 
 def run_probe(args) -> int:
-    """--probe gemv|fetch|codec|copy|grouped|shared|hbm|step|contention|loader|routefetch: the named
+    """--probe gemv|fetch|codec|copy|grouped|shared|hbm|step|contention|loader|routefetch|transfer: the named
     kernel(s) alone (or the captured decode step, or the host-side load), one JSON line."""
     import torch
     import hipfetch
@@ -1187,6 +1265,16 @@ def run_probe(args) -> int:
         res = {"probe": "hbm", **hbm_probe(lib, dev, calls=args.steps)}
     elif args.probe == "loader":
         res = {"probe": "loader", **loader_probe(layers=args.layers if args.layers != 40 else 4)}
+    elif args.probe == "transfer":
+        # one layer's 8 records every way the reference's copy benchmarks
+        # compared, from 4 page-locked pools of 256 (and a pageable copy)
+        pools = [HostPool(256, DRAMA3) for _ in range(4)]
+        for i, p in enumerate(pools):
+            fill_pool_bytes(p, dev, i)
+        res = {"probe": "transfer", **transfer_split(lib, pools, dev)}
+        for p in pools:
+            p.close()
+        del pools
     elif args.probe == "routefetch":
         # the decode step's route + fetch + gate/up launch alone at --misses
         # misses per call (events around the one dispatch), 4 pools of 256
@@ -1418,7 +1506,8 @@ def main() -> int:
     ap.add_argument("--misses", type=int, default=8,
                     help="misses per call of --probe routefetch (0..8)")
     ap.add_argument("--probe", choices=["gemv", "fetch", "codec", "copy", "grouped", "shared",
-                                        "hbm", "step", "contention", "loader", "routefetch"],
+                                        "hbm", "step", "contention", "loader", "routefetch",
+                                        "transfer"],
                     help="time one kernel alone (--steps launches) instead of the decode step")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -1486,6 +1575,8 @@ def main() -> int:
     lists = fetch_lists(lib, pools, dev)
     rf = route_fetch_probe(lib, pools[:4], dev)
     log(f"route + fetch + gate/up launch alone: {rf['by_misses']}")
+    transfers = transfer_split(lib, pools, dev)
+    log(f"one layer's transfer, every way: {transfers}")
     contended = contention(lib, pools, dev)
     log(f"fetch beside the GEMV: {contended}")
     streams = hbm_stream(dev)
@@ -1639,6 +1730,7 @@ def main() -> int:
         "hbm_measured_GBps": streams,
         "hbm_read_floors": floors,
         "fetch_compute_contention": contended,
+        "transfer_split": transfers,
         "drift": drift,
         "router_contracts": contracts,
         "cpu_baseline": cpu,

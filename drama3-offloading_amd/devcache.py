@@ -66,7 +66,9 @@ CODED_POOL = False
 
 
 def init_dev_cache(experts, device: torch.device, capacity: int) -> None:
-    """Allocate one layer's cache buffers and slot table (bin/devcache.py:138-167)."""
+    """Allocate one layer's cache buffers and slot table (bin/devcache.py:138-167).
+    The per-call scratch holds 8 ids, the reference's top-k; a model routing
+    to more sets experts._dc_kmax to its top-k first."""
     import offload
     lib = hipfetch.require()
     n_experts = experts.num_experts

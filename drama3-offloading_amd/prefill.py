@@ -96,12 +96,22 @@ class DevicePrefill:
 
     @classmethod
     def for_experts(cls, experts, top_k: int, max_tokens: int, device,
-                    tiles: bool = False) -> "DevicePrefill":
+                    tiles: bool = False, rows: list[torch.Tensor] | None = None
+                    ) -> "DevicePrefill":
         """Gather buffers shaped like an experts module's four host buffers.
         tiles: the host's row-major w13/w2 land in MFMA tile order, which the
-        FFN then reads as LAYOUT_TILES (the scales are copied as they are)."""
-        bufs = [torch.empty_like(getattr(experts, n), device=device)
-                for n in ("w13_weight", "w2_weight", "w13_scale_inv", "w2_scale_inv")]
+        FFN then reads as LAYOUT_TILES (the scales are copied as they are).
+        rows: another DevicePrefill's gather buffers to share (its calls and
+        this one's must be ordered on one stream); new ones by default."""
+        names = ("w13_weight", "w2_weight", "w13_scale_inv", "w2_scale_inv")
+        if rows is None:
+            bufs = [torch.empty_like(getattr(experts, n), device=device) for n in names]
+        else:
+            bufs = list(rows)
+            for b, n in zip(bufs, names):
+                h = getattr(experts, n)
+                if b.shape != h.shape or b.dtype != h.dtype:
+                    raise ValueError(f"shared gather rows do not match {n}")
         views = (bufs[0], bufs[2], bufs[1], bufs[3])
         hidden, inter = experts.w13_weight.shape[2], experts.w2_weight.shape[2]
         if tiles:

@@ -157,6 +157,57 @@ def test_hook_fetch_ffn_repeated_expert_in_a_row(lib, dev, pair, cap, monkeypatc
     assert hits > 0 and misses > 0
 
 
+@pytest.mark.parametrize("E_,H_,I_,K_,cap", [(24, 8192, 2048, 16, 18), (40, 4096, 1024, 8, 12)],
+                         ids=["h8192_i2048_top16", "h4096_i1024"])
+def test_hook_fetch_ffn_at_the_limits(lib, dev, E_, H_, I_, K_, cap, monkeypatch):
+    """moe_fetch_ffn at the largest shapes it takes (hidden 8192,
+    intermediate 2048, top-16) and at 4096 / 1024: through the hooks, equal
+    to the unfused path on a twin cache bit for bit, step for step, with
+    equal tables and tile-ordered slot bytes."""
+    import devcache
+    import moe
+    import offload
+    import synth
+    from hostpool import to_tiles
+    monkeypatch.setattr(offload, "DEVICE_TILES", True)
+    say(f"devcache fetch_ffn at the limits: E {E_}, H {H_}, I {I_}, top-{K_}, cap {cap}")
+    ref = moe.MoEExperts(E_, H_, I_, device=dev)
+    synth.fill_experts(ref, seed=8, recipe="devtest", gen_device=dev)
+    mods = []
+    for _ in range(2):
+        m = moe.MoEExperts(E_, H_, I_, device="cpu")
+        m._dc_kmax = K_                  # per-call scratch for a top-16 router
+        mods.append(m)
+    for n in ("w13_weight", "w2_weight", "w13_scale_inv", "w2_scale_inv"):
+        pinned = getattr(ref, n).cpu().pin_memory()
+        for m in mods:
+            setattr(m, n, pinned)
+    host, twin = mods
+    devcache.init_dev_cache(host, dev, cap)
+    devcache.init_dev_cache(twin, dev, cap)
+    g = torch.Generator().manual_seed(70 + K_)
+    for step in range(12):
+        ids = torch.randperm(E_, generator=g)[:K_].view(1, K_).to(dev)
+        x = torch.randn((1, H_), generator=g).to(torch.bfloat16).to(dev)
+        w = torch.softmax(torch.rand((1, K_), generator=g), -1).to(dev)
+        monkeypatch.setattr(devcache, "FUSED_FFN", True)
+        fused = devcache.dev_cached_forward(host, x, ids, w)
+        monkeypatch.setattr(devcache, "FUSED_FFN", False)
+        unfused = devcache.dev_cached_forward(twin, x, ids, w)
+        torch.cuda.synchronize()
+        assert torch.equal(fused, unfused), f"step {step}"
+        assert torch.equal(host._dc_slot_of, twin._dc_slot_of), f"step {step}"
+    assert bool(torch.isfinite(fused.float()).all())
+    for s_, e in enumerate(host._dc_slot_expert.tolist()):
+        if e < 0:
+            continue
+        assert torch.equal(host._dc_w13[s_].view(torch.uint8).cpu(),
+                           to_tiles(host.w13_weight[e].view(torch.uint8))), (s_, e)
+        assert torch.equal(host._dc_w2[s_].view(torch.uint8), twin._dc_w2[s_].view(torch.uint8))
+    hits, misses = devcache.cache_stats(host)
+    assert hits > 0 and misses > 0
+
+
 def test_capture_dynamic_and_bytes(lib, dev, pair):
     import devcache
     from fp8_moe import fp8_moe_forward

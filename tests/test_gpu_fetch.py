@@ -253,3 +253,66 @@ def test_capture_replays_dynamic_and_honours_job_count(lib, dev, pool):
     torch.cuda.synchronize()
     assert _check(cache, B[:jobs // 2]) == 0
     assert _untouched(cache, jobs // 2, jobs)
+
+
+def test_copy_engine_capture_is_frozen_fetch_kernel_dynamic(lib, dev, pool):
+    """The premise of the fetch kernel, measured on ROCm with the
+    reference's A/C/B protocol (bin/bench_hostread.py:852-934,
+    notes/06-cuda-graphs-plan.md:182): a captured copy_ per miss from the
+    page-locked pool (hipMemcpyAsync, a memcpy node) resolves the expert to
+    a source address when it is captured, so the replay after the ids were
+    set to B serves C's records, the capture-time experts (FROZEN); the
+    fetch kernel, which reads the ids on the device, serves B (DYNAMIC)."""
+    jobs = 4
+    A, C_, B = [10, 20, 30, 40], [50, 60, 70, 80], [90, 100, 110, 120]
+    src = lib.device_ptr_of(pool.data_ptr())
+    records = pool.view(-1, RB)
+    results = {}
+    for mech in ("copy_", "fetch kernel"):
+        cache = torch.full((jobs * RB,), 255, dtype=torch.uint8, device=dev)
+        slots = cache.view(jobs, RB)
+        ids_live = torch.zeros(jobs, dtype=torch.int32, device=dev)
+        ids_host = [0] * jobs
+        fslot = torch.arange(jobs, dtype=torch.int32, device=dev)
+        nmiss = torch.tensor([jobs], dtype=torch.int32, device=dev)
+
+        def set_ids(ids):
+            ids_host[:] = ids
+            ids_live.copy_(torch.tensor(ids, dtype=torch.int32))
+
+        def run():
+            if mech == "copy_":
+                for j, e in enumerate(ids_host):
+                    slots[j].copy_(records[e], non_blocking=True)
+            else:
+                lib.fetch([(src, cache.data_ptr(), RB)], ids_live, fslot, nmiss, max_jobs=jobs,
+                          blocks_per_job=2)
+
+        say(f"A/C/B capture protocol: {mech}")
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                set_ids(A)
+                run()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        set_ids(C_)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            run()
+        cache.fill_(255)
+        set_ids(B)
+        g.replay()
+        torch.cuda.synchronize()
+        if _check(cache, B) == 0:
+            results[mech] = "DYNAMIC"
+        elif _check(cache, C_) == 0:
+            results[mech] = "FROZEN"
+        elif bool((cache == 255).all()):
+            results[mech] = "untouched (the replay did nothing)"
+        else:
+            results[mech] = "WRONG"
+        del g
+    print(f"A/C/B on MI355X: {results}")
+    assert results == {"copy_": "FROZEN", "fetch kernel": "DYNAMIC"}

@@ -146,6 +146,46 @@ def test_direct_gather_is_capturable_and_dynamic(lib, dev, models):
         assert torch.equal(out, want), f"replay {r}"
 
 
+def test_captured_gather_survives_a_larger_call(lib, dev, models):
+    """A call with more tokens than the shared gather scratch holds grows
+    it; a graph captured before still replays correctly, because the old
+    scratch is kept (offload._DeviceGather) and the gather rows are shared."""
+    import offload
+    ref, host, _ = models
+    T = 12
+    x, ids, w, _ = _call(ref, T, 500, dev)
+    offload.offloaded_forward(host, x, ids, w)
+    xs, idb, wb = x.clone(), ids.clone(), w.clone()
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        offload.offloaded_forward(host, xs, idb, wb)
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize(dev)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = offload.offloaded_forward(host, xs, idb, wb)
+    retired = len(offload._DeviceGather._retired)
+    big = max(g_.max_tokens for g_ in offload._DeviceGather._by_key.values()) + 1
+    say(f"offload: a {big}-token call grows the gather scratch")
+    xb, ib, wb2, want_b = _call(ref, big, 501, dev)
+    got_b = offload.offloaded_forward(host, xb, ib, wb2)
+    torch.cuda.synchronize(dev)
+    assert torch.equal(got_b, want_b)
+    assert len(offload._DeviceGather._retired) == retired + 1
+    for r in range(3):
+        x, ids, w, want = _call(ref, T, 510 + r, dev)
+        xs.copy_(x)
+        idb.copy_(ids)
+        wb.copy_(w)
+        g.replay()
+        torch.cuda.synchronize(dev)
+        assert torch.equal(out, want), f"replay {r} after the scratch grew"
+    del g
+    torch.cuda.synchronize(dev)
+    offload._DeviceGather.release()
+
+
 @pytest.mark.parametrize("tiles", [True, False])
 def test_host_lru_and_fallbacks(lib, dev, models, tiles, monkeypatch):
     import offload

@@ -235,3 +235,74 @@ def test_prefill_from_coded_pool_equals_raw_pool(lib, dev):
     finally:
         coded.close()
         pool.close()
+
+
+def test_prefill_at_full_size_512_tokens_256_experts(lib, dev):
+    """The workload's prefill at its real size: 512 tokens, uniform top-8 of
+    256 experts, H 2048 / I 512, through DevicePrefill (host-only gather),
+    through offload.offloaded_forward (the hook's direct mode) and through
+    the hybrid gather with a 50-slot decode cache.  All three equal the
+    all-resident forward bit for bit; 6 sampled tokens against the W8A8
+    oracle within 1e-2 (bin/offload.py:137-239, 195-224)."""
+    import devcache
+    import moe
+    import offload
+    import synth
+    from fp8_moe import fp8_moe_forward
+    from oracle import moe as omoe
+    from prefill import DevicePrefill
+    E_, T = 256, 512
+    say("prefill full size: 256 experts on the GPU and page-locked on the host")
+    ref = moe.MoEExperts(E_, H, I, device=dev)
+    synth.fill_experts(ref, seed=13, recipe="devtest", gen_device=dev)
+    host = moe.MoEExperts(E_, H, I, device="cpu")
+    for n in ("w13_weight", "w2_weight", "w13_scale_inv", "w2_scale_inv"):
+        setattr(host, n, getattr(ref, n).cpu().pin_memory())
+    host._layer_index = 0
+    rng = np.random.default_rng(512)
+    ids = torch.tensor(np.stack([rng.choice(E_, K, replace=False) for _ in range(T)]), device=dev)
+    w = torch.softmax(torch.randn((T, K), generator=torch.Generator().manual_seed(5)), -1).to(dev)
+    x = synth.hidden_states(21, T, H).to(dev)
+    want = fp8_moe_forward(x, ids, w, ref.w13_weight, ref.w13_scale_inv, ref.w2_weight,
+                           ref.w2_scale_inv)
+    src = [devcache._device_ptr(lib, getattr(host, n)) for n in
+           ("w13_weight", "w2_weight", "w13_scale_inv", "w2_scale_inv")]
+    say("prefill full size: DevicePrefill, host-only gather")
+    pf = DevicePrefill.for_experts(host, K, T, dev, tiles=True)
+    got = pf.forward(x, ids, w, src)
+    torch.cuda.synchronize()
+    n = int(pf.n_unique)
+    assert n == int(torch.unique(ids).numel()) and n > 240
+    assert torch.equal(got, want)
+    del pf
+    say("prefill full size: offload.offloaded_forward (direct mode)")
+    assert offload.COPY_MODE == "direct"
+    got_hook = offload.offloaded_forward(host, x, ids, w)
+    torch.cuda.synchronize()
+    assert torch.equal(got_hook, want)
+    say("prefill full size: hybrid gather with a 50-slot cache")
+    devcache.init_dev_cache(host, dev, 50)
+    for s in range(12):
+        devcache.dev_resolve_and_fetch(host, ids[s * 3:s * 3 + 1])
+    torch.cuda.synchronize()
+    stamp = host._dc_stamp.clone()
+    pairs = devcache._copy_pairs(host)
+    hy = DevicePrefill.for_experts(host, K, T, dev, tiles=host._dc_tiles)
+    got_hy = hy.forward(x, ids, w, src, cache=(host._dc_slot_of, host._dc_cap,
+                                               [c.data_ptr() for _, c in pairs]))
+    torch.cuda.synchronize()
+    from_cache, from_host = hy.copy_stats()
+    assert from_cache > 0 and from_cache + from_host == n
+    assert torch.equal(got_hy, want)
+    assert torch.equal(stamp, host._dc_stamp)
+    say("prefill full size: 6 tokens against the W8A8 oracle")
+    w13q = ref.w13_weight.view(torch.uint8).cpu().numpy()
+    w2q = ref.w2_weight.view(torch.uint8).cpu().numpy()
+    s13, s2 = ref.w13_scale_inv.cpu().numpy(), ref.w2_scale_inv.cpu().numpy()
+    rows = [0, 97, 200, 311, 450, 511]
+    ora = omoe.forward_w8a8(x[rows].float().cpu().numpy(), ids[rows].cpu().numpy(),
+                            w[rows].cpu().numpy().astype(np.float64), w13q, s13, w2q, s2)
+    err = omoe.max_rel_err(got[rows].float().cpu().numpy(), ora)
+    print(f"prefill full size: {n} experts, {from_cache} from the cache; "
+          f"max rel err vs the W8A8 oracle on 6 tokens {err:.2e}")
+    assert err <= 1e-2

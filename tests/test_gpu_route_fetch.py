@@ -80,7 +80,11 @@ def test_route_fetch_equals_route_resolve_then_fetch(lib, dev, shape):
     dict(n_experts=64, top_k=4, hidden=512, inter=128, capacity=5, ffn_blocks_per_job=1),
     # the limits: 1024 experts and slots, top-16 (16 jobs over the grid's 8)
     dict(n_experts=1024, top_k=16, hidden=1024, inter=128, capacity=1024, ffn_blocks_per_job=2),
-], ids=["drama3", "wide", "tight", "limits"])
+    # the largest hidden and intermediate sizes (the LDS tables at their
+    # maximum: 64 K-blocks, 128 units of 16 columns), at top-16
+    dict(n_experts=24, top_k=16, hidden=8192, inter=2048, capacity=18, ffn_blocks_per_job=2),
+    dict(n_experts=48, top_k=8, hidden=4096, inter=1024, capacity=12),
+], ids=["drama3", "wide", "tight", "limits", "h8192_i2048_top16", "h4096_i1024"])
 def test_route_fetch_ffn_equals_separate_launches(lib, dev, shape):
     """moe_route_fetch_ffn (three launches: the misses' gate/up inside the
     fetch, the hits' beside it) against moe_route_resolve + moe_fetch +

@@ -99,3 +99,40 @@ def test_simulator_static_is_an_upper_bound_of_lru_on_reference_trace(traces):
         assert lru[1] == st[1] == dev[1] == len(recs) * 8
         assert st[0] >= lru[0] * 0.9
         assert abs(dev[0] - lru[0]) / lru[1] < 0.02       # step-LRU ~ exact LRU
+
+
+def test_simulator_static_equals_its_closed_form(traces):
+    """Static keeps each layer's `capacity` most frequent experts over the
+    whole trace, so its hits are the sum over layers of the top-C counts,
+    whatever the order among equal counts (bin/simulate_cache.py:66-71)."""
+    import numpy as np
+    for name in ("t512", "direct"):
+        layer = traces[f"{name}_decode_layer"]
+        ids = traces[f"{name}_decode_ids"]
+        recs = list(zip(layer.tolist(), ids.tolist()))
+        for cap in (1, 8, 32, 69, 113, 256):
+            want = 0
+            for l in range(40):
+                counts = np.bincount(ids[layer == l].ravel(), minlength=256)
+                want += int(np.sort(counts)[::-1][:cap].sum())
+            assert slots.simulate(recs, cap, "static") == (want, ids.size), (name, cap)
+
+
+def test_simulator_lfu_hand_worked():
+    """LFU evicts the lowest count, and among equal counts the expert
+    inserted first (bin/simulate_cache.py:93-94: min over the dict's
+    insertion order).  One layer, capacity 3, [1, 2, 3, 4, 1, 2, 3]:
+      1 2 3   miss, miss, miss               {1:1, 2:1, 3:1}
+      4       miss, evicts 1 (first of the count-1 ties)   {2, 3, 4}
+      1       miss, evicts 2                 {3, 4, 1}
+      2       miss, evicts 3                 {4, 1, 2}
+      3       miss, evicts 4                 {1, 2, 3}
+    0 hits; evicting the last-inserted tie would give 2, the lowest id 1.
+    Capacity 2, [1, 1, 2, 3, 4, 1]: 1 misses, 1 hits (count 2), 2 misses,
+    3 evicts 2 (count 1 < 2), 4 evicts 3, 1 hits: 2 hits, where LRU (which
+    evicts 1 at the 3) gets 1."""
+    assert slots.simulate([(0, [1, 2, 3, 4, 1, 2, 3])], 3, "lfu") == (0, 7)
+    assert slots.simulate([(0, [1, 1, 2, 3, 4, 1])], 2, "lfu") == (2, 6)
+    assert slots.simulate([(0, [1, 1, 2, 3, 4, 1])], 2, "lru") == (1, 6)
+    # the same calls split over two records and two layers: layers are independent
+    assert slots.simulate([(0, [1, 2, 3]), (5, [9]), (0, [4, 1, 2, 3])], 3, "lfu") == (0, 8)
