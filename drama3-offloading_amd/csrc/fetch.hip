@@ -3,8 +3,10 @@
 // Why a kernel and not hipMemcpyAsync: a captured memcpy node bakes its
 // source address, so a replayed graph would copy the capture-time experts
 // forever (measured as FROZEN in the reference, notes/06-cuda-graphs-plan.md
-// :182).  This kernel reads which expert goes to which slot, and how many
-// jobs there are, from device memory when it runs.
+// :182, and on MI355X by the same A/C/B protocol: a captured copy_ per miss
+// from a page-locked pool replays the capture-time experts, this kernel the
+// experts set after the capture).  This kernel reads which expert goes to
+// which slot, and how many jobs there are, from device memory when it runs.
 //
 // Work distribution: the nmiss queued records (read at run time) are cut
 // into pieces of kFetchThreads * kFetchUnroll 16-byte vectors (8 KiB) per
