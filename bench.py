@@ -887,7 +887,12 @@ def prefill_bench(lib, harness, tokens: int = 512, passes: int = 2, coded=None, 
 def resident_bench(lib, harness, batches=(1, 8, 32, 128), steps: int = 20, warmup: int = 3):
     """All 40 x 256 expert records resident in HBM (30 GiB, no offload):
     batched decode at B tokens per step, top-8 of a uniform router, the
-    non-expert stub per layer, the whole step in one hipGraph."""
+    non-expert stub per layer, the whole step in one hipGraph.  Batch 1
+    runs the decode step's launches: the router's logits, then route +
+    gate/up in one launch (moe_route_fetch_ffn over the resident records
+    with a table that holds every expert, so nothing is ever fetched), then
+    down; the five-launch form (logits, top-k, gate/up, down) is timed
+    beside it and must give the same output."""
     import numpy as np
     import torch
     import decode
@@ -911,7 +916,7 @@ def resident_bench(lib, harness, batches=(1, 8, 32, 128), steps: int = 20, warmu
         logits = torch.zeros((B, E), dtype=torch.float32, device=dev)
         ws = torch.empty(lib.fp8_moe_workspace(B, K, E, H, I), dtype=torch.uint8, device=dev)
 
-        def step(_r=0):
+        def step_separate(_r=0):
             x.copy_(x0)
             for l in range(L):
                 decode.stub_linear(x, harness.w_stub[l], h)
@@ -919,25 +924,55 @@ def resident_bench(lib, harness, batches=(1, 8, 32, 128), steps: int = 20, warmu
                 lib.fp8_moe_forward(h, ids[l], wts[l], *views[l], x, ws, residual=h,
                                     layout=harness.layout.code)
 
-        s = torch.cuda.Stream(device=dev)
-        s.wait_stream(torch.cuda.current_stream(dev))
-        with torch.cuda.stream(s):
-            step()
-        torch.cuda.current_stream(dev).wait_stream(s)
-        torch.cuda.synchronize(dev)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            step()
-        for _ in range(warmup):
-            graph.replay()
-        torch.cuda.synchronize(dev)
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(steps):
-            graph.replay()
-        b.record()
-        torch.cuda.synchronize(dev)
-        dt = a.elapsed_time(b) / 1000.0 / steps
+        if B == 1:
+            tabs = [decode.resident_table(E, dev) for _ in range(L)]
+            i32 = dict(dtype=torch.int32, device=dev)
+            out_slot, fslot, fexp = (torch.empty(K, **i32) for _ in range(3))
+            nmiss = torch.zeros((L, 1), **i32)
+
+            def step_fused(_r=0):
+                x.copy_(x0)
+                for l in range(L):
+                    decode.stub_linear(x, harness.w_stub[l], h)
+                    lib.route_fetch_ffn(h, gate[l], None, K, logits, ids[l], wts[l], *tabs[l],
+                                        out_slot, fslot, fexp, nmiss[l], recs[l].data_ptr(),
+                                        recs[l], I, 4, x, ws, residual=h)
+
+        def timed(step):
+            s = torch.cuda.Stream(device=dev)
+            s.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(s):
+                step()
+            torch.cuda.current_stream(dev).wait_stream(s)
+            torch.cuda.synchronize(dev)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                step()
+            for _ in range(warmup):
+                graph.replay()
+            torch.cuda.synchronize(dev)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(steps):
+                graph.replay()
+            b.record()
+            torch.cuda.synchronize(dev)
+            del graph
+            return a.elapsed_time(b) / 1000.0 / steps
+
+        extra = {}
+        if B == 1:
+            dt_sep = timed(step_separate)
+            x_sep = x.clone()
+            dt = timed(step_fused)
+            extra = {"launches_per_layer": "stub, logits, route + gate/up, down",
+                     "separate_launches": {"launches_per_layer": "stub, logits, top-k, gate/up, down",
+                                           "tokens_per_s": round(1 / dt_sep, 1),
+                                           "ms_per_step": round(1e3 * dt_sep, 4)},
+                     "x_equal_separate_launches": bool(torch.equal(x, x_sep)),
+                     "misses_queued": int(nmiss.sum())}
+        else:
+            dt = timed(step_separate)
         distinct = np.array([np.unique(ids[l].cpu().numpy()).size for l in range(L)])
         wbytes = float(distinct.sum()) * lay.record_bytes
         flops = L * B * K * 2 * (2 * I * H + H * I)
@@ -946,8 +981,7 @@ def resident_bench(lib, harness, batches=(1, 8, 32, 128), steps: int = 20, warmu
                        "expert_GBps": round(wbytes / dt / 1e9, 1),
                        "expert_TFLOPs": round(flops / dt / 1e12, 3),
                        "kernels": "GEMV" if B <= 16 else "grouped",
-                       "finite_output": bool(torch.isfinite(x.float()).all())}
-        del graph
+                       "finite_output": bool(torch.isfinite(x.float()).all()), **extra}
     del recs, views
     torch.cuda.empty_cache()
     return {"workload": f"all {L}x{E} expert records resident in HBM ({L * E * lay.record_bytes / 2**30:.1f} GiB), "
@@ -1174,7 +1208,7 @@ def loader_probe(layers: int = 4, threads: int = 16) -> dict:
 
 
 def run_probe(args) -> int:
-    """--probe gemv|fetch|codec|copy|grouped|shared|hbm|step|contention|loader|routefetch|transfer: the named
+    """--probe gemv|fetch|codec|copy|grouped|shared|hbm|step|contention|loader|routefetch|transfer|blockffn: the named
     kernel(s) alone (or the captured decode step, or the host-side load), one JSON line."""
     import torch
     import hipfetch
@@ -1265,6 +1299,10 @@ def run_probe(args) -> int:
         res = {"probe": "hbm", **hbm_probe(lib, dev, calls=args.steps)}
     elif args.probe == "loader":
         res = {"probe": "loader", **loader_probe(layers=args.layers if args.layers != 40 else 4)}
+    elif args.probe == "blockffn":
+        # the routed expert FFN and the MoE block (shared expert carried in
+        # the same two launches) on resident records
+        res = {"probe": "blockffn", **block_resident(lib, dev, DRAMA3, calls=args.steps)}
     elif args.probe == "transfer":
         # one layer's 8 records every way the reference's copy benchmarks
         # compared, from 4 page-locked pools of 256 (and a pageable copy)
@@ -1343,6 +1381,40 @@ def shared_resident(lib, dev, weights, calls: int = 200):
         lib.shared_down(act, sig, wd[r % L], out, routed=x, residual=x)
     dt = graph_time(dev, body, calls)
     return dt, 2 * (3 * Is * H + H)
+
+
+def block_resident(lib, dev, layout, calls: int = 200, n_records: int = 2048,
+                   top_k: int = 8) -> dict:
+    """The shared expert carried in the routed decode launches: the routed
+    expert FFN (fp8_moe_forward) and the MoE block (fp8_moe_block_forward,
+    the same launches with the shared expert's rows in extra workgroups)
+    over the same random experts of `n_records` resident records and 40
+    layers' shared weights, each a graph of `calls` back-to-back calls."""
+    import numpy as np
+    import torch
+    rec = resident_records(dev, n_records, layout)
+    views = layout.views(rec)
+    wg, wu, wd, wsg = shared_weights(dev, 40, layout.hidden, 512)
+    rng = np.random.default_rng(13)
+    ids = torch.tensor(np.stack([rng.choice(n_records, top_k, replace=False)
+                                 for _ in range(calls)])[:, None, :], dtype=torch.int32, device=dev)
+    x = torch.randn((1, layout.hidden), device=dev).to(torch.bfloat16)
+    w = torch.full((1, top_k), 1.0 / top_k, device=dev)
+    out = torch.empty_like(x)
+    ws = torch.empty(lib.fp8_moe_block_workspace(1, top_k, n_records, layout.hidden,
+                                                 layout.inter, 512), dtype=torch.uint8, device=dev)
+    routed = graph_time(dev, lambda r: lib.fp8_moe_forward(x, ids[r], w, *views, out, ws, mode=1,
+                                                          residual=x, layout=layout.code), calls)
+    block = graph_time(dev, lambda r: lib.fp8_moe_block_forward(
+        x, ids[r], w, *views, (wg[r % 40], wu[r % 40], wd[r % 40], wsg[r % 40]), out, ws,
+        residual=x, layout=layout.code), calls)
+    if not bool(torch.isfinite(out.float()).all()):
+        raise RuntimeError("block probe produced non-finite output")
+    del rec
+    return {"what": f"{calls} back-to-back calls in a graph, 1 token, top-{top_k} of "
+                    f"{n_records} resident records, shared expert of 40 layers (I 512)",
+            "routed_us_per_call": round(1e6 * routed, 3), "block_us_per_call": round(1e6 * block, 3),
+            "shared_bytes_per_call": 2 * (3 * 512 * layout.hidden + layout.hidden)}
 
 
 def moe_block_bench(lib, cfg, pools, dev, steps: int, warmup: int):
@@ -1507,7 +1579,7 @@ def main() -> int:
                     help="misses per call of --probe routefetch (0..8)")
     ap.add_argument("--probe", choices=["gemv", "fetch", "codec", "copy", "grouped", "shared",
                                         "hbm", "step", "contention", "loader", "routefetch",
-                                        "transfer"],
+                                        "transfer", "blockffn"],
                     help="time one kernel alone (--steps launches) instead of the decode step")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

@@ -110,6 +110,21 @@ def fill_pool_on_gpu(pool: HostPool, seed: int, layer: int, device, chunk: int =
     torch.cuda.synchronize(device)
 
 
+def resident_table(n_experts: int, device):
+    """A double-buffered slot table over records that are all resident
+    (slot e holds expert e, both buffers; stamps -E..-1): given to
+    moe_route_fetch_ffn with the records as the cache, every pick hits, no
+    miss is queued and the pool is never read, so the launch is the route
+    and the gate/up of the all-resident decode step."""
+    i32 = dict(dtype=torch.int32, device=device)
+    ar = torch.arange(n_experts, **i32)
+    slot_of = ar.repeat(2, 1).contiguous()
+    slot_expert = ar.repeat(2, 1).contiguous()
+    stamp = (torch.arange(n_experts, dtype=torch.int64, device=device) - n_experts).repeat(2, 1)
+    step = torch.zeros(1, dtype=torch.int64, device=device)
+    return slot_of, slot_expert, stamp.contiguous(), step
+
+
 class DecodeHarness:
     def __init__(self, cfg: DecodeConfig, device=None, pools: list[HostPool] | None = None,
                  coded: list | None = None):

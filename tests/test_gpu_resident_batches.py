@@ -78,3 +78,56 @@ def test_resident_batch_against_oracle(lib, dev, resident, B):
         err = omoe.max_rel_err(outs[0][t:t + 1].float().cpu().numpy(), want)
         say(f"resident: B={B} token {t}: max rel err {err:.2e}")
         assert err <= TOL
+
+
+def test_resident_batch1_fused_launch_against_oracle(lib, dev, resident):
+    """Batch 1 on the decode step's fused launch (moe_route_fetch_ffn over
+    the 256 resident records with a table that holds every expert: route +
+    gate/up in one launch, then down): no miss is ever queued; router ids
+    bit-exact against oracle.router; the output equals the separate router
+    + GEMV launches bit for bit (with and without the residual) and the
+    W8A8 oracle within 1e-2, token after token."""
+    import decode
+    import moe
+    import synth
+    from hostpool import DRAMA3
+    rec, gate = resident
+    views = DRAMA3.views(rec)
+    so, se, st, step = decode.resident_table(E, dev)
+    i32 = dict(dtype=torch.int32, device=dev)
+    logits = torch.empty((1, E), dtype=torch.float32, device=dev)
+    ids = torch.empty((1, K), **i32)
+    wts = torch.empty((1, K), dtype=torch.float32, device=dev)
+    out_slot, fslot, fexp = (torch.empty(K, **i32) for _ in range(3))
+    nmiss = torch.empty(1, **i32)
+    stats = torch.zeros(2, dtype=torch.int64, device=dev)
+    ws = torch.empty(lib.fp8_moe_workspace(1, K, E, H, I), dtype=torch.uint8, device=dev)
+    for t in range(4):
+        x = synth.hidden_states(300 + t, 1).to(dev)
+        outs = {}
+        for res in (None, x):
+            o = torch.empty_like(x)
+            lib.route_fetch_ffn(x, gate, None, K, logits, ids, wts, so, se, st, step, out_slot,
+                                fslot, fexp, nmiss, rec.data_ptr(), rec, I, 4, o, ws,
+                                residual=res, stats=stats)
+            outs[res is None] = o
+        say(f"resident B=1 fused: token {t}")
+        r_ids, r_w, _ = moe.route(x, gate, K, ids_dtype=torch.int32)
+        sep = torch.empty_like(x)
+        sep_res = torch.empty_like(x)
+        lib.fp8_moe_forward(x, r_ids, r_w, *views, sep, ws, mode=1, layout=DRAMA3.code)
+        lib.fp8_moe_forward(x, r_ids, r_w, *views, sep_res, ws, mode=1, residual=x,
+                            layout=DRAMA3.code)
+        torch.cuda.synchronize()
+        assert int(nmiss[0]) == 0
+        assert torch.equal(ids, r_ids) and torch.equal(out_slot.view(1, K), ids)
+        o_ids, o_w, _ = orouter.route(x.float().cpu().numpy(), gate.float().cpu().numpy(), K)
+        assert np.array_equal(ids.cpu().numpy(), o_ids)
+        assert torch.equal(outs[True].view(torch.int16), sep.view(torch.int16))
+        assert torch.equal(outs[False].view(torch.int16), sep_res.view(torch.int16))
+        dense = _unpack(rec[torch.from_numpy(o_ids[0].astype(np.int64)).to(dev)].cpu().numpy())
+        want = omoe.forward_w8a8(x.float().cpu().numpy(), np.arange(K)[None, :],
+                                 wts.cpu().numpy().astype(np.float64), *dense)
+        err = omoe.max_rel_err(outs[True].float().cpu().numpy(), want)
+        assert err <= 1e-2, f"token {t}: max rel err {err:.2e}"
+    assert stats.tolist() == [8 * 8, 0]
