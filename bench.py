@@ -1208,7 +1208,7 @@ def loader_probe(layers: int = 4, threads: int = 16) -> dict:
 
 
 def run_probe(args) -> int:
-    """--probe gemv|fetch|codec|copy|grouped|shared|hbm|step|contention|loader|routefetch|transfer|blockffn: the named
+    """--probe gemv|fetch|codec|copy|grouped|shared|hbm|step|contention|loader|routefetch|transfer|blockffn|stub: the named
     kernel(s) alone (or the captured decode step, or the host-side load), one JSON line."""
     import torch
     import hipfetch
@@ -1299,6 +1299,21 @@ def run_probe(args) -> int:
         res = {"probe": "hbm", **hbm_probe(lib, dev, calls=args.steps)}
     elif args.probe == "loader":
         res = {"probe": "loader", **loader_probe(layers=args.layers if args.layers != 40 else 4)}
+    elif args.probe == "stub":
+        # the non-expert stand-in: a bf16 [2048, 2048] matrix times one token,
+        # rotating over 40 layers' matrices (320 MiB), torch.mv against
+        # moe_linear_bf16 at 1, 2 and 4 rows per wave
+        H = DRAMA3.hidden
+        w = (torch.randn((40, H, H), device=dev) / H ** 0.5).to(torch.bfloat16)
+        x = torch.randn((1, H), device=dev).to(torch.bfloat16)
+        y = torch.empty_like(x)
+        res = {"probe": "stub", "what": "graph of back-to-back calls, 1 token, bf16 "
+               "[2048, 2048] per layer, 40 layers' weights in rotation", "us_per_call": {}}
+        res["us_per_call"]["torch.mv"] = round(1e6 * graph_time(
+            dev, lambda r: torch.mv(w[r % 40], x[0], out=y[0]), args.steps), 3)
+        for rpw in (1, 2, 4):
+            res["us_per_call"][f"moe_linear_bf16 rows_per_wave {rpw}"] = round(1e6 * graph_time(
+                dev, lambda r: lib.linear_bf16(x, w[r % 40], y, rows_per_wave=rpw), args.steps), 3)
     elif args.probe == "blockffn":
         # the routed expert FFN and the MoE block (shared expert carried in
         # the same two launches) on resident records
@@ -1579,7 +1594,7 @@ def main() -> int:
                     help="misses per call of --probe routefetch (0..8)")
     ap.add_argument("--probe", choices=["gemv", "fetch", "codec", "copy", "grouped", "shared",
                                         "hbm", "step", "contention", "loader", "routefetch",
-                                        "transfer", "blockffn"],
+                                        "transfer", "blockffn", "stub"],
                     help="time one kernel alone (--steps launches) instead of the decode step")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

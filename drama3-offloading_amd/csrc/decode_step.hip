@@ -348,13 +348,41 @@ __global__ __launch_bounds__(kStepThreads) void route_fetch_gateup_kernel(
 // piece in LDS before it is overwritten; the other buffers' pieces are
 // plain moe_fetch pieces.  Hit workgroups do a hit's unit from its slot.
 // Same arithmetic as route_fetch_gateup_kernel.
+//
+// RESOLVE (moe_resolve_fetch_ffn): no resolve launch before it; every
+// workgroup's first wave makes the call's slot decisions itself from the
+// reference's single-buffer table (resolve.hpp, the decisions of
+// bin/devcache.py:65-98), which no workgroup of the launch writes:
+// workgroup 0 writes the outputs and the table's next state into staging,
+// which the down launch copies into the table.
+struct ResolveArgs {
+  const void* ids;
+  int32_t ids64;
+  int32_t n_experts;
+  const int32_t* slot_of;
+  const int32_t* slot_expert;
+  const int64_t* stamp;
+  const int64_t* step;
+  int32_t cap;
+  int32_t* next_slot_of;
+  int32_t* next_slot_expert;
+  int64_t* next_stamp;
+  int64_t* next_step;
+  int32_t* out_slot;
+  int32_t* fetch_slot;
+  int32_t* fetch_expert;
+  int32_t* nmiss;
+  int64_t* stats;
+};
+
+template <bool RESOLVE, int PER, int PERC>
 __global__ __launch_bounds__(kStepThreads) void fetch_gateup_kernel(
     FetchArgs a, int32_t nfetch, const int32_t* __restrict__ fetch_expert,
     const int32_t* __restrict__ fetch_slot, const int32_t* __restrict__ nmiss_ptr,
     int32_t max_jobs, const int32_t* __restrict__ slots, int32_t top_k,
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ w13c,
     const float* __restrict__ s13c, int64_t w13_es, int64_t s13_es, int32_t n_slots,
-    int32_t hidden, int32_t inter, float* __restrict__ act) {
+    int32_t hidden, int32_t inter, float* __restrict__ act, ResolveArgs ra) {
   __shared__ u32x4 stage[16 * 33];
   __shared__ __align__(16) uint8_t xq[kGemvMaxHidden];
   __shared__ float xs[kGemvMaxHidden / 128];
@@ -374,24 +402,93 @@ __global__ __launch_bounds__(kStepThreads) void fetch_gateup_kernel(
   const int kq = hidden / 512;
   const int units = inter / 16;
   if (wave == 0) {
-    // the miss list and the picks' slots; a pick missed when its slot is in
-    // the list (a repeated expert's picks all did)
-    const int nm = min(*nmiss_ptr, max_jobs);
-    const int32_t fe = fetch_expert[min(lane, max_jobs - 1)];
-    const int32_t fs = fetch_slot[min(lane, max_jobs - 1)];
-    const int32_t sl = slots[min(lane, top_k - 1)];
-    bool miss = false;
-    uint32_t km = 0;
-    for (int j = 0; j < nm; ++j) miss |= __builtin_amdgcn_readlane(fs, j) == sl;
-    for (int k = 0; k < top_k; ++k)
-      if (__builtin_amdgcn_readlane(sl, k) == fs) km |= 1u << k;
-    if (lane < nm) {
-      job_e[lane] = fe;
-      job_s[lane] = fs;
-      job_km[lane] = km;
+    if constexpr (RESOLVE) {
+      // the table, the step, the counters and the ids in one round trip
+      SlotRegs<PERC> t;
+      t.load(ra.stamp, ra.slot_expert, ra.cap);
+      ExpertRegs<PER> xr;
+      xr.load(ra.slot_of, ra.n_experts);
+      StatsPrefetch prev;
+      prev.load(ra.stats);
+      const int64_t step = *ra.step + 1;
+      const int li = min(lane, top_k - 1);
+      const int64_t e64 = ra.ids64 ? static_cast<const int64_t*>(ra.ids)[li]
+                                   : static_cast<int64_t>(static_cast<const int32_t*>(ra.ids)[li]);
+      // ids out of range get slot -1 (the down launch poisons their rows)
+      const int32_t my_e =
+          (lane < top_k && e64 >= 0 && e64 < ra.n_experts) ? static_cast<int32_t>(e64) : -1;
+      const int32_t found = xr.lookup(my_e < 0 ? 0 : my_e);
+      const int32_t my_s = my_e < 0 ? -1 : found;
+      int32_t nm = 0;
+      int64_t hits = 0;
+      int32_t slot_r;
+      bool miss_r;
+      resolve_regs<PER, PERC>(t, xr, my_e, my_s, top_k, step, ra.cap, job_e, job_s, nullptr, nm,
+                              hits, slot_r, miss_r);
+      // a pick is formed by the fetch when a miss of this call fills its
+      // slot (its own, or an earlier pick's of the same expert)
+      bool fetched = false;
+      int jn = 0;
+      for (int k = 0; k < top_k; ++k) {
+        const int32_t mk = __builtin_amdgcn_readlane(miss_r ? 1 : 0, k);
+        const int32_t sk = __builtin_amdgcn_readlane(slot_r, k);
+        if (mk) {
+          const uint64_t b = __ballot(lane < top_k && slot_r == sk);
+          if (lane == 0) job_km[jn] = static_cast<uint32_t>(b);
+          fetched |= slot_r == sk;
+          ++jn;
+        }
+      }
+      if (lane < top_k) pick_slot[lane] = (slot_r < 0 || fetched) ? -1 : slot_r;
+      if (lane == 0) job_n = nm;
+      if (blockIdx.x == 0) {
+        if (lane < top_k) ra.out_slot[lane] = slot_r;
+#pragma unroll
+        for (int j = 0; j < PERC; ++j) {
+          const int c = lane + 64 * j;
+          if (c < ra.cap) {
+            ra.next_stamp[c] = t.st[j];
+            ra.next_slot_expert[c] = t.se[j];
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+          const int e = lane + 64 * j;
+          if (e < ra.n_experts) ra.next_slot_of[e] = xr.so[j];
+        }
+        if (lane == 0) {
+          for (int j = 0; j < nm; ++j) {
+            ra.fetch_expert[j] = job_e[j];
+            ra.fetch_slot[j] = job_s[j];
+          }
+          *ra.next_step = step;
+          *ra.nmiss = nm;
+          if (ra.stats) {
+            ra.stats[0] = prev.hits + hits;
+            ra.stats[1] = prev.misses + nm;
+          }
+        }
+      }
+    } else {
+      // the miss list and the picks' slots; a pick missed when its slot is in
+      // the list (a repeated expert's picks all did)
+      const int nm = min(*nmiss_ptr, max_jobs);
+      const int32_t fe = fetch_expert[min(lane, max_jobs - 1)];
+      const int32_t fs = fetch_slot[min(lane, max_jobs - 1)];
+      const int32_t sl = slots[min(lane, top_k - 1)];
+      bool miss = false;
+      uint32_t km = 0;
+      for (int j = 0; j < nm; ++j) miss |= __builtin_amdgcn_readlane(fs, j) == sl;
+      for (int k = 0; k < top_k; ++k)
+        if (__builtin_amdgcn_readlane(sl, k) == fs) km |= 1u << k;
+      if (lane < nm) {
+        job_e[lane] = fe;
+        job_s[lane] = fs;
+        job_km[lane] = km;
+      }
+      if (lane < top_k) pick_slot[lane] = miss ? -1 : sl;
+      if (lane == 0) job_n = nm;
     }
-    if (lane < top_k) pick_slot[lane] = miss ? -1 : sl;
-    if (lane == 0) job_n = nm;
   } else {
     constexpr int NC = kGemvMaxHidden / 512;
     uint4 raw[NC];
@@ -712,6 +809,60 @@ extern "C" int moe_route_fetch_ffn(const void* x, const void* w, const float* bi
                           shared ? &sh : nullptr, s);
 }
 
+// The checks moe_fetch_ffn and moe_resolve_fetch_ffn share: the four buffer
+// pairs against the cache buffers and the shapes the kernels take; fills a.
+static int fetch_ffn_checks(const char* what, const moe_fetch_pair* pairs, int32_t npairs,
+                            int32_t max_jobs, int32_t blocks_per_job, const void* x,
+                            int32_t w_dtype, int32_t top_k, const void* w13, const float* s13,
+                            const void* w2, const float* s2, int32_t n_slots, int32_t hidden,
+                            int32_t inter, const moe_expert_strides* strides, void* workspace,
+                            size_t workspace_bytes, FetchArgs* a) {
+  MOE_REQUIRE(npairs == 4, "%s: takes the four buffers w13, w2, s13, s2 (got %d)", what, npairs);
+  MOE_REQUIRE(w_dtype == MOE_F32 || w_dtype == MOE_BF16,
+              "%s: w_dtype must be MOE_F32 or MOE_BF16", what);
+  MOE_REQUIRE(hidden >= 512 && hidden % 512 == 0 && hidden <= kGemvMaxHidden,
+              "%s: hidden must be a multiple of 512 up to %d (got %d)", what, kGemvMaxHidden,
+              hidden);
+  MOE_REQUIRE(inter >= 128 && inter % 128 == 0 && inter <= kGemvMaxInter,
+              "%s: inter must be a multiple of 128 up to %d (got %d)", what, kGemvMaxInter, inter);
+  MOE_REQUIRE(top_k >= 1 && top_k <= kGemvMaxTopK && top_k <= n_slots && n_slots >= 1,
+              "%s: need 1 <= top_k <= min(%d, n_slots)", what, kGemvMaxTopK);
+  MOE_REQUIRE(max_jobs >= top_k && max_jobs <= kMaxTopK, "%s: need top_k <= max_jobs <= %d",
+              what, kMaxTopK);
+  MOE_REQUIRE(strides->layout == MOE_LAYOUT_TILES, "%s: the cache must hold w13/w2 in tile order",
+              what);
+  const int64_t w13b = 2LL * inter * hidden;
+  const int64_t s13b = (2LL * inter / 128) * (hidden / 128) * 4;
+  const int64_t w2b = static_cast<int64_t>(hidden) * inter;
+  const int64_t s2b = (static_cast<int64_t>(hidden) / 128) * (inter / 128) * 4;
+  MOE_REQUIRE(pairs[0].bytes == w13b && pairs[0].tile_k == hidden,
+              "%s: pair 0 must be w13 (%lld bytes, tile_k = hidden)", what, (long long)w13b);
+  MOE_REQUIRE(pairs[1].bytes == w2b && pairs[1].tile_k == inter,
+              "%s: pair 1 must be w2 (tile_k = inter)", what);
+  MOE_REQUIRE(pairs[2].bytes == s13b && pairs[2].tile_k == 0,
+              "%s: pair 2 must be s13 (%lld bytes, a byte copy)", what, (long long)s13b);
+  MOE_REQUIRE(pairs[3].bytes == s2b && pairs[3].tile_k == 0,
+              "%s: pair 3 must be s2 (%lld bytes, a byte copy)", what, (long long)s2b);
+  MOE_REQUIRE(pairs[0].dst == w13 && pairs[2].dst == s13 && strides->w13 == w13b &&
+                  strides->s13 == s13b / 4,
+              "%s: the w13 and s13 pairs must fill the cache buffers w13 and s13 (dense, one "
+              "expert after another)", what);
+  MOE_REQUIRE(pairs[1].dst == w2 && pairs[3].dst == s2 && strides->w2 == w2b &&
+                  strides->s2 == s2b / 4,
+              "%s: the w2 and s2 pairs must fill the cache buffers w2 and s2 (dense, one expert "
+              "after another)", what);
+  MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0, "%s: x must be 16-byte aligned", what);
+  MOE_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
+                  workspace_bytes >= static_cast<size_t>(top_k) * inter * sizeof(float),
+              "%s: the workspace must be 16-byte aligned and hold top_k * inter floats", what);
+  MOE_REQUIRE(blocks_per_job >= 1 && blocks_per_job <= 4096,
+              "%s: need 1 <= blocks_per_job <= 4096", what);
+  const int rc0 = fetch_args(pairs, npairs, max_jobs, a);
+  if (rc0 != MOE_OK) return rc0;
+  MOE_REQUIRE(a->tile_wlog[0] == 5, "%s: w13 pieces must be 32 column units wide", what);
+  return MOE_OK;
+}
+
 extern "C" int moe_fetch_ffn(const moe_fetch_pair* pairs, int32_t npairs,
                              const int32_t* fetch_expert, const int32_t* fetch_slot,
                              const int32_t* nmiss, int32_t max_jobs, int32_t blocks_per_job,
@@ -726,61 +877,19 @@ extern "C" int moe_fetch_ffn(const moe_fetch_pair* pairs, int32_t npairs,
   MOE_REQUIRE(pairs && fetch_expert && fetch_slot && nmiss && x && slots && weights && w13 &&
                   s13 && w2 && s2 && strides && out && workspace,
               "moe_fetch_ffn: NULL pointer");
-  MOE_REQUIRE(npairs == 4, "moe_fetch_ffn: takes the four buffers w13, w2, s13, s2 (got %d)",
-              npairs);
-  MOE_REQUIRE(w_dtype == MOE_F32 || w_dtype == MOE_BF16,
-              "moe_fetch_ffn: w_dtype must be MOE_F32 or MOE_BF16");
-  MOE_REQUIRE(hidden >= 512 && hidden % 512 == 0 && hidden <= kGemvMaxHidden,
-              "moe_fetch_ffn: hidden must be a multiple of 512 up to %d (got %d)", kGemvMaxHidden,
-              hidden);
-  MOE_REQUIRE(inter >= 128 && inter % 128 == 0 && inter <= kGemvMaxInter,
-              "moe_fetch_ffn: inter must be a multiple of 128 up to %d (got %d)", kGemvMaxInter,
-              inter);
-  MOE_REQUIRE(top_k >= 1 && top_k <= kGemvMaxTopK && top_k <= n_slots && n_slots >= 1,
-              "moe_fetch_ffn: need 1 <= top_k <= min(%d, n_slots)", kGemvMaxTopK);
-  MOE_REQUIRE(max_jobs >= top_k && max_jobs <= kMaxTopK,
-              "moe_fetch_ffn: need top_k <= max_jobs <= %d", kMaxTopK);
-  MOE_REQUIRE(strides->layout == MOE_LAYOUT_TILES,
-              "moe_fetch_ffn: the cache must hold w13/w2 in tile order");
-  const int64_t w13b = 2LL * inter * hidden;
-  const int64_t s13b = (2LL * inter / 128) * (hidden / 128) * 4;
-  MOE_REQUIRE(pairs[0].bytes == w13b && pairs[0].tile_k == hidden,
-              "moe_fetch_ffn: pair 0 must be w13 (%lld bytes, tile_k = hidden)", (long long)w13b);
-  MOE_REQUIRE(pairs[1].bytes == static_cast<int64_t>(hidden) * inter && pairs[1].tile_k == inter,
-              "moe_fetch_ffn: pair 1 must be w2 (tile_k = inter)");
-  const int64_t w2b = static_cast<int64_t>(hidden) * inter;
-  const int64_t s2b = (static_cast<int64_t>(hidden) / 128) * (inter / 128) * 4;
-  MOE_REQUIRE(pairs[2].bytes == s13b && pairs[2].tile_k == 0,
-              "moe_fetch_ffn: pair 2 must be s13 (%lld bytes, a byte copy)", (long long)s13b);
-  MOE_REQUIRE(pairs[3].bytes == s2b && pairs[3].tile_k == 0,
-              "moe_fetch_ffn: pair 3 must be s2 (%lld bytes, a byte copy)", (long long)s2b);
-  MOE_REQUIRE(pairs[0].dst == w13 && pairs[2].dst == s13 && strides->w13 == w13b &&
-                  strides->s13 == s13b / 4,
-              "moe_fetch_ffn: the w13 and s13 pairs must fill the cache buffers w13 and s13 "
-              "(dense, one expert after another)");
-  MOE_REQUIRE(pairs[1].dst == w2 && pairs[3].dst == s2 && strides->w2 == w2b &&
-                  strides->s2 == s2b / 4,
-              "moe_fetch_ffn: the w2 and s2 pairs must fill the cache buffers w2 and s2 "
-              "(dense, one expert after another)");
-  MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0, "moe_fetch_ffn: x must be 16-byte aligned");
-  MOE_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
-                  workspace_bytes >= static_cast<size_t>(top_k) * inter * sizeof(float),
-              "moe_fetch_ffn: the workspace must be 16-byte aligned and hold top_k * inter "
-              "floats");
-  MOE_REQUIRE(blocks_per_job >= 1 && blocks_per_job <= 4096,
-              "moe_fetch_ffn: need 1 <= blocks_per_job <= 4096");
   FetchArgs a;
-  const int rc0 = fetch_args(pairs, npairs, max_jobs, &a);
+  const int rc0 = fetch_ffn_checks("moe_fetch_ffn", pairs, npairs, max_jobs, blocks_per_job, x,
+                                   w_dtype, top_k, w13, s13, w2, s2, n_slots, hidden, inter,
+                                   strides, workspace, workspace_bytes, &a);
   if (rc0 != MOE_OK) return rc0;
-  MOE_REQUIRE(a.tile_wlog[0] == 5, "moe_fetch_ffn: w13 pieces must be 32 column units wide");
   hipStream_t s = as_stream(stream);
   const int nfetch = blocks_per_job * (max_jobs < kFetchMaxJobsInGrid ? max_jobs : kFetchMaxJobsInGrid);
   float* act = static_cast<float*>(workspace);
-  hipExtLaunchKernelGGL(fetch_gateup_kernel, dim3(nfetch + top_k * (inter / 16)),
+  hipExtLaunchKernelGGL((fetch_gateup_kernel<false, 4, 4>), dim3(nfetch + top_k * (inter / 16)),
                         dim3(kStepThreads), 0, s, ev0, ev1, 0, a, nfetch, fetch_expert, fetch_slot,
                         nmiss, max_jobs, slots, top_k, static_cast<const uint16_t*>(x),
                         static_cast<const uint8_t*>(w13), s13, strides->w13, strides->s13, n_slots,
-                        hidden, inter, act);
+                        hidden, inter, act, ResolveArgs{});
   const int rc = check_launch("moe_fetch_ffn(fetch+gate/up)");
   if (rc) return rc;
   return launch_down_gemv(act, slots, weights, w_dtype == MOE_BF16 ? 1 : 0, 1, top_k,
@@ -788,4 +897,70 @@ extern "C" int moe_fetch_ffn(const moe_fetch_pair* pairs, int32_t npairs,
                           MOE_LAYOUT_TILES, n_slots, hidden, inter,
                           static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out),
                           nullptr, s);
+}
+
+extern "C" int moe_resolve_fetch_ffn(const void* ids, int32_t ids_dtype, int32_t top_k,
+                                     const moe_slot_table* table, int32_t* out_slot,
+                                     int32_t* fetch_slot, int32_t* fetch_expert, int32_t* nmiss,
+                                     int64_t* stats, const moe_fetch_pair* pairs, int32_t npairs,
+                                     int32_t blocks_per_job, const void* x, const void* weights,
+                                     int32_t w_dtype, const void* w13, const float* s13,
+                                     const void* w2, const float* s2, int32_t hidden,
+                                     int32_t inter, const moe_expert_strides* strides,
+                                     const void* residual, void* out, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  hipEvent_t ev0, ev1;
+  take_fused_events(ev0, ev1);
+  MOE_REQUIRE(ids && table && out_slot && fetch_slot && fetch_expert && nmiss && pairs && x &&
+                  weights && w13 && s13 && w2 && s2 && strides && out && workspace,
+              "moe_resolve_fetch_ffn: NULL pointer");
+  MOE_REQUIRE(ids_dtype == MOE_I32 || ids_dtype == MOE_I64,
+              "moe_resolve_fetch_ffn: ids_dtype must be MOE_I32 or MOE_I64");
+  const moe_slot_table& tb = *table;
+  MOE_REQUIRE(tb.slot_of && tb.slot_expert && tb.stamp && tb.step && tb.next_slot_of &&
+                  tb.next_slot_expert && tb.next_stamp && tb.next_step,
+              "moe_resolve_fetch_ffn: NULL table or staging pointer");
+  MOE_REQUIRE(tb.n_experts >= 1 && tb.n_experts <= 1024,
+              "moe_resolve_fetch_ffn: need 1 <= n_experts <= 1024 (got %d)", tb.n_experts);
+  MOE_REQUIRE(tb.cap >= 1 && tb.cap <= 1024, "moe_resolve_fetch_ffn: need 1 <= cap <= 1024");
+  MOE_REQUIRE(top_k <= tb.cap, "moe_resolve_fetch_ffn: top_k (%d) exceeds the cache capacity (%d)",
+              top_k, tb.cap);
+  MOE_REQUIRE(tb.next_slot_of != tb.slot_of && tb.next_slot_expert != tb.slot_expert &&
+                  tb.next_stamp != tb.stamp && tb.next_step != tb.step,
+              "moe_resolve_fetch_ffn: the staging buffers must not be the table's");
+  FetchArgs a;
+  const int rc0 = fetch_ffn_checks("moe_resolve_fetch_ffn", pairs, npairs, top_k, blocks_per_job,
+                                   x, w_dtype, top_k, w13, s13, w2, s2, tb.cap, hidden, inter,
+                                   strides, workspace, workspace_bytes, &a);
+  if (rc0 != MOE_OK) return rc0;
+  hipStream_t s = as_stream(stream);
+  const int nfetch = blocks_per_job * (top_k < kFetchMaxJobsInGrid ? top_k : kFetchMaxJobsInGrid);
+  float* act = static_cast<float*>(workspace);
+  ResolveArgs ra{ids, ids_dtype == MOE_I64 ? 1 : 0, tb.n_experts, tb.slot_of, tb.slot_expert,
+                 tb.stamp, tb.step, tb.cap, tb.next_slot_of, tb.next_slot_expert, tb.next_stamp,
+                 tb.next_step, out_slot, fetch_slot, fetch_expert, nmiss, stats};
+  const dim3 grid(nfetch + top_k * (inter / 16));
+#define MOE_RFF(PE, PC)                                                                       \
+  hipExtLaunchKernelGGL((fetch_gateup_kernel<true, PE, PC>), grid, dim3(kStepThreads), 0, s,  \
+                        ev0, ev1, 0, a, nfetch, fetch_expert, fetch_slot, nmiss, top_k,      \
+                        out_slot, top_k, static_cast<const uint16_t*>(x),                     \
+                        static_cast<const uint8_t*>(w13), s13, strides->w13, strides->s13,   \
+                        tb.cap, hidden, inter, act, ra)
+  if (tb.n_experts <= 256) {
+    if (tb.cap <= 256) MOE_RFF(4, 4); else MOE_RFF(4, 16);
+  } else {
+    if (tb.cap <= 256) MOE_RFF(16, 4); else MOE_RFF(16, 16);
+  }
+#undef MOE_RFF
+  const int rc = check_launch("moe_resolve_fetch_ffn(resolve+fetch+gate/up)");
+  if (rc) return rc;
+  // the down launch reads the slots written above and copies the staged
+  // table into the table
+  const TableCommit cm{tb.next_slot_of, tb.slot_of, tb.next_slot_expert, tb.slot_expert,
+                       tb.next_stamp, tb.stamp, tb.next_step, tb.step, tb.n_experts, tb.cap};
+  return launch_down_gemv(act, out_slot, weights, w_dtype == MOE_BF16 ? 1 : 0, 1, top_k,
+                          static_cast<const uint8_t*>(w2), s2, strides->w2, strides->s2,
+                          MOE_LAYOUT_TILES, tb.cap, hidden, inter,
+                          static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out),
+                          nullptr, s, &cm);
 }

@@ -1,0 +1,123 @@
+// A bf16 matrix-vector product for up to 4 tokens: y[t] = x[t] W^T with W
+// [out, in] in nn.Linear layout, every output the f32 sum of its row's
+// products rounded once to bf16.  The decode benchmark's stand-in for the
+// non-expert compute between two MoE layers (one [2048, 2048] matrix per
+// layer) runs on it: at one token the product is one pass over 8 MiB of
+// weights, HBM-bound, and the MoE layer after it cannot start before its
+// last output is written.
+//
+// Each wave takes NR consecutive rows; lane l sums the row's 16-byte slices
+// l, l + 64, l + 128, ... in order with one fma per product, and the 64
+// lane sums are added by DPP (the order of rows_dot_bf16, the shared
+// expert's dot product).  All of a lane's slices of its rows are loaded
+// before any is used, so every wave issues its whole share of the matrix
+// at once: x first (every wave reads it, from L2), then the weights with
+// nontemporal loads (read once).
+#include "shared.hpp"
+
+namespace moe {
+
+// One wave per workgroup, one row per wave by default: a graph of
+// 1-token calls over 40 layers' [2048, 2048] matrices (MI355X) took 3.55 us
+// per call with 1, 2 or 4 one-row waves per workgroup (3.55 / 3.59 / 3.60),
+// 3.89 with two rows per wave and 4.54 with four, against 6.9 us for
+// torch.mv; loading the weights with ordinary loads and x after them took
+// 3.85.
+constexpr int kLinearWaves = 1;      // waves per workgroup
+constexpr int kLinearMaxTokens = 4;
+
+template <int NR, int TB>
+__global__ __launch_bounds__(64 * kLinearWaves) void linear_bf16_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int32_t tokens, int32_t in,
+    int32_t out, uint16_t* __restrict__ y) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r0 = (static_cast<int>(blockIdx.x) * kLinearWaves + wave) * NR;
+  if (r0 >= out) return;                       // the whole wave; no barrier below
+  const uint16_t* rows[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) rows[i] = w + static_cast<int64_t>(min(r0 + i, out - 1)) * in;
+  constexpr int U = 4;                         // slices per lane per row in flight
+  const int n16 = in >> 3;
+  float acc[NR][TB];
+#pragma unroll
+  for (int i = 0; i < NR; ++i)
+#pragma unroll
+    for (int t = 0; t < TB; ++t) acc[i][t] = 0.0f;
+  for (int c0 = 0; c0 < n16; c0 += 64 * U) {
+    u32x4 xv[TB][U], wv[U][NR];
+#pragma unroll
+    for (int t = 0; t < TB; ++t)
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = min(c0 + u * 64 + lane, n16 - 1);
+        xv[t][u] = load16(x + static_cast<int64_t>(min(t, tokens - 1)) * in + c * 8);
+      }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = min(c0 + u * 64 + lane, n16 - 1);
+#pragma unroll
+      for (int i = 0; i < NR; ++i)
+        wv[u][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rows[i] + c * 8));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (c0 + u * 64 + lane >= n16) continue;
+#pragma unroll
+      for (int t = 0; t < TB; ++t)
+#pragma unroll
+        for (int i = 0; i < NR; ++i) acc[i][t] = dot8_bf16(wv[u][i], xv[t][u], acc[i][t]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NR; ++i)
+#pragma unroll
+    for (int t = 0; t < TB; ++t) acc[i][t] = wave_sum_f32(acc[i][t]);
+  if (lane == 0) {
+#pragma unroll
+    for (int t = 0; t < TB; ++t)
+#pragma unroll
+      for (int i = 0; i < NR; ++i)
+        if (t < tokens && r0 + i < out)
+          y[static_cast<int64_t>(t) * out + r0 + i] = f32_to_bf16(acc[i][t]);
+  }
+}
+
+template <int NR>
+static void launch_linear(const uint16_t* x, const uint16_t* w, int32_t tokens, int32_t in,
+                          int32_t out, uint16_t* y, hipStream_t s) {
+  const unsigned grid = static_cast<unsigned>((out + kLinearWaves * NR - 1) / (kLinearWaves * NR));
+  if (tokens == 1)
+    hipLaunchKernelGGL((linear_bf16_kernel<NR, 1>), dim3(grid), dim3(64 * kLinearWaves), 0, s, x,
+                       w, tokens, in, out, y);
+  else
+    hipLaunchKernelGGL((linear_bf16_kernel<NR, kLinearMaxTokens>), dim3(grid),
+                       dim3(64 * kLinearWaves), 0, s, x, w, tokens, in, out, y);
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" int moe_linear_bf16(const void* x, const void* w, int32_t tokens, int32_t in_features,
+                               int32_t out_features, void* y, int32_t rows_per_wave,
+                               void* stream) {
+  MOE_REQUIRE(x && w && y, "moe_linear_bf16: NULL pointer");
+  MOE_REQUIRE(tokens >= 1 && tokens <= kLinearMaxTokens, "moe_linear_bf16: need 1 <= tokens <= %d",
+              kLinearMaxTokens);
+  MOE_REQUIRE(in_features >= 8 && in_features % 8 == 0 && out_features >= 1,
+              "moe_linear_bf16: in_features must be a positive multiple of 8, out_features >= 1");
+  MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0,
+              "moe_linear_bf16: x and w must be 16-byte aligned");
+  MOE_REQUIRE(rows_per_wave == 0 || rows_per_wave == 1 || rows_per_wave == 2 || rows_per_wave == 4,
+              "moe_linear_bf16: rows_per_wave must be 0 (default), 1, 2 or 4");
+  hipStream_t s = as_stream(stream);
+  const auto* xb = static_cast<const uint16_t*>(x);
+  const auto* wb = static_cast<const uint16_t*>(w);
+  auto* yb = static_cast<uint16_t*>(y);
+  switch (rows_per_wave) {
+    case 2: launch_linear<2>(xb, wb, tokens, in_features, out_features, yb, s); break;
+    case 4: launch_linear<4>(xb, wb, tokens, in_features, out_features, yb, s); break;
+    default: launch_linear<1>(xb, wb, tokens, in_features, out_features, yb, s); break;
+  }
+  return check_launch("moe_linear_bf16");
+}

@@ -290,13 +290,29 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
 constexpr int kDownChunk = 4;   // K-blocks of w2 in flight per lane (inter 512 = one chunk)
 constexpr int kDownRows = 8;    // output rows per workgroup
 
+// The down launch's extra workgroup: the staged table copied into the table.
+__device__ __forceinline__ void commit_table(const TableCommit& cm) {
+  const int n = static_cast<int>(blockDim.x);
+  for (int i = threadIdx.x; i < cm.n_experts; i += n) cm.so_dst[i] = cm.so_src[i];
+  for (int i = threadIdx.x; i < cm.cap; i += n) {
+    cm.se_dst[i] = cm.se_src[i];
+    cm.st_dst[i] = cm.st_src[i];
+  }
+  if (threadIdx.x == 0) *cm.step_dst = *cm.step_src;
+}
+
 template <bool SHARED>
 __global__ __launch_bounds__(64 * (kMaxK / 2 + 1)) void down_gemv_kernel(
     const float* __restrict__ act, const void* __restrict__ ids, int ids64,
     const void* __restrict__ weights, int wbf16, int32_t top_k, const uint8_t* __restrict__ w2,
     const float* __restrict__ s2, int64_t w2_es, int64_t s2_es, int tiled, int32_t n_experts,
     int32_t hidden, int32_t inter, const uint16_t* __restrict__ residual,
-    uint16_t* __restrict__ out, SharedRefs sh) {
+    uint16_t* __restrict__ out, SharedRefs sh, TableCommit cm) {
+  if (static_cast<int>(blockIdx.x) * kDownRows >= hidden) {
+    // the workgroup past the output rows (a launch with a staged table)
+    if (blockIdx.y == 0) commit_table(cm);
+    return;
+  }
   __shared__ __align__(16) uint8_t aq[kMaxK][kMaxInter];
   __shared__ float as_[kMaxK][kMaxInter / 128];
   __shared__ __align__(16) float part[kMaxK + 1][kDownRows];   // [kMaxK]: discarded quadrants
@@ -497,13 +513,14 @@ static int launch_gemv(const uint16_t* x, const void* ids, int ids64, const void
     hipLaunchKernelGGL(down_gemv_kernel<true>, dim3(hidden / kDownRows, tokens),
                        dim3(64 * ((top_k + 1) / 2 + 1)),
                        0, s, h, ids, ids64, weights, wbf16, top_k, w2, s2, es.w2, es.s2,
-                       static_cast<int>(es.layout), n_experts, hidden, inter, residual, out, *sh);
+                       static_cast<int>(es.layout), n_experts, hidden, inter, residual, out, *sh,
+                       TableCommit{});
   } else {
     hipLaunchKernelGGL(down_gemv_kernel<false>, dim3(hidden / kDownRows, tokens),
                        dim3(64 * ((top_k + 1) / 2)), 0, s,
                        h, ids, ids64, weights, wbf16, top_k, w2, s2, es.w2, es.s2,
                        static_cast<int>(es.layout), n_experts, hidden, inter, residual, out,
-                       SharedRefs{});
+                       SharedRefs{}, TableCommit{});
   }
   return check_launch("moe_fp8_moe_forward(down)");
 }
@@ -512,17 +529,19 @@ int launch_down_gemv(const float* act, const int32_t* slots, const void* weights
                      int32_t tokens, int32_t top_k, const uint8_t* w2, const float* s2,
                      int64_t w2_es, int64_t s2_es, int tiled, int32_t n_slots, int32_t hidden,
                      int32_t inter, const uint16_t* residual, uint16_t* out,
-                     const SharedRefs* sh, hipStream_t s) {
+                     const SharedRefs* sh, hipStream_t s, const TableCommit* commit) {
+  const TableCommit cm = commit ? *commit : TableCommit{};
+  const unsigned extra = commit ? 1u : 0u;
   if (sh) {
-    hipLaunchKernelGGL(down_gemv_kernel<true>, dim3(hidden / kDownRows, tokens),
+    hipLaunchKernelGGL(down_gemv_kernel<true>, dim3(hidden / kDownRows + extra, tokens),
                        dim3(64 * ((top_k + 1) / 2 + 1)), 0, s, act, slots, 0, weights, wbf16,
                        top_k, w2, s2, w2_es, s2_es, tiled, n_slots, hidden, inter, residual, out,
-                       *sh);
+                       *sh, cm);
   } else {
-    hipLaunchKernelGGL(down_gemv_kernel<false>, dim3(hidden / kDownRows, tokens),
+    hipLaunchKernelGGL(down_gemv_kernel<false>, dim3(hidden / kDownRows + extra, tokens),
                        dim3(64 * ((top_k + 1) / 2)), 0, s, act, slots, 0, weights, wbf16, top_k,
                        w2, s2, w2_es, s2_es, tiled, n_slots, hidden, inter, residual, out,
-                       SharedRefs{});
+                       SharedRefs{}, cm);
   }
   return check_launch("down_gemv_kernel");
 }

@@ -58,11 +58,12 @@ from hostpool import DRAMA3, HostPool, RecordLayout
 
 def stub_linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor) -> None:
     """The non-expert stand-in, out = x w^T with w [out, in] bf16 (an
-    nn.Linear without bias).  One token takes torch's matrix-vector product
-    (6.8 us for 2048 x 2048 on MI355X against 12.0 us for the same product
-    as a 1-row torch.mm); more tokens a matrix product."""
-    if x.shape[0] == 1:
-        torch.mv(w, x[0], out=out[0])
+    nn.Linear without bias).  Up to 4 tokens take moe_linear_bf16, one pass
+    over the weights (3.55 us for 2048 x 2048 at one token on MI355X,
+    against 6.9 us for torch.mv and 12.0 us for a 1-row torch.mm); more
+    tokens a matrix product."""
+    if x.shape[0] <= 4:
+        hipfetch.require().linear_bf16(x, w, out)
     else:
         torch.mm(x, w.t(), out=out)
 

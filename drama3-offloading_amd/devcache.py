@@ -50,10 +50,13 @@ _BACKEND_NOTED = False
 # ~192 KiB of host reads in flight, about the link's bandwidth-delay product
 # (the best of 2, 3, 4, 6 and 8 measured at 1, 3 and 8 misses).
 CPP_BLOCKS_PER_JOB = 3
-# dev_cached_forward: the misses' fetch and the expert FFN in two launches
-# (moe_fetch_ffn: the fetch workgroups run a miss's gate/up on its rows as
-# they arrive) instead of a fetch and the FFN's two; same output.  Applies
-# to tile-ordered caches of raw pools, hidden a multiple of 512, top_k <= 16.
+# dev_cached_forward: the slot resolve, the misses' fetch and the expert FFN
+# in two launches (moe_resolve_fetch_ffn: every workgroup of the first makes
+# the resolve's decisions, the fetch workgroups run a miss's gate/up on its
+# rows as they arrive, the second launch forms the output and updates the
+# table) instead of a resolve, a fetch and the FFN's two; same output, same
+# table.  Applies to tile-ordered caches of raw pools, hidden a multiple of
+# 512, top_k <= 16.
 FUSED_FFN = True
 _dev_ptr_cache: dict[int, int] = {}
 # True: init_dev_cache also keeps the layer's w13 and w2 entropy-coded in
@@ -101,6 +104,10 @@ def init_dev_cache(experts, device: torch.device, capacity: int) -> None:
     experts._dc_fexp = torch.zeros(kmax, dtype=torch.int32, device=device)
     experts._dc_nmiss = torch.zeros(1, dtype=torch.int32, device=device)
     experts._dc_stats = torch.zeros(2, dtype=torch.int64, device=device)
+    # the table's next state, staged by the fused decode call's first launch
+    # (all of whose workgroups read the table) and copied in by its second
+    experts._dc_next = tuple(torch.empty_like(t) for t in (
+        experts._dc_slot_of, experts._dc_slot_expert, experts._dc_stamp, experts._dc_step))
     experts._dc_pairs = None
     experts._dc_tiles = bool(offload.DEVICE_TILES)
     experts._dc_coded = _code_weights(experts, device) if CODED_POOL else None
@@ -271,16 +278,26 @@ def dev_cached_forward(self, x, topk_ids, topk_weights):
     if (FUSED_FFN and self._dc_tiles and getattr(self, "_dc_coded", None) is None
             and H % 512 == 0 and k <= 16 and x.dtype == torch.bfloat16 and x.is_contiguous()
             and topk_weights.dtype in (torch.float32, torch.bfloat16)):
+        # the resolve, the misses' fetch and every pick's gate/up in one
+        # launch (its workgroups make the decisions of moe_resolve_slots
+        # from the table), the down projection and the table's update in
+        # the next
         _note_backend()
         lib = hipfetch.require()
-        slots = _dev_resolve(self, topk_ids, lib)
+        if k > self._dc_out.numel():
+            raise ValueError(f"{k} ids exceed the preallocated scratch ({self._dc_out.numel()})")
+        ids = topk_ids.reshape(-1)
+        if ids.dtype not in (torch.int32, torch.int64):
+            ids = ids.to(torch.int32)
         inter = self._dc_w2.shape[-1]
         out = torch.empty_like(x)
         ws = torch.empty(k * inter * 4, dtype=torch.uint8, device=x.device)
-        lib.fetch_ffn(_fetch_pairs(self, lib), self._dc_fexp, self._dc_fslot, self._dc_nmiss,
-                      k, CPP_BLOCKS_PER_JOB, x, slots,
-                      topk_weights.reshape(-1).contiguous(), self._dc_w13, self._dc_s13,
-                      self._dc_w2, self._dc_s2, out, ws)
+        lib.resolve_fetch_ffn(ids, (self._dc_slot_of, self._dc_slot_expert, self._dc_stamp,
+                                    self._dc_step), self._dc_next, self._dc_out, self._dc_fslot,
+                              self._dc_fexp, self._dc_nmiss, _fetch_pairs(self, lib),
+                              CPP_BLOCKS_PER_JOB, x, topk_weights.reshape(-1).contiguous(),
+                              self._dc_w13, self._dc_s13, self._dc_w2, self._dc_s2, out, ws,
+                              stats=self._dc_stats)
         return out
     slots = dev_resolve_and_fetch(self, topk_ids)
     return fp8_moe_forward(x, slots.reshape(topk_ids.shape), topk_weights, self._dc_w13,

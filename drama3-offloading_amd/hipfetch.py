@@ -75,6 +75,14 @@ class FetchPair(C.Structure):
                 ("tile_k", C.c_int64)]
 
 
+class SlotTable(C.Structure):
+    """moe_slot_table (include/moe_offload.h)."""
+    _fields_ = [("slot_of", C.c_void_p), ("slot_expert", C.c_void_p), ("stamp", C.c_void_p),
+                ("step", C.c_void_p), ("n_experts", C.c_int32), ("cap", C.c_int32),
+                ("next_slot_of", C.c_void_p), ("next_slot_expert", C.c_void_p),
+                ("next_stamp", C.c_void_p), ("next_step", C.c_void_p)]
+
+
 _vp, _i32, _i64, _sz = C.c_void_p, C.c_int32, C.c_int64, C.c_size_t
 
 # name -> (restype, argtypes); every entry point of include/moe_offload.h
@@ -124,6 +132,11 @@ SIGNATURES = {
     "moe_silu_check": (C.c_int, [_vp, _vp, _vp, C.c_uint32, _vp]),
     "moe_stream_read": (C.c_int, [_vp, _i64, _i32, _vp, _vp]),
     "moe_time_fused_launch": (C.c_int, [_vp, _vp]),
+    "moe_linear_bf16": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp]),
+    "moe_resolve_fetch_ffn": (C.c_int, [_vp, _i32, _i32, C.POINTER(SlotTable), _vp, _vp, _vp, _vp,
+                                        _vp, C.POINTER(FetchPair), _i32, _i32, _vp, _vp, _i32, _vp,
+                                        _vp, _vp, _vp, _i32, _i32, C.POINTER(ExpertStrides), _vp,
+                                        _vp, _vp, _sz, _vp]),
     "moe_codec_histogram": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _i32]),
     "moe_codec_bound": (_i64, [_i64, _i64]),
     "moe_codec_encode": (_i64, [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i32]),
@@ -502,6 +515,50 @@ class Native:
             out.data_ptr(), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
             self.stream()), what)
 
+    def resolve_fetch_ffn(self, ids, table, next_table, out_slot, fetch_slot, fetch_expert,
+                          nmiss, pairs, blocks_per_job: int, x, weights, w13, s13, w2, s2, out,
+                          workspace, residual=None, stats=None) -> None:
+        """The drop-in's decode call in two launches (moe_resolve_fetch_ffn):
+        the slot resolve of ids [top_k] on table = (slot_of [E], slot_expert
+        [C], stamp [C], step [1]) made by the fetch + gate/up launch itself,
+        the next table staged in next_table (the same shapes) and copied
+        into `table` by the down launch; out [1, H] bf16 = residual + MoE(x)."""
+        import torch
+        what = "moe_resolve_fetch_ffn"
+        self._on_gpu(what, ids, *table, *next_table, out_slot, fetch_slot, fetch_expert, nmiss,
+                     x, weights, w13, s13, w2, s2, out, workspace, residual, stats)
+        if x.dim() != 2 or x.shape[0] != 1:
+            raise ValueError(f"{what} takes exactly one token")
+        H = x.shape[1]
+        K = ids.numel()
+        slot_of, slot_expert, stamp, step = table
+        E, cap = slot_of.numel(), slot_expert.numel()
+        self._buf(what, "ids", ids, K, torch.int32, torch.int64)
+        self._slot_bufs(what, slot_of, E, slot_expert, stamp, step, out_slot, K, fetch_slot,
+                        fetch_expert, nmiss, stats)
+        for name, t, ref in zip(("next_slot_of", "next_slot_expert", "next_stamp", "next_step"),
+                                next_table, table):
+            self._buf(what, name, t, ref.numel(), ref.dtype)
+        self._buf(what, "x", x, H, torch.bfloat16)
+        self._buf(what, "weights", weights, K, torch.float32, torch.bfloat16)
+        self._buf(what, "out", out, H, torch.bfloat16)
+        self._buf(what, "residual", residual, H, torch.bfloat16)
+        self._buf(what, "workspace", workspace, 0)
+        if w13.shape[0] != cap:
+            raise ValueError(f"{what}: the cache holds {w13.shape[0]} slots, the table {cap}")
+        es = _expert_strides(w13, s13, w2, s2, LAYOUT_TILES)
+        tab = SlotTable(slot_of.data_ptr(), slot_expert.data_ptr(), stamp.data_ptr(),
+                        step.data_ptr(), E, cap, *(t.data_ptr() for t in next_table))
+        arr = (FetchPair * len(pairs))(*[FetchPair(*((tuple(p) + (0,))[:4])) for p in pairs])
+        self._check(self.cdll.moe_resolve_fetch_ffn(
+            ids.data_ptr(), self._dtype_code(ids), K, C.byref(tab), out_slot.data_ptr(),
+            fetch_slot.data_ptr(), fetch_expert.data_ptr(), nmiss.data_ptr(), self._ptr(stats),
+            arr, len(pairs), blocks_per_job, x.data_ptr(), weights.data_ptr(),
+            self._dtype_code(weights), w13.data_ptr(), s13.data_ptr(), w2.data_ptr(),
+            s2.data_ptr(), H, w2.shape[-1], C.byref(es), self._ptr(residual), out.data_ptr(),
+            workspace.data_ptr(), workspace.numel() * workspace.element_size(), self.stream()),
+            what)
+
     # ------------------------------------------------------------ experts
     def fp8_moe_workspace(self, tokens, top_k, n_experts, hidden, inter) -> int:
         return int(self.cdll.moe_fp8_moe_workspace(tokens, top_k, n_experts, hidden, inter))
@@ -692,6 +749,22 @@ class Native:
         self._check(self.cdll.moe_stream_read(src.data_ptr() + offset, nbytes, workgroups,
                                                sink.data_ptr(), self.stream()),
                     "moe_stream_read")
+
+    def linear_bf16(self, x, w, out, rows_per_wave: int = 0) -> None:
+        """out [T, N] = x [T, K] w^T, w [N, K] bf16 (nn.Linear layout), 1 <= T <= 4
+        (moe_linear_bf16)."""
+        import torch
+        what = "moe_linear_bf16"
+        self._on_gpu(what, x, w, out)
+        if x.dim() != 2 or w.dim() != 2 or x.shape[1] != w.shape[1]:
+            raise ValueError(f"{what}: x [T, K] and w [N, K] must agree on K")
+        T, K = x.shape
+        N = w.shape[0]
+        self._buf(what, "x", x, T * K, torch.bfloat16)
+        self._buf(what, "w", w, N * K, torch.bfloat16)
+        self._buf(what, "out", out, T * N, torch.bfloat16)
+        self._check(self.cdll.moe_linear_bf16(x.data_ptr(), w.data_ptr(), T, K, N, out.data_ptr(),
+                                              rows_per_wave, self.stream()), what)
 
     def time_fused_launch(self, start, stop) -> None:
         """Arm torch.cuda.Event start/stop (enable_timing=True) around this

@@ -77,6 +77,17 @@ int moe_silu_check(const float* g, const float* u, float* out, uint32_t n, void*
 int moe_stream_read(const void* src, int64_t bytes, int32_t workgroups, uint32_t* sink,
                     void* stream);
 
+/* y[t] = x[t] W^T in bf16 for 1..4 tokens: W [out_features, in_features]
+ * bf16 (nn.Linear layout, in_features a multiple of 8), x [tokens,
+ * in_features], y [tokens, out_features]; each output the f32 sum of its
+ * row's products (per lane in slice order, then a fixed lane tree), rounded
+ * once to bf16.  rows_per_wave: 1, 2 or 4 rows per wave, 0 for the default
+ * (1); the outputs do not depend on it.  x and w 16-byte aligned.  No counterpart in the reference: the
+ * decode benchmark's stand-in for the non-expert compute of a layer (one
+ * [2048, 2048] matrix) runs on it, one pass over the weights. */
+int moe_linear_bf16(const void* x, const void* w, int32_t tokens, int32_t in_features,
+                    int32_t out_features, void* y, int32_t rows_per_wave, void* stream);
+
 /* Measurement: the calling thread's next moe_route_fetch_ffn or
  * moe_fetch_ffn call records `start` and `stop` (hipEvent_t, created by the
  * caller) around its fetch + gate/up launch alone, through
@@ -279,8 +290,10 @@ int moe_route_fetch_ffn(const void* x, const void* w, const float* bias, int32_t
  * max_jobs <= 32), weights [top_k] w_dtype MOE_F32/MOE_BF16, out [hidden]
  * bf16 = bf16(residual + bf16(MoE(x))) (residual nullable), the workspace
  * top_k * inter floats.  Constraints: those of moe_route_fetch_ffn on
- * hidden, inter and top_k; the w13/s13 pairs fill the cache buffers w13/s13
- * (dense); strides->layout MOE_LAYOUT_TILES.  Replaces fetch_experts +
+ * hidden, inter and top_k; the w13/s13 and w2/s2 pairs fill the cache
+ * buffers w13/s13 and w2/s2 (dense); strides->layout MOE_LAYOUT_TILES.
+ * A slot that two picks share (an expert repeated in the row) is fetched
+ * once and both picks read its activations.  Replaces fetch_experts +
  * fp8_moe_forward in dev_cached_forward (bin/devcache.py:270-277); no
  * single counterpart. */
 int moe_fetch_ffn(const moe_fetch_pair* pairs, int32_t npairs, const int32_t* fetch_expert,
@@ -291,6 +304,48 @@ int moe_fetch_ffn(const moe_fetch_pair* pairs, int32_t npairs, const int32_t* fe
                   int32_t hidden, int32_t inter, const struct moe_expert_strides* strides,
                   const void* residual, void* out, void* workspace, size_t workspace_bytes,
                   void* stream);
+
+/* A slot table in the reference's single-buffer form (bin/devcache.py:146-
+ * 152: slot_of [n_experts] int32, slot_expert [cap] int32, stamp [cap]
+ * int64, step [1] int64) and staging of the same sizes for its next state:
+ * the launch that resolves a call writes the next state there, because all
+ * its workgroups read the table, and the launch after it copies it in. */
+typedef struct moe_slot_table {
+  int32_t* slot_of;
+  int32_t* slot_expert;
+  int64_t* stamp;
+  int64_t* step;
+  int32_t n_experts;
+  int32_t cap;
+  int32_t* next_slot_of;
+  int32_t* next_slot_expert;
+  int64_t* next_stamp;
+  int64_t* next_step;
+} moe_slot_table;
+
+/* The drop-in's whole decode call in two launches: moe_resolve_slots on the
+ * reference's table for ids [top_k] (ids_dtype MOE_I32/MOE_I64), then
+ * moe_fetch_ffn.  Every workgroup of the first launch makes the call's slot
+ * decisions from the table (the decisions of moe_resolve_slots, bit for
+ * bit), workgroup 0 writes out_slot [top_k], the miss list (fetch_slot,
+ * fetch_expert [top_k], nmiss), the hit/miss counters `stats` (nullable)
+ * and the table's next state into the staging; the misses are fetched and
+ * every pick's gate/up formed as in moe_fetch_ffn; the down launch forms
+ * the output and copies the staging into the table, so the table holds the
+ * call's decisions when the call's work is done, as after
+ * moe_resolve_slots.  Constraints: those of moe_fetch_ffn with n_slots =
+ * table->cap and max_jobs = top_k; 1 <= n_experts <= 1024, top_k <= cap <=
+ * 1024.  Replaces _resolve_slots + fetch_experts + fp8_moe_forward in
+ * dev_cached_forward (bin/devcache.py:230-277); no single counterpart. */
+int moe_resolve_fetch_ffn(const void* ids, int32_t ids_dtype, int32_t top_k,
+                          const moe_slot_table* table, int32_t* out_slot, int32_t* fetch_slot,
+                          int32_t* fetch_expert, int32_t* nmiss, int64_t* stats,
+                          const moe_fetch_pair* pairs, int32_t npairs, int32_t blocks_per_job,
+                          const void* x, const void* weights, int32_t w_dtype, const void* w13,
+                          const float* s13, const void* w2, const float* s2, int32_t hidden,
+                          int32_t inter, const struct moe_expert_strides* strides,
+                          const void* residual, void* out, void* workspace,
+                          size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------- expert compute */
 

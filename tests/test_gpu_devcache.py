@@ -365,3 +365,108 @@ def test_decode_row_wider_than_the_cache_takes_the_gather(lib, dev, pair):
     assert torch.equal(got, want)
     for t0, t1 in zip(before, (host._dc_slot_of, host._dc_stamp, host._dc_step)):
         assert torch.equal(t0, t1)
+
+
+def _twin(host):
+    import moe
+    t = moe.MoEExperts(E, H, I, device="cpu")
+    for n in ("w13_weight", "w2_weight", "w13_scale_inv", "w2_scale_inv"):
+        setattr(t, n, getattr(host, n))          # the same pinned tensors
+    return t
+
+
+@pytest.mark.parametrize("cap,ids64", [(9, True), (20, False)])
+def test_resolve_fetch_ffn_equals_resolve_then_fetch_ffn(lib, dev, pair, cap, ids64,
+                                                         monkeypatch):
+    """moe_resolve_fetch_ffn (the resolve made by every workgroup of the
+    fetch + gate/up launch, the table staged and copied in by the down
+    launch) against moe_resolve_slots followed by moe_fetch_ffn on a twin
+    cache, call for call: outputs (bit patterns: an out-of-range id gives a
+    NaN row in both), out_slot, the miss list, the counters and the tables
+    equal; rows repeat experts and one names an expert past the table."""
+    import devcache
+    import offload
+    ref, host = pair
+    twin = _twin(host)
+    monkeypatch.setattr(offload, "DEVICE_TILES", True)
+    monkeypatch.setattr(devcache, "FUSED_FFN", True)
+    devcache.init_dev_cache(host, dev, cap)
+    devcache.init_dev_cache(twin, dev, cap)
+    lib_ = lib
+    rows = _rows_with_repeats(E, K, 24, 40 + cap)
+    rows.insert(5, torch.tensor([[1, 2, E + 3, 4, 5, 6, 7, 8]]))
+    g = torch.Generator().manual_seed(cap)
+    ws = torch.empty(K * I * 4, dtype=torch.uint8, device=dev)
+    for step, ids_cpu in enumerate(rows):
+        ids = ids_cpu.to(dev) if ids64 else ids_cpu.to(torch.int32).to(dev)
+        x = torch.randn((1, H), generator=g).to(torch.bfloat16).to(dev)
+        w = torch.softmax(torch.rand((1, K), generator=g), -1).to(dev)
+        say(f"resolve_fetch_ffn: capacity {cap}, step {step}, ids {ids_cpu.tolist()}")
+        got = devcache.dev_cached_forward(host, x, ids, w)
+        # the three-launch form on the twin
+        lib_.resolve_slots(ids.reshape(-1), twin._dc_slot_of, twin._dc_slot_expert,
+                           twin._dc_stamp, twin._dc_step, twin._dc_out, twin._dc_fslot,
+                           twin._dc_fexp, twin._dc_nmiss, twin._dc_stats)
+        want = torch.empty_like(x)
+        lib_.fetch_ffn(devcache._fetch_pairs(twin, lib_), twin._dc_fexp, twin._dc_fslot,
+                       twin._dc_nmiss, K, devcache.CPP_BLOCKS_PER_JOB, x, twin._dc_out[:K],
+                       w.reshape(-1), twin._dc_w13, twin._dc_s13, twin._dc_w2, twin._dc_s2,
+                       want, ws)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"step {step}"
+        n = int(host._dc_nmiss[0])
+        assert n == int(twin._dc_nmiss[0]), f"step {step}"
+        assert torch.equal(host._dc_out[:K], twin._dc_out[:K]), f"step {step}"
+        assert torch.equal(host._dc_fslot[:n], twin._dc_fslot[:n]), f"step {step}"
+        assert torch.equal(host._dc_fexp[:n], twin._dc_fexp[:n]), f"step {step}"
+        for a in ("_dc_slot_of", "_dc_slot_expert", "_dc_stamp", "_dc_step", "_dc_stats"):
+            assert torch.equal(getattr(host, a), getattr(twin, a)), (step, a)
+        if step == 5:
+            assert bool(torch.isnan(got.float()).all())
+    for c_ in ("_dc_w13", "_dc_w2", "_dc_s13", "_dc_s2"):
+        assert torch.equal(getattr(host, c_).view(torch.uint8), getattr(twin, c_).view(torch.uint8))
+
+
+def test_resolve_fetch_ffn_graph_replays_match_eager(lib, dev, pair, monkeypatch):
+    """dev_cached_forward on the two-launch path captured once: every replay
+    (new ids, new x, eager work and syncs between replays) equals the same
+    call made eagerly on a twin cache, tables included."""
+    import devcache
+    import offload
+    ref, host = pair
+    twin = _twin(host)
+    monkeypatch.setattr(offload, "DEVICE_TILES", True)
+    monkeypatch.setattr(devcache, "FUSED_FFN", True)
+    devcache.init_dev_cache(host, dev, 16)
+    devcache.init_dev_cache(twin, dev, 16)
+    ids_live = torch.zeros((1, K), dtype=torch.int64, device=dev)
+    x_live = torch.zeros((1, H), dtype=torch.bfloat16, device=dev)
+    w_live = torch.full((1, K), 1.0 / K, device=dev)
+    rows = _rows_with_repeats(E, K, 8, 77)
+    ids_live.copy_(rows[0])
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        devcache.dev_cached_forward(host, x_live, ids_live, w_live)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    devcache.reset_dev_cache(host)
+    g_ = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_):
+        out = devcache.dev_cached_forward(host, x_live, ids_live, w_live)
+    devcache.reset_dev_cache(host)
+    gen = torch.Generator().manual_seed(3)
+    for r, ids_cpu in enumerate(rows):
+        x = torch.randn((1, H), generator=gen).to(torch.bfloat16).to(dev)
+        ids_live.copy_(ids_cpu)
+        x_live.copy_(x)
+        g_.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        _ = torch.randn(1000, device=dev).sum().item()      # eager work between replays
+        want = devcache.dev_cached_forward(twin, x, ids_cpu.to(dev), w_live)
+        torch.cuda.synchronize()
+        say(f"resolve_fetch_ffn graph replay {r}")
+        assert torch.equal(got, want), f"replay {r}"
+        for a in ("_dc_slot_of", "_dc_slot_expert", "_dc_stamp", "_dc_step", "_dc_stats"):
+            assert torch.equal(getattr(host, a), getattr(twin, a)), (r, a)

@@ -1,0 +1,65 @@
+"""moe_linear_bf16, the decode benchmark's non-expert stand-in (y = x W^T,
+bf16, 1-4 tokens): against the float64 product of the same bf16 operands
+rounded once to bf16 (the f32 sum may round differently on a value close to
+a bf16 midpoint: at most 1 ulp, on few outputs), identical for 1, 2 and 4
+rows per wave (each row's sum does not depend on the grid), and within 1
+ulp of torch's own bf16 matrix-vector product."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import say
+from oracle import router as orouter
+
+pytestmark = pytest.mark.gpu
+
+
+def _ulps(a, b):
+    """Distance in bf16 steps between two bf16 tensors of finite values."""
+    ia = a.view(torch.int16).to(torch.int32)
+    ib = b.view(torch.int16).to(torch.int32)
+    # order-preserving map of the sign-magnitude bit patterns
+    ka = torch.where(ia < 0, -(ia & 0x7fff), ia)
+    kb = torch.where(ib < 0, -(ib & 0x7fff), ib)
+    return (ka - kb).abs()
+
+
+@pytest.mark.parametrize("T,K,N", [(1, 2048, 2048), (3, 2048, 2048), (4, 264, 1001),
+                                   (1, 8, 5), (2, 520, 64)])
+def test_linear_bf16_against_float64(lib, dev, T, K, N):
+    g = torch.Generator(device="cpu").manual_seed(K + N + T)
+    x = torch.randn((T, K), generator=g).to(torch.bfloat16)
+    w = (torch.randn((N, K), generator=g) / K ** 0.5).to(torch.bfloat16)
+    exact = x.double() @ w.double().T
+    want = torch.from_numpy(orouter.bf16_round(exact.numpy())).to(torch.bfloat16)
+    xd, wd = x.to(dev), w.to(dev)
+    outs = []
+    for rpw in (0, 1, 2, 4):
+        y = torch.full((T, N), float("nan"), dtype=torch.bfloat16, device=dev)
+        say(f"linear_bf16: T={T} K={K} N={N} rows_per_wave={rpw}")
+        lib.linear_bf16(xd, wd, y, rows_per_wave=rpw)
+        outs.append(y)
+    torch.cuda.synchronize()
+    for y in outs[1:]:
+        assert torch.equal(y.view(torch.int16), outs[0].view(torch.int16))
+    got = outs[0].cpu()
+    assert bool(torch.isfinite(got.float()).all())
+    d = _ulps(got, want)
+    assert int(d.max()) <= 1
+    assert float((d == 0).float().mean()) >= 0.99
+    if T == 1:
+        ref = torch.mv(wd, xd[0]).cpu()
+        assert int(_ulps(got[0], ref).max()) <= 1
+
+
+def test_linear_bf16_preconditions(lib, dev):
+    import hipfetch
+    x = torch.zeros((5, 64), dtype=torch.bfloat16, device=dev)
+    w = torch.zeros((16, 64), dtype=torch.bfloat16, device=dev)
+    y = torch.zeros((5, 16), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(hipfetch.NativeError, match="tokens"):
+        lib.linear_bf16(x, w, y)
+    with pytest.raises(hipfetch.NativeError, match="rows_per_wave"):
+        lib.linear_bf16(x[:1], w, y[:1], rows_per_wave=3)
+    with pytest.raises(ValueError, match="agree"):
+        lib.linear_bf16(x[:1, :32], w, y[:1])

@@ -119,6 +119,37 @@ def test_fetch_ffn_refuses_pairs_that_miss_the_cache_buffers(lib):
         assert msg in c.moe_last_error(), (msg, c.moe_last_error())
 
 
+def test_resolve_fetch_ffn_refuses_bad_tables(lib):
+    """moe_resolve_fetch_ffn checks the ids dtype, the table's sizes and
+    that the staging is not the table itself before any launch (each case
+    below fails a check ahead of the launch)."""
+    import ctypes as C
+    import hipfetch
+    c = lib.cdll
+    H, I = 2048, 512
+    W13, W2, S13, S2 = 0x100000, 0x200000, 0x300000, 0x400000
+    pairs = (hipfetch.FetchPair * 4)(*[hipfetch.FetchPair(*p) for p in (
+        (0x10000, W13, 2 * I * H, H), (0x20000, W2, H * I, I), (0x30000, S13, 512, 0),
+        (0x40000, S2, 256, 0))])
+    es = hipfetch.ExpertStrides(2 * I * H, 128, H * I, 64, hipfetch.LAYOUT_TILES)
+    one = C.c_void_p(256)
+
+    def call(ids_dtype=hipfetch.MOE_I32, top_k=8, E=256, cap=16, alias=False):
+        t = hipfetch.SlotTable(0x1000, 0x2000, 0x3000, 0x4000, E, cap,
+                               0x1000 if alias else 0x5000, 0x6000, 0x7000, 0x8000)
+        return c.moe_resolve_fetch_ffn(one, ids_dtype, top_k, C.byref(t), one, one, one, one, None,
+                                       pairs, 4, 3, one, one, hipfetch.MOE_F32, W13, S13, W2, S2,
+                                       H, I, C.byref(es), None, one, one, 1 << 20, None)
+    for kw, msg in ((dict(ids_dtype=hipfetch.MOE_F32), b"ids_dtype"),
+                    (dict(E=2000), b"n_experts"),
+                    (dict(cap=2000), b"cap"),
+                    (dict(top_k=12, cap=10), b"exceeds the cache capacity"),
+                    (dict(alias=True), b"staging"),
+                    (dict(top_k=17, cap=20), b"top_k")):
+        assert call(**kw) == -1, msg
+        assert msg in c.moe_last_error(), (msg, c.moe_last_error())
+
+
 def test_shared_and_block_preconditions_are_rejected_without_launching(lib):
     import ctypes as C
     import hipfetch
