@@ -427,10 +427,14 @@ def graph_time(dev, body, calls: int) -> float:
     return a.elapsed_time(b) / 1000.0 / calls
 
 
-def gemv_resident(lib, dev, layout, n_records: int = 2048, calls: int = 200, top_k: int = 8):
+def gemv_resident(lib, dev, layout, n_records: int = 2048, calls: int = 200, top_k: int = 8,
+                  idle_cycles: int = 0):
     """Decode expert FFN (gate/up GEMV + down GEMV, 8 experts, 1 token) over
     random experts of n_records resident records (6.4 GB at 2048, so the
-    256 MB Infinity Cache serves few of them).  Returns (s/call, bytes/call)."""
+    256 MB Infinity Cache serves few of them).  Returns (s/call, bytes/call).
+    idle_cycles > 0 puts a one-workgroup spin of that many cycles before
+    each call (the GPU idles as in a link-bound decode layer; the per-call
+    time then includes the spin, and the kernel trace gives the kernels')."""
     import numpy as np
     import torch
     rec = resident_records(dev, n_records, layout)
@@ -443,8 +447,11 @@ def gemv_resident(lib, dev, layout, n_records: int = 2048, calls: int = 200, top
     out = torch.empty_like(x)
     ws = torch.empty(lib.fp8_moe_workspace(1, top_k, n_records, layout.hidden, layout.inter),
                      dtype=torch.uint8, device=dev)
-    dt = graph_time(dev, lambda r: lib.fp8_moe_forward(x, ids[r], w, *views, out, ws, mode=1,
-                                                      layout=layout.code), calls)
+    def body(r):
+        if idle_cycles:
+            torch.cuda._sleep(idle_cycles)
+        lib.fp8_moe_forward(x, ids[r], w, *views, out, ws, mode=1, layout=layout.code)
+    dt = graph_time(dev, body, calls)
     if not bool(torch.isfinite(out.float()).all()):
         raise RuntimeError("GEMV probe produced non-finite output")
     del rec
@@ -1218,9 +1225,12 @@ def run_probe(args) -> int:
     lib = hipfetch.require()
     dev = torch.device("cuda:0")
     if args.probe == "gemv":
-        dt, nbytes = gemv_resident(lib, dev, DRAMA3, calls=args.steps)
+        dt, nbytes = gemv_resident(lib, dev, DRAMA3, calls=args.steps,
+                                   idle_cycles=int(2500 * args.idle_us))
         res = {"probe": "gemv", "what": "decode expert FFN, 8 experts x 1 token, resident records, "
-               "graph of back-to-back calls", "us_per_call": round(1e6 * dt, 3),
+               "graph of back-to-back calls" + (f", each after a {args.idle_us} us spin"
+                                                if args.idle_us else ""),
+               "us_per_call": round(1e6 * dt, 3),
                "bytes_per_call": nbytes, "GBps": round(nbytes / dt / 1e9, 2)}
     elif args.probe == "fetch":
         pools = [HostPool(256, DRAMA3) for _ in range(4)]
@@ -1592,6 +1602,8 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the prefill and all-resident measurements")
     ap.add_argument("--tokens", type=int, default=512, help="tokens per call of --probe grouped")
+    ap.add_argument("--idle-us", type=float, default=0.0,
+                    help="--probe gemv: a spin of about this many microseconds before each call")
     ap.add_argument("--misses", type=int, default=8,
                     help="misses per call of --probe routefetch (0..8)")
     ap.add_argument("--probe", choices=["gemv", "fetch", "codec", "copy", "grouped", "shared",
