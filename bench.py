@@ -1554,11 +1554,12 @@ def cpu_baseline(harness, budget_s: float):
     cfg = harness.cfg
     w_stub = harness.w_stub.float().cpu()
     gate = harness.gate.float().cpu()
-    bias = harness.bias_all[0].cpu()
+    bias_steps = harness.bias_all[:20].cpu()          # the schedule's first 20 steps
+    bias = bias_steps[0]
     records = [p.tensor for p in harness.pools]
     x0 = harness.x0.float().cpu()
     torch.set_num_threads(os.cpu_count() or 1)
-    sec_per_tok, layers_run, threads = cpu_moe.time_decode(w_stub, gate, bias, records,
+    sec_per_tok, layers_run, threads = cpu_moe.time_decode(w_stub, gate, bias_steps, records,
                                                            harness.layout, x0, budget_s, cfg.top_k)
     layer_all = cpu_moe.time_single_layer(x0, w_stub, gate, bias, records, harness.layout,
                                           cfg.top_k, iters=20)
@@ -1575,7 +1576,8 @@ def cpu_baseline(harness, budget_s: float):
         pass
     return {"value": round(1.0 / sec_per_tok, 4), "unit": "tokens/s", "cores": threads,
             "kind": "port",
-            "sample": (f"{layers_run} layer evaluations ({layers_run / cfg.layers:.2f} tokens) of "
+            "sample": (f"{layers_run} layer evaluations ({layers_run / cfg.layers:.2f} tokens, "
+                       f"each on its own schedule step's routing) of "
                        f"the same 40-layer decode step on the host cores: stub matmul, router, "
                        f"dequantise-then-matmul MoE reading the page-locked pool; float32 torch, "
                        f"{threads} threads, os.cpu_count()={os.cpu_count()}, CPU '{model}'"),
@@ -1596,7 +1598,8 @@ def main() -> int:
     ap.add_argument("--target-hit", type=float, default=0.60)
     ap.add_argument("--capacity", type=int, default=0, help="per-layer slots (0 = size for --target-hit)")
     ap.add_argument("--layers", type=int, default=40)
-    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
+    ap.add_argument("--cpu-budget", type=float, default=25.0,
+                    help="seconds of CPU baseline work (at most 20 tokens)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--noncoherent-pool", action="store_true")
     ap.add_argument("--no-extra", action="store_true",

@@ -85,25 +85,32 @@ def decode_step_cpu(x, w_stub, gate, bias, records, layout, top_k=8, layers=None
     return x
 
 
-def time_decode(w_stub, gate, bias, records, layout, x0, budget_s: float = 12.0,
-                top_k: int = 8):
-    """Run whole layers until ~budget_s of CPU work; returns
-    (seconds per token, layers run, threads)."""
+def time_decode(w_stub, gate, bias, records, layout, x0, budget_s: float = 25.0,
+                top_k: int = 8, max_tokens: int = 20):
+    """Run whole layers, token after token, until ~budget_s of CPU work or
+    max_tokens tokens; bias [L, E], or [S, L, E] for token t to take the
+    routing bias of schedule step t % S.  Returns (seconds per token,
+    layers run, threads)."""
     global UNTILE_SECONDS
     L = w_stub.shape[0]
+    per_step = bias.dim() == 3
+    step_bias = (lambda t: bias[t % bias.shape[0]]) if per_step else (lambda t: bias)
     x = x0
     # warm-up one layer
-    decode_step_cpu(x, w_stub[:1], gate[:1], bias[:1], records[:1], layout, top_k)
+    decode_step_cpu(x, w_stub[:1], gate[:1], step_bias(0)[:1], records[:1], layout, top_k)
     UNTILE_SECONDS = 0.0
     t0 = time.perf_counter()
     done = 0
     while True:
         l = done % L
-        x = decode_step_cpu(x, w_stub[l:l + 1], gate[l:l + 1], bias[l:l + 1],
+        if l == 0:
+            x = x0                      # every token starts from the same input state
+        b = step_bias(done // L)
+        x = decode_step_cpu(x, w_stub[l:l + 1], gate[l:l + 1], b[l:l + 1],
                             records[l:l + 1], layout, top_k)
         done += 1
         el = time.perf_counter() - t0 - UNTILE_SECONDS
-        if (el >= budget_s and done >= 4) or done >= 4 * L:
+        if (el >= budget_s and done >= 4) or done >= max_tokens * L:
             break
     per_layer = el / done
     return per_layer * L, done, torch.get_num_threads()
