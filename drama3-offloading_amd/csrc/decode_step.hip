@@ -3,8 +3,9 @@
 // misses' fetch and the gate/up half of the expert FFN in one launch; the
 // down half.  The separate form is moe_route_fetch followed by
 // moe_fp8_moe_forward_ex (four launches); both give the same bytes.  The
-// drop-in's form (moe_fetch_ffn, fetch_gateup_kernel below) does the same
-// after the resolve launch, on the reference's four buffers.
+// drop-in's form (fetch_gateup_kernel below) does the same on the
+// reference's four buffers and single-buffer slot table, after a resolve
+// launch (moe_fetch_ffn) or making the resolve itself (moe_resolve_fetch_ffn).
 //
 // Records: w13 [2I, H] | w2 [H, I] in MFMA tile order | s13 [2I/128, H/128]
 // | s2 [H/128, I/128] f32, record_bytes apart in the host pool and in the

@@ -210,9 +210,9 @@ def _note_backend() -> None:
               file=_sys.stderr, flush=True)
 
 
-def _dev_resolve(experts, topk_ids: torch.Tensor, lib) -> torch.Tensor:
-    """The slot resolve of dev_resolve_and_fetch alone: slots [k] int32 and
-    the miss list in experts._dc_fexp/_dc_fslot/_dc_nmiss, no sync."""
+def _call_ids(experts, topk_ids: torch.Tensor) -> torch.Tensor:
+    """One decode call's ids, flat, int32 or int64, checked against the
+    cache's capacity and the per-call scratch."""
     k = topk_ids.numel()
     if k > experts._dc_cap:
         # more ids than slots would make the table hand out a slot twice in
@@ -222,8 +222,14 @@ def _dev_resolve(experts, topk_ids: torch.Tensor, lib) -> torch.Tensor:
     if k > experts._dc_out.numel():
         raise ValueError(f"{k} ids exceed the preallocated scratch ({experts._dc_out.numel()})")
     ids = topk_ids.reshape(-1)
-    if ids.dtype not in (torch.int32, torch.int64):
-        ids = ids.to(torch.int32)
+    return ids if ids.dtype in (torch.int32, torch.int64) else ids.to(torch.int32)
+
+
+def _dev_resolve(experts, topk_ids: torch.Tensor, lib) -> torch.Tensor:
+    """The slot resolve of dev_resolve_and_fetch alone: slots [k] int32 and
+    the miss list in experts._dc_fexp/_dc_fslot/_dc_nmiss, no sync."""
+    k = topk_ids.numel()
+    ids = _call_ids(experts, topk_ids)
     lib.resolve_slots(ids, experts._dc_slot_of, experts._dc_slot_expert, experts._dc_stamp,
                       experts._dc_step, experts._dc_out, experts._dc_fslot, experts._dc_fexp,
                       experts._dc_nmiss, experts._dc_stats)
@@ -236,19 +242,7 @@ def dev_resolve_and_fetch(experts, topk_ids: torch.Tensor) -> torch.Tensor:
     _note_backend()
     lib = hipfetch.require()
     k = topk_ids.numel()
-    if k > experts._dc_cap:
-        # more ids than slots would make the table hand out a slot twice in
-        # one call; the reference's gather path handles such calls
-        raise ValueError(f"{k} ids exceed the cache capacity {experts._dc_cap}; "
-                         "use offload.offloaded_forward for this call")
-    if k > experts._dc_out.numel():
-        raise ValueError(f"{k} ids exceed the preallocated scratch ({experts._dc_out.numel()})")
-    ids = topk_ids.reshape(-1)
-    if ids.dtype not in (torch.int32, torch.int64):
-        ids = ids.to(torch.int32)
-    lib.resolve_slots(ids, experts._dc_slot_of, experts._dc_slot_expert, experts._dc_stamp,
-                      experts._dc_step, experts._dc_out, experts._dc_fslot, experts._dc_fexp,
-                      experts._dc_nmiss, experts._dc_stats)
+    _dev_resolve(experts, topk_ids, lib)
     coded = getattr(experts, "_dc_coded", None)
     if coded is None:
         lib.fetch(_fetch_pairs(experts, lib), experts._dc_fexp, experts._dc_fslot,
@@ -284,11 +278,7 @@ def dev_cached_forward(self, x, topk_ids, topk_weights):
         # the next
         _note_backend()
         lib = hipfetch.require()
-        if k > self._dc_out.numel():
-            raise ValueError(f"{k} ids exceed the preallocated scratch ({self._dc_out.numel()})")
-        ids = topk_ids.reshape(-1)
-        if ids.dtype not in (torch.int32, torch.int64):
-            ids = ids.to(torch.int32)
+        ids = _call_ids(self, topk_ids)
         inter = self._dc_w2.shape[-1]
         out = torch.empty_like(x)
         ws = torch.empty(k * inter * 4, dtype=torch.uint8, device=x.device)

@@ -63,8 +63,9 @@ def test_cache_is_bit_exact_against_resident(lib, dev, pair, cap, tiles, monkeyp
 
 @pytest.mark.parametrize("cap,wdtype", [(16, torch.bfloat16), (E, torch.float32), (9, torch.float32)])
 def test_hook_fetch_ffn_is_bit_exact_against_resident(lib, dev, pair, cap, wdtype, monkeypatch):
-    """dev_cached_forward through moe_fetch_ffn (the misses' gate/up run by
-    the workgroups that fetch them, the hits' beside them) against the
+    """dev_cached_forward through moe_resolve_fetch_ffn (the resolve made by
+    the fetch launch's workgroups, the misses' gate/up run by the
+    workgroups that fetch them, the hits' beside them) against the
     all-resident forward, bit for bit, and the slots' bytes in tile order."""
     import devcache
     import offload
@@ -109,7 +110,7 @@ def _rows_with_repeats(E_, K_, n, seed):
 def test_hook_fetch_ffn_repeated_expert_in_a_row(lib, dev, pair, cap, monkeypatch):
     """A row that names an expert twice (bin/devcache.py:73-97: the second
     occurrence is a hit on the slot the first one took; a miss is queued
-    once).  dev_cached_forward through moe_fetch_ffn must give every pick
+    once).  dev_cached_forward through moe_resolve_fetch_ffn must give every pick
     of that expert its activations, whether the expert misses or hits:
     the output equals the unfused path (resolve, fetch, forward on the
     slots) on a twin cache and the all-resident forward bit for bit, and
@@ -160,7 +161,7 @@ def test_hook_fetch_ffn_repeated_expert_in_a_row(lib, dev, pair, cap, monkeypatc
 @pytest.mark.parametrize("E_,H_,I_,K_,cap", [(24, 8192, 2048, 16, 18), (40, 4096, 1024, 8, 12)],
                          ids=["h8192_i2048_top16", "h4096_i1024"])
 def test_hook_fetch_ffn_at_the_limits(lib, dev, E_, H_, I_, K_, cap, monkeypatch):
-    """moe_fetch_ffn at the largest shapes it takes (hidden 8192,
+    """moe_resolve_fetch_ffn at the largest shapes it takes (hidden 8192,
     intermediate 2048, top-16) and at 4096 / 1024: through the hooks, equal
     to the unfused path on a twin cache bit for bit, step for step, with
     equal tables and tile-ordered slot bytes."""
