@@ -39,6 +39,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "route.hpp"
 
 namespace moe {
 
@@ -69,27 +70,49 @@ __device__ __forceinline__ int wave_exclusive_sum(int v) {
   return incl - v;
 }
 
-// Where unit u (job u / nblk, block u % nblk) comes from and goes to.
+// Where unit u (job u / nblk, block u % nblk) comes from and goes to; the
+// miss list through `jobs` (expert(j), slot(j), both uniform).
 struct CodedUnit {
   const uint8_t* src;   // coded block (host)
   uint8_t* dst;         // decoded block (cache slot)
   int rest;             // bytes after the nibble plane: header + streams, multiple of 16
 };
 
+template <class Jobs>
 __device__ __forceinline__ CodedUnit coded_unit(int64_t u, int32_t nblk, const uint8_t* pool,
                                                 const int64_t* rec_off, const uint32_t* blk_off,
-                                                const int32_t* fexp, const int32_t* fslot,
-                                                uint8_t* cache, int64_t slot_bytes) {
+                                                const Jobs& jobs, uint8_t* cache,
+                                                int64_t slot_bytes) {
   const int64_t j = u / nblk;
   const int b = static_cast<int>(u - j * nblk);
-  const int64_t e = fexp[j];
+  const int64_t e = jobs.expert(j);
   const uint32_t* bo = blk_off + e * (static_cast<int64_t>(nblk) + 1);
   CodedUnit c;
   c.src = pool + rec_off[e] + bo[b];
-  c.dst = cache + fslot[j] * slot_bytes + static_cast<int64_t>(b) * kCodecBlock;
+  c.dst = cache + jobs.slot(j) * slot_bytes + static_cast<int64_t>(b) * kCodecBlock;
   c.rest = static_cast<int>(bo[b + 1] - bo[b]) - kCodecPlane;
   return c;
 }
+
+// The miss list in device memory (moe_fetch_coded: the resolve's outputs).
+struct JobsInMemory {
+  const int32_t* fexp;
+  const int32_t* fslot;
+  __device__ __forceinline__ int64_t expert(int64_t j) const { return fexp[j]; }
+  __device__ __forceinline__ int64_t slot(int64_t j) const { return fslot[j]; }
+};
+
+// The miss list in LDS (the route made by the same launch), made scalar.
+struct JobsInLds {
+  const int32_t* je;
+  const int32_t* js;
+  __device__ __forceinline__ int64_t expert(int64_t j) const {
+    return __builtin_amdgcn_readfirstlane(je[j]);
+  }
+  __device__ __forceinline__ int64_t slot(int64_t j) const {
+    return __builtin_amdgcn_readfirstlane(js[j]);
+  }
+};
 
 // The host loads of one coded block for this lane: its 64 nibble-plane bytes
 // and its share of header + streams.  Only the wave-wide loads that reach
@@ -117,48 +140,41 @@ struct CodedLoads {
   }
 };
 
-// Fetch of coded records: job j copies coded record fetch_expert[j] of the
-// pool into cache slot fetch_slot[j], decoded; j < *nmiss (read on the
-// device).  The nmiss * nblk blocks are dealt to the waves of the grid
-// round-robin; a wave loads a block, then decodes it.  Waves are spread
-// thin (4 per workgroup, one workgroup per CU at the default grid), and at
-// any time only the waves between blocks have host reads outstanding.
-// Measured on MI355X, 8 records per launch: 389 us against 447 us for the
-// raw fetch; issuing the next block's loads before decoding the current one
-// (every wave holding ~7 KB in flight) lowered the link's rate from ~56 to
-// ~52 GB/s and took 412 us.  The raw tails (block scales) are copied first,
-// one per wave.
-__global__ __launch_bounds__(64 * kCodecWaves) void fetch_coded_kernel(
-    const uint8_t* __restrict__ pool, const int64_t* __restrict__ rec_off,
-    const uint32_t* __restrict__ blk_off, int32_t nblk, int64_t tail,
-    const uint16_t* __restrict__ lut_g, const int32_t* __restrict__ fexp,
-    const int32_t* __restrict__ fslot, const int32_t* __restrict__ nmiss, int32_t max_jobs,
-    uint8_t* __restrict__ cache, int64_t slot_bytes) {
-  __shared__ __align__(16) uint8_t lds[kCodecWaves][kCodecLds];
-  __shared__ uint16_t lut[kCodecLutSize];
+// The fetch of nm coded records by the grid's waves: job j copies coded
+// record jobs.expert(j) into cache slot jobs.slot(j), decoded.  The nm * nblk
+// blocks are dealt to the waves round-robin; a wave loads a block, then
+// decodes it.  Waves are spread thin (4 per workgroup, one workgroup per CU
+// at the default grid), and at any time only the waves between blocks have
+// host reads outstanding.  Measured on MI355X, 8 records per launch: 389 us
+// against 447 us for the raw fetch; issuing the next block's loads before
+// decoding the current one (every wave holding ~7 KB in flight) lowered the
+// link's rate from ~56 to ~52 GB/s and took 412 us.  The raw tails (block
+// scales) are copied first, one per wave.  `lut` is the decode table in LDS.
+template <class Jobs>
+__device__ __forceinline__ void coded_fetch_run(
+    const Jobs& jobs, int32_t nm, const uint8_t* __restrict__ pool,
+    const int64_t* __restrict__ rec_off, const uint32_t* __restrict__ blk_off, int32_t nblk,
+    int64_t tail, const uint16_t* lut, uint8_t* __restrict__ cache, int64_t slot_bytes,
+    uint8_t (*lds)[kCodecLds]) {
   // wave-uniform as a scalar: block indices and addresses then come from
   // scalar loads, which do not wait behind this wave's host loads
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  for (int i = threadIdx.x; i < kCodecLutSize; i += 64 * kCodecWaves) lut[i] = lut_g[i];
-  __syncthreads();
-  const int32_t nm = min(*nmiss, max_jobs);
   const int64_t gw = static_cast<int64_t>(blockIdx.x) * kCodecWaves + wave;   // global wave
   const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kCodecWaves;
   for (int64_t j = gw; j < nm; j += nwaves) {     // raw tails
-    const int64_t e = fexp[j];
+    const int64_t e = jobs.expert(j);
     const uint8_t* src = pool + rec_off[e] + blk_off[e * (static_cast<int64_t>(nblk) + 1) + nblk];
-    uint8_t* dst = cache + fslot[j] * slot_bytes + static_cast<int64_t>(nblk) * kCodecBlock;
+    uint8_t* dst = cache + jobs.slot(j) * slot_bytes + static_cast<int64_t>(nblk) * kCodecBlock;
     for (int64_t i = lane * 16; i < tail; i += 64 * 16)
       *reinterpret_cast<u32x4*>(dst + i) = *reinterpret_cast<const u32x4*>(src + i);
   }
   const int64_t units = static_cast<int64_t>(nm) * nblk;
-  if (gw >= units) return;                        // this wave has no block (no barrier below)
+  if (gw >= units) return;                        // this wave has no block (no barrier follows)
   const uint32_t* w32 = reinterpret_cast<const uint32_t*>(lds[wave]);
   CodedLoads ld;
   for (int64_t u = gw; u < units; u += nwaves) {
-    const CodedUnit cur =
-        coded_unit(u, nblk, pool, rec_off, blk_off, fexp, fslot, cache, slot_bytes);
+    const CodedUnit cur = coded_unit(u, nblk, pool, rec_off, blk_off, jobs, cache, slot_bytes);
     ld.issue(cur, lane);
     // this block's header + streams to LDS, its nibbles to registers
 #pragma unroll
@@ -207,6 +223,58 @@ __global__ __launch_bounds__(64 * kCodecWaves) void fetch_coded_kernel(
       d[q] = u32x4{ow[0], ow[1], ow[2], ow[3]};
     }
   }
+}
+
+// Fetch of coded records: job j copies coded record fetch_expert[j] of the
+// pool into cache slot fetch_slot[j], decoded; j < *nmiss (read on the
+// device).
+__global__ __launch_bounds__(64 * kCodecWaves) void fetch_coded_kernel(
+    const uint8_t* __restrict__ pool, const int64_t* __restrict__ rec_off,
+    const uint32_t* __restrict__ blk_off, int32_t nblk, int64_t tail,
+    const uint16_t* __restrict__ lut_g, const int32_t* __restrict__ fexp,
+    const int32_t* __restrict__ fslot, const int32_t* __restrict__ nmiss, int32_t max_jobs,
+    uint8_t* __restrict__ cache, int64_t slot_bytes) {
+  __shared__ __align__(16) uint8_t lds[kCodecWaves][kCodecLds];
+  __shared__ uint16_t lut[kCodecLutSize];
+  for (int i = threadIdx.x; i < kCodecLutSize; i += 64 * kCodecWaves) lut[i] = lut_g[i];
+  __syncthreads();
+  const int32_t nm = min(*nmiss, max_jobs);
+  coded_fetch_run(JobsInMemory{fexp, fslot}, nm, pool, rec_off, blk_off, nblk, tail, lut, cache,
+                  slot_bytes, lds);
+}
+
+// The decode step's route and the coded fetch of its misses in one launch
+// (moe_route_fetch_coded): every workgroup's first wave makes the route
+// (route.hpp: top-k + slot resolve on the double-buffered table, workgroup
+// 0 writing the outputs and the next table) while the others copy the
+// decode table to LDS; then all its waves decode the misses' blocks from
+// the miss list in LDS, as fetch_coded_kernel does from memory.
+template <int PER, int PERC>
+__global__ __launch_bounds__(64 * kCodecWaves) void route_fetch_coded_kernel(
+    const float* __restrict__ logits, int32_t n_experts, int32_t top_k, int32_t* __restrict__ ids,
+    float* __restrict__ weights, int32_t* __restrict__ slot_of, int32_t* __restrict__ slot_expert,
+    int64_t* __restrict__ stamp, int32_t cap, const int64_t* __restrict__ step_ptr,
+    int32_t* __restrict__ out_slot, int32_t* __restrict__ fetch_slot,
+    int32_t* __restrict__ fetch_expert, int32_t* __restrict__ nmiss_ptr,
+    int64_t* __restrict__ stats, const uint8_t* __restrict__ pool,
+    const int64_t* __restrict__ rec_off, const uint32_t* __restrict__ blk_off, int32_t nblk,
+    int64_t tail, const uint16_t* __restrict__ lut_g, uint8_t* __restrict__ cache,
+    int64_t slot_bytes) {
+  __shared__ __align__(16) uint8_t lds[kCodecWaves][kCodecLds];
+  __shared__ uint16_t lut[kCodecLutSize];
+  __shared__ int32_t job_e[kMaxTopK], job_s[kMaxTopK], job_n;
+  int32_t slot_r;
+  bool miss_r;
+  route_wave<PER, PERC>(logits, n_experts, top_k, ids, weights, slot_of, slot_expert, stamp, cap,
+                        step_ptr, out_slot, fetch_slot, fetch_expert, nmiss_ptr, stats, job_e,
+                        job_s, nullptr, &job_n, slot_r, miss_r);
+  if (threadIdx.x >= 64)
+    for (int i = threadIdx.x - 64; i < kCodecLutSize; i += 64 * (kCodecWaves - 1))
+      lut[i] = lut_g[i];
+  __syncthreads();
+  const int32_t nm = __builtin_amdgcn_readfirstlane(job_n);
+  coded_fetch_run(JobsInLds{job_e, job_s}, nm, pool, rec_off, blk_off, nblk, tail, lut, cache,
+                  slot_bytes, lds);
 }
 
 // ---------------------------------------------------------------- host
@@ -453,4 +521,61 @@ extern "C" int moe_fetch_coded(const void* pool, const int64_t* rec_offset,
                      fetch_expert, fetch_slot, nmiss, max_jobs, static_cast<uint8_t*>(cache),
                      slot_bytes);
   return check_launch("moe_fetch_coded");
+}
+
+extern "C" int moe_route_fetch_coded(
+    const void* x, const void* w, const float* bias, int32_t logit_dtype, int32_t hidden,
+    int32_t n_experts, int32_t top_k, float* logits, int32_t* ids, float* weights,
+    int32_t* slot_of, int32_t* slot_expert, int64_t* slot_stamp, int32_t cap, int64_t* step,
+    int32_t* out_slot, int32_t* fetch_slot, int32_t* fetch_expert, int32_t* nmiss,
+    int64_t* stats, const void* pool, const int64_t* rec_offset, const uint32_t* blk_offset,
+    int64_t record_bytes, int64_t fp8_bytes, const uint16_t* lut, void* cache,
+    int64_t slot_bytes, int32_t workgroups, void* stream) {
+  MOE_REQUIRE(x && w && logits && ids && weights && slot_of && slot_expert && slot_stamp && step &&
+                  out_slot && fetch_slot && fetch_expert && nmiss && pool && rec_offset &&
+                  blk_offset && lut && cache,
+              "moe_route_fetch_coded: NULL pointer");
+  MOE_REQUIRE(logit_dtype == MOE_F32 || logit_dtype == MOE_BF16,
+              "moe_route_fetch_coded: logit_dtype must be MOE_F32 or MOE_BF16");
+  MOE_REQUIRE(hidden > 0 && hidden % 8 == 0, "moe_route_fetch_coded: hidden %% 8 != 0 (%d)",
+              hidden);
+  MOE_REQUIRE(top_k >= 1 && top_k <= kMaxTopK && top_k <= n_experts && n_experts <= 1024,
+              "moe_route_fetch_coded: need 1 <= top_k <= min(32, n_experts), n_experts <= 1024");
+  MOE_REQUIRE(cap >= 1 && cap <= 1024, "moe_route_fetch_coded: need 1 <= cap <= 1024");
+  MOE_REQUIRE(top_k <= cap, "moe_route_fetch_coded: top_k (%d) exceeds the cache capacity (%d)",
+              top_k, cap);
+  MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0,
+              "moe_route_fetch_coded: x and w must be 16-byte aligned");
+  MOE_REQUIRE(fp8_bytes > 0 && fp8_bytes % kCodecBlock == 0 && record_bytes >= fp8_bytes &&
+                  (record_bytes - fp8_bytes) % 16 == 0,
+              "moe_route_fetch_coded: fp8 bytes must be a positive multiple of %d and the tail "
+              "of 16", kCodecBlock);
+  MOE_REQUIRE(slot_bytes >= record_bytes && slot_bytes % 16 == 0,
+              "moe_route_fetch_coded: slots of at least one record, 16-byte multiples");
+  MOE_REQUIRE(reinterpret_cast<uintptr_t>(pool) % 256 == 0 &&
+                  reinterpret_cast<uintptr_t>(cache) % 16 == 0,
+              "moe_route_fetch_coded: pool 256-byte and cache 16-byte aligned");
+  MOE_REQUIRE(workgroups >= 1 && workgroups <= 65535,
+              "moe_route_fetch_coded: need 1 <= workgroups <= 65535");
+  hipStream_t s = as_stream(stream);
+  const int rc = launch_decode_logits(x, w, bias, hidden, n_experts,
+                                      logit_dtype == MOE_BF16 ? 1 : 0, logits, step, s);
+  if (rc) return rc;
+  const auto* pl = static_cast<const uint8_t*>(pool);
+  auto* ca = static_cast<uint8_t*>(cache);
+  const int32_t nblk = static_cast<int32_t>(fp8_bytes / kCodecBlock);
+  const int64_t tail = record_bytes - fp8_bytes;
+#define MOE_RFC(PE, PC)                                                                         \
+  hipLaunchKernelGGL((route_fetch_coded_kernel<PE, PC>), dim3(workgroups),                      \
+                     dim3(64 * kCodecWaves), 0, s, logits, n_experts, top_k, ids, weights,      \
+                     slot_of, slot_expert, slot_stamp, cap, step, out_slot, fetch_slot,         \
+                     fetch_expert, nmiss, stats, pl, rec_offset, blk_offset, nblk, tail, lut,   \
+                     ca, slot_bytes)
+  if (n_experts <= 256) {
+    if (cap <= 256) MOE_RFC(4, 4); else MOE_RFC(4, 16);
+  } else {
+    if (cap <= 256) MOE_RFC(16, 4); else MOE_RFC(16, 16);
+  }
+#undef MOE_RFC
+  return check_launch("moe_route_fetch_coded(route+fetch)");
 }

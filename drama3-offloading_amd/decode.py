@@ -16,8 +16,9 @@ half of the FFN, every workgroup resolving the call itself from a
 double-buffered slot table, the workgroups that fetch a miss's rows running
 its gate/up MFMAs on them as they arrive; the down half).  With
 fused_ffn=False the FFN is its own two launches after moe_route_fetch's two;
-with fused_fetch=False (and always with coded pools) the route is
-moe_route_resolve and the fetch a launch of its own.
+with fused_fetch=False the route is moe_route_resolve and the fetch a launch
+of its own.  With coded pools the route and the decode of the misses share
+a launch (moe_route_fetch_coded) and the FFN is its own two.
 
 With `shared_expert`, the step is the full MoE block, one call after the
 fetch: the gated bf16 shared expert rides in the two routed GEMV launches
@@ -193,11 +194,12 @@ class DecodeHarness:
             if len(coded) != L:
                 raise ValueError(f"{len(coded)} coded pools for {L} layers")
             self.coded = coded
-        # the step takes moe_route_fetch (router + resolve + fetch), decided once
-        self.fused = cfg.mode == "cached" and cfg.fused_fetch and self.coded is None
-        # ... and the FFN with it (packed tile-ordered records, routed experts only)
-        self.fused_ffn = (self.fused and cfg.fused_ffn and self.layout.tiled and
-                          cfg.hidden % 512 == 0 and cfg.top_k <= 16)
+        # the step takes moe_route_fetch (router + resolve + fetch; for coded
+        # pools moe_route_fetch_coded), decided once
+        self.fused = cfg.mode == "cached" and cfg.fused_fetch
+        # ... and the FFN with it (raw packed tile-ordered records)
+        self.fused_ffn = (self.fused and self.coded is None and cfg.fused_ffn and
+                          self.layout.tiled and cfg.hidden % 512 == 0 and cfg.top_k <= 16)
         if cfg.shared_expert:
             # seeded bf16 shared experts, resident (6 MiB per layer at 2048 x 512)
             g2 = torch.Generator(device=dev).manual_seed(cfg.seed + 3)
@@ -274,7 +276,18 @@ class DecodeHarness:
                                 logit_dtype=cfg.router_logits,
                                 shared=self.shared(l) if cfg.shared_expert else None)
             return
-        if self.fused:
+        if self.fused and self.coded is not None:
+            # router, then resolve + decode of the misses' coded records
+            c = self.coded[l]
+            lib.route_fetch_coded(self.h, self.gate[l], self.bias_live[l], cfg.top_k,
+                                  self.logits[l], self.ids[l], self.wts[l], self.tab_slot_of[l],
+                                  self.tab_slot_expert[l], self.tab_stamp[l], self.step[l],
+                                  self.out_slot[l], self.fslot[l], self.fexp[l], self.nmiss[l],
+                                  c.dev_ptr, c.rec_off, c.blk_off, c.record_bytes, c.fp8_bytes,
+                                  c.lut, self.cache[l], workgroups=cfg.coded_workgroups,
+                                  stats=self.stats[l], logit_dtype=cfg.router_logits)
+            slots = self.out_slot[l]
+        elif self.fused:
             # router, then resolve + miss fetch in one launch (double-buffered table)
             lib.route_fetch(self.h, self.gate[l], self.bias_live[l], cfg.top_k, self.logits[l],
                             self.ids[l], self.wts[l], self.tab_slot_of[l],

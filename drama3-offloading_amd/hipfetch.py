@@ -143,6 +143,9 @@ SIGNATURES = {
     "moe_codec_table": (C.c_int, [_vp, _vp]),
     "moe_fetch_coded": (C.c_int, [_vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _vp, _i64,
                                   _i32, _vp]),
+    "moe_route_fetch_coded": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp,
+                                        _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                        _vp, _vp, _i64, _i64, _vp, _vp, _i64, _i32, _vp]),
     "moe_fp8_moe_block_workspace": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "moe_fp8_moe_block_forward": (C.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp,
                                             _vp, _i32, _i32, _i32, C.POINTER(ExpertStrides),
@@ -837,6 +840,53 @@ class Native:
             lut.data_ptr(), fetch_expert.data_ptr(), fetch_slot.data_ptr(), nmiss.data_ptr(),
             max_jobs, cache.data_ptr(), cache.stride(0) * cache.element_size(), workgroups,
             self.stream()), "moe_fetch_coded")
+
+    def route_fetch_coded(self, x, w, bias, top_k: int, logits, ids, weights, slot_of,
+                          slot_expert, stamp, step, out_slot, fetch_slot, fetch_expert, nmiss,
+                          pool_dev_ptr: int, rec_off, blk_off, record_bytes: int, fp8_bytes: int,
+                          lut, cache, workgroups: int = 32, stats=None,
+                          logit_dtype: str = "bf16") -> None:
+        """route_fetch for a coded pool (moe_route_fetch_coded): the router,
+        the slot resolve on the double-buffered table and the decode of the
+        misses' coded records into cache (uint8 [cap, >= record_bytes]), in
+        two launches; the outputs those of route_resolve + fetch_coded."""
+        import torch
+        what = "moe_route_fetch_coded"
+        if x.shape[0] != 1:
+            raise ValueError("route_fetch_coded takes exactly one token")
+        if slot_of.dim() != 2 or slot_of.shape[0] != 2 or slot_expert.dim() != 2 \
+                or slot_expert.shape[0] != 2 or tuple(stamp.shape) != tuple(slot_expert.shape):
+            raise ValueError("route_fetch_coded takes double-buffered tables: slot_of [2, E], "
+                             "slot_expert and stamp [2, C]")
+        self._on_gpu(what, x, w, bias, logits, ids, weights, slot_of, slot_expert, stamp, step,
+                     out_slot, fetch_slot, fetch_expert, nmiss, stats, rec_off, blk_off, lut,
+                     cache)
+        H, E = self._router_bufs(what, x, w, bias, logits, 1, top_k)
+        if slot_of.shape[1] != E:
+            raise ValueError(f"slot_of [2, {slot_of.shape[1]}] does not match {E} experts")
+        self._buf(what, "ids", ids, top_k, torch.int32)
+        self._buf(what, "weights", weights, top_k, torch.float32)
+        self._slot_bufs(what, slot_of, 2 * E, slot_expert, stamp, step, out_slot, top_k,
+                        fetch_slot, fetch_expert, nmiss, stats)
+        self._buf(what, "lut", lut, 4096, torch.uint16, torch.int16)
+        self._buf(what, "rec_off", rec_off, E + 1, torch.int64)
+        nblk = fp8_bytes // 8192
+        self._buf(what, "blk_off", blk_off, E * (nblk + 1), torch.uint32, torch.int32)
+        if cache.dim() != 2 or cache.stride(1) != 1 or \
+                cache.shape[1] * cache.element_size() < record_bytes:
+            raise ValueError(f"{what}: cache must be [slots, >= record_bytes] with contiguous "
+                             "rows")
+        if cache.shape[0] < slot_expert.shape[1]:
+            raise ValueError(f"{what}: cache has {cache.shape[0]} slots, the table "
+                             f"{slot_expert.shape[1]}")
+        self._check(self.cdll.moe_route_fetch_coded(
+            x.data_ptr(), w.data_ptr(), self._ptr(bias), self._logit_code(logit_dtype), H, E,
+            top_k, logits.data_ptr(), ids.data_ptr(), weights.data_ptr(), slot_of.data_ptr(),
+            slot_expert.data_ptr(), stamp.data_ptr(), slot_expert.shape[1], step.data_ptr(),
+            out_slot.data_ptr(), fetch_slot.data_ptr(), fetch_expert.data_ptr(),
+            nmiss.data_ptr(), self._ptr(stats), pool_dev_ptr, rec_off.data_ptr(),
+            blk_off.data_ptr(), record_bytes, fp8_bytes, lut.data_ptr(), cache.data_ptr(),
+            cache.stride(0) * cache.element_size(), workgroups, self.stream()), what)
 
     def unpermute(self, y, pair_pos, weights, out) -> None:
         import torch

@@ -586,6 +586,30 @@ int moe_fetch_coded(const void* pool, const int64_t* rec_offset,
                     const int32_t* nmiss, int32_t max_jobs, void* cache,
                     int64_t slot_bytes, int32_t workgroups, void* stream);
 
+/* moe_route_fetch for a coded pool: the router's logits (which count the
+ * step), then one launch whose every workgroup makes the route (top-k and
+ * slot resolve on the double-buffered table, workgroup 0 writing ids,
+ * weights, out_slot, the fetch lists, nmiss, stats and the next buffer) and
+ * decodes its share of the misses' coded records into their slots.
+ * Outputs and cache contents are those of moe_route_resolve on the same
+ * table followed by moe_fetch_coded(..., fetch_expert, fetch_slot, nmiss,
+ * top_k, ...).  The table and the step as for moe_route_fetch; the pool,
+ * offsets, table and grid as for moe_fetch_coded.
+ * No counterpart in the reference: it fuses the router (moe.py:217-220),
+ * _resolve_slots (bin/devcache.py:45-98) and the fetch of the misses
+ * (csrc/fetch_experts.cu:49-94) for the coded pool format.  Constraints:
+ * those of moe_route_fetch and moe_fetch_coded. */
+int moe_route_fetch_coded(const void* x, const void* w, const float* bias,
+                          int32_t logit_dtype, int32_t hidden, int32_t n_experts,
+                          int32_t top_k, float* logits, int32_t* ids, float* weights,
+                          int32_t* slot_of, int32_t* slot_expert, int64_t* slot_stamp,
+                          int32_t cap, int64_t* step, int32_t* out_slot,
+                          int32_t* fetch_slot, int32_t* fetch_expert, int32_t* nmiss,
+                          int64_t* stats, const void* pool, const int64_t* rec_offset,
+                          const uint32_t* blk_offset, int64_t record_bytes,
+                          int64_t fp8_bytes, const uint16_t* lut, void* cache,
+                          int64_t slot_bytes, int32_t workgroups, void* stream);
+
 /* The MoE block's shared expert as one argument: bf16 weights w_gate and
  * w_up [inter, hidden], w_down [hidden, inter], w_sgate [hidden], all
  * 16-byte aligned. */

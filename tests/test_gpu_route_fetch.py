@@ -1,7 +1,8 @@
 """moe_route_fetch, the decode step's router + resolve + fetch in two
 launches, against moe_route_resolve followed by moe_fetch (three launches),
-and moe_route_fetch_ffn (the same with the expert FFN, three launches)
-against those and the FFN's own two,
+moe_route_fetch_ffn (the same with the expert FFN, three launches)
+against those and the FFN's own two, and moe_route_fetch_coded (the route
+in the coded fetch's launch) against moe_route_resolve + moe_fetch_coded,
 at Drama-3 shape (256 experts, top-8, H 2048, I 512) and two others (320
 experts, top-12, 272 slots; 64 experts, top-4, 5 slots) over 3 layers and
 popularity drifts: two harnesses on the same pools, one per path, step for
@@ -149,6 +150,45 @@ def test_route_fetch_ffn_block_equals_separate_launches(lib, dev, shape):
         say(f"route_fetch_ffn block: replay {s}")
         _same(fused, plain, f"replay {s}")
     plain.pools = []                     # owned by the fused harness
+    fused.close()
+
+
+@pytest.mark.parametrize("shape", [
+    dict(capacity=20),
+    # E, cap > 256 (16-per-lane registers), 12 jobs over 5 workgroups' 20 waves
+    dict(n_experts=320, top_k=12, hidden=512, inter=256, capacity=272, coded_workgroups=5),
+    # evictions on almost every step; one workgroup decodes every block
+    dict(n_experts=64, top_k=4, hidden=256, inter=128, capacity=5, coded_workgroups=1),
+], ids=["drama3", "wide", "tight"])
+def test_route_fetch_coded_equals_route_resolve_then_fetch_coded(lib, dev, shape):
+    """moe_route_fetch_coded (the route in every workgroup of the coded
+    fetch's launch) against moe_route_resolve + moe_fetch_coded on the same
+    coded pools: outputs, tables and decoded cache bytes equal step for
+    step, eager and replayed."""
+    import decode
+    base = dict(layers=3, drift_every=3, schedule_steps=12, coded_pool=True, **shape)
+    fused = decode.DecodeHarness(decode.DecodeConfig(**base), dev)
+    plain = decode.DecodeHarness(decode.DecodeConfig(**base, fused_fetch=False), dev,
+                                 pools=fused.pools, coded=fused.coded)
+    assert fused.fused and not fused.fused_ffn and not plain.fused
+    for s in range(7):
+        for h in (fused, plain):
+            h.stage(s)
+            h.step_eager()
+        torch.cuda.synchronize(dev)
+        say(f"route_fetch_coded {shape}: eager step {s}")
+        _same(fused, plain, f"eager {s}")
+    hits, misses = fused.hit_rate()
+    assert hits > 0 and misses > 0
+    for h in (fused, plain):
+        h.capture()
+    for s in range(9):
+        for h in (fused, plain):
+            h.replay(1)
+        torch.cuda.synchronize(dev)
+        say(f"route_fetch_coded: replay {s}")
+        _same(fused, plain, f"replay {s}")
+    plain.pools, plain.coded = [], None  # owned by the fused harness
     fused.close()
 
 

@@ -68,6 +68,23 @@ def test_preconditions_are_rejected_without_launching(lib):
                     (dict(wbytes=8 * 512 * 4 - 4), b"workspace")):
         assert rff(**kw) == -1, msg
         assert msg in c.moe_last_error(), (msg, c.moe_last_error())
+    # the coded route + fetch: the route's limits and the coded fetch's record shape
+    def rfc(top_k=8, cap=50, n_experts=256, record_bytes=3146496, fp8_bytes=3145728, pool=256,
+            slot_bytes=3146496, workgroups=32):
+        return c.moe_route_fetch_coded(16, 16, None, bf16, 2048, n_experts, top_k, 1, 1, 1, 1,
+                                       1, 1, cap, 1, 1, 1, 1, 1, None, pool, 1, 1, record_bytes,
+                                       fp8_bytes, 1, 256, slot_bytes, workgroups, None)
+    for kw, msg in ((dict(top_k=33, cap=64), b"top_k"),
+                    (dict(n_experts=1025), b"n_experts <= 1024"),
+                    (dict(cap=1025), b"cap <= 1024"),
+                    (dict(top_k=9, cap=8), b"exceeds the cache capacity"),
+                    (dict(fp8_bytes=3145728 - 16), b"multiple of 8192"),
+                    (dict(record_bytes=3145728 + 8), b"multiple of 8192"),
+                    (dict(slot_bytes=3146496 - 16), b"at least one record"),
+                    (dict(pool=272), b"256-byte"),
+                    (dict(workgroups=0), b"workgroups")):
+        assert rfc(**kw) == -1, msg
+        assert msg in c.moe_last_error(), (msg, c.moe_last_error())
     # tile-order pairs: K a multiple of 128, whole 16-row groups, 16-byte aligned
     FetchPair = __import__("hipfetch").FetchPair
     for src, dst, nbytes, tile_k, msg in ((0x1000, 0x2000, 16 * 256, 192, b"multiple of 128"),
@@ -385,6 +402,29 @@ def test_wrappers_check_buffer_sizes_and_dtypes(lib, monkeypatch):
                       (dict(stats=i32(2)), "stats must be int64")):
         with pytest.raises(ValueError, match=msg):
             route_fetch(**over)
+
+    def route_fetch_coded(**over):
+        a = dict(x=x, w=w, bias=None, top_k=K, logits=torch.zeros(E), ids=i32(K),
+                 weights=torch.zeros(K), slot_of=i32(2, E), slot_expert=i32(2, C),
+                 stamp=i64(2, C), step=i64(1), out_slot=i32(K), fetch_slot=i32(K),
+                 fetch_expert=i32(K), nmiss=i32(1), pool_dev_ptr=256, rec_off=i64(E + 1),
+                 blk_off=torch.zeros(E * 385, dtype=torch.uint32), record_bytes=3146496,
+                 fp8_bytes=3145728, lut=torch.zeros(4096, dtype=torch.int16),
+                 cache=torch.zeros((C, 3146496), dtype=torch.uint8, device="meta"))
+        a.update(over)
+        lib.route_fetch_coded(**a)
+    with pytest.raises(AssertionError, match="moe_route_fetch_coded reached"):
+        route_fetch_coded()
+    for over, msg in ((dict(rec_off=i64(E)), "rec_off holds 256 elements, needs 257"),
+                      (dict(blk_off=i32(E * 385 - 1)), "blk_off holds"),
+                      (dict(lut=i32(4096)), "lut must be"),
+                      (dict(slot_of=i32(2, E + 1)), "does not match"),
+                      (dict(cache=torch.zeros((C - 1, 3146496), dtype=torch.uint8,
+                                              device="meta")), "cache has 63 slots"),
+                      (dict(cache=torch.zeros((C, 3146480), dtype=torch.uint8, device="meta")),
+                       "record_bytes")):
+        with pytest.raises(ValueError, match=msg):
+            route_fetch_coded(**over)
 
     with pytest.raises(ValueError, match="offsets holds 256 elements, needs 257"):
         lib.permute(i32(4, K), E, i32(E), i32(E), i32(4 * K), i32(4 * K))
