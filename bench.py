@@ -589,10 +589,12 @@ def dropin_bench(lib, hc, steps: int, start: int, split: int, x_headline) -> dic
     calling experts(h, ids, w), i.e. dev_cached_forward: moe_resolve_slots,
     one moe_fetch of the four buffers (w13/w2 written in tile order), the
     expert FFN on the cache.  Router, stub and routing schedule are the
-    headline's; the residual add is a separate torch add, as in a model
-    that calls the experts module.  The same replays, window and split as
-    the headline: the decisions are the same, so the hit/miss counts must
-    match the headline's and the step output must equal it bit for bit."""
+    headline's.  The model code around the hook adds the residual: folded
+    into the next layer's stub loads (moe_linear_bf16 with x_add; the last
+    layer's add a torch add), and, as a second graph, a separate torch add
+    per layer.  The same replays, window and split as the headline: the
+    decisions are the same, so the hit/miss counts must match the
+    headline's and the step output must equal it bit for bit."""
     import types
     import torch
     import decode
@@ -620,15 +622,30 @@ def dropin_bench(lib, hc, steps: int, start: int, split: int, x_headline) -> dic
         logits = torch.zeros((L, 1, E), dtype=torch.float32, device=dev)
         x = hc.x0.clone()
         h = torch.empty_like(x)
+        hh = (torch.empty_like(x), torch.empty_like(x))     # the folded form's stub outputs
 
-        def step():
+        def step(fold: bool = True):
             x.copy_(hc.x0)
+            if not fold:
+                for l in range(L):
+                    decode.stub_linear(x, hc.w_stub[l], h)
+                    lib.router_topk(h, hc.gate[l], hc.bias_live[l], K, logits[l], ids[l], wts[l],
+                                    logit_dtype=cfg.router_logits)
+                    y = mods[l](h, ids[l], wts[l])
+                    torch.add(h, y, out=x)
+                return
+            # x = h + y folded into the next stub: h' = bf16(h + y) W^T
+            y = None
             for l in range(L):
-                decode.stub_linear(x, hc.w_stub[l], h)
-                lib.router_topk(h, hc.gate[l], hc.bias_live[l], K, logits[l], ids[l], wts[l],
+                hp, hn = hh[(l + 1) % 2], hh[l % 2]
+                if l == 0:
+                    decode.stub_linear(x, hc.w_stub[l], hn)
+                else:
+                    decode.stub_linear(hp, hc.w_stub[l], hn, x_add=y)
+                lib.router_topk(hn, hc.gate[l], hc.bias_live[l], K, logits[l], ids[l], wts[l],
                                 logit_dtype=cfg.router_logits)
-                y = mods[l](h, ids[l], wts[l])
-                torch.add(h, y, out=x)
+                y = mods[l](hn, ids[l], wts[l])
+            torch.add(hh[(L - 1) % 2], y, out=x)
 
         # the window run eagerly first (no graph: one launch at a time)
         for c in range(start):
@@ -682,6 +699,29 @@ def dropin_bench(lib, hc, steps: int, start: int, split: int, x_headline) -> dic
         dt = ev[0].elapsed_time(ev[2]) / 1000.0
         hits, misses = (s2_ - s0).tolist()
         x_step = x.clone()
+        del g
+
+        # the same window with the residual add as a torch add per layer
+        for m in mods:
+            devcache.reset_dev_cache(m)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step(fold=False)
+        for m in mods:
+            devcache.reset_dev_cache(m)
+        replay(0, start)
+        torch.cuda.synchronize(dev)
+        ta, tb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ta.record()
+        replay(start, steps)
+        tb.record()
+        torch.cuda.synchronize(dev)
+        t_dt = ta.elapsed_time(tb) / 1000.0
+        torch_add = {"what": "the same graph with the residual add as a torch add after each "
+                             "layer's hook call",
+                     "tokens_per_s": round(steps / t_dt, 3),
+                     "ms_per_step": round(1e3 * t_dt / steps, 4),
+                     "x_equal_headline_step": bool(torch.equal(x, x_headline))}
         del g
 
         # prefill through the same hooks: a call of 512 rows goes to
@@ -755,8 +795,10 @@ def dropin_bench(lib, hc, steps: int, start: int, split: int, x_headline) -> dic
         return {
             "workload": "the headline step through the reference's hooks: MoEExperts modules "
                         "with the four page-locked host buffers, devcache.install_dev_cache, "
-                        "experts(h, ids, w) per layer (resolve, one four-buffer fetch writing "
-                        "w13/w2 in tile order, expert FFN), residual add in torch; one hipGraph",
+                        "experts(h, ids, w) per layer (the resolve, the fetch of the misses' "
+                        "four buffers with their gate/up and the hits' in one launch, then the "
+                        "down launch), the residual add folded into the next layer's stub; "
+                        "one hipGraph",
             "layers_hooked": n, "pinned_GiB": round(gib, 2), "pin_experts_s": round(pin_s, 2),
             "build_s": round(build_s, 1),
             "tokens_per_s": round(steps / dt, 3), "ms_per_step": round(1e3 * dt / steps, 4),
@@ -766,6 +808,7 @@ def dropin_bench(lib, hc, steps: int, start: int, split: int, x_headline) -> dic
             "hits_misses": [int(hits), int(misses)],
             "x_equal_headline_step": bool(torch.equal(x_step, x_headline)),
             "eager": eager,
+            "residual_torch_add": torch_add,
             "prefill": prefill_hooks,
             "host_lru": host_lru,
         }, xp.clone()

@@ -13,9 +13,32 @@
 // before any is used, so every wave issues its whole share of the matrix
 // at once: x first (every wave reads it, from L2), then the weights with
 // nontemporal loads (read once).
+//
+// With an addend r (moe_linear_bf16's x_add), the product is of bf16(x + r),
+// each element's float sum rounded once to bf16 (a torch add of two bf16
+// tensors): a decode step whose residual add sits between two layers'
+// products folds it into the second one's loads.  r is loaded beside x and
+// the sums are formed after the weight loads are issued; forming them
+// before (x's round trip ahead of the weights') cost the saved launch back.
 #include "shared.hpp"
 
 namespace moe {
+
+// bf16(a + b) of the 8 bf16 pairs of two 16-byte slices, each sum in float
+// rounded once to nearest even.
+__device__ __forceinline__ u32x4 add8_bf16(u32x4 a, u32x4 b) {
+  const uint32_t av[4] = {a.x, a.y, a.z, a.w};
+  const uint32_t bv[4] = {b.x, b.y, b.z, b.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t lo = f32_to_bf16(__uint_as_float(av[i] << 16) + __uint_as_float(bv[i] << 16));
+    const uint32_t hi = f32_to_bf16(__uint_as_float(av[i] & 0xffff0000u) +
+                                    __uint_as_float(bv[i] & 0xffff0000u));
+    o[i] = lo | (hi << 16);
+  }
+  return u32x4{o[0], o[1], o[2], o[3]};
+}
 
 // One wave per workgroup, one row per wave by default: a graph of
 // 1-token calls over 40 layers' [2048, 2048] matrices (MI355X) took 3.55 us
@@ -26,10 +49,11 @@ namespace moe {
 constexpr int kLinearWaves = 1;      // waves per workgroup
 constexpr int kLinearMaxTokens = 4;
 
-template <int NR, int TB>
+template <int NR, int TB, bool ADD>
 __global__ __launch_bounds__(64 * kLinearWaves) void linear_bf16_kernel(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int32_t tokens, int32_t in,
-    int32_t out, uint16_t* __restrict__ y) {
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ xa,
+    const uint16_t* __restrict__ w, int32_t tokens, int32_t in, int32_t out,
+    uint16_t* __restrict__ y) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int r0 = (static_cast<int>(blockIdx.x) * kLinearWaves + wave) * NR;
   if (r0 >= out) return;                       // the whole wave; no barrier below
@@ -44,13 +68,15 @@ __global__ __launch_bounds__(64 * kLinearWaves) void linear_bf16_kernel(
 #pragma unroll
     for (int t = 0; t < TB; ++t) acc[i][t] = 0.0f;
   for (int c0 = 0; c0 < n16; c0 += 64 * U) {
-    u32x4 xv[TB][U], wv[U][NR];
+    u32x4 xv[TB][U], av[ADD ? TB : 1][U], wv[U][NR];
 #pragma unroll
     for (int t = 0; t < TB; ++t)
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int c = min(c0 + u * 64 + lane, n16 - 1);
-        xv[t][u] = load16(x + static_cast<int64_t>(min(t, tokens - 1)) * in + c * 8);
+        const int64_t o = static_cast<int64_t>(min(t, tokens - 1)) * in + c * 8;
+        xv[t][u] = load16(x + o);
+        if constexpr (ADD) av[t][u] = load16(xa + o);
       }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -58,6 +84,12 @@ __global__ __launch_bounds__(64 * kLinearWaves) void linear_bf16_kernel(
 #pragma unroll
       for (int i = 0; i < NR; ++i)
         wv[u][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rows[i] + c * 8));
+    }
+    if constexpr (ADD) {                         // after every load is issued
+#pragma unroll
+      for (int t = 0; t < TB; ++t)
+#pragma unroll
+        for (int u = 0; u < U; ++u) xv[t][u] = add8_bf16(xv[t][u], av[t][u]);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -82,42 +114,53 @@ __global__ __launch_bounds__(64 * kLinearWaves) void linear_bf16_kernel(
   }
 }
 
-template <int NR>
-static void launch_linear(const uint16_t* x, const uint16_t* w, int32_t tokens, int32_t in,
-                          int32_t out, uint16_t* y, hipStream_t s) {
+template <int NR, bool ADD>
+static void launch_linear(const uint16_t* x, const uint16_t* xa, const uint16_t* w,
+                          int32_t tokens, int32_t in, int32_t out, uint16_t* y, hipStream_t s) {
   const unsigned grid = static_cast<unsigned>((out + kLinearWaves * NR - 1) / (kLinearWaves * NR));
   if (tokens == 1)
-    hipLaunchKernelGGL((linear_bf16_kernel<NR, 1>), dim3(grid), dim3(64 * kLinearWaves), 0, s, x,
-                       w, tokens, in, out, y);
+    hipLaunchKernelGGL((linear_bf16_kernel<NR, 1, ADD>), dim3(grid), dim3(64 * kLinearWaves), 0,
+                       s, x, xa, w, tokens, in, out, y);
   else
-    hipLaunchKernelGGL((linear_bf16_kernel<NR, kLinearMaxTokens>), dim3(grid),
-                       dim3(64 * kLinearWaves), 0, s, x, w, tokens, in, out, y);
+    hipLaunchKernelGGL((linear_bf16_kernel<NR, kLinearMaxTokens, ADD>), dim3(grid),
+                       dim3(64 * kLinearWaves), 0, s, x, xa, w, tokens, in, out, y);
+}
+
+template <int NR>
+static void launch_linear(const uint16_t* x, const uint16_t* xa, const uint16_t* w,
+                          int32_t tokens, int32_t in, int32_t out, uint16_t* y, hipStream_t s) {
+  if (xa)
+    launch_linear<NR, true>(x, xa, w, tokens, in, out, y, s);
+  else
+    launch_linear<NR, false>(x, xa, w, tokens, in, out, y, s);
 }
 
 }  // namespace moe
 
 using namespace moe;
 
-extern "C" int moe_linear_bf16(const void* x, const void* w, int32_t tokens, int32_t in_features,
-                               int32_t out_features, void* y, int32_t rows_per_wave,
-                               void* stream) {
+extern "C" int moe_linear_bf16(const void* x, const void* x_add, const void* w, int32_t tokens,
+                               int32_t in_features, int32_t out_features, void* y,
+                               int32_t rows_per_wave, void* stream) {
   MOE_REQUIRE(x && w && y, "moe_linear_bf16: NULL pointer");
   MOE_REQUIRE(tokens >= 1 && tokens <= kLinearMaxTokens, "moe_linear_bf16: need 1 <= tokens <= %d",
               kLinearMaxTokens);
   MOE_REQUIRE(in_features >= 8 && in_features % 8 == 0 && out_features >= 1,
               "moe_linear_bf16: in_features must be a positive multiple of 8, out_features >= 1");
-  MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0,
-              "moe_linear_bf16: x and w must be 16-byte aligned");
+  MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(x_add) % 16 == 0,
+              "moe_linear_bf16: x, x_add and w must be 16-byte aligned");
   MOE_REQUIRE(rows_per_wave == 0 || rows_per_wave == 1 || rows_per_wave == 2 || rows_per_wave == 4,
               "moe_linear_bf16: rows_per_wave must be 0 (default), 1, 2 or 4");
   hipStream_t s = as_stream(stream);
   const auto* xb = static_cast<const uint16_t*>(x);
+  const auto* ab = static_cast<const uint16_t*>(x_add);
   const auto* wb = static_cast<const uint16_t*>(w);
   auto* yb = static_cast<uint16_t*>(y);
   switch (rows_per_wave) {
-    case 2: launch_linear<2>(xb, wb, tokens, in_features, out_features, yb, s); break;
-    case 4: launch_linear<4>(xb, wb, tokens, in_features, out_features, yb, s); break;
-    default: launch_linear<1>(xb, wb, tokens, in_features, out_features, yb, s); break;
+    case 2: launch_linear<2>(xb, ab, wb, tokens, in_features, out_features, yb, s); break;
+    case 4: launch_linear<4>(xb, ab, wb, tokens, in_features, out_features, yb, s); break;
+    default: launch_linear<1>(xb, ab, wb, tokens, in_features, out_features, yb, s); break;
   }
   return check_launch("moe_linear_bf16");
 }

@@ -132,7 +132,7 @@ SIGNATURES = {
     "moe_silu_check": (C.c_int, [_vp, _vp, _vp, C.c_uint32, _vp]),
     "moe_stream_read": (C.c_int, [_vp, _i64, _i32, _vp, _vp]),
     "moe_time_fused_launch": (C.c_int, [_vp, _vp]),
-    "moe_linear_bf16": (C.c_int, [_vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp]),
+    "moe_linear_bf16": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp]),
     "moe_resolve_fetch_ffn": (C.c_int, [_vp, _i32, _i32, C.POINTER(SlotTable), _vp, _vp, _vp, _vp,
                                         _vp, C.POINTER(FetchPair), _i32, _i32, _vp, _vp, _i32, _vp,
                                         _vp, _vp, _vp, _i32, _i32, C.POINTER(ExpertStrides), _vp,
@@ -753,21 +753,24 @@ class Native:
                                                sink.data_ptr(), self.stream()),
                     "moe_stream_read")
 
-    def linear_bf16(self, x, w, out, rows_per_wave: int = 0) -> None:
+    def linear_bf16(self, x, w, out, rows_per_wave: int = 0, x_add=None) -> None:
         """out [T, N] = x [T, K] w^T, w [N, K] bf16 (nn.Linear layout), 1 <= T <= 4
-        (moe_linear_bf16)."""
+        (moe_linear_bf16); with x_add [T, K] bf16 the product is of x + x_add
+        (a bf16 add)."""
         import torch
         what = "moe_linear_bf16"
-        self._on_gpu(what, x, w, out)
+        self._on_gpu(what, x, w, out, x_add)
         if x.dim() != 2 or w.dim() != 2 or x.shape[1] != w.shape[1]:
             raise ValueError(f"{what}: x [T, K] and w [N, K] must agree on K")
         T, K = x.shape
         N = w.shape[0]
         self._buf(what, "x", x, T * K, torch.bfloat16)
+        self._buf(what, "x_add", x_add, T * K, torch.bfloat16)
         self._buf(what, "w", w, N * K, torch.bfloat16)
         self._buf(what, "out", out, T * N, torch.bfloat16)
-        self._check(self.cdll.moe_linear_bf16(x.data_ptr(), w.data_ptr(), T, K, N, out.data_ptr(),
-                                              rows_per_wave, self.stream()), what)
+        self._check(self.cdll.moe_linear_bf16(x.data_ptr(), self._ptr(x_add), w.data_ptr(), T, K,
+                                              N, out.data_ptr(), rows_per_wave, self.stream()),
+                    what)
 
     def time_fused_launch(self, start, stop) -> None:
         """Arm torch.cuda.Event start/stop (enable_timing=True) around this

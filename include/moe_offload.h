@@ -81,12 +81,16 @@ int moe_stream_read(const void* src, int64_t bytes, int32_t workgroups, uint32_t
  * bf16 (nn.Linear layout, in_features a multiple of 8), x [tokens,
  * in_features], y [tokens, out_features]; each output the f32 sum of its
  * row's products (per lane in slice order, then a fixed lane tree), rounded
- * once to bf16.  rows_per_wave: 1, 2 or 4 rows per wave, 0 for the default
- * (1); the outputs do not depend on it.  x and w 16-byte aligned.  No counterpart in the reference: the
+ * once to bf16.  x_add (nullable, x's shape): the product is of
+ * bf16(x + x_add) instead, each element's float sum rounded once to bf16
+ * (a residual add folded into the loads).  rows_per_wave: 1, 2 or 4 rows
+ * per wave, 0 for the default (1); the outputs do not depend on it.  x,
+ * x_add and w 16-byte aligned.  No counterpart in the reference: the
  * decode benchmark's stand-in for the non-expert compute of a layer (one
  * [2048, 2048] matrix) runs on it, one pass over the weights. */
-int moe_linear_bf16(const void* x, const void* w, int32_t tokens, int32_t in_features,
-                    int32_t out_features, void* y, int32_t rows_per_wave, void* stream);
+int moe_linear_bf16(const void* x, const void* x_add, const void* w, int32_t tokens,
+                    int32_t in_features, int32_t out_features, void* y,
+                    int32_t rows_per_wave, void* stream);
 
 /* Measurement: the calling thread's next moe_route_fetch_ffn or
  * moe_fetch_ffn call records `start` and `stop` (hipEvent_t, created by the

@@ -3,7 +3,8 @@ bf16, 1-4 tokens): against the float64 product of the same bf16 operands
 rounded once to bf16 (the f32 sum may round differently on a value close to
 a bf16 midpoint: at most 1 ulp, on few outputs), identical for 1, 2 and 4
 rows per wave (each row's sum does not depend on the grid), and within 1
-ulp of torch's own bf16 matrix-vector product."""
+ulp of torch's own bf16 matrix-vector product; with an addend, bit-equal to
+a torch bf16 add followed by the product."""
 import numpy as np
 import pytest
 import torch
@@ -52,6 +53,28 @@ def test_linear_bf16_against_float64(lib, dev, T, K, N):
         assert int(_ulps(got[0], ref).max()) <= 1
 
 
+@pytest.mark.parametrize("T,K,N", [(1, 2048, 2048), (4, 264, 1001), (2, 8, 3)])
+def test_linear_bf16_with_addend_equals_torch_add_then_product(lib, dev, T, K, N):
+    """With x_add the kernel multiplies bf16(x + x_add): bit-equal to a
+    torch bf16 add followed by the plain kernel, for every rows_per_wave,
+    and the device's bf16 add itself equal to the CPU's."""
+    g = torch.Generator(device="cpu").manual_seed(7 * K + N + T)
+    x = torch.randn((T, K), generator=g).to(torch.bfloat16)
+    r = (torch.randn((T, K), generator=g) * 3).to(torch.bfloat16)
+    w = (torch.randn((N, K), generator=g) / K ** 0.5).to(torch.bfloat16)
+    xd, rd, wd = x.to(dev), r.to(dev), w.to(dev)
+    s = xd + rd
+    assert torch.equal(s.cpu().view(torch.int16), (x + r).view(torch.int16))
+    plain = torch.empty((T, N), dtype=torch.bfloat16, device=dev)
+    lib.linear_bf16(s, wd, plain)
+    for rpw in (0, 2, 4):
+        y = torch.full((T, N), float("nan"), dtype=torch.bfloat16, device=dev)
+        say(f"linear_bf16 x_add: T={T} K={K} N={N} rows_per_wave={rpw}")
+        lib.linear_bf16(xd, wd, y, rows_per_wave=rpw, x_add=rd)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), plain.view(torch.int16)), rpw
+
+
 def test_linear_bf16_preconditions(lib, dev):
     import hipfetch
     x = torch.zeros((5, 64), dtype=torch.bfloat16, device=dev)
@@ -63,3 +86,7 @@ def test_linear_bf16_preconditions(lib, dev):
         lib.linear_bf16(x[:1], w, y[:1], rows_per_wave=3)
     with pytest.raises(ValueError, match="agree"):
         lib.linear_bf16(x[:1, :32], w, y[:1])
+    with pytest.raises(ValueError, match="x_add must be bfloat16"):
+        lib.linear_bf16(x[:1], w, y[:1], x_add=x[:1].float())
+    with pytest.raises(ValueError, match="x_add holds"):
+        lib.linear_bf16(x[:2], w, y[:2], x_add=x[:1])
