@@ -937,11 +937,11 @@ def prefill_bench(lib, harness, tokens: int = 512, passes: int = 2, coded=None, 
 def resident_bench(lib, harness, batches=(1, 8, 32, 128), steps: int = 20, warmup: int = 3):
     """All 40 x 256 expert records resident in HBM (30 GiB, no offload):
     batched decode at B tokens per step, top-8 of a uniform router, the
-    non-expert stub per layer, the whole step in one hipGraph.  Batch 1 is
-    also timed on the decode step's fused launch (logits, then route +
-    gate/up in one launch: moe_route_fetch_ffn over the resident records
-    with a table that holds every expert, so nothing is ever fetched, then
-    down), which must give the same output."""
+    non-expert stub per layer, the whole step in one hipGraph.  Batch 1 runs
+    the router's top-k inside the gate/up launch (moe_router_fp8_moe_forward:
+    logits, top-k + gate/up, down); it is also timed with the top-k as a
+    launch of its own (moe_router_topk, then moe_fp8_moe_forward), which
+    must give the same output."""
     import numpy as np
     import torch
     import decode
@@ -974,18 +974,13 @@ def resident_bench(lib, harness, batches=(1, 8, 32, 128), steps: int = 20, warmu
                                     layout=harness.layout.code)
 
         if B == 1:
-            tabs = [decode.resident_table(E, dev) for _ in range(L)]
-            i32 = dict(dtype=torch.int32, device=dev)
-            out_slot, fslot, fexp = (torch.empty(K, **i32) for _ in range(3))
-            nmiss = torch.zeros((L, 1), **i32)
-
             def step_fused(_r=0):
                 x.copy_(x0)
                 for l in range(L):
                     decode.stub_linear(x, harness.w_stub[l], h)
-                    lib.route_fetch_ffn(h, gate[l], None, K, logits, ids[l], wts[l], *tabs[l],
-                                        out_slot, fslot, fexp, nmiss[l], recs[l].data_ptr(),
-                                        recs[l], I, 4, x, ws, residual=h)
+                    lib.router_fp8_moe_forward(h, gate[l], None, K, logits[0], ids[l, 0],
+                                               wts[l, 0], *views[l], x, ws, residual=h,
+                                               layout=harness.layout.code)
 
         def timed(step):
             s = torch.cuda.Stream(device=dev)
@@ -1011,18 +1006,17 @@ def resident_bench(lib, harness, batches=(1, 8, 32, 128), steps: int = 20, warmu
 
         extra = {}
         if B == 1:
-            dt_fused = timed(step_fused)
-            x_fused = x.clone()
-            dt = timed(step_separate)
-            extra = {"launches_per_layer": "stub, logits, top-k, gate/up, down",
-                     "fused_launch": {
-                         "launches_per_layer": "stub, logits, route + gate/up "
-                                               "(moe_route_fetch_ffn over the resident records, "
-                                               "no miss), down",
-                         "tokens_per_s": round(1 / dt_fused, 1),
-                         "ms_per_step": round(1e3 * dt_fused, 4),
-                         "x_equal": bool(torch.equal(x, x_fused)),
-                         "misses_queued": int(nmiss.sum())}}
+            dt_sep = timed(step_separate)
+            x_sep = x.clone()
+            dt = timed(step_fused)
+            extra = {"launches_per_layer": "stub, logits, top-k + gate/up "
+                                           "(moe_router_fp8_moe_forward), down",
+                     "separate_launches": {
+                         "launches_per_layer": "stub, logits, top-k (moe_router_topk), "
+                                               "gate/up, down",
+                         "tokens_per_s": round(1 / dt_sep, 1),
+                         "ms_per_step": round(1e3 * dt_sep, 4),
+                         "x_equal": bool(torch.equal(x, x_sep))}}
         else:
             dt = timed(step_separate)
         distinct = np.array([np.unique(ids[l].cpu().numpy()).size for l in range(L)])

@@ -26,6 +26,7 @@
 #include "common.hpp"
 #include "gemv.hpp"
 #include "grouped.hpp"
+#include "route.hpp"
 #include "shared.hpp"
 
 #include <mutex>
@@ -94,12 +95,21 @@ constexpr int kGateUpWaves = kGateUpSplit * kGateUpTiles;
 static_assert(kGateUpTiles == 2, "a workgroup pairs one gate tile with the up tile of its columns");
 constexpr int kGateUpChunk = 8;                  // K-blocks in flight per lane
 
-template <bool SHARED>
+//
+// TOPK > 0 (one token, moe_router_fp8_moe_forward): no ids are read; every
+// wave takes the top-k of the token's logits itself (TOPK logits per lane,
+// the router's wave_topk_of, so the same picks and weights), its workgroup's
+// pick p being lane p's, and workgroup (0, 0) writes the ids (int32, to
+// `ids`) and the routing weights (float32, to `wout`) for the down launch.
+// The logits' round trip and the top-k take the place of the id load ahead
+// of the weight loads, and the top-k needs no launch of its own.
+template <bool SHARED, int TOPK>
 __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
     const uint16_t* __restrict__ x, const void* __restrict__ ids, int ids64, int32_t top_k,
     const uint8_t* __restrict__ w13, const float* __restrict__ s13, int64_t w13_es,
     int64_t s13_es, int tiled, int32_t n_experts, int32_t hidden, int32_t inter,
-    float* __restrict__ act, int32_t tokens, SharedRefs sh) {
+    float* __restrict__ act, int32_t tokens, SharedRefs sh, const float* __restrict__ logits,
+    float* __restrict__ wout) {
   __shared__ __align__(16) uint8_t xq[kMaxHidden];
   __shared__ float xs[kMaxHidden / 128];
   __shared__ __align__(16) float dpart[kGateUpTiles][kMaxHidden / 128][16];
@@ -153,7 +163,21 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
   const uint16_t* xr = x + static_cast<int64_t>(t) * hidden;
   const int i0 = wave * 512 + lane * 8;
   const uint4 xraw = *reinterpret_cast<const uint4*>(xr + (i0 < hidden ? i0 : 0));
-  const int64_t e = load_id(ids, ids64, p);
+  int64_t e;
+  if constexpr (TOPK > 0) {
+    float lv[TOPK];
+    load_logits<TOPK>(logits, n_experts, lv);
+    int32_t id;
+    float wt;
+    wave_topk_of<TOPK>(lv, n_experts, top_k, &id, &wt);
+    e = __builtin_amdgcn_readlane(id, p);
+    if (blockIdx.x == 0 && p == 0 && wave == 0 && lane < top_k) {
+      static_cast<int32_t*>(const_cast<void*>(ids))[lane] = id;
+      wout[lane] = wt;
+    }
+  } else {
+    e = load_id(ids, ids64, p);
+  }
   const bool valid = e >= 0 && e < n_experts;
   const int G = hidden >> 7;
   // wave is uniform: so are the tile, the K range and the scale row, which
@@ -485,27 +509,56 @@ __global__ __launch_bounds__(64 * (kMaxK / 2 + 1)) void down_gemv_kernel(
 }
 
 // The two decode launches; `sh` (nullable) carries the shared expert along.
+// The router of one token in front of the GEMV launches: its logits launch
+// (gate weight, bias, logit rounding, the logits buffer), then the top-k
+// made inside the gate/up launch (gateup_gemv_kernel's TOPK), which writes
+// the ids and weights.
+struct RouterTopK {
+  const void* w_gate;
+  const float* bias;
+  int bf16_logits;
+  float* logits;
+  int32_t* ids;
+  float* weights;
+};
+
 static int launch_gemv(const uint16_t* x, const void* ids, int ids64, const void* weights,
                        int wbf16, int32_t tokens, int32_t top_k, const uint8_t* w13,
                        const float* s13, const uint8_t* w2, const float* s2,
                        const moe_expert_strides& es, int32_t n_experts, int32_t hidden,
                        int32_t inter, const uint16_t* residual, uint16_t* out, float* h,
-                       const SharedRefs* sh, hipStream_t s) {
+                       const SharedRefs* sh, hipStream_t s, const RouterTopK* rt = nullptr) {
   const int64_t pairs = static_cast<int64_t>(tokens) * top_k;
   const unsigned gx = static_cast<unsigned>((2 * inter) / 16);
   if (sh) {
     // extra rows of workgroups for the shared expert's Is + 1 rows (the last: sigmoid gate)
     const unsigned per_y = kSharedJPW * (gx / kGateUpTiles) * kGateUpWaves;
     const unsigned sy = static_cast<unsigned>((sh->inter + 1 + per_y - 1) / per_y);
-    hipLaunchKernelGGL(gateup_gemv_kernel<true>, dim3(gx / kGateUpTiles, pairs + sy),
+    hipLaunchKernelGGL((gateup_gemv_kernel<true, 0>), dim3(gx / kGateUpTiles, pairs + sy),
                        dim3(64 * kGateUpWaves), 0, s, x, ids,
                        ids64, top_k, w13, s13, es.w13, es.s13, static_cast<int>(es.layout),
-                       n_experts, hidden, inter, h, tokens, *sh);
+                       n_experts, hidden, inter, h, tokens, *sh, nullptr, nullptr);
+  } else if (rt) {
+    // one token: the ids and weights the down launch reads are the top-k's
+    ids = rt->ids;
+    ids64 = 0;
+    weights = rt->weights;
+    wbf16 = 0;
+    if (n_experts <= 256)
+      hipLaunchKernelGGL((gateup_gemv_kernel<false, 4>), dim3(gx / kGateUpTiles, pairs),
+                         dim3(64 * kGateUpWaves), 0, s, x, ids, 0, top_k, w13, s13, es.w13,
+                         es.s13, static_cast<int>(es.layout), n_experts, hidden, inter, h, tokens,
+                         SharedRefs{}, rt->logits, rt->weights);
+    else
+      hipLaunchKernelGGL((gateup_gemv_kernel<false, 16>), dim3(gx / kGateUpTiles, pairs),
+                         dim3(64 * kGateUpWaves), 0, s, x, ids, 0, top_k, w13, s13, es.w13,
+                         es.s13, static_cast<int>(es.layout), n_experts, hidden, inter, h, tokens,
+                         SharedRefs{}, rt->logits, rt->weights);
   } else {
-    hipLaunchKernelGGL(gateup_gemv_kernel<false>, dim3(gx / kGateUpTiles, pairs),
+    hipLaunchKernelGGL((gateup_gemv_kernel<false, 0>), dim3(gx / kGateUpTiles, pairs),
                        dim3(64 * kGateUpWaves), 0, s, x, ids, ids64,
                        top_k, w13, s13, es.w13, es.s13, static_cast<int>(es.layout), n_experts,
-                       hidden, inter, h, tokens, SharedRefs{});
+                       hidden, inter, h, tokens, SharedRefs{}, nullptr, nullptr);
   }
   int rc = check_launch("moe_fp8_moe_forward(gate/up)");
   if (rc) return rc;
@@ -653,7 +706,7 @@ static int forward_impl(const void* x, const void* ids, int32_t ids_dtype, const
                         int32_t hidden, int32_t inter, const moe_expert_strides* strides,
                         const void* residual, void* out, void* workspace, size_t workspace_bytes,
                         int32_t mode, const SharedRefs* sh, bool* fused, void* stream,
-                        bool static_scratch = false) {
+                        bool static_scratch = false, const RouterTopK* rt = nullptr) {
   *fused = false;
   MOE_REQUIRE(tokens >= 0, "moe_fp8_moe_forward: tokens < 0");
   MOE_REQUIRE(top_k >= 1 && top_k <= kMaxK, "moe_fp8_moe_forward: need 1 <= top_k <= %d", kMaxK);
@@ -726,10 +779,16 @@ static int forward_impl(const void* x, const void* ids, int32_t ids_dtype, const
   // the shared expert rides along (the down workgroup's ceil(top_k/2) + 1
   // waves fit its launch bounds for every top_k)
   *fused = sh != nullptr;
+  if (rt) {
+    MOE_REQUIRE(tokens == 1 && !sh, "moe_router_fp8_moe_forward: one token, no shared expert");
+    const int rc = launch_decode_logits(x, rt->w_gate, rt->bias, hidden, n_experts,
+                                        rt->bf16_logits, rt->logits, nullptr, s);
+    if (rc) return rc;
+  }
   return launch_gemv(static_cast<const uint16_t*>(x), ids, ids64, weights, wbf16, tokens, top_k,
                      static_cast<const uint8_t*>(w13), s13, static_cast<const uint8_t*>(w2), s2,
                      es, n_experts, hidden, inter, static_cast<const uint16_t*>(residual),
-                     static_cast<uint16_t*>(out), h, sh, s);
+                     static_cast<uint16_t*>(out), h, sh, s, rt);
 }
 
 extern "C" int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t ids_dtype,
@@ -745,6 +804,31 @@ extern "C" int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t id
   return forward_impl(x, ids, ids_dtype, weights, w_dtype, tokens, top_k, w13, s13, w2, s2,
                       n_experts, hidden, inter, strides, residual, out, workspace, workspace_bytes,
                       mode, nullptr, &fused, stream);
+}
+
+extern "C" int moe_router_fp8_moe_forward(const void* x, const void* w_gate, const float* bias,
+                                          int32_t logit_dtype, int32_t hidden,
+                                          int32_t n_experts, int32_t top_k, float* logits,
+                                          int32_t* ids, float* weights, const void* w13,
+                                          const float* s13, const void* w2, const float* s2,
+                                          int32_t inter, const moe_expert_strides* strides,
+                                          const void* residual, void* out, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+  MOE_REQUIRE(x && w_gate && logits && ids && weights, "moe_router_fp8_moe_forward: NULL pointer");
+  MOE_REQUIRE(logit_dtype == MOE_F32 || logit_dtype == MOE_BF16,
+              "moe_router_fp8_moe_forward: logit_dtype must be MOE_F32 or MOE_BF16");
+  MOE_REQUIRE(top_k >= 1 && top_k <= kMaxK && top_k <= n_experts && n_experts <= 1024,
+              "moe_router_fp8_moe_forward: need 1 <= top_k <= min(%d, n_experts), "
+              "n_experts <= 1024", kMaxK);
+  MOE_REQUIRE(reinterpret_cast<uintptr_t>(w_gate) % 16 == 0,
+              "moe_router_fp8_moe_forward: w_gate must be 16-byte aligned");
+  const RouterTopK rt{w_gate, bias, logit_dtype == MOE_BF16 ? 1 : 0, logits, ids, weights};
+  bool fused;
+  // mode 1: the per-pair GEMV kernels, whose gate/up launch makes the top-k;
+  // every check of the expert call runs before the logits launch is enqueued
+  return forward_impl(x, ids, MOE_I32, weights, MOE_F32, 1, top_k, w13, s13, w2, s2, n_experts,
+                      hidden, inter, strides, residual, out, workspace, workspace_bytes, 1,
+                      nullptr, &fused, stream, false, &rt);
 }
 
 extern "C" size_t moe_fp8_moe_block_workspace(int32_t tokens, int32_t top_k, int32_t n_experts,
