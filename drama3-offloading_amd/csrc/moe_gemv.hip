@@ -167,13 +167,15 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
   if constexpr (TOPK > 0) {
     float lv[TOPK];
     load_logits<TOPK>(logits, n_experts, lv);
-    int32_t id;
-    float wt;
-    wave_topk_of<TOPK>(lv, n_experts, top_k, &id, &wt);
+    const uint64_t pick = wave_topk_keys<TOPK>(lv, n_experts, top_k);
+    const int32_t id = topk_id(pick, top_k);
     e = __builtin_amdgcn_readlane(id, p);
-    if (blockIdx.x == 0 && p == 0 && wave == 0 && lane < top_k) {
-      static_cast<int32_t*>(const_cast<void*>(ids))[lane] = id;
-      wout[lane] = wt;
+    if (blockIdx.x == 0 && p == 0 && wave == 0) {   // uniform: the weights only here
+      const float wt = topk_weight(pick, top_k);
+      if (lane < top_k) {
+        static_cast<int32_t*>(const_cast<void*>(ids))[lane] = id;
+        wout[lane] = wt;
+      }
     }
   } else {
     e = load_id(ids, ids64, p);

@@ -1,6 +1,8 @@
 // The decode router's top-k and the decode step's route (top-k + slot
 // resolve on a double-buffered table by one wave), shared by the router
-// kernels (router.hip) and the decode step's fused launch (decode_step.hip).
+// kernels (router.hip), the decode step's fused launches (decode_step.hip,
+// codec.hip) and the GEMV's gate/up launch when it makes the top-k itself
+// (moe_gemv.hip).
 #pragma once
 
 #include "common.hpp"
@@ -53,9 +55,12 @@ __device__ __forceinline__ void load_logits(const float* __restrict__ row, int32
   for (int j = 0; j < PER; ++j) lv[j] = row[min(lane + 64 * j, n_experts - 1)];
 }
 
+// The picks alone: lane r < k returns pick r's 64-bit key, (logit key << 32)
+// | ~index (0 past k); topk_id and topk_weight turn it into the expert id
+// and the renormalised softmax weight.
 template <int PER>
-__device__ __forceinline__ void wave_topk_of(const float (&lv)[PER], int32_t n_experts,
-                                             int32_t top_k, int32_t* id, float* wt) {
+__device__ __forceinline__ uint64_t wave_topk_keys(const float (&lv)[PER], int32_t n_experts,
+                                                   int32_t top_k) {
   const int lane = threadIdx.x & 63;
   uint64_t key[PER];
 #pragma unroll
@@ -101,11 +106,29 @@ __device__ __forceinline__ void wave_topk_of(const float (&lv)[PER], int32_t n_e
       if (lane == r) pick = best;
     }
   }
+  return pick;
+}
+
+__device__ __forceinline__ int32_t topk_id(uint64_t pick, int32_t top_k) {
+  const int lane = threadIdx.x & 63;
+  return lane < top_k ? static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(pick)) : -1;
+}
+
+// exp(l_r - l_0) over the sum of the k picks' (a wave-wide call)
+__device__ __forceinline__ float topk_weight(uint64_t pick, int32_t top_k) {
+  const int lane = threadIdx.x & 63;
   const float v = key_logit(static_cast<uint32_t>(pick >> 32));
   const float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
   const float ex = lane < top_k ? expf(v - m) : 0.0f;
-  *id = lane < top_k ? static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(pick)) : -1;
-  *wt = ex / wave_sum_f32_dpp(ex);
+  return ex / wave_sum_f32_dpp(ex);
+}
+
+template <int PER>
+__device__ __forceinline__ void wave_topk_of(const float (&lv)[PER], int32_t n_experts,
+                                             int32_t top_k, int32_t* id, float* wt) {
+  const uint64_t pick = wave_topk_keys<PER>(lv, n_experts, top_k);
+  *id = topk_id(pick, top_k);
+  *wt = topk_weight(pick, top_k);
 }
 
 template <int PER>
