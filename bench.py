@@ -1351,18 +1351,28 @@ def run_probe(args) -> int:
     elif args.probe == "stub":
         # the non-expert stand-in: a bf16 [2048, 2048] matrix times one token,
         # rotating over 40 layers' matrices (320 MiB), torch.mv against
-        # moe_linear_bf16 at 1, 2 and 4 rows per wave
+        # moe_linear_bf16 at 1, 2 and 4 rows per wave; then 8, 32 and 128
+        # tokens, torch.mm against moe_linear_bf16
         H = DRAMA3.hidden
         w = (torch.randn((40, H, H), device=dev) / H ** 0.5).to(torch.bfloat16)
         x = torch.randn((1, H), device=dev).to(torch.bfloat16)
         y = torch.empty_like(x)
-        res = {"probe": "stub", "what": "graph of back-to-back calls, 1 token, bf16 "
+        res = {"probe": "stub", "what": "graph of back-to-back calls, 1 to 128 tokens, bf16 "
                "[2048, 2048] per layer, 40 layers' weights in rotation", "us_per_call": {}}
         res["us_per_call"]["torch.mv"] = round(1e6 * graph_time(
             dev, lambda r: torch.mv(w[r % 40], x[0], out=y[0]), args.steps), 3)
         for rpw in (1, 2, 4):
             res["us_per_call"][f"moe_linear_bf16 rows_per_wave {rpw}"] = round(1e6 * graph_time(
                 dev, lambda r: lib.linear_bf16(x, w[r % 40], y, rows_per_wave=rpw), args.steps), 3)
+        # the batched decode's stub: torch.mm (hipBLASLt) against the
+        # matrix-core moe_linear_bf16
+        for T in (8, 32, 128):
+            xb = torch.randn((T, H), device=dev).to(torch.bfloat16)
+            yb = torch.empty_like(xb)
+            res["us_per_call"][f"torch.mm {T} tokens"] = round(1e6 * graph_time(
+                dev, lambda r: torch.mm(xb, w[r % 40].t(), out=yb), args.steps), 3)
+            res["us_per_call"][f"moe_linear_bf16 {T} tokens"] = round(1e6 * graph_time(
+                dev, lambda r: lib.linear_bf16(xb, w[r % 40], yb), args.steps), 3)
     elif args.probe == "blockffn":
         # the routed expert FFN and the MoE block (shared expert carried in
         # the same two launches) on resident records

@@ -60,11 +60,15 @@ from hostpool import DRAMA3, HostPool, RecordLayout
 def stub_linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor, x_add=None) -> None:
     """The non-expert stand-in, out = x w^T with w [out, in] bf16 (an
     nn.Linear without bias); with x_add, out = (x + x_add) w^T, the bf16
-    add folded into the product's loads.  Up to 4 tokens take
-    moe_linear_bf16, one pass over the weights (3.55 us for 2048 x 2048 at
-    one token on MI355X, against 6.9 us for torch.mv and 12.0 us for a 1-row
-    torch.mm); more tokens a matrix product."""
-    if x.shape[0] <= 4:
+    add folded into the product's loads.  moe_linear_bf16 takes up to 4
+    tokens on the vector units, one pass over the weights (3.55 us for
+    2048 x 2048 at one token on MI355X, against 6.9 us for torch.mv and
+    12.0 us for a 1-row torch.mm), and 5 to 128 on the matrix cores (5.3 /
+    7.7 / 11.2 us at 8 / 32 / 128 tokens, against 10.9 / 11.1 / 11.2 for
+    torch.mm); beyond that, or for shapes it does not take, a torch
+    matrix product."""
+    T, K = x.shape
+    if T <= 4 or (T <= 128 and x_add is None and K % 64 == 0 and w.shape[0] % 16 == 0):
         hipfetch.require().linear_bf16(x, w, out, x_add=x_add)
     else:
         torch.mm(x if x_add is None else x + x_add, w.t(), out=out)

@@ -77,15 +77,17 @@ int moe_silu_check(const float* g, const float* u, float* out, uint32_t n, void*
 int moe_stream_read(const void* src, int64_t bytes, int32_t workgroups, uint32_t* sink,
                     void* stream);
 
-/* y[t] = x[t] W^T in bf16 for 1..4 tokens: W [out_features, in_features]
+/* y[t] = x[t] W^T in bf16 for 1..128 tokens: W [out_features, in_features]
  * bf16 (nn.Linear layout, in_features a multiple of 8), x [tokens,
  * in_features], y [tokens, out_features]; each output the f32 sum of its
- * row's products (per lane in slice order, then a fixed lane tree), rounded
- * once to bf16.  x_add (nullable, x's shape): the product is of
+ * row's products rounded once to bf16 (up to 4 tokens: per lane in slice
+ * order, then a fixed lane tree; 5 to 128 tokens: on the matrix cores,
+ * with in_features a multiple of 64, out_features of 16 and no x_add).
+ * x_add (nullable, x's shape, up to 4 tokens): the product is of
  * bf16(x + x_add) instead, each element's float sum rounded once to bf16
- * (a residual add folded into the loads).  rows_per_wave: 1, 2 or 4 rows
- * per wave, 0 for the default (1); the outputs do not depend on it.  x,
- * x_add and w 16-byte aligned.  No counterpart in the reference: the
+ * (a residual add folded into the loads).  rows_per_wave (up to 4
+ * tokens): 1, 2 or 4 rows per wave, 0 for the default (1); the outputs do
+ * not depend on it.  x, x_add and w 16-byte aligned.  No counterpart in the reference: the
  * decode benchmark's stand-in for the non-expert compute of a layer (one
  * [2048, 2048] matrix) runs on it, one pass over the weights. */
 int moe_linear_bf16(const void* x, const void* x_add, const void* w, int32_t tokens,
