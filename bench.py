@@ -937,11 +937,12 @@ def prefill_bench(lib, harness, tokens: int = 512, passes: int = 2, coded=None, 
 def resident_bench(lib, harness, batches=(1, 8, 32, 128), steps: int = 20, warmup: int = 3):
     """All 40 x 256 expert records resident in HBM (30 GiB, no offload):
     batched decode at B tokens per step, top-8 of a uniform router, the
-    non-expert stub per layer, the whole step in one hipGraph.  Batch 1 runs
-    the router's top-k inside the gate/up launch (moe_router_fp8_moe_forward:
-    logits, top-k + gate/up, down); it is also timed with the top-k as a
-    launch of its own (moe_router_topk, then moe_fp8_moe_forward), which
-    must give the same output."""
+    non-expert stub per layer, the whole step in one hipGraph.  Batches of
+    up to 16 tokens (the per-pair GEMV) run the router's top-k inside the
+    gate/up launch (moe_router_fp8_moe_forward: logits, top-k + gate/up,
+    down); they are also timed with the top-k as a launch of its own
+    (moe_router_topk, then moe_fp8_moe_forward), which must give the same
+    output."""
     import numpy as np
     import torch
     import decode
@@ -973,13 +974,13 @@ def resident_bench(lib, harness, batches=(1, 8, 32, 128), steps: int = 20, warmu
                 lib.fp8_moe_forward(h, ids[l], wts[l], *views[l], x, ws, residual=h,
                                     layout=harness.layout.code)
 
-        if B == 1:
+        if B <= 16:
             def step_fused(_r=0):
                 x.copy_(x0)
                 for l in range(L):
                     decode.stub_linear(x, harness.w_stub[l], h)
-                    lib.router_fp8_moe_forward(h, gate[l], None, K, logits[0], ids[l, 0],
-                                               wts[l, 0], *views[l], x, ws, residual=h,
+                    lib.router_fp8_moe_forward(h, gate[l], None, K, logits, ids[l], wts[l],
+                                               *views[l], x, ws, residual=h,
                                                layout=harness.layout.code)
 
         def timed(step):
@@ -1005,7 +1006,7 @@ def resident_bench(lib, harness, batches=(1, 8, 32, 128), steps: int = 20, warmu
             return a.elapsed_time(b) / 1000.0 / steps
 
         extra = {}
-        if B == 1:
+        if B <= 16:
             dt_sep = timed(step_separate)
             x_sep = x.clone()
             dt = timed(step_fused)
@@ -1014,7 +1015,7 @@ def resident_bench(lib, harness, batches=(1, 8, 32, 128), steps: int = 20, warmu
                      "separate_launches": {
                          "launches_per_layer": "stub, logits, top-k (moe_router_topk), "
                                                "gate/up, down",
-                         "tokens_per_s": round(1 / dt_sep, 1),
+                         "tokens_per_s": round(B / dt_sep, 1),
                          "ms_per_step": round(1e3 * dt_sep, 4),
                          "x_equal": bool(torch.equal(x, x_sep))}}
         else:

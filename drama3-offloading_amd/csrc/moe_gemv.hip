@@ -96,11 +96,12 @@ static_assert(kGateUpTiles == 2, "a workgroup pairs one gate tile with the up ti
 constexpr int kGateUpChunk = 8;                  // K-blocks in flight per lane
 
 //
-// TOPK > 0 (one token, moe_router_fp8_moe_forward): no ids are read; every
-// wave takes the top-k of the token's logits itself (TOPK logits per lane,
-// the router's wave_topk_of, so the same picks and weights), its workgroup's
-// pick p being lane p's, and workgroup (0, 0) writes the ids (int32, to
-// `ids`) and the routing weights (float32, to `wout`) for the down launch.
+// TOPK > 0 (moe_router_fp8_moe_forward): no ids are read; every wave takes
+// the top-k of its token's logits itself (TOPK logits per lane, the
+// router's wave_topk_keys, so the same picks and weights), its workgroup's
+// pick k being lane k's, and workgroup (0, t * top_k) writes token t's ids
+// (int32, to `ids`) and routing weights (float32, to `wout`) for the down
+// launch.
 // The logits' round trip and the top-k take the place of the id load ahead
 // of the weight loads, and the top-k needs no launch of its own.
 template <bool SHARED, int TOPK>
@@ -165,16 +166,17 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
   const uint4 xraw = *reinterpret_cast<const uint4*>(xr + (i0 < hidden ? i0 : 0));
   int64_t e;
   if constexpr (TOPK > 0) {
+    const int k = p - t * top_k;
     float lv[TOPK];
-    load_logits<TOPK>(logits, n_experts, lv);
+    load_logits<TOPK>(logits + static_cast<int64_t>(t) * n_experts, n_experts, lv);
     const uint64_t pick = wave_topk_keys<TOPK>(lv, n_experts, top_k);
     const int32_t id = topk_id(pick, top_k);
-    e = __builtin_amdgcn_readlane(id, p);
-    if (blockIdx.x == 0 && p == 0 && wave == 0) {   // uniform: the weights only here
+    e = __builtin_amdgcn_readlane(id, k);
+    if (blockIdx.x == 0 && k == 0 && wave == 0) {   // uniform: the weights only here
       const float wt = topk_weight(pick, top_k);
       if (lane < top_k) {
-        static_cast<int32_t*>(const_cast<void*>(ids))[lane] = id;
-        wout[lane] = wt;
+        static_cast<int32_t*>(const_cast<void*>(ids))[p + lane] = id;
+        wout[p + lane] = wt;
       }
     }
   } else {
@@ -511,7 +513,7 @@ __global__ __launch_bounds__(64 * (kMaxK / 2 + 1)) void down_gemv_kernel(
 }
 
 // The two decode launches; `sh` (nullable) carries the shared expert along.
-// The router of one token in front of the GEMV launches: its logits launch
+// The router of up to 16 tokens in front of the GEMV launches: its logits launch
 // (gate weight, bias, logit rounding, the logits buffer), then the top-k
 // made inside the gate/up launch (gateup_gemv_kernel's TOPK), which writes
 // the ids and weights.
@@ -782,9 +784,10 @@ static int forward_impl(const void* x, const void* ids, int32_t ids_dtype, const
   // waves fit its launch bounds for every top_k)
   *fused = sh != nullptr;
   if (rt) {
-    MOE_REQUIRE(tokens == 1 && !sh, "moe_router_fp8_moe_forward: one token, no shared expert");
-    const int rc = launch_decode_logits(x, rt->w_gate, rt->bias, hidden, n_experts,
-                                        rt->bf16_logits, rt->logits, nullptr, s);
+    MOE_REQUIRE(tokens <= kGemvMaxTokens && !sh,
+                "moe_router_fp8_moe_forward: 1 to %d tokens, no shared expert", kGemvMaxTokens);
+    const int rc = launch_router_logits(x, rt->w_gate, rt->bias, tokens, hidden, n_experts,
+                                        rt->bf16_logits, rt->logits, s);
     if (rc) return rc;
   }
   return launch_gemv(static_cast<const uint16_t*>(x), ids, ids64, weights, wbf16, tokens, top_k,
@@ -809,13 +812,15 @@ extern "C" int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t id
 }
 
 extern "C" int moe_router_fp8_moe_forward(const void* x, const void* w_gate, const float* bias,
-                                          int32_t logit_dtype, int32_t hidden,
+                                          int32_t logit_dtype, int32_t tokens, int32_t hidden,
                                           int32_t n_experts, int32_t top_k, float* logits,
                                           int32_t* ids, float* weights, const void* w13,
                                           const float* s13, const void* w2, const float* s2,
                                           int32_t inter, const moe_expert_strides* strides,
                                           const void* residual, void* out, void* workspace,
                                           size_t workspace_bytes, void* stream) {
+  MOE_REQUIRE(tokens >= 1 && tokens <= kGemvMaxTokens,
+              "moe_router_fp8_moe_forward: need 1 <= tokens <= %d", kGemvMaxTokens);
   MOE_REQUIRE(x && w_gate && logits && ids && weights, "moe_router_fp8_moe_forward: NULL pointer");
   MOE_REQUIRE(logit_dtype == MOE_F32 || logit_dtype == MOE_BF16,
               "moe_router_fp8_moe_forward: logit_dtype must be MOE_F32 or MOE_BF16");
@@ -828,7 +833,7 @@ extern "C" int moe_router_fp8_moe_forward(const void* x, const void* w_gate, con
   bool fused;
   // mode 1: the per-pair GEMV kernels, whose gate/up launch makes the top-k;
   // every check of the expert call runs before the logits launch is enqueued
-  return forward_impl(x, ids, MOE_I32, weights, MOE_F32, 1, top_k, w13, s13, w2, s2, n_experts,
+  return forward_impl(x, ids, MOE_I32, weights, MOE_F32, tokens, top_k, w13, s13, w2, s2, n_experts,
                       hidden, inter, strides, residual, out, workspace, workspace_bytes, 1,
                       nullptr, &fused, stream, false, &rt);
 }

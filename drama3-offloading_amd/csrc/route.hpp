@@ -19,6 +19,12 @@ int launch_decode_logits(const void* x, const void* w, const float* bias, int32_
                          int32_t n_experts, int bf16_logits, float* logits, int64_t* step_inc,
                          hipStream_t s);
 
+// The router's logits launch for `tokens` tokens (moe_router_topk's first
+// launch): logits [tokens, n_experts].
+int launch_router_logits(const void* x, const void* w, const float* bias, int32_t tokens,
+                         int32_t hidden, int32_t n_experts, int bf16_logits, float* logits,
+                         hipStream_t s);
+
 // Order-preserving 32-bit key of a float logit: larger logit, larger key;
 // NaN ranks below every number (it is picked only when nothing else is left).
 __device__ __forceinline__ uint32_t logit_key(float f) {

@@ -281,6 +281,22 @@ int launch_decode_logits(const void* x, const void* w, const float* bias, int32_
   return check_launch("router_logits_kernel");
 }
 
+int launch_router_logits(const void* x, const void* w, const float* bias, int32_t tokens,
+                         int32_t hidden, int32_t n_experts, int bf16_logits, float* logits,
+                         hipStream_t s) {
+  const dim3 grid((n_experts + kLogitWaves - 1) / kLogitWaves,
+                  (tokens + kTokBlock - 1) / kTokBlock);
+  if (tokens == 1)
+    hipLaunchKernelGGL(router_logits_kernel<1>, grid, dim3(64 * kLogitWaves), 0, s,
+                       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias,
+                       tokens, hidden, n_experts, bf16_logits, logits, nullptr);
+  else
+    hipLaunchKernelGGL(router_logits_kernel<kTokBlock>, grid, dim3(64 * kLogitWaves), 0, s,
+                       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias,
+                       tokens, hidden, n_experts, bf16_logits, logits, nullptr);
+  return check_launch("router_logits_kernel");
+}
+
 }  // namespace moe
 
 using namespace moe;
@@ -305,15 +321,8 @@ extern "C" int moe_router_topk(const void* x, const void* w, const float* bias,
                   (tokens + kTokBlock - 1) / kTokBlock);
   MOE_REQUIRE(grid.y <= 65535, "moe_router_topk: too many tokens (%d)", tokens);
   hipStream_t s = as_stream(stream);
-  if (tokens == 1)
-    hipLaunchKernelGGL(router_logits_kernel<1>, grid, dim3(64 * kLogitWaves), 0, s,
-                       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias,
-                       tokens, hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0, logits, nullptr);
-  else
-    hipLaunchKernelGGL(router_logits_kernel<kTokBlock>, grid, dim3(64 * kLogitWaves), 0, s,
-                       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias,
-                       tokens, hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0, logits, nullptr);
-  int rc = check_launch("moe_router_topk(logits)");
+  int rc = launch_router_logits(x, w, bias, tokens, hidden, n_experts,
+                                logit_dtype == MOE_BF16 ? 1 : 0, logits, s);
   if (rc) return rc;
   const int i64 = ids_dtype == MOE_I64 ? 1 : 0, bf = w_dtype == MOE_BF16 ? 1 : 0;
   if (n_experts <= 256)

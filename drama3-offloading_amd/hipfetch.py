@@ -117,7 +117,7 @@ SIGNATURES = {
     "moe_fp8_moe_forward_ex": (C.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _vp,
                                          _vp, _i32, _i32, _i32, C.POINTER(ExpertStrides), _vp,
                                          _vp, _vp, _sz, _i32, _vp]),
-    "moe_router_fp8_moe_forward": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp,
+    "moe_router_fp8_moe_forward": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp,
                                              _vp, _vp, _vp, _vp, _vp, _i32,
                                              C.POINTER(ExpertStrides), _vp, _vp, _vp, _sz, _vp]),
     "moe_fp8_moe_forward_noalloc": (C.c_int, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp,
@@ -592,27 +592,28 @@ class Native:
     def router_fp8_moe_forward(self, x, w_gate, bias, top_k: int, logits, ids, weights, w13,
                                s13, w2, s2, out, workspace, residual=None,
                                logit_dtype: str = "bf16", layout: int = LAYOUT_ROWS) -> None:
-        """One token's router and expert FFN over resident experts
-        (moe_router_fp8_moe_forward): logits [E] f32, ids [top_k] int32 and
-        weights [top_k] f32 written; out [1, H] = residual + MoE(x), as
-        router_topk followed by fp8_moe_forward(mode=1)."""
+        """The router and expert FFN of 1-16 tokens over resident experts
+        (moe_router_fp8_moe_forward): logits [T, E] f32, ids [T, top_k] int32
+        and weights [T, top_k] f32 written; out [T, H] = residual + MoE(x),
+        as router_topk followed by fp8_moe_forward(mode=1)."""
         import torch
         what = "moe_router_fp8_moe_forward"
         self._on_gpu(what, x, w_gate, bias, logits, ids, weights, w13, s13, w2, s2, out,
                      workspace, residual)
-        if x.dim() != 2 or x.shape[0] != 1:
-            raise ValueError(f"{what} takes exactly one token")
-        H, E = self._router_bufs(what, x, w_gate, bias, logits, 1, top_k)
+        if x.dim() != 2:
+            raise ValueError(f"{what}: x must be [T, H]")
+        T = x.shape[0]
+        H, E = self._router_bufs(what, x, w_gate, bias, logits, T, top_k)
         if w13.shape[0] != E:
             raise ValueError(f"{what}: {w13.shape[0]} experts' weights for a {E}-expert router")
-        self._buf(what, "ids", ids, top_k, torch.int32)
-        self._buf(what, "weights", weights, top_k, torch.float32)
-        self._buf(what, "out", out, H, torch.bfloat16)
-        self._buf(what, "residual", residual, H, torch.bfloat16)
+        self._buf(what, "ids", ids, T * top_k, torch.int32)
+        self._buf(what, "weights", weights, T * top_k, torch.float32)
+        self._buf(what, "out", out, T * H, torch.bfloat16)
+        self._buf(what, "residual", residual, T * H, torch.bfloat16)
         es = _expert_strides(w13, s13, w2, s2, layout)
         self._check(self.cdll.moe_router_fp8_moe_forward(
-            x.data_ptr(), w_gate.data_ptr(), self._ptr(bias), self._logit_code(logit_dtype), H,
-            E, top_k, logits.data_ptr(), ids.data_ptr(), weights.data_ptr(), w13.data_ptr(),
+            x.data_ptr(), w_gate.data_ptr(), self._ptr(bias), self._logit_code(logit_dtype), T,
+            H, E, top_k, logits.data_ptr(), ids.data_ptr(), weights.data_ptr(), w13.data_ptr(),
             s13.data_ptr(), w2.data_ptr(), s2.data_ptr(), w2.shape[-1], C.byref(es),
             self._ptr(residual), out.data_ptr(), workspace.data_ptr(),
             workspace.numel() * workspace.element_size(), self.stream()), what)

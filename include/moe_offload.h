@@ -426,20 +426,21 @@ int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t ids_dtype,
                            void* workspace, size_t workspace_bytes,
                            int32_t mode, void* stream);
 
-/* The router and the expert FFN of ONE token over resident experts, in
+/* The router and the expert FFN of 1..16 tokens over resident experts, in
  * three launches instead of four: the router's logits (x . w_gate^T as in
- * moe_router_topk, + bias) into logits [n_experts], then the per-pair GEMV
- * gate/up launch, each of whose waves takes the top-k of the logits itself
- * (workgroup 0 writing ids [top_k] int32 and weights [top_k] float32), then
- * the down launch.  ids, weights, logits and out equal moe_router_topk
- * followed by moe_fp8_moe_forward_ex (mode 1, int32 ids, float32 weights)
- * bit for bit.  No counterpart in the reference: it fuses the router's
- * top-k (moe.py:217-220) into fp8_moe_forward (bin/devcache.py:275-277) for
- * the all-resident decode.  Constraints: those of both, with
- * 1 <= top_k <= min(16, n_experts), n_experts <= 1024, w_gate 16-byte
- * aligned. */
+ * moe_router_topk, + bias) into logits [tokens, n_experts], then the
+ * per-pair GEMV gate/up launch, each of whose waves takes the top-k of its
+ * token's logits itself (writing ids [tokens, top_k] int32 and weights
+ * [tokens, top_k] float32), then the down launch.  ids, weights, logits and
+ * out equal moe_router_topk followed by moe_fp8_moe_forward_ex (mode 1,
+ * int32 ids, float32 weights) bit for bit.  No counterpart in the
+ * reference: it fuses the router's top-k (moe.py:217-220) into
+ * fp8_moe_forward (bin/devcache.py:275-277) for the all-resident decode.
+ * Constraints: those of both, with 1 <= top_k <= min(16, n_experts),
+ * n_experts <= 1024, w_gate 16-byte aligned. */
 int moe_router_fp8_moe_forward(const void* x, const void* w_gate, const float* bias,
-                               int32_t logit_dtype, int32_t hidden, int32_t n_experts,
+                               int32_t logit_dtype, int32_t tokens, int32_t hidden,
+                               int32_t n_experts,
                                int32_t top_k, float* logits, int32_t* ids, float* weights,
                                const void* w13, const float* s13, const void* w2,
                                const float* s2, int32_t inter,

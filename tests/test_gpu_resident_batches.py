@@ -134,22 +134,27 @@ def test_resident_batch1_fused_launch_against_oracle(lib, dev, resident):
 
 
 @pytest.mark.parametrize("shape", [
-    dict(E=256, K=8, H=2048, I=512, bias=False),
+    dict(E=256, K=8, H=2048, I=512, T=1, bias=False),
+    dict(E=256, K=8, H=2048, I=512, T=8, bias=False),
+    # the GEMV path's most tokens
+    dict(E=256, K=8, H=2048, I=512, T=16, bias=True),
     # the 16-per-lane logits (E > 256), the largest top_k, a router bias
-    dict(E=320, K=16, H=1024, I=256, bias=True),
-    dict(E=1024, K=4, H=512, I=128, bias=True),
-], ids=["drama3", "e320_top16", "e1024"])
-def test_resident_batch1_router_in_gateup_equals_separate_launches(lib, dev, resident, shape):
+    dict(E=320, K=16, H=1024, I=256, T=1, bias=True),
+    dict(E=320, K=16, H=1024, I=256, T=5, bias=True),
+    dict(E=1024, K=4, H=512, I=128, T=3, bias=True),
+], ids=["drama3", "drama3_t8", "drama3_t16", "e320_top16", "e320_top16_t5", "e1024_t3"])
+def test_resident_router_in_gateup_equals_separate_launches(lib, dev, resident, shape):
     """moe_router_fp8_moe_forward (the logits launch, then the top-k made by
     every wave of the gate/up launch, then down) against moe_router_topk +
-    moe_fp8_moe_forward(mode 1): logits, ids, weights and the output (with
-    and without the residual) bit for bit, token after token, eager and
-    replayed from a graph; at Drama-3 shape the ids against oracle.router
-    and the output against the W8A8 oracle within 1e-2."""
+    moe_fp8_moe_forward(mode 1), for 1 to 16 tokens: logits, ids, weights
+    and the output (with and without the residual) bit for bit, batch after
+    batch, eager and replayed from a graph; at Drama-3 shape the ids against
+    oracle.router and the first tokens' output against the W8A8 oracle
+    within 1e-2."""
     import moe
     import synth
     from hostpool import DRAMA3, RecordLayout
-    E_, K_, H_, I_ = shape["E"], shape["K"], shape["H"], shape["I"]
+    E_, K_, H_, I_, T_ = shape["E"], shape["K"], shape["H"], shape["I"], shape["T"]
     if E_ == E:
         rec, gate = resident
         lay = DRAMA3
@@ -164,12 +169,12 @@ def test_resident_batch1_router_in_gateup_equals_separate_launches(lib, dev, res
     bias = (torch.randn(E_, generator=torch.Generator().manual_seed(5)) * 0.01).to(dev) \
         if shape["bias"] else None
     i32 = dict(dtype=torch.int32, device=dev)
-    ws = torch.empty(lib.fp8_moe_workspace(1, K_, E_, H_, I_), dtype=torch.uint8, device=dev)
-    xs = [synth.hidden_states(500 + t, 1, H_).to(dev) for t in range(4)]
+    ws = torch.empty(lib.fp8_moe_workspace(T_, K_, E_, H_, I_), dtype=torch.uint8, device=dev)
+    xs = [synth.hidden_states(500 + t, T_, H_).to(dev) for t in range(4)]
     x = torch.empty_like(xs[0])
-    logits = torch.empty(E_, dtype=torch.float32, device=dev)
-    ids = torch.empty(K_, **i32)
-    wts = torch.empty(K_, dtype=torch.float32, device=dev)
+    logits = torch.empty((T_, E_), dtype=torch.float32, device=dev)
+    ids = torch.empty((T_, K_), **i32)
+    wts = torch.empty((T_, K_), dtype=torch.float32, device=dev)
     outs = [torch.empty_like(x) for _ in range(2)]
 
     def fused():
@@ -178,9 +183,9 @@ def test_resident_batch1_router_in_gateup_equals_separate_launches(lib, dev, res
                                        residual=res, layout=lay.code)
 
     def separate():
-        r_logits = torch.empty((1, E_), dtype=torch.float32, device=dev)
-        r_ids = torch.empty((1, K_), **i32)
-        r_w = torch.empty((1, K_), dtype=torch.float32, device=dev)
+        r_logits = torch.empty((T_, E_), dtype=torch.float32, device=dev)
+        r_ids = torch.empty((T_, K_), **i32)
+        r_w = torch.empty((T_, K_), dtype=torch.float32, device=dev)
         lib.router_topk(x, gate, bias, K_, r_logits, r_ids, r_w)
         sep = [torch.empty_like(x) for _ in range(2)]
         for o, res in zip(sep, (None, x)):
@@ -191,19 +196,21 @@ def test_resident_batch1_router_in_gateup_equals_separate_launches(lib, dev, res
     def check(tag):
         r_logits, r_ids, r_w, sep = separate()
         torch.cuda.synchronize()
-        assert torch.equal(logits, r_logits[0]), f"{tag}: logits"
-        assert torch.equal(ids, r_ids[0]), f"{tag}: ids"
-        assert torch.equal(wts, r_w[0]), f"{tag}: weights"
+        assert torch.equal(logits, r_logits), f"{tag}: logits"
+        assert torch.equal(ids, r_ids), f"{tag}: ids"
+        assert torch.equal(wts, r_w), f"{tag}: weights"
         for o, s_, name in zip(outs, sep, ("out", "out + residual")):
             assert torch.equal(o.view(torch.int16), s_.view(torch.int16)), f"{tag}: {name}"
-        if E_ == E:
+        if E_ == E and bias is None:
             o_ids, _, _ = orouter.route(x.float().cpu().numpy(), gate.float().cpu().numpy(), K_)
-            assert np.array_equal(ids.cpu().numpy()[None], o_ids), tag
-            dense = _unpack(rec[ids.long()].cpu().numpy())
-            want = omoe.forward_w8a8(x.float().cpu().numpy(), np.arange(K_)[None, :],
-                                     wts.cpu().numpy().astype(np.float64)[None], *dense)
-            err = omoe.max_rel_err(outs[0].float().cpu().numpy(), want)
-            assert err <= 1e-2, f"{tag}: max rel err {err:.2e}"
+            assert np.array_equal(ids.cpu().numpy(), o_ids), tag
+            for t in range(min(T_, 2)):
+                dense = _unpack(rec[ids[t].long()].cpu().numpy())
+                want = omoe.forward_w8a8(x[t:t + 1].float().cpu().numpy(),
+                                         np.arange(K_)[None, :],
+                                         wts[t:t + 1].cpu().numpy().astype(np.float64), *dense)
+                err = omoe.max_rel_err(outs[0][t:t + 1].float().cpu().numpy(), want)
+                assert err <= 1e-2, f"{tag} token {t}: max rel err {err:.2e}"
 
     for t, xt in enumerate(xs):
         x.copy_(xt)
