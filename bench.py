@@ -1388,6 +1388,14 @@ def run_probe(args) -> int:
         for p in pools:
             p.close()
         del pools
+    elif args.probe == "resident":
+        # the all-resident batched decode step alone at --tokens per step
+        # (1 to 128), the headline's pools copied to HBM
+        import decode
+        hc = decode.DecodeHarness(decode.DecodeConfig(capacity=50, schedule_steps=50), dev)
+        res = {"probe": "resident",
+               **resident_bench(lib, hc, batches=(args.tokens,), steps=args.steps)}
+        hc.close()
     elif args.probe == "routefetch":
         # the decode step's route + fetch + gate/up launch alone at --misses
         # misses per call (events around the one dispatch), 4 pools of 256
@@ -1652,14 +1660,15 @@ def main() -> int:
     ap.add_argument("--noncoherent-pool", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the prefill and all-resident measurements")
-    ap.add_argument("--tokens", type=int, default=512, help="tokens per call of --probe grouped")
+    ap.add_argument("--tokens", type=int, default=512,
+                    help="tokens per call of --probe grouped, per step of --probe resident")
     ap.add_argument("--idle-us", type=float, default=0.0,
                     help="--probe gemv: a spin of about this many microseconds before each call")
     ap.add_argument("--misses", type=int, default=8,
                     help="misses per call of --probe routefetch (0..8)")
     ap.add_argument("--probe", choices=["gemv", "fetch", "codec", "copy", "grouped", "shared",
                                         "hbm", "step", "contention", "loader", "routefetch",
-                                        "transfer", "blockffn", "stub"],
+                                        "transfer", "blockffn", "stub", "resident"],
                     help="time one kernel alone (--steps launches) instead of the decode step")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
