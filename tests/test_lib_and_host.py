@@ -85,6 +85,25 @@ def test_preconditions_are_rejected_without_launching(lib):
                     (dict(workgroups=0), b"workgroups")):
         assert rfc(**kw) == -1, msg
         assert msg in c.moe_last_error(), (msg, c.moe_last_error())
+    # the router inside the GEMV's gate/up launch: 1..16 tokens, top_k <= 16,
+    # n_experts <= 1024, and the expert call's own checks, all before a launch
+    def rff_router(tokens=1, top_k=8, n_experts=256, hidden=2048, ws=1 << 20):
+        return c.moe_router_fp8_moe_forward(16, 16, None, bf16, tokens, hidden, n_experts, top_k,
+                                            1, 1, 1, 16, 1, 16, 1, 512, None, None, 1, 256, ws,
+                                            None)
+    for kw, msg in ((dict(tokens=0), b"tokens"), (dict(tokens=17), b"tokens"),
+                    (dict(top_k=17), b"top_k"), (dict(n_experts=1025), b"n_experts"),
+                    (dict(hidden=2000), b"hidden"), (dict(ws=16), b"workspace")):
+        assert rff_router(**kw) == -1, msg
+        assert msg in c.moe_last_error(), (msg, c.moe_last_error())
+    # the stub product: 1..128 tokens; beyond 4, K % 64, N % 16 and no addend
+    for args, msg in (((16, None, 16, 129, 64, 16, 16, 0, None), b"tokens"),
+                      ((16, None, 16, 5, 72, 16, 16, 0, None), b"multiple of 64"),
+                      ((16, None, 16, 5, 64, 8, 16, 0, None), b"multiple of 64"),
+                      ((16, 16, 16, 5, 64, 16, 16, 0, None), b"x_add NULL"),
+                      ((16, None, 16, 2, 64, 16, 16, 3, None), b"rows_per_wave")):
+        assert c.moe_linear_bf16(*args) == -1, msg
+        assert msg in c.moe_last_error(), (msg, c.moe_last_error())
     # tile-order pairs: K a multiple of 128, whole 16-row groups, 16-byte aligned
     FetchPair = __import__("hipfetch").FetchPair
     for src, dst, nbytes, tile_k, msg in ((0x1000, 0x2000, 16 * 256, 192, b"multiple of 128"),
