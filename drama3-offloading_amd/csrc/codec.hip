@@ -30,6 +30,10 @@
 // peeked bits always hold two whole codes: entry = both symbols and their
 // total length) and writes its 128 bytes to the cache slot.  The next stream
 // word is read one step ahead, so a step waits on one LDS access.
+//
+// Two launches use the decoder: moe_fetch_coded (the miss list read from
+// device memory) and moe_route_fetch_coded (the decode step's route made by
+// every workgroup first, the miss list then read from LDS).
 #include <string.h>
 
 #include <algorithm>

@@ -23,6 +23,9 @@
 // combine): grid (H/8, tokens), one wave per two experts; each wave
 // quantises its two a rows into LDS, does the 8 output rows of w2 of both in
 // one MFMA per K-block, and the workgroup sums the k partials in order.
+// moe_router_fp8_moe_forward puts the router's logits launch in front and
+// lets kernel 1's waves take the top-k of the logits themselves instead of
+// reading ids (gateup_gemv_kernel's TOPK).
 #include "common.hpp"
 #include "gemv.hpp"
 #include "grouped.hpp"
