@@ -174,6 +174,88 @@ __global__ __launch_bounds__(64 * kLogitWaves) void router_logits_kernel(
     __hip_atomic_fetch_add(step_inc, int64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Many tokens: the logits on the float64 matrix cores.  A workgroup takes 16
+// experts x 16 tokens; its kLogitMmaWaves waves split K, wave v taking the
+// 32-wide chunks v, v + kLogitMmaWaves, ...  Lane (q, i) = (lane / 16, lane %
+// 16) loads 16 bytes of expert i's gate row and of token i's row, K 8q ..
+// 8q + 7 of a chunk, and each of its 8 bf16 pairs is one 16x16x4 float64
+// MFMA (the lane group q's K index of every MFMA), so every product of the
+// chunk is formed once, exact in float64.  The products are the vector
+// kernel's, and so is the float64 sum wherever it is exact (ordinary
+// data), whatever its order; the partial sums of the waves are added
+// through LDS, and the logit is rounded as the vector kernel rounds it.
+typedef double v4d __attribute__((ext_vector_type(4)));
+
+// A 16 x 16 tile is 512 float64 MFMAs over H 2048, about 3.4 us of one CU's
+// float64 matrix rate, so the form pays from the token count at which the
+// vector kernel's per-token work exceeds that.  Measured on MI355X
+// (moe_router_topk, 256 experts, H 2048, a graph over 40 gates): vector
+// 8.2 / 9.9 / 12.7 / 15.5 / 18.2 / 28.6 / 50.5 us at 16 / 32 / 64 / 96 /
+// 128 / 256 / 512 tokens, this form 12.0 up to 256 tokens and 19.2 at 512.
+constexpr int kLogitMmaWaves = 8;       // K slices per workgroup
+constexpr int kLogitMmaChunks = 8;      // 32-wide K chunks per wave in flight
+constexpr int kLogitMmaFrom = 64;       // tokens from which this form runs
+
+__device__ __forceinline__ double bf16_elem(u32x4 v, int m) {
+  const uint32_t w = m < 2 ? v.x : m < 4 ? v.y : m < 6 ? v.z : v.w;
+  return static_cast<double>(__uint_as_float((m & 1) ? (w & 0xffff0000u) : (w << 16)));
+}
+
+__global__ __launch_bounds__(64 * kLogitMmaWaves) void router_logits_mma_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ bias,
+    int32_t tokens, int32_t hidden, int32_t n_experts, int bf16_logits,
+    float* __restrict__ logits) {
+  __shared__ double part[kLogitMmaWaves][16][17];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i = lane & 15, q = lane >> 4;
+  const int e0 = static_cast<int>(blockIdx.x) * 16, t0 = static_cast<int>(blockIdx.y) * 16;
+  const uint16_t* wr = w + static_cast<int64_t>(min(e0 + i, n_experts - 1)) * hidden + 8 * q;
+  const uint16_t* xr = x + static_cast<int64_t>(min(t0 + i, tokens - 1)) * hidden + 8 * q;
+  const int nchunk = hidden >> 5;
+  v4d acc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) acc[c] = v4d{0.0, 0.0, 0.0, 0.0};
+  for (int c0 = wave; c0 < nchunk; c0 += kLogitMmaWaves * kLogitMmaChunks) {
+    u32x4 a[kLogitMmaChunks], b[kLogitMmaChunks];
+#pragma unroll
+    for (int u = 0; u < kLogitMmaChunks; ++u) {
+      const int64_t o = static_cast<int64_t>(min(c0 + u * kLogitMmaWaves, nchunk - 1)) * 32;
+      a[u] = *reinterpret_cast<const u32x4*>(wr + o);
+      b[u] = *reinterpret_cast<const u32x4*>(xr + o);
+    }
+    __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the math below
+#pragma unroll
+    for (int u = 0; u < kLogitMmaChunks; ++u) {
+      // a chunk past the end re-read the last one: zeros (no branch)
+      const bool live = c0 + u * kLogitMmaWaves < nchunk;
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const double av = live ? bf16_elem(a[u], m) : 0.0;
+        const double bv = live ? bf16_elem(b[u], m) : 0.0;
+        acc[m & 3] = __builtin_amdgcn_mfma_f64_16x16x4f64(av, bv, acc[m & 3], 0, 0, 0);
+      }
+    }
+  }
+  // element r of lane (q, i) holds expert 4r + q of token column i (the
+  // float64 MFMA's result layout)
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    part[wave][4 * r + q][i] = (acc[0][r] + acc[1][r]) + (acc[2][r] + acc[3][r]);
+  __syncthreads();
+  if (threadIdx.x < 256) {
+    const int rr = threadIdx.x & 15, j = threadIdx.x >> 4;
+    double sum = part[0][rr][j];
+#pragma unroll
+    for (int v = 1; v < kLogitMmaWaves; ++v) sum += part[v][rr][j];
+    const int e = e0 + rr, t = t0 + j;
+    if (e < n_experts && t < tokens) {
+      float l = bf16_logits ? bf16_of_f64(sum) : static_cast<float>(sum);
+      if (bias) l += bias[e];
+      logits[static_cast<int64_t>(t) * n_experts + e] = l;
+    }
+  }
+}
+
 template <int PER>
 __global__ __launch_bounds__(64) void router_topk_kernel(const float* __restrict__ logits,
                                                          int32_t n_experts, int32_t top_k,
@@ -286,7 +368,12 @@ int launch_router_logits(const void* x, const void* w, const float* bias, int32_
                          hipStream_t s) {
   const dim3 grid((n_experts + kLogitWaves - 1) / kLogitWaves,
                   (tokens + kTokBlock - 1) / kTokBlock);
-  if (tokens == 1)
+  if (tokens >= kLogitMmaFrom && hidden % 32 == 0) {
+    hipLaunchKernelGGL(router_logits_mma_kernel, dim3((n_experts + 15) / 16, (tokens + 15) / 16),
+                       dim3(64 * kLogitMmaWaves), 0, s, static_cast<const uint16_t*>(x),
+                       static_cast<const uint16_t*>(w), bias, tokens, hidden, n_experts,
+                       bf16_logits, logits);
+  } else if (tokens == 1)
     hipLaunchKernelGGL(router_logits_kernel<1>, grid, dim3(64 * kLogitWaves), 0, s,
                        static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias,
                        tokens, hidden, n_experts, bf16_logits, logits, nullptr);

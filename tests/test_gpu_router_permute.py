@@ -173,3 +173,31 @@ def test_route_resolve_equals_router_then_resolve(lib, dev, logit_dtype):
     so, se, st, stp = tab.arrays()
     assert np.array_equal(slot_of.cpu().numpy(), so) and np.array_equal(stamp.cpu().numpy(), st)
     assert int(step.item()) == int(stp)
+
+
+@pytest.mark.parametrize("E,H,T", [(320, 1056, 100), (256, 2048, 64), (40, 96, 65)])
+def test_router_logits_matrix_cores_equal_vector_kernel(lib, dev, E, H, T):
+    """From 64 tokens the logits run on the float64 matrix cores: the same
+    logits, ids and weights as the vector kernel (the same call cut into
+    pieces of fewer than 64 tokens), with a bias, ragged expert and token
+    tiles, and the oracle's ids."""
+    g = torch.Generator(device="cpu").manual_seed(E + H + T)
+    x = torch.randn((T, H), generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn((E, H), generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    bias = (torch.randn(E, generator=g) * 0.01).to(dev)
+    K = 8
+    out = [torch.empty((T, E), device=dev), torch.empty((T, K), dtype=torch.int32, device=dev),
+           torch.empty((T, K), device=dev)]
+    say(f"router matrix cores: E={E} H={H} T={T}")
+    lib.router_topk(x, w, bias, K, out[0], out[1], out[2])
+    ref = [torch.empty_like(t) for t in out]
+    for t0 in range(0, T, 40):                    # pieces of at most 40 tokens
+        t1 = min(T, t0 + 40)
+        parts = [r[t0:t1] for r in ref]
+        lib.router_topk(x[t0:t1], w, bias, K, *parts)
+    torch.cuda.synchronize()
+    for a, b, name in zip(out, ref, ("logits", "ids", "weights")):
+        assert torch.equal(a, b), name
+    o_ids, _, _ = orouter.route(x.float().cpu().numpy(), w.float().cpu().numpy(), K,
+                                bias=bias.cpu().numpy())
+    assert np.array_equal(out[1].cpu().numpy(), o_ids)
