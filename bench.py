@@ -154,6 +154,43 @@ def link_peak(pools, dev, chunk_mib: int = 256, reps: int = 8) -> float:
     return len(srcs) * nb / (a.elapsed_time(b) / 1000.0) / 1e9
 
 
+def fetch_vram_control(lib, pool, dev, jobs: int = 8, reps: int = 160, bpj: int = 3) -> dict:
+    """The kernel-quality control of the reference's fetch benchmark: the
+    same fetch launches (8 distinct records) reading a copy of the pool in
+    HBM instead of page-locked host memory, at the host fetch's grid and at
+    64 workgroups per job, so that the link, not the kernel, is shown to
+    bound the host fetch.  Returns GB/s and the launch time of each; the
+    last launch of each is checked byte for byte."""
+    import numpy as np
+    import torch
+    RB = pool.layout.record_bytes
+    src = pool.tensor.to(dev)                       # 256 records in HBM (805 MB)
+    cache = torch.zeros((jobs, RB), dtype=torch.uint8, device=dev)
+    rng = np.random.default_rng(17)
+    lists = torch.tensor(np.stack([rng.choice(pool.n, jobs, replace=False) for _ in range(reps)]),
+                         dtype=torch.int32, device=dev)
+    fslot = torch.arange(jobs, dtype=torch.int32, device=dev)
+    nmiss = torch.tensor([jobs], dtype=torch.int32, device=dev)
+    pair = [(src.data_ptr(), cache.data_ptr(), RB)]
+    res = {"what": f"fetch_kernel, {jobs} records per launch read from a copy of the pool in "
+                   "HBM instead of page-locked host memory; a graph of "
+                   f"{reps} launches (the reference's VRAM-source control row), at the host "
+                   f"fetch's {bpj} workgroups per job and at 64"}
+    for w in (bpj, 64):
+        dt = graph_time(dev, lambda r: lib.fetch(pair, lists[r % reps], fslot, nmiss, jobs, w),
+                        reps)
+        last = lists[(reps - 1) % reps].tolist()
+        torch.cuda.synchronize()
+        for j, e in enumerate(last):
+            if not torch.equal(cache[j], src[e]):
+                raise RuntimeError(f"VRAM-source fetch verification failed: slot {j} != expert {e}")
+        res[f"workgroups_per_job_{w}"] = {"us_per_launch": round(1e6 * dt, 2),
+                                          "GBps": round(jobs * RB / dt / 1e9, 1)}
+    del src, cache
+    torch.cuda.empty_cache()
+    return res
+
+
 def fetch_standalone(lib, pools, dev, jobs: int = 8, reps: int = 160, bpj: int = 3,
                      coded=None, workgroups: int = 32):
     """Average duration of one fetch launch moving `jobs` distinct records,
@@ -1734,6 +1771,8 @@ def main() -> int:
     fetch_gbs = f_bytes / f_dt / 1e9
     gemv_gbs = g_bytes / g_dt / 1e9
     lists = fetch_lists(lib, pools, dev)
+    vram = fetch_vram_control(lib, pools[0], dev)
+    log(f"fetch kernel from an HBM source (control): {vram}")
     rf = route_fetch_probe(lib, pools[:4], dev)
     log(f"route + fetch + gate/up launch alone: {rf['by_misses']}")
     transfers = transfer_split(lib, pools, dev)
@@ -1884,6 +1923,7 @@ def main() -> int:
             "traffic_note": "HBM bytes per call, PMC, algorithmic 25,180,160",
             "call_us": round(1e6 * g_dt, 3),
         },
+        "fetch_vram_control": vram,
         "fetch_miss_lists_GBps": {"lists": lists,
                                   "what": "Zipf(1.1) miss lists of distinct experts into a "
                                           "128-slot cache, 8 trials each, byte-exact; 256 "
