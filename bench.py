@@ -896,7 +896,11 @@ def prefill_bench(lib, harness, tokens: int = 512, passes: int = 2, coded=None, 
         x.copy_(x0)
         for l in range(L):
             lib.router_topk(x, gate[l], None, K, logits, ids, wts)
-            if from_coded:
+            if from_coded and from_cache:
+                slot_of, cap, cache = hybrid[l]
+                pf.forward(x, ids, wts, None, out=y, residual=x,
+                           cache=(slot_of, cap, [cache.data_ptr()]), coded=coded[l])
+            elif from_coded:
                 pf.forward(x, ids, wts, None, out=y, residual=x, coded=coded[l])
             elif from_cache:
                 slot_of, cap, cache = hybrid[l]
@@ -937,6 +941,13 @@ def prefill_bench(lib, harness, tokens: int = 512, passes: int = 2, coded=None, 
             "ms_per_pass": round(1e3 * h_dt, 3), "tokens_per_s": round(tokens / h_dt, 1),
             "experts_from_cache": round(borrowed / (borrowed + fetched_h), 4),
             "output_equal_raw_pool_pass": bool(torch.equal(x, x_raw))}
+        if coded is not None:
+            ch_dt = timed(True, True)
+            hybrid_res["with_coded_pools"] = {
+                "what": "both: the cache's residents copied on the device, the rest decoded "
+                        "from the coded pools",
+                "ms_per_pass": round(1e3 * ch_dt, 3), "tokens_per_s": round(tokens / ch_dt, 1),
+                "output_equal_raw_pool_pass": bool(torch.equal(x, x_raw))}
     uniq = n_unique.float()
     fetched = float(uniq.sum()) * harness.layout.record_bytes
     finite = bool(torch.isfinite(x.float()).all())
