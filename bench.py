@@ -1838,6 +1838,19 @@ def main() -> int:
     dt0 = timed_replays(h0c, args.steps)
     tps_nocache = args.steps / dt0
     log(f"0% hit: {tps_nocache:.2f} tok/s, {1e3 * dt0 / args.steps:.3f} ms/step")
+    # the same in the separate launches (router top-k, fetch of the ids into
+    # slots 0..7, the FFN's two): the fused form's gain, and its output
+    h0s = decode.DecodeHarness(decode.DecodeConfig(**{**cfg0.__dict__, "fused_fetch": False}),
+                               dev, pools=pools)
+    h0s.capture()
+    h0s.replay(args.warmup)
+    dt0s = timed_replays(h0s, args.steps)
+    same0 = bool(torch.equal(h0s.x, h0c.x)) and h0s.cursor == h0c.cursor
+    h0s.graph = None
+    h0s.pools = []
+    del h0s
+    torch.cuda.empty_cache()
+    log(f"0% hit, separate launches: {args.steps / dt0s:.2f} tok/s, output equal: {same0}")
 
     prefill = resident = None
     if not args.no_extra:
@@ -1880,6 +1893,13 @@ def main() -> int:
         "hit_rate_simulated": round(sim_hit, 4) if sim_hit == sim_hit else None,
         "tokens_per_s_0pct_hit": round(tps_nocache, 3),
         "ms_per_step_0pct_hit": round(1e3 * dt0 / args.steps, 4),
+        "zero_hit_separate_launches": {
+            "what": "the 0 % hit step with the router top-k, the fetch and the FFN's gate/up "
+                    "as separate launches (five per layer instead of three)",
+            "tokens_per_s": round(args.steps / dt0s, 3),
+            "ms_per_step": round(1e3 * dt0s / args.steps, 4),
+            "x_equal_fused_step": same0,
+        },
         "fetch_bytes_per_step": int(miss_bytes_per_step),
         "effective_fetch_GBps_in_step": round(miss_bytes_per_step * tps_cached / 1e9, 3),
         "roofline": {

@@ -71,7 +71,10 @@ struct StepGeom {
 
 __device__ __forceinline__ int32_t uniform(int32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 
-template <int PER, int PERC>
+// UNCACHED (moe_route_fetch_ffn_uncached): no slot table; every pick is a
+// miss fetched into slot k (its place in the top-k), so the grid has no hit
+// workgroups and the table arguments are unused.
+template <bool UNCACHED, int PER, int PERC>
 __global__ __launch_bounds__(kStepThreads) void route_fetch_gateup_kernel(
     StepGeom g, const uint16_t* __restrict__ x, const float* __restrict__ logits,
     int32_t n_experts, int32_t top_k, int32_t* __restrict__ ids, float* __restrict__ weights,
@@ -80,7 +83,7 @@ __global__ __launch_bounds__(kStepThreads) void route_fetch_gateup_kernel(
     int32_t* __restrict__ out_slot, int32_t* __restrict__ fetch_slot,
     int32_t* __restrict__ fetch_expert, int32_t* __restrict__ nmiss_ptr,
     int64_t* __restrict__ stats, float* __restrict__ act, SharedRefs sh) {
-  const int first_shared = g.nfetch + top_k * g.units;
+  const int first_shared = g.nfetch + (UNCACHED ? 0 : top_k * g.units);
   if (static_cast<int>(blockIdx.x) >= first_shared) {
     // shared expert rows j0, j0 + 1 of this wave (gate and up each; row Is
     // is the sigmoid gate), the token's x; no barrier on this branch
@@ -120,9 +123,14 @@ __global__ __launch_bounds__(kStepThreads) void route_fetch_gateup_kernel(
   const int q = lane >> 4;
   int32_t slot_r;
   bool miss_r;
-  route_wave<PER, PERC>(logits, n_experts, top_k, ids, weights, slot_of, slot_expert, stamp, cap,
-                        step_ptr, out_slot, fetch_slot, fetch_expert, nmiss_ptr, stats, job_e,
-                        job_s, job_k, &job_n, slot_r, miss_r);
+  if constexpr (UNCACHED)
+    route_wave_uncached<PER>(logits, n_experts, top_k, ids, weights, out_slot, fetch_slot,
+                             fetch_expert, nmiss_ptr, stats, job_e, job_s, job_k, &job_n, slot_r,
+                             miss_r);
+  else
+    route_wave<PER, PERC>(logits, n_experts, top_k, ids, weights, slot_of, slot_expert, stamp,
+                          cap, step_ptr, out_slot, fetch_slot, fetch_expert, nmiss_ptr, stats,
+                          job_e, job_s, job_k, &job_n, slot_r, miss_r);
   if (wave == 0 && lane < top_k) pick_slot[lane] = miss_r ? -1 : slot_r;
   if (wave == 1) {
     // x -> e4m3 codes + per-128 scales in LDS while the first wave routes:
@@ -140,7 +148,7 @@ __global__ __launch_bounds__(kStepThreads) void route_fetch_gateup_kernel(
   }
   __syncthreads();
   const int I = g.inter;
-  if (static_cast<int>(blockIdx.x) >= g.nfetch) {
+  if (!UNCACHED && static_cast<int>(blockIdx.x) >= g.nfetch) {
     // hit workgroup (pick k, unit t): gate rows 16t.. (first wave), up rows
     // I + 16t.. (second wave) from the pick's cache slot
     const int hb = static_cast<int>(blockIdx.x) - g.nfetch;
@@ -692,50 +700,47 @@ extern "C" int moe_time_fused_launch(void* start, void* stop) {
   return MOE_OK;
 }
 
-extern "C" int moe_route_fetch_ffn(const void* x, const void* w, const float* bias,
-                                   int32_t logit_dtype, int32_t hidden, int32_t n_experts,
-                                   int32_t top_k, float* logits, int32_t* ids, float* weights,
-                                   int32_t* slot_of, int32_t* slot_expert, int64_t* slot_stamp,
-                                   int32_t cap, int64_t* step, int32_t* out_slot,
-                                   int32_t* fetch_slot, int32_t* fetch_expert, int32_t* nmiss,
-                                   int64_t* stats, const void* pool, void* cache,
-                                   int64_t record_bytes, int32_t inter, int32_t blocks_per_job,
-                                   const moe_shared_expert* shared, const void* residual,
-                                   void* out, void* workspace, size_t workspace_bytes,
-                                   void* stream) {
+// moe_route_fetch_ffn and, with no slot table (slot_of, slot_expert,
+// slot_stamp and step NULL), moe_route_fetch_ffn_uncached: the checks and
+// the three launches.
+static int route_fetch_ffn_impl(const char* fn, bool uncached, const void* x, const void* w,
+                                const float* bias, int32_t logit_dtype, int32_t hidden,
+                                int32_t n_experts, int32_t top_k, float* logits, int32_t* ids,
+                                float* weights, int32_t* slot_of, int32_t* slot_expert,
+                                int64_t* slot_stamp, int32_t cap, int64_t* step,
+                                int32_t* out_slot, int32_t* fetch_slot, int32_t* fetch_expert,
+                                int32_t* nmiss, int64_t* stats, const void* pool, void* cache,
+                                int64_t record_bytes, int32_t inter, int32_t blocks_per_job,
+                                const moe_shared_expert* shared, const void* residual, void* out,
+                                void* workspace, size_t workspace_bytes, void* stream) {
   hipEvent_t ev0, ev1;
   take_fused_events(ev0, ev1);
-  MOE_REQUIRE(x && w && logits && ids && weights && slot_of && slot_expert && slot_stamp && step &&
-                  out_slot && fetch_slot && fetch_expert && nmiss && pool && cache && out &&
-                  workspace,
-              "moe_route_fetch_ffn: NULL pointer");
+  MOE_REQUIRE(x && w && logits && ids && weights && out_slot && fetch_slot && fetch_expert &&
+                  nmiss && pool && cache && out && workspace,
+              "%s: NULL pointer", fn);
+  MOE_REQUIRE(uncached || (slot_of && slot_expert && slot_stamp && step), "%s: NULL pointer", fn);
   MOE_REQUIRE(logit_dtype == MOE_F32 || logit_dtype == MOE_BF16,
-              "moe_route_fetch_ffn: logit_dtype must be MOE_F32 or MOE_BF16");
+              "%s: logit_dtype must be MOE_F32 or MOE_BF16", fn);
   MOE_REQUIRE(hidden >= 512 && hidden % 512 == 0 && hidden <= kGemvMaxHidden,
-              "moe_route_fetch_ffn: hidden must be a multiple of 512 up to %d (got %d)",
-              kGemvMaxHidden, hidden);
+              "%s: hidden must be a multiple of 512 up to %d (got %d)", fn, kGemvMaxHidden, hidden);
   MOE_REQUIRE(inter >= 128 && inter % 128 == 0 && inter <= kGemvMaxInter,
-              "moe_route_fetch_ffn: inter must be a multiple of 128 up to %d (got %d)",
-              kGemvMaxInter, inter);
+              "%s: inter must be a multiple of 128 up to %d (got %d)", fn, kGemvMaxInter, inter);
   MOE_REQUIRE(top_k >= 1 && top_k <= kGemvMaxTopK && top_k <= n_experts && n_experts <= 1024,
-              "moe_route_fetch_ffn: need 1 <= top_k <= min(%d, n_experts), n_experts <= 1024",
-              kGemvMaxTopK);
-  MOE_REQUIRE(cap >= 1 && cap <= 1024, "moe_route_fetch_ffn: need 1 <= cap <= 1024");
-  MOE_REQUIRE(top_k <= cap, "moe_route_fetch_ffn: top_k (%d) exceeds the cache capacity (%d)",
-              top_k, cap);
+              "%s: need 1 <= top_k <= min(%d, n_experts), n_experts <= 1024", fn, kGemvMaxTopK);
+  MOE_REQUIRE(cap >= 1 && cap <= 1024, "%s: need 1 <= cap <= 1024", fn);
+  MOE_REQUIRE(top_k <= cap, "%s: top_k (%d) exceeds the cache capacity (%d)", fn, top_k, cap);
   const int64_t w13 = 2LL * inter * hidden;
   const int64_t off_s13 = w13 + static_cast<int64_t>(hidden) * inter;
   const int64_t off_s2 = off_s13 + (2LL * inter / 128) * (hidden / 128) * 4;
   const int64_t payload = off_s2 + (static_cast<int64_t>(hidden) / 128) * (inter / 128) * 4;
   MOE_REQUIRE(record_bytes >= payload && record_bytes % 256 == 0,
-              "moe_route_fetch_ffn: record_bytes (%lld) must hold the %lld-byte record and be a "
-              "multiple of 256",
-              (long long)record_bytes, (long long)payload);
+              "%s: record_bytes (%lld) must hold the %lld-byte record and be a multiple of 256",
+              fn, (long long)record_bytes, (long long)payload);
   MOE_REQUIRE(reinterpret_cast<uintptr_t>(pool) % 256 == 0 &&
                   reinterpret_cast<uintptr_t>(cache) % 256 == 0,
-              "moe_route_fetch_ffn: pool and cache must be 256-byte aligned");
+              "%s: pool and cache must be 256-byte aligned", fn);
   MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0,
-              "moe_route_fetch_ffn: x and w must be 16-byte aligned");
+              "%s: x and w must be 16-byte aligned", fn);
   // workspace: act [top_k, inter] f32 from byte 0; with the shared expert,
   // its act [Is] bf16 and sig f32 after it (moe_fp8_moe_block_forward's
   // layout for one token)
@@ -745,14 +750,14 @@ extern "C" int moe_route_fetch_ffn(const void* x, const void* w, const float* bi
   if (shared) {
     const int32_t Is = shared->inter;
     MOE_REQUIRE(Is >= 128 && Is % 128 == 0,
-                "moe_route_fetch_ffn: shared inter must be a positive multiple of 128");
+                "%s: shared inter must be a positive multiple of 128", fn);
     MOE_REQUIRE(shared->w_gate && shared->w_up && shared->w_down && shared->w_sgate,
-                "moe_route_fetch_ffn: NULL shared expert weight");
+                "%s: NULL shared expert weight", fn);
     MOE_REQUIRE(reinterpret_cast<uintptr_t>(shared->w_gate) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(shared->w_up) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(shared->w_down) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(shared->w_sgate) % 16 == 0,
-                "moe_route_fetch_ffn: shared expert weights must be 16-byte aligned");
+                "%s: shared expert weights must be 16-byte aligned", fn);
     need = moe_fp8_moe_block_workspace(1, top_k, cap, hidden, inter, Is);
     char* ws = static_cast<char*>(workspace);
     sh = SharedRefs{static_cast<const uint16_t*>(shared->w_gate),
@@ -764,11 +769,10 @@ extern "C" int moe_route_fetch_ffn(const void* x, const void* w, const float* bi
                                                           ~size_t{255}))};
   }
   MOE_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0 && workspace_bytes >= need,
-              "moe_route_fetch_ffn: the workspace must be 256-byte aligned and hold %zu bytes "
-              "(%zu given)",
+              "%s: the workspace must be 256-byte aligned and hold %zu bytes (%zu given)", fn,
               need, workspace_bytes);
   MOE_REQUIRE(blocks_per_job >= 1 && blocks_per_job <= 4096,
-              "moe_route_fetch_ffn: need 1 <= blocks_per_job <= 4096");
+              "%s: need 1 <= blocks_per_job <= 4096", fn);
   hipStream_t s = as_stream(stream);
   int rc = launch_decode_logits(x, w, bias, hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0,
                                 logits, step, s);
@@ -787,20 +791,23 @@ extern "C" int moe_route_fetch_ffn(const void* x, const void* w, const float* bi
   g.plain = static_cast<int32_t>((record_bytes - w13 + kPieceBytes - 1) / kPieceBytes);
   g.nfetch = blocks_per_job * (top_k < kFetchMaxJobsInGrid ? top_k : kFetchMaxJobsInGrid);
   const int nshared = shared ? (shared->inter + 1 + 2 * kSharedJPW - 1) / (2 * kSharedJPW) : 0;
-  const unsigned grid = static_cast<unsigned>(g.nfetch + top_k * g.units + nshared);
+  const unsigned grid =
+      static_cast<unsigned>(g.nfetch + (uncached ? 0 : top_k * g.units) + nshared);
   float* act = static_cast<float*>(workspace);
-#define MOE_RFG(PE, PC)                                                                        \
-  hipExtLaunchKernelGGL((route_fetch_gateup_kernel<PE, PC>), dim3(grid), dim3(kStepThreads), 0,  \
-                        s, ev0, ev1, 0, g, static_cast<const uint16_t*>(x), logits, n_experts,   \
+#define MOE_RFG(U, PE, PC)                                                                     \
+  hipExtLaunchKernelGGL((route_fetch_gateup_kernel<U, PE, PC>), dim3(grid), dim3(kStepThreads),  \
+                        0, s, ev0, ev1, 0, g, static_cast<const uint16_t*>(x), logits, n_experts, \
                         top_k, ids, weights, slot_of, slot_expert, slot_stamp, cap, step,        \
                         out_slot, fetch_slot, fetch_expert, nmiss, stats, act, sh)
-  if (n_experts <= 256) {
-    if (cap <= 256) MOE_RFG(4, 4); else MOE_RFG(4, 16);
+  if (uncached) {
+    if (n_experts <= 256) MOE_RFG(true, 4, 4); else MOE_RFG(true, 16, 4);
+  } else if (n_experts <= 256) {
+    if (cap <= 256) MOE_RFG(false, 4, 4); else MOE_RFG(false, 4, 16);
   } else {
-    if (cap <= 256) MOE_RFG(16, 4); else MOE_RFG(16, 16);
+    if (cap <= 256) MOE_RFG(false, 16, 4); else MOE_RFG(false, 16, 16);
   }
 #undef MOE_RFG
-  rc = check_launch("moe_route_fetch_ffn(route+fetch+gate/up)");
+  rc = check_launch(fn);
   if (rc) return rc;
   const uint8_t* cb = static_cast<const uint8_t*>(cache);
   return launch_down_gemv(act, out_slot, weights, 0, 1, top_k, cb + w13,
@@ -808,6 +815,38 @@ extern "C" int moe_route_fetch_ffn(const void* x, const void* w, const float* bi
                           record_bytes / 4, MOE_LAYOUT_TILES, cap, hidden, inter,
                           static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out),
                           shared ? &sh : nullptr, s);
+}
+
+extern "C" int moe_route_fetch_ffn(const void* x, const void* w, const float* bias,
+                                   int32_t logit_dtype, int32_t hidden, int32_t n_experts,
+                                   int32_t top_k, float* logits, int32_t* ids, float* weights,
+                                   int32_t* slot_of, int32_t* slot_expert, int64_t* slot_stamp,
+                                   int32_t cap, int64_t* step, int32_t* out_slot,
+                                   int32_t* fetch_slot, int32_t* fetch_expert, int32_t* nmiss,
+                                   int64_t* stats, const void* pool, void* cache,
+                                   int64_t record_bytes, int32_t inter, int32_t blocks_per_job,
+                                   const moe_shared_expert* shared, const void* residual,
+                                   void* out, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  return route_fetch_ffn_impl("moe_route_fetch_ffn", false, x, w, bias, logit_dtype, hidden,
+                              n_experts, top_k, logits, ids, weights, slot_of, slot_expert,
+                              slot_stamp, cap, step, out_slot, fetch_slot, fetch_expert, nmiss,
+                              stats, pool, cache, record_bytes, inter, blocks_per_job, shared,
+                              residual, out, workspace, workspace_bytes, stream);
+}
+
+extern "C" int moe_route_fetch_ffn_uncached(
+    const void* x, const void* w, const float* bias, int32_t logit_dtype, int32_t hidden,
+    int32_t n_experts, int32_t top_k, float* logits, int32_t* ids, float* weights,
+    int32_t cap, int32_t* out_slot, int32_t* fetch_slot, int32_t* fetch_expert, int32_t* nmiss,
+    int64_t* stats, const void* pool, void* cache, int64_t record_bytes, int32_t inter,
+    int32_t blocks_per_job, const moe_shared_expert* shared, const void* residual, void* out,
+    void* workspace, size_t workspace_bytes, void* stream) {
+  return route_fetch_ffn_impl("moe_route_fetch_ffn_uncached", true, x, w, bias, logit_dtype,
+                              hidden, n_experts, top_k, logits, ids, weights, nullptr, nullptr,
+                              nullptr, cap, nullptr, out_slot, fetch_slot, fetch_expert, nmiss,
+                              stats, pool, cache, record_bytes, inter, blocks_per_job, shared,
+                              residual, out, workspace, workspace_bytes, stream);
 }
 
 // The checks moe_fetch_ffn and moe_resolve_fetch_ffn share: the four buffer

@@ -243,4 +243,56 @@ __device__ __forceinline__ void route_wave(
   }
 }
 
+// The uncached route by the first wave of a workgroup (the other threads
+// pass through): the top-k of one token's logits, every pick a miss fetched
+// into slot r (its position in the top-k), with no slot table: the
+// reference's uncached per-expert transfer, every routed expert copied on
+// every call (bin/offload.py:137-239).  The same LDS lists and per-lane
+// returns as route_wave; workgroup 0 writes ids, weights, out_slot (= r),
+// the fetch lists and nmiss (= top_k), and adds top_k misses to stats.
+template <int PER>
+__device__ __forceinline__ void route_wave_uncached(
+    const float* __restrict__ logits, int32_t n_experts, int32_t top_k,
+    int32_t* __restrict__ ids, float* __restrict__ weights, int32_t* __restrict__ out_slot,
+    int32_t* __restrict__ fetch_slot, int32_t* __restrict__ fetch_expert,
+    int32_t* __restrict__ nmiss_ptr, int64_t* __restrict__ stats, int32_t* job_e,
+    int32_t* job_s, int32_t* job_k, int32_t* job_n, int32_t& slot_r, bool& miss_r) {
+  slot_r = -1;
+  miss_r = false;
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    StatsPrefetch prev;
+    prev.load(stats);
+    float lv[PER];
+    load_logits<PER>(logits, n_experts, lv);
+    int32_t id;
+    float wt;
+    wave_topk_of<PER>(lv, n_experts, top_k, &id, &wt);
+    if (lane < top_k) {
+      job_e[lane] = id;
+      job_s[lane] = lane;
+      if (job_k) job_k[lane] = lane;
+      slot_r = lane;
+      miss_r = true;
+    }
+    if (lane == 0) *job_n = top_k;
+    if (blockIdx.x == 0) {
+      if (lane < top_k) {
+        ids[lane] = id;
+        weights[lane] = wt;
+        out_slot[lane] = lane;
+        fetch_expert[lane] = id;
+        fetch_slot[lane] = lane;
+      }
+      if (lane == 0) {
+        *nmiss_ptr = top_k;
+        if (stats) {
+          stats[0] = prev.hits;
+          stats[1] = prev.misses + top_k;
+        }
+      }
+    }
+  }
+}
+
 }  // namespace moe

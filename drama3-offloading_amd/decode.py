@@ -39,7 +39,10 @@ replay.
 
 mode "cached": per-layer cache of `capacity` packed records, LRU on device.
 mode "nocache": every routed expert is fetched on every step (0 % hit; the
-reference's uncached per-expert transfer), into 8 fixed slots.
+reference's uncached per-expert transfer), into 8 fixed slots: the router,
+the fetch and the gate/up in one launch as on the cached path
+(moe_route_fetch_ffn_uncached), or with fused_fetch off, moe_router_topk +
+moe_fetch + moe_fp8_moe_forward.
 
 With `coded_pool`, each layer's records are also held entropy-coded in host
 memory (codec.CodedPool) and the fetch decodes them into the same cache
@@ -205,6 +208,12 @@ class DecodeHarness:
         # ... and the FFN with it (raw packed tile-ordered records)
         self.fused_ffn = (self.fused and self.coded is None and cfg.fused_ffn and
                           self.layout.tiled and cfg.hidden % 512 == 0 and cfg.top_k <= 16)
+        # at 0 % hit: the same three launches with no slot table
+        # (moe_route_fetch_ffn_uncached), every pick fetched into slot k; no
+        # hit/miss counts at 0 % hit, as on the separate launches
+        self.fused_uncached = (cfg.mode == "nocache" and cfg.fused_fetch and cfg.fused_ffn and
+                               self.coded is None and self.layout.tiled and
+                               cfg.hidden % 512 == 0 and cfg.top_k <= 16)
         if cfg.shared_expert:
             # seeded bf16 shared experts, resident (6 MiB per layer at 2048 x 512)
             g2 = torch.Generator(device=dev).manual_seed(cfg.seed + 3)
@@ -280,6 +289,16 @@ class DecodeHarness:
                                 residual=self.h, stats=self.stats[l],
                                 logit_dtype=cfg.router_logits,
                                 shared=self.shared(l) if cfg.shared_expert else None)
+            return
+        if self.fused_uncached:
+            lib.route_fetch_ffn_uncached(self.h, self.gate[l], self.bias_live[l], cfg.top_k,
+                                         self.logits[l], self.ids[l], self.wts[l],
+                                         self.out_slot[l], self.fslot[l], self.fexp[l],
+                                         self.nmiss[l], self.pools[l].dev_ptr, self.cache[l],
+                                         cfg.inter, cfg.ffn_blocks_per_job, self.x,
+                                         self.ws_block if cfg.shared_expert else self.ws,
+                                         residual=self.h, logit_dtype=cfg.router_logits,
+                                         shared=self.shared(l) if cfg.shared_expert else None)
             return
         if self.fused and self.coded is not None:
             # router, then resolve + decode of the misses' coded records

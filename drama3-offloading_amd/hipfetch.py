@@ -108,6 +108,10 @@ SIGNATURES = {
                                       _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                       _vp, C.c_int64, _i32, _i32, C.POINTER(SharedExpert), _vp,
                                       _vp, _vp, _sz, _vp]),
+    "moe_route_fetch_ffn_uncached": (C.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp,
+                                               _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                               C.c_int64, _i32, _i32, C.POINTER(SharedExpert),
+                                               _vp, _vp, _vp, _sz, _vp]),
     "moe_fetch_ffn": (C.c_int, [C.POINTER(FetchPair), _i32, _vp, _vp, _vp, _i32, _i32, _vp,
                                 _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _i32,
                                 C.POINTER(ExpertStrides), _vp, _vp, _vp, _sz, _vp]),
@@ -464,21 +468,7 @@ class Native:
         if cache.dim() != 2 or cache.dtype != torch.uint8 or not cache.is_contiguous() \
                 or cache.shape[0] < C_:
             raise ValueError(f"{what}: cache must be contiguous uint8 [>= {C_}, record_bytes]")
-        self._buf(what, "out", out, H, torch.bfloat16)
-        self._buf(what, "residual", residual, H, torch.bfloat16)
-        self._buf(what, "workspace", workspace, 0)
-        se = None
-        if shared is not None:
-            wg, wu, wd, wsg = shared
-            self._on_gpu(what, x, *shared)
-            Is = wg.shape[0]
-            if wg.shape != (Is, H) or wu.shape != (Is, H) or wd.shape != (H, Is) \
-                    or wsg.numel() != H:
-                raise ValueError(f"{what}: shared expert weights do not match x")
-            for name, t in zip(("w_gate", "w_up", "w_down", "w_sgate"), shared):
-                self._buf(what, name, t, t.numel(), torch.bfloat16)
-            se = C.byref(SharedExpert(wg.data_ptr(), wu.data_ptr(), wd.data_ptr(),
-                                      wsg.data_ptr(), Is))
+        se = self._ffn_tail(what, x, H, out, residual, workspace, shared)
         self._check(self.cdll.moe_route_fetch_ffn(
             x.data_ptr(), w.data_ptr(), self._ptr(bias), self._logit_code(logit_dtype), H, E,
             top_k, logits.data_ptr(), ids.data_ptr(), weights.data_ptr(), slot_of.data_ptr(),
@@ -487,6 +477,60 @@ class Native:
             pool_dev_ptr, cache.data_ptr(), cache.shape[1], inter, blocks_per_job, se,
             self._ptr(residual), out.data_ptr(), workspace.data_ptr(),
             workspace.numel() * workspace.element_size(), self.stream()), what)
+
+    def route_fetch_ffn_uncached(self, x, w, bias, top_k: int, logits, ids, weights, out_slot,
+                                 fetch_slot, fetch_expert, nmiss, pool_dev_ptr: int, cache,
+                                 inter: int, blocks_per_job: int, out, workspace, residual=None,
+                                 stats=None, logit_dtype: str = "bf16", shared=None) -> None:
+        """route_fetch_ffn with no cache policy (moe_route_fetch_ffn_uncached):
+        every routed expert fetched into cache slot k (its place in the
+        top-k) on every call; out_slot = 0..top_k-1, the miss list = ids."""
+        import torch
+        if x.shape[0] != 1:
+            raise ValueError("route_fetch_ffn_uncached takes exactly one token")
+        what = "moe_route_fetch_ffn_uncached"
+        self._on_gpu(what, x, w, bias, logits, ids, weights, out_slot, fetch_slot, fetch_expert,
+                     nmiss, stats, cache, out, workspace, residual)
+        H, E = self._router_bufs(what, x, w, bias, logits, 1, top_k)
+        i32 = torch.int32
+        for name, t, n, dt in (("ids", ids, top_k, i32), ("weights", weights, top_k, torch.float32),
+                               ("out_slot", out_slot, top_k, i32),
+                               ("fetch_slot", fetch_slot, top_k, i32),
+                               ("fetch_expert", fetch_expert, top_k, i32),
+                               ("nmiss", nmiss, 1, i32), ("stats", stats, 2, torch.int64)):
+            self._buf(what, name, t, n, dt)
+        if cache.dim() != 2 or cache.dtype != torch.uint8 or not cache.is_contiguous():
+            raise ValueError(f"{what}: cache must be contiguous uint8 [slots, record_bytes]")
+        se = self._ffn_tail(what, x, H, out, residual, workspace, shared)
+        self._check(self.cdll.moe_route_fetch_ffn_uncached(
+            x.data_ptr(), w.data_ptr(), self._ptr(bias), self._logit_code(logit_dtype), H, E,
+            top_k, logits.data_ptr(), ids.data_ptr(), weights.data_ptr(), cache.shape[0],
+            out_slot.data_ptr(), fetch_slot.data_ptr(), fetch_expert.data_ptr(),
+            nmiss.data_ptr(), self._ptr(stats), pool_dev_ptr, cache.data_ptr(), cache.shape[1],
+            inter, blocks_per_job, se, self._ptr(residual), out.data_ptr(),
+            workspace.data_ptr(), workspace.numel() * workspace.element_size(), self.stream()),
+            what)
+
+    def _ffn_tail(self, what, x, H, out, residual, workspace, shared):
+        """The output, residual and workspace buffers of the fused step, and
+        the shared expert (w_gate [Is, H], w_up [Is, H], w_down [H, Is],
+        w_sgate [H] bf16, or None) as a moe_shared_expert reference."""
+        import torch
+        self._buf(what, "out", out, H, torch.bfloat16)
+        self._buf(what, "residual", residual, H, torch.bfloat16)
+        self._buf(what, "workspace", workspace, 0)
+        if shared is None:
+            return None
+        wg, wu, wd, wsg = shared
+        self._on_gpu(what, x, *shared)
+        Is = wg.shape[0]
+        if wg.shape != (Is, H) or wu.shape != (Is, H) or wd.shape != (H, Is) \
+                or wsg.numel() != H:
+            raise ValueError(f"{what}: shared expert weights do not match x")
+        for name, t in zip(("w_gate", "w_up", "w_down", "w_sgate"), shared):
+            self._buf(what, name, t, t.numel(), torch.bfloat16)
+        return C.byref(SharedExpert(wg.data_ptr(), wu.data_ptr(), wd.data_ptr(), wsg.data_ptr(),
+                                    Is))
 
     def fetch_ffn(self, pairs, fetch_expert, fetch_slot, nmiss, max_jobs: int,
                   blocks_per_job: int, x, slots, weights, w13, s13, w2, s2, out, workspace,

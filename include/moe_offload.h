@@ -283,6 +283,29 @@ int moe_route_fetch_ffn(const void* x, const void* w, const float* bias, int32_t
                         const struct moe_shared_expert* shared, const void* residual, void* out,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* moe_route_fetch_ffn with no cache policy: every routed expert is a miss,
+ * fetched on every call into cache slot k, its place in the top-k (0-hit
+ * decode; the cache holds cap >= top_k slots).  There is no slot table;
+ * out_slot[k] = k, the miss list is fetch_expert = ids and fetch_slot[k] = k
+ * with *nmiss = top_k, and stats (nullable) gains top_k misses.  The three
+ * launches, the other arguments and the outputs are moe_route_fetch_ffn's:
+ * with every pick a miss, the step's output, ids, weights and slot bytes
+ * equal moe_router_topk + moe_fetch of ids into slots 0..top_k-1 +
+ * moe_fp8_moe_forward_ex (or moe_fp8_moe_block_forward with `shared`) bit
+ * for bit.  Replaces the uncached offloaded_forward's router top-k,
+ * per-expert host-to-device copies and fp8_moe_forward
+ * (bin/offload.py:137-239) for one decode token; no single counterpart. */
+int moe_route_fetch_ffn_uncached(const void* x, const void* w, const float* bias,
+                                 int32_t logit_dtype, int32_t hidden, int32_t n_experts,
+                                 int32_t top_k, float* logits, int32_t* ids, float* weights,
+                                 int32_t cap, int32_t* out_slot, int32_t* fetch_slot,
+                                 int32_t* fetch_expert, int32_t* nmiss, int64_t* stats,
+                                 const void* pool, void* cache, int64_t record_bytes,
+                                 int32_t inter, int32_t blocks_per_job,
+                                 const struct moe_shared_expert* shared, const void* residual,
+                                 void* out, void* workspace, size_t workspace_bytes,
+                                 void* stream);
+
 /* The drop-in's fetch and expert FFN of one token: moe_fetch of the four
  * buffers (pairs in the order w13, w2, s13, s2, as the reference's
  * _cpp_fetch copies them, w13 and w2 with tile_k set so the cache holds

@@ -1,8 +1,10 @@
 """moe_route_fetch, the decode step's router + resolve + fetch in two
 launches, against moe_route_resolve followed by moe_fetch (three launches),
 moe_route_fetch_ffn (the same with the expert FFN, three launches)
-against those and the FFN's own two, and moe_route_fetch_coded (the route
-in the coded fetch's launch) against moe_route_resolve + moe_fetch_coded,
+against those and the FFN's own two, moe_route_fetch_ffn_uncached (its
+0 %-hit form) against moe_router_topk + moe_fetch + the FFN, and
+moe_route_fetch_coded (the route in the coded fetch's launch) against
+moe_route_resolve + moe_fetch_coded,
 at Drama-3 shape (256 experts, top-8, H 2048, I 512) and two others (320
 experts, top-12, 272 slots; 64 experts, top-4, 5 slots) over 3 layers and
 popularity drifts: two harnesses on the same pools, one per path, step for
@@ -189,6 +191,74 @@ def test_route_fetch_coded_equals_route_resolve_then_fetch_coded(lib, dev, shape
         say(f"route_fetch_coded: replay {s}")
         _same(fused, plain, f"replay {s}")
     plain.pools, plain.coded = [], None  # owned by the fused harness
+    fused.close()
+
+
+@pytest.mark.parametrize("shape", [
+    dict(),
+    # 12 jobs over the grid's 8, the 16-per-lane expert registers (E > 256)
+    dict(n_experts=320, top_k=12, hidden=512, inter=256, ffn_blocks_per_job=2),
+    dict(n_experts=64, top_k=4, hidden=512, inter=128, ffn_blocks_per_job=1),
+    # the MoE block: the shared expert's rows beside the fetch
+    dict(n_experts=64, top_k=4, hidden=512, inter=128, shared_expert=True, shared_inter=256),
+], ids=["drama3", "wide", "tight", "block"])
+def test_route_fetch_ffn_uncached_equals_separate_launches(lib, dev, shape):
+    """moe_route_fetch_ffn_uncached (0 % hit: every pick fetched into slot
+    k, three launches) against moe_router_topk + moe_fetch of the ids into
+    slots 0..top_k-1 + moe_fp8_moe_forward (block_forward with the shared
+    expert): step outputs, router outputs and every cache slot equal step
+    for step, eager and replayed; the fused path's miss lists are the ids
+    in slots 0..top_k-1 and its counters, when given, count every pick a
+    miss."""
+    import decode
+    base = dict(layers=3, drift_every=3, schedule_steps=12, mode="nocache", **shape)
+    fused = decode.DecodeHarness(decode.DecodeConfig(**base), dev)
+    plain = decode.DecodeHarness(decode.DecodeConfig(**base, fused_fetch=False), dev,
+                                 pools=fused.pools)
+    assert fused.fused_uncached and not plain.fused_uncached and not plain.fused
+    K = fused.cfg.top_k
+    ar = torch.arange(K, dtype=torch.int32, device=dev)
+
+    def same(tag):
+        assert torch.equal(fused.x, plain.x), f"{tag}: step output"
+        assert torch.equal(fused.ids, plain.ids) and torch.equal(fused.wts, plain.wts), tag
+        for l in range(fused.cfg.layers):
+            assert torch.equal(fused.cache[l], plain.cache[l]), f"{tag} layer {l}: cache"
+            assert torch.equal(fused.out_slot[l].view(-1), ar), f"{tag} layer {l}: out_slot"
+            assert torch.equal(fused.fslot[l], ar), f"{tag} layer {l}: fetch_slot"
+            assert torch.equal(fused.fexp[l], fused.ids[l].view(-1)), f"{tag} layer {l}: fetch"
+            assert int(fused.nmiss[l]) == K, f"{tag} layer {l}: nmiss"
+        if fused.cfg.shared_expert:
+            assert int(fused.finite) == int(plain.finite) == 1
+
+    for s in range(5):
+        for h in (fused, plain):
+            h.stage(s)
+            h.step_eager()
+        torch.cuda.synchronize(dev)
+        say(f"route_fetch_ffn_uncached {shape}: eager step {s}")
+        same(f"eager {s}")
+    for h in (fused, plain):
+        h.capture()
+    for s in range(6):
+        for h in (fused, plain):
+            h.replay(1)
+        torch.cuda.synchronize(dev)
+        say(f"route_fetch_ffn_uncached: replay {s}")
+        same(f"replay {s}")
+    # the counters, when given: every pick a miss, added to what they hold
+    stats = torch.tensor([5, 7], dtype=torch.int64, device=dev)
+    cfg = fused.cfg
+    lib.route_fetch_ffn_uncached(fused.h, fused.gate[0], fused.bias_live[0], K, fused.logits[0],
+                                 fused.ids[0], fused.wts[0], fused.out_slot[0], fused.fslot[0],
+                                 fused.fexp[0], fused.nmiss[0], fused.pools[0].dev_ptr,
+                                 fused.cache[0], cfg.inter, cfg.ffn_blocks_per_job, fused.y,
+                                 fused.ws_block if cfg.shared_expert else fused.ws,
+                                 stats=stats,
+                                 shared=fused.shared(0) if cfg.shared_expert else None)
+    torch.cuda.synchronize(dev)
+    assert stats.tolist() == [5, 7 + K]
+    plain.pools = []                     # owned by the fused harness
     fused.close()
 
 

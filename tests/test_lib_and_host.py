@@ -68,6 +68,22 @@ def test_preconditions_are_rejected_without_launching(lib):
                     (dict(wbytes=8 * 512 * 4 - 4), b"workspace")):
         assert rff(**kw) == -1, msg
         assert msg in c.moe_last_error(), (msg, c.moe_last_error())
+    # its 0 %-hit form: the same checks, no table (a NULL one is no refusal)
+    def rffu(hidden=2048, top_k=8, cap=8, record_bytes=3146496, inter=512, pool=256,
+             ws=1 << 20, wbytes=1 << 20, ids=1):
+        return c.moe_route_fetch_ffn_uncached(16, 16, None, bf16, hidden, 256, top_k, 1, ids, 1,
+                                              cap, 1, 1, 1, 1, None, pool, 256, record_bytes,
+                                              inter, 4, None, None, 256, ws, wbytes, None)
+    for kw, msg in ((dict(hidden=1024 + 256), b"multiple of 512"),
+                    (dict(top_k=17, cap=64), b"top_k"),
+                    (dict(top_k=9, cap=8), b"exceeds the cache capacity"),
+                    (dict(record_bytes=3146496 - 256), b"must hold"),
+                    (dict(pool=264), b"256-byte aligned"),
+                    (dict(wbytes=8 * 512 * 4 - 4), b"workspace"),
+                    (dict(ids=None), b"NULL pointer")):
+        assert rffu(**kw) == -1, msg
+        assert msg in c.moe_last_error(), (msg, c.moe_last_error())
+        assert c.moe_last_error().startswith(b"moe_route_fetch_ffn_uncached:")
     # the coded route + fetch: the route's limits and the coded fetch's record shape
     def rfc(top_k=8, cap=50, n_experts=256, record_bytes=3146496, fp8_bytes=3145728, pool=256,
             slot_bytes=3146496, workgroups=32):
@@ -444,6 +460,29 @@ def test_wrappers_check_buffer_sizes_and_dtypes(lib, monkeypatch):
                        "record_bytes")):
         with pytest.raises(ValueError, match=msg):
             route_fetch_coded(**over)
+
+    def route_fetch_ffn_uncached(**over):
+        a = dict(x=x, w=w, bias=None, top_k=K, logits=torch.zeros(E), ids=i32(K),
+                 weights=torch.zeros(K), out_slot=i32(K), fetch_slot=i32(K),
+                 fetch_expert=i32(K), nmiss=i32(1), pool_dev_ptr=256,
+                 cache=torch.zeros((K, 3146496), dtype=torch.uint8, device="meta"), inter=512,
+                 blocks_per_job=4, out=torch.zeros((1, H), dtype=torch.bfloat16),
+                 workspace=torch.zeros(1 << 16, dtype=torch.uint8))
+        a.update(over)
+        lib.route_fetch_ffn_uncached(**a)
+    with pytest.raises(AssertionError, match="moe_route_fetch_ffn_uncached reached"):
+        route_fetch_ffn_uncached()
+    for over, msg in ((dict(ids=i64(K)), "ids must be int32"),
+                      (dict(out_slot=i32(K - 1)), "out_slot holds 7"),
+                      (dict(nmiss=i32(0)), "nmiss holds 0"),
+                      (dict(stats=i32(2)), "stats must be int64"),
+                      (dict(out=torch.zeros((1, H))), "out must be bfloat16"),
+                      (dict(cache=torch.zeros((K, 3146496), dtype=torch.int8, device="meta")),
+                       "cache must be contiguous uint8"),
+                      (dict(shared=(torch.zeros((256, H), dtype=torch.bfloat16),) * 4),
+                       "shared expert weights do not match")):
+        with pytest.raises(ValueError, match=msg):
+            route_fetch_ffn_uncached(**over)
 
     with pytest.raises(ValueError, match="offsets holds 256 elements, needs 257"):
         lib.permute(i32(4, K), E, i32(E), i32(E), i32(4 * K), i32(4 * K))
