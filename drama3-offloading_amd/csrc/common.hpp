@@ -60,6 +60,14 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 }
 
 // ------------------------------------------------------------ wave utils
+//
+// The DPP exchanges below (quad permutes and row mirrors) read only lanes
+// inside the reading lane's row of 16, so the bound control never applies;
+// they are written with old = 0 and bound_ctrl set, the form the compiler
+// folds into the instruction that consumes the exchange (v_max_u32_dpp,
+// v_add_f32_dpp) instead of a separate copy and DPP move.  An inactive
+// source lane would read as 0 in this form, so every lane of a row of 16
+// (of the wave, for the wave-wide reductions) takes part in each call.
 
 // Max over each row of 16 lanes, in every lane of the row, by DPP exchanges
 // (quad xor 1, quad xor 2, half-row mirror, row mirror): no LDS crossbar, so
@@ -67,8 +75,8 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 // NaN operand in any order, so this equals a shuffle butterfly bit for bit.
 __device__ __forceinline__ float row16_max_f32(float v) {
 #define MOE_DPP_MAX(CTRL)                                                                  \
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), \
-                                                          CTRL, 0xf, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, \
+                                                          true)));
   MOE_DPP_MAX(0x0B1)   // quad_perm [1,0,3,2]
   MOE_DPP_MAX(0x04E)   // quad_perm [2,3,0,1]
   MOE_DPP_MAX(0x141)   // row_half_mirror
@@ -150,6 +158,29 @@ __device__ __forceinline__ float wave_max_f32(float v) {
   return v;
 }
 
+// Wave-wide maximum of a 32-bit unsigned value, returned as a scalar: the
+// row-of-16 DPP exchanges of wave_reduce_u64 on one register, then the
+// four row maxima combined on the scalar unit.  About a third of the
+// 64-bit reduction's instructions.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#define MOE_DPP_UMAX(CTRL)                                                             \
+  {                                                                                    \
+    const uint32_t o = __builtin_amdgcn_update_dpp(0u, v, CTRL, 0xf, 0xf, true);       \
+    v = o > v ? o : v;                                                                 \
+  }
+  MOE_DPP_UMAX(0x0B1)   // quad_perm [1,0,3,2]
+  MOE_DPP_UMAX(0x04E)   // quad_perm [2,3,0,1]
+  MOE_DPP_UMAX(0x141)   // row_half_mirror
+  MOE_DPP_UMAX(0x140)   // row_mirror
+#undef MOE_DPP_UMAX
+  const uint32_t a = __builtin_amdgcn_readlane(static_cast<int>(v), 0);
+  const uint32_t b = __builtin_amdgcn_readlane(static_cast<int>(v), 16);
+  const uint32_t c = __builtin_amdgcn_readlane(static_cast<int>(v), 32);
+  const uint32_t d = __builtin_amdgcn_readlane(static_cast<int>(v), 48);
+  const uint32_t ab = a > b ? a : b, cd = c > d ? c : d;
+  return ab > cd ? ab : cd;
+}
+
 // Wave-wide max / min of a 64-bit key, returned uniform (in every lane):
 // DPP exchanges inside each row of 16 lanes (quad xor 1, quad xor 2, half-row
 // mirror, row mirror), then the four row results are read as scalars.  A
@@ -159,8 +190,8 @@ __device__ __forceinline__ uint64_t wave_reduce_u64(uint64_t v) {
   uint32_t lo = static_cast<uint32_t>(v), hi = static_cast<uint32_t>(v >> 32);
 #define MOE_DPP_STEP(CTRL)                                                             \
   {                                                                                    \
-    const uint32_t olo = __builtin_amdgcn_update_dpp(lo, lo, CTRL, 0xf, 0xf, false);   \
-    const uint32_t ohi = __builtin_amdgcn_update_dpp(hi, hi, CTRL, 0xf, 0xf, false);   \
+    const uint32_t olo = __builtin_amdgcn_update_dpp(0u, lo, CTRL, 0xf, 0xf, true);    \
+    const uint32_t ohi = __builtin_amdgcn_update_dpp(0u, hi, CTRL, 0xf, 0xf, true);    \
     const uint64_t o = (static_cast<uint64_t>(ohi) << 32) | olo;                       \
     const uint64_t c = (static_cast<uint64_t>(hi) << 32) | lo;                         \
     if (kMax ? (o > c) : (o < c)) {                                                    \
@@ -188,8 +219,7 @@ __device__ __forceinline__ uint64_t wave_reduce_u64(uint64_t v) {
 // 16 lanes, then the four row sums read as scalars and added in row order.
 __device__ __forceinline__ float wave_sum_f32_dpp(float v) {
 #define MOE_DPP_ADD(CTRL)                                                                  \
-  v += __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, \
-                                                  0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
   MOE_DPP_ADD(0x0B1)   // quad_perm [1,0,3,2]
   MOE_DPP_ADD(0x04E)   // quad_perm [2,3,0,1]
   MOE_DPP_ADD(0x141)   // row_half_mirror

@@ -21,13 +21,14 @@
 // into LDS.
 //   * fetch workgroups (the first nfetch): the misses' records, cut into
 //     units of 16 intermediate columns (the 16 gate rows and the 16 up rows
-//     of those columns, 2 * H/512 pieces of 8 KiB) and plain 8 KiB pieces
+//     of those columns, 2 * H/512 pieces of 8 KiB) and plain 4 KiB pieces
 //     (w2, the scales).  A unit's pieces go through one workgroup, which
 //     stores them to the cache slot as they arrive and runs the gate/up
 //     MFMAs on the bytes in its registers: the unit ends with the 16
 //     SiLU(gate) * up values of the miss's pick.  Units go round robin over
-//     the workgroups, and plain pieces fill the workgroups with one unit
-//     fewer first, so every workgroup moves the same bytes within a piece.
+//     the workgroups; then each wave takes plain pieces from a counter
+//     until none is left, so the workgroups that receive host bytes sooner
+//     move more of them.
 //   * hit workgroups (top_k * I/16 of them, one per pick and unit): a hit's
 //     16 gate rows (first wave) and 16 up rows (second wave) from its cache
 //     slot; a pick that missed leaves its workgroup idle.
@@ -65,8 +66,9 @@ struct StepGeom {
   int32_t gb;              // K-blocks per row: H / 128
   int32_t kq;              // pieces per 16-row group: H / 512
   int32_t units;           // units per record: I / 16
-  int32_t plain;           // 8 KiB pieces from w13_bytes to the record's end
+  int32_t plain;           // 4 KiB pieces from w13_bytes to the record's end
   int32_t nfetch;          // fetch workgroups (the first of the grid)
+  int32_t* ticket;         // the plain pieces' counter, zeroed by the logits launch
 };
 
 __device__ __forceinline__ int32_t uniform(int32_t v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -194,21 +196,15 @@ __global__ __launch_bounds__(kStepThreads) void route_fetch_gateup_kernel(
     return;
   }
 
-  // fetch workgroup b of G.  Its work is one sequence of 8 KiB pieces:
-  // its units' pieces, unit after unit, then its plain pieces.  Units go
-  // round robin (u = b, b + G, ...); plain pieces go first 8 to each
-  // workgroup with one unit fewer (b >= r, r = U % G), then round robin.
+  // fetch workgroup b of G.  Its units go round robin (u = b, b + G, ...),
+  // as 8 KiB pieces through both waves; then each wave takes the plain
+  // bytes (w2, the scales) 4 KiB at a time by ticket (below).
   const int nm = uniform(job_n);
   const int G = g.nfetch;
   const int b = static_cast<int>(blockIdx.x);
   const int U = nm * g.units;
-  const int P = nm * g.plain;
-  const int r = U % G;
-  const int A = r > 0 ? min(P, 8 * (G - r)) : 0;
   const int np = 2 * g.kq;                   // pieces per unit (even)
   const int nu = U > b ? (U - 1 - b) / G + 1 : 0;
-  const int na = (r > 0 && b >= r && A > b - r) ? (A - 1 - (b - r)) / (G - r) + 1 : 0;
-  const int nb = P > A + b ? (P - 1 - A - b) / G + 1 : 0;
   const int64_t plain_units = (g.rb - g.w13_bytes) >> 4;   // 16-byte units after w13
   // One piece in flight per workgroup, as in the fetch kernel: the next
   // piece's loads go out once this piece has arrived and its stores are
@@ -309,42 +305,49 @@ __global__ __launch_bounds__(kStepThreads) void route_fetch_gateup_kernel(
     }
   }
 
-  // ---- plain pieces: the workgroup's n-th is global plain piece gi, of job
-  // gi / plain; 16-byte unit m * 512 + thread + 128 h after w13, the last
-  // unit again past the record's end (read, never stored)
-  const int npl = na + nb;
-  auto plain_gi = [&](int n) { return n < na ? (b - r) + n * (G - r) : A + b + (n - na) * G; };
-  auto plain_load = [&](int n, u32x4 (&v)[4]) {
-    const int gi = plain_gi(n);
+  // ---- plain bytes, dealt by ticket: each wave takes 4 KiB pieces (64
+  // lanes x 4 x 16 bytes) from the counter the logits launch zeroed, piece
+  // gi of job gi / plain (16-byte unit m * 256 + lane + 64 h after w13, the
+  // last unit again past the record's end, read and never stored), one in
+  // flight, the next ticket requested behind its loads.  Waves whose pieces
+  // arrive sooner take more of them, so the fetch ends within about a piece
+  // of each wave's last: dealt round robin instead, the workgroups on the
+  // XCDs farther from the host link (their first bytes arrive ~3 us later)
+  // finished up to 11 us after the others at 8 misses.
+  const int P = nm * g.plain;
+  auto plain_load = [&](int gi, u32x4 (&v)[4]) {
     const int j = gi / g.plain;
     const int m = gi - j * g.plain;
     const char* src = g.pool + uniform(job_e[j]) * g.rb + g.w13_bytes;
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
-      const int64_t uidx = min(static_cast<int64_t>(m) * (kPieceBytes / 16) + threadIdx.x +
-                                   h * kStepThreads,
-                               plain_units - 1);
+      const int64_t uidx = min(static_cast<int64_t>(m) * 256 + lane + 64 * h, plain_units - 1);
       v[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + uidx * 16));
     }
   };
-  auto plain_store = [&](int n, const u32x4 (&v)[4]) {
-    const int gi = plain_gi(n);
+  auto plain_store = [&](int gi, const u32x4 (&v)[4]) {
     const int j = gi / g.plain;
     const int m = gi - j * g.plain;
     char* dst = g.cache + uniform(job_s[j]) * g.rb + g.w13_bytes;
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
-      const int64_t uidx = static_cast<int64_t>(m) * (kPieceBytes / 16) + threadIdx.x +
-                           h * kStepThreads;
+      const int64_t uidx = static_cast<int64_t>(m) * 256 + lane + 64 * h;
       if (uidx < plain_units) *reinterpret_cast<u32x4*>(dst + uidx * 16) = v[h];
     }
   };
-  // (one piece in flight per workgroup, as in the fetch kernel: with no
-  // MFMAs between a piece's arrival and the next piece's loads, the
-  // fetch's grid keeps the link busy this way)
-  for (int n = 0; n < npl; ++n) {
-    plain_load(n, va);
-    plain_store(n, va);
+  // lane 0's ticket; the other lanes' value is never read
+  auto take = [&]() -> int32_t {
+    int32_t tk = 0;
+    if (lane == 0)
+      tk = __hip_atomic_fetch_add(g.ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return tk;
+  };
+  int32_t tv = take();
+  for (int gi = __builtin_amdgcn_readfirstlane(tv); gi < P;
+       gi = __builtin_amdgcn_readfirstlane(tv)) {
+    plain_load(gi, va);
+    tv = take();
+    plain_store(gi, va);
   }
 }
 
@@ -741,11 +744,14 @@ static int route_fetch_ffn_impl(const char* fn, bool uncached, const void* x, co
               "%s: pool and cache must be 256-byte aligned", fn);
   MOE_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0,
               "%s: x and w must be 16-byte aligned", fn);
-  // workspace: act [top_k, inter] f32 from byte 0; with the shared expert,
-  // its act [Is] bf16 and sig f32 after it (moe_fp8_moe_block_forward's
-  // layout for one token)
+  // workspace: act [top_k, inter] f32 from byte 0, the fetch's piece
+  // counter (int32) at the next 256-byte boundary; with the shared expert,
+  // its act [Is] bf16 and sig f32 after them (moe_fp8_moe_block_forward's
+  // layout for one token, from moe_fp8_moe_workspace(1, ...) >= 8 top_k
+  // inter bytes, past the counter since top_k inter >= 128)
   const size_t base = (moe_fp8_moe_workspace(1, top_k, cap, hidden, inter) + 255) & ~size_t{255};
-  size_t need = static_cast<size_t>(top_k) * inter * sizeof(float);
+  const size_t act_bytes = (static_cast<size_t>(top_k) * inter * sizeof(float) + 255) & ~size_t{255};
+  size_t need = act_bytes + 256;
   SharedRefs sh{};
   if (shared) {
     const int32_t Is = shared->inter;
@@ -774,10 +780,12 @@ static int route_fetch_ffn_impl(const char* fn, bool uncached, const void* x, co
   MOE_REQUIRE(blocks_per_job >= 1 && blocks_per_job <= 4096,
               "%s: need 1 <= blocks_per_job <= 4096", fn);
   hipStream_t s = as_stream(stream);
+  int32_t* ticket = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + act_bytes);
   int rc = launch_decode_logits(x, w, bias, hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0,
-                                logits, step, s);
+                                logits, step, s, ticket);
   if (rc) return rc;
   StepGeom g;
+  g.ticket = ticket;
   g.pool = static_cast<const char*>(pool);
   g.cache = static_cast<char*>(cache);
   g.rb = record_bytes;
@@ -788,7 +796,7 @@ static int route_fetch_ffn_impl(const char* fn, bool uncached, const void* x, co
   g.gb = hidden / 128;
   g.kq = hidden / 512;
   g.units = inter / 16;
-  g.plain = static_cast<int32_t>((record_bytes - w13 + kPieceBytes - 1) / kPieceBytes);
+  g.plain = static_cast<int32_t>((record_bytes - w13 + 4095) / 4096);
   g.nfetch = blocks_per_job * (top_k < kFetchMaxJobsInGrid ? top_k : kFetchMaxJobsInGrid);
   const int nshared = shared ? (shared->inter + 1 + 2 * kSharedJPW - 1) / (2 * kSharedJPW) : 0;
   const unsigned grid =

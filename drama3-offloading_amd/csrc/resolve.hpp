@@ -162,6 +162,54 @@ __device__ __forceinline__ void resolve_chunk(SlotRegs<PER>& t, int32_t my_e, in
 // id r's slot in slot_r (-1 for an id out of range) and miss_r set when id r
 // missed; the misses are appended to job_e / job_s, and their positions r
 // to job_k when it is given, by lane 0.
+//
+// The stamps this call gives are kept as one bit per slot register
+// (`touched`) and written into t.st at the end, and a miss's victim comes
+// from 32-bit keys, (age << 12) | (4095 - slot) with age = step - stamp (0
+// for a slot touched by this call), whose wave maximum is the smallest
+// stamp, lowest slot on a tie.  An age outside [0, kAgeMax) is keyed as
+// kAgeMax; when such a key wins, the victim is taken from the 64-bit
+// stamps instead (take_victim on the stamps as they stand), so the
+// decisions are resolve_chunk's for every table.
+constexpr uint32_t kAgeMax = (1u << 20) - 1;
+
+template <int PER>
+__device__ __forceinline__ int32_t take_victim_age(SlotRegs<PER>& t, const uint32_t (&vkey)[PER],
+                                                   uint32_t touched, int32_t e, int32_t cap,
+                                                   int64_t step, int32_t* victim) {
+  const int lane = threadIdx.x & 63;
+  uint32_t mine = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const uint32_t k = ((touched >> j) & 1u) ? (vkey[j] & 4095u) : vkey[j];
+    mine = k > mine ? k : mine;
+  }
+  const uint32_t m = wave_max_u32(mine);
+  if ((m >> 12) != kAgeMax) {
+    const int32_t s = 4095 - static_cast<int32_t>(m & 4095u);
+    int32_t vloc = -1;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      if (j == (s >> 6)) {
+        vloc = t.se[j];
+        if ((s & 63) == lane) t.se[j] = e;
+      }
+    }
+    *victim = lane_value(vloc, s & 63);
+    return s;
+  }
+  // an age past kAgeMax (or a stamp after the step): the 64-bit stamps,
+  // with this call's stamps applied
+  SlotRegs<PER> u = t;
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+    if ((touched >> j) & 1u) u.st[j] = step;
+  const int32_t s = take_victim(u, e, cap, victim);
+#pragma unroll
+  for (int j = 0; j < PER; ++j) t.se[j] = u.se[j];
+  return s;
+}
+
 template <int PER, int PERC>
 __device__ __forceinline__ void resolve_regs(SlotRegs<PERC>& t, ExpertRegs<PER>& x, int32_t my_e,
                                              int32_t my_s, int n, int64_t step, int32_t cap,
@@ -171,13 +219,22 @@ __device__ __forceinline__ void resolve_regs(SlotRegs<PERC>& t, ExpertRegs<PER>&
   const int lane = threadIdx.x & 63;
   slot_r = -1;
   miss_r = false;
+  uint32_t vkey[PERC];
+#pragma unroll
+  for (int j = 0; j < PERC; ++j) {
+    const int c = lane + 64 * j;
+    const int64_t age = step - t.st[j];
+    const uint32_t a = (age >= 0 && age < kAgeMax) ? static_cast<uint32_t>(age) : kAgeMax;
+    vkey[j] = c < cap ? (a << 12) | static_cast<uint32_t>(4095 - c) : 0u;
+  }
+  uint32_t touched = 0;
   for (int r = 0; r < n; ++r) {
     const int32_t e = lane_value(my_e, r);
     int32_t s = lane_value(my_s, r);
     if (e < 0) continue;
     if (s < 0) {
       int32_t victim;
-      s = take_victim(t, e, cap, &victim);
+      s = take_victim_age(t, vkey, touched, e, cap, step, &victim);
       if (lane > r) {                      // later ids see the table as it is now
         if (my_e == victim) my_s = -1;
         if (my_e == e) my_s = s;
@@ -194,11 +251,12 @@ __device__ __forceinline__ void resolve_regs(SlotRegs<PERC>& t, ExpertRegs<PER>&
     } else {
       ++hits;
     }
-#pragma unroll
-    for (int j = 0; j < PERC; ++j)
-      if (j == (s >> 6) && (s & 63) == lane) t.st[j] = step;
+    if ((s & 63) == lane) touched |= 1u << (s >> 6);
     if (lane == r) slot_r = s;
   }
+#pragma unroll
+  for (int j = 0; j < PERC; ++j)
+    if ((touched >> j) & 1u) t.st[j] = step;
 }
 
 // The device hit/miss counters, read when the kernel starts (with the other

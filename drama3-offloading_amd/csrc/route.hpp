@@ -14,10 +14,11 @@ constexpr int kMaxTopK = 32;
 
 // The decode router's logits launch (router.hip): one token's logits
 // x . W^T rounded to bf16 (bf16_logits) or float32, + bias, into logits
-// [n_experts]; adds one to *step_inc (nullable) for the route that follows.
+// [n_experts]; adds one to *step_inc (nullable) for the route that follows
+// and sets *ticket (nullable), the piece counter of its fetch, to zero.
 int launch_decode_logits(const void* x, const void* w, const float* bias, int32_t hidden,
                          int32_t n_experts, int bf16_logits, float* logits, int64_t* step_inc,
-                         hipStream_t s);
+                         hipStream_t s, int32_t* ticket = nullptr);
 
 // The router's logits launch for `tokens` tokens (moe_router_topk's first
 // launch): logits [tokens, n_experts].
@@ -91,13 +92,34 @@ __device__ __forceinline__ uint64_t wave_topk_keys(const float (&lv)[PER], int32
       cswap(key[0], key[2]); cswap(key[1], key[3]);
       cswap(key[1], key[2]);
     }
-    for (int r = 0; r < top_k; ++r) {
-      const uint64_t best = wave_reduce_u64<true>(key[0]);
-      if (lane == r) pick = best;
-      if (key[0] == best) {
+    // A round's wave maximum of the lanes' leading keys, on 32-bit halves:
+    // the largest logit key first; its index half read from the one lane
+    // that holds it, or, when several lanes tie on the logit (bf16 logits
+    // do), the largest index half among them (the lowest expert).  The
+    // same key as the 64-bit maximum, for about a third of its
+    // instructions.
+    uint32_t hi[PER], lo[PER];
 #pragma unroll
-        for (int j = 0; j + 1 < PER; ++j) key[j] = key[j + 1];
-        key[PER - 1] = 0ull;
+    for (int j = 0; j < PER; ++j) {
+      hi[j] = static_cast<uint32_t>(key[j] >> 32);
+      lo[j] = static_cast<uint32_t>(key[j]);
+    }
+    for (int r = 0; r < top_k; ++r) {
+      const uint32_t mh = wave_max_u32(hi[0]);
+      const uint64_t tied = __builtin_amdgcn_ballot_w64(hi[0] == mh);
+      const uint32_t ml =
+          __builtin_popcountll(tied) == 1
+              ? static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lo[0]),
+                                                                __builtin_ctzll(tied)))
+              : wave_max_u32(hi[0] == mh ? lo[0] : 0u);
+      if (lane == r) pick = (static_cast<uint64_t>(mh) << 32) | ml;
+      if (hi[0] == mh && lo[0] == ml) {
+#pragma unroll
+        for (int j = 0; j + 1 < PER; ++j) {
+          hi[j] = hi[j + 1];
+          lo[j] = lo[j + 1];
+        }
+        hi[PER - 1] = lo[PER - 1] = 0u;
       }
     }
   } else {

@@ -41,11 +41,10 @@ constexpr int kLogitWaves = 1;
 template <int CTRL>
 __device__ __forceinline__ double dpp_f64(double v) {
   const uint64_t u = __double_as_longlong(v);
-  const uint32_t lo = __builtin_amdgcn_update_dpp(static_cast<uint32_t>(u), static_cast<uint32_t>(u),
-                                                  CTRL, 0xf, 0xf, false);
-  const uint32_t hi = __builtin_amdgcn_update_dpp(static_cast<uint32_t>(u >> 32),
-                                                  static_cast<uint32_t>(u >> 32), CTRL, 0xf, 0xf,
-                                                  false);
+  const uint32_t lo = __builtin_amdgcn_update_dpp(0u, static_cast<uint32_t>(u), CTRL, 0xf, 0xf,
+                                                  true);
+  const uint32_t hi = __builtin_amdgcn_update_dpp(0u, static_cast<uint32_t>(u >> 32), CTRL, 0xf,
+                                                  0xf, true);
   return __longlong_as_double(static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo));
 }
 
@@ -86,7 +85,7 @@ template <int TB>
 __global__ __launch_bounds__(64 * kLogitWaves) void router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ bias,
     int32_t tokens, int32_t hidden, int32_t n_experts, int bf16_logits,
-    float* __restrict__ logits, int64_t* __restrict__ step_inc) {
+    float* __restrict__ logits, int64_t* __restrict__ step_inc, int32_t* __restrict__ ticket) {
   constexpr int U = 4;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -172,6 +171,8 @@ __global__ __launch_bounds__(64 * kLogitWaves) void router_logits_kernel(
   // argument loads back either.
   if (step_inc && e_raw == 0 && blockIdx.y == 0 && lane == 0)
     __hip_atomic_fetch_add(step_inc, int64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // ... and finds the counter its fetch waves take pieces from at zero
+  if (ticket && e_raw == 0 && blockIdx.y == 0 && lane == 0) *ticket = 0;
 }
 
 // Many tokens: the logits on the float64 matrix cores.  A workgroup takes 16
@@ -355,11 +356,11 @@ __global__ __launch_bounds__(kFetchThreads) void route_fetch_kernel(
 
 int launch_decode_logits(const void* x, const void* w, const float* bias, int32_t hidden,
                          int32_t n_experts, int bf16_logits, float* logits, int64_t* step_inc,
-                         hipStream_t s) {
+                         hipStream_t s, int32_t* ticket) {
   hipLaunchKernelGGL(router_logits_kernel<1>, dim3((n_experts + kLogitWaves - 1) / kLogitWaves, 1),
                      dim3(64 * kLogitWaves), 0, s, static_cast<const uint16_t*>(x),
                      static_cast<const uint16_t*>(w), bias, 1, hidden, n_experts, bf16_logits,
-                     logits, step_inc);
+                     logits, step_inc, ticket);
   return check_launch("router_logits_kernel");
 }
 
@@ -376,11 +377,11 @@ int launch_router_logits(const void* x, const void* w, const float* bias, int32_
   } else if (tokens == 1)
     hipLaunchKernelGGL(router_logits_kernel<1>, grid, dim3(64 * kLogitWaves), 0, s,
                        static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias,
-                       tokens, hidden, n_experts, bf16_logits, logits, nullptr);
+                       tokens, hidden, n_experts, bf16_logits, logits, nullptr, nullptr);
   else
     hipLaunchKernelGGL(router_logits_kernel<kTokBlock>, grid, dim3(64 * kLogitWaves), 0, s,
                        static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias,
-                       tokens, hidden, n_experts, bf16_logits, logits, nullptr);
+                       tokens, hidden, n_experts, bf16_logits, logits, nullptr, nullptr);
   return check_launch("router_logits_kernel");
 }
 
@@ -449,7 +450,7 @@ extern "C" int moe_route_resolve(const void* x, const void* w, const float* bias
   hipLaunchKernelGGL(router_logits_kernel<1>, dim3((n_experts + kLogitWaves - 1) / kLogitWaves, 1),
                      dim3(64 * kLogitWaves), 0, s,
                      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias, 1,
-                     hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0, logits, nullptr);
+                     hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0, logits, nullptr, nullptr);
   int rc = check_launch("moe_route_resolve(logits)");
   if (rc) return rc;
 #define MOE_TR(PE, PC)                                                                          \
@@ -497,7 +498,7 @@ extern "C" int moe_route_fetch(const void* x, const void* w, const float* bias, 
   hipLaunchKernelGGL(router_logits_kernel<1>, dim3((n_experts + kLogitWaves - 1) / kLogitWaves, 1),
                      dim3(64 * kLogitWaves), 0, s,
                      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), bias, 1,
-                     hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0, logits, step);
+                     hidden, n_experts, logit_dtype == MOE_BF16 ? 1 : 0, logits, step, nullptr);
   int rc = check_launch("moe_route_fetch(logits)");
   if (rc) return rc;
   const int grid = blocks_per_job * (top_k < kFetchMaxJobsInGrid ? top_k : kFetchMaxJobsInGrid);

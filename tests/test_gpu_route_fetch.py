@@ -155,6 +155,42 @@ def test_route_fetch_ffn_block_equals_separate_launches(lib, dev, shape):
     fused.close()
 
 
+@pytest.mark.parametrize("fused_ffn", [False, True], ids=["route_fetch", "route_fetch_ffn"])
+@pytest.mark.parametrize("shape", [
+    dict(capacity=20),
+    dict(n_experts=320, top_k=12, hidden=512, inter=256, capacity=272, blocks_per_job=2,
+         ffn_blocks_per_job=2),
+], ids=["drama3", "wide"])
+def test_route_fetch_equals_route_resolve_after_a_long_idle(lib, dev, shape, fused_ffn):
+    """The fused route keys a miss's victim by the slots' ages (step -
+    stamp) in 20 bits and falls back to the 64-bit stamps when an age
+    reaches 2^20 - 1: with every layer's step counter advanced by 2^21 +
+    2 between two steps, the slots stamped before are that old, later
+    steps mix old and new stamps, and the decisions still equal
+    moe_route_resolve's step for step."""
+    import decode
+    base = dict(layers=2, drift_every=2, schedule_steps=12, **shape)
+    fused = decode.DecodeHarness(decode.DecodeConfig(**base, fused_ffn=fused_ffn), dev)
+    plain = decode.DecodeHarness(decode.DecodeConfig(**base, fused_fetch=False), dev,
+                                 pools=fused.pools)
+    assert fused.fused and fused.fused_ffn == fused_ffn and not plain.fused
+    for s in range(10):
+        if s == 4:
+            for h in (fused, plain):          # an even jump keeps the buffer parity
+                for st in h.step:
+                    st += 2 ** 21 + 2
+        for h in (fused, plain):
+            h.stage(s)
+            h.step_eager()
+        torch.cuda.synchronize(dev)
+        say(f"route_fetch after a long idle {shape} fused_ffn={fused_ffn}: step {s}")
+        _same(fused, plain, f"step {s}")
+    hits, misses = fused.hit_rate()
+    assert hits > 0 and misses > 0
+    plain.pools = []                     # owned by the fused harness
+    fused.close()
+
+
 @pytest.mark.parametrize("shape", [
     dict(capacity=20),
     # E, cap > 256 (16-per-lane registers), 12 jobs over 5 workgroups' 20 waves
