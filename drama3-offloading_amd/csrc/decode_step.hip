@@ -123,16 +123,36 @@ __global__ __launch_bounds__(kStepThreads) void route_fetch_gateup_kernel(
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int q = lane >> 4;
+  // A fetch workgroup whose first unit is of job 0 (b < units) reads that
+  // unit's first piece as soon as each wave knows the first miss (before
+  // the resolve, which only decides where it is stored): its host reads
+  // overlap the resolve.  The routing wave learns it from the route, the
+  // second wave by taking the same top-k and table lookup itself before it
+  // quantises x.
+  const bool early_wg = static_cast<int>(blockIdx.x) < g.nfetch &&
+                        static_cast<int>(blockIdx.x) < g.units;
+  u32x4 va[4], vb[4];
+  int32_t early_e = -1;
+  auto early = [&](int32_t e0) {
+    early_e = e0;
+    if (early_wg && e0 >= 0) {
+      const char* src = g.pool + static_cast<int64_t>(e0) * g.rb +
+                        static_cast<int64_t>(blockIdx.x) * 16 * g.hidden + wave * 4096 + lane * 16;
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+        va[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + h * 1024));
+    }
+  };
   int32_t slot_r;
   bool miss_r;
   if constexpr (UNCACHED)
     route_wave_uncached<PER>(logits, n_experts, top_k, ids, weights, out_slot, fetch_slot,
                              fetch_expert, nmiss_ptr, stats, job_e, job_s, job_k, &job_n, slot_r,
-                             miss_r);
+                             miss_r, early);
   else
     route_wave<PER, PERC>(logits, n_experts, top_k, ids, weights, slot_of, slot_expert, stamp,
                           cap, step_ptr, out_slot, fetch_slot, fetch_expert, nmiss_ptr, stats,
-                          job_e, job_s, job_k, &job_n, slot_r, miss_r);
+                          job_e, job_s, job_k, &job_n, slot_r, miss_r, early);
   if (wave == 0 && lane < top_k) pick_slot[lane] = miss_r ? -1 : slot_r;
   if (wave == 1) {
     // x -> e4m3 codes + per-128 scales in LDS while the first wave routes:
@@ -144,6 +164,7 @@ __global__ __launch_bounds__(kStepThreads) void route_fetch_gateup_kernel(
       const int i = c * 512 + lane * 8;
       raw[c] = *reinterpret_cast<const uint4*>(x + (i < g.hidden ? i : 0));
     }
+    if (early_wg) early(route_first_miss<PER, UNCACHED>(logits, n_experts, top_k, slot_of, step_ptr));
 #pragma unroll
     for (int c = 0; c < NC; ++c)
       if (c * 512 < g.hidden) quantize_x8(raw[c], c * 512 + lane * 8 < g.hidden, c * 512 + lane * 8, xq, xs);
@@ -212,8 +233,7 @@ __global__ __launch_bounds__(kStepThreads) void route_fetch_gateup_kernel(
   // register buffers (a copy between them would wait for the loads just
   // issued).  Issuing them before this piece had arrived (two in flight)
   // made the step 1.3 % slower on MI355X: more outstanding host reads lower
-  // the link's rate.
-  u32x4 va[4], vb[4];
+  // the link's rate.  (va, vb: declared with the early read above.)
 
   // ---- unit pieces: unit u = b + ui * G, pieces p = 0 .. np - 1 (np even,
   // so piece p always lands in buffer p & 1 and a unit's first piece in va)
@@ -259,7 +279,7 @@ __global__ __launch_bounds__(kStepThreads) void route_fetch_gateup_kernel(
       *reinterpret_cast<float4*>(&dpart[tw][gbk][4 * q]) = make_float4(d[0], d[1], d[2], d[3]);
     }
   };
-  if (nu > 0) unit_load(0, 0, va, true);
+  if (nu > 0 && !(early_wg && early_e >= 0)) unit_load(0, 0, va, true);
   for (int ui = 0; ui < nu; ++ui) {
     int j, t;
     unit_off(ui, 0, j, t);

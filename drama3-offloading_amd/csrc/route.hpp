@@ -177,8 +177,24 @@ __device__ __forceinline__ void wave_topk(const float* __restrict__ row, int32_t
 // none of which a workgroup of the launch writes, and gets the miss list in
 // LDS: job_e / job_s (and job_k, the misses' positions in the top-k, when
 // given), their count in *job_n.  Lane r of the first wave returns pick r's
-// slot in slot_r and whether it missed in miss_r.
-template <int PER, int PERC>
+// slot in slot_r and whether it missed in miss_r.  early(e) is called by
+// the routing wave with the first miss's expert (first_miss) before the
+// resolve, so that its caller can start reading that record.
+struct NoEarly {
+  __device__ void operator()(int32_t) const {}
+};
+
+// The expert of the route's first miss (-1 when every pick is in the
+// table), known before the resolve: the picks ahead of the first one absent
+// from the table are hits and evict nothing, so that one is the first miss
+// and the resolve's job 0, whatever it decides for the picks after it.
+// my_e: pick `lane` (-1 past top_k), my_s: its slot in the table (-1 absent).
+__device__ __forceinline__ int32_t first_miss(int32_t my_e, int32_t my_s) {
+  const uint64_t m = __builtin_amdgcn_ballot_w64(my_e >= 0 && my_s < 0);
+  return m ? __builtin_amdgcn_readlane(my_e, __builtin_ctzll(m)) : -1;
+}
+
+template <int PER, int PERC, typename Early = NoEarly>
 __device__ __forceinline__ void route_wave(
     const float* __restrict__ logits, int32_t n_experts, int32_t top_k,
     int32_t* __restrict__ ids, float* __restrict__ weights, int32_t* __restrict__ slot_of,
@@ -186,7 +202,7 @@ __device__ __forceinline__ void route_wave(
     const int64_t* __restrict__ step_ptr, int32_t* __restrict__ out_slot,
     int32_t* __restrict__ fetch_slot, int32_t* __restrict__ fetch_expert,
     int32_t* __restrict__ nmiss_ptr, int64_t* __restrict__ stats, int32_t* job_e, int32_t* job_s,
-    int32_t* job_k, int32_t* job_n, int32_t& slot_r, bool& miss_r) {
+    int32_t* job_k, int32_t* job_n, int32_t& slot_r, bool& miss_r, Early early = Early()) {
   slot_r = -1;
   miss_r = false;
   if (threadIdx.x < 64) {
@@ -206,9 +222,8 @@ __device__ __forceinline__ void route_wave(
     // the step passes through this (empty) statement once every load above
     // is issued, so it is not loaded late, after the top-k
     asm volatile("" : "+s"(step));
-    int32_t id;
-    float wt;
-    wave_topk_of<PER>(lv, n_experts, top_k, &id, &wt);
+    const uint64_t pick = wave_topk_keys<PER>(lv, n_experts, top_k);
+    const int32_t id = topk_id(pick, top_k);
     const int cur = static_cast<int>((step - 1) & 1);
     SlotRegs<PERC> t;
     ExpertRegs<PER> x;
@@ -222,6 +237,8 @@ __device__ __forceinline__ void route_wave(
     const int32_t my_e = lane < top_k ? id : -1;
     const int32_t found = x.lookup(my_e < 0 ? 0 : my_e);
     const int32_t my_s = my_e < 0 ? -1 : found;
+    early(first_miss(my_e, my_s));
+    const float wt = topk_weight(pick, top_k);
     int32_t nm = 0;
     int64_t hits = 0;
     resolve_regs<PER, PERC>(t, x, my_e, my_s, top_k, step, cap, job_e, job_s, job_k, nm, hits,
@@ -265,6 +282,39 @@ __device__ __forceinline__ void route_wave(
   }
 }
 
+// first_miss by a second wave of the route's workgroup, from the same
+// inputs (the logits, the table's current slot_of, the counted step) as the
+// routing wave; with UNCACHED, pick 0 (every pick misses).
+template <int PER, bool UNCACHED>
+__device__ __forceinline__ int32_t route_first_miss(const float* __restrict__ logits,
+                                                    int32_t n_experts, int32_t top_k,
+                                                    const int32_t* __restrict__ slot_of,
+                                                    const int64_t* __restrict__ step_ptr) {
+  const int lane = threadIdx.x & 63;
+  ExpertRegs<PER> xa, xb;
+  int64_t step = 0;
+  if constexpr (!UNCACHED) {
+    xa.load(slot_of, n_experts);
+    xb.load(slot_of + n_experts, n_experts);
+    step = *step_ptr;
+  }
+  float lv[PER];
+  load_logits<PER>(logits, n_experts, lv);
+  asm volatile("" : "+s"(step));
+  const int32_t id = topk_id(wave_topk_keys<PER>(lv, n_experts, top_k), top_k);
+  if constexpr (UNCACHED) {
+    return __builtin_amdgcn_readlane(id, 0);
+  } else {
+    const int cur = static_cast<int>((step - 1) & 1);
+    ExpertRegs<PER> x;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) x.so[j] = cur ? xb.so[j] : xa.so[j];
+    const int32_t my_e = lane < top_k ? id : -1;
+    const int32_t found = x.lookup(my_e < 0 ? 0 : my_e);
+    return first_miss(my_e, my_e < 0 ? -1 : found);
+  }
+}
+
 // The uncached route by the first wave of a workgroup (the other threads
 // pass through): the top-k of one token's logits, every pick a miss fetched
 // into slot r (its position in the top-k), with no slot table: the
@@ -272,13 +322,14 @@ __device__ __forceinline__ void route_wave(
 // every call (bin/offload.py:137-239).  The same LDS lists and per-lane
 // returns as route_wave; workgroup 0 writes ids, weights, out_slot (= r),
 // the fetch lists and nmiss (= top_k), and adds top_k misses to stats.
-template <int PER>
+template <int PER, typename Early = NoEarly>
 __device__ __forceinline__ void route_wave_uncached(
     const float* __restrict__ logits, int32_t n_experts, int32_t top_k,
     int32_t* __restrict__ ids, float* __restrict__ weights, int32_t* __restrict__ out_slot,
     int32_t* __restrict__ fetch_slot, int32_t* __restrict__ fetch_expert,
     int32_t* __restrict__ nmiss_ptr, int64_t* __restrict__ stats, int32_t* job_e,
-    int32_t* job_s, int32_t* job_k, int32_t* job_n, int32_t& slot_r, bool& miss_r) {
+    int32_t* job_s, int32_t* job_k, int32_t* job_n, int32_t& slot_r, bool& miss_r,
+    Early early = Early()) {
   slot_r = -1;
   miss_r = false;
   if (threadIdx.x < 64) {
@@ -287,9 +338,10 @@ __device__ __forceinline__ void route_wave_uncached(
     prev.load(stats);
     float lv[PER];
     load_logits<PER>(logits, n_experts, lv);
-    int32_t id;
-    float wt;
-    wave_topk_of<PER>(lv, n_experts, top_k, &id, &wt);
+    const uint64_t pick = wave_topk_keys<PER>(lv, n_experts, top_k);
+    const int32_t id = topk_id(pick, top_k);
+    early(__builtin_amdgcn_readlane(id, 0));   // pick 0 is job 0
+    const float wt = topk_weight(pick, top_k);
     if (lane < top_k) {
       job_e[lane] = id;
       job_s[lane] = lane;
