@@ -433,6 +433,29 @@ __global__ __launch_bounds__(kStepThreads) void fetch_gateup_kernel(
   const int gb = hidden / 128;
   const int kq = hidden / 512;
   const int units = inter / 16;
+  const uint32_t upr = a.tile_upr[0];      // 16-byte units per w13 row: H / 16
+  const int64_t rec0 = a.bytes[0];
+  // With RESOLVE, a fetch workgroup whose first unit is of job 0 (b <
+  // units) reads that unit's first piece as soon as each wave knows the
+  // first miss, before the resolve (which only decides its slot), as
+  // route_fetch_gateup_kernel does: the first wave from its lookup, the
+  // second from the ids and the table itself.
+  const bool early_wg = RESOLVE && static_cast<int>(blockIdx.x) < nfetch &&
+                        static_cast<int>(blockIdx.x) < units;
+  u32x4 v[4];
+  int32_t early_e = -1;
+  auto early = [&](int32_t e0) {
+    early_e = e0;
+    if (early_wg && e0 >= 0) {
+      const u32x4* sv = reinterpret_cast<const u32x4*>(a.src[0] + e0 * rec0) +
+                        static_cast<int64_t>(blockIdx.x) * 16 * upr;
+#pragma unroll
+      for (int uu = 0; uu < 4; ++uu) {
+        const uint32_t i = threadIdx.x + uu * kStepThreads;
+        v[uu] = __builtin_nontemporal_load(sv + (i >> 5) * upr + (i & 31));
+      }
+    }
+  };
   if (wave == 0) {
     if constexpr (RESOLVE) {
       // the table, the step, the counters and the ids in one round trip
@@ -451,6 +474,7 @@ __global__ __launch_bounds__(kStepThreads) void fetch_gateup_kernel(
           (lane < top_k && e64 >= 0 && e64 < ra.n_experts) ? static_cast<int32_t>(e64) : -1;
       const int32_t found = xr.lookup(my_e < 0 ? 0 : my_e);
       const int32_t my_s = my_e < 0 ? -1 : found;
+      early(first_miss(my_e, my_s));
       int32_t nm = 0;
       int64_t hits = 0;
       int32_t slot_r;
@@ -529,6 +553,18 @@ __global__ __launch_bounds__(kStepThreads) void fetch_gateup_kernel(
       const int i = c * 512 + lane * 8;
       raw[c] = *reinterpret_cast<const uint4*>(x + (i < hidden ? i : 0));
     }
+    if (early_wg) {
+      // the first miss: the first pick absent from the table
+      ExpertRegs<PER> xr;
+      xr.load(ra.slot_of, ra.n_experts);
+      const int li = min(lane, top_k - 1);
+      const int64_t e64 = ra.ids64 ? static_cast<const int64_t*>(ra.ids)[li]
+                                   : static_cast<int64_t>(static_cast<const int32_t*>(ra.ids)[li]);
+      const int32_t my_e =
+          (lane < top_k && e64 >= 0 && e64 < ra.n_experts) ? static_cast<int32_t>(e64) : -1;
+      const int32_t found = xr.lookup(my_e < 0 ? 0 : my_e);
+      early(first_miss(my_e, my_e < 0 ? -1 : found));
+    }
 #pragma unroll
     for (int c = 0; c < NC; ++c)
       if (c * 512 < hidden) quantize_x8(raw[c], c * 512 + lane * 8 < hidden, c * 512 + lane * 8, xq, xs);
@@ -588,8 +624,6 @@ __global__ __launch_bounds__(kStepThreads) void fetch_gateup_kernel(
   const int A = r > 0 ? min(P, 8 * (G - r)) : 0;
   const int np = 2 * kq;
   const int nu = U > b ? (U - 1 - b) / G + 1 : 0;
-  const uint32_t upr = a.tile_upr[0];      // 16-byte units per w13 row: H / 16
-  const int64_t rec0 = a.bytes[0];
   // unit piece p of the workgroup's unit ui: its host rows (lane's loads) and
   // its cache run; live == false reads the same offsets of the cache (the
   // loads stay unconditional: behind a branch, the compiler's wait at the
@@ -611,8 +645,7 @@ __global__ __launch_bounds__(kStepThreads) void fetch_gateup_kernel(
       v[uu] = __builtin_nontemporal_load(sv + (i >> 5) * upr + (i & 31));
     }
   };
-  u32x4 v[4];
-  if (nu > 0) load_piece(piece_src(0, 0, true), v);
+  if (nu > 0 && !(early_wg && early_e >= 0)) load_piece(piece_src(0, 0, true), v);
   for (int ui = 0; ui < nu; ++ui) {
     const int u = b + ui * G;
     const int j = u / units;
