@@ -262,7 +262,10 @@ int moe_route_fetch(const void* x, const void* w, const float* bias, int32_t log
  * the page-locked host pool, n_experts records) and in `cache` (cap slots),
  * both 256-byte aligned.  out [hidden] bf16 = bf16(residual + bf16(MoE(x)))
  * (residual nullable, may be x), the workspace 256-byte aligned with
- * top_k * inter floats.  With `shared` (nullable) the call is the MoE block
+ * top_k * inter floats rounded up to 256 bytes plus 256 bytes (the
+ * fetch's piece counter, which the logits launch zeroes;
+ * moe_fp8_moe_workspace(1, top_k, cap, hidden, inter) bytes always
+ * suffice).  With `shared` (nullable) the call is the MoE block
  * of moe_fp8_moe_block_forward: the shared expert's gate/up rows ride in the
  * fetch launch and its down rows in the down launch, out = bf16(residual +
  * bf16(routed + sigmoid-gated shared)), and the workspace holds
