@@ -237,7 +237,9 @@ def test_route_fetch_coded_equals_route_resolve_then_fetch_coded(lib, dev, shape
     dict(n_experts=64, top_k=4, hidden=512, inter=128, ffn_blocks_per_job=1),
     # the MoE block: the shared expert's rows beside the fetch
     dict(n_experts=64, top_k=4, hidden=512, inter=128, shared_expert=True, shared_inter=256),
-], ids=["drama3", "wide", "tight", "block"])
+    # the kernels' limits: hidden 8192, intermediate 2048, top-16
+    dict(n_experts=24, top_k=16, hidden=8192, inter=2048, ffn_blocks_per_job=2),
+], ids=["drama3", "wide", "tight", "block", "h8192_i2048_top16"])
 def test_route_fetch_ffn_uncached_equals_separate_launches(lib, dev, shape):
     """moe_route_fetch_ffn_uncached (0 % hit: every pick fetched into slot
     k, three launches) against moe_router_topk + moe_fetch of the ids into
