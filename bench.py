@@ -316,7 +316,7 @@ def transfer_split(lib, pools, dev, reps: int = 20, warm: int = 4, seed: int = 5
 
 
 def route_fetch_probe(lib, pools, dev, misses=(0, 3, 8), reps: int = 40, capacity: int = 16,
-                      blocks_per_job: int = 4, seed: int = 9) -> dict:
+                      blocks_per_job: int = 5, seed: int = 9) -> dict:
     """The decode step's dominant kernel alone: route_fetch_gateup_kernel,
     the second of moe_route_fetch_ffn's three launches (route, the misses'
     fetch and every pick's gate/up), timed by HIP events that

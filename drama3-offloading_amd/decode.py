@@ -94,9 +94,12 @@ class DecodeConfig:
     blocks_per_job: int = 3
     fused_fetch: bool = True        # router + resolve + fetch in two launches (moe_route_fetch)
     fused_ffn: bool = True          # ... and the FFN's gate/up in the same launch (moe_route_fetch_ffn)
-    # fetch workgroups per miss on that path: 7.712 / 7.700 / 7.880 / 7.990 ms
-    # per step at 3 / 4 / 5 / 6 (MI355X, 62 % hit), 7.776 at 2
-    ffn_blocks_per_job: int = 4
+    # fetch workgroups per miss on that path (MI355X, ms per step): 7.712 /
+    # 7.700 / 7.880 / 7.990 at 3 / 4 / 5 / 6 when the plain pieces were
+    # dealt round robin (62 % hit); with them dealt by counter and the first
+    # piece read early, 7.798 / 7.757 / 7.743 / 7.773 (100-step windows,
+    # alternating), and 7.786 / 7.767 at 4 / 5 over six 200-step windows
+    ffn_blocks_per_job: int = 5
     noncoherent_pool: bool = False
     shared_expert: bool = False     # the MoE block's gated bf16 shared expert
     shared_inter: int = 512
