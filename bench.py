@@ -40,7 +40,7 @@ TRAFFIC_GEMV_BYTES = (16614 + 8463 + 16 + 8) * 1024   # gate/up + down, 8 expert
 TRAFFIC_CODED_BYTES = (21530 + 24582) * 1024          # coded host reads + HBM writes, 8 records
 # route_fetch_gateup_kernel at 8 misses (--probe routefetch --misses 8): host
 # reads + HBM writes, 8 records (profiles/route_fetch_gateup_kernel.md)
-TRAFFIC_ROUTEFETCH_BYTES = (25297 + 24666) * 1024
+TRAFFIC_ROUTEFETCH_BYTES = (25303 + 24666) * 1024
 PCIE5_X16_GBS = 64.0
 
 
