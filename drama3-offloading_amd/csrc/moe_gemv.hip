@@ -47,13 +47,25 @@ constexpr int kMaxK = kGemvMaxTopK;
 // always read (the same one twice for 32-bit ids, both halves of a float
 // weight) and the dtype only selects how they combine.  With p uniform the
 // id reads are scalar loads.
-__device__ __forceinline__ int64_t load_id(const void* ids, int ids64, int p) {
-  const int32_t* w = static_cast<const int32_t*>(ids);
+//
+// The compiler turns a select between a loaded word and another value into
+// a branch that loads the word on one side only, and waits for the first
+// word inside the other; a second id's loads then go out one round trip
+// later.  So the words are loaded first (load_id_words), every id's words
+// are pinned together by one empty asm that takes them all (the loads go
+// out back to back and are waited for once, where the asm stands), and
+// only then combined (id_of).
+struct IdWords {
+  uint32_t lo, hi;
+};
+__device__ __forceinline__ IdWords load_id_words(const void* ids, int ids64, int p) {
+  const uint32_t* w = static_cast<const uint32_t*>(ids);
   const int i = ids64 ? 2 * p : p;
-  const uint32_t lo = static_cast<uint32_t>(w[i]);
-  const int32_t hi = w[ids64 ? i + 1 : i];
-  return ids64 ? static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | lo)
-               : static_cast<int64_t>(static_cast<int32_t>(lo));
+  return {w[i], w[ids64 ? i + 1 : i]};
+}
+__device__ __forceinline__ int64_t id_of(IdWords v, int ids64) {
+  return ids64 ? static_cast<int64_t>((static_cast<uint64_t>(v.hi) << 32) | v.lo)
+               : static_cast<int64_t>(static_cast<int32_t>(v.lo));
 }
 
 // Routing weight of pair p as two 16-bit halves (a bf16 weight: the same
@@ -164,6 +176,9 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
   // (lanes and blocks past the end re-read an in-bounds address and ignore
   // it): a conditional load makes the compiler's wait at the join cover
   // every load issued before it, weights included.
+  IdWords iw = {0u, 0u};
+  if constexpr (TOPK == 0) iw = load_id_words(ids, ids64, p);
+  __builtin_amdgcn_sched_barrier(0);
   const uint16_t* xr = x + static_cast<int64_t>(t) * hidden;
   const int i0 = wave * 512 + lane * 8;
   const uint4 xraw = *reinterpret_cast<const uint4*>(xr + (i0 < hidden ? i0 : 0));
@@ -183,7 +198,8 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
       }
     }
   } else {
-    e = load_id(ids, ids64, p);
+    asm volatile("" : "+s"(iw.lo), "+s"(iw.hi));
+    e = id_of(iw, ids64);
   }
   const bool valid = e >= 0 && e < n_experts;
   const int G = hidden >> 7;
@@ -391,6 +407,9 @@ __global__ __launch_bounds__(64 * (kMaxK / 2 + 1)) void down_gemv_kernel(
   // depend on the sums, and loaded in the combine they would add a memory
   // round trip after it.  Without a residual the load reads the first word
   // of the wave's own activation row (loaded next anyway) and is ignored.
+  IdWords iw0 = load_id_words(ids, ids64, p0);
+  IdWords iw1 = load_id_words(ids, ids64, p1);
+  __builtin_amdgcn_sched_barrier(0);
   const float* ap0 = act + static_cast<int64_t>(p0) * inter;
   const int64_t o_mine =
       static_cast<int64_t>(t) * hidden + c0 + min(static_cast<int>(threadIdx.x), kDownRows - 1);
@@ -406,8 +425,9 @@ __global__ __launch_bounds__(64 * (kMaxK / 2 + 1)) void down_gemv_kernel(
   // the pairs' routing weights, combined only where they are used
   const RouteHalves wr0 = load_route_halves(weights, wbf16, p0);
   const RouteHalves wr1 = load_route_halves(weights, wbf16, p1);
-  const int64_t e0 = load_id(ids, ids64, p0);
-  const int64_t e1 = load_id(ids, ids64, p1);
+  asm volatile("" : "+s"(iw0.lo), "+s"(iw0.hi), "+s"(iw1.lo), "+s"(iw1.hi));
+  const int64_t e0 = id_of(iw0, ids64);
+  const int64_t e1 = id_of(iw1, ids64);
   const bool valid0 = e0 >= 0 && e0 < n_experts;
   const bool valid1 = e1 >= 0 && e1 < n_experts;
   const int Gi = inter >> 7;
