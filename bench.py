@@ -495,6 +495,97 @@ def gemv_resident(lib, dev, layout, n_records: int = 2048, calls: int = 200, top
     return dt, top_k * layout.record_bytes + 2 * 2 * layout.hidden
 
 
+GEMV_MARKS = (("start", "id in, weight loads out", "own share of x quantised", "after barrier 1",
+               "weights in, MFMAs done", "after barrier 2", "end"),
+              ("start", "ids in, weight loads out", "activations quantised",
+               "weights in, MFMAs done", "after barrier", "end"))
+
+
+def gemv_phases(args) -> dict:
+    """--probe gemvphases: where a decode GEMV call's time goes.  The call of
+    `gemv_resident` (8 experts, 1 token, 2048 resident records, a graph of
+    back-to-back calls, an optional spin before each) runs on
+    libmoeoffload_marks.so, whose two launches record per-wave phase marks
+    on the device's constant clock; after each of `reps` replays the last
+    call's marks give the gate/up span (first wave start to last wave end),
+    the gap to the down launch's first wave, the down span, and each mark's
+    median / p10 / p90 over waves, from its kernel's first start.  The rest
+    of the call time is the boundary before the next call's gate/up.  The
+    product library's own call time is measured first, in a child process
+    started before this one touches the GPU; the marks add their own cost."""
+    import ctypes
+    import subprocess
+    import numpy as np
+    marks_lib = ROOT / "drama3-offloading_amd" / "libmoeoffload_marks.so"
+    if not marks_lib.exists():
+        raise SystemExit(f"{marks_lib} is missing: build first")
+    cmd = [sys.executable, str(Path(__file__).resolve()), "--probe", "gemv", "--steps",
+           str(args.steps), "--idle-us", str(args.idle_us)]
+    child = subprocess.run(cmd, stdout=subprocess.PIPE, text=True, timeout=600, check=True)
+    plain = json.loads(child.stdout.strip().splitlines()[-1])
+    os.environ["MOE_OFFLOAD_LIB"] = str(marks_lib)
+    import torch
+    import hipfetch
+    from hostpool import DRAMA3
+    lib = hipfetch.require()
+    if Path(hipfetch.LIB_PATH).resolve() != marks_lib.resolve():
+        raise SystemExit(f"hipfetch loaded {hipfetch.LIB_PATH}, not the marks build")
+    cdll = ctypes.CDLL(str(marks_lib))
+    cdll.moe_phase_marks_read.argtypes = [ctypes.c_void_p, ctypes.c_int32]
+    dev = torch.device("cuda:0")
+    torch.zeros(1, device=dev)
+    khz = int(cdll.moe_phase_marks_clock_khz())
+    if khz <= 0:
+        raise SystemExit("no wall clock rate for the phase marks")
+    ns_per_tick = 1e6 / khz
+    n_marks = 2 * 256 * 4 * 8
+    buf = np.zeros(n_marks, dtype=np.uint64)
+    rows = {0: [], 1: []}
+    spans, times = [], []
+    for _ in range(args.reps):
+        buf[:] = 0
+        dt, _ = gemv_resident(lib, dev, DRAMA3, calls=args.steps,
+                              idle_cycles=int(2500 * args.idle_us))
+        if cdll.moe_phase_marks_read(buf.ctypes.data, n_marks) != 0:
+            raise SystemExit("moe_phase_marks_read failed")
+        m = buf.reshape(2, 256, 4, 8).astype(np.int64)
+        gu, dn = m[0, :, :, :7], m[1, :, :, :6]
+        if (gu == 0).any() or (dn == 0).any():
+            raise SystemExit("a wave of the last call recorded no marks")
+        g0, g1, d0, d1 = gu[..., 0].min(), gu[..., 6].max(), dn[..., 0].min(), dn[..., 5].max()
+        times.append(dt * 1e6)
+        spans.append([(g1 - g0) * ns_per_tick / 1e3, (d0 - g1) * ns_per_tick / 1e3,
+                      (d1 - d0) * ns_per_tick / 1e3])
+        rows[0].append(((gu - g0) * ns_per_tick / 1e3).reshape(-1, 7))
+        rows[1].append(((dn - d0) * ns_per_tick / 1e3).reshape(-1, 6))
+    med = lambda a: round(float(np.median(a)), 3)
+    sp = np.array(spans)
+    call = med(times)
+    res = {"probe": "gemvphases",
+           "what": "decode expert FFN (8 experts x 1 token over 2048 resident records, graph "
+                   f"of {args.steps} back-to-back calls" +
+                   (f", each after a {args.idle_us} us spin" if args.idle_us else "") +
+                   ") on libmoeoffload_marks.so: the last call's per-wave phase marks after "
+                   f"each of {args.reps} replays, medians over replays; marks in us from "
+                   "their kernel's first wave start, median / p10 / p90 over 256 workgroups "
+                   "x 4 waves x replays",
+           "clock_khz": khz,
+           "us_per_call_product_library": plain["us_per_call"],
+           "us_per_call_marks_build": call,
+           "gateup_span_us": med(sp[:, 0]),
+           "gap_gateup_to_down_us": med(sp[:, 1]),
+           "down_span_us": med(sp[:, 2]),
+           "rest_to_next_call_us": round(call - med(sp.sum(axis=1)), 3),
+           "marks": {}}
+    for kern, name in ((0, "gateup"), (1, "down")):
+        a = np.concatenate(rows[kern])
+        res["marks"][name] = {
+            label: [round(float(np.median(a[:, j])), 3), round(float(np.percentile(a[:, j], 10)), 3),
+                    round(float(np.percentile(a[:, j], 90)), 3)]
+            for j, label in enumerate(GEMV_MARKS[kern])}
+    return res
+
+
 def contention(lib, pools, dev, gemv_calls: int = 2000, fetches: int = 40,
                jobs: int = 8) -> dict:
     """The reference's open question (notes/06-cuda-graphs-plan.md:216-225):
@@ -1712,17 +1803,23 @@ def main() -> int:
                     help="tokens per call of --probe grouped, per step of --probe resident")
     ap.add_argument("--idle-us", type=float, default=0.0,
                     help="--probe gemv: a spin of about this many microseconds before each call")
+    ap.add_argument("--reps", type=int, default=5,
+                    help="--probe gemvphases: replays whose last call's marks are read")
     ap.add_argument("--misses", type=int, default=8,
                     help="misses per call of --probe routefetch (0..8)")
     ap.add_argument("--probe", choices=["gemv", "fetch", "codec", "copy", "grouped", "shared",
                                         "hbm", "step", "contention", "loader", "routefetch",
-                                        "transfer", "blockffn", "stub", "resident"],
+                                        "transfer", "blockffn", "stub", "resident",
+                                        "gemvphases"],
                     help="time one kernel alone (--steps launches) instead of the decode step")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(expert parallelism is a design note only); run with --gpus 1", file=sys.stderr)
         return 2
+    if args.probe == "gemvphases":
+        print(json.dumps(gemv_phases(args)))
+        return 0
     if args.probe:
         return run_probe(args)
 

@@ -15,6 +15,11 @@ the device code as usual, for the CPU tests:
     MOE_OFFLOAD_LIB=drama3-offloading_amd/_build/asan/libmoeoffload.so \
     LD_PRELOAD=$(/opt/rocm/llvm/bin/clang -print-file-name=libclang_rt.asan-x86_64.so) \
     ASAN_OPTIONS=detect_leaks=0 python -m pytest tests -m "not gpu"
+
+Every build also links libmoeoffload_marks.so: the same objects with
+moe_gemv.hip compiled under MOE_PHASE_MARKS, whose decode GEMV launches
+record per-wave phase marks (the bench's `--probe gemvphases` loads it in
+place of the product library).
 """
 from __future__ import annotations
 
@@ -30,6 +35,7 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIB = HERE / "libmoeoffload.so"
+MARKS_LIB = HERE / "libmoeoffload_marks.so"
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC") or shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
@@ -89,7 +95,23 @@ def build(jobs: int = 8, asm: bool = False, asan_host: bool = False) -> Path:
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *link_extra, "-o", str(tmp),
           *map(str, objs), "-ldl"])
     os.replace(tmp, lib)
+    if not asan_host:
+        build_marks(objs)
     return lib
+
+
+def build_marks(objs: list[Path]) -> Path:
+    """libmoeoffload_marks.so: `objs` with moe_gemv's object rebuilt under
+    MOE_PHASE_MARKS (the decode GEMV launches record phase marks)."""
+    marks_dir = BUILD / "marks"
+    marks_dir.mkdir(parents=True, exist_ok=True)
+    marked = compile_one(CSRC / "moe_gemv.hip", False, marks_dir, ["-DMOE_PHASE_MARKS"])
+    rest = [o for o in objs if o.name != marked.name]
+    tmp = MARKS_LIB.with_suffix(".so.tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+          *map(str, rest), str(marked), "-ldl"])
+    os.replace(tmp, MARKS_LIB)
+    return MARKS_LIB
 
 
 def main() -> None:

@@ -40,6 +40,40 @@ constexpr int kMaxHidden = kGemvMaxHidden;
 constexpr int kMaxInter = kGemvMaxInter;
 constexpr int kMaxK = kGemvMaxTopK;
 
+// Phase marks of the two decode launches, in a separate build of this file
+// only (MOE_PHASE_MARKS: libmoeoffload_marks.so, read by the bench's GEMV
+// phase probe).  Lane 0 of every wave of the first kMarkWgs workgroups
+// records the 100 MHz constant clock (s_memrealtime) at fixed points of its
+// kernel, kept in registers and stored at the end with vector stores; each
+// call overwrites them, so they hold the last call's.  The marks cost time
+// themselves (their clock reads share the scalar/LDS wait counter), so the
+// probe reports the marked build's call time beside the plain one.  In the
+// product build every PHASE_* macro is empty.
+#if defined(MOE_PHASE_MARKS)
+constexpr int kMarkWgs = 256, kMarkWaves = 4, kMarks = 8;
+__device__ uint64_t g_phase_marks[2 * kMarkWgs * kMarkWaves * kMarks];
+__device__ __forceinline__ void phase_marks_store(int kern, const uint64_t* m, int n) {
+  const int b = blockIdx.y * gridDim.x + blockIdx.x;
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0 && b < kMarkWgs && wave < kMarkWaves) {
+    uint64_t* dst = g_phase_marks + ((kern * kMarkWgs + b) * kMarkWaves + wave) * kMarks;
+    for (int i = 0; i < n; ++i) dst[i] = m[i];
+  }
+}
+#define PHASE_MARKS_DECL uint64_t phase_marks_[kMarks]
+#define PHASE_MARK(i)                                          \
+  do {                                                         \
+    __builtin_amdgcn_sched_barrier(0);                         \
+    phase_marks_[i] = __builtin_amdgcn_s_memrealtime();        \
+    __builtin_amdgcn_sched_barrier(0);                         \
+  } while (0)
+#define PHASE_MARKS_STORE(kern, n) phase_marks_store(kern, phase_marks_, n)
+#else
+#define PHASE_MARKS_DECL do {} while (0)
+#define PHASE_MARK(i) do {} while (0)
+#define PHASE_MARKS_STORE(kern, n) do {} while (0)
+#endif
+
 // The id and the routing weight of pair p are read without a branch on
 // their dtype: a load inside a branch is waited for inside it, and that wait
 // (vmcnt counts in issue order) would also cover every load issued before,
@@ -168,6 +202,8 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
   // critical path of a launch whose loads all go out at once: 32-bit
   // arithmetic only (a 64-bit division is ~130 scalar instructions), and
   // x[t], which does not depend on the expert, goes out before the id.
+  PHASE_MARKS_DECL;
+  PHASE_MARK(0);                       // start
   const int p = blockIdx.y;
   const int t = static_cast<int>(static_cast<uint32_t>(p) / static_cast<uint32_t>(top_k));
   // This wave's first 512 values of x[t] are loaded before the weights:
@@ -226,6 +262,7 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
 #pragma unroll
   for (int c = 0; c < kGateUpChunk; ++c) sw[c] = srow[min(gb + c, G - 1)];
   __builtin_amdgcn_sched_barrier(0);
+  PHASE_MARK(1);                       // the id is in: the weight loads go out
   v8i a[kGateUpChunk];
 #pragma unroll
   for (int c = 0; c < kGateUpChunk; ++c)
@@ -239,7 +276,9 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
     const uint4 raw = *reinterpret_cast<const uint4*>(xr + (i < hidden ? i : 0));
     quantize_x8(raw, i < hidden, i, xq, xs);
   }
+  PHASE_MARK(2);                       // this wave's share of x quantised
   __syncthreads();
+  PHASE_MARK(3);
   float* ap = act + static_cast<int64_t>(p) * inter;
   if (!valid) {   // no such expert (the whole workgroup): poison the columns, read nothing
     if (wu == 0 && lane < 16) ap[j0 + lane] = __builtin_nanf("");
@@ -290,7 +329,9 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
       }
     }
   }
+  PHASE_MARK(4);                       // weights in, this wave's MFMAs done
   __syncthreads();
+  PHASE_MARK(5);
   if (owner) {
     // unrolled so that the LDS reads of several blocks are in flight at once
 #pragma unroll 8
@@ -313,6 +354,8 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_kernel(
         make_float4(silu_mul(acc[0], u.x), silu_mul(acc[1], u.y), silu_mul(acc[2], u.z),
                     silu_mul(acc[3], u.w));
   }
+  PHASE_MARK(6);                       // end (SiLU(gate) * up stored)
+  PHASE_MARKS_STORE(0, 7);
 }
 
 // ------------------------------------------------------------ kernel 2
@@ -365,6 +408,8 @@ __global__ __launch_bounds__(64 * (kMaxK / 2 + 1)) void down_gemv_kernel(
   __shared__ __align__(16) float part[kMaxK + 1][kDownRows];   // [kMaxK]: discarded quadrants
   __shared__ float wpart[kMaxK];
   __shared__ float spart[SHARED ? kDownRows : 1];
+  PHASE_MARKS_DECL;
+  PHASE_MARK(0);                       // start
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.y;
@@ -442,6 +487,7 @@ __global__ __launch_bounds__(64 * (kMaxK / 2 + 1)) void down_gemv_kernel(
 #pragma unroll
   for (int c = 0; c < kDownChunk; ++c) sw[c] = srow[c < Gi ? c : Gi - 1];
   __builtin_amdgcn_sched_barrier(0);
+  PHASE_MARK(1);                       // the ids are in: the weight loads go out
   v8i a[kDownChunk];
 #pragma unroll
   for (int c = 0; c < kDownChunk; ++c)
@@ -466,6 +512,7 @@ __global__ __launch_bounds__(64 * (kMaxK / 2 + 1)) void down_gemv_kernel(
   // moving the reads above the writes) replaces a workgroup barrier
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
+  PHASE_MARK(2);                       // both pairs' activations quantised
 
   // B operand: this lane's column is its slot's activation; the row sums
   // of slot dhalf run in K-block order with that slot's scales
@@ -508,7 +555,9 @@ __global__ __launch_bounds__(64 * (kMaxK / 2 + 1)) void down_gemv_kernel(
   }
   wpart[k0] = route_weight(wr0, wbf16);
   wpart[k0 + 1] = route_weight(wr1, wbf16);
+  PHASE_MARK(3);                       // weights in, MFMAs done, partials stored
   __syncthreads();
+  PHASE_MARK(4);
   if (threadIdx.x < kDownRows) {
     // sum = fma(w_k, y_k, sum), k in order: the combine of the grouped path
     // too.  All kMaxK partials are read at once (one LDS round trip); the
@@ -533,6 +582,8 @@ __global__ __launch_bounds__(64 * (kMaxK / 2 + 1)) void down_gemv_kernel(
     }
     out[o] = y;
   }
+  PHASE_MARK(5);                       // end (outputs stored)
+  PHASE_MARKS_STORE(1, 6);
 }
 
 // The two decode launches; `sh` (nullable) carries the shared expert along.
@@ -959,3 +1010,25 @@ extern "C" int moe_fp8_moe_forward_noalloc(const void* x, const void* ids, int32
                       n_experts, hidden, inter, strides, residual, out, nullptr, 0, mode, nullptr,
                       &fused, stream, /*static_scratch=*/true);
 }
+
+#if defined(MOE_PHASE_MARKS)
+// The marks build's reader (no counterpart in the reference, not part of
+// the product library): copies the first n words of the phase marks,
+// [kernel: gate/up, down][workgroup][wave][mark], to host memory.
+extern "C" int moe_phase_marks_read(uint64_t* dst, int32_t n) {
+  if (!dst || n < 0 || n > static_cast<int32_t>(sizeof(g_phase_marks) / sizeof(uint64_t)))
+    return -1;
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_phase_marks), static_cast<size_t>(n) * 8) ==
+                 hipSuccess
+             ? 0
+             : -1;
+}
+// The marks' clock in kHz (the device's constant wall clock), or -1.
+extern "C" int32_t moe_phase_marks_clock_khz() {
+  int dev = 0, khz = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess)
+    return -1;
+  return khz;
+}
+#endif

@@ -17,6 +17,24 @@ def test_library_exports_every_declared_symbol(lib):
     assert set(declared) == set(hipfetch.SIGNATURES)
 
 
+def test_phase_marks_build_is_separate(lib):
+    """The decode GEMV's phase marks live only in libmoeoffload_marks.so (the
+    bench's gemvphases probe), which exports the product's symbols too."""
+    import subprocess
+    import sys
+    import hipfetch
+    assert not hasattr(lib.cdll, "moe_phase_marks_read")
+    marks = hipfetch.LIB_PATH.parent / "libmoeoffload_marks.so"
+    if not marks.exists():
+        pytest.skip("marks build not present")
+    names = ["moe_phase_marks_read", "moe_phase_marks_clock_khz", *hipfetch.declared_symbols()]
+    code = ("import ctypes, sys; l = ctypes.CDLL(sys.argv[1]); "
+            "print(' '.join(n for n in sys.argv[2:] if not hasattr(l, n)))")
+    out = subprocess.run([sys.executable, "-c", code, str(marks), *names],
+                         stdout=subprocess.PIPE, text=True, timeout=120, check=True)
+    assert out.stdout.strip() == ""
+
+
 def test_library_shares_torchs_hip_runtime(lib):
     import hipfetch
     ours = lib.hip_runtime_path()
