@@ -465,13 +465,14 @@ def graph_time(dev, body, calls: int) -> float:
 
 
 def gemv_resident(lib, dev, layout, n_records: int = 2048, calls: int = 200, top_k: int = 8,
-                  idle_cycles: int = 0):
+                  idle_cycles: int = 0, mode: int = 1):
     """Decode expert FFN (gate/up GEMV + down GEMV, 8 experts, 1 token) over
     random experts of n_records resident records (6.4 GB at 2048, so the
     256 MB Infinity Cache serves few of them).  Returns (s/call, bytes/call).
     idle_cycles > 0 puts a one-workgroup spin of that many cycles before
     each call (the GPU idles as in a link-bound decode layer; the per-call
-    time then includes the spin, and the kernel trace gives the kernels')."""
+    time then includes the spin, and the kernel trace gives the kernels').
+    `mode` 3 runs the bf16-activation GEMV instead of the e4m3 one."""
     import numpy as np
     import torch
     rec = resident_records(dev, n_records, layout)
@@ -487,7 +488,7 @@ def gemv_resident(lib, dev, layout, n_records: int = 2048, calls: int = 200, top
     def body(r):
         if idle_cycles:
             torch.cuda._sleep(idle_cycles)
-        lib.fp8_moe_forward(x, ids[r], w, *views, out, ws, mode=1, layout=layout.code)
+        lib.fp8_moe_forward(x, ids[r], w, *views, out, ws, mode=mode, layout=layout.code)
     dt = graph_time(dev, body, calls)
     if not bool(torch.isfinite(out.float()).all()):
         raise RuntimeError("GEMV probe produced non-finite output")
@@ -1402,11 +1403,13 @@ def run_probe(args) -> int:
     lib = hipfetch.require()
     dev = torch.device("cuda:0")
     if args.probe == "gemv":
+        mode = 3 if args.a16 else 1
         dt, nbytes = gemv_resident(lib, dev, DRAMA3, calls=args.steps,
-                                   idle_cycles=int(2500 * args.idle_us))
+                                   idle_cycles=int(2500 * args.idle_us), mode=mode)
         res = {"probe": "gemv", "what": "decode expert FFN, 8 experts x 1 token, resident records, "
                "graph of back-to-back calls" + (f", each after a {args.idle_us} us spin"
-                                                if args.idle_us else ""),
+                                                if args.idle_us else "") +
+               (", bf16 activations (mode 3)" if args.a16 else ""),
                "us_per_call": round(1e6 * dt, 3),
                "bytes_per_call": nbytes, "GBps": round(nbytes / dt / 1e9, 2)}
     elif args.probe == "fetch":
@@ -1803,6 +1806,8 @@ def main() -> int:
                     help="tokens per call of --probe grouped, per step of --probe resident")
     ap.add_argument("--idle-us", type=float, default=0.0,
                     help="--probe gemv: a spin of about this many microseconds before each call")
+    ap.add_argument("--a16", action="store_true",
+                    help="--probe gemv: the bf16-activation GEMV (fp8_moe_forward mode 3)")
     ap.add_argument("--reps", type=int, default=5,
                     help="--probe gemvphases: replays whose last call's marks are read")
     ap.add_argument("--misses", type=int, default=8,

@@ -586,6 +586,293 @@ __global__ __launch_bounds__(64 * (kMaxK / 2 + 1)) void down_gemv_kernel(
   PHASE_MARKS_STORE(1, 6);
 }
 
+// ------------------------------------------------ bf16 activations (mode 3)
+
+// moe_fp8_moe_forward_ex mode 3: the per-pair GEMV with the activations kept
+// in bf16 instead of quantised to e4m3, the numerics of the dequantise-then-
+// matmul path (bin/offload.py's CPU expert path; the closed form of
+// notes/13-non-ada-gpus.md:43-53):
+//   h[p][r] = sum_g s13[e][r/128][g] * <w13[e][r][g*128:+128], x[t][g*128:+128]>
+//   a = SiLU(h[:I]) * h[I:] in float32, rounded to bf16 for the down products
+//   y[c]    = sum_g s2[e][c/128][g] * <w2[e][c][g*128:+128], a[g*128:+128]>
+//   out[t]  = fma(w[t][k], y_k, out[t]) for k in order, float32 -> bf16.
+// An e4m3 weight converts to bf16 exactly (v_cvt_scalef32_pk_bf16_fp8, scale
+// 1), and a bf16 product is exact in float32, so each 128-term block product
+// is four v_mfma_f32_16x16x32_bf16 summing exact products in float32.  A
+// lane's 32 weight bytes of a K-block hold reduction indices 32q..32q+31
+// (q = lane / 16, in either record layout); MFMA j takes indices
+// 32q + 8j..+7 from each lane group, and its B operand the activation at
+// those indices, so the four MFMAs cover the block once.  Grids, waves, the
+// weights' loads, the in-order K-block chains and the k-order combine are
+// the e4m3 kernels'.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// 8 e4m3 bytes (two words, lowest byte first) -> 8 bf16 in the same order.
+__device__ __forceinline__ bf16x8 e4m3x8_to_bf16(uint32_t lo, uint32_t hi) {
+  const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false);
+  const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true);
+  const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false);
+  const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true);
+  return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// One K-block's product: the lane's 32 weight bytes `a` against the bf16
+// activations `b` at the block's indices 32q.. (b points at index 32q).
+__device__ __forceinline__ v4f block_bf16(v8i a, const uint16_t* b) {
+  v4f d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const bf16x8 bj = *reinterpret_cast<const bf16x8*>(b + 8 * j);
+    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+        e4m3x8_to_bf16(static_cast<uint32_t>(a[2 * j]), static_cast<uint32_t>(a[2 * j + 1])), bj,
+        d, 0, 0, 0);
+  }
+  return d;
+}
+
+// Gate/up + SiLU with bf16 activations: gateup_gemv_kernel's grid and waves,
+// x[t] copied into LDS as it is instead of quantised.
+__global__ __launch_bounds__(64 * kGateUpWaves) void gateup_gemv_a16_kernel(
+    const uint16_t* __restrict__ x, const void* __restrict__ ids, int ids64, int32_t top_k,
+    const uint8_t* __restrict__ w13, const float* __restrict__ s13, int64_t w13_es,
+    int64_t s13_es, int tiled, int32_t n_experts, int32_t hidden, int32_t inter,
+    float* __restrict__ act) {
+  __shared__ __align__(16) uint16_t xb[kMaxHidden];
+  __shared__ __align__(16) float dpart[kGateUpTiles][kMaxHidden / 128][16];
+  __shared__ float spart[kGateUpTiles][kMaxHidden / 128];
+  __shared__ __align__(16) float upsum[16];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int p = blockIdx.y;
+  const int t = static_cast<int>(static_cast<uint32_t>(p) / static_cast<uint32_t>(top_k));
+  // the id's words, then this wave's first 512 values of x[t], go out
+  // before the weights (the order of gateup_gemv_kernel)
+  IdWords iw = load_id_words(ids, ids64, p);
+  __builtin_amdgcn_sched_barrier(0);
+  const uint16_t* xr = x + static_cast<int64_t>(t) * hidden;
+  const int i0 = wave * 512 + lane * 8;
+  const uint4 xraw = *reinterpret_cast<const uint4*>(xr + (i0 < hidden ? i0 : 0));
+  asm volatile("" : "+s"(iw.lo), "+s"(iw.hi));
+  const int64_t e = id_of(iw, ids64);
+  const bool valid = e >= 0 && e < n_experts;
+  const int G = hidden >> 7;
+  const int wu = __builtin_amdgcn_readfirstlane(wave);
+  const int tile = wu / kGateUpSplit;
+  const int part = wu % kGateUpSplit;
+  const bool owner = part == 0;
+  const int Gs = (G + kGateUpSplit - 1) / kGateUpSplit;
+  const int gb = min(part * Gs, G);
+  const int gn = min(gb + Gs, G) - gb;
+  const int j0 = blockIdx.x * 16;
+  const int r0 = tile * inter + j0;
+  const int q = lane >> 4;
+  const OperandWalk ow = operand_walk(r0 + (lane & 15), q, hidden, tiled);
+  const uint8_t* wrow = w13 + (valid ? e : 0) * w13_es + ow.off;
+  const float* srow =
+      s13 + (valid ? e : 0) * s13_es + static_cast<int64_t>(r0 >> 7) * G;
+  float sw[kGateUpChunk];
+#pragma unroll
+  for (int c = 0; c < kGateUpChunk; ++c) sw[c] = srow[min(gb + c, G - 1)];
+  __builtin_amdgcn_sched_barrier(0);
+  v8i a[kGateUpChunk];
+#pragma unroll
+  for (int c = 0; c < kGateUpChunk; ++c)
+    a[c] = load_op_nt(wrow + min(gb + c, G - 1) * ow.kstep, ow.half);
+  __builtin_amdgcn_sched_barrier(0);
+  if (i0 < hidden) *reinterpret_cast<uint4*>(&xb[i0]) = xraw;
+  for (int base = (wave + kGateUpWaves) * 512; base < hidden; base += kGateUpWaves * 512) {
+    const int i = base + lane * 8;
+    const uint4 raw = *reinterpret_cast<const uint4*>(xr + (i < hidden ? i : 0));
+    if (i < hidden) *reinterpret_cast<uint4*>(&xb[i]) = raw;
+  }
+  __syncthreads();
+  float* ap = act + static_cast<int64_t>(p) * inter;
+  if (!valid) {
+    if (wu == 0 && lane < 16) ap[j0 + lane] = __builtin_nanf("");
+    return;
+  }
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+  for (int k0 = 0; k0 < gn; k0 += kGateUpChunk) {
+    if (k0 > 0) {
+#pragma unroll
+      for (int c = 0; c < kGateUpChunk; ++c)
+        if (k0 + c < gn) {
+          a[c] = load_op_nt(wrow + (gb + k0 + c) * ow.kstep, ow.half);
+          sw[c] = srow[gb + k0 + c];
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < kGateUpChunk; ++c) {
+      const int k = k0 + c;
+      if (k < gn) {
+        const int g = gb + k;
+        const v4f d = block_bf16(a[c], xb + g * 128 + q * 32);
+        if (owner) {
+          block_fma(acc, d, sw[c]);
+        } else {
+          // every lane stores (see gateup_gemv_kernel)
+          *reinterpret_cast<float4*>(&dpart[tile][g][4 * q]) = make_float4(d[0], d[1], d[2], d[3]);
+          spart[tile][g] = sw[c];
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (owner) {
+#pragma unroll 8
+    for (int g = gn; g < G; ++g) {
+      const float4 d = *reinterpret_cast<const float4*>(&dpart[tile][g][4 * q]);
+      const v4f dv = {d.x, d.y, d.z, d.w};
+      block_fma(acc, dv, spart[tile][g]);
+    }
+    if (tile == 1)
+      *reinterpret_cast<float4*>(&upsum[4 * q]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  }
+  __syncthreads();
+  if (owner && tile == 0 && (lane & 15) == 0) {
+    const float4 u = *reinterpret_cast<const float4*>(&upsum[4 * q]);
+    *reinterpret_cast<float4*>(ap + j0 + 4 * q) =
+        make_float4(silu_mul(acc[0], u.x), silu_mul(acc[1], u.y), silu_mul(acc[2], u.z),
+                    silu_mul(acc[3], u.w));
+  }
+}
+
+// Down + combine with bf16 activations: down_gemv_kernel's grid and waves,
+// each wave rounding its two pairs' SiLU(gate) * up rows to bf16 into LDS
+// instead of quantising them.
+__global__ __launch_bounds__(64 * (kMaxK / 2)) void down_gemv_a16_kernel(
+    const float* __restrict__ act, const void* __restrict__ ids, int ids64,
+    const void* __restrict__ weights, int wbf16, int32_t top_k, const uint8_t* __restrict__ w2,
+    const float* __restrict__ s2, int64_t w2_es, int64_t s2_es, int tiled, int32_t n_experts,
+    int32_t hidden, int32_t inter, const uint16_t* __restrict__ residual,
+    uint16_t* __restrict__ out) {
+  __shared__ __align__(16) uint16_t ab[kMaxK][kMaxInter];
+  __shared__ __align__(16) float part[kMaxK + 1][kDownRows];
+  __shared__ float wpart[kMaxK];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.y;
+  const int c0 = blockIdx.x * kDownRows;
+  const int wu = __builtin_amdgcn_readfirstlane(wave);
+  const int q = lane >> 4;
+  const int half = (lane & 15) >> 3;
+  const int dhalf = q >> 1;
+  const int k0 = 2 * wu;
+  const int k1 = min(2 * wu + 1, top_k - 1);
+  const int p0 = t * top_k + k0;
+  const int p1 = t * top_k + k1;
+  const int j0 = lane * 8 < inter ? lane * 8 : 0;
+  IdWords iw0 = load_id_words(ids, ids64, p0);
+  IdWords iw1 = load_id_words(ids, ids64, p1);
+  __builtin_amdgcn_sched_barrier(0);
+  const float* ap0 = act + static_cast<int64_t>(p0) * inter;
+  const int64_t o_mine =
+      static_cast<int64_t>(t) * hidden + c0 + min(static_cast<int>(threadIdx.x), kDownRows - 1);
+  const uint16_t res_v =
+      *(residual ? residual + o_mine : reinterpret_cast<const uint16_t*>(ap0));
+  const float* ap1 = act + static_cast<int64_t>(p1) * inter;
+  float4 araw0[2], araw1[2];
+  araw0[0] = *reinterpret_cast<const float4*>(ap0 + j0);
+  araw0[1] = *reinterpret_cast<const float4*>(ap0 + j0 + 4);
+  araw1[0] = *reinterpret_cast<const float4*>(ap1 + j0);
+  araw1[1] = *reinterpret_cast<const float4*>(ap1 + j0 + 4);
+  const RouteHalves wr0 = load_route_halves(weights, wbf16, p0);
+  const RouteHalves wr1 = load_route_halves(weights, wbf16, p1);
+  asm volatile("" : "+s"(iw0.lo), "+s"(iw0.hi), "+s"(iw1.lo), "+s"(iw1.hi));
+  const int64_t e0 = id_of(iw0, ids64);
+  const int64_t e1 = id_of(iw1, ids64);
+  const bool valid0 = e0 >= 0 && e0 < n_experts;
+  const bool valid1 = e1 >= 0 && e1 < n_experts;
+  const int Gi = inter >> 7;
+  const int64_t ea = half ? (valid1 ? e1 : 0) : (valid0 ? e0 : 0);
+  const OperandWalk ow = operand_walk(c0 + (lane & 7), q, inter, tiled);
+  const uint8_t* wrow = w2 + ea * w2_es + ow.off;
+  const int64_t ed = dhalf ? (valid1 ? e1 : 0) : (valid0 ? e0 : 0);
+  const float* srow = s2 + ed * s2_es + static_cast<int64_t>(c0 >> 7) * Gi;
+  float sw[kDownChunk];
+#pragma unroll
+  for (int c = 0; c < kDownChunk; ++c) sw[c] = srow[c < Gi ? c : Gi - 1];
+  __builtin_amdgcn_sched_barrier(0);
+  v8i a[kDownChunk];
+#pragma unroll
+  for (int c = 0; c < kDownChunk; ++c)
+    a[c] = load_op_nt(wrow + (c < Gi ? c : Gi - 1) * ow.kstep, ow.half);
+  __builtin_amdgcn_sched_barrier(0);
+  // both pairs' activation rows -> bf16 in LDS, 8 values per lane per 512
+  auto put8 = [&](const float4* r, int j, uint16_t* dst) {
+    if (j < inter) {
+      const uint4 v = {
+          static_cast<uint32_t>(f32_to_bf16(r[0].x)) | (static_cast<uint32_t>(f32_to_bf16(r[0].y)) << 16),
+          static_cast<uint32_t>(f32_to_bf16(r[0].z)) | (static_cast<uint32_t>(f32_to_bf16(r[0].w)) << 16),
+          static_cast<uint32_t>(f32_to_bf16(r[1].x)) | (static_cast<uint32_t>(f32_to_bf16(r[1].y)) << 16),
+          static_cast<uint32_t>(f32_to_bf16(r[1].z)) | (static_cast<uint32_t>(f32_to_bf16(r[1].w)) << 16)};
+      *reinterpret_cast<uint4*>(dst + j) = v;
+    }
+  };
+  put8(araw0, lane * 8, ab[k0]);
+  put8(araw1, lane * 8, ab[k0 + 1]);
+  for (int base = 512; base < inter; base += 512) {
+    const int j = base + lane * 8;
+    const int jj = j < inter ? j : 0;
+    float4 ar[2];
+    ar[0] = *reinterpret_cast<const float4*>(ap0 + jj);
+    ar[1] = *reinterpret_cast<const float4*>(ap0 + jj + 4);
+    put8(ar, j, ab[k0]);
+    ar[0] = *reinterpret_cast<const float4*>(ap1 + jj);
+    ar[1] = *reinterpret_cast<const float4*>(ap1 + jj + 4);
+    put8(ar, j, ab[k0 + 1]);
+  }
+  // the wave's own rows: a wave-scope fence stands for a barrier (see down_gemv_kernel)
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  const uint16_t* bq = ab[k0 + half];
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+  for (int g0 = 0; g0 < Gi; g0 += kDownChunk) {
+    if (g0 > 0) {
+#pragma unroll
+      for (int c = 0; c < kDownChunk; ++c)
+        if (g0 + c < Gi) {
+          a[c] = load_op_nt(wrow + (g0 + c) * ow.kstep, ow.half);
+          sw[c] = srow[g0 + c];
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < kDownChunk; ++c) {
+      const int g = g0 + c;
+      if (g < Gi) block_fma(acc, block_bf16(a[c], bq + g * 128 + q * 32), sw[c]);
+    }
+  }
+  {
+    const int kd = k0 + dhalf;
+    const bool mine = half == dhalf;
+    const bool ok = dhalf ? valid1 : valid0;
+    const float nan = __builtin_nanf("");
+    float* dst = mine ? &part[kd][4 * (q & 1)] : &part[kMaxK][4 * (q & 1)];
+    *reinterpret_cast<float4*>(dst) =
+        ok ? make_float4(acc[0], acc[1], acc[2], acc[3]) : make_float4(nan, nan, nan, nan);
+  }
+  wpart[k0] = route_weight(wr0, wbf16);
+  wpart[k0 + 1] = route_weight(wr1, wbf16);
+  __syncthreads();
+  if (threadIdx.x < kDownRows) {
+    float wk[kMaxK], yk[kMaxK];
+#pragma unroll
+    for (int k = 0; k < kMaxK; ++k) {
+      wk[k] = wpart[k];
+      yk[k] = part[k][threadIdx.x];
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kMaxK; ++k)
+      if (k < top_k) sum = fmaf(wk[k], yk[k], sum);
+    const int64_t o = static_cast<int64_t>(t) * hidden + c0 + threadIdx.x;
+    uint16_t y = f32_to_bf16(sum);
+    if (residual) y = f32_to_bf16(bf16_to_f32(res_v) + bf16_to_f32(y));
+    out[o] = y;
+  }
+}
+
 // The two decode launches; `sh` (nullable) carries the shared expert along.
 // The router of up to 16 tokens in front of the GEMV launches: its logits launch
 // (gate weight, bias, logit rounding, the logits buffer), then the top-k
@@ -656,6 +943,27 @@ static int launch_gemv(const uint16_t* x, const void* ids, int ids64, const void
   return check_launch("moe_fp8_moe_forward(down)");
 }
 
+// The two decode launches of mode 3 (bf16 activations).
+static int launch_gemv_a16(const uint16_t* x, const void* ids, int ids64, const void* weights,
+                           int wbf16, int32_t tokens, int32_t top_k, const uint8_t* w13,
+                           const float* s13, const uint8_t* w2, const float* s2,
+                           const moe_expert_strides& es, int32_t n_experts, int32_t hidden,
+                           int32_t inter, const uint16_t* residual, uint16_t* out, float* h,
+                           hipStream_t s) {
+  const int64_t pairs = static_cast<int64_t>(tokens) * top_k;
+  const unsigned gx = static_cast<unsigned>((2 * inter) / 16);
+  hipLaunchKernelGGL(gateup_gemv_a16_kernel, dim3(gx / kGateUpTiles, pairs),
+                     dim3(64 * kGateUpWaves), 0, s, x, ids, ids64, top_k, w13, s13, es.w13,
+                     es.s13, static_cast<int>(es.layout), n_experts, hidden, inter, h);
+  int rc = check_launch("moe_fp8_moe_forward(gate/up, bf16 activations)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(down_gemv_a16_kernel, dim3(hidden / kDownRows, tokens),
+                     dim3(64 * ((top_k + 1) / 2)), 0, s, h, ids, ids64, weights, wbf16, top_k, w2,
+                     s2, es.w2, es.s2, static_cast<int>(es.layout), n_experts, hidden, inter,
+                     residual, out);
+  return check_launch("moe_fp8_moe_forward(down, bf16 activations)");
+}
+
 int launch_down_gemv(const float* act, const int32_t* slots, const void* weights, int wbf16,
                      int32_t tokens, int32_t top_k, const uint8_t* w2, const float* s2,
                      int64_t w2_es, int64_t s2_es, int tiled, int32_t n_slots, int32_t hidden,
@@ -696,7 +1004,7 @@ constexpr int32_t kGemvMaxTokens = 16;
 constexpr int32_t kCarrySharedMaxTokens = 2;
 
 static bool use_grouped(int32_t tokens, int32_t hidden, int32_t mode) {
-  if (mode == 1) return false;
+  if (mode == 1 || mode == 3) return false;
   if (mode == 2) return true;
   return tokens > kGemvMaxTokens;
 }
@@ -797,7 +1105,7 @@ static int forward_impl(const void* x, const void* ids, int32_t ids_dtype, const
   MOE_REQUIRE(n_experts >= 1, "moe_fp8_moe_forward: n_experts < 1");
   MOE_REQUIRE(ids_dtype == MOE_I32 || ids_dtype == MOE_I64, "moe_fp8_moe_forward: bad ids_dtype");
   MOE_REQUIRE(w_dtype == MOE_F32 || w_dtype == MOE_BF16, "moe_fp8_moe_forward: bad w_dtype");
-  MOE_REQUIRE(mode >= 0 && mode <= 2, "moe_fp8_moe_forward: mode must be 0, 1 or 2");
+  MOE_REQUIRE(mode >= 0 && mode <= 3, "moe_fp8_moe_forward: mode must be 0, 1, 2 or 3");
   if (tokens == 0) return MOE_OK;   // an empty call touches nothing (its tensors may be NULL)
   MOE_REQUIRE(x && ids && weights && w13 && s13 && w2 && s2 && out,
               "moe_fp8_moe_forward: NULL pointer");
@@ -854,6 +1162,15 @@ static int forward_impl(const void* x, const void* ids, int32_t ids_dtype, const
   }
   MOE_REQUIRE(pairs <= 65535LL, "moe_fp8_moe_forward: too many (token, expert) pairs (%lld)",
               (long long)pairs);
+  if (mode == 3) {
+    MOE_REQUIRE(!sh && !rt, "moe_fp8_moe_forward: mode 3 (bf16 activations) carries no shared "
+                            "expert or router");
+    return launch_gemv_a16(static_cast<const uint16_t*>(x), ids, ids64, weights, wbf16, tokens,
+                           top_k, static_cast<const uint8_t*>(w13), s13,
+                           static_cast<const uint8_t*>(w2), s2, es, n_experts, hidden, inter,
+                           static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out), h,
+                           s);
+  }
   // the shared expert rides along (the down workgroup's ceil(top_k/2) + 1
   // waves fit its launch bounds for every top_k)
   *fused = sh != nullptr;
@@ -963,7 +1280,7 @@ extern "C" int moe_fp8_moe_block_forward(const void* x, const void* ids, int32_t
                       static_cast<const uint16_t*>(shared->w_up),
                       static_cast<const uint16_t*>(shared->w_down),
                       static_cast<const uint16_t*>(shared->w_sgate), Is, act, sig};
-  if (!use_grouped(tokens, hidden, mode) && tokens <= kCarrySharedMaxTokens) {
+  if (mode != 3 && !use_grouped(tokens, hidden, mode) && tokens <= kCarrySharedMaxTokens) {
     // decode: the shared expert rides in the two GEMV launches, residual last
     const int rc = forward_impl(x, ids, ids_dtype, weights, w_dtype, tokens, top_k, w13, s13,
                                 w2, s2, n_experts, hidden, inter, strides, residual, out,

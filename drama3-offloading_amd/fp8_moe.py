@@ -16,8 +16,10 @@ import torch
 import hipfetch
 
 # kernel choice: automatic (per-pair GEMV up to 16 tokens, grouped beyond),
-# per-pair GEMV, grouped
-MODE_AUTO, MODE_GEMV, MODE_GROUPED = 0, 1, 2
+# per-pair GEMV, grouped -- all W8A8 (activations quantised to e4m3 per 128
+# columns) -- and the per-pair GEMV with bf16 activations (W8A16: the
+# numerics of the dequantise-then-matmul path, bin/offload.py's CPU experts)
+MODE_AUTO, MODE_GEMV, MODE_GROUPED, MODE_GEMV_A16 = 0, 1, 2, 3
 
 
 def workspace_bytes(tokens: int, top_k: int, n_experts: int, hidden: int, inter: int) -> int:
@@ -35,7 +37,9 @@ def fp8_moe_forward(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch
     `out` and `workspace` may be passed in (preallocated, e.g. for graph
     capture); otherwise they are allocated from torch's caching allocator.
     `layout`: byte order of w13/w2 -- row-major as in the checkpoint
-    (default), or hipfetch.LAYOUT_TILES for views of packed records."""
+    (default), or hipfetch.LAYOUT_TILES for views of packed records.
+    `mode` MODE_GEMV_A16 keeps the activations in bf16 (x as given,
+    SiLU(gate) * up rounded to bf16) instead of quantising them to e4m3."""
     lib = hipfetch.require()
     if not x.is_cuda:
         raise RuntimeError("fp8_moe_forward runs on the GPU only; x is on "

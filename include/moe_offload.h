@@ -441,7 +441,14 @@ typedef struct moe_expert_strides {
  * bf16 tensor add would (out = bf16(residual + bf16(sum_k w*y)); NULL =
  * none; it may be x itself, not out), and a kernel choice: mode 0 automatic
  * (per-pair GEMV up to 16 tokens, grouped beyond), 1 per-pair GEMV, 2
- * grouped. */
+ * grouped, 3 per-pair GEMV with bf16 activations.  Modes 0-2 quantise the
+ * activations (x, and SiLU(gate) * up) per 128 columns to e4m3 and give
+ * bit-identical rows.  Mode 3 keeps them in bf16 (x as given, SiLU(gate) *
+ * up rounded to bf16) and multiplies them with the e4m3 weights converted
+ * exactly to bf16, accumulating in float32: the numerics of the
+ * dequantise-then-matmul path (bin/offload.py's CPU experts), at any token
+ * count the GEMV takes (pairs <= 65535); with moe_fp8_moe_block_forward its
+ * shared expert runs in its own two launches after the routed call. */
 int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t ids_dtype,
                            const void* weights, int32_t w_dtype,
                            int32_t tokens, int32_t top_k, const void* w13,

@@ -262,6 +262,22 @@ def test_shared_and_block_preconditions_are_rejected_without_launching(lib):
     assert b"shared inter" in c.moe_last_error()
 
 
+def test_forward_modes(lib):
+    """Modes 0-3 pass the preconditions (an empty call touches nothing);
+    any other mode is refused before anything is enqueued."""
+    import hipfetch
+    c = lib.cdll
+    for mode in range(4):
+        assert c.moe_fp8_moe_forward_ex(None, None, hipfetch.MOE_I32, None, hipfetch.MOE_F32, 0, 8,
+                                        None, None, None, None, 256, 2048, 512, None, None, None,
+                                        None, 0, mode, None) == 0, mode
+    for mode in (-1, 4):
+        assert c.moe_fp8_moe_forward_ex(None, None, hipfetch.MOE_I32, None, hipfetch.MOE_F32, 0, 8,
+                                        None, None, None, None, 256, 2048, 512, None, None, None,
+                                        None, 0, mode, None) == -1
+        assert b"mode must be 0, 1, 2 or 3" in c.moe_last_error()
+
+
 def test_noalloc_forward_refuses_calls_beyond_its_scratch(lib):
     import ctypes as C
     import hipfetch
