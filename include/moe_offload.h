@@ -447,8 +447,10 @@ typedef struct moe_expert_strides {
  * up rounded to bf16) and multiplies them with the e4m3 weights converted
  * exactly to bf16, accumulating in float32: the numerics of the
  * dequantise-then-matmul path (bin/offload.py's CPU experts), at any token
- * count the GEMV takes (pairs <= 65535); with moe_fp8_moe_block_forward its
- * shared expert runs in its own two launches after the routed call. */
+ * count the GEMV takes (pairs <= 65535: each pair reads its expert's weights,
+ * where the grouped e4m3 path of a prefill-sized call reads each expert
+ * once); with moe_fp8_moe_block_forward its shared expert runs in its own
+ * two launches after the routed call. */
 int moe_fp8_moe_forward_ex(const void* x, const void* ids, int32_t ids_dtype,
                            const void* weights, int32_t w_dtype,
                            int32_t tokens, int32_t top_k, const void* w13,

@@ -122,3 +122,39 @@ def test_a16_bad_id_poisons_only_its_token(lib, dev):
     got = _forward(lib, dev, host, x, ids, w, MODE_GEMV_A16)
     assert np.isfinite(got[0]).all() and np.isfinite(got[2]).all()
     assert np.isnan(got[1]).all()
+
+
+def test_a16_graph_replays_and_noalloc_equal_eager(lib, dev):
+    """Mode 3 captured in a hipGraph: every replay, with eager work and a
+    synchronisation between replays, equals the eager call; the
+    allocation-free entry point gives the same bytes."""
+    H, I, E, T, K = 2048, 512, 12, 2, 8
+    host, x, ids, w = _case(9, E, H, I, T, K)
+    d = [t.to(dev) for t in host]
+    bufs = (d[0].view(torch.float8_e4m3fn), d[1], d[2].view(torch.float8_e4m3fn), d[3])
+    xd, idd, wd = x.to(dev), torch.from_numpy(ids).to(dev), w.to(dev)
+    ws = torch.empty(lib.fp8_moe_workspace(T, K, E, H, I), dtype=torch.uint8, device=dev)
+    eager = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+    lib.fp8_moe_forward(xd, idd, wd, *bufs, eager, ws, mode=MODE_GEMV_A16)
+    out = torch.empty_like(eager)
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        lib.fp8_moe_forward(xd, idd, wd, *bufs, out, ws, mode=MODE_GEMV_A16)
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        lib.fp8_moe_forward(xd, idd, wd, *bufs, out, ws, mode=MODE_GEMV_A16)
+    for r in range(3):
+        out.zero_()
+        ws.fill_(0xFF)                     # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {r}"
+    del g
+    na = torch.empty_like(eager)
+    lib.fp8_moe_forward_noalloc(xd, idd, wd, *bufs, na, mode=MODE_GEMV_A16)
+    torch.cuda.synchronize()
+    assert torch.equal(na, eager)
